@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""bench.py -- µs per absorbed-MLA layer on one MI355X, with per-step roofline figures.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg2] [--no-cpu-baseline]
+
+One "step" is one MLA layer, steps 2a1 -> 3d, through the drop-in surface
+(mla_custom_cuda.q_absorbed + mla_custom_cuda.mla_attention), on inputs already resident
+in HBM.  The default workload is BASELINE configs[1]: B=128, Sq=1, Sk=4989, fp32,
+DeepSeek-V3 dims.  Output: ONE JSON line on stdout.
+
+Timed region: W untimed warm-up layers, then exactly K layers bracketed by
+torch.cuda.synchronize() on both sides and HIP events on the current stream.  A second,
+separately timed pass runs the same kernels through the per-step ops with an event
+between consecutive steps; it gives each step's average launch duration, from which the
+per-step GFLOP/s, GB/s, MFMA % and HBM % (algorithmic work, formulas below) and the
+`roofline` object of the dominant kernel are computed.
+
+cpu_baseline: the CPU oracle (oracle/mla_ref.py, the reference's PyTorch formulation
+restated) timed on this machine's host cores on the same inputs -- the only place this
+script touches oracle/.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "mla-cuda_amd")
+for _p in (ROOT, PKG):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "µs per MLA layer (B=128 decode, Sk=4989) + HBM GB/s & MFMA util % per step"
+PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
+PEAK_F32 = 157.3e12        # flop/s, dense fp32 MFMA
+REF_A6000_US = 16920.0     # reference's published layer time at this shape (README.md:367)
+
+CONFIGS = {
+    # name: (B, Sq, Sk, description)
+    "cfg2": (128, 1, 4989, "B=128 Sq=1 Sk=4989 fp32 decode (BASELINE configs[1])"),
+    "cfg1": (1, 1, 512, "B=1 Sq=1 Sk=512 fp32 decode (BASELINE configs[0])"),
+    "b1": (1, 1, 4989, "B=1 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
+    "b8": (8, 1, 4989, "B=8 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
+    "b32": (32, 1, 4989, "B=32 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
+}
+
+
+def step_work(B, Sq, Sk, dims, e=4):
+    """Algorithmic FLOPs and compulsory HBM bytes per step (each input read once, each
+    output written once; fp32 intermediates).  FLOP formulas follow the reference's own
+    roofline (stage_profile.py:85-93)."""
+    H, R, D, V = dims.n_heads, dims.kv_rank, dims.rope, dims.v
+    hid, ql, qk, nope = dims.hidden, dims.q_lora, dims.qk_head, dims.nope
+    bq = B * Sq
+    flat = bq * H
+    P = -(-Sk // 128)
+    w = {
+        "2a1": (2 * bq * hid * ql, e * (bq * hid + hid * ql) + 4 * bq * ql),
+        "2a-n": (3 * bq * ql, 4 * bq * ql + e * ql + e * bq * ql),
+        "2a2": (2 * bq * ql * H * qk, e * (bq * ql + ql * H * qk) + 4 * bq * H * qk),
+        "2b": (6 * bq * H * D // 2, 4 * bq * H * D + e * bq * H * D),
+        "2c": (2 * bq * H * nope * R, 4 * bq * H * nope + e * H * nope * R + e * bq * H * R),
+        "3a": (2 * flat * Sk * (R + D), e * (flat * (R + D) + B * Sk * (R + D))
+               + 4 * (flat * Sk + 2 * flat * P)),
+        "3b": (3 * flat * P, 4 * (3 * flat * P + flat)),
+        "3c": (2 * flat * Sk * R, 4 * (flat * Sk + flat * P) + e * (B * Sk * R) + 4 * flat * R),
+        "3d": (2 * flat * R * V, 4 * flat * R + e * H * V * R + 4 * flat + e * flat * V),
+    }
+    return w
+
+
+def build_inputs(B, Sq, Sk, seed=0):
+    import mla_inputs
+    return mla_inputs.make_inputs(B, Sq, Sk, seed=seed)
+
+
+def cpu_baseline(inp, gpu_out, budget_s=30.0):
+    """Time the CPU oracle on the host cores: 1 warm-up, then the median of up to 3 runs,
+    on the full workload if one layer fits the budget, else on the first sequences of the
+    batch (scaled to the full batch; every sequence costs the same)."""
+    import torch
+    from oracle import mla_ref as R
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    B = inp["x"].shape[0]
+
+    def layer(b):
+        return R.mla_layer(inp["x"][:b], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
+                           inp["wkv_b"], inp["c_kv"][:b], inp["pe_cache"][:b],
+                           inp["positions"])
+
+    # probe with a small sample to size the run
+    bs = min(B, 8)
+    t0 = time.perf_counter()
+    ref = layer(bs)
+    t_probe = time.perf_counter() - t0
+    est_full = t_probe * B / bs
+    b_use = B if est_full * 4 <= budget_s else max(1, min(B, int(budget_s / 4 / (t_probe / bs))))
+    ref = layer(b_use)  # warm-up at the chosen size
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        ref = layer(b_use)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    us = t * 1e6 * (B / b_use)
+    err = (gpu_out[:b_use].float().cpu() - ref).abs().max().item()
+    sample = (f"{'full batch' if b_use == B else f'first {b_use} of {B} sequences, scaled x{B / b_use:.1f}'}"
+              f"; oracle layer on CPU, 1 warm-up + median of 3")
+    return {"value": round(us, 1), "unit": "µs", "cores": threads, "kind": "port",
+            "sample": sample}, err, b_use
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mla_custom_cuda as ext
+    import mla_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    dims = mla_inputs.DEEPSEEK_V3
+    B, Sq, Sk, desc = CONFIGS[args.config]
+    print(f"[bench] config {args.config}: {desc}", file=sys.stderr, flush=True)
+
+    inp = build_inputs(B, Sq, Sk, args.seed)
+    W_uk = inp["wkv_b"][:, :dims.nope, :].contiguous()
+    W_uv = inp["wkv_b"][:, dims.nope:, :].contiguous()
+    g = {k: v.to(dev) for k, v in inp.items()}
+    W_uk_d, W_uv_d = W_uk.to(dev), W_uv.to(dev)
+    scale = math.sqrt(dims.qk_head)
+    eps = 1e-6
+
+    def layer():
+        qa, qr = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
+                                g["positions"], dims.nope, dims.rope, eps)
+        return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale)
+
+    # ---- timed region: the fused boundary calls
+    for _ in range(args.warmup):
+        out = layer()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        out = layer()
+    end.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    ms_per_step = start.elapsed_time(end) / args.steps
+    print(f"[bench] fused layer: {ms_per_step * 1e3:.1f} µs/step over {args.steps} steps",
+          file=sys.stderr, flush=True)
+
+    # ---- per-step pass: same kernels via the per-step ops, an event between steps
+    x2d = g["x"].reshape(B * Sq, dims.hidden)
+    names = ["2a1", "2a-n", "2a2", "2b", "2c", "3a", "3b", "3c", "3d"]
+
+    def steps(ev):
+        ev[0].record()
+        lat_acc = ext.gemm(x2d, g["W_q_a"]); ev[1].record()
+        lat = ext.rmsnorm(lat_acc, g["q_norm_w"], eps); ev[2].record()
+        raw = ext.gemm(lat, g["W_q_b"]); ev[3].record()
+        qr = ext.rope(raw, g["positions"], B, Sq, dims.n_heads, dims.nope, dims.rope,
+                      torch.float32); ev[4].record()
+        qa = ext.absorb(raw, W_uk_d, B, Sq, dims.rope); ev[5].record()
+        p, m, l = ext.scores(qa, qr, g["c_kv"], g["pe_cache"], scale); ev[6].record()
+        alpha, rs = ext.combine(m, l); ev[7].record()
+        ctx = ext.ctx(p, alpha, g["c_kv"], Sq, dims.n_heads); ev[8].record()
+        o = ext.out(ctx, rs, W_uv_d); ev[9].record()
+        return o
+
+    for _ in range(2):
+        steps([torch.cuda.Event(enable_timing=True) for _ in range(10)])
+    torch.cuda.synchronize()
+    all_ev = [[torch.cuda.Event(enable_timing=True) for _ in range(10)] for _ in range(args.steps)]
+    for ev in all_ev:
+        o_steps = steps(ev)
+    torch.cuda.synchronize()
+    step_us = {n: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in all_ev) * 1e3
+               for i, n in enumerate(names)}
+    steps_sum = sum(step_us.values())
+    same = (o_steps - out).abs().max().item()
+
+    work = step_work(B, Sq, Sk, dims)
+    per_step = {}
+    for n in names:
+        fl, by = work[n]
+        t = step_us[n] * 1e-6
+        per_step[n] = {"us": round(step_us[n], 2), "gflop": round(fl / 1e9, 3),
+                       "mbytes": round(by / 1e6, 2),
+                       "tflops": round(fl / t / 1e12, 2), "gbps": round(by / t / 1e9, 1),
+                       "mfma_pct": round(100 * fl / t / PEAK_F32, 1),
+                       "hbm_pct": round(100 * by / t / PEAK_HBM, 1)}
+    dom = max(("3a", "3c"), key=lambda n: step_us[n])
+    fl, by = work[dom]
+    achieved = fl / (step_us[dom] * 1e-6) / 1e12
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
+                "frac": round(achieved / (PEAK_F32 / 1e12), 4), "traffic": None,
+                "algorithmic_flop": fl, "algorithmic_bytes": by}
+
+    value_us = ms_per_step * 1e3
+    rec = {
+        "metric": METRIC,
+        "value": round(value_us, 2),
+        "unit": "µs",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": round(value_us / REF_A6000_US, 4) if args.config == "cfg2" else None,
+        "vs_baseline_ref": "reference kernels, RTX A6000, 16.92 ms (README.md:367)",
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": desc, "B": B, "Sq": Sq, "Sk": Sk, "hidden": dims.hidden,
+                   "heads": dims.n_heads, "q_lora": dims.q_lora, "kv_rank": dims.kv_rank,
+                   "nope": dims.nope, "rope": dims.rope, "v": dims.v},
+        "roofline": roofline,
+        "steps_us": per_step,
+        "per_step_sum_us": round(steps_sum, 2),
+        "per_step_vs_fused_max_abs": same,
+        "wall_s_timed": round(t_wall, 3),
+    }
+
+    if not args.no_cpu_baseline:
+        print("[bench] timing the CPU oracle ...", file=sys.stderr, flush=True)
+        cb, err, _ = cpu_baseline(inp, out.cpu())
+        rec["cpu_baseline"] = cb
+        rec["parity_max_abs_vs_cpu_oracle"] = err
+        rec["gpu_speedup_vs_cpu"] = round(cb["value"] / value_us, 1)
+    else:
+        rec["cpu_baseline"] = None
+
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,183 @@
+/*
+ * mla.h -- C ABI of libmla_amd.so, the MI355X (gfx950) absorbed-MLA layer.
+ *
+ * The library replaces the reference's CUDA extension (pgangwar-ucsd/mla-cuda,
+ * mla_kernels.cu).  Its two fused entry points are the reference's pybind surface
+ * (mla_kernels.cu:1688-1693); the per-step entry points expose each of the nine kernels
+ * of that file on its own, so each step can be checked and profiled alone.
+ *
+ * Conventions shared by every entry point
+ *   - All tensor arguments are DEVICE pointers to dense row-major storage with the shapes
+ *     given in the comments; every pointer must be 16-byte aligned.
+ *   - `dtype` names the storage type of the layer's inputs and outputs.  Intermediates that
+ *     the reference keeps in its accumulate dtype (mla_kernels.cu:115-120) are float32
+ *     here ("acc" below): q_lat_acc, q_raw, scores, m/l/alpha, row_sum, ctx.
+ *   - Work is enqueued on `stream` (NULL = the null stream); no entry point synchronises
+ *     the host, none allocates device memory.  Scratch memory comes from the caller through
+ *     `workspace` / `workspace_bytes`, sized by the matching *_workspace_bytes() query.
+ *   - Return value: MLA_OK, or an mla_status_t error code with a message available from
+ *     mla_last_error() on the calling thread.  Arguments are validated before any HIP call,
+ *     so a rejected call has no side effect on the device.
+ *   - Calls that share a workspace must be ordered on one stream.
+ */
+#ifndef MLA_AMD_MLA_H_
+#define MLA_AMD_MLA_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The HIP runtime's own stream handle type (hip_runtime_api.h declares the same). */
+typedef struct ihipStream_t* hipStream_t;
+
+typedef enum mla_dtype {
+    MLA_DTYPE_F32 = 0,   /* float32 storage, float32 MFMA (v_mfma_f32_32x32x2_f32)       */
+    MLA_DTYPE_BF16 = 1,  /* bfloat16 storage, float32 accumulation on bf16 MFMA          */
+} mla_dtype_t;
+
+typedef enum mla_status {
+    MLA_OK = 0,
+    MLA_ERR_INVALID_ARGUMENT = 1,  /* shape, pointer, alignment or value out of range   */
+    MLA_ERR_UNSUPPORTED = 2,       /* valid request this build does not implement       */
+    MLA_ERR_WORKSPACE = 3,         /* workspace missing or smaller than the query says  */
+    MLA_ERR_HIP = 4,               /* a HIP runtime call or kernel launch failed        */
+} mla_status_t;
+
+/* Layer dimensions.  Reference values (DeepSeek-V3, exhaustive_benchmark_suite.py:30-49):
+ * hidden 7168, q_lora 1536, heads 128, nope 128, rope 64, kv_rank 512, v 128. */
+typedef struct mla_dims {
+    int32_t batch;    /* B                                   */
+    int32_t sq;       /* query tokens per sequence           */
+    int32_t sk;       /* cached keys per sequence            */
+    int32_t hidden;   /* model width                         */
+    int32_t q_lora;   /* Q latent rank                       */
+    int32_t heads;    /* H                                   */
+    int32_t nope;     /* per-head non-rotary q/k width       */
+    int32_t rope;     /* per-head rotary width (even)        */
+    int32_t kv_rank;  /* latent cache width R                */
+    int32_t v;        /* per-head value width                */
+} mla_dims_t;
+
+/* Thread-local message describing the most recent failed call ("" if none). */
+const char* mla_last_error(void);
+/* Library version string. */
+const char* mla_version(void);
+/* Keys covered by one softmax partial of the scores step (128): the m/l/alpha row length
+ * is ceil(sk / mla_score_tile()). */
+int32_t mla_score_tile(void);
+/* Row stride, in elements, of the `scores` buffer for a given sk (sk rounded up to 32). */
+int32_t mla_score_ld(int32_t sk);
+
+/* ======================================================================================
+ * Fused entry points -- the reference's boundary
+ * ==================================================================================== */
+
+/* Q path, steps 2a1 -> 2a-n -> 2a2 -> 2b -> 2c.
+ * Replaces mla_custom_cuda.q_absorbed / launch_q_absorbed (mla_kernels.cu:599-767).
+ *   x          [B, Sq, hidden]                 dtype
+ *   W_q_a      [hidden, q_lora]                dtype
+ *   q_norm_w   [q_lora]                        dtype  RMSNorm gain
+ *   W_q_b      [q_lora, H*(nope+rope)]         dtype
+ *   W_uk       [H, nope, kv_rank]              dtype
+ *   positions  [Sq]                            int64  absolute position of each query
+ *   inv_freq   [rope/2]                        float32 RoPE inverse frequencies, computed by
+ *                                              the caller as 1/10000^(2i/rope) in float32
+ *   q_absorbed [B, Sq, H, kv_rank]             dtype  (out)
+ *   q_rope     [B, Sq, H, rope]                dtype  (out)
+ */
+size_t mla_q_absorbed_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims);
+int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims,
+                   const void* x, const void* W_q_a, const void* q_norm_w,
+                   const void* W_q_b, const void* W_uk, const int64_t* positions,
+                   const float* inv_freq, double eps,
+                   void* q_absorbed, void* q_rope,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Attention, steps 3a -> 3b -> 3c -> 3d.
+ * Replaces mla_custom_cuda.mla_attention / launch_mla_attention (mla_kernels.cu:1479-1682).
+ *   q_absorbed [B, Sq, H, kv_rank], q_rope [B, Sq, H, rope]          dtype
+ *   c_kv       [B, Sk, kv_rank],    pe_cache [B, Sk, rope]           dtype
+ *   W_uv       [H, v, kv_rank]                                      dtype
+ *   out        [B, Sq, H, v]                                        dtype (out)
+ *   scale      softmax DIVISOR (the reference passes sqrt(nope+rope))
+ *   causal     0: every key visible; 1: key j visible to query i iff j <= Sk - Sq + i
+ *              (not in the reference; used for chunked prefill)
+ */
+size_t mla_attention_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal);
+int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims,
+                  const void* q_absorbed, const void* q_rope, const void* c_kv,
+                  const void* pe_cache, const void* W_uv, double scale, int causal,
+                  void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ======================================================================================
+ * Per-step entry points (no reference counterpart: the reference fuses them behind the
+ * two calls above).  dims fields a step does not use are ignored.
+ * ==================================================================================== */
+
+/* 2a1 / 2a2: C[M, N] (float32) = A[M, K] @ W[K, N]; A and W in dtype.
+ * The reference's q_raw_gemm_kernel (mla_kernels.cu:233-366). */
+size_t mla_gemm_workspace_bytes(mla_dtype_t dtype, int32_t M, int32_t N, int32_t K);
+int mla_gemm(mla_dtype_t dtype, const void* A, const void* W, float* C,
+             int32_t M, int32_t N, int32_t K,
+             void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* 2a-n: out[M, N] (dtype) = in[M, N] * rsqrt(mean(in^2) + eps) * gain[N];
+ * in float32, gain dtype.  The reference's q_lat_norm_kernel (mla_kernels.cu:377-420). */
+int mla_rmsnorm(mla_dtype_t dtype, const float* in, const void* gain, void* out,
+                int32_t M, int32_t N, double eps, hipStream_t stream);
+
+/* 2b: q_rope[B, Sq, H, rope] (dtype) = RoPE of q_raw[b*Sq+s, h*(nope+rope)+nope : +rope]
+ * (q_raw float32 [B*Sq, H*(nope+rope)]) at positions[s].
+ * The reference's q_rope_kernel (mla_kernels.cu:425-466). */
+int mla_rope(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
+             const int64_t* positions, const float* inv_freq, void* q_rope,
+             hipStream_t stream);
+
+/* 2c: q_absorbed[b, s, h, :] (dtype) = q_raw[b*Sq+s, h*(nope+rope) : +nope] @ W_uk[h].
+ * The reference's q_absorb_kernel (mla_kernels.cu:474-596). */
+int mla_absorb(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
+               const void* W_uk, void* q_absorbed, hipStream_t stream);
+
+/* 3a: for every row f = (b*Sq + s)*H + h and key k < Sk:
+ *   t = (q_absorbed[f]·c_kv[b,k] + q_rope[f]·pe_cache[b,k]) / scale
+ * and for each block j of mla_score_tile() keys: m_part[f, j] = max of t over the block's
+ * visible keys, scores[f, k] = exp(t - m_part[f, j]) (0 where masked or k >= Sk, up to
+ * ld_scores), l_part[f, j] = sum of scores over the block.  scores float32
+ * [B*Sq*H, ld_scores] with ld_scores >= mla_score_ld(Sk); m_part, l_part float32
+ * [B*Sq*H, ceil(Sk/tile)].  The reference's mla_scores_kernel (mla_kernels.cu:808-1033). */
+int mla_scores(mla_dtype_t dtype, const mla_dims_t* dims,
+               const void* q_absorbed, const void* q_rope, const void* c_kv,
+               const void* pe_cache, double scale, int causal,
+               float* scores, int32_t ld_scores, float* m_part, float* l_part,
+               hipStream_t stream);
+
+/* 3b: per row: M = max_j m_part[row, j]; alpha[row, j] = exp(m_part[row, j] - M)
+ * (exactly 1 where equal); row_sum[row] = sum_j l_part[row, j] * alpha[row, j].
+ * All float32.  The reference's mla_combine_kernel (mla_kernels.cu:1036-1081). */
+int mla_combine(const float* m_part, const float* l_part, float* alpha, float* row_sum,
+                int32_t rows, int32_t n_partials, hipStream_t stream);
+
+/* 3c: ctx[b, s, h, :] (float32) = sum_k scores[f, k] * alpha[f, k / tile] * c_kv[b, k, :]
+ * -- the unnormalised attention numerator.  scores/alpha float32, c_kv dtype.
+ * The reference's mla_ctx_kernel (mla_kernels.cu:1088-1326). */
+size_t mla_ctx_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims);
+int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores,
+            int32_t ld_scores, const float* alpha, const void* c_kv, float* ctx,
+            void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* 3d: out[b, s, h, :] (dtype) = (ctx[b, s, h, :] / row_sum[f]) @ W_uv[h]^T;
+ * ctx/row_sum float32, W_uv dtype [H, v, kv_rank].
+ * The reference's mla_output_smem_kernel (mla_kernels.cu:1339-1476). */
+size_t mla_out_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims);
+int mla_out(mla_dtype_t dtype, const mla_dims_t* dims, const float* ctx,
+            const float* row_sum, const void* W_uv, void* out,
+            void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif  /* MLA_AMD_MLA_H_ */

@@ -1,0 +1,555 @@
+// extern "C" surface of libmla_amd.so (declared in include/mla/mla.h).
+//
+// Every entry point validates its arguments completely -- dims, pointers, alignment,
+// workspace size, dtype -- before the first HIP call, so a rejected call leaves the
+// device untouched and the validation is testable on a machine without a GPU.  Kernel
+// grids are planned from the shapes alone (plan_gemm / fixed 3a tiles), so the
+// *_workspace_bytes() queries and the launches always agree.
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/mla/mla.h"
+#include "kernels.h"
+
+using namespace mla;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int ok() {
+    g_last_error.clear();
+    return MLA_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(MLA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define MLA_TRY_HIP(expr, what)                         \
+    do {                                                \
+        hipError_t e_ = (expr);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
+int cdiv(int a, int b) { return (a + b - 1) / b; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_ptr(const void* p, const char* name) {
+    if (!p) return fail(MLA_ERR_INVALID_ARGUMENT, "%s must not be NULL", name);
+    if (!aligned16(p)) return fail(MLA_ERR_INVALID_ARGUMENT, "%s must be 16-byte aligned", name);
+    return MLA_OK;
+}
+
+#define MLA_CHECK(expr)            \
+    do {                           \
+        int st_ = (expr);          \
+        if (st_ != MLA_OK) return st_; \
+    } while (0)
+
+int check_dtype(mla_dtype_t dt) {
+    if (dt == MLA_DTYPE_F32) return MLA_OK;
+    if (dt == MLA_DTYPE_BF16)
+        return fail(MLA_ERR_UNSUPPORTED, "dtype bf16 is not implemented by this build");
+    return fail(MLA_ERR_INVALID_ARGUMENT, "unknown dtype %d", (int)dt);
+}
+
+int check_pos(int64_t v, const char* name) {
+    if (v <= 0) return fail(MLA_ERR_INVALID_ARGUMENT, "%s must be positive (got %lld)", name,
+                            (long long)v);
+    return MLA_OK;
+}
+
+int check_mult4(int v, const char* name) {
+    if (v <= 0 || v % 4 != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "%s must be a positive multiple of 4 (got %d)",
+                    name, v);
+    return MLA_OK;
+}
+
+// Upper bound for any row count / flattened index the kernels form in 32-bit ints.
+constexpr int64_t kMaxI32 = 0x7fffffffLL;
+
+int check_q_dims(const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_mult4(d->hidden, "dims.hidden"));
+    MLA_CHECK(check_mult4(d->q_lora, "dims.q_lora"));
+    MLA_CHECK(check_mult4(d->nope, "dims.nope"));
+    MLA_CHECK(check_mult4(d->rope, "dims.rope"));
+    MLA_CHECK(check_mult4(d->kv_rank, "dims.kv_rank"));
+    const int64_t bq = (int64_t)d->batch * d->sq;
+    if (bq * d->heads * (int64_t)(d->nope + d->rope) > kMaxI32 ||
+        bq * d->heads * (int64_t)d->kv_rank > (int64_t)1 << 40)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    return MLA_OK;
+}
+
+int check_attn_dims(const mla_dims_t* d, int causal) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->sk, "dims.sk"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_mult4(d->rope, "dims.rope"));
+    MLA_CHECK(check_mult4(d->kv_rank, "dims.kv_rank"));
+    MLA_CHECK(check_mult4(d->v, "dims.v"));
+    if (causal && d->sk < d->sq)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "causal attention needs sk >= sq (got sk=%d, sq=%d)", d->sk, d->sq);
+    const int64_t rows = (int64_t)d->batch * d->sq * d->heads;
+    if (rows > kMaxI32 / 2) return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    if ((int64_t)d->sk > kMaxI32 / 1024)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "sk too large (%d)", d->sk);
+    return MLA_OK;
+}
+
+int check_ws(void* ws, size_t have, size_t need) {
+    if (need == 0) return MLA_OK;
+    if (!ws) return fail(MLA_ERR_WORKSPACE, "workspace is NULL but %zu bytes are required", need);
+    if (have < need)
+        return fail(MLA_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu required", have,
+                    need);
+    if ((reinterpret_cast<uintptr_t>(ws) & (kAlign - 1)) != 0)
+        return fail(MLA_ERR_WORKSPACE, "workspace must be %zu-byte aligned", kAlign);
+    return MLA_OK;
+}
+
+// ------------------------------------------------------------------ problem builders
+
+GemmProblem q_down_problem(const mla_dims_t* d, const float* x, const float* W, float* C) {
+    GemmProblem p;
+    p.A = x; p.lda = d->hidden;
+    p.B = W; p.ldb = d->q_lora;
+    p.C = C; p.ldc = d->q_lora;
+    p.M = d->batch * d->sq; p.N = d->q_lora; p.K = d->hidden;
+    return p;
+}
+
+GemmProblem q_up_problem(const mla_dims_t* d, const float* q_lat, const float* W, float* C) {
+    const int n = d->heads * (d->nope + d->rope);
+    GemmProblem p;
+    p.A = q_lat; p.lda = d->q_lora;
+    p.B = W; p.ldb = n;
+    p.C = C; p.ldc = n;
+    p.M = d->batch * d->sq; p.N = n; p.K = d->q_lora;
+    return p;
+}
+
+GemmProblem absorb_problem(const mla_dims_t* d, const float* q_raw, const float* W_uk,
+                           void* q_abs) {
+    const int qk = d->nope + d->rope;
+    GemmProblem p;
+    p.A = q_raw; p.lda = (int64_t)d->heads * qk; p.sAg = qk;
+    p.B = W_uk; p.ldb = d->kv_rank; p.sBg = (int64_t)d->nope * d->kv_rank;
+    p.C = q_abs; p.ldc = (int64_t)d->heads * d->kv_rank; p.sCg = d->kv_rank;
+    p.M = d->batch * d->sq; p.N = d->kv_rank; p.K = d->nope; p.G = d->heads;
+    return p;
+}
+
+GemmProblem ctx_problem(const mla_dims_t* d, const float* p_scores, int ld_p,
+                        const float* alpha, const float* c_kv, float* ctx) {
+    const int rows_b = d->sq * d->heads;
+    GemmProblem p;
+    p.A = p_scores; p.lda = ld_p; p.sAg = (int64_t)rows_b * ld_p;
+    p.B = c_kv; p.ldb = d->kv_rank; p.sBg = (int64_t)d->sk * d->kv_rank;
+    p.C = ctx; p.ldc = d->kv_rank; p.sCg = (int64_t)rows_b * d->kv_rank;
+    p.M = rows_b; p.N = d->kv_rank; p.K = d->sk; p.G = d->batch;
+    p.amode = kAAlpha; p.alpha = alpha; p.alpha_ld = cdiv(d->sk, kScoreTile);
+    p.alpha_tile = kScoreTile;
+    return p;
+}
+
+GemmProblem out_problem(const mla_dims_t* d, const float* ctx, const float* row_sum,
+                        const float* W_uv, void* out) {
+    GemmProblem p;
+    p.A = ctx; p.lda = (int64_t)d->heads * d->kv_rank; p.sAg = d->kv_rank;
+    p.B = W_uv; p.ldb = d->kv_rank; p.sBg = (int64_t)d->v * d->kv_rank; p.b_nt = true;
+    p.C = out; p.ldc = (int64_t)d->heads * d->v; p.sCg = d->v;
+    p.M = d->batch * d->sq; p.N = d->v; p.K = d->kv_rank; p.G = d->heads;
+    p.amode = kARowRecip; p.rs = row_sum; p.rs_m = d->heads; p.rs_g = 1;
+    return p;
+}
+
+// ------------------------------------------------------------------ workspace layouts
+
+struct QLayout {
+    GemmPlan down, up, absorb;
+    size_t off_lat_acc, off_lat, off_raw, off_up_ws, off_abs_ws, total;
+};
+
+QLayout q_layout(const mla_dims_t* d) {
+    QLayout L;
+    const size_t bq = (size_t)d->batch * d->sq;
+    const size_t n_raw = (size_t)d->heads * (d->nope + d->rope);
+    L.down = plan_gemm(q_down_problem(d, nullptr, nullptr, nullptr));
+    L.up = plan_gemm(q_up_problem(d, nullptr, nullptr, nullptr));
+    L.absorb = plan_gemm(absorb_problem(d, nullptr, nullptr, nullptr));
+    size_t o = 0;
+    L.off_lat_acc = o;  // 2a1 output or its split partials (summed by the norm kernel)
+    o = align_up(o + (size_t)L.down.split * bq * d->q_lora * sizeof(float));
+    L.off_lat = o;
+    o = align_up(o + bq * d->q_lora * sizeof(float));
+    L.off_raw = o;
+    o = align_up(o + bq * n_raw * sizeof(float));
+    L.off_up_ws = o;
+    o = align_up(o + L.up.workspace_bytes);
+    L.off_abs_ws = o;
+    o = align_up(o + L.absorb.workspace_bytes);
+    L.total = o;
+    return L;
+}
+
+struct AttnLayout {
+    int ld_p, P;
+    GemmPlan ctx, out;
+    size_t off_p, off_m, off_l, off_alpha, off_rowsum, off_ctx, off_ctx_ws, off_out_ws, total;
+};
+
+AttnLayout attn_layout(const mla_dims_t* d) {
+    AttnLayout L;
+    const size_t rows = (size_t)d->batch * d->sq * d->heads;
+    L.ld_p = mla_score_ld(d->sk);
+    L.P = cdiv(d->sk, kScoreTile);
+    L.ctx = plan_gemm(ctx_problem(d, nullptr, L.ld_p, nullptr, nullptr, nullptr));
+    L.out = plan_gemm(out_problem(d, nullptr, nullptr, nullptr, nullptr));
+    size_t o = 0;
+    L.off_p = o;      o = align_up(o + rows * L.ld_p * sizeof(float));
+    L.off_m = o;      o = align_up(o + rows * L.P * sizeof(float));
+    L.off_l = o;      o = align_up(o + rows * L.P * sizeof(float));
+    L.off_alpha = o;  o = align_up(o + rows * L.P * sizeof(float));
+    L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
+    L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
+    L.off_ctx_ws = o; o = align_up(o + L.ctx.workspace_bytes);
+    L.off_out_ws = o; o = align_up(o + L.out.workspace_bytes);
+    L.total = o;
+    return L;
+}
+
+template <typename T> T* at(void* base, size_t off) {
+    return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+// ------------------------------------------------------------------ step bodies
+
+int run_scores(const mla_dims_t* d, const void* qa, const void* qr, const void* ckv,
+               const void* pe, double scale, int causal, float* p, int ld_p, float* m_part,
+               float* l_part, hipStream_t stream) {
+    ScoresProblem sp;
+    sp.qa = static_cast<const float*>(qa);
+    sp.qr = static_cast<const float*>(qr);
+    sp.ckv = static_cast<const float*>(ckv);
+    sp.pe = static_cast<const float*>(pe);
+    sp.p = p; sp.m_part = m_part; sp.l_part = l_part;
+    sp.B = d->batch; sp.Sq = d->sq; sp.Sk = d->sk; sp.H = d->heads;
+    sp.R = d->kv_rank; sp.D = d->rope; sp.ld_p = ld_p; sp.P = cdiv(d->sk, kScoreTile);
+    sp.inv_scale = 1.0f / (float)scale;
+    sp.causal = causal != 0;
+    MLA_TRY_HIP(launch_scores(sp, stream), "scores kernel launch");
+    return MLA_OK;
+}
+
+int check_scale(double scale) {
+    if (!(scale > 0.0) || !std::isfinite(scale))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "scale must be a positive finite divisor");
+    return MLA_OK;
+}
+
+}  // namespace
+
+// ====================================================================== C ABI
+// The library is built with -fvisibility=hidden; only this block is exported.
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+const char* mla_last_error(void) { return g_last_error.c_str(); }
+const char* mla_version(void) { return "mla_amd 0.1.0 (gfx950)"; }
+int32_t mla_score_tile(void) { return kScoreTile; }
+int32_t mla_score_ld(int32_t sk) { return sk <= 0 ? 0 : ((sk + 31) / 32) * 32; }
+
+size_t mla_gemm_workspace_bytes(mla_dtype_t dtype, int32_t M, int32_t N, int32_t K) {
+    (void)dtype;
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    GemmProblem p;
+    p.M = M; p.N = N; p.K = K;
+    return plan_gemm(p).workspace_bytes;
+}
+
+int mla_gemm(mla_dtype_t dtype, const void* A, const void* W, float* C, int32_t M, int32_t N,
+             int32_t K, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_pos(M, "M"));
+    MLA_CHECK(check_mult4(N, "N"));
+    MLA_CHECK(check_mult4(K, "K"));
+    MLA_CHECK(check_ptr(A, "A"));
+    MLA_CHECK(check_ptr(W, "W"));
+    MLA_CHECK(check_ptr(C, "C"));
+    GemmProblem p;
+    p.A = static_cast<const float*>(A); p.lda = K;
+    p.B = static_cast<const float*>(W); p.ldb = N;
+    p.C = C; p.ldc = N;
+    p.M = M; p.N = N; p.K = K;
+    const GemmPlan plan = plan_gemm(p);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, plan.workspace_bytes));
+    MLA_TRY_HIP(launch_gemm(p, plan, workspace, stream), "gemm launch");
+    return ok();
+}
+
+int mla_rmsnorm(mla_dtype_t dtype, const float* in, const void* gain, void* out, int32_t M,
+                int32_t N, double eps, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_pos(M, "M"));
+    MLA_CHECK(check_mult4(N, "N"));
+    MLA_CHECK(check_ptr(in, "in"));
+    MLA_CHECK(check_ptr(gain, "gain"));
+    MLA_CHECK(check_ptr(out, "out"));
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    MLA_TRY_HIP(launch_rmsnorm(in, 1, 0, gain, out, kOutF32, M, N, (float)eps, stream),
+                "rmsnorm launch");
+    return ok();
+}
+
+int mla_rope(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
+             const int64_t* positions, const float* inv_freq, void* q_rope,
+             hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_q_dims(dims));
+    MLA_CHECK(check_ptr(q_raw, "q_raw"));
+    MLA_CHECK(check_ptr(positions, "positions"));
+    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_TRY_HIP(launch_rope(q_raw, positions, inv_freq, q_rope, kOutF32, dims->batch,
+                            dims->sq, dims->heads, dims->nope, dims->rope, stream),
+                "rope launch");
+    return ok();
+}
+
+int mla_absorb(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
+               const void* W_uk, void* q_absorbed, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_q_dims(dims));
+    MLA_CHECK(check_ptr(q_raw, "q_raw"));
+    MLA_CHECK(check_ptr(W_uk, "W_uk"));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    GemmProblem p = absorb_problem(dims, q_raw, static_cast<const float*>(W_uk), q_absorbed);
+    const GemmPlan plan = plan_gemm(p);
+    if (plan.workspace_bytes)
+        return fail(MLA_ERR_UNSUPPORTED, "absorb at this shape needs split-K; use mla_q_absorbed");
+    MLA_TRY_HIP(launch_gemm(p, plan, nullptr, stream), "absorb launch");
+    return ok();
+}
+
+int mla_scores(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+               const void* q_rope, const void* c_kv, const void* pe_cache, double scale,
+               int causal, float* scores, int32_t ld_scores, float* m_part, float* l_part,
+               hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dims, causal));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    MLA_CHECK(check_ptr(scores, "scores"));
+    MLA_CHECK(check_ptr(m_part, "m_part"));
+    MLA_CHECK(check_ptr(l_part, "l_part"));
+    if (ld_scores < mla_score_ld(dims->sk) || ld_scores % 4 != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "ld_scores must be a multiple of 4 and >= mla_score_ld(sk)=%d (got %d)",
+                    mla_score_ld(dims->sk), ld_scores);
+    MLA_CHECK(run_scores(dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, scores,
+                         ld_scores, m_part, l_part, stream));
+    return ok();
+}
+
+int mla_combine(const float* m_part, const float* l_part, float* alpha, float* row_sum,
+                int32_t rows, int32_t n_partials, hipStream_t stream) {
+    MLA_CHECK(check_pos(rows, "rows"));
+    MLA_CHECK(check_pos(n_partials, "n_partials"));
+    MLA_CHECK(check_ptr(m_part, "m_part"));
+    MLA_CHECK(check_ptr(l_part, "l_part"));
+    MLA_CHECK(check_ptr(alpha, "alpha"));
+    MLA_CHECK(check_ptr(row_sum, "row_sum"));
+    MLA_TRY_HIP(launch_combine(m_part, l_part, alpha, row_sum, rows, n_partials, stream),
+                "combine launch");
+    return ok();
+}
+
+size_t mla_ctx_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
+    (void)dtype;
+    if (!dims || check_attn_dims(dims, 0) != MLA_OK) return 0;
+    return plan_gemm(ctx_problem(dims, nullptr, mla_score_ld(dims->sk), nullptr, nullptr,
+                                 nullptr)).workspace_bytes;
+}
+
+int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores, int32_t ld_scores,
+            const float* alpha, const void* c_kv, float* ctx, void* workspace,
+            size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dims, 0));
+    MLA_CHECK(check_ptr(scores, "scores"));
+    MLA_CHECK(check_ptr(alpha, "alpha"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(ctx, "ctx"));
+    if (ld_scores < mla_score_ld(dims->sk) || ld_scores % 4 != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "ld_scores must be a multiple of 4 and >= mla_score_ld(sk)=%d (got %d)",
+                    mla_score_ld(dims->sk), ld_scores);
+    GemmProblem p = ctx_problem(dims, scores, ld_scores, alpha,
+                                static_cast<const float*>(c_kv), ctx);
+    const GemmPlan plan = plan_gemm(p);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, plan.workspace_bytes));
+    MLA_TRY_HIP(launch_gemm(p, plan, workspace, stream), "ctx launch");
+    return ok();
+}
+
+size_t mla_out_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
+    (void)dtype;
+    if (!dims || check_attn_dims(dims, 0) != MLA_OK) return 0;
+    return plan_gemm(out_problem(dims, nullptr, nullptr, nullptr, nullptr)).workspace_bytes;
+}
+
+int mla_out(mla_dtype_t dtype, const mla_dims_t* dims, const float* ctx, const float* row_sum,
+            const void* W_uv, void* out, void* workspace, size_t workspace_bytes,
+            hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dims, 0));
+    MLA_CHECK(check_ptr(ctx, "ctx"));
+    MLA_CHECK(check_ptr(row_sum, "row_sum"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    GemmProblem p = out_problem(dims, ctx, row_sum, static_cast<const float*>(W_uv), out);
+    const GemmPlan plan = plan_gemm(p);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, plan.workspace_bytes));
+    MLA_TRY_HIP(launch_gemm(p, plan, workspace, stream), "out launch");
+    return ok();
+}
+
+size_t mla_q_absorbed_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
+    (void)dtype;
+    if (!dims || check_q_dims(dims) != MLA_OK) return 0;
+    return q_layout(dims).total;
+}
+
+int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_q_a,
+                   const void* q_norm_w, const void* W_q_b, const void* W_uk,
+                   const int64_t* positions, const float* inv_freq, double eps,
+                   void* q_absorbed, void* q_rope, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_q_dims(dims));
+    MLA_CHECK(check_ptr(x, "x"));
+    MLA_CHECK(check_ptr(W_q_a, "W_q_a"));
+    MLA_CHECK(check_ptr(q_norm_w, "q_norm_w"));
+    MLA_CHECK(check_ptr(W_q_b, "W_q_b"));
+    MLA_CHECK(check_ptr(W_uk, "W_uk"));
+    MLA_CHECK(check_ptr(positions, "positions"));
+    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    const QLayout L = q_layout(dims);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+
+    const int bq = dims->batch * dims->sq;
+    float* lat_acc = at<float>(workspace, L.off_lat_acc);
+    float* lat = at<float>(workspace, L.off_lat);
+    float* raw = at<float>(workspace, L.off_raw);
+
+    // 2a1: split-K partials land in lat_acc[split][bq][q_lora]; 2a-n sums them.
+    GemmProblem down = q_down_problem(dims, static_cast<const float*>(x),
+                                      static_cast<const float*>(W_q_a), lat_acc);
+    GemmPlan down_plan = L.down;
+    int nsplit = 1;
+    if (down_plan.split > 1) {
+        nsplit = down_plan.split;
+        down_plan.workspace_bytes = 0;
+        MLA_TRY_HIP(launch_gemm_partials(down, down_plan, lat_acc, stream), "2a1 launch");
+    } else {
+        MLA_TRY_HIP(launch_gemm(down, down_plan, nullptr, stream), "2a1 launch");
+    }
+    // 2a-n
+    MLA_TRY_HIP(launch_rmsnorm(lat_acc, nsplit, (int64_t)bq * dims->q_lora, q_norm_w, lat,
+                               kOutF32, bq, dims->q_lora, (float)eps, stream),
+                "2a-n launch");
+    // 2a2
+    GemmProblem up = q_up_problem(dims, lat, static_cast<const float*>(W_q_b), raw);
+    MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
+    // 2b
+    MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, kOutF32, dims->batch, dims->sq,
+                            dims->heads, dims->nope, dims->rope, stream),
+                "2b launch");
+    // 2c
+    GemmProblem ab = absorb_problem(dims, raw, static_cast<const float*>(W_uk), q_absorbed);
+    MLA_TRY_HIP(launch_gemm(ab, L.absorb, at<void>(workspace, L.off_abs_ws), stream),
+                "2c launch");
+    return ok();
+}
+
+size_t mla_attention_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal) {
+    (void)dtype;
+    if (!dims || check_attn_dims(dims, causal) != MLA_OK) return 0;
+    return attn_layout(dims).total;
+}
+
+int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                  const void* q_rope, const void* c_kv, const void* pe_cache, const void* W_uv,
+                  double scale, int causal, void* out, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dims, causal));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const AttnLayout L = attn_layout(dims);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+
+    float* p = at<float>(workspace, L.off_p);
+    float* m = at<float>(workspace, L.off_m);
+    float* l = at<float>(workspace, L.off_l);
+    float* alpha = at<float>(workspace, L.off_alpha);
+    float* row_sum = at<float>(workspace, L.off_rowsum);
+    float* ctx = at<float>(workspace, L.off_ctx);
+    const int rows = dims->batch * dims->sq * dims->heads;
+
+    // 3a
+    MLA_CHECK(run_scores(dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, p, L.ld_p, m,
+                         l, stream));
+    // 3b
+    MLA_TRY_HIP(launch_combine(m, l, alpha, row_sum, rows, L.P, stream), "3b launch");
+    // 3c
+    GemmProblem cp = ctx_problem(dims, p, L.ld_p, alpha, static_cast<const float*>(c_kv), ctx);
+    MLA_TRY_HIP(launch_gemm(cp, L.ctx, at<void>(workspace, L.off_ctx_ws), stream), "3c launch");
+    // 3d
+    GemmProblem op = out_problem(dims, ctx, row_sum, static_cast<const float*>(W_uv), out);
+    MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
+    return ok();
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

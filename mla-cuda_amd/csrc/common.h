@@ -1,0 +1,99 @@
+// Device-side building blocks shared by every gfx950 kernel of the layer:
+// MFMA fragment types, wave64 reductions on DPP / ds_swizzle, XCD-aware block order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace mla {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;      // CDNA wavefront width
+constexpr int kNumCUs = 256;   // MI355X: 8 XCDs x 32 CUs
+constexpr int kNumXCDs = 8;
+
+// ----------------------------------------------------------------------------------
+// fp32 MFMA: D(32x32) += A(32x2) * B(2x32).  Lane l supplies A[l%32][l/32] and
+// B[l/32][l%32]; accumulator i of lane l is D[8*(i/4) + 4*(l/32) + i%4][l%32].
+// The kernels drive four of these per 8-deep slice and permute K so that lane l's four
+// A (or B) values are k = 4*(l/32) + 0..3: one 128-bit LDS read feeds four MFMAs.
+// ----------------------------------------------------------------------------------
+__device__ __forceinline__ v16f mfma_32x32x2(float a, float b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ int acc_row(int i, int lane) {
+    return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+}
+
+// ----------------------------------------------------------------------------------
+// Wave reductions.  Steps 1..8 move data with DPP (quad_perm, row_half_mirror,
+// row_mirror); step 16 with ds_swizzle's bitmask mode; the two 32-lane halves meet
+// through readlane.  Each step leaves the partial result in every lane of its group.
+// ----------------------------------------------------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF,
+                                                      false));
+}
+__device__ __forceinline__ float swizzle_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+
+struct OpMax {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct OpSum {
+    __device__ float operator()(float a, float b) const { return a + b; }
+};
+
+// Reduce across the 32 lanes of each half-wave; every lane gets its half's result.
+template <class Op>
+__device__ __forceinline__ float half_wave_reduce(float v, Op op) {
+    v = op(v, dpp_move<0xB1>(v));   // quad_perm [1,0,3,2]  (lane ^ 1)
+    v = op(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]  (lane ^ 2)
+    v = op(v, dpp_move<0x141>(v));  // row_half_mirror      (other quad of 8)
+    v = op(v, dpp_move<0x140>(v));  // row_mirror           (other half of 16)
+    v = op(v, swizzle_xor16(v));    // ds_swizzle xor 16    (other row of 32)
+    return v;
+}
+
+// Reduce across the whole wave; the result is wave-uniform.
+template <class Op>
+__device__ __forceinline__ float wave_reduce(float v, Op op) {
+    v = half_wave_reduce(v, op);
+    const float lo = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float hi = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    return op(lo, hi);
+}
+
+// ----------------------------------------------------------------------------------
+// XCD-aware block order.  The dispatcher hands workgroup b to XCD b % 8; this maps the
+// hardware id to a logical tile id so that each XCD walks a CONTIGUOUS run of logical
+// tiles (and therefore keeps the operands those tiles share in its own L2).
+// ----------------------------------------------------------------------------------
+__device__ __forceinline__ int xcd_logical_block(int bid, int nblocks) {
+    const int q = nblocks / kNumXCDs;
+    const int r = nblocks % kNumXCDs;
+    const int x = bid % kNumXCDs;
+    const int s = bid / kNumXCDs;
+    return x * q + (x < r ? x : r) + s;
+}
+
+// ----------------------------------------------------------------------------------
+// Element conversion helpers
+// ----------------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return __bfloat162float(v); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
+    return __float2bfloat16(v);
+}
+
+}  // namespace mla

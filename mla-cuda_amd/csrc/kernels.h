@@ -1,0 +1,78 @@
+// Host-side launch interface of the gfx950 kernels (internal to libmla_amd.so).
+// Every launcher assumes its arguments were validated by the C ABI layer (abi.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mla {
+
+// ---------------------------------------------------------------- batched MFMA GEMM
+// C[g][m][n] = sum_k opA(A)[g][m][k] * opB(B)[g][k][n]   (float32 in, float32 accumulate)
+//   A[g][m][k]  at A + g*sAg + m*lda + k
+//   B (NN)      at B + g*sBg + k*ldb + n      B (NT) at B + g*sBg + n*ldb + k
+//   C[g][m][n]  at C + g*sCg + m*ldc + n
+// A modes: kAPlain; kARowRecip (row m of batch g scaled by 1/rs[m*rs_m + g*rs_g]);
+//          kAAlpha (A[g][m][k] scaled by alpha[(g*M + m)*alpha_ld + k/alpha_tile]).
+enum AMode { kAPlain = 0, kARowRecip = 1, kAAlpha = 2 };
+enum OutType { kOutF32 = 0, kOutBF16 = 1 };
+
+struct GemmProblem {
+    const float* A = nullptr; int64_t lda = 0, sAg = 0;
+    const float* B = nullptr; int64_t ldb = 0, sBg = 0;
+    void* C = nullptr;        int64_t ldc = 0, sCg = 0;
+    int M = 0, N = 0, K = 0, G = 1;
+    bool b_nt = false;
+    AMode amode = kAPlain;
+    const float* rs = nullptr; int64_t rs_m = 0, rs_g = 0;
+    const float* alpha = nullptr; int alpha_ld = 0, alpha_tile = 1;
+    OutType out_type = kOutF32;
+};
+
+// Tile/split plan chosen for a problem (pure function of the shape; see plan_gemm).
+struct GemmPlan {
+    int bm = 128, bn = 128;   // workgroup tile
+    int split = 1;            // K slices
+    int k_chunk = 0;          // K elements per slice (multiple of 32)
+    size_t workspace_bytes = 0;  // fp32 partials when split > 1
+};
+
+GemmPlan plan_gemm(const GemmProblem& p);
+hipError_t launch_gemm(const GemmProblem& p, const GemmPlan& plan, void* workspace,
+                       hipStream_t stream);
+// Split-K slices only (plan.split > 1): fp32 partials [split][G][M][N] into `partials`,
+// left for the consumer to sum (2a-n sums 2a1's partials while it normalises).
+hipError_t launch_gemm_partials(const GemmProblem& p, const GemmPlan& plan, float* partials,
+                                hipStream_t stream);
+
+// ---------------------------------------------------------------- row kernels
+// 2a-n: out[m][:] = sum_s in[s][m][:] * rsqrt(mean((sum_s in)^2) + eps) * gain
+hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride,
+                          const void* gain, void* out, OutType out_type, int M, int N,
+                          float eps, hipStream_t stream);
+// 2b
+hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
+                       void* q_rope, OutType out_type, int B, int Sq, int H, int nope,
+                       int rope, hipStream_t stream);
+// 3b
+hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
+                          float* row_sum, int rows, int P, hipStream_t stream);
+
+// ---------------------------------------------------------------- 3a scores
+struct ScoresProblem {
+    const float* qa = nullptr;   // [B*Sq*H, R]
+    const float* qr = nullptr;   // [B*Sq*H, D]
+    const float* ckv = nullptr;  // [B, Sk, R]
+    const float* pe = nullptr;   // [B, Sk, D]
+    float* p = nullptr;          // [B*Sq*H, ld_p]
+    float* m_part = nullptr;     // [B*Sq*H, P]
+    float* l_part = nullptr;
+    int B = 0, Sq = 0, Sk = 0, H = 0, R = 0, D = 0, ld_p = 0, P = 0;
+    float inv_scale = 1.f;
+    bool causal = false;
+};
+hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream);
+
+constexpr int kScoreTile = 128;  // keys per softmax partial (one 3a workgroup's key tile)
+
+}  // namespace mla

@@ -1,0 +1,164 @@
+// Row-wise steps of the layer: 2a-n RMSNorm, 2b RoPE, 3b softmax-partial combine.
+// All three are HBM/latency bound and tiny next to the contractions; they use 128-bit
+// loads where the row is contiguous and wave64 DPP reductions.
+
+#include "common.h"
+#include "kernels.h"
+
+#include <algorithm>
+
+namespace mla {
+
+namespace {
+
+// ---- 2a-n: one 256-thread workgroup per row.  The input may be nsplit fp32 partial
+// sums of 2a1 (split-K); they are added here in slice order, which is what makes the
+// split-K of 2a1 free of a separate reduction pass.
+template <int OUT>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ in, int nsplit,
+                                                      int64_t split_stride, const void* gain_v,
+                                                      void* out_v, int N, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int n4 = N >> 2;
+    const float* base = in + (int64_t)row * N;
+
+    auto load4 = [&](int c4) {
+        v4f v = *reinterpret_cast<const v4f*>(base + 4 * c4);
+        for (int s = 1; s < nsplit; ++s)
+            v += *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
+        return v;
+    };
+
+    float ss = 0.f;
+    for (int c4 = tid; c4 < n4; c4 += 256) {
+        const v4f v = load4(c4);
+        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    }
+    ss = wave_reduce(ss, OpSum());
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float total = red[0] + red[1] + red[2] + red[3];
+    const float inv = rsqrtf(total / (float)N + eps);
+
+    for (int c4 = tid; c4 < n4; c4 += 256) {
+        const v4f v = load4(c4);
+        if (OUT == kOutF32) {
+            const v4f g = *reinterpret_cast<const v4f*>(static_cast<const float*>(gain_v) + 4 * c4);
+            v4f o;
+            #pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = v[j] * inv * g[j];
+            *reinterpret_cast<v4f*>(static_cast<float*>(out_v) + (int64_t)row * N + 4 * c4) = o;
+        } else {
+            const __hip_bfloat16* g = static_cast<const __hip_bfloat16*>(gain_v) + 4 * c4;
+            __hip_bfloat16* o = static_cast<__hip_bfloat16*>(out_v) + (int64_t)row * N + 4 * c4;
+            #pragma unroll
+            for (int j = 0; j < 4; ++j) o[j] = __float2bfloat16(v[j] * inv * __bfloat162float(g[j]));
+        }
+    }
+}
+
+// ---- 2b: one thread per (row, head, rotary pair).  Angle = float(pos) * inv_freq[i] in
+// fp32 with the caller's inv_freq table; accurate cosf/sinf (not the fast intrinsics): at
+// positions ~5e3 an angle ulp is ~5e-4 rad, so the table and the multiply must match the
+// oracle bit for bit and the trig functions must be accurate.
+template <int OUT>
+__global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_raw,
+                                                   const int64_t* __restrict__ positions,
+                                                   const float* __restrict__ inv_freq,
+                                                   void* out_v, int total, int Sq, int H,
+                                                   int nope, int rope) {
+    const int half = rope >> 1;
+    const int qk = nope + rope;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += gridDim.x * blockDim.x) {
+        const int i = idx % half;
+        const int rh = idx / half;        // (bq, h)
+        const int h = rh % H;
+        const int bq = rh / H;
+        const int s = bq % Sq;
+        const float2 x = *reinterpret_cast<const float2*>(
+            q_raw + (int64_t)bq * H * qk + (int64_t)h * qk + nope + 2 * i);
+        const float ang = (float)positions[s] * inv_freq[i];
+        const float c = cosf(ang), sn = sinf(ang);
+        const float e = x.x * c - x.y * sn;
+        const float o = x.x * sn + x.y * c;
+        const int64_t dst = (int64_t)rh * rope + 2 * i;
+        if (OUT == kOutF32) {
+            *reinterpret_cast<float2*>(static_cast<float*>(out_v) + dst) = make_float2(e, o);
+        } else {
+            __hip_bfloat16* op = static_cast<__hip_bfloat16*>(out_v) + dst;
+            op[0] = __float2bfloat16(e);
+            op[1] = __float2bfloat16(o);
+        }
+    }
+}
+
+// ---- 3b: one wave per row.  M = max_j m_j; alpha_j = exp(m_j - M), exactly 1 where
+// m_j == M (which also keeps an all-masked partial at -inf from producing NaN);
+// row_sum = sum_j l_j alpha_j.  Rows are contiguous, so the lanes' loads coalesce.
+__global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ m_part,
+                                                      const float* __restrict__ l_part,
+                                                      float* __restrict__ alpha,
+                                                      float* __restrict__ row_sum, int rows,
+                                                      int P) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const float* mr = m_part + (int64_t)row * P;
+    const float* lr = l_part + (int64_t)row * P;
+    float* ar = alpha + (int64_t)row * P;
+    float m = -INFINITY;
+    for (int j = lane; j < P; j += 64) m = fmaxf(m, mr[j]);
+    const float M = wave_reduce(m, OpMax());
+    float l = 0.f;
+    for (int j = lane; j < P; j += 64) {
+        const float mj = mr[j];
+        const float aj = (mj == M) ? 1.f : expf(mj - M);
+        ar[j] = aj;
+        l += lr[j] * aj;
+    }
+    l = wave_reduce(l, OpSum());
+    if (lane == 0) row_sum[row] = l;
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, const void* gain,
+                          void* out, OutType out_type, int M, int N, float eps,
+                          hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    if (out_type == kOutF32)
+        hipLaunchKernelGGL(rmsnorm_kernel<kOutF32>, dim3(M), dim3(256), 0, stream, in, nsplit,
+                           split_stride, gain, out, N, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<kOutBF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
+                           split_stride, gain, out, N, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
+                       void* q_rope, OutType out_type, int B, int Sq, int H, int nope, int rope,
+                       hipStream_t stream) {
+    const int64_t total = (int64_t)B * Sq * H * (rope / 2);
+    if (total <= 0) return hipSuccess;
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16 * kNumCUs);
+    if (out_type == kOutF32)
+        hipLaunchKernelGGL(rope_kernel<kOutF32>, dim3(blocks), dim3(256), 0, stream, q_raw,
+                           positions, inv_freq, q_rope, (int)total, Sq, H, nope, rope);
+    else
+        hipLaunchKernelGGL(rope_kernel<kOutBF16>, dim3(blocks), dim3(256), 0, stream, q_raw,
+                           positions, inv_freq, q_rope, (int)total, Sq, H, nope, rope);
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
+                          float* row_sum, int rows, int P, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(combine_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, m_part,
+                       l_part, alpha, row_sum, rows, P);
+    return hipGetLastError();
+}
+
+}  // namespace mla

@@ -1,0 +1,62 @@
+"""Brute-force scalar-loop restatement of the absorbed MLA layer, for tiny shapes only.
+
+Independent of ``oracle/mla_ref.py`` (no torch ops, no shared helpers): plain Python floats
+(IEEE double) and ``math`` functions, written straight from the mathematics of
+exhaustive_benchmark_suite.py:210-304.  Used to pin the oracle.
+"""
+
+from __future__ import annotations
+
+import math
+
+
+def rope_angles(pos, rope_dim, base=10000.0):
+    return [pos / (base ** ((2 * i) / rope_dim)) for i in range(rope_dim // 2)]
+
+
+def layer(x, W_q_a, gain, W_q_b, wkv_b, c_kv, pe, positions, H, nope, rope, v,
+          eps=1e-6, causal=False, scale=None):
+    """All arguments are nested Python lists (fp64 values).  Returns out[b][s][h][d]."""
+    B, Sq, hidden = len(x), len(x[0]), len(x[0][0])
+    q_lora = len(gain)
+    R = len(c_kv[0][0])
+    Sk = len(c_kv[0])
+    qk = nope + rope
+    if scale is None:
+        scale = math.sqrt(qk)
+    out = [[[[0.0] * v for _ in range(H)] for _ in range(Sq)] for _ in range(B)]
+    for b in range(B):
+        for s in range(Sq):
+            lat = [sum(x[b][s][c] * W_q_a[c][j] for c in range(hidden)) for j in range(q_lora)]
+            ms = sum(t * t for t in lat) / q_lora
+            inv = 1.0 / math.sqrt(ms + eps)
+            lat = [lat[j] * inv * gain[j] for j in range(q_lora)]
+            q = [sum(lat[j] * W_q_b[j][n] for j in range(q_lora)) for n in range(H * qk)]
+            ang = rope_angles(float(positions[s]), rope)
+            for h in range(H):
+                qh = q[h * qk:(h + 1) * qk]
+                qn, qp = qh[:nope], qh[nope:]
+                # RoPE on interleaved pairs
+                qr = [0.0] * rope
+                for i in range(rope // 2):
+                    e, o = qp[2 * i], qp[2 * i + 1]
+                    c_, s_ = math.cos(ang[i]), math.sin(ang[i])
+                    qr[2 * i] = e * c_ - o * s_
+                    qr[2 * i + 1] = e * s_ + o * c_
+                # absorption with W_uk = wkv_b[h][:nope]
+                qa = [sum(qn[i] * wkv_b[h][i][r] for i in range(nope)) for r in range(R)]
+                # scores over visible keys
+                lim = Sk - Sq + s if causal else Sk - 1
+                sc = []
+                for k in range(lim + 1):
+                    dot = sum(qa[r] * c_kv[b][k][r] for r in range(R))
+                    dot += sum(qr[d] * pe[b][k][d] for d in range(rope))
+                    sc.append(dot / scale)
+                mx = max(sc)
+                ex = [math.exp(t - mx) for t in sc]
+                den = sum(ex)
+                ctx = [sum(ex[k] / den * c_kv[b][k][r] for k in range(len(ex)))
+                       for r in range(R)]
+                for d in range(v):
+                    out[b][s][h][d] = sum(ctx[r] * wkv_b[h][nope + d][r] for r in range(R))
+    return out

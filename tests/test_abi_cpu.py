@@ -1,0 +1,228 @@
+"""CPU-only checks of the drop-in boundary: the C ABI library and the torch binding.
+
+No test here launches device work.  Every call below is rejected by argument validation,
+which the C ABI performs completely before its first HIP call (so these run on a machine
+without a GPU), or is a pure host query (workspace sizes, score layout).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mla", "mla.h")
+LIB = os.path.join(ROOT, "mla-cuda_amd", "libmla_amd.so")
+
+MLA_OK, MLA_ERR_INVALID_ARGUMENT, MLA_ERR_UNSUPPORTED, MLA_ERR_WORKSPACE, MLA_ERR_HIP = range(5)
+F32, BF16 = 0, 1
+
+
+class Dims(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int32) for n in
+                ("batch", "sq", "sk", "hidden", "q_lora", "heads", "nope", "rope", "kv_rank", "v")]
+
+
+def dsv3(B=1, Sq=1, Sk=512):
+    return Dims(B, Sq, Sk, 7168, 1536, 128, 128, 64, 512, 128)
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built: run `python -c 'import __graft_entry__ as g; g.build()'`")
+    L = ctypes.CDLL(LIB)
+    L.mla_last_error.restype = ctypes.c_char_p
+    L.mla_version.restype = ctypes.c_char_p
+    for n in ("mla_q_absorbed_workspace_bytes", "mla_attention_workspace_bytes",
+              "mla_gemm_workspace_bytes", "mla_ctx_workspace_bytes", "mla_out_workspace_bytes"):
+        getattr(L, n).restype = ctypes.c_size_t
+    return L
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mla_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    names = header_functions()
+    for must in ("mla_q_absorbed", "mla_attention", "mla_gemm", "mla_rmsnorm", "mla_rope",
+                 "mla_absorb", "mla_scores", "mla_combine", "mla_ctx", "mla_out",
+                 "mla_last_error"):
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in mla.h but not exported"
+
+
+def test_library_exports_only_the_abi():
+    out = os.popen(f"nm -D --defined-only {LIB}").read()
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert exported == set(header_functions())
+
+
+def test_version_and_layout_queries(lib):
+    assert b"gfx950" in lib.mla_version()
+    assert lib.mla_score_tile() == 128
+    assert lib.mla_score_ld(4989) == 4992
+    assert lib.mla_score_ld(32) == 32 and lib.mla_score_ld(33) == 64
+    assert lib.mla_score_ld(0) == 0
+
+
+def test_workspace_queries_are_pure_host(lib):
+    d = dsv3(128, 1, 4989)
+    wq = lib.mla_q_absorbed_workspace_bytes(F32, ctypes.byref(d))
+    wa = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0)
+    rows = 128 * 128
+    # scores [rows, 4992] fp32 alone is 327 MB
+    assert wa >= rows * 4992 * 4 + rows * 512 * 4
+    assert wa < rows * 4992 * 4 * 1.3
+    # q path: q_lat, q_raw at least
+    assert wq >= 128 * (1536 + 128 * 192) * 4
+    bad = dsv3(0, 1, 4989)
+    assert lib.mla_attention_workspace_bytes(F32, ctypes.byref(bad), 0) == 0
+
+
+def _err(lib):
+    return lib.mla_last_error().decode()
+
+
+P16 = ctypes.c_void_p(1 << 20)   # aligned fake device pointer (never dereferenced)
+P_ODD = ctypes.c_void_p((1 << 20) + 4)
+
+
+def test_gemm_validation(lib):
+    st = lib.mla_gemm(F32, P16, P16, P16, 0, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "M must be positive" in _err(lib)
+    st = lib.mla_gemm(F32, P16, P16, P16, 4, 18, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "N must be a positive multiple of 4" in _err(lib)
+    st = lib.mla_gemm(F32, None, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "A must not be NULL" in _err(lib)
+    st = lib.mla_gemm(F32, P_ODD, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "16-byte aligned" in _err(lib)
+    st = lib.mla_gemm(7, P16, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "unknown dtype" in _err(lib)
+
+
+def test_gemm_split_needs_workspace(lib):
+    need = lib.mla_gemm_workspace_bytes(F32, 1, 1536, 7168)
+    assert need > 0, "B=1 2a1 is split over K"
+    st = lib.mla_gemm(F32, P16, P16, P16, 1, 1536, 7168, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_WORKSPACE and "workspace is NULL" in _err(lib)
+    st = lib.mla_gemm(F32, P16, P16, P16, 1, 1536, 7168, P16, ctypes.c_size_t(need - 1), None)
+    assert st == MLA_ERR_WORKSPACE and "too small" in _err(lib)
+
+
+def test_attention_validation(lib):
+    d = dsv3(2, 3, 2)
+    args = [P16] * 5
+    st = lib.mla_attention(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 1, P16, P16,
+                           ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "sk >= sq" in _err(lib)
+    d = dsv3(2, 1, 100)
+    st = lib.mla_attention(F32, ctypes.byref(d), *args, ctypes.c_double(0.0), 0, P16, P16,
+                           ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "scale" in _err(lib)
+    st = lib.mla_attention(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, None,
+                           ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_WORKSPACE
+    d.kv_rank = 510
+    st = lib.mla_attention(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, P16,
+                           ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "kv_rank" in _err(lib)
+    st = lib.mla_attention(F32, None, *args, ctypes.c_double(13.85), 0, P16, P16,
+                           ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "dims" in _err(lib)
+
+
+def test_q_absorbed_validation(lib):
+    d = dsv3(1, 1, 1)
+    d.rope = 6
+    ptrs = [P16] * 7
+    st = lib.mla_q_absorbed(F32, ctypes.byref(d), *ptrs, ctypes.c_double(1e-6), P16, P16, P16,
+                            ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "rope" in _err(lib)
+    d.rope = 64
+    st = lib.mla_q_absorbed(F32, ctypes.byref(d), *ptrs, ctypes.c_double(-1.0), P16, P16, P16,
+                            ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "eps" in _err(lib)
+
+
+def test_scores_validation(lib):
+    d = dsv3(1, 1, 100)
+    st = lib.mla_scores(F32, ctypes.byref(d), P16, P16, P16, P16, ctypes.c_double(13.8), 0,
+                        P16, 100, P16, P16, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "ld_scores" in _err(lib)
+
+
+# ------------------------------------------------------------------ torch binding
+
+
+@pytest.fixture(scope="module")
+def ext():
+    import mla_custom_cuda
+    return mla_custom_cuda
+
+
+def test_binding_surface(ext):
+    for name in ("q_absorbed", "mla_attention", "gemm", "rmsnorm", "rope", "absorb", "scores",
+                 "combine", "ctx", "out", "rope_inv_freq"):
+        assert callable(getattr(ext, name))
+
+
+def test_binding_inv_freq_matches_oracle_bitwise(ext):
+    from oracle import mla_ref as R
+    for rope in (64, 16, 128):
+        assert torch.equal(ext.rope_inv_freq(rope), R.rope_inv_freq(rope, torch.float32))
+
+
+def _attn(B=1, Sq=1, Sk=8, H=4, Rk=16, D=8, V=8, dtype=torch.float32):
+    return (torch.zeros(B, Sq, H, Rk, dtype=dtype), torch.zeros(B, Sq, H, D, dtype=dtype),
+            torch.zeros(B, Sk, Rk, dtype=dtype), torch.zeros(B, Sk, D, dtype=dtype),
+            torch.zeros(H, V, Rk, dtype=dtype))
+
+
+def test_binding_attention_shape_errors(ext):
+    qa, qr, ck, pe, wuv = _attn()
+    with pytest.raises(RuntimeError, match="c_kv must be"):
+        ext.mla_attention(qa, qr, ck[:, :, :8], pe, wuv, 1.0)
+    with pytest.raises(RuntimeError, match="pe_cache must be"):
+        ext.mla_attention(qa, qr, ck, pe[:, :4], wuv, 1.0)
+    with pytest.raises(RuntimeError, match="W_uv must be"):
+        ext.mla_attention(qa, qr, ck, pe, wuv[:2], 1.0)
+    with pytest.raises(RuntimeError, match="q_absorbed must be"):
+        ext.mla_attention(qa[0], qr, ck, pe, wuv, 1.0)
+    with pytest.raises(RuntimeError, match="dtype"):
+        ext.mla_attention(qa.double(), qr.double(), ck.double(), pe.double(), wuv.double(), 1.0)
+    with pytest.raises(RuntimeError, match="c_kv has dtype"):
+        ext.mla_attention(qa, qr, ck.bfloat16(), pe, wuv, 1.0)
+    with pytest.raises(RuntimeError, match="causal attention needs Sk >= Sq"):
+        a = _attn(Sq=9, Sk=8)
+        ext.mla_attention(*a, 1.0, True)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        ext.mla_attention(qa, qr, ck, pe, wuv, 1.0)
+
+
+def test_binding_q_absorbed_shape_errors(ext):
+    x = torch.zeros(2, 1, 64)
+    wa, g = torch.zeros(64, 32), torch.zeros(32)
+    wb, wuk = torch.zeros(32, 4 * 24), torch.zeros(4, 16, 16)
+    pos = torch.zeros(1, dtype=torch.int64)
+    with pytest.raises(RuntimeError, match="W_q_a must be"):
+        ext.q_absorbed(x, wa[:60], g, wb, wuk, pos, 16, 8, 1e-6)
+    with pytest.raises(RuntimeError, match="W_q_b must be"):
+        ext.q_absorbed(x, wa, g, wb[:, :90], wuk, pos, 16, 8, 1e-6)
+    with pytest.raises(RuntimeError, match="q_norm_w must be"):
+        ext.q_absorbed(x, wa, g[:31], wb, wuk, pos, 16, 8, 1e-6)
+    with pytest.raises(RuntimeError, match="positions must be"):
+        ext.q_absorbed(x, wa, g, wb, wuk, torch.zeros(2, dtype=torch.int64), 16, 8, 1e-6)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        ext.q_absorbed(x, wa, g, wb, wuk, pos, 16, 8, 1e-6)

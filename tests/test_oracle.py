@@ -1,0 +1,273 @@
+"""Pin the CPU oracle (oracle/mla_ref.py) before any GPU result is compared with it.
+
+The reference commits no golden vectors or known-answer tests, and its CUDA build and
+Python oracle cannot run here.  Each oracle function is therefore pinned by checks the
+mathematics fixes:
+
+* the whole layer against an independent scalar-loop brute force (tests/brute_mla.py)
+  on tiny shapes, both non-causal and causal, and against the committed fixtures that
+  brute force wrote (tests/golden/*.npz);
+* RoPE against the closed-form rotation, the identity at position 0 and norm
+  preservation; RMSNorm against the unit-RMS property;
+* the nine-step decomposition (split softmax of 3a/3b, unnormalised ctx of 3c, deferred
+  divide of 3d) against the direct formulation in fp64;
+* softmax normalisation, causal Sq=1 == non-causal, causal Sq=Sk == lower triangle.
+
+``test_planted_mistakes_are_caught`` plants plausible mistakes in the oracle (a dropped
+gain, swapped W_uk/W_uv, non-interleaved RoPE pairs, a multiplied scale, an off-by-one
+causal limit, a dropped alpha) and shows the brute-force comparison rejects every one.
+"""
+
+from __future__ import annotations
+
+import glob
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import brute_mla
+from oracle import mla_ref as R
+
+TINY = R.MLADims(hidden=6, n_heads=2, q_lora=4, kv_rank=4, nope=2, rope=4, v=3)
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _brute(inp, dims, causal):
+    return torch.tensor(brute_mla.layer(
+        inp["x"].tolist(), inp["W_q_a"].tolist(), inp["q_norm_w"].tolist(),
+        inp["W_q_b"].tolist(), inp["wkv_b"].tolist(), inp["c_kv"].tolist(),
+        inp["pe_cache"].tolist(), inp["positions"].tolist(), dims.n_heads, dims.nope,
+        dims.rope, dims.v, causal=causal), dtype=torch.float64)
+
+
+def _oracle(inp, dims, causal):
+    return R.mla_layer(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"], inp["wkv_b"],
+                       inp["c_kv"], inp["pe_cache"], inp["positions"], dims, causal=causal)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(2, 3, 5), (1, 1, 7), (3, 2, 2)])
+def test_layer_matches_brute_force(shape, causal):
+    B, Sq, Sk = shape
+    inp = R.make_inputs(B, Sq, Sk, TINY, seed=3, dtype=torch.float64)
+    got = _oracle(inp, TINY, causal)
+    ref = _brute(inp, TINY, causal)
+    assert got.shape == (B, Sq, TINY.n_heads, TINY.v)
+    torch.testing.assert_close(got, ref, rtol=1e-11, atol=1e-12)
+
+
+def test_layer_matches_brute_force_large_positions():
+    inp = R.make_inputs(1, 2, 6, TINY, seed=4, dtype=torch.float64)
+    inp["positions"] = torch.tensor([4988, 65535], dtype=torch.int64)
+    torch.testing.assert_close(_oracle(inp, TINY, False), _brute(inp, TINY, False),
+                               rtol=1e-10, atol=1e-11)
+
+
+@pytest.mark.parametrize("path", sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))))
+def test_oracle_matches_golden_fixtures(path):
+    z = np.load(path)  # allow_pickle defaults to False
+    B, Sq, Sk, hidden, H, q_lora, Rk, nope, rope, v, causal = [int(t) for t in z["dims"]]
+    dims = R.MLADims(hidden=hidden, n_heads=H, q_lora=q_lora, kv_rank=Rk, nope=nope,
+                     rope=rope, v=v)
+    t = {k: torch.from_numpy(z[k]) for k in z.files if k not in ("dims", "out")}
+    got = _oracle(t, dims, bool(causal))
+    torch.testing.assert_close(got, torch.from_numpy(z["out"]), rtol=1e-10, atol=1e-11)
+    steps = R.layer_by_steps(t, dims, causal=bool(causal), tile=4)
+    torch.testing.assert_close(steps["out"], torch.from_numpy(z["out"]), rtol=1e-10,
+                               atol=1e-11)
+
+
+# --------------------------------------------------------------------------- RoPE
+
+
+def test_rope_closed_form_rotation():
+    rope = 64
+    pos = torch.tensor([0, 1, 17, 4988], dtype=torch.int64)
+    for i in (0, 5, 31):
+        x = torch.zeros(1, len(pos), 1, rope, dtype=torch.float64)
+        x[..., 2 * i] = 1.0  # unit vector on the even element of pair i
+        y = R.apply_rope(x, pos, rope)
+        for s, p in enumerate(pos.tolist()):
+            th = p / (10000.0 ** (2 * i / rope))
+            assert abs(y[0, s, 0, 2 * i].item() - math.cos(th)) < 1e-9
+            assert abs(y[0, s, 0, 2 * i + 1].item() - math.sin(th)) < 1e-9
+            others = torch.cat([y[0, s, 0, :2 * i], y[0, s, 0, 2 * i + 2:]])
+            assert others.abs().max().item() == 0.0
+
+
+def test_rope_identity_at_zero_and_norm_preserving():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(2, 3, 4, 64, generator=g, dtype=torch.float64)
+    y0 = R.apply_rope(x, torch.zeros(3, dtype=torch.int64), 64)
+    torch.testing.assert_close(y0, x, rtol=0, atol=0)
+    y = R.apply_rope(x, torch.tensor([5, 900, 4988]), 64)
+    n_in = x.reshape(-1, 32, 2).norm(dim=-1)
+    n_out = y.reshape(-1, 32, 2).norm(dim=-1)
+    torch.testing.assert_close(n_out, n_in, rtol=1e-12, atol=1e-12)
+
+
+def test_rope_inv_freq_is_torch_fp32_formula():
+    f = R.rope_inv_freq(64, torch.float32)
+    assert f.dtype == torch.float32 and f.shape == (32,)
+    assert f[0].item() == 1.0
+    exact = torch.tensor([10000.0 ** (-2 * i / 64) for i in range(32)], dtype=torch.float64)
+    assert (f.double() - exact).abs().max().item() < 2e-7 * 1.0
+
+
+def test_step_rope_matches_apply_rope_fp64():
+    B, Sq, H, nope, rope = 2, 3, 4, 8, 16
+    g = torch.Generator().manual_seed(1)
+    q_raw = torch.randn(B * Sq, H * (nope + rope), generator=g, dtype=torch.float64)
+    pos = torch.tensor([3, 70, 4988])
+    a = R.step_rope(q_raw, pos, R.rope_inv_freq(rope, torch.float64), B, Sq, H, nope, rope,
+                    torch.float64)
+    b = R.apply_rope(q_raw.reshape(B, Sq, H, -1)[..., nope:], pos, rope)
+    torch.testing.assert_close(a, b, rtol=1e-14, atol=1e-14)
+
+
+# --------------------------------------------------------------------------- RMSNorm
+
+
+def test_rmsnorm_unit_rms_and_gain():
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(5, 1536, generator=g, dtype=torch.float64) * 3.0
+    y = R.rmsnorm(x, torch.ones(1536, dtype=torch.float64), eps=0.0)
+    torch.testing.assert_close(y.square().mean(-1), torch.ones(5, dtype=torch.float64))
+    w = 1.0 + 0.1 * torch.randn(1536, generator=g, dtype=torch.float64)
+    yw = R.rmsnorm(x, w, eps=0.0)
+    torch.testing.assert_close(yw / w, y)
+    yk = R.step_norm(x, w, 0.0, torch.float64)
+    torch.testing.assert_close(yk, yw, rtol=1e-14, atol=1e-14)
+
+
+# --------------------------------------------------------------------------- decomposition
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("tile", [2, 3, 128])
+def test_steps_equal_direct_formulation(causal, tile):
+    dims = R.MLADims(hidden=16, n_heads=4, q_lora=8, kv_rank=8, nope=4, rope=4, v=4)
+    inp = R.make_inputs(2, 3, 11, dims, seed=5, dtype=torch.float64)
+    steps = R.layer_by_steps(inp, dims, causal=causal, tile=tile)
+    direct = _oracle(inp, dims, causal)
+    torch.testing.assert_close(steps["out"], direct, rtol=1e-12, atol=1e-12)
+    # the split softmax reassembles to a normalised distribution per row
+    a = steps["alpha"].repeat_interleave(tile, dim=1)[:, :11]
+    probs = steps["p"] * a / steps["row_sum"].unsqueeze(1)
+    torch.testing.assert_close(probs.sum(-1), torch.ones(probs.shape[0], dtype=torch.float64))
+    assert (steps["p"] >= 0).all() and (steps["p"] <= 1).all()
+
+
+def test_causal_single_query_equals_noncausal():
+    dims = R.MLADims(hidden=16, n_heads=4, q_lora=8, kv_rank=8, nope=4, rope=4, v=4)
+    inp = R.make_inputs(2, 1, 9, dims, seed=6, dtype=torch.float64)
+    torch.testing.assert_close(_oracle(inp, dims, True), _oracle(inp, dims, False),
+                               rtol=0, atol=0)
+
+
+def test_causal_mask_shape():
+    m = R.causal_mask(4, 4)
+    assert torch.equal(m, torch.ones(4, 4, dtype=torch.bool).tril())
+    m2 = R.causal_mask(2, 5)
+    assert m2.tolist() == [[True] * 4 + [False], [True] * 5]
+
+
+def test_uniform_keys_give_that_key():
+    dims = R.MLADims(hidden=16, n_heads=2, q_lora=8, kv_rank=8, nope=4, rope=4, v=4)
+    inp = R.make_inputs(1, 1, 6, dims, seed=7, dtype=torch.float64)
+    inp["c_kv"][:] = inp["c_kv"][:, :1, :]
+    inp["pe_cache"][:] = inp["pe_cache"][:, :1, :]
+    W_uk, W_uv = R.split_wkv_b(inp["wkv_b"], dims.nope)
+    out = _oracle(inp, dims, False)
+    exp = torch.einsum("r,hdr->hd", inp["c_kv"][0, 0], W_uv)
+    torch.testing.assert_close(out[0, 0], exp, rtol=1e-12, atol=1e-12)
+
+
+def test_make_inputs_deterministic():
+    a = R.make_inputs(2, 1, 5, TINY, seed=0)
+    b = R.make_inputs(2, 1, 5, TINY, seed=0)
+    for k in a:
+        assert torch.equal(a[k], b[k])
+    assert a["positions"].tolist() == [4]
+    c = R.make_inputs(2, 1, 5, TINY, seed=0, dtype=torch.bfloat16)
+    assert c["x"].dtype == torch.bfloat16
+    torch.testing.assert_close(c["x"].float(), a["x"], rtol=1e-2, atol=1e-2)
+
+
+# --------------------------------------------------------------------------- mutants
+
+
+def _mut_no_gain(mp):
+    orig = R.rmsnorm
+    mp.setattr(R, "rmsnorm", lambda x, g, eps=1e-6: orig(x, torch.ones_like(g), eps))
+
+
+def _mut_swap_wkv(mp):
+    mp.setattr(R, "split_wkv_b", lambda w, nope: (w[:, -nope:, :], w[:, :-nope, :]))
+
+
+def _mut_rope_half_split(mp):
+    # rotates pairs (i, i + rope/2) instead of the interleaved pairs (2i, 2i+1)
+    def rope(x, positions, rope_dim):
+        half = rope_dim // 2
+        acc = R.acc_dtype(x.dtype)
+        ang = torch.outer(positions.to(acc), R.rope_inv_freq(rope_dim, acc))
+        c = torch.cos(ang).reshape(1, -1, 1, half)
+        s = torch.sin(ang).reshape(1, -1, 1, half)
+        a, b = x[..., :half], x[..., half:]
+        return torch.cat([a * c - b * s, a * s + b * c], -1)
+    mp.setattr(R, "apply_rope", rope)
+
+
+def _mut_scale_multiplied(mp):
+    orig = R.mla_attention_official
+    mp.setattr(R, "mla_attention_official",
+               lambda qa, qr, ck, pe, w, scale, causal=False: orig(qa, qr, ck, pe, w,
+                                                                  1.0 / scale, causal))
+
+
+def _mut_causal_off_by_one(mp):
+    # key j visible iff j < Sk - Sq + i (strict), one key short of the rule
+    mp.setattr(R, "causal_mask", lambda Sq, Sk: torch.arange(Sk).unsqueeze(0)
+               < (Sk - Sq + torch.arange(Sq).unsqueeze(1)))
+
+
+def _mut_rope_sin_sign(mp):
+    orig = R.apply_rope
+    mp.setattr(R, "apply_rope", lambda x, p, d: orig(x, -p, d))
+
+
+MUTANTS = {
+    "no_gain": _mut_no_gain,
+    "swap_wkv": _mut_swap_wkv,
+    "rope_half_split": _mut_rope_half_split,
+    "scale_multiplied": _mut_scale_multiplied,
+    "causal_off_by_one": _mut_causal_off_by_one,
+    "rope_sin_sign": _mut_rope_sin_sign,
+}
+
+
+@pytest.mark.parametrize("name", sorted(MUTANTS))
+def test_planted_mistakes_are_caught(name, monkeypatch):
+    dims = R.MLADims(hidden=6, n_heads=2, q_lora=4, kv_rank=4, nope=2, rope=4, v=2)
+    causal = name == "causal_off_by_one"
+    inp = R.make_inputs(2, 3, 5, dims, seed=9, dtype=torch.float64)
+    inp["positions"] = torch.tensor([3, 40, 977])
+    ref = _brute(inp, dims, causal)
+    torch.testing.assert_close(_oracle(inp, dims, causal), ref, rtol=1e-11, atol=1e-12)
+    MUTANTS[name](monkeypatch)
+    bad = _oracle(inp, dims, causal)
+    assert (bad - ref).abs().max().item() > 1e-6, f"mutant {name} was not detected"
+
+
+def test_planted_combine_without_alpha_is_caught():
+    dims = R.MLADims(hidden=16, n_heads=2, q_lora=8, kv_rank=8, nope=4, rope=4, v=4)
+    inp = R.make_inputs(1, 2, 9, dims, seed=10, dtype=torch.float64)
+    r = R.layer_by_steps(inp, dims, tile=2)
+    W_uv = R.split_wkv_b(inp["wkv_b"], dims.nope)[1]
+    ctx_bad = R.step_ctx(r["p"], torch.ones_like(r["alpha"]), inp["c_kv"], 1, 2, 2, tile=2)
+    bad = R.step_out(ctx_bad, r["row_sum"], W_uv, torch.float64)
+    assert (bad - _oracle(inp, dims, False)).abs().max().item() > 1e-6
