@@ -15,9 +15,12 @@
 // reported (and testable) without a GPU.
 
 #include <torch/extension.h>
-#include <c10/hip/HIPGuard.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 
+#include <map>
+#include <mutex>
+#include <utility>
 #include <vector>
 
 #include "mla/mla.h"
@@ -71,6 +74,21 @@ torch::Tensor rope_inv_freq(int64_t rope) {
     return torch::pow(10000, e).reciprocal();
 }
 
+// The table lives on the device once per (device, rope width): a per-call host->device
+// copy would be a synchronous pageable copy that stalls the caller's stream every layer.
+// The cache is intentionally leaked so no tensor is freed after the HIP runtime shuts down.
+torch::Tensor device_inv_freq(int64_t rope, const torch::Device& dev) {
+    static std::mutex mu;
+    static auto* cache = new std::map<std::pair<int, int64_t>, torch::Tensor>();
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(static_cast<int>(dev.index()), rope);
+    auto it = cache->find(key);
+    if (it != cache->end()) return it->second;
+    auto t = rope_inv_freq(rope).to(dev);
+    cache->emplace(key, t);
+    return t;
+}
+
 // ------------------------------------------------------------------ fused: Q path
 
 std::vector<torch::Tensor> op_q_absorbed(torch::Tensor x, torch::Tensor W_q_a, torch::Tensor q_norm_w,
@@ -101,14 +119,14 @@ std::vector<torch::Tensor> op_q_absorbed(torch::Tensor x, torch::Tensor W_q_a, t
     check_same_dtype(x, W_uk, "W_uk");
     check_device({&x, &W_q_a, &q_norm_w, &W_q_b, &W_uk, &positions});
 
-    c10::hip::HIPGuard guard(x.device());
+    c10::DeviceGuard guard(x.device());
     auto xc = x.contiguous();
     auto wa = W_q_a.contiguous();
     auto g = q_norm_w.contiguous();
     auto wb = W_q_b.contiguous();
     auto wuk = W_uk.contiguous();
     auto pos = positions.to(torch::kLong).contiguous();
-    auto inv_freq = rope_inv_freq(rope_dim).to(x.device());
+    auto inv_freq = device_inv_freq(rope_dim, x.device());
 
     mla_dims_t d{};
     d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.hidden = (int32_t)hidden;
@@ -168,7 +186,7 @@ torch::Tensor op_mla_attention(torch::Tensor q_absorbed, torch::Tensor q_rope, t
     TORCH_CHECK(!causal || d.sk >= d.sq, "MLA: causal attention needs Sk >= Sq");
     check_device({&q_absorbed, &q_rope, &c_kv, &pe_cache, &W_uv});
 
-    c10::hip::HIPGuard guard(q_absorbed.device());
+    c10::DeviceGuard guard(q_absorbed.device());
     auto qa = q_absorbed.contiguous();
     auto qr = q_rope.contiguous();
     auto ck = c_kv.contiguous();
@@ -199,7 +217,7 @@ torch::Tensor step_gemm(torch::Tensor A, torch::Tensor W) {
     check_contig(A, "A");
     check_contig(W, "W");
     check_device({&A, &W});
-    c10::hip::HIPGuard guard(A.device());
+    c10::DeviceGuard guard(A.device());
     const int32_t M = (int32_t)A.size(0), K = (int32_t)A.size(1), N = (int32_t)W.size(1);
     auto C = torch::empty({M, N}, A.options().dtype(torch::kFloat32));
     const size_t wsb = mla_gemm_workspace_bytes(dt, M, N, K);
@@ -218,7 +236,7 @@ torch::Tensor step_rmsnorm(torch::Tensor in, torch::Tensor gain, double eps) {
     check_contig(in, "in");
     check_contig(gain, "gain");
     check_device({&in, &gain});
-    c10::hip::HIPGuard guard(in.device());
+    c10::DeviceGuard guard(in.device());
     auto out = torch::empty(in.sizes(), gain.options());
     check_status(mla_rmsnorm(dt, in.data_ptr<float>(), gain.data_ptr(), out.data_ptr(),
                              (int32_t)in.size(0), (int32_t)in.size(1), eps, current_stream()),
@@ -248,9 +266,9 @@ torch::Tensor step_rope(torch::Tensor q_raw, torch::Tensor positions, int64_t B,
     const mla_dtype_t dt = to_mla_dtype(torch::empty({0}, torch::TensorOptions().dtype(out_dtype)),
                                         "out_dtype");
     check_device({&q_raw, &positions});
-    c10::hip::HIPGuard guard(q_raw.device());
+    c10::DeviceGuard guard(q_raw.device());
     auto pos = positions.to(torch::kLong).contiguous();
-    auto inv_freq = rope_inv_freq(rope).to(q_raw.device());
+    auto inv_freq = device_inv_freq(rope, q_raw.device());
     auto out = torch::empty({B, Sq, H, rope}, q_raw.options().dtype(out_dtype));
     check_status(mla_rope(dt, &d, q_raw.data_ptr<float>(), pos.data_ptr<int64_t>(),
                           inv_freq.data_ptr<float>(), out.data_ptr(), current_stream()),
@@ -267,7 +285,7 @@ torch::Tensor step_absorb(torch::Tensor q_raw, torch::Tensor W_uk, int64_t B, in
     const mla_dtype_t dt = to_mla_dtype(W_uk, "W_uk");
     check_contig(W_uk, "W_uk");
     check_device({&q_raw, &W_uk});
-    c10::hip::HIPGuard guard(q_raw.device());
+    c10::DeviceGuard guard(q_raw.device());
     auto out = torch::empty({B, Sq, H, R}, W_uk.options());
     check_status(mla_absorb(dt, &d, q_raw.data_ptr<float>(), W_uk.data_ptr(), out.data_ptr(),
                             current_stream()),
@@ -285,7 +303,7 @@ std::vector<torch::Tensor> step_scores(torch::Tensor qa, torch::Tensor qr, torch
     check_same_dtype(qa, pe, "pe_cache");
     for (auto* t : {&qa, &qr, &ckv, &pe}) check_contig(*t, "scores input");
     check_device({&qa, &qr, &ckv, &pe});
-    c10::hip::HIPGuard guard(qa.device());
+    c10::DeviceGuard guard(qa.device());
     const int64_t rows = (int64_t)d.batch * d.sq * d.heads;
     const int32_t ld = mla_score_ld(d.sk);
     const int64_t P = (d.sk + mla_score_tile() - 1) / mla_score_tile();
@@ -308,7 +326,7 @@ std::vector<torch::Tensor> step_combine(torch::Tensor m, torch::Tensor l) {
     check_contig(m, "m_part");
     check_contig(l, "l_part");
     check_device({&m, &l});
-    c10::hip::HIPGuard guard(m.device());
+    c10::DeviceGuard guard(m.device());
     auto alpha = torch::empty_like(m);
     auto rs = torch::empty({m.size(0)}, m.options());
     check_status(mla_combine(m.data_ptr<float>(), l.data_ptr<float>(), alpha.data_ptr<float>(),
@@ -332,7 +350,7 @@ torch::Tensor step_ctx(torch::Tensor p, torch::Tensor alpha, torch::Tensor c_kv,
     const mla_dtype_t dt = to_mla_dtype(c_kv, "c_kv");
     for (auto* t : {&p, &alpha, &c_kv}) check_contig(*t, "ctx input");
     check_device({&p, &alpha, &c_kv});
-    c10::hip::HIPGuard guard(p.device());
+    c10::DeviceGuard guard(p.device());
     mla_dims_t d{};
     d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.sk = (int32_t)Sk; d.heads = (int32_t)H;
     d.kv_rank = (int32_t)R; d.rope = 4; d.v = 4;
@@ -357,7 +375,7 @@ torch::Tensor step_out(torch::Tensor ctx, torch::Tensor row_sum, torch::Tensor W
     const mla_dtype_t dt = to_mla_dtype(W_uv, "W_uv");
     for (auto* t : {&ctx, &row_sum, &W_uv}) check_contig(*t, "out input");
     check_device({&ctx, &row_sum, &W_uv});
-    c10::hip::HIPGuard guard(ctx.device());
+    c10::DeviceGuard guard(ctx.device());
     mla_dims_t d{};
     d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.sk = 1; d.heads = (int32_t)H;
     d.kv_rank = (int32_t)R; d.rope = 4; d.v = (int32_t)W_uv.size(1);

@@ -96,6 +96,7 @@ int check_q_dims(const mla_dims_t* d) {
     MLA_CHECK(check_mult4(d->nope, "dims.nope"));
     MLA_CHECK(check_mult4(d->rope, "dims.rope"));
     MLA_CHECK(check_mult4(d->kv_rank, "dims.kv_rank"));
+    if (d->rope > 512) return fail(MLA_ERR_INVALID_ARGUMENT, "dims.rope must be <= 512");
     const int64_t bq = (int64_t)d->batch * d->sq;
     if (bq * d->heads * (int64_t)(d->nope + d->rope) > kMaxI32 ||
         bq * d->heads * (int64_t)d->kv_rank > (int64_t)1 << 40)

@@ -24,6 +24,8 @@
 #include "kernels.h"
 
 #include <algorithm>
+#include <cstdio>
+#include <cstdlib>
 
 namespace mla {
 
@@ -89,6 +91,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     }
 
     v4f ra[A_LD], rb[B_LD];
+    float rsc[A_LD];  // per-load A scale, applied when the slice is written to LDS so the
+                      // multiply does not force a wait on the load ahead of the MFMAs
 
     auto load_slice = [&](int k0) {
         #pragma unroll
@@ -104,11 +108,13 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                     #pragma unroll
                     for (int j = 0; j < 4; ++j) v[j] = (k + j < k_end) ? src[j] : 0.f;
                 }
-                float s = row_scale[i];
-                if (AMODE == kAAlpha)
-                    s = a.alpha[((int64_t)g * a.M + m) * a.alpha_ld + k / a.alpha_tile];
-                if (AMODE != kAPlain) v *= s;
             }
+            float sc = row_scale[i];
+            if (AMODE == kAAlpha)
+                sc = (m < a.M && k < k_end)
+                         ? a.alpha[((int64_t)g * a.M + m) * a.alpha_ld + k / a.alpha_tile]
+                         : 0.f;
+            rsc[i] = sc;
             ra[i] = v;
         }
         #pragma unroll
@@ -140,7 +146,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     auto store_slice = [&](int buf) {
         #pragma unroll
         for (int i = 0; i < A_LD; ++i)
-            *reinterpret_cast<v4f*>(&As[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = ra[i];
+            *reinterpret_cast<v4f*>(&As[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) =
+                (AMODE == kAPlain) ? ra[i] : ra[i] * rsc[i];
         #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             if (NT) {
@@ -263,6 +270,7 @@ template <bool NT, int AMODE, int OUT>
 hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks,
                         hipStream_t stream) {
     if (bm == 128 && bn == 128) return launch_cfg<128, 128, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
+    if (bm == 128 && bn == 96) return launch_cfg<128, 96, 4, 1, NT, AMODE, OUT>(args, nblocks, stream);
     if (bm == 128 && bn == 64) return launch_cfg<128, 64, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
     if (bm == 64 && bn == 128) return launch_cfg<64, 128, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
     if (bm == 64 && bn == 64) return launch_cfg<64, 64, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
@@ -295,37 +303,93 @@ int cdiv(int a, int b) { return (a + b - 1) / b; }
 
 }  // namespace
 
-// Tile and split choice.  Candidates are the six tile shapes above; the cost model counts
-// per-CU MFMA work (tiles are padded to 32x32 blocks, so small M or N wastes work) plus a
-// wave-quantisation penalty, then splits K while the grid is under two workgroups per CU.
+// Tile and split choice: a small time model evaluated for every tile shape and power-of-two
+// split.  MFMA time = rounds of co-resident workgroups x the padded tile work (32x32
+// blocks waste rows/cols at small M or N) at a per-tile efficiency; memory time = the
+// operand bytes that must come from HBM; split-K adds its fp32 partial traffic and one
+// reduction launch.  MLA_GEMM_PLAN="M,N,K,G=bm,bn,split;..." forces a plan for a matching
+// problem (tuning aid; the chosen plan always goes through the same validity checks).
+namespace {
+
+struct TileShape { int bm, bn; double eff; };
+constexpr TileShape kTiles[] = {
+    {128, 128, 0.80}, {128, 96, 0.78}, {128, 64, 0.72}, {64, 128, 0.72},
+    {64, 64, 0.60},   {32, 128, 0.55}, {128, 32, 0.55}};
+
+int lds_bytes(int bm, int bn, bool nt) {
+    const int a = 2 * bm * (kBK + kPadK);
+    const int b = nt ? 2 * bn * (kBK + kPadK) : 2 * kBK * (bn + kPadN);
+    return (a + b) * 4;
+}
+
+bool tile_supported(int bm, int bn) {
+    for (const auto& t : kTiles)
+        if (t.bm == bm && t.bn == bn) return true;
+    return false;
+}
+
+bool plan_override(const GemmProblem& p, GemmPlan* out) {
+    const char* env = getenv("MLA_GEMM_PLAN");
+    if (!env) return false;
+    const char* s = env;
+    while (*s) {
+        long M, N, K, G;
+        int bm, bn, split, used = 0;
+        if (sscanf(s, "%ld,%ld,%ld,%ld=%d,%d,%d%n", &M, &N, &K, &G, &bm, &bn, &split, &used) == 7) {
+            if (M == p.M && N == p.N && K == p.K && G == p.G && tile_supported(bm, bn) &&
+                split >= 1) {
+                out->bm = bm; out->bn = bn; out->split = split;
+                return true;
+            }
+            s += used;
+        } else {
+            break;
+        }
+        while (*s == ';' || *s == ' ') ++s;
+    }
+    return false;
+}
+
+}  // namespace
+
 GemmPlan plan_gemm(const GemmProblem& p) {
-    static const int cand[][2] = {{128, 128}, {128, 64}, {64, 128}, {64, 64}, {32, 128}, {128, 32}};
+    constexpr double kCuRate = 256.0 * 2.4e9;   // fp32 MFMA flop/s per CU
+    constexpr double kHbm = 5.0e12;             // sustained HBM B/s
+    constexpr double kReduceLaunch = 3e-6;      // s
+    const int kslices = cdiv(p.K, kBK);
     GemmPlan best;
-    double best_cost = 1e300;
-    for (const auto& c : cand) {
-        const int bm = c[0], bn = c[1];
-        const int64_t tiles = (int64_t)cdiv(p.M, bm) * cdiv(p.N, bn) * p.G;
-        // split K until the grid covers >= 2 workgroups per CU, keeping >= 4 slices of 32
-        int split = 1;
-        const int kslices = cdiv(p.K, kBK);
-        while (tiles * split < 2 * kNumCUs && split * 2 <= kslices / 4) split *= 2;
-        const int64_t blocks = tiles * split;
-        const int64_t per_cu = (blocks + 2 * kNumCUs - 1) / (2 * kNumCUs);  // 2 WG/CU
-        // time ~ rounds * work per workgroup (MFMA work of a padded tile over its K chunk)
-        const double work = (double)bm * bn * ((double)p.K / split);
-        // small tiles re-read operands more; favour larger tiles slightly
-        const double eff = (bm == 128 && bn == 128) ? 1.0 : (bm * bn >= 8192 ? 1.06 : 1.15);
-        double cost = (double)per_cu * work * eff;
-        if (split > 1) cost *= 1.03;  // partial write + reduction
-        if (cost < best_cost) {
-            best_cost = cost;
-            best.bm = bm;
-            best.bn = bn;
-            best.split = split;
+    double best_t = 1e300;
+    if (!plan_override(p, &best)) {
+        for (const auto& t : kTiles) {
+            const int tm = cdiv(p.M, t.bm), tn = cdiv(p.N, t.bn);
+            const int64_t tiles = (int64_t)tm * tn * p.G;
+            const int occ = std::max(1, std::min(2, 163840 / lds_bytes(t.bm, t.bn, p.b_nt)));
+            for (int split = 1; split <= std::max(1, kslices / 2); split *= 2) {
+                const int per = cdiv(kslices, split);
+                const int real_split = cdiv(kslices, per);
+                if (real_split != split && split > 1) continue;
+                const int64_t blocks = tiles * split;
+                // the busiest CU runs ceil(blocks / CUs) workgroups back to back or side by
+                // side; a lone workgroup per CU hides latency worse than two
+                const int64_t per_cu = (blocks + kNumCUs - 1) / kNumCUs;
+                const double hide = std::min<int64_t>(per_cu, occ) >= 2 ? 1.0 : 0.8;
+                const double wg_flops = 2.0 * t.bm * t.bn * (double)per * kBK;
+                const double t_mfma = per_cu * wg_flops / (kCuRate * t.eff * hide);
+                // B operand streamed once per M tile (weights / cache), A once per N tile
+                // (small, mostly L2), C written once
+                const double bytes = 4.0 * ((double)p.K * p.N * p.G * std::min(tm, 2) +
+                                            (double)p.M * p.K * p.G + (double)p.M * p.N * p.G);
+                double tt = std::max(t_mfma, bytes / kHbm);
+                if (split > 1)
+                    tt += 4.0 * (split + 1) * (double)p.M * p.N * p.G / kHbm + kReduceLaunch;
+                if (tt < best_t * 0.999) {
+                    best_t = tt;
+                    best.bm = t.bm; best.bn = t.bn; best.split = split;
+                }
+            }
         }
     }
-    const int kslices = cdiv(p.K, kBK);
-    const int per = cdiv(kslices, best.split);
+    const int per = cdiv(kslices, std::max(1, std::min(best.split, kslices)));
     best.k_chunk = per * kBK;
     best.split = cdiv(kslices, per);  // no empty slices
     best.workspace_bytes =

@@ -13,7 +13,12 @@ namespace {
 
 // ---- 2a-n: one 256-thread workgroup per row.  The input may be nsplit fp32 partial
 // sums of 2a1 (split-K); they are added here in slice order, which is what makes the
-// split-K of 2a1 free of a separate reduction pass.
+// split-K of 2a1 free of a separate reduction pass.  Each thread keeps its summed
+// elements in registers between the sum-of-squares pass and the output pass (rows up to
+// 4096 wide), so the partials are read once; the partial loop is unrolled so the loads
+// of all slices are in flight together.
+constexpr int kNormCache = 4;  // float4 per thread kept in registers (256*4*4 = 4096 wide)
+
 template <int OUT>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ in, int nsplit,
                                                       int64_t split_stride, const void* gain_v,
@@ -26,13 +31,29 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
 
     auto load4 = [&](int c4) {
         v4f v = *reinterpret_cast<const v4f*>(base + 4 * c4);
-        for (int s = 1; s < nsplit; ++s)
+        int s = 1;
+        for (; s + 4 <= nsplit; s += 4) {
+            const v4f a = *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
+            const v4f b = *reinterpret_cast<const v4f*>(base + (s + 1) * split_stride + 4 * c4);
+            const v4f c = *reinterpret_cast<const v4f*>(base + (s + 2) * split_stride + 4 * c4);
+            const v4f d = *reinterpret_cast<const v4f*>(base + (s + 3) * split_stride + 4 * c4);
+            v += a; v += b; v += c; v += d;
+        }
+        for (; s < nsplit; ++s)
             v += *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
         return v;
     };
 
+    v4f cache[kNormCache];
     float ss = 0.f;
-    for (int c4 = tid; c4 < n4; c4 += 256) {
+    #pragma unroll
+    for (int j = 0; j < kNormCache; ++j) {
+        const int c4 = tid + 256 * j;
+        cache[j] = (c4 < n4) ? load4(c4) : v4f{0.f, 0.f, 0.f, 0.f};
+        ss += cache[j][0] * cache[j][0] + cache[j][1] * cache[j][1] +
+              cache[j][2] * cache[j][2] + cache[j][3] * cache[j][3];
+    }
+    for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256) {
         const v4f v = load4(c4);
         ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     }
@@ -42,8 +63,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     const float total = red[0] + red[1] + red[2] + red[3];
     const float inv = rsqrtf(total / (float)N + eps);
 
-    for (int c4 = tid; c4 < n4; c4 += 256) {
-        const v4f v = load4(c4);
+    auto emit = [&](int c4, const v4f& v) {
         if (OUT == kOutF32) {
             const v4f g = *reinterpret_cast<const v4f*>(static_cast<const float*>(gain_v) + 4 * c4);
             v4f o;
@@ -56,35 +76,51 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
             #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = __float2bfloat16(v[j] * inv * __bfloat162float(g[j]));
         }
+    };
+    #pragma unroll
+    for (int j = 0; j < kNormCache; ++j) {
+        const int c4 = tid + 256 * j;
+        if (c4 < n4) emit(c4, cache[j]);
     }
+    for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256) emit(c4, load4(c4));
 }
 
-// ---- 2b: one thread per (row, head, rotary pair).  Angle = float(pos) * inv_freq[i] in
-// fp32 with the caller's inv_freq table; accurate cosf/sinf (not the fast intrinsics): at
-// positions ~5e3 an angle ulp is ~5e-4 rad, so the table and the multiply must match the
-// oracle bit for bit and the trig functions must be accurate.
+// ---- 2b: one workgroup per (query row bq, chunk of 32 heads).  Every head of a row uses
+// the same rope/2 angles, so the workgroup evaluates them once into LDS: angle =
+// float(pos) * inv_freq[i] in fp32 with the caller's inv_freq table, then accurate
+// cosf/sinf (not the fast intrinsics: at positions ~5e3 an angle ulp is ~5e-4 rad and
+// large arguments need full range reduction).  Threads then rotate the (head, pair)
+// elements of the chunk with 64-bit loads and stores.
+constexpr int kRopeHeads = 32;
+constexpr int kRopeMaxHalf = 256;
+
 template <int OUT>
 __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_raw,
                                                    const int64_t* __restrict__ positions,
                                                    const float* __restrict__ inv_freq,
-                                                   void* out_v, int total, int Sq, int H,
-                                                   int nope, int rope) {
+                                                   void* out_v, int Sq, int H, int nope,
+                                                   int rope) {
+    __shared__ float cs[kRopeMaxHalf], sn[kRopeMaxHalf];
     const int half = rope >> 1;
     const int qk = nope + rope;
-    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total;
-         idx += gridDim.x * blockDim.x) {
+    const int bq = blockIdx.x;
+    const int h0 = blockIdx.y * kRopeHeads;
+    const int nh = min(kRopeHeads, H - h0);
+    const float pos = (float)positions[bq % Sq];
+    for (int i = threadIdx.x; i < half; i += blockDim.x) {
+        const float ang = pos * inv_freq[i];
+        cs[i] = cosf(ang);
+        sn[i] = sinf(ang);
+    }
+    __syncthreads();
+    const float* src = q_raw + (int64_t)bq * H * qk + nope;
+    for (int idx = threadIdx.x; idx < nh * half; idx += blockDim.x) {
+        const int h = h0 + idx / half;
         const int i = idx % half;
-        const int rh = idx / half;        // (bq, h)
-        const int h = rh % H;
-        const int bq = rh / H;
-        const int s = bq % Sq;
-        const float2 x = *reinterpret_cast<const float2*>(
-            q_raw + (int64_t)bq * H * qk + (int64_t)h * qk + nope + 2 * i);
-        const float ang = (float)positions[s] * inv_freq[i];
-        const float c = cosf(ang), sn = sinf(ang);
-        const float e = x.x * c - x.y * sn;
-        const float o = x.x * sn + x.y * c;
-        const int64_t dst = (int64_t)rh * rope + 2 * i;
+        const float2 x = *reinterpret_cast<const float2*>(src + (int64_t)h * qk + 2 * i);
+        const float e = x.x * cs[i] - x.y * sn[i];
+        const float o = x.x * sn[i] + x.y * cs[i];
+        const int64_t dst = ((int64_t)bq * H + h) * rope + 2 * i;
         if (OUT == kOutF32) {
             *reinterpret_cast<float2*>(static_cast<float*>(out_v) + dst) = make_float2(e, o);
         } else {
@@ -141,15 +177,15 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, con
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope, int rope,
                        hipStream_t stream) {
-    const int64_t total = (int64_t)B * Sq * H * (rope / 2);
-    if (total <= 0) return hipSuccess;
-    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16 * kNumCUs);
+    if ((int64_t)B * Sq <= 0 || H <= 0) return hipSuccess;
+    if (rope / 2 > kRopeMaxHalf) return hipErrorInvalidValue;
+    const dim3 grid(B * Sq, (H + kRopeHeads - 1) / kRopeHeads);
     if (out_type == kOutF32)
-        hipLaunchKernelGGL(rope_kernel<kOutF32>, dim3(blocks), dim3(256), 0, stream, q_raw,
-                           positions, inv_freq, q_rope, (int)total, Sq, H, nope, rope);
+        hipLaunchKernelGGL(rope_kernel<kOutF32>, grid, dim3(256), 0, stream, q_raw, positions,
+                           inv_freq, q_rope, Sq, H, nope, rope);
     else
-        hipLaunchKernelGGL(rope_kernel<kOutBF16>, dim3(blocks), dim3(256), 0, stream, q_raw,
-                           positions, inv_freq, q_rope, (int)total, Sq, H, nope, rope);
+        hipLaunchKernelGGL(rope_kernel<kOutBF16>, grid, dim3(256), 0, stream, q_raw, positions,
+                           inv_freq, q_rope, Sq, H, nope, rope);
     return hipGetLastError();
 }
 
