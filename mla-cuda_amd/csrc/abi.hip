@@ -64,10 +64,20 @@ int check_ptr(const void* p, const char* name) {
     } while (0)
 
 int check_dtype(mla_dtype_t dt) {
-    if (dt == MLA_DTYPE_F32) return MLA_OK;
-    if (dt == MLA_DTYPE_BF16)
-        return fail(MLA_ERR_UNSUPPORTED, "dtype bf16 is not implemented by this build");
+    if (dt == MLA_DTYPE_F32 || dt == MLA_DTYPE_BF16) return MLA_OK;
     return fail(MLA_ERR_INVALID_ARGUMENT, "unknown dtype %d", (int)dt);
+}
+
+bool is_bf16(mla_dtype_t dt) { return dt == MLA_DTYPE_BF16; }
+OutType storage_out(mla_dtype_t dt) { return is_bf16(dt) ? kOutBF16 : kOutF32; }
+
+// Row lengths of storage-dtype tensors must be whole 16-byte chunks: 4 fp32 / 8 bf16.
+int check_row(mla_dtype_t dt, int v, const char* name) {
+    const int q = is_bf16(dt) ? 8 : 4;
+    if (v <= 0 || v % q != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "%s must be a positive multiple of %d for %s (got %d)",
+                    name, q, is_bf16(dt) ? "bf16" : "fp32", v);
+    return MLA_OK;
 }
 
 int check_pos(int64_t v, const char* name) {
@@ -86,16 +96,16 @@ int check_mult4(int v, const char* name) {
 // Upper bound for any row count / flattened index the kernels form in 32-bit ints.
 constexpr int64_t kMaxI32 = 0x7fffffffLL;
 
-int check_q_dims(const mla_dims_t* d) {
+int check_q_dims(mla_dtype_t dt, const mla_dims_t* d) {
     if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
     MLA_CHECK(check_pos(d->batch, "dims.batch"));
     MLA_CHECK(check_pos(d->sq, "dims.sq"));
     MLA_CHECK(check_pos(d->heads, "dims.heads"));
-    MLA_CHECK(check_mult4(d->hidden, "dims.hidden"));
-    MLA_CHECK(check_mult4(d->q_lora, "dims.q_lora"));
-    MLA_CHECK(check_mult4(d->nope, "dims.nope"));
-    MLA_CHECK(check_mult4(d->rope, "dims.rope"));
-    MLA_CHECK(check_mult4(d->kv_rank, "dims.kv_rank"));
+    MLA_CHECK(check_row(dt, d->hidden, "dims.hidden"));
+    MLA_CHECK(check_row(dt, d->q_lora, "dims.q_lora"));
+    MLA_CHECK(check_row(dt, d->nope, "dims.nope"));
+    MLA_CHECK(check_row(dt, d->rope, "dims.rope"));
+    MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
     if (d->rope > 512) return fail(MLA_ERR_INVALID_ARGUMENT, "dims.rope must be <= 512");
     const int64_t bq = (int64_t)d->batch * d->sq;
     if (bq * d->heads * (int64_t)(d->nope + d->rope) > kMaxI32 ||
@@ -104,14 +114,55 @@ int check_q_dims(const mla_dims_t* d) {
     return MLA_OK;
 }
 
-int check_attn_dims(const mla_dims_t* d, int causal) {
+// The fields the 2b / 2c steps read: batch, sq, heads, nope, rope (+ kv_rank for 2c).
+int check_qraw_dims(mla_dtype_t dt, const mla_dims_t* d, bool absorb) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_row(dt, d->nope, "dims.nope"));
+    MLA_CHECK(check_row(dt, d->rope, "dims.rope"));
+    if (d->rope > 512) return fail(MLA_ERR_INVALID_ARGUMENT, "dims.rope must be <= 512");
+    if (absorb) MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
+    if ((int64_t)d->batch * d->sq * d->heads * (int64_t)(d->nope + d->rope) > kMaxI32)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    return MLA_OK;
+}
+
+// 3c reads batch, sq, sk, heads, kv_rank; 3d reads batch, sq, heads, kv_rank, v.
+int check_ctx_dims(mla_dtype_t dt, const mla_dims_t* d) {
     if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
     MLA_CHECK(check_pos(d->batch, "dims.batch"));
     MLA_CHECK(check_pos(d->sq, "dims.sq"));
     MLA_CHECK(check_pos(d->sk, "dims.sk"));
     MLA_CHECK(check_pos(d->heads, "dims.heads"));
-    MLA_CHECK(check_mult4(d->rope, "dims.rope"));
-    MLA_CHECK(check_mult4(d->kv_rank, "dims.kv_rank"));
+    MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
+    if ((int64_t)d->batch * d->sq * d->heads > kMaxI32 / 2)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    if ((int64_t)d->sk > kMaxI32 / 1024) return fail(MLA_ERR_INVALID_ARGUMENT, "sk too large");
+    return MLA_OK;
+}
+
+int check_out_dims(mla_dtype_t dt, const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
+    MLA_CHECK(check_mult4(d->v, "dims.v"));
+    if ((int64_t)d->batch * d->sq * d->heads > kMaxI32 / 2)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    return MLA_OK;
+}
+
+int check_attn_dims(mla_dtype_t dt, const mla_dims_t* d, int causal) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->sk, "dims.sk"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_row(dt, d->rope, "dims.rope"));
+    MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
     MLA_CHECK(check_mult4(d->v, "dims.v"));
     if (causal && d->sk < d->sq)
         return fail(MLA_ERR_INVALID_ARGUMENT,
@@ -136,8 +187,10 @@ int check_ws(void* ws, size_t have, size_t need) {
 
 // ------------------------------------------------------------------ problem builders
 
-GemmProblem q_down_problem(const mla_dims_t* d, const float* x, const float* W, float* C) {
+GemmProblem q_down_problem(mla_dtype_t dt, const mla_dims_t* d, const void* x, const void* W,
+                           float* C) {
     GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt);
     p.A = x; p.lda = d->hidden;
     p.B = W; p.ldb = d->q_lora;
     p.C = C; p.ldc = d->q_lora;
@@ -145,9 +198,11 @@ GemmProblem q_down_problem(const mla_dims_t* d, const float* x, const float* W, 
     return p;
 }
 
-GemmProblem q_up_problem(const mla_dims_t* d, const float* q_lat, const float* W, float* C) {
+GemmProblem q_up_problem(mla_dtype_t dt, const mla_dims_t* d, const void* q_lat, const void* W,
+                         float* C) {
     const int n = d->heads * (d->nope + d->rope);
     GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt);
     p.A = q_lat; p.lda = d->q_lora;
     p.B = W; p.ldb = n;
     p.C = C; p.ldc = n;
@@ -155,10 +210,11 @@ GemmProblem q_up_problem(const mla_dims_t* d, const float* q_lat, const float* W
     return p;
 }
 
-GemmProblem absorb_problem(const mla_dims_t* d, const float* q_raw, const float* W_uk,
-                           void* q_abs) {
+GemmProblem absorb_problem(mla_dtype_t dt, const mla_dims_t* d, const float* q_raw,
+                           const void* W_uk, void* q_abs) {
     const int qk = d->nope + d->rope;
     GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
     p.A = q_raw; p.lda = (int64_t)d->heads * qk; p.sAg = qk;
     p.B = W_uk; p.ldb = d->kv_rank; p.sBg = (int64_t)d->nope * d->kv_rank;
     p.C = q_abs; p.ldc = (int64_t)d->heads * d->kv_rank; p.sCg = d->kv_rank;
@@ -166,10 +222,11 @@ GemmProblem absorb_problem(const mla_dims_t* d, const float* q_raw, const float*
     return p;
 }
 
-GemmProblem ctx_problem(const mla_dims_t* d, const float* p_scores, int ld_p,
-                        const float* alpha, const float* c_kv, float* ctx) {
+GemmProblem ctx_problem(mla_dtype_t dt, const mla_dims_t* d, const float* p_scores, int ld_p,
+                        const float* alpha, const void* c_kv, float* ctx) {
     const int rows_b = d->sq * d->heads;
     GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = true;
     p.A = p_scores; p.lda = ld_p; p.sAg = (int64_t)rows_b * ld_p;
     p.B = c_kv; p.ldb = d->kv_rank; p.sBg = (int64_t)d->sk * d->kv_rank;
     p.C = ctx; p.ldc = d->kv_rank; p.sCg = (int64_t)rows_b * d->kv_rank;
@@ -179,9 +236,10 @@ GemmProblem ctx_problem(const mla_dims_t* d, const float* p_scores, int ld_p,
     return p;
 }
 
-GemmProblem out_problem(const mla_dims_t* d, const float* ctx, const float* row_sum,
-                        const float* W_uv, void* out) {
+GemmProblem out_problem(mla_dtype_t dt, const mla_dims_t* d, const float* ctx,
+                        const float* row_sum, const void* W_uv, void* out) {
     GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
     p.A = ctx; p.lda = (int64_t)d->heads * d->kv_rank; p.sAg = d->kv_rank;
     p.B = W_uv; p.ldb = d->kv_rank; p.sBg = (int64_t)d->v * d->kv_rank; p.b_nt = true;
     p.C = out; p.ldc = (int64_t)d->heads * d->v; p.sCg = d->v;
@@ -197,13 +255,13 @@ struct QLayout {
     size_t off_lat_acc, off_lat, off_raw, off_up_ws, off_abs_ws, total;
 };
 
-QLayout q_layout(const mla_dims_t* d) {
+QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     QLayout L;
     const size_t bq = (size_t)d->batch * d->sq;
     const size_t n_raw = (size_t)d->heads * (d->nope + d->rope);
-    L.down = plan_gemm(q_down_problem(d, nullptr, nullptr, nullptr));
-    L.up = plan_gemm(q_up_problem(d, nullptr, nullptr, nullptr));
-    L.absorb = plan_gemm(absorb_problem(d, nullptr, nullptr, nullptr));
+    L.down = plan_gemm(q_down_problem(dt, d, nullptr, nullptr, nullptr));
+    L.up = plan_gemm(q_up_problem(dt, d, nullptr, nullptr, nullptr));
+    L.absorb = plan_gemm(absorb_problem(dt, d, nullptr, nullptr, nullptr));
     size_t o = 0;
     L.off_lat_acc = o;  // 2a1 output or its split partials (summed by the norm kernel)
     o = align_up(o + (size_t)L.down.split * bq * d->q_lora * sizeof(float));
@@ -225,13 +283,13 @@ struct AttnLayout {
     size_t off_p, off_m, off_l, off_alpha, off_rowsum, off_ctx, off_ctx_ws, off_out_ws, total;
 };
 
-AttnLayout attn_layout(const mla_dims_t* d) {
+AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     AttnLayout L;
     const size_t rows = (size_t)d->batch * d->sq * d->heads;
     L.ld_p = mla_score_ld(d->sk);
     L.P = cdiv(d->sk, kScoreTile);
-    L.ctx = plan_gemm(ctx_problem(d, nullptr, L.ld_p, nullptr, nullptr, nullptr));
-    L.out = plan_gemm(out_problem(d, nullptr, nullptr, nullptr, nullptr));
+    L.ctx = plan_gemm(ctx_problem(dt, d, nullptr, L.ld_p, nullptr, nullptr, nullptr));
+    L.out = plan_gemm(out_problem(dt, d, nullptr, nullptr, nullptr, nullptr));
     size_t o = 0;
     L.off_p = o;      o = align_up(o + rows * L.ld_p * sizeof(float));
     L.off_m = o;      o = align_up(o + rows * L.P * sizeof(float));
@@ -251,14 +309,12 @@ template <typename T> T* at(void* base, size_t off) {
 
 // ------------------------------------------------------------------ step bodies
 
-int run_scores(const mla_dims_t* d, const void* qa, const void* qr, const void* ckv,
+int run_scores(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* qr, const void* ckv,
                const void* pe, double scale, int causal, float* p, int ld_p, float* m_part,
                float* l_part, hipStream_t stream) {
     ScoresProblem sp;
-    sp.qa = static_cast<const float*>(qa);
-    sp.qr = static_cast<const float*>(qr);
-    sp.ckv = static_cast<const float*>(ckv);
-    sp.pe = static_cast<const float*>(pe);
+    sp.qa = qa; sp.qr = qr; sp.ckv = ckv; sp.pe = pe;
+    sp.bf16 = is_bf16(dt);
     sp.p = p; sp.m_part = m_part; sp.l_part = l_part;
     sp.B = d->batch; sp.Sq = d->sq; sp.Sk = d->sk; sp.H = d->heads;
     sp.R = d->kv_rank; sp.D = d->rope; sp.ld_p = ld_p; sp.P = cdiv(d->sk, kScoreTile);
@@ -288,10 +344,10 @@ int32_t mla_score_tile(void) { return kScoreTile; }
 int32_t mla_score_ld(int32_t sk) { return sk <= 0 ? 0 : ((sk + 31) / 32) * 32; }
 
 size_t mla_gemm_workspace_bytes(mla_dtype_t dtype, int32_t M, int32_t N, int32_t K) {
-    (void)dtype;
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     GemmProblem p;
     p.M = M; p.N = N; p.K = K;
+    p.bf16 = is_bf16(dtype); p.a_f32 = !is_bf16(dtype);
     return plan_gemm(p).workspace_bytes;
 }
 
@@ -299,14 +355,15 @@ int mla_gemm(mla_dtype_t dtype, const void* A, const void* W, float* C, int32_t 
              int32_t K, void* workspace, size_t workspace_bytes, hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
     MLA_CHECK(check_pos(M, "M"));
-    MLA_CHECK(check_mult4(N, "N"));
-    MLA_CHECK(check_mult4(K, "K"));
+    MLA_CHECK(check_row(dtype, N, "N"));
+    MLA_CHECK(check_row(dtype, K, "K"));
     MLA_CHECK(check_ptr(A, "A"));
     MLA_CHECK(check_ptr(W, "W"));
     MLA_CHECK(check_ptr(C, "C"));
     GemmProblem p;
-    p.A = static_cast<const float*>(A); p.lda = K;
-    p.B = static_cast<const float*>(W); p.ldb = N;
+    p.A = A; p.lda = K;
+    p.B = W; p.ldb = N;
+    p.bf16 = is_bf16(dtype); p.a_f32 = !is_bf16(dtype);
     p.C = C; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
     const GemmPlan plan = plan_gemm(p);
@@ -325,7 +382,7 @@ int mla_rmsnorm(mla_dtype_t dtype, const float* in, const void* gain, void* out,
     MLA_CHECK(check_ptr(out, "out"));
     if (!(eps >= 0.0) || !std::isfinite(eps))
         return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
-    MLA_TRY_HIP(launch_rmsnorm(in, 1, 0, gain, out, kOutF32, M, N, (float)eps, stream),
+    MLA_TRY_HIP(launch_rmsnorm(in, 1, 0, gain, out, storage_out(dtype), M, N, (float)eps, stream),
                 "rmsnorm launch");
     return ok();
 }
@@ -334,12 +391,12 @@ int mla_rope(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
              const int64_t* positions, const float* inv_freq, void* q_rope,
              hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_q_dims(dims));
+    MLA_CHECK(check_qraw_dims(dtype, dims, false));
     MLA_CHECK(check_ptr(q_raw, "q_raw"));
     MLA_CHECK(check_ptr(positions, "positions"));
     MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
     MLA_CHECK(check_ptr(q_rope, "q_rope"));
-    MLA_TRY_HIP(launch_rope(q_raw, positions, inv_freq, q_rope, kOutF32, dims->batch,
+    MLA_TRY_HIP(launch_rope(q_raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch,
                             dims->sq, dims->heads, dims->nope, dims->rope, stream),
                 "rope launch");
     return ok();
@@ -348,11 +405,11 @@ int mla_rope(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
 int mla_absorb(mla_dtype_t dtype, const mla_dims_t* dims, const float* q_raw,
                const void* W_uk, void* q_absorbed, hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_q_dims(dims));
+    MLA_CHECK(check_qraw_dims(dtype, dims, true));
     MLA_CHECK(check_ptr(q_raw, "q_raw"));
     MLA_CHECK(check_ptr(W_uk, "W_uk"));
     MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
-    GemmProblem p = absorb_problem(dims, q_raw, static_cast<const float*>(W_uk), q_absorbed);
+    GemmProblem p = absorb_problem(dtype, dims, q_raw, W_uk, q_absorbed);
     const GemmPlan plan = plan_gemm(p);
     if (plan.workspace_bytes)
         return fail(MLA_ERR_UNSUPPORTED, "absorb at this shape needs split-K; use mla_q_absorbed");
@@ -365,7 +422,7 @@ int mla_scores(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed
                int causal, float* scores, int32_t ld_scores, float* m_part, float* l_part,
                hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_attn_dims(dims, causal));
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
     MLA_CHECK(check_scale(scale));
     MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
     MLA_CHECK(check_ptr(q_rope, "q_rope"));
@@ -378,7 +435,7 @@ int mla_scores(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed
         return fail(MLA_ERR_INVALID_ARGUMENT,
                     "ld_scores must be a multiple of 4 and >= mla_score_ld(sk)=%d (got %d)",
                     mla_score_ld(dims->sk), ld_scores);
-    MLA_CHECK(run_scores(dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, scores,
+    MLA_CHECK(run_scores(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, scores,
                          ld_scores, m_part, l_part, stream));
     return ok();
 }
@@ -397,9 +454,8 @@ int mla_combine(const float* m_part, const float* l_part, float* alpha, float* r
 }
 
 size_t mla_ctx_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
-    (void)dtype;
-    if (!dims || check_attn_dims(dims, 0) != MLA_OK) return 0;
-    return plan_gemm(ctx_problem(dims, nullptr, mla_score_ld(dims->sk), nullptr, nullptr,
+    if (!dims || check_ctx_dims(dtype, dims) != MLA_OK) return 0;
+    return plan_gemm(ctx_problem(dtype, dims, nullptr, mla_score_ld(dims->sk), nullptr, nullptr,
                                  nullptr)).workspace_bytes;
 }
 
@@ -407,7 +463,7 @@ int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores, int3
             const float* alpha, const void* c_kv, float* ctx, void* workspace,
             size_t workspace_bytes, hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_attn_dims(dims, 0));
+    MLA_CHECK(check_ctx_dims(dtype, dims));
     MLA_CHECK(check_ptr(scores, "scores"));
     MLA_CHECK(check_ptr(alpha, "alpha"));
     MLA_CHECK(check_ptr(c_kv, "c_kv"));
@@ -416,8 +472,7 @@ int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores, int3
         return fail(MLA_ERR_INVALID_ARGUMENT,
                     "ld_scores must be a multiple of 4 and >= mla_score_ld(sk)=%d (got %d)",
                     mla_score_ld(dims->sk), ld_scores);
-    GemmProblem p = ctx_problem(dims, scores, ld_scores, alpha,
-                                static_cast<const float*>(c_kv), ctx);
+    GemmProblem p = ctx_problem(dtype, dims, scores, ld_scores, alpha, c_kv, ctx);
     const GemmPlan plan = plan_gemm(p);
     MLA_CHECK(check_ws(workspace, workspace_bytes, plan.workspace_bytes));
     MLA_TRY_HIP(launch_gemm(p, plan, workspace, stream), "ctx launch");
@@ -425,21 +480,20 @@ int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores, int3
 }
 
 size_t mla_out_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
-    (void)dtype;
-    if (!dims || check_attn_dims(dims, 0) != MLA_OK) return 0;
-    return plan_gemm(out_problem(dims, nullptr, nullptr, nullptr, nullptr)).workspace_bytes;
+    if (!dims || check_out_dims(dtype, dims) != MLA_OK) return 0;
+    return plan_gemm(out_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr)).workspace_bytes;
 }
 
 int mla_out(mla_dtype_t dtype, const mla_dims_t* dims, const float* ctx, const float* row_sum,
             const void* W_uv, void* out, void* workspace, size_t workspace_bytes,
             hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_attn_dims(dims, 0));
+    MLA_CHECK(check_out_dims(dtype, dims));
     MLA_CHECK(check_ptr(ctx, "ctx"));
     MLA_CHECK(check_ptr(row_sum, "row_sum"));
     MLA_CHECK(check_ptr(W_uv, "W_uv"));
     MLA_CHECK(check_ptr(out, "out"));
-    GemmProblem p = out_problem(dims, ctx, row_sum, static_cast<const float*>(W_uv), out);
+    GemmProblem p = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
     const GemmPlan plan = plan_gemm(p);
     MLA_CHECK(check_ws(workspace, workspace_bytes, plan.workspace_bytes));
     MLA_TRY_HIP(launch_gemm(p, plan, workspace, stream), "out launch");
@@ -447,9 +501,8 @@ int mla_out(mla_dtype_t dtype, const mla_dims_t* dims, const float* ctx, const f
 }
 
 size_t mla_q_absorbed_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
-    (void)dtype;
-    if (!dims || check_q_dims(dims) != MLA_OK) return 0;
-    return q_layout(dims).total;
+    if (!dims || check_q_dims(dtype, dims) != MLA_OK) return 0;
+    return q_layout(dtype, dims).total;
 }
 
 int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_q_a,
@@ -458,7 +511,7 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, con
                    void* q_absorbed, void* q_rope, void* workspace, size_t workspace_bytes,
                    hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_q_dims(dims));
+    MLA_CHECK(check_q_dims(dtype, dims));
     MLA_CHECK(check_ptr(x, "x"));
     MLA_CHECK(check_ptr(W_q_a, "W_q_a"));
     MLA_CHECK(check_ptr(q_norm_w, "q_norm_w"));
@@ -470,17 +523,16 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, con
     MLA_CHECK(check_ptr(q_rope, "q_rope"));
     if (!(eps >= 0.0) || !std::isfinite(eps))
         return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
-    const QLayout L = q_layout(dims);
+    const QLayout L = q_layout(dtype, dims);
     MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
 
     const int bq = dims->batch * dims->sq;
     float* lat_acc = at<float>(workspace, L.off_lat_acc);
-    float* lat = at<float>(workspace, L.off_lat);
+    void* lat = at<void>(workspace, L.off_lat);  // storage dtype
     float* raw = at<float>(workspace, L.off_raw);
 
     // 2a1: split-K partials land in lat_acc[split][bq][q_lora]; 2a-n sums them.
-    GemmProblem down = q_down_problem(dims, static_cast<const float*>(x),
-                                      static_cast<const float*>(W_q_a), lat_acc);
+    GemmProblem down = q_down_problem(dtype, dims, x, W_q_a, lat_acc);
     GemmPlan down_plan = L.down;
     int nsplit = 1;
     if (down_plan.split > 1) {
@@ -492,26 +544,25 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, con
     }
     // 2a-n
     MLA_TRY_HIP(launch_rmsnorm(lat_acc, nsplit, (int64_t)bq * dims->q_lora, q_norm_w, lat,
-                               kOutF32, bq, dims->q_lora, (float)eps, stream),
+                               storage_out(dtype), bq, dims->q_lora, (float)eps, stream),
                 "2a-n launch");
     // 2a2
-    GemmProblem up = q_up_problem(dims, lat, static_cast<const float*>(W_q_b), raw);
+    GemmProblem up = q_up_problem(dtype, dims, lat, W_q_b, raw);
     MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
     // 2b
-    MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, kOutF32, dims->batch, dims->sq,
+    MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch, dims->sq,
                             dims->heads, dims->nope, dims->rope, stream),
                 "2b launch");
     // 2c
-    GemmProblem ab = absorb_problem(dims, raw, static_cast<const float*>(W_uk), q_absorbed);
+    GemmProblem ab = absorb_problem(dtype, dims, raw, W_uk, q_absorbed);
     MLA_TRY_HIP(launch_gemm(ab, L.absorb, at<void>(workspace, L.off_abs_ws), stream),
                 "2c launch");
     return ok();
 }
 
 size_t mla_attention_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal) {
-    (void)dtype;
-    if (!dims || check_attn_dims(dims, causal) != MLA_OK) return 0;
-    return attn_layout(dims).total;
+    if (!dims || check_attn_dims(dtype, dims, causal) != MLA_OK) return 0;
+    return attn_layout(dtype, dims).total;
 }
 
 int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
@@ -519,7 +570,7 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
                   double scale, int causal, void* out, void* workspace, size_t workspace_bytes,
                   hipStream_t stream) {
     MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_attn_dims(dims, causal));
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
     MLA_CHECK(check_scale(scale));
     MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
     MLA_CHECK(check_ptr(q_rope, "q_rope"));
@@ -527,7 +578,7 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
     MLA_CHECK(check_ptr(W_uv, "W_uv"));
     MLA_CHECK(check_ptr(out, "out"));
-    const AttnLayout L = attn_layout(dims);
+    const AttnLayout L = attn_layout(dtype, dims);
     MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
 
     float* p = at<float>(workspace, L.off_p);
@@ -539,15 +590,15 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     const int rows = dims->batch * dims->sq * dims->heads;
 
     // 3a
-    MLA_CHECK(run_scores(dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, p, L.ld_p, m,
+    MLA_CHECK(run_scores(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, p, L.ld_p, m,
                          l, stream));
     // 3b
     MLA_TRY_HIP(launch_combine(m, l, alpha, row_sum, rows, L.P, stream), "3b launch");
     // 3c
-    GemmProblem cp = ctx_problem(dims, p, L.ld_p, alpha, static_cast<const float*>(c_kv), ctx);
+    GemmProblem cp = ctx_problem(dtype, dims, p, L.ld_p, alpha, c_kv, ctx);
     MLA_TRY_HIP(launch_gemm(cp, L.ctx, at<void>(workspace, L.off_ctx_ws), stream), "3c launch");
     // 3d
-    GemmProblem op = out_problem(dims, ctx, row_sum, static_cast<const float*>(W_uv), out);
+    GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
     return ok();
 }

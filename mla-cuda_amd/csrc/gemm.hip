@@ -1,44 +1,46 @@
-// Batched fp32 MFMA GEMM for the layer's dense contractions:
+// Batched MFMA GEMM for the layer's dense contractions, fp32 or bf16:
 //   2a1 / 2a2  x @ W_q_a, q_lat @ W_q_b          (NN, G = 1)
 //   2c         q_nope[h] @ W_uk[h]                (NN, G = heads)
 //   3c         (p * alpha) @ c_kv[b]              (NN, G = batch, A scaled by alpha)
 //   3d         (ctx[h] / row_sum) @ W_uv[h]^T     (NT, G = heads, A scaled by 1/row_sum)
 //
 // Workgroup = 4 wave64s.  A BM x BN output tile is split 2x2 / 4x1 / 1x4 over the waves,
-// each wave covering its sub-tile with 32x32 v_mfma_f32_32x32x2_f32 blocks.  K is walked in
-// 32-deep slices staged through LDS with double buffering: the next slice's 128-bit global
-// loads are in flight while the current slice feeds the MFMAs.  Within a slice, K is
-// permuted so lane l's operands for four consecutive MFMAs are contiguous in LDS
-// (k = 4*(l/32) + j), making each fragment one ds_read_b128 (K-contiguous operands) or
-// four conflict-free ds_read_b32 (N-contiguous operands).
+// each wave covering its sub-tile with 32x32 MFMA accumulator blocks
+// (v_mfma_f32_32x32x2_f32, or v_mfma_f32_32x32x16_bf16 in the bf16 path; see mma.h).
+// K is walked in slices of 128 bytes per row (32 fp32 / 64 bf16) staged through
+// double-buffered LDS: the next slice's 128-bit global loads are in flight while the
+// current slice feeds the MFMAs.  Within a slice, K is permuted so each lane's operands
+// for one K step are 16 contiguous bytes: one ds_read_b128 per fragment for K-contiguous
+// operands, four ds_read_b32 (fp32) / eight ds_read_u16 (bf16) for N-contiguous ones.
+// In the bf16 path, fp32 A operands (q_raw, p, ctx) are scaled in fp32 and rounded to
+// bf16 (nearest even) as they are written to LDS.
 //
-// LDS rows of K-contiguous tiles are padded to 36 floats (144 B): the eight lanes of a
+// LDS rows of K-contiguous tiles are 144 B (128 B + 16 B pad): the eight lanes of a
 // ds_read_b128 / ds_write_b128 phase then land on disjoint bank groups.  N-contiguous
-// tiles are padded to BN + 8 so the two half-waves of a ds_read_b32 hit opposite bank
-// halves.
+// tiles are padded so the row read by the second half-wave is 32 banks away from the
+// first half-wave's row.  The measured LDS bank-conflict counter is 0 for every kernel.
 //
 // Split-K is deterministic: slices write fp32 partials to a workspace and a reduction
-// kernel sums them in a fixed order (no float atomics).
+// kernel (or the consumer, for 2a1) sums them in a fixed order -- no float atomics.
 
-#include "common.h"
+#include "mma.h"
 #include "kernels.h"
 
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <type_traits>
 
 namespace mla {
 
 namespace {
 
-constexpr int kBK = 32;         // K per LDS slice
-constexpr int kPadK = 4;        // K-contiguous row padding (floats)
-constexpr int kPadN = 8;        // N-contiguous row padding (floats)
+constexpr int kRowWords = 36;   // K-contiguous LDS row: 128 B of K + 16 B pad, in words
 constexpr int kThreads = 256;
 
 struct GemmArgs {
-    const float* A; int64_t lda, sAg;
-    const float* B; int64_t ldb, sBg;
+    const void* A; int64_t lda, sAg;
+    const void* B; int64_t ldb, sBg;
     void* C; int64_t ldc, sCg;
     float* ws; int64_t ws_split;   // partials [split][G][M][N] when split > 1
     int M, N, K, G;
@@ -47,21 +49,34 @@ struct GemmArgs {
     const float* alpha; int alpha_ld, alpha_tile;
 };
 
-template <int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
+template <typename TL, int BN>
+constexpr int nn_row_words() {
+    // BN elements plus a pad that puts the second half-wave's row 32 banks away
+    return BN * (int)sizeof(TL) / 4 + (sizeof(TL) == 4 ? 8 : 4);
+}
+
+// TL: LDS / MFMA element type (float or bf16_t).  TA: global element type of A (float,
+// or bf16_t when TL is bf16).  B is always TL in global memory.
+template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
-    constexpr int WTM = BM / WM, WTN = BN / WN;     // rows / cols per wave
-    constexpr int TM = WTM / 32, TN = WTN / 32;     // 32x32 blocks per wave
+    using MM = Mma<TL>;
+    constexpr int E = MM::kElems;          // elements per 16-byte chunk
+    constexpr int KS = MM::kSlice;         // K elements per slice
+    constexpr int WTM = BM / WM, WTN = BN / WN;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(WM * WN == 4 && TM >= 1 && TN >= 1, "4 waves, 32x32 blocks");
-    constexpr int A_LD = BM / 32;                   // float4 loads per thread for A
-    constexpr int B_LD = BN / 32;                   // ... for B (both layouts)
-    constexpr int BROWS = NT ? BN : kBK;
-    constexpr int BCOLS = NT ? kBK + kPadK : BN + kPadN;
+    constexpr int A_LD = BM / 32;          // 16-byte LDS chunks per thread per slice (A)
+    constexpr int B_LD = BN / 32;          // ... (B, both layouts)
+    constexpr int BROWS = NT ? BN : KS;
+    constexpr int BWORDS = NT ? kRowWords : nn_row_words<TL, BN>();
+    constexpr bool A_F32 = std::is_same<TA, float>::value;
+    constexpr int A_F4 = A_F32 ? E / 4 : 1;  // float4 loads per A chunk
+    static_assert(A_F32 || AMODE == kAPlain, "scaled A operands are fp32");
 
-    __shared__ __attribute__((aligned(16))) float As[2][BM][kBK + kPadK];
-    __shared__ __attribute__((aligned(16))) float Bs[2][BROWS][BCOLS];
+    __shared__ __attribute__((aligned(16))) uint32_t As[2][BM][kRowWords];
+    __shared__ __attribute__((aligned(16))) uint32_t Bs[2][BROWS][BWORDS];
 
-    const int nblocks = gridDim.x;
-    int t = xcd_logical_block(blockIdx.x, nblocks);
+    int t = xcd_logical_block(blockIdx.x, gridDim.x);
     const int tn = t % a.tiles_n; t /= a.tiles_n;
     const int tm = t % a.tiles_m; t /= a.tiles_m;
     const int sp = t % a.split;
@@ -76,8 +91,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     const int wave = tid >> 6;
     const int wm = wave / WN, wn = wave % WN;
 
-    const float* __restrict__ Ag = a.A + (int64_t)g * a.sAg;
-    const float* __restrict__ Bg = a.B + (int64_t)g * a.sBg;
+    const TA* __restrict__ Ag = static_cast<const TA*>(a.A) + (int64_t)g * a.sAg;
+    const TL* __restrict__ Bg = static_cast<const TL*>(a.B) + (int64_t)g * a.sBg;
 
     // per-thread A rows are fixed across the K loop: row = i*32 + tid/8
     float row_scale[A_LD];
@@ -90,54 +105,47 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
         }
     }
 
-    v4f ra[A_LD], rb[B_LD];
-    float rsc[A_LD];  // per-load A scale, applied when the slice is written to LDS so the
-                      // multiply does not force a wait on the load ahead of the MFMAs
+    // staging registers: fp32 A is kept as floats (scaled and, in the bf16 path, rounded
+    // only when written to LDS, so the multiply does not wait on the load ahead of the
+    // MFMAs); bf16 A and all B chunks are raw 16-byte words
+    v4f raf[A_LD][A_F4];
+    v4u ra[A_LD];
+    float rsc[A_LD];
+    v4u rb[B_LD];
 
     auto load_slice = [&](int k0) {
         #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             const int m = m0 + i * 32 + (tid >> 3);
-            const int k = k0 + 4 * (tid & 7);
-            v4f v = {0.f, 0.f, 0.f, 0.f};
-            if (m < a.M && k < k_end) {
-                const float* src = Ag + (int64_t)m * a.lda + k;
-                if (k + 3 < k_end) {
-                    v = *reinterpret_cast<const v4f*>(src);
-                } else {
-                    #pragma unroll
-                    for (int j = 0; j < 4; ++j) v[j] = (k + j < k_end) ? src[j] : 0.f;
-                }
+            const int k = k0 + E * (tid & 7);
+            const bool in = m < a.M && k < k_end;
+            const TA* src = Ag + (int64_t)m * a.lda + k;
+            if constexpr (A_F32) {
+                #pragma unroll
+                for (int f = 0; f < A_F4; ++f)
+                    raf[i][f] = in ? __builtin_bit_cast(v4f, load_chunk<float>(src + 4 * f, k + 4 * f, k_end))
+                                   : v4f{0.f, 0.f, 0.f, 0.f};
+            } else {
+                ra[i] = in ? load_chunk<TL>(reinterpret_cast<const TL*>(src), k, k_end)
+                           : v4u{0u, 0u, 0u, 0u};
             }
             float sc = row_scale[i];
             if (AMODE == kAAlpha)
-                sc = (m < a.M && k < k_end)
-                         ? a.alpha[((int64_t)g * a.M + m) * a.alpha_ld + k / a.alpha_tile]
-                         : 0.f;
+                sc = in ? a.alpha[((int64_t)g * a.M + m) * a.alpha_ld + k / a.alpha_tile] : 0.f;
             rsc[i] = sc;
-            ra[i] = v;
         }
         #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
-            v4f v = {0.f, 0.f, 0.f, 0.f};
+            v4u v = {0u, 0u, 0u, 0u};
             if (NT) {
                 const int n = n0 + i * 32 + (tid >> 3);
-                const int k = k0 + 4 * (tid & 7);
-                if (n < a.N && k < k_end) {
-                    const float* src = Bg + (int64_t)n * a.ldb + k;
-                    if (k + 3 < k_end) {
-                        v = *reinterpret_cast<const v4f*>(src);
-                    } else {
-                        #pragma unroll
-                        for (int j = 0; j < 4; ++j) v[j] = (k + j < k_end) ? src[j] : 0.f;
-                    }
-                }
+                const int k = k0 + E * (tid & 7);
+                if (n < a.N && k < k_end) v = load_chunk<TL>(Bg + (int64_t)n * a.ldb + k, k, k_end);
             } else {
                 const int e = i * kThreads + tid;
-                const int k = k0 + e / (BN / 4);
-                const int n = n0 + 4 * (e % (BN / 4));
-                if (k < k_end && n < a.N)
-                    v = *reinterpret_cast<const v4f*>(Bg + (int64_t)k * a.ldb + n);
+                const int k = k0 + e / (BN / E);
+                const int n = n0 + E * (e % (BN / E));
+                if (k < k_end && n < a.N) v = *reinterpret_cast<const v4u*>(Bg + (int64_t)k * a.ldb + n);
             }
             rb[i] = v;
         }
@@ -145,16 +153,28 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
 
     auto store_slice = [&](int buf) {
         #pragma unroll
-        for (int i = 0; i < A_LD; ++i)
-            *reinterpret_cast<v4f*>(&As[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) =
-                (AMODE == kAPlain) ? ra[i] : ra[i] * rsc[i];
+        for (int i = 0; i < A_LD; ++i) {
+            v4u w;
+            if constexpr (A_F32 && sizeof(TL) == 4) {
+                const v4f f = (AMODE == kAPlain) ? raf[i][0] : raf[i][0] * rsc[i];
+                w = __builtin_bit_cast(v4u, f);
+            } else if constexpr (A_F32) {
+                const float s = (AMODE == kAPlain) ? 1.f : rsc[i];
+                const v4f f0 = raf[i][0] * s, f1 = raf[i][A_F4 - 1] * s;
+                w = v4u{pack_bf16x2(f0[0], f0[1]), pack_bf16x2(f0[2], f0[3]),
+                        pack_bf16x2(f1[0], f1[1]), pack_bf16x2(f1[2], f1[3])};
+            } else {
+                w = ra[i];
+            }
+            *reinterpret_cast<v4u*>(&As[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = w;
+        }
         #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             if (NT) {
-                *reinterpret_cast<v4f*>(&Bs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rb[i];
+                *reinterpret_cast<v4u*>(&Bs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rb[i];
             } else {
                 const int e = i * kThreads + tid;
-                *reinterpret_cast<v4f*>(&Bs[buf][e / (BN / 4)][4 * (e % (BN / 4))]) = rb[i];
+                *reinterpret_cast<v4u*>(&Bs[buf][e / (BN / E)][4 * (e % (BN / E))]) = rb[i];
             }
         }
     };
@@ -167,7 +187,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    const int nslices = (k_end > k_begin) ? (k_end - k_begin + kBK - 1) / kBK : 0;
+    const int nslices = (k_end > k_begin) ? (k_end - k_begin + KS - 1) / KS : 0;
     if (nslices > 0) {
         load_slice(k_begin);
         store_slice(0);
@@ -175,35 +195,40 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     __syncthreads();
 
     const int l32 = lane & 31;
-    const int kq = 4 * (lane >> 5);
+    const int half = lane >> 5;
     for (int s = 0; s < nslices; ++s) {
         const int buf = s & 1;
-        if (s + 1 < nslices) load_slice(k_begin + (s + 1) * kBK);
+        if (s + 1 < nslices) load_slice(k_begin + (s + 1) * KS);
 
         #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 8) {
-            v4f fa[TM], fb[TN];
+        for (int st = 0; st < 4; ++st) {
+            v4u fa[TM], fb[TN];
             #pragma unroll
             for (int i = 0; i < TM; ++i)
-                fa[i] = *reinterpret_cast<const v4f*>(&As[buf][wm * WTM + i * 32 + l32][kk + kq]);
+                fa[i] = *reinterpret_cast<const v4u*>(&As[buf][wm * WTM + i * 32 + l32][8 * st + 4 * half]);
             #pragma unroll
             for (int j = 0; j < TN; ++j) {
+                const int n = wn * WTN + j * 32 + l32;
                 if (NT) {
-                    fb[j] = *reinterpret_cast<const v4f*>(
-                        &Bs[buf][wn * WTN + j * 32 + l32][kk + kq]);
+                    fb[j] = *reinterpret_cast<const v4u*>(&Bs[buf][n][8 * st + 4 * half]);
+                } else if constexpr (sizeof(TL) == 4) {
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) fb[j][q] = Bs[buf][8 * st + 4 * half + q][n];
                 } else {
+                    const uint16_t* b16 = reinterpret_cast<const uint16_t*>(&Bs[buf][0][0]);
+                    const int r0 = 16 * st + 8 * half;
                     #pragma unroll
                     for (int q = 0; q < 4; ++q)
-                        fb[j][q] = Bs[buf][kk + kq + q][wn * WTN + j * 32 + l32];
+                        fb[j][q] = (uint32_t)b16[(r0 + 2 * q) * (2 * BWORDS) + n] |
+                                   ((uint32_t)b16[(r0 + 2 * q + 1) * (2 * BWORDS) + n] << 16);
                 }
             }
             #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < MM::kSub; ++q)
                 #pragma unroll
                 for (int i = 0; i < TM; ++i)
                     #pragma unroll
-                    for (int j = 0; j < TN; ++j)
-                        acc[i][j] = mfma_32x32x2(fa[i][q], fb[j][q], acc[i][j]);
+                    for (int j = 0; j < TN; ++j) acc[i][j] = MM::sub(fa[i], fb[j], q, acc[i][j]);
         }
 
         if (s + 1 < nslices) store_slice(buf ^ 1);
@@ -228,9 +253,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                         static_cast<float*>(a.C)[(int64_t)g * a.sCg + (int64_t)row * a.ldc + col] =
                             acc[i][j][e];
                     } else {
-                        static_cast<__hip_bfloat16*>(a.C)[(int64_t)g * a.sCg +
-                                                          (int64_t)row * a.ldc + col] =
-                            __float2bfloat16(acc[i][j][e]);
+                        static_cast<bf16_t*>(a.C)[(int64_t)g * a.sCg + (int64_t)row * a.ldc + col] =
+                            (bf16_t)f32_to_bf16_bits(acc[i][j][e]);
                     }
                 }
             }
@@ -255,46 +279,63 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
         const int g = gm / M;
         const int64_t off = (int64_t)g * sCg + (int64_t)m * ldc + n;
         if (OUT == kOutF32) static_cast<float*>(C)[off] = s;
-        else static_cast<__hip_bfloat16*>(C)[off] = __float2bfloat16(s);
+        else static_cast<bf16_t*>(C)[off] = (bf16_t)f32_to_bf16_bits(s);
     }
 }
 
-template <int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
+template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
 hipError_t launch_cfg(const GemmArgs& args, int nblocks, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, NT, AMODE, OUT>), dim3(nblocks),
+    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT>), dim3(nblocks),
                        dim3(kThreads), 0, stream, args);
     return hipGetLastError();
 }
 
-template <bool NT, int AMODE, int OUT>
-hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks,
-                        hipStream_t stream) {
-    if (bm == 128 && bn == 128) return launch_cfg<128, 128, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
-    if (bm == 128 && bn == 96) return launch_cfg<128, 96, 4, 1, NT, AMODE, OUT>(args, nblocks, stream);
-    if (bm == 128 && bn == 64) return launch_cfg<128, 64, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
-    if (bm == 64 && bn == 128) return launch_cfg<64, 128, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
-    if (bm == 64 && bn == 64) return launch_cfg<64, 64, 2, 2, NT, AMODE, OUT>(args, nblocks, stream);
-    if (bm == 32 && bn == 128) return launch_cfg<32, 128, 1, 4, NT, AMODE, OUT>(args, nblocks, stream);
-    if (bm == 128 && bn == 32) return launch_cfg<128, 32, 4, 1, NT, AMODE, OUT>(args, nblocks, stream);
+template <typename TL, typename TA, bool NT, int AMODE, int OUT>
+hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipStream_t stream) {
+#define MLA_TILE(BM_, BN_, WM_, WN_)                                                       \
+    if (bm == BM_ && bn == BN_)                                                             \
+        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT>(args, nblocks, stream);
+    MLA_TILE(128, 128, 2, 2)
+    MLA_TILE(128, 96, 4, 1)
+    MLA_TILE(128, 64, 2, 2)
+    MLA_TILE(64, 128, 2, 2)
+    MLA_TILE(64, 64, 2, 2)
+    MLA_TILE(32, 128, 1, 4)
+    MLA_TILE(128, 32, 4, 1)
+#undef MLA_TILE
     return hipErrorInvalidValue;
 }
 
-template <bool NT>
-hipError_t dispatch_mode(const GemmArgs& args, AMode amode, OutType out, int bm, int bn,
-                         int nblocks, hipStream_t stream) {
-    // partial sums are always fp32; only a direct store converts
-    if (out == kOutF32 || args.split > 1) {
-        switch (amode) {
-            case kAPlain: return launch_tiles<NT, kAPlain, kOutF32>(args, bm, bn, nblocks, stream);
-            case kARowRecip: return launch_tiles<NT, kARowRecip, kOutF32>(args, bm, bn, nblocks, stream);
-            case kAAlpha: return launch_tiles<NT, kAAlpha, kOutF32>(args, bm, bn, nblocks, stream);
-        }
-    } else {
-        switch (amode) {
-            case kAPlain: return launch_tiles<NT, kAPlain, kOutBF16>(args, bm, bn, nblocks, stream);
-            case kARowRecip: return launch_tiles<NT, kARowRecip, kOutBF16>(args, bm, bn, nblocks, stream);
-            case kAAlpha: return launch_tiles<NT, kAAlpha, kOutBF16>(args, bm, bn, nblocks, stream);
-        }
+// The operand/epilogue combinations the layer uses (others are rejected):
+//   fp32:  NN plain  -> f32 (2a1, 2a2, 2c) | NN alpha -> f32 (3c) | NT rowrecip -> f32 (3d)
+//   bf16:  NN plain, A bf16 -> f32 (2a1, 2a2) | NN plain, A f32 -> bf16 (2c)
+//          NN alpha, A f32 -> f32 (3c)         | NT rowrecip, A f32 -> bf16 (3d)
+// A split-K launch writes fp32 partials whatever the output type.
+hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
+                    hipStream_t stream) {
+    const bool split = a.split > 1;
+    if (!p.bf16) {
+        if (!p.b_nt && p.amode == kAPlain && (p.out_type == kOutF32 || split))
+            return launch_tiles<float, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+        if (!p.b_nt && p.amode == kAAlpha && (p.out_type == kOutF32 || split))
+            return launch_tiles<float, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
+        if (p.b_nt && p.amode == kARowRecip && (p.out_type == kOutF32 || split))
+            return launch_tiles<float, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
+        return hipErrorInvalidValue;
+    }
+    if (!p.b_nt && p.amode == kAPlain && !p.a_f32 && (p.out_type == kOutF32 || split))
+        return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+    if (!p.b_nt && p.amode == kAPlain && p.a_f32) {
+        if (split || p.out_type == kOutF32)
+            return launch_tiles<bf16_t, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<bf16_t, float, false, kAPlain, kOutBF16>(a, bm, bn, nblocks, stream);
+    }
+    if (!p.b_nt && p.amode == kAAlpha && p.a_f32 && (p.out_type == kOutF32 || split))
+        return launch_tiles<bf16_t, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
+    if (p.b_nt && p.amode == kARowRecip && p.a_f32) {
+        if (split || p.out_type == kOutF32)
+            return launch_tiles<bf16_t, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<bf16_t, float, true, kARowRecip, kOutBF16>(a, bm, bn, nblocks, stream);
     }
     return hipErrorInvalidValue;
 }
@@ -316,10 +357,11 @@ constexpr TileShape kTiles[] = {
     {128, 128, 0.80}, {128, 96, 0.78}, {128, 64, 0.72}, {64, 128, 0.72},
     {64, 64, 0.60},   {32, 128, 0.55}, {128, 32, 0.55}};
 
-int lds_bytes(int bm, int bn, bool nt) {
-    const int a = 2 * bm * (kBK + kPadK);
-    const int b = nt ? 2 * bn * (kBK + kPadK) : 2 * kBK * (bn + kPadN);
-    return (a + b) * 4;
+int lds_bytes(int bm, int bn, bool nt, bool bf16) {
+    const int a = 2 * bm * kRowWords * 4;
+    const int nn_row = bf16 ? bn * 2 + 16 : bn * 4 + 32;
+    const int b = nt ? 2 * bn * kRowWords * 4 : 2 * (bf16 ? 64 : 32) * nn_row;
+    return a + b;
 }
 
 bool tile_supported(int bm, int bn) {
@@ -353,9 +395,13 @@ bool plan_override(const GemmProblem& p, GemmPlan* out) {
 }  // namespace
 
 GemmPlan plan_gemm(const GemmProblem& p) {
-    constexpr double kCuRate = 256.0 * 2.4e9;   // fp32 MFMA flop/s per CU
+    // fp32 MFMA: 256 flop/clk/CU at 2.4 GHz; dense bf16 MFMA is 16x that
+    const double kCuRate = 256.0 * 2.4e9 * (p.bf16 ? 16.0 : 1.0);
     constexpr double kHbm = 5.0e12;             // sustained HBM B/s
     constexpr double kReduceLaunch = 3e-6;      // s
+    const int kBK = p.bf16 ? 64 : 32;           // K per slice
+    const double eb = p.bf16 ? 2.0 : 4.0;       // bytes per B element
+    const double ea = p.a_f32 || !p.bf16 ? 4.0 : 2.0;
     const int kslices = cdiv(p.K, kBK);
     GemmPlan best;
     double best_t = 1e300;
@@ -363,7 +409,7 @@ GemmPlan plan_gemm(const GemmProblem& p) {
         for (const auto& t : kTiles) {
             const int tm = cdiv(p.M, t.bm), tn = cdiv(p.N, t.bn);
             const int64_t tiles = (int64_t)tm * tn * p.G;
-            const int occ = std::max(1, std::min(2, 163840 / lds_bytes(t.bm, t.bn, p.b_nt)));
+            const int occ = std::max(1, std::min(2, 163840 / lds_bytes(t.bm, t.bn, p.b_nt, p.bf16)));
             for (int split = 1; split <= std::max(1, kslices / 2); split *= 2) {
                 const int per = cdiv(kslices, split);
                 const int real_split = cdiv(kslices, per);
@@ -377,8 +423,8 @@ GemmPlan plan_gemm(const GemmProblem& p) {
                 const double t_mfma = per_cu * wg_flops / (kCuRate * t.eff * hide);
                 // B operand streamed once per M tile (weights / cache), A once per N tile
                 // (small, mostly L2), C written once
-                const double bytes = 4.0 * ((double)p.K * p.N * p.G * std::min(tm, 2) +
-                                            (double)p.M * p.K * p.G + (double)p.M * p.N * p.G);
+                const double bytes = eb * (double)p.K * p.N * p.G * std::min(tm, 2) +
+                                     ea * (double)p.M * p.K * p.G + 4.0 * (double)p.M * p.N * p.G;
                 double tt = std::max(t_mfma, bytes / kHbm);
                 if (split > 1)
                     tt += 4.0 * (split + 1) * (double)p.M * p.N * p.G / kHbm + kReduceLaunch;
@@ -390,7 +436,7 @@ GemmPlan plan_gemm(const GemmProblem& p) {
         }
     }
     const int per = cdiv(kslices, std::max(1, std::min(best.split, kslices)));
-    best.k_chunk = per * kBK;
+    best.k_chunk = per * kBK;  // whole slices; the kernel's slice is the same kBK
     best.split = cdiv(kslices, per);  // no empty slices
     best.workspace_bytes =
         best.split > 1 ? (size_t)best.split * p.G * p.M * p.N * sizeof(float) : 0;
@@ -416,8 +462,7 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     const int64_t nblocks64 = (int64_t)a.tiles_m * a.tiles_n * a.G * a.split;
     if (nblocks64 <= 0 || nblocks64 > 0x7fffffff) return hipErrorInvalidValue;
     const int nblocks = (int)nblocks64;
-    hipError_t e = p.b_nt ? dispatch_mode<true>(a, p.amode, p.out_type, plan.bm, plan.bn, nblocks, stream)
-                          : dispatch_mode<false>(a, p.amode, p.out_type, plan.bm, plan.bn, nblocks, stream);
+    hipError_t e = dispatch(p, a, plan.bm, plan.bn, nblocks, stream);
     if (e != hipSuccess || plan.split == 1 || !reduce) return e;
     const int64_t total = (int64_t)p.G * p.M * p.N;
     const int rblocks = (int)std::min<int64_t>((total + 255) / 256, 8 * kNumCUs);

@@ -8,7 +8,8 @@
 namespace mla {
 
 // ---------------------------------------------------------------- batched MFMA GEMM
-// C[g][m][n] = sum_k opA(A)[g][m][k] * opB(B)[g][k][n]   (float32 in, float32 accumulate)
+// C[g][m][n] = sum_k opA(A)[g][m][k] * opB(B)[g][k][n]   (fp32 accumulate; fp32 or bf16
+// MFMA as GemmProblem::bf16 says)
 //   A[g][m][k]  at A + g*sAg + m*lda + k
 //   B (NN)      at B + g*sBg + k*ldb + n      B (NT) at B + g*sBg + n*ldb + k
 //   C[g][m][n]  at C + g*sCg + m*ldc + n
@@ -18,11 +19,13 @@ enum AMode { kAPlain = 0, kARowRecip = 1, kAAlpha = 2 };
 enum OutType { kOutF32 = 0, kOutBF16 = 1 };
 
 struct GemmProblem {
-    const float* A = nullptr; int64_t lda = 0, sAg = 0;
-    const float* B = nullptr; int64_t ldb = 0, sBg = 0;
+    const void* A = nullptr; int64_t lda = 0, sAg = 0;
+    const void* B = nullptr; int64_t ldb = 0, sBg = 0;
     void* C = nullptr;        int64_t ldc = 0, sCg = 0;
     int M = 0, N = 0, K = 0, G = 1;
     bool b_nt = false;
+    bool bf16 = false;   // B (weights / cache) and the MFMA are bf16 (else fp32)
+    bool a_f32 = true;   // A is fp32 in global memory (else the storage dtype)
     AMode amode = kAPlain;
     const float* rs = nullptr; int64_t rs_m = 0, rs_g = 0;
     const float* alpha = nullptr; int alpha_ld = 0, alpha_tile = 1;
@@ -60,10 +63,11 @@ hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha
 
 // ---------------------------------------------------------------- 3a scores
 struct ScoresProblem {
-    const float* qa = nullptr;   // [B*Sq*H, R]
-    const float* qr = nullptr;   // [B*Sq*H, D]
-    const float* ckv = nullptr;  // [B, Sk, R]
-    const float* pe = nullptr;   // [B, Sk, D]
+    const void* qa = nullptr;    // [B*Sq*H, R]   storage dtype
+    const void* qr = nullptr;    // [B*Sq*H, D]
+    const void* ckv = nullptr;   // [B, Sk, R]
+    const void* pe = nullptr;    // [B, Sk, D]
+    bool bf16 = false;           // storage / MFMA dtype bf16 (else fp32)
     float* p = nullptr;          // [B*Sq*H, ld_p]
     float* m_part = nullptr;     // [B*Sq*H, P]
     float* l_part = nullptr;

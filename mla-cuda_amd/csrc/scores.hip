@@ -5,10 +5,10 @@
 // (R+D)-deep reduction whose last D columns come from the second operand pair.
 //
 // Workgroup tile: 128 rows x 128 keys (one softmax partial).  Each of the 4 waves owns
-// 32 rows x 128 keys = 4 v_mfma_f32_32x32x2_f32 accumulator blocks, so a row's 128 keys
+// 32 rows x 128 keys = 4 MFMA accumulator blocks (fp32 or bf16 steps, mma.h), so a row's 128 keys
 // live in one wave: the row max and row sum need no LDS, only a 32-lane reduction
-// (DPP + ds_swizzle) of each accumulator register.  Depth is walked in 32-deep slices
-// staged through double-buffered LDS, exactly like the GEMM engine.
+// (DPP + ds_swizzle) of each accumulator register.  Depth is walked in 128-byte slices
+// (32 fp32 / 64 bf16) staged through double-buffered LDS, exactly like the GEMM engine.
 //
 // Epilogue per row and 128-key tile j (mla_kernels.cu:971-1032 computes the same
 // quantities): m_j = max over visible keys of t = s/scale, p = exp(t - m_j) stored into
@@ -16,26 +16,29 @@
 // Grid: batch x row tiles x key tiles, XCD-ordered so one XCD streams one batch's keys
 // while its L2 keeps that batch's Q rows.
 
-#include "common.h"
 #include "kernels.h"
+#include "mma.h"
 
 namespace mla {
 
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 32, kPad = 4, kThreads = 256;
+constexpr int kBM = 128, kBN = 128, kRowWords = 36, kThreads = 256;
 
 struct ScoresArgs {
-    const float* qa; const float* qr; const float* ckv; const float* pe;
+    const void* qa; const void* qr; const void* ckv; const void* pe;
     float* p; float* m_part; float* l_part;
     int B, Sq, Sk, H, R, D, ld_p, P, tiles_r;
     float inv_scale;
     int causal;
 };
 
+template <typename TL>
 __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
-    __shared__ __attribute__((aligned(16))) float Qs[2][kBM][kBK + kPad];
-    __shared__ __attribute__((aligned(16))) float Ks[2][kBN][kBK + kPad];
+    using MM = Mma<TL>;
+    constexpr int E = MM::kElems, KS = MM::kSlice;
+    __shared__ __attribute__((aligned(16))) uint32_t Qs[2][kBM][kRowWords];
+    __shared__ __attribute__((aligned(16))) uint32_t Ks[2][kBN][kRowWords];
 
     int t = xcd_logical_block(blockIdx.x, gridDim.x);
     const int kt = t % a.P; t /= a.P;
@@ -48,38 +51,37 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
     const int64_t row_base = (int64_t)b * rows_b;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, kq = 4 * (lane >> 5);
+    const int l32 = lane & 31, half = lane >> 5;
 
-    const int nsl_r = (a.R + kBK - 1) / kBK;
-    const int nsl = nsl_r + (a.D + kBK - 1) / kBK;
+    const int nsl_r = (a.R + KS - 1) / KS;
+    const int nsl = nsl_r + (a.D + KS - 1) / KS;
 
-    v4f rq[4], rk[4];
+    v4u rq[4], rk[4];
     auto load_slice = [&](int s) {
         const bool rope = s >= nsl_r;
-        const int c0 = rope ? (s - nsl_r) * kBK : s * kBK;
+        const int c0 = rope ? (s - nsl_r) * KS : s * KS;
         const int cw = rope ? a.D : a.R;
-        const float* qsrc = rope ? a.qr : a.qa;
-        const float* ksrc = rope ? a.pe : a.ckv;
-        const int c = c0 + 4 * (tid & 7);
+        const TL* qsrc = static_cast<const TL*>(rope ? a.qr : a.qa);
+        const TL* ksrc = static_cast<const TL*>(rope ? a.pe : a.ckv);
+        const int c = c0 + E * (tid & 7);
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = r0 + i * 32 + (tid >> 3);
-            v4f v = {0.f, 0.f, 0.f, 0.f};
-            if (r < rows_b && c < cw)
-                v = *reinterpret_cast<const v4f*>(qsrc + (row_base + r) * cw + c);
+            v4u v = {0u, 0u, 0u, 0u};
+            if (r < rows_b && c < cw) v = load_chunk<TL>(qsrc + (row_base + r) * cw + c, c, cw);
             rq[i] = v;
             const int k = k0 + i * 32 + (tid >> 3);
-            v4f w = {0.f, 0.f, 0.f, 0.f};
+            v4u w = {0u, 0u, 0u, 0u};
             if (k < a.Sk && c < cw)
-                w = *reinterpret_cast<const v4f*>(ksrc + ((int64_t)b * a.Sk + k) * cw + c);
+                w = load_chunk<TL>(ksrc + ((int64_t)b * a.Sk + k) * cw + c, c, cw);
             rk[i] = w;
         }
     };
     auto store_slice = [&](int buf) {
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<v4f*>(&Qs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rq[i];
-            *reinterpret_cast<v4f*>(&Ks[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rk[i];
+            *reinterpret_cast<v4u*>(&Qs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rq[i];
+            *reinterpret_cast<v4u*>(&Ks[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rk[i];
         }
     };
 
@@ -96,16 +98,16 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         const int buf = s & 1;
         if (s + 1 < nsl) load_slice(s + 1);
         #pragma unroll
-        for (int kk = 0; kk < kBK; kk += 8) {
-            const v4f fq = *reinterpret_cast<const v4f*>(&Qs[buf][wave * 32 + l32][kk + kq]);
-            v4f fk[4];
+        for (int st = 0; st < 4; ++st) {
+            const v4u fq = *reinterpret_cast<const v4u*>(&Qs[buf][wave * 32 + l32][8 * st + 4 * half]);
+            v4u fk[4];
             #pragma unroll
             for (int j = 0; j < 4; ++j)
-                fk[j] = *reinterpret_cast<const v4f*>(&Ks[buf][j * 32 + l32][kk + kq]);
+                fk[j] = *reinterpret_cast<const v4u*>(&Ks[buf][j * 32 + l32][8 * st + 4 * half]);
             #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < MM::kSub; ++q)
                 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[j] = mfma_32x32x2(fq[q], fk[j][q], acc[j]);
+                for (int j = 0; j < 4; ++j) acc[j] = MM::sub(fq, fk[j], q, acc[j]);
         }
         if (s + 1 < nsl) store_slice(buf ^ 1);
         __syncthreads();
@@ -159,7 +161,10 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     a.causal = p.causal ? 1 : 0;
     const int64_t nblocks = (int64_t)p.B * a.tiles_r * a.P;
     if (nblocks <= 0 || nblocks > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(scores_kernel, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
+    if (p.bf16)
+        hipLaunchKernelGGL(scores_kernel<bf16_t>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(scores_kernel<float>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -156,6 +156,15 @@ def test_q_absorbed_validation(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "eps" in _err(lib)
 
 
+def test_bf16_needs_8_element_rows(lib):
+    d = dsv3(1, 1, 100)
+    d.rope = 68
+    st = lib.mla_attention(BF16, ctypes.byref(d), *([P16] * 5), ctypes.c_double(13.85), 0, P16,
+                           P16, ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "multiple of 8 for bf16" in _err(lib)
+    assert lib.mla_attention_workspace_bytes(BF16, ctypes.byref(dsv3(2, 1, 100)), 0) > 0
+
+
 def test_scores_validation(lib):
     d = dsv3(1, 1, 100)
     st = lib.mla_scores(F32, ctypes.byref(d), P16, P16, P16, P16, ctypes.c_double(13.8), 0,

@@ -1,0 +1,140 @@
+"""GPU parity of the bf16 path (bf16 storage, fp32 accumulation on
+bf16 MFMA).
+
+Per step, the oracle runs in fp32 on the very bf16 values the kernel reads (and, where the
+kernel rounds an fp32 operand to bf16 before its MFMA -- q_raw in 2c, p*alpha in 3c, ctx in
+3d -- on the rounded operand), so each step is held to fp32-accumulation accuracy.  The
+whole layer is compared with the fp32 oracle on the bf16-rounded inputs at BASELINE's
+bf16 tolerance, rtol 2e-2 (atol 2e-2 on O(1) outputs).
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import mla_ref as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+D = R.DSV3
+SCALE = math.sqrt(D.qk_head)
+BF = torch.bfloat16
+
+
+@pytest.fixture(scope="module")
+def ext():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import mla_custom_cuda
+    return mla_custom_cuda
+
+
+def gpu(t):
+    return t.to(DEV)
+
+
+def rb(t):
+    """Round to bf16 and back (what the kernel does to an fp32 MFMA operand)."""
+    return t.to(BF).float()
+
+
+@pytest.mark.parametrize("M,N,K", [(128, 1536, 7168), (1, 24576, 1536), (40, 200, 72)])
+def test_gemm_bf16(ext, M, N, K):
+    g = torch.Generator().manual_seed(M + N)
+    A = torch.randn(M, K, generator=g).to(BF)
+    W = (torch.randn(K, N, generator=g) / math.sqrt(K)).to(BF)
+    got = ext.gemm(gpu(A), gpu(W)).cpu()
+    assert got.dtype == torch.float32
+    ref = (A.double() @ W.double()).float()
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_rmsnorm_rope_bf16(ext):
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(16, 1536, generator=g)
+    w = (1 + 0.1 * torch.randn(1536, generator=g)).to(BF)
+    got = ext.rmsnorm(gpu(x), gpu(w), 1e-6).cpu()
+    assert got.dtype == BF
+    ref = R.step_norm(x, w.float(), 1e-6, BF)
+    torch.testing.assert_close(got.float(), ref.float(), rtol=1e-2, atol=1e-2)
+    q_raw = torch.randn(8, D.n_heads * D.qk_head, generator=g)
+    pos = torch.tensor([4988])
+    got = ext.rope(gpu(q_raw), gpu(pos), 8, 1, D.n_heads, D.nope, D.rope, BF).cpu()
+    ref = R.step_rope(q_raw, pos, R.rope_inv_freq(D.rope), 8, 1, D.n_heads, D.nope, D.rope, BF)
+    assert got.dtype == BF
+    torch.testing.assert_close(got.float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_absorb_bf16(ext):
+    g = torch.Generator().manual_seed(4)
+    B, Sq = 16, 1
+    q_raw = torch.randn(B * Sq, D.n_heads * D.qk_head, generator=g)
+    W_uk = (torch.randn(D.n_heads, D.nope, D.kv_rank, generator=g) / math.sqrt(D.kv_rank)).to(BF)
+    got = ext.absorb(gpu(q_raw), gpu(W_uk), B, Sq, D.rope).cpu()
+    assert got.dtype == BF
+    ref = R.step_absorb(rb(q_raw).double(), W_uk.double(), B, Sq, D.nope, torch.float64)
+    torch.testing.assert_close(got.float(), ref.float(), rtol=8e-3, atol=8e-3)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", [(2, 1, 4989, False), (1, 8, 300, True)])
+def test_attention_steps_bf16(ext, B, Sq, Sk, causal):
+    g = torch.Generator().manual_seed(Sk)
+    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(BF)  # noqa: E731
+    qa, qr = mk(B, Sq, D.n_heads, D.kv_rank, sc=0.05), mk(B, Sq, D.n_heads, D.rope, sc=0.05)
+    ck, pe = mk(B, Sk, D.kv_rank), mk(B, Sk, D.rope)
+    wuv = mk(D.n_heads, D.v, D.kv_rank, sc=1 / math.sqrt(D.kv_rank))
+    p, m, l = ext.scores(gpu(qa), gpu(qr), gpu(ck), gpu(pe), SCALE, causal)
+    rp, rm, rl = R.step_scores(qa.float(), qr.float(), ck.float(), pe.float(), SCALE,
+                               R.SCORE_TILE, causal)
+    torch.testing.assert_close(m.cpu(), rm, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(l.cpu(), rl, rtol=1e-4, atol=1e-4)
+    torch.testing.assert_close(p.cpu()[:, :Sk], rp, rtol=1e-4, atol=1e-5)
+    alpha, rs = ext.combine(m, l)
+    ctx = ext.ctx(p, alpha, gpu(ck), Sq, D.n_heads)
+    a = alpha.cpu().repeat_interleave(R.SCORE_TILE, dim=1)[:, :Sk]
+    w = rb(p.cpu()[:, :Sk] * a).double().reshape(B, Sq * D.n_heads, Sk)
+    rctx = torch.bmm(w, ck.double()).reshape(B, Sq, D.n_heads, -1).float()
+    torch.testing.assert_close(ctx.cpu(), rctx, rtol=1e-4, atol=1e-3)
+    out = ext.out(ctx, rs, gpu(wuv)).cpu()
+    assert out.dtype == BF
+    cn = rb(ctx.cpu() / rs.cpu().reshape(B, Sq, D.n_heads, 1))
+    rout = torch.einsum("bshr,hdr->bshd", cn.double(), wuv.double()).float()
+    torch.testing.assert_close(out.float(), rout, rtol=8e-3, atol=8e-3)
+
+
+def run_layer(ext, inp, causal=False):
+    W_uk, W_uv = R.split_wkv_b(inp["wkv_b"], D.nope)
+    g = {k: gpu(v) for k, v in inp.items()}
+    qa, qr = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"],
+                            gpu(W_uk.contiguous()), g["positions"], D.nope, D.rope, 1e-6)
+    out = ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], gpu(W_uv.contiguous()), SCALE,
+                            causal)
+    return qa, qr, out
+
+
+@pytest.mark.parametrize("B,Sq,Sk", [(4, 1, 4989), (1, 1, 512), (2, 3, 1000)])
+def test_layer_bf16_vs_fp32_oracle(ext, B, Sq, Sk):
+    inp = R.make_inputs(B, Sq, Sk, seed=0, dtype=BF)
+    qa, qr, out = run_layer(ext, inp)
+    assert out.dtype == BF and qa.dtype == BF and qr.dtype == BF
+    f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
+    ref = R.mla_layer(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], f32["wkv_b"],
+                      f32["c_kv"], f32["pe_cache"], f32["positions"])
+    torch.testing.assert_close(out.float().cpu(), ref, rtol=2e-2, atol=2e-2)
+
+
+def test_layer_bf16_cfg4_full_size(ext):
+    """B=128, Sq=1, Sk=4989 in bf16; oracle on three sequences."""
+    inp = R.make_inputs(128, 1, 4989, seed=0, dtype=BF)
+    qa, qr, out = run_layer(ext, inp)
+    pick = [0, 64, 127]
+    f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
+    for k in ("x", "c_kv", "pe_cache"):
+        f32[k] = f32[k][pick]
+    ref = R.mla_layer(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], f32["wkv_b"],
+                      f32["c_kv"], f32["pe_cache"], f32["positions"])
+    torch.testing.assert_close(out.float().cpu()[pick], ref, rtol=2e-2, atol=2e-2)
