@@ -39,11 +39,13 @@ for _p in (ROOT, PKG):
 METRIC = "µs per MLA layer (B=128 decode, Sk=4989) + HBM GB/s & MFMA util % per step"
 PEAK_HBM = 8.0e12          # B/s, MI355X HBM3E
 PEAK_F32 = 157.3e12        # flop/s, dense fp32 MFMA
+PEAK_BF16 = 2.5e15         # flop/s, dense bf16 MFMA
 REF_A6000_US = 16920.0     # reference's published layer time at this shape (README.md:367)
 
 CONFIGS = {
     # name: (B, Sq, Sk, description)
     "cfg2": (128, 1, 4989, "B=128 Sq=1 Sk=4989 fp32 decode (BASELINE configs[1])"),
+    "cfg4": (128, 1, 4989, "B=128 Sq=1 Sk=4989 bf16 decode (BASELINE configs[3])"),
     "cfg1": (1, 1, 512, "B=1 Sq=1 Sk=512 fp32 decode (BASELINE configs[0])"),
     "b1": (1, 1, 4989, "B=1 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
     "b8": (8, 1, 4989, "B=8 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
@@ -75,9 +77,10 @@ def step_work(B, Sq, Sk, dims, e=4):
     return w
 
 
-def build_inputs(B, Sq, Sk, seed=0):
+def build_inputs(B, Sq, Sk, seed=0, dtype=None):
+    import torch
     import mla_inputs
-    return mla_inputs.make_inputs(B, Sq, Sk, seed=seed)
+    return mla_inputs.make_inputs(B, Sq, Sk, seed=seed, dtype=dtype or torch.float32)
 
 
 def cpu_baseline(inp, gpu_out, budget_s=30.0):
@@ -90,6 +93,8 @@ def cpu_baseline(inp, gpu_out, budget_s=30.0):
     threads = max(1, min(16, os.cpu_count() or 1))
     torch.set_num_threads(threads)
     B = inp["x"].shape[0]
+
+    inp = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
 
     def layer(b):
         return R.mla_layer(inp["x"][:b], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
@@ -124,8 +129,15 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--dtype", default=None, choices=["f32", "bf16"],
+                    help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES, 3 times (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                    help="HBM traffic per launch measured by rocprofv3 --pmc (see DESIGN.md)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -143,11 +155,23 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.empty(args.copy_probe // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe}), flush=True)
+        return
     dims = mla_inputs.DEEPSEEK_V3
     B, Sq, Sk, desc = CONFIGS[args.config]
+    dname = args.dtype or ("bf16" if args.config == "cfg4" else "f32")
+    dt = torch.bfloat16 if dname == "bf16" else torch.float32
+    if dname == "bf16" and "bf16" not in desc:
+        desc = desc.replace("fp32", "bf16")
     print(f"[bench] config {args.config}: {desc}", file=sys.stderr, flush=True)
 
-    inp = build_inputs(B, Sq, Sk, args.seed)
+    inp = build_inputs(B, Sq, Sk, args.seed, dt)
     W_uk = inp["wkv_b"][:, :dims.nope, :].contiguous()
     W_uv = inp["wkv_b"][:, dims.nope:, :].contiguous()
     g = {k: v.to(dev) for k, v in inp.items()}
@@ -187,7 +211,7 @@ def main():
         lat = ext.rmsnorm(lat_acc, g["q_norm_w"], eps); ev[2].record()
         raw = ext.gemm(lat, g["W_q_b"]); ev[3].record()
         qr = ext.rope(raw, g["positions"], B, Sq, dims.n_heads, dims.nope, dims.rope,
-                      torch.float32); ev[4].record()
+                      dt); ev[4].record()
         qa = ext.absorb(raw, W_uk_d, B, Sq, dims.rope); ev[5].record()
         p, m, l = ext.scores(qa, qr, g["c_kv"], g["pe_cache"], scale); ev[6].record()
         alpha, rs = ext.combine(m, l); ev[7].record()
@@ -207,7 +231,8 @@ def main():
     steps_sum = sum(step_us.values())
     same = (o_steps - out).abs().max().item()
 
-    work = step_work(B, Sq, Sk, dims)
+    work = step_work(B, Sq, Sk, dims, e=2 if dname == "bf16" else 4)
+    peak_mfma = PEAK_BF16 if dname == "bf16" else PEAK_F32
     per_step = {}
     for n in names:
         fl, by = work[n]
@@ -215,15 +240,31 @@ def main():
         per_step[n] = {"us": round(step_us[n], 2), "gflop": round(fl / 1e9, 3),
                        "mbytes": round(by / 1e6, 2),
                        "tflops": round(fl / t / 1e12, 2), "gbps": round(by / t / 1e9, 1),
-                       "mfma_pct": round(100 * fl / t / PEAK_F32, 1),
+                       "mfma_pct": round(100 * fl / t / peak_mfma, 1),
                        "hbm_pct": round(100 * by / t / PEAK_HBM, 1)}
     dom = max(("3a", "3c"), key=lambda n: step_us[n])
     fl, by = work[dom]
-    achieved = fl / (step_us[dom] * 1e-6) / 1e12
-    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
-                "peak": PEAK_F32 / 1e12, "unit": "TFLOP/s",
-                "frac": round(achieved / (PEAK_F32 / 1e12), 4), "traffic": None,
-                "algorithmic_flop": fl, "algorithmic_bytes": by}
+    t_dom = step_us[dom] * 1e-6
+    if fl / by > peak_mfma / PEAK_HBM:   # above the ridge: compute-bound
+        achieved = fl / t_dom / 1e12
+        roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                    "peak": peak_mfma / 1e12, "unit": "TFLOP/s",
+                    "frac": round(achieved / (peak_mfma / 1e12), 4)}
+    else:
+        achieved = by / t_dom / 1e9
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": round(achieved, 1),
+                    "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                    "frac": round(achieved / (PEAK_HBM / 1e9), 4)}
+    traffic = None
+    try:
+        with open(args.traffic) as f:
+            tr = json.load(f)
+        key = f"{args.config}/{dname}/{dom}"
+        if key in tr.get("kernels", {}):
+            traffic = tr["kernels"][key]["hbm_bytes_per_launch"]
+    except (OSError, ValueError):
+        traffic = None
+    roofline.update({"traffic": traffic, "algorithmic_flop": fl, "algorithmic_bytes": by})
 
     value_us = ms_per_step * 1e3
     rec = {
@@ -236,9 +277,10 @@ def main():
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": False,
         "scaling": "weak",
-        "vs_baseline": round(value_us / REF_A6000_US, 4) if args.config == "cfg2" else None,
+        "vs_baseline": (round(value_us / REF_A6000_US, 4)
+                        if args.config == "cfg2" and dname == "f32" else None),
         "vs_baseline_ref": "reference kernels, RTX A6000, 16.92 ms (README.md:367)",
-        "dtype": "f32",
+        "dtype": dname,
         "data": "synthetic",
         "config": {"workload": desc, "B": B, "Sq": Sq, "Sk": Sk, "hidden": dims.hidden,
                    "heads": dims.n_heads, "q_lora": dims.q_lora, "kv_rank": dims.kv_rank,
