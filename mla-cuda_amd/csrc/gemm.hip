@@ -57,8 +57,12 @@ constexpr int nn_row_words() {
 
 // TL: LDS / MFMA element type (float or bf16_t).  TA: global element type of A (float,
 // or bf16_t when TL is bf16).  B is always TL in global memory.
+// PD = depth of the register prefetch ring (slices in flight while one feeds the MFMAs):
+// 1 for fp32 (MFMA-bound, ~4K MFMA cycles per slice), 2 for bf16 (8x less MFMA work per
+// slice, so more HBM latency to cover).
 template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
+    constexpr int PD = sizeof(TL) == 2 ? 2 : 1;
     using MM = Mma<TL>;
     constexpr int E = MM::kElems;          // elements per 16-byte chunk
     constexpr int KS = MM::kSlice;         // K elements per slice
@@ -67,8 +71,13 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     static_assert(WM * WN == 4 && TM >= 1 && TN >= 1, "4 waves, 32x32 blocks");
     constexpr int A_LD = BM / 32;          // 16-byte LDS chunks per thread per slice (A)
     constexpr int B_LD = BN / 32;          // ... (B, both layouts)
-    constexpr int BROWS = NT ? BN : KS;
-    constexpr int BWORDS = NT ? kRowWords : nn_row_words<TL, BN>();
+    // bf16 N-contiguous B (weights, c_kv) is transposed while staging so LDS holds it
+    // K-contiguous like an NT operand: each of 2*BN threads loads a 4-row x 8-column block
+    // and writes eight 8-byte k-runs; every fragment is then one ds_read_b128 instead of
+    // eight ds_read_u16 (which made the bf16 NN kernels LDS-issue bound).
+    constexpr bool TRN = !NT && sizeof(TL) == 2;
+    constexpr int BROWS = (NT || TRN) ? BN : KS;
+    constexpr int BWORDS = (NT || TRN) ? kRowWords : nn_row_words<TL, BN>();
     constexpr bool A_F32 = std::is_same<TA, float>::value;
     constexpr int A_F4 = A_F32 ? E / 4 : 1;  // float4 loads per A chunk
     static_assert(A_F32 || AMODE == kAPlain, "scaled A operands are fp32");
@@ -108,12 +117,12 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     // staging registers: fp32 A is kept as floats (scaled and, in the bf16 path, rounded
     // only when written to LDS, so the multiply does not wait on the load ahead of the
     // MFMAs); bf16 A and all B chunks are raw 16-byte words
-    v4f raf[A_LD][A_F4];
-    v4u ra[A_LD];
-    float rsc[A_LD];
-    v4u rb[B_LD];
+    v4f raf[PD][A_LD][A_F4];
+    v4u ra[PD][A_LD];
+    float rsc[PD][A_LD];
+    v4u rb[PD][TRN ? 4 : B_LD];
 
-    auto load_slice = [&](int k0) {
+    auto load_slice = [&](int k0, int slot) {
         #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             const int m = m0 + i * 32 + (tid >> 3);
@@ -123,16 +132,30 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             if constexpr (A_F32) {
                 #pragma unroll
                 for (int f = 0; f < A_F4; ++f)
-                    raf[i][f] = in ? __builtin_bit_cast(v4f, load_chunk<float>(src + 4 * f, k + 4 * f, k_end))
-                                   : v4f{0.f, 0.f, 0.f, 0.f};
+                    raf[slot][i][f] = in ? __builtin_bit_cast(v4f, load_chunk<float>(src + 4 * f, k + 4 * f, k_end))
+                                         : v4f{0.f, 0.f, 0.f, 0.f};
             } else {
-                ra[i] = in ? load_chunk<TL>(reinterpret_cast<const TL*>(src), k, k_end)
-                           : v4u{0u, 0u, 0u, 0u};
+                ra[slot][i] = in ? load_chunk<TL>(reinterpret_cast<const TL*>(src), k, k_end)
+                                 : v4u{0u, 0u, 0u, 0u};
             }
             float sc = row_scale[i];
             if (AMODE == kAAlpha)
                 sc = in ? a.alpha[((int64_t)g * a.M + m) * a.alpha_ld + k / a.alpha_tile] : 0.f;
-            rsc[i] = sc;
+            rsc[slot][i] = sc;
+        }
+        if constexpr (TRN) {
+            if (tid < 2 * BN) {
+                const int g = tid & 15, c = tid >> 4;   // rows 4g..4g+3, columns 8c..8c+7
+                const int n = n0 + 8 * c;
+                #pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int k = k0 + 4 * g + i;
+                    rb[slot][i] = (k < k_end && n < a.N)
+                                      ? *reinterpret_cast<const v4u*>(Bg + (int64_t)k * a.ldb + n)
+                                      : v4u{0u, 0u, 0u, 0u};
+                }
+            }
+            return;
         }
         #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
@@ -147,34 +170,50 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                 const int n = n0 + E * (e % (BN / E));
                 if (k < k_end && n < a.N) v = *reinterpret_cast<const v4u*>(Bg + (int64_t)k * a.ldb + n);
             }
-            rb[i] = v;
+            rb[slot][i] = v;
         }
     };
 
-    auto store_slice = [&](int buf) {
+    auto store_slice = [&](int buf, int slot) {
         #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             v4u w;
             if constexpr (A_F32 && sizeof(TL) == 4) {
-                const v4f f = (AMODE == kAPlain) ? raf[i][0] : raf[i][0] * rsc[i];
+                const v4f f = (AMODE == kAPlain) ? raf[slot][i][0] : raf[slot][i][0] * rsc[slot][i];
                 w = __builtin_bit_cast(v4u, f);
             } else if constexpr (A_F32) {
-                const float s = (AMODE == kAPlain) ? 1.f : rsc[i];
-                const v4f f0 = raf[i][0] * s, f1 = raf[i][A_F4 - 1] * s;
+                const float s = (AMODE == kAPlain) ? 1.f : rsc[slot][i];
+                const v4f f0 = raf[slot][i][0] * s, f1 = raf[slot][i][A_F4 - 1] * s;
                 w = v4u{pack_bf16x2(f0[0], f0[1]), pack_bf16x2(f0[2], f0[3]),
                         pack_bf16x2(f1[0], f1[1]), pack_bf16x2(f1[2], f1[3])};
             } else {
-                w = ra[i];
+                w = ra[slot][i];
             }
             *reinterpret_cast<v4u*>(&As[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = w;
+        }
+        if constexpr (TRN) {
+            if (tid < 2 * BN) {
+                const int g = tid & 15, c = tid >> 4;
+                #pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    // column j of the 4x8 block: k-pairs (rows 0,1) and (rows 2,3)
+                    const int w = j >> 1, hi = j & 1;
+                    const uint32_t r0 = rb[slot][0][w], r1 = rb[slot][1][w];
+                    const uint32_t r2 = rb[slot][2][w], r3 = rb[slot][3][w];
+                    const uint32_t lo01 = hi ? ((r0 >> 16) | (r1 & 0xffff0000u)) : ((r0 & 0xffffu) | (r1 << 16));
+                    const uint32_t lo23 = hi ? ((r2 >> 16) | (r3 & 0xffff0000u)) : ((r2 & 0xffffu) | (r3 << 16));
+                    *reinterpret_cast<uint2*>(&Bs[buf][8 * c + j][2 * g]) = make_uint2(lo01, lo23);
+                }
+            }
+            return;
         }
         #pragma unroll
         for (int i = 0; i < B_LD; ++i) {
             if (NT) {
-                *reinterpret_cast<v4u*>(&Bs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rb[i];
+                *reinterpret_cast<v4u*>(&Bs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rb[slot][i];
             } else {
                 const int e = i * kThreads + tid;
-                *reinterpret_cast<v4u*>(&Bs[buf][e / (BN / E)][4 * (e % (BN / E))]) = rb[i];
+                *reinterpret_cast<v4u*>(&Bs[buf][e / (BN / E)][4 * (e % (BN / E))]) = rb[slot][i];
             }
         }
     };
@@ -188,51 +227,58 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
     const int nslices = (k_end > k_begin) ? (k_end - k_begin + KS - 1) / KS : 0;
-    if (nslices > 0) {
-        load_slice(k_begin);
-        store_slice(0);
-    }
+    #pragma unroll
+    for (int u = 0; u < PD; ++u)
+        if (u < nslices) load_slice(k_begin + u * KS, u);
+    if (nslices > 0) store_slice(0, 0);
     __syncthreads();
 
     const int l32 = lane & 31;
     const int half = lane >> 5;
-    for (int s = 0; s < nslices; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < nslices) load_slice(k_begin + (s + 1) * KS);
-
+    // slice s sits in LDS buffer s&1 and came from ring slot s%PD; the loop is unrolled by
+    // PD so every slot index is a compile-time constant
+    for (int s0 = 0; s0 < nslices; s0 += PD) {
         #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            v4u fa[TM], fb[TN];
+        for (int u = 0; u < PD; ++u) {
+            const int s = s0 + u;
+            if (s >= nslices) break;
+            const int buf = (PD == 1) ? (s & 1) : (u & 1);
+            if (s + PD < nslices) load_slice(k_begin + (s + PD) * KS, u);
+
             #pragma unroll
-            for (int i = 0; i < TM; ++i)
-                fa[i] = *reinterpret_cast<const v4u*>(&As[buf][wm * WTM + i * 32 + l32][8 * st + 4 * half]);
-            #pragma unroll
-            for (int j = 0; j < TN; ++j) {
-                const int n = wn * WTN + j * 32 + l32;
-                if (NT) {
-                    fb[j] = *reinterpret_cast<const v4u*>(&Bs[buf][n][8 * st + 4 * half]);
-                } else if constexpr (sizeof(TL) == 4) {
-                    #pragma unroll
-                    for (int q = 0; q < 4; ++q) fb[j][q] = Bs[buf][8 * st + 4 * half + q][n];
-                } else {
-                    const uint16_t* b16 = reinterpret_cast<const uint16_t*>(&Bs[buf][0][0]);
-                    const int r0 = 16 * st + 8 * half;
-                    #pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        fb[j][q] = (uint32_t)b16[(r0 + 2 * q) * (2 * BWORDS) + n] |
-                                   ((uint32_t)b16[(r0 + 2 * q + 1) * (2 * BWORDS) + n] << 16);
-                }
-            }
-            #pragma unroll
-            for (int q = 0; q < MM::kSub; ++q)
+            for (int st = 0; st < 4; ++st) {
+                v4u fa[TM], fb[TN];
                 #pragma unroll
                 for (int i = 0; i < TM; ++i)
+                    fa[i] = *reinterpret_cast<const v4u*>(&As[buf][wm * WTM + i * 32 + l32][8 * st + 4 * half]);
+                #pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int n = wn * WTN + j * 32 + l32;
+                    if (NT || TRN) {
+                        fb[j] = *reinterpret_cast<const v4u*>(&Bs[buf][n][8 * st + 4 * half]);
+                    } else if constexpr (sizeof(TL) == 4) {
+                        #pragma unroll
+                        for (int q = 0; q < 4; ++q) fb[j][q] = Bs[buf][8 * st + 4 * half + q][n];
+                    } else {
+                        const uint16_t* b16 = reinterpret_cast<const uint16_t*>(&Bs[buf][0][0]);
+                        const int r0 = 16 * st + 8 * half;
+                        #pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            fb[j][q] = (uint32_t)b16[(r0 + 2 * q) * (2 * BWORDS) + n] |
+                                       ((uint32_t)b16[(r0 + 2 * q + 1) * (2 * BWORDS) + n] << 16);
+                    }
+                }
+                #pragma unroll
+                for (int q = 0; q < MM::kSub; ++q)
                     #pragma unroll
-                    for (int j = 0; j < TN; ++j) acc[i][j] = MM::sub(fa[i], fb[j], q, acc[i][j]);
-        }
+                    for (int i = 0; i < TM; ++i)
+                        #pragma unroll
+                        for (int j = 0; j < TN; ++j) acc[i][j] = MM::sub(fa[i], fb[j], q, acc[i][j]);
+            }
 
-        if (s + 1 < nslices) store_slice(buf ^ 1);
-        __syncthreads();
+            if (s + 1 < nslices) store_slice(buf ^ 1, (u + 1) % PD);
+            __syncthreads();
+        }
     }
 
     // epilogue: each accumulator register holds one row; lanes 0-31 / 32-63 write
@@ -360,7 +406,8 @@ constexpr TileShape kTiles[] = {
 int lds_bytes(int bm, int bn, bool nt, bool bf16) {
     const int a = 2 * bm * kRowWords * 4;
     const int nn_row = bf16 ? bn * 2 + 16 : bn * 4 + 32;
-    const int b = nt ? 2 * bn * kRowWords * 4 : 2 * (bf16 ? 64 : 32) * nn_row;
+    // bf16 N-contiguous B is staged transposed, i.e. in the NT layout
+    const int b = (nt || bf16) ? 2 * bn * kRowWords * 4 : 2 * 32 * nn_row;
     return a + b;
 }
 

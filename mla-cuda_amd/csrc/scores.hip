@@ -29,14 +29,19 @@ struct ScoresArgs {
     const void* qa; const void* qr; const void* ckv; const void* pe;
     float* p; float* m_part; float* l_part;
     int B, Sq, Sk, H, R, D, ld_p, P, tiles_r;
-    float inv_scale;
+    float scale_log2;   // log2(e) / scale
     int causal;
 };
 
-template <typename TL>
+// PD = depth of the register prefetch ring: while slice s feeds the MFMAs from LDS, slices
+// s+1 .. s+PD are in flight from global memory.  fp32 is MFMA-bound with ~4K MFMA cycles
+// per slice and uses PD = 1; bf16 slices hold 8x less MFMA work, so HBM latency is only
+// hidden with several slices in flight (PD = 4).
+template <typename TL, int PD>
 __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
     using MM = Mma<TL>;
     constexpr int E = MM::kElems, KS = MM::kSlice;
+    static_assert(PD == 1 || PD % 2 == 0, "ring depth 1 or even (LDS buffer index is slot parity)");
     __shared__ __attribute__((aligned(16))) uint32_t Qs[2][kBM][kRowWords];
     __shared__ __attribute__((aligned(16))) uint32_t Ks[2][kBN][kRowWords];
 
@@ -56,8 +61,8 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
     const int nsl_r = (a.R + KS - 1) / KS;
     const int nsl = nsl_r + (a.D + KS - 1) / KS;
 
-    v4u rq[4], rk[4];
-    auto load_slice = [&](int s) {
+    v4u rq[PD][4], rk[PD][4];
+    auto load_slice = [&](int s, int slot) {
         const bool rope = s >= nsl_r;
         const int c0 = rope ? (s - nsl_r) * KS : s * KS;
         const int cw = rope ? a.D : a.R;
@@ -69,19 +74,19 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
             const int r = r0 + i * 32 + (tid >> 3);
             v4u v = {0u, 0u, 0u, 0u};
             if (r < rows_b && c < cw) v = load_chunk<TL>(qsrc + (row_base + r) * cw + c, c, cw);
-            rq[i] = v;
+            rq[slot][i] = v;
             const int k = k0 + i * 32 + (tid >> 3);
             v4u w = {0u, 0u, 0u, 0u};
             if (k < a.Sk && c < cw)
                 w = load_chunk<TL>(ksrc + ((int64_t)b * a.Sk + k) * cw + c, c, cw);
-            rk[i] = w;
+            rk[slot][i] = w;
         }
     };
-    auto store_slice = [&](int buf) {
+    auto store_slice = [&](int buf, int slot) {
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            *reinterpret_cast<v4u*>(&Qs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rq[i];
-            *reinterpret_cast<v4u*>(&Ks[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rk[i];
+            *reinterpret_cast<v4u*>(&Qs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rq[slot][i];
+            *reinterpret_cast<v4u*>(&Ks[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rk[slot][i];
         }
     };
 
@@ -91,30 +96,43 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         #pragma unroll
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
 
-    load_slice(0);
-    store_slice(0);
+    #pragma unroll
+    for (int u = 0; u < PD; ++u)
+        if (u < nsl) load_slice(u, u);
+    store_slice(0, 0);
     __syncthreads();
-    for (int s = 0; s < nsl; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < nsl) load_slice(s + 1);
+    // slice s sits in LDS buffer s&1 and came from ring slot s%PD; the loop is unrolled by
+    // PD so every slot index is a compile-time constant
+    for (int s0 = 0; s0 < nsl; s0 += PD) {
         #pragma unroll
-        for (int st = 0; st < 4; ++st) {
-            const v4u fq = *reinterpret_cast<const v4u*>(&Qs[buf][wave * 32 + l32][8 * st + 4 * half]);
-            v4u fk[4];
-            #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                fk[j] = *reinterpret_cast<const v4u*>(&Ks[buf][j * 32 + l32][8 * st + 4 * half]);
-            #pragma unroll
-            for (int q = 0; q < MM::kSub; ++q)
+        for (int u = 0; u < PD; ++u) {
+            const int s = s0 + u;
+            if (s < nsl) {
+                const int buf = (PD == 1) ? (s & 1) : (u & 1);
+                if (s + PD < nsl) load_slice(s + PD, u);
                 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[j] = MM::sub(fq, fk[j], q, acc[j]);
+                for (int st = 0; st < 4; ++st) {
+                    const v4u fq = *reinterpret_cast<const v4u*>(&Qs[buf][wave * 32 + l32][8 * st + 4 * half]);
+                    v4u fk[4];
+                    #pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        fk[j] = *reinterpret_cast<const v4u*>(&Ks[buf][j * 32 + l32][8 * st + 4 * half]);
+                    #pragma unroll
+                    for (int q = 0; q < MM::kSub; ++q)
+                        #pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[j] = MM::sub(fq, fk[j], q, acc[j]);
+                }
+                if (s + 1 < nsl) store_slice(buf ^ 1, (u + 1) % PD);
+                __syncthreads();
+            }
         }
-        if (s + 1 < nsl) store_slice(buf ^ 1);
-        __syncthreads();
     }
 
     // ---- epilogue: per accumulator register e the lane holds row acc_row(e, lane) and
-    // keys k0 + 32*j + l32 (j = 0..3).
+    // keys k0 + 32*j + l32 (j = 0..3).  Work in the log2 domain: t2 = s * (log2(e)/scale),
+    // p = 2^(t2 - max t2) is one v_exp_f32, and m = max t2 * ln(2) is stored in the natural
+    // units of s/scale.  (The exponent's rounding differs from exp(s/scale - m) by ~1e-7
+    // relative to |s/scale|, i.e. ~1e-6 relative in p.)
     #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int r = r0 + wave * 32 + acc_row(e, lane);   // row within the batch
@@ -126,7 +144,7 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int k = k0 + 32 * j + l32;
-            tv[j] = acc[j][e] * a.inv_scale;
+            tv[j] = acc[j][e] * a.scale_log2;
             if (k <= kmax && k < a.Sk) mx = fmaxf(mx, tv[j]);
         }
         mx = half_wave_reduce(mx, OpMax());
@@ -136,13 +154,13 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         for (int j = 0; j < 4; ++j) {
             const int k = k0 + 32 * j + l32;
             const bool vis = (k <= kmax) && (k < a.Sk);
-            const float pv = vis ? expf(tv[j] - mx) : 0.f;
+            const float pv = vis ? __builtin_amdgcn_exp2f(tv[j] - mx) : 0.f;
             sum += pv;
             if (row_ok && k < a.ld_p) prow[k] = pv;
         }
         sum = half_wave_reduce(sum, OpSum());
         if (row_ok && l32 == 0) {
-            a.m_part[(row_base + r) * a.P + kt] = mx;
+            a.m_part[(row_base + r) * a.P + kt] = mx * 0.69314718055994531f;  // ln 2
             a.l_part[(row_base + r) * a.P + kt] = sum;
         }
     }
@@ -157,14 +175,14 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     a.B = p.B; a.Sq = p.Sq; a.Sk = p.Sk; a.H = p.H; a.R = p.R; a.D = p.D;
     a.ld_p = p.ld_p; a.P = p.P;
     a.tiles_r = (p.Sq * p.H + kBM - 1) / kBM;
-    a.inv_scale = p.inv_scale;
+    a.scale_log2 = p.inv_scale * 1.4426950408889634f;
     a.causal = p.causal ? 1 : 0;
     const int64_t nblocks = (int64_t)p.B * a.tiles_r * a.P;
     if (nblocks <= 0 || nblocks > 0x7fffffff) return hipErrorInvalidValue;
     if (p.bf16)
-        hipLaunchKernelGGL(scores_kernel<bf16_t>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((scores_kernel<bf16_t, 4>), dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
     else
-        hipLaunchKernelGGL(scores_kernel<float>, dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
+        hipLaunchKernelGGL((scores_kernel<float, 1>), dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
     return hipGetLastError();
 }
 
