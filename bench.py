@@ -5,7 +5,7 @@
 
 One "step" is one MLA layer, steps 2a1 -> 3d, through the drop-in surface
 (mla_custom_cuda.q_absorbed + mla_custom_cuda.mla_attention), on inputs already resident
-in HBM.  The default workload is BASELINE configs[1]: B=128, Sq=1, Sk=4989, fp32,
+in HBM.  The default workload is the headline decode shape: B=128, Sq=1, Sk=4989, fp32,
 DeepSeek-V3 dims.  Output: ONE JSON line on stdout.
 
 Timed region: W untimed warm-up layers, then exactly K layers bracketed by
@@ -44,12 +44,12 @@ REF_A6000_US = 16920.0     # reference's published layer time at this shape (REA
 
 CONFIGS = {
     # name: (B, Sq, Sk, description)
-    "cfg2": (128, 1, 4989, "B=128 Sq=1 Sk=4989 fp32 decode (BASELINE configs[1])"),
-    "cfg4": (128, 1, 4989, "B=128 Sq=1 Sk=4989 bf16 decode (BASELINE configs[3])"),
-    "cfg1": (1, 1, 512, "B=1 Sq=1 Sk=512 fp32 decode (BASELINE configs[0])"),
-    "b1": (1, 1, 4989, "B=1 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
-    "b8": (8, 1, 4989, "B=8 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
-    "b32": (32, 1, 4989, "B=32 Sq=1 Sk=4989 fp32 decode (BASELINE configs[2])"),
+    "cfg2": (128, 1, 4989, "B=128 Sq=1 Sk=4989 fp32 decode (headline workload)"),
+    "cfg4": (128, 1, 4989, "B=128 Sq=1 Sk=4989 bf16 decode (bf16 storage, fp32 accumulation)"),
+    "cfg1": (1, 1, 512, "B=1 Sq=1 Sk=512 fp32 decode (single short sequence)"),
+    "b1": (1, 1, 4989, "B=1 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
+    "b8": (8, 1, 4989, "B=8 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
+    "b32": (32, 1, 4989, "B=32 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
 }
 
 
@@ -137,7 +137,7 @@ def main():
                     help="only run a plain device copy of BYTES, 3 times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
-                    help="HBM traffic per launch measured by rocprofv3 --pmc (see DESIGN.md)")
+                    help="JSON of HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a 1 GiB copy calibration")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))

@@ -112,6 +112,21 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims,
                   const void* pe_cache, const void* W_uv, double scale, int causal,
                   void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* Attention over a long key range without materialising the [B*Sq*H, Sk] score matrix:
+ * keys are processed in chunks of `key_chunk` (a multiple of mla_score_tile(); 0 = choose
+ * so the per-chunk score buffer stays <= 1 GiB).  Each chunk runs 3a -> 3b -> 3c into a
+ * bounded buffer and is merged into running (max, sum, unnormalised ctx) state with the
+ * online-softmax rescale; 3d runs once at the end.  Same arguments and result as
+ * mla_attention (not in the reference, which always materialises the scores,
+ * mla_kernels.cu:1526-1529; at B=4, Sq=128, Sk=32768 that matrix alone is 8.6 GB). */
+size_t mla_attention_streaming_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                               int causal, int32_t key_chunk);
+int mla_attention_streaming(mla_dtype_t dtype, const mla_dims_t* dims,
+                            const void* q_absorbed, const void* q_rope, const void* c_kv,
+                            const void* pe_cache, const void* W_uv, double scale, int causal,
+                            int32_t key_chunk, void* out, void* workspace,
+                            size_t workspace_bytes, hipStream_t stream);
+
 /* ======================================================================================
  * Per-step entry points (no reference counterpart: the reference fuses them behind the
  * two calls above).  dims fields a step does not use are ignored.

@@ -202,6 +202,43 @@ torch::Tensor op_mla_attention(torch::Tensor q_absorbed, torch::Tensor q_rope, t
     return out;
 }
 
+// Same contract as mla_attention, with keys processed in bounded chunks (the score matrix
+// is never materialised whole); key_chunk = 0 picks the chunk so one chunk's fp32 score
+// buffer stays within 1 GiB.
+torch::Tensor op_mla_attention_streaming(torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                         torch::Tensor c_kv, torch::Tensor pe_cache,
+                                         torch::Tensor W_uv, double scale, bool causal,
+                                         int64_t key_chunk) {
+    mla_dims_t d = attn_dims(q_absorbed, q_rope, c_kv, pe_cache, &W_uv);
+    const mla_dtype_t dt = to_mla_dtype(q_absorbed, "q_absorbed");
+    check_same_dtype(q_absorbed, q_rope, "q_rope");
+    check_same_dtype(q_absorbed, c_kv, "c_kv");
+    check_same_dtype(q_absorbed, pe_cache, "pe_cache");
+    check_same_dtype(q_absorbed, W_uv, "W_uv");
+    TORCH_CHECK(d.sk > 0, "MLA: c_kv must hold at least one key");
+    TORCH_CHECK(!causal || d.sk >= d.sq, "MLA: causal attention needs Sk >= Sq");
+    TORCH_CHECK(key_chunk >= 0 && key_chunk % mla_score_tile() == 0,
+                "MLA: key_chunk must be 0 or a positive multiple of ", mla_score_tile());
+    check_device({&q_absorbed, &q_rope, &c_kv, &pe_cache, &W_uv});
+
+    c10::DeviceGuard guard(q_absorbed.device());
+    auto qa = q_absorbed.contiguous();
+    auto qr = q_rope.contiguous();
+    auto ck = c_kv.contiguous();
+    auto pe = pe_cache.contiguous();
+    auto wuv = W_uv.contiguous();
+    auto out = torch::empty({d.batch, d.sq, d.heads, d.v}, qa.options());
+    const size_t wsb = mla_attention_streaming_workspace_bytes(dt, &d, causal ? 1 : 0,
+                                                               (int32_t)key_chunk);
+    auto ws = workspace(wsb, qa);
+    check_status(mla_attention_streaming(dt, &d, qa.data_ptr(), qr.data_ptr(), ck.data_ptr(),
+                                         pe.data_ptr(), wuv.data_ptr(), scale, causal ? 1 : 0,
+                                         (int32_t)key_chunk, out.data_ptr(), ws.data_ptr(), wsb,
+                                         current_stream()),
+                 "mla_attention_streaming");
+    return out;
+}
+
 // ------------------------------------------------------------------ per-step ops
 
 void check_contig(const torch::Tensor& t, const char* name) {
@@ -400,6 +437,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Absorbed attention 3a -> 3b -> 3c -> 3d: returns out [B, Sq, H, v]",
           py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),
           py::arg("W_uv"), py::arg("scale"), py::arg("causal") = false);
+    m.def("mla_attention_streaming", &op_mla_attention_streaming,
+          "Attention with keys in bounded chunks (online-softmax merge): returns out [B, Sq, H, v]",
+          py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),
+          py::arg("W_uv"), py::arg("scale"), py::arg("causal") = false, py::arg("key_chunk") = 0);
     m.def("rope_inv_freq", &rope_inv_freq, "float32 RoPE inverse-frequency table", py::arg("rope"));
     m.def("gemm", &step_gemm, "2a1/2a2: float32 C = A @ W", py::arg("A"), py::arg("W"));
     m.def("rmsnorm", &step_rmsnorm, "2a-n", py::arg("input"), py::arg("gain"), py::arg("eps"));

@@ -29,7 +29,8 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-shared",
     "-fvisibility=hidden",
-    # packed fp32 VALU ops are disabled in all device code
+    # packed fp32 VALU ops (v_pk_*_f32) are disabled in all device code: some of their
+    # forms have given silently wrong results on this platform
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",

@@ -6,6 +6,7 @@
 // grids are planned from the shapes alone (plan_gemm / fixed 3a tiles), so the
 // *_workspace_bytes() queries and the launches always agree.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -303,6 +304,58 @@ AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     return L;
 }
 
+struct StreamLayout {
+    int chunk;  // keys per chunk
+    GemmPlan out;
+    size_t off_p, off_m, off_l, off_alpha, off_sum_c, off_max_c, off_ctx_c, off_ctx, off_run_max,
+        off_run_sum, off_ctx_ws, off_out_ws, total;
+};
+
+// Chunk choice for streaming attention: the largest multiple of the score tile whose fp32
+// score buffer stays within 1 GiB (at least one tile; at most the whole key range).
+int stream_chunk(const mla_dims_t* d, int32_t key_chunk) {
+    const int64_t rows = (int64_t)d->batch * d->sq * d->heads;
+    const int full = cdiv(d->sk, kScoreTile) * kScoreTile;
+    int c = key_chunk;
+    if (c == 0) {
+        const int64_t fit = ((int64_t)1 << 30) / (rows * 4) / kScoreTile * kScoreTile;
+        c = (int)std::max<int64_t>(kScoreTile, std::min<int64_t>(fit, full));
+    }
+    return std::min(c, full);
+}
+
+StreamLayout stream_layout(mla_dtype_t dt, const mla_dims_t* d, int32_t key_chunk) {
+    StreamLayout L;
+    const size_t rows = (size_t)d->batch * d->sq * d->heads;
+    L.chunk = stream_chunk(d, key_chunk);
+    const int P = cdiv(L.chunk, kScoreTile);
+    // the 3c plan depends on the chunk length: take the larger workspace of a full chunk
+    // and of the (possibly shorter) last one
+    size_t ctx_ws = 0;
+    for (int kc : {L.chunk, d->sk - (cdiv(d->sk, L.chunk) - 1) * L.chunk}) {
+        mla_dims_t dc = *d;
+        dc.sk = kc;
+        GemmProblem cp = ctx_problem(dt, &dc, nullptr, mla_score_ld(kc), nullptr, nullptr, nullptr);
+        ctx_ws = std::max(ctx_ws, plan_gemm(cp).workspace_bytes);
+    }
+    L.out = plan_gemm(out_problem(dt, d, nullptr, nullptr, nullptr, nullptr));
+    size_t o = 0;
+    L.off_p = o;       o = align_up(o + rows * mla_score_ld(L.chunk) * sizeof(float));
+    L.off_m = o;       o = align_up(o + rows * P * sizeof(float));
+    L.off_l = o;       o = align_up(o + rows * P * sizeof(float));
+    L.off_alpha = o;   o = align_up(o + rows * P * sizeof(float));
+    L.off_sum_c = o;   o = align_up(o + rows * sizeof(float));
+    L.off_max_c = o;   o = align_up(o + rows * sizeof(float));
+    L.off_ctx_c = o;   o = align_up(o + rows * d->kv_rank * sizeof(float));
+    L.off_ctx = o;     o = align_up(o + rows * d->kv_rank * sizeof(float));
+    L.off_run_max = o; o = align_up(o + rows * sizeof(float));
+    L.off_run_sum = o; o = align_up(o + rows * sizeof(float));
+    L.off_ctx_ws = o;  o = align_up(o + ctx_ws);
+    L.off_out_ws = o;  o = align_up(o + L.out.workspace_bytes);
+    L.total = o;
+    return L;
+}
+
 template <typename T> T* at(void* base, size_t off) {
     return reinterpret_cast<T*>(static_cast<char*>(base) + off);
 }
@@ -311,7 +364,8 @@ template <typename T> T* at(void* base, size_t off) {
 
 int run_scores(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* qr, const void* ckv,
                const void* pe, double scale, int causal, float* p, int ld_p, float* m_part,
-               float* l_part, hipStream_t stream) {
+               float* l_part, hipStream_t stream, int64_t key_stride = 0, int key_offset = 0,
+               int sk_total = 0) {
     ScoresProblem sp;
     sp.qa = qa; sp.qr = qr; sp.ckv = ckv; sp.pe = pe;
     sp.bf16 = is_bf16(dt);
@@ -320,6 +374,7 @@ int run_scores(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* 
     sp.R = d->kv_rank; sp.D = d->rope; sp.ld_p = ld_p; sp.P = cdiv(d->sk, kScoreTile);
     sp.inv_scale = 1.0f / (float)scale;
     sp.causal = causal != 0;
+    sp.key_stride = key_stride; sp.key_offset = key_offset; sp.sk_total = sk_total;
     MLA_TRY_HIP(launch_scores(sp, stream), "scores kernel launch");
     return MLA_OK;
 }
@@ -448,7 +503,7 @@ int mla_combine(const float* m_part, const float* l_part, float* alpha, float* r
     MLA_CHECK(check_ptr(l_part, "l_part"));
     MLA_CHECK(check_ptr(alpha, "alpha"));
     MLA_CHECK(check_ptr(row_sum, "row_sum"));
-    MLA_TRY_HIP(launch_combine(m_part, l_part, alpha, row_sum, rows, n_partials, stream),
+    MLA_TRY_HIP(launch_combine(m_part, l_part, alpha, row_sum, nullptr, rows, n_partials, stream),
                 "combine launch");
     return ok();
 }
@@ -593,13 +648,83 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     MLA_CHECK(run_scores(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, p, L.ld_p, m,
                          l, stream));
     // 3b
-    MLA_TRY_HIP(launch_combine(m, l, alpha, row_sum, rows, L.P, stream), "3b launch");
+    MLA_TRY_HIP(launch_combine(m, l, alpha, row_sum, nullptr, rows, L.P, stream), "3b launch");
     // 3c
     GemmProblem cp = ctx_problem(dtype, dims, p, L.ld_p, alpha, c_kv, ctx);
     MLA_TRY_HIP(launch_gemm(cp, L.ctx, at<void>(workspace, L.off_ctx_ws), stream), "3c launch");
     // 3d
     GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
+    return ok();
+}
+
+size_t mla_attention_streaming_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                               int causal, int32_t key_chunk) {
+    if (!dims || check_attn_dims(dtype, dims, causal) != MLA_OK) return 0;
+    if (key_chunk < 0 || key_chunk % kScoreTile != 0) return 0;
+    return stream_layout(dtype, dims, key_chunk).total;
+}
+
+int mla_attention_streaming(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                            const void* q_rope, const void* c_kv, const void* pe_cache,
+                            const void* W_uv, double scale, int causal, int32_t key_chunk,
+                            void* out, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    MLA_CHECK(check_scale(scale));
+    if (key_chunk < 0 || key_chunk % kScoreTile != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "key_chunk must be 0 or a positive multiple of %d",
+                    kScoreTile);
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const StreamLayout L = stream_layout(dtype, dims, key_chunk);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+
+    const int rows = dims->batch * dims->sq * dims->heads;
+    const size_t esz = is_bf16(dtype) ? 2 : 4;
+    float* p = at<float>(workspace, L.off_p);
+    float* m = at<float>(workspace, L.off_m);
+    float* l = at<float>(workspace, L.off_l);
+    float* alpha = at<float>(workspace, L.off_alpha);
+    float* sum_c = at<float>(workspace, L.off_sum_c);
+    float* max_c = at<float>(workspace, L.off_max_c);
+    float* ctx_c = at<float>(workspace, L.off_ctx_c);
+    float* ctx = at<float>(workspace, L.off_ctx);
+    float* run_max = at<float>(workspace, L.off_run_max);
+    float* run_sum = at<float>(workspace, L.off_run_sum);
+
+    for (int c0 = 0, chunk = 0; c0 < dims->sk; c0 += L.chunk, ++chunk) {
+        mla_dims_t dc = *dims;
+        dc.sk = std::min(L.chunk, dims->sk - c0);
+        const int ld_p = mla_score_ld(dc.sk);
+        const int P = cdiv(dc.sk, kScoreTile);
+        const char* ck = static_cast<const char*>(c_kv) + (size_t)c0 * dims->kv_rank * esz;
+        const char* pe = static_cast<const char*>(pe_cache) + (size_t)c0 * dims->rope * esz;
+        // 3a on the chunk (keys c0 .. c0+sk-1 of every sequence; causal rule on absolute keys)
+        MLA_CHECK(run_scores(dtype, &dc, q_absorbed, q_rope, ck, pe, scale, causal, p, ld_p, m, l,
+                             stream, dims->sk, c0, dims->sk));
+        // 3b: per-chunk maximum and sum relative to it
+        MLA_TRY_HIP(launch_combine(m, l, alpha, sum_c, max_c, rows, P, stream), "stream 3b launch");
+        // 3c on the chunk
+        GemmProblem cp = ctx_problem(dtype, &dc, p, ld_p, alpha, ck, ctx_c);
+        cp.sBg = (int64_t)dims->sk * dims->kv_rank;  // batch stride of the whole cache
+        const GemmPlan plan = plan_gemm(cp);
+        MLA_TRY_HIP(launch_gemm(cp, plan, at<void>(workspace, L.off_ctx_ws), stream),
+                    "stream 3c launch");
+        // online-softmax merge into the running state
+        MLA_TRY_HIP(launch_stream_merge(ctx, run_max, run_sum, ctx_c, max_c, sum_c, rows,
+                                        dims->kv_rank, chunk == 0, stream),
+                    "stream merge launch");
+    }
+    // 3d on the merged state
+    GemmProblem op = out_problem(dtype, dims, ctx, run_sum, W_uv, out);
+    MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
+                "stream 3d launch");
     return ok();
 }
 

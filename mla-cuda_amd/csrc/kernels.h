@@ -57,9 +57,15 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride,
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope,
                        int rope, hipStream_t stream);
-// 3b
+// 3b (row_max may be null; when given it receives M = max_j m_part[row, j])
 hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
-                          float* row_sum, int rows, int P, hipStream_t stream);
+                          float* row_sum, float* row_max, int rows, int P, hipStream_t stream);
+// Streaming merge of one key chunk into the running softmax state (online softmax):
+//   M' = max(M, Mc); a = exp(M - M'), b = exp(Mc - M');
+//   ctx = ctx*a + ctx_c*b;  L = L*a + Lc*b;  M = M'      (first chunk: plain copy)
+hipError_t launch_stream_merge(float* ctx, float* run_max, float* run_sum, const float* ctx_c,
+                               const float* max_c, const float* sum_c, int rows, int R,
+                               bool first, hipStream_t stream);
 
 // ---------------------------------------------------------------- 3a scores
 struct ScoresProblem {
@@ -72,6 +78,9 @@ struct ScoresProblem {
     float* m_part = nullptr;     // [B*Sq*H, P]
     float* l_part = nullptr;
     int B = 0, Sq = 0, Sk = 0, H = 0, R = 0, D = 0, ld_p = 0, P = 0;
+    int64_t key_stride = 0;      // rows between batches of ckv / pe (>= Sk; Sk_total when chunked)
+    int key_offset = 0;          // absolute index of key 0 (causal rule uses absolute keys)
+    int sk_total = 0;            // keys in the whole sequence (causal rule)
     float inv_scale = 1.f;
     bool causal = false;
 };

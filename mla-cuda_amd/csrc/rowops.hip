@@ -137,7 +137,8 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
 __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ m_part,
                                                       const float* __restrict__ l_part,
                                                       float* __restrict__ alpha,
-                                                      float* __restrict__ row_sum, int rows,
+                                                      float* __restrict__ row_sum,
+                                                      float* __restrict__ row_max, int rows,
                                                       int P) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -156,7 +157,39 @@ __global__ void __launch_bounds__(256) combine_kernel(const float* __restrict__ 
         l += lr[j] * aj;
     }
     l = wave_reduce(l, OpSum());
-    if (lane == 0) row_sum[row] = l;
+    if (lane == 0) {
+        row_sum[row] = l;
+        if (row_max) row_max[row] = M;
+    }
+}
+
+// ---- streaming merge: one wave per row; lanes walk the row's R ctx values as float4.
+// Exact when both maxima are equal; a fully masked state (M = -inf, L = 0) contributes 0.
+__global__ void __launch_bounds__(256) stream_merge_kernel(float* __restrict__ ctx,
+                                                           float* __restrict__ run_max,
+                                                           float* __restrict__ run_sum,
+                                                           const float* __restrict__ ctx_c,
+                                                           const float* __restrict__ max_c,
+                                                           const float* __restrict__ sum_c,
+                                                           int rows, int R, int first) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const float mc = max_c[row];
+    float a = 0.f, b = 1.f, mn = mc;
+    if (!first) {
+        const float mo = run_max[row];
+        mn = fmaxf(mo, mc);
+        a = (mo == mn) ? 1.f : expf(mo - mn);
+        b = (mc == mn) ? 1.f : expf(mc - mn);
+    }
+    v4f* dst = reinterpret_cast<v4f*>(ctx + (int64_t)row * R);
+    const v4f* src = reinterpret_cast<const v4f*>(ctx_c + (int64_t)row * R);
+    for (int c = lane; c < R / 4; c += 64) dst[c] = first ? src[c] : dst[c] * a + src[c] * b;
+    if (lane == 0) {
+        run_sum[row] = first ? sum_c[row] : run_sum[row] * a + sum_c[row] * b;
+        run_max[row] = mn;
+    }
 }
 
 }  // namespace
@@ -190,10 +223,19 @@ hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float
 }
 
 hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
-                          float* row_sum, int rows, int P, hipStream_t stream) {
+                          float* row_sum, float* row_max, int rows, int P, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(combine_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, m_part,
-                       l_part, alpha, row_sum, rows, P);
+                       l_part, alpha, row_sum, row_max, rows, P);
+    return hipGetLastError();
+}
+
+hipError_t launch_stream_merge(float* ctx, float* run_max, float* run_sum, const float* ctx_c,
+                               const float* max_c, const float* sum_c, int rows, int R,
+                               bool first, hipStream_t stream) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(stream_merge_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, ctx,
+                       run_max, run_sum, ctx_c, max_c, sum_c, rows, R, first ? 1 : 0);
     return hipGetLastError();
 }
 

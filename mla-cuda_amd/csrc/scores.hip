@@ -29,6 +29,8 @@ struct ScoresArgs {
     const void* qa; const void* qr; const void* ckv; const void* pe;
     float* p; float* m_part; float* l_part;
     int B, Sq, Sk, H, R, D, ld_p, P, tiles_r;
+    int64_t key_stride;   // key rows between batches
+    int causal_base;      // sk_total - Sq - key_offset: query s sees local keys <= base + s
     float scale_log2;   // log2(e) / scale
     int causal;
 };
@@ -78,7 +80,7 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
             const int k = k0 + i * 32 + (tid >> 3);
             v4u w = {0u, 0u, 0u, 0u};
             if (k < a.Sk && c < cw)
-                w = load_chunk<TL>(ksrc + ((int64_t)b * a.Sk + k) * cw + c, c, cw);
+                w = load_chunk<TL>(ksrc + ((int64_t)b * a.key_stride + k) * cw + c, c, cw);
             rk[slot][i] = w;
         }
     };
@@ -137,8 +139,8 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
     for (int e = 0; e < 16; ++e) {
         const int r = r0 + wave * 32 + acc_row(e, lane);   // row within the batch
         const bool row_ok = r < rows_b;
-        // causal: query index s = r / H sees keys <= Sk - Sq + s
-        const int kmax = a.causal ? (a.Sk - a.Sq + (row_ok ? r / a.H : 0)) : (a.Sk - 1);
+        // causal: query index s = r / H sees absolute keys <= Sk_total - Sq + s
+        const int kmax = a.causal ? (a.causal_base + (row_ok ? r / a.H : 0)) : (a.Sk - 1);
         float tv[4];
         float mx = -INFINITY;
         #pragma unroll
@@ -175,6 +177,8 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     a.B = p.B; a.Sq = p.Sq; a.Sk = p.Sk; a.H = p.H; a.R = p.R; a.D = p.D;
     a.ld_p = p.ld_p; a.P = p.P;
     a.tiles_r = (p.Sq * p.H + kBM - 1) / kBM;
+    a.key_stride = p.key_stride ? p.key_stride : p.Sk;
+    a.causal_base = (p.sk_total ? p.sk_total : p.Sk) - p.Sq - p.key_offset;
     a.scale_log2 = p.inv_scale * 1.4426950408889634f;
     a.causal = p.causal ? 1 : 0;
     const int64_t nblocks = (int64_t)p.B * a.tiles_r * a.P;

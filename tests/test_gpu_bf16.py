@@ -1,11 +1,11 @@
-"""GPU parity of the bf16 path (BASELINE configs[3]: bf16 storage, fp32 accumulation on
+"""GPU parity of the bf16 path (bf16 storage, fp32 accumulation on
 bf16 MFMA).
 
 Per step, the oracle runs in fp32 on the very bf16 values the kernel reads (and, where the
 kernel rounds an fp32 operand to bf16 before its MFMA -- q_raw in 2c, p*alpha in 3c, ctx in
 3d -- on the rounded operand), so each step is held to fp32-accumulation accuracy.  The
-whole layer is compared with the fp32 oracle on the bf16-rounded inputs at BASELINE's
-bf16 tolerance, rtol 2e-2 (atol 2e-2 on O(1) outputs).
+whole layer is compared with the fp32 oracle on the bf16-rounded inputs at the bf16
+tolerance rtol 2e-2 (atol 2e-2 on O(1) outputs).
 """
 
 from __future__ import annotations
@@ -128,7 +128,7 @@ def test_layer_bf16_vs_fp32_oracle(ext, B, Sq, Sk):
 
 
 def test_layer_bf16_cfg4_full_size(ext):
-    """B=128, Sq=1, Sk=4989 in bf16; oracle on three sequences."""
+    """bf16 decode at B=128, Sq=1, Sk=4989; oracle on three sequences."""
     inp = R.make_inputs(128, 1, 4989, seed=0, dtype=BF)
     qa, qr, out = run_layer(ext, inp)
     pick = [0, 64, 127]

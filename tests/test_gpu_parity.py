@@ -8,7 +8,7 @@ copied to the GPU, so HIP path and oracle see identical values.  Tolerances:
   fp32-vs-fp64 noise of the same op (check_3d.py:40-44);
 * per-step fp32 intermediates: rtol/atol 1e-4 on O(1) quantities, 1e-5 on softmax factors.
 
-At BASELINE's full sizes the oracle runs on a subset of sequences (each sequence's
+At the full decode sizes the oracle runs on a subset of sequences (each sequence's
 attention is independent), which keeps every test to seconds on the box's CPU.
 """
 
@@ -228,7 +228,7 @@ def test_layer_cfg3_small_batch(ext, B):
 
 
 def test_layer_cfg2_full_size(ext):
-    """B=128, Sq=1, Sk=4989, fp32, full DeepSeek-V3 dims."""
+    """Headline decode shape: B=128, Sq=1, Sk=4989, fp32, full DeepSeek-V3 dims."""
     inp = R.make_inputs(128, 1, 4989, seed=0)
     qa, qr, out = run_layer(ext, inp)
     assert torch.isfinite(out).all()
