@@ -50,6 +50,7 @@ CONFIGS = {
     "b1": (1, 1, 4989, "B=1 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
     "b8": (8, 1, 4989, "B=8 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
     "b32": (32, 1, 4989, "B=32 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
+    "cfg5": (4, 128, 32768, "B=4 Sq=128 Sk=32768 fp32 causal chunked prefill (streaming attention)"),
 }
 
 
@@ -83,7 +84,7 @@ def build_inputs(B, Sq, Sk, seed=0, dtype=None):
     return mla_inputs.make_inputs(B, Sq, Sk, seed=seed, dtype=dtype or torch.float32)
 
 
-def cpu_baseline(inp, gpu_out, budget_s=30.0):
+def cpu_baseline(inp, gpu_out, budget_s=30.0, causal=False):
     """Time the CPU oracle on the host cores: 1 warm-up, then the median of up to 3 runs,
     on the full workload if one layer fits the budget, else on the first sequences of the
     batch (scaled to the full batch; every sequence costs the same)."""
@@ -99,7 +100,7 @@ def cpu_baseline(inp, gpu_out, budget_s=30.0):
     def layer(b):
         return R.mla_layer(inp["x"][:b], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
                            inp["wkv_b"], inp["c_kv"][:b], inp["pe_cache"][:b],
-                           inp["positions"])
+                           inp["positions"], causal=causal)
 
     # probe with a small sample to size the run
     bs = min(B, 8)
@@ -179,9 +180,14 @@ def main():
     scale = math.sqrt(dims.qk_head)
     eps = 1e-6
 
+    causal = args.config == "cfg5"
+
     def layer():
         qa, qr = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
                                 g["positions"], dims.nope, dims.rope, eps)
+        if causal:
+            return ext.mla_attention_streaming(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale,
+                                               True)
         return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale)
 
     # ---- timed region: the fused boundary calls
@@ -213,7 +219,7 @@ def main():
         qr = ext.rope(raw, g["positions"], B, Sq, dims.n_heads, dims.nope, dims.rope,
                       dt); ev[4].record()
         qa = ext.absorb(raw, W_uk_d, B, Sq, dims.rope); ev[5].record()
-        p, m, l = ext.scores(qa, qr, g["c_kv"], g["pe_cache"], scale); ev[6].record()
+        p, m, l = ext.scores(qa, qr, g["c_kv"], g["pe_cache"], scale, causal); ev[6].record()
         alpha, rs = ext.combine(m, l); ev[7].record()
         ctx = ext.ctx(p, alpha, g["c_kv"], Sq, dims.n_heads); ev[8].record()
         o = ext.out(ctx, rs, W_uv_d); ev[9].record()
@@ -294,7 +300,7 @@ def main():
 
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU oracle ...", file=sys.stderr, flush=True)
-        cb, err, _ = cpu_baseline(inp, out.cpu())
+        cb, err, _ = cpu_baseline(inp, out.cpu(), causal=causal)
         rec["cpu_baseline"] = cb
         rec["parity_max_abs_vs_cpu_oracle"] = err
         rec["gpu_speedup_vs_cpu"] = round(cb["value"] / value_us, 1)

@@ -39,7 +39,8 @@ def lib():
     L.mla_last_error.restype = ctypes.c_char_p
     L.mla_version.restype = ctypes.c_char_p
     for n in ("mla_q_absorbed_workspace_bytes", "mla_attention_workspace_bytes",
-              "mla_gemm_workspace_bytes", "mla_ctx_workspace_bytes", "mla_out_workspace_bytes"):
+              "mla_gemm_workspace_bytes", "mla_ctx_workspace_bytes", "mla_out_workspace_bytes",
+              "mla_attention_streaming_workspace_bytes"):
         getattr(L, n).restype = ctypes.c_size_t
     return L
 
@@ -163,6 +164,23 @@ def test_bf16_needs_8_element_rows(lib):
                            P16, ctypes.c_size_t(1 << 30), None)
     assert st == MLA_ERR_INVALID_ARGUMENT and "multiple of 8 for bf16" in _err(lib)
     assert lib.mla_attention_workspace_bytes(BF16, ctypes.byref(dsv3(2, 1, 100)), 0) > 0
+
+
+def test_streaming_validation_and_bounded_workspace(lib):
+    d = dsv3(4, 128, 32768)
+    full = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 1)
+    stream = lib.mla_attention_streaming_workspace_bytes(F32, ctypes.byref(d), 1, 0)
+    assert full > 8.5e9            # the materialised [65536 x 32768] fp32 scores
+    assert 0 < stream < 1.6e9      # one <= 1 GiB chunk of scores plus the running state
+    small = lib.mla_attention_streaming_workspace_bytes(F32, ctypes.byref(d), 1, 128)
+    assert 0 < small < stream
+    assert lib.mla_attention_streaming_workspace_bytes(F32, ctypes.byref(d), 1, 100) == 0
+    st = lib.mla_attention_streaming(F32, ctypes.byref(d), *([P16] * 5), ctypes.c_double(13.85),
+                                     1, 100, P16, P16, ctypes.c_size_t(1 << 31), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "key_chunk" in _err(lib)
+    st = lib.mla_attention_streaming(F32, ctypes.byref(d), *([P16] * 5), ctypes.c_double(13.85),
+                                     1, 0, P16, P16, ctypes.c_size_t(stream - 1), None)
+    assert st == MLA_ERR_WORKSPACE
 
 
 def test_scores_validation(lib):
