@@ -80,6 +80,10 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     constexpr int BWORDS = (NT || TRN) ? kRowWords : nn_row_words<TL, BN>();
     constexpr bool A_F32 = std::is_same<TA, float>::value;
     constexpr int A_F4 = A_F32 ? E / 4 : 1;  // float4 loads per A chunk
+    // instruction counts of one slice, for its issue schedule
+    constexpr int kStepReads = TM + TN * ((NT || TRN) ? 1 : 2);   // fp32 NN B: 2 ds_read2_b32
+    constexpr int kSliceLoads = A_LD * A_F4 + (TRN ? 4 : B_LD) + (AMODE == kAAlpha ? A_LD : 0);
+    constexpr int kSliceWrites = A_LD + (TRN ? 8 : B_LD);
     static_assert(A_F32 || AMODE == kAPlain, "scaled A operands are fp32");
 
     __shared__ __attribute__((aligned(16))) uint32_t As[2][BM][kRowWords];
@@ -114,64 +118,81 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
         }
     }
 
+    // Staging geometry, fixed for the whole tile.  Byte offsets are relative to the current
+    // slice's origin in each operand (the scalar base walks K); rows or columns outside the
+    // problem get kOob.  K-contiguous tiles (A, NT B): thread tid loads chunk tid%8 of rows
+    // i*32 + tid/8.  N-contiguous B: chunk e%(BN/E) of K row e/(BN/E), e = i*256 + tid;
+    // transposed bf16 B: rows 4*(tid%16) + i, columns 8*(tid/16).
+    const int kc = E * (tid & 7);                  // chunk column within the slice
+    uint32_t oa[A_LD], oal[A_LD];
+    #pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+        const int r = i * 32 + (tid >> 3);
+        const bool ok = m0 + r < a.M;
+        oa[i] = ok ? (uint32_t)(((int64_t)r * a.lda + kc) * sizeof(TA)) : kOob;
+        oal[i] = ok ? (uint32_t)((int64_t)r * a.alpha_ld * 4) : kOob;
+    }
+    constexpr int NB_LD = TRN ? 4 : B_LD;
+    uint32_t ob[NB_LD];
+    int bk[NB_LD];                                 // K row of a N-contiguous B chunk
+    #pragma unroll
+    for (int i = 0; i < NB_LD; ++i) {
+        if constexpr (TRN) {
+            const int gq = tid & 15, c = tid >> 4;
+            bk[i] = 4 * gq + i;
+            ob[i] = (tid < 2 * BN && n0 + 8 * c < a.N)
+                        ? (uint32_t)(((int64_t)bk[i] * a.ldb + 8 * c) * sizeof(TL)) : kOob;
+        } else if constexpr (NT) {
+            const int r = i * 32 + (tid >> 3);
+            bk[i] = 0;
+            ob[i] = (n0 + r < a.N) ? (uint32_t)(((int64_t)r * a.ldb + kc) * sizeof(TL)) : kOob;
+        } else {
+            const int e = i * kThreads + tid;
+            const int nc = E * (e % (BN / E));
+            bk[i] = e / (BN / E);
+            ob[i] = (n0 + nc < a.N) ? (uint32_t)(((int64_t)bk[i] * a.ldb + nc) * sizeof(TL)) : kOob;
+        }
+    }
+    const TA* A_t = Ag + (int64_t)m0 * a.lda;
+    const TL* B_t = NT ? Bg + (int64_t)n0 * a.ldb : Bg + n0;
+    const float* al_t = (AMODE == kAAlpha) ? a.alpha + ((int64_t)g * a.M + m0) * a.alpha_ld : nullptr;
+
     // staging registers: fp32 A is kept as floats (scaled and, in the bf16 path, rounded
     // only when written to LDS, so the multiply does not wait on the load ahead of the
     // MFMAs); bf16 A and all B chunks are raw 16-byte words
     v4f raf[PD][A_LD][A_F4];
     v4u ra[PD][A_LD];
     float rsc[PD][A_LD];
-    v4u rb[PD][TRN ? 4 : B_LD];
+    v4u rb[PD][NB_LD];
 
+    // Slices at or past k_end load zeros (every column or K-row test fails), so the ring
+    // needs no bounds branches; the zeros land in an LDS buffer nobody reads.
     auto load_slice = [&](int k0, int slot) {
+        const int klim = k_end - k0;               // valid K columns / rows of this slice
+        const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A_t + k0);
+        const __amdgpu_buffer_rsrc_t rsb =
+            make_rsrc(NT ? B_t + k0 : B_t + (int64_t)k0 * a.ldb);
         #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
-            const int m = m0 + i * 32 + (tid >> 3);
-            const int k = k0 + E * (tid & 7);
-            const bool in = m < a.M && k < k_end;
-            const TA* src = Ag + (int64_t)m * a.lda + k;
             if constexpr (A_F32) {
                 #pragma unroll
                 for (int f = 0; f < A_F4; ++f)
-                    raf[slot][i][f] = in ? __builtin_bit_cast(v4f, load_chunk<float>(src + 4 * f, k + 4 * f, k_end))
-                                         : v4f{0.f, 0.f, 0.f, 0.f};
+                    raf[slot][i][f] = __builtin_bit_cast(
+                        v4f, load16(rsa, (oa[i] + 16u * f) | oob_mask(kc + 4 * f, klim)));
             } else {
-                ra[slot][i] = in ? load_chunk<TL>(reinterpret_cast<const TL*>(src), k, k_end)
-                                 : v4u{0u, 0u, 0u, 0u};
+                ra[slot][i] = load16(rsa, oa[i] | oob_mask(kc, klim));
             }
             float sc = row_scale[i];
-            if (AMODE == kAAlpha)
-                sc = in ? a.alpha[((int64_t)g * a.M + m) * a.alpha_ld + k / a.alpha_tile] : 0.f;
+            if constexpr (AMODE == kAAlpha) {
+                // one alpha per 128-key tile: every chunk of a slice shares k0 / alpha_tile
+                const __amdgpu_buffer_rsrc_t rsl = make_rsrc(al_t + k0 / a.alpha_tile);
+                sc = load_f32(rsl, oal[i] | oob_mask(kc, klim));
+            }
             rsc[slot][i] = sc;
         }
-        if constexpr (TRN) {
-            if (tid < 2 * BN) {
-                const int g = tid & 15, c = tid >> 4;   // rows 4g..4g+3, columns 8c..8c+7
-                const int n = n0 + 8 * c;
-                #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int k = k0 + 4 * g + i;
-                    rb[slot][i] = (k < k_end && n < a.N)
-                                      ? *reinterpret_cast<const v4u*>(Bg + (int64_t)k * a.ldb + n)
-                                      : v4u{0u, 0u, 0u, 0u};
-                }
-            }
-            return;
-        }
         #pragma unroll
-        for (int i = 0; i < B_LD; ++i) {
-            v4u v = {0u, 0u, 0u, 0u};
-            if (NT) {
-                const int n = n0 + i * 32 + (tid >> 3);
-                const int k = k0 + E * (tid & 7);
-                if (n < a.N && k < k_end) v = load_chunk<TL>(Bg + (int64_t)n * a.ldb + k, k, k_end);
-            } else {
-                const int e = i * kThreads + tid;
-                const int k = k0 + e / (BN / E);
-                const int n = n0 + E * (e % (BN / E));
-                if (k < k_end && n < a.N) v = *reinterpret_cast<const v4u*>(Bg + (int64_t)k * a.ldb + n);
-            }
-            rb[slot][i] = v;
-        }
+        for (int i = 0; i < NB_LD; ++i)
+            rb[slot][i] = load16(rsb, ob[i] | oob_mask(NT ? kc : bk[i], klim));
     };
 
     auto store_slice = [&](int buf, int slot) {
@@ -228,9 +249,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
 
     const int nslices = (k_end > k_begin) ? (k_end - k_begin + KS - 1) / KS : 0;
     #pragma unroll
-    for (int u = 0; u < PD; ++u)
-        if (u < nslices) load_slice(k_begin + u * KS, u);
-    if (nslices > 0) store_slice(0, 0);
+    for (int u = 0; u < PD; ++u) load_slice(k_begin + u * KS, u);
+    store_slice(0, 0);
     __syncthreads();
 
     const int l32 = lane & 31;
@@ -241,9 +261,9 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
         #pragma unroll
         for (int u = 0; u < PD; ++u) {
             const int s = s0 + u;
-            if (s >= nslices) break;
+            if (PD > 1 && s >= nslices) break;
             const int buf = (PD == 1) ? (s & 1) : (u & 1);
-            if (s + PD < nslices) load_slice(k_begin + (s + PD) * KS, u);
+            load_slice(k_begin + (s + PD) * KS, u);
 
             #pragma unroll
             for (int st = 0; st < 4; ++st) {
@@ -276,7 +296,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                         for (int j = 0; j < TN; ++j) acc[i][j] = MM::sub(fa[i], fb[j], q, acc[i][j]);
             }
 
-            if (s + 1 < nslices) store_slice(buf ^ 1, (u + 1) % PD);
+            store_slice(buf ^ 1, (u + 1) % PD);
+            sched_slice<kStepReads, MM::kSub * TM * TN, kSliceLoads, kSliceWrites>();
             __syncthreads();
         }
     }

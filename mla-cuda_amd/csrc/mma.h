@@ -55,6 +55,74 @@ template <> struct Mma<bf16_t> {
     }
 };
 
+// ---- buffer-resource staging loads --------------------------------------------------
+// Tile staging goes through buffer resources (V#: base address and range in SGPRs) with a
+// 32-bit per-lane byte offset.  The hardware range-checks every load: an offset at or
+// beyond num_records returns zeros without touching memory.  Rows and columns outside a
+// tile get the offset kOob, so the staging code is branch-free, and the per-lane offsets
+// stay fixed while the scalar base walks the K slices.  Every offset a kernel forms for a
+// valid element is below kRsrcRange; the launchers check the leading dimensions for that.
+constexpr uint32_t kOob = 0x80000000u;
+constexpr int kRsrcRange = 0x7fffffff;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base) {
+    // dword3 0x00020000: 32-bit data format, as the gfx9 family requires for raw loads
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, kRsrcRange,
+                                             0x00020000);
+}
+// kOob when x >= lim, else 0 (x >= 0): the sign of x - lim, moved to bit 31 and inverted.
+// Written as arithmetic so the compiler keeps it a VALU op instead of splitting the load
+// that consumes it into divergent branches, which it does for a select.
+__device__ __forceinline__ uint32_t oob_mask(int x, int lim) {
+    return ~(uint32_t)(x - lim) & kOob;
+}
+// 16 bytes at byte offset `off`.  Callers consume all four words: LLVM narrows a b128
+// buffer load whose leading words are unused to a dword load without moving the offset.
+__device__ __forceinline__ v4u load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+}
+__device__ __forceinline__ float load_f32(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// ---- issue order of one staged K slice ------------------------------------------------
+// A slice body is one basic block: next-slice global loads, 4 K steps of LDS fragment reads
+// + MFMAs, LDS writes of the next slice.  Left alone, the scheduler sinks the global loads
+// to the LDS writes (exposing the whole memory latency) and reads each step's fragments
+// only after the previous step's MFMAs.  sched_group_barrier fixes the issue order:
+//   step-0 reads, global loads, step-1 reads,
+//   step-0 MFMAs with step-2 reads spread between them, step-1 MFMAs with step-3 reads,
+//   step-2 MFMAs, step-3 MFMAs with the LDS writes spread between them.
+// Data dependencies are unchanged; only the order of independent instructions is.
+constexpr int kSgMfma = 0x008, kSgVmemRd = 0x020, kSgDsRd = 0x100, kSgDsWr = 0x200;
+
+// NA instructions of class MA and NB of class MB, the B's spread evenly among the A's
+template <int MA, int NA, int MB, int NB>
+__device__ __forceinline__ void sched_spread() {
+    if constexpr (NB == 0) {
+        if constexpr (NA > 0) __builtin_amdgcn_sched_group_barrier(MA, NA, 0);
+    } else if constexpr (NA == 0) {
+        __builtin_amdgcn_sched_group_barrier(MB, NB, 0);
+    } else {
+        constexpr int a = (NA + NB - 1) / NB;
+        __builtin_amdgcn_sched_group_barrier(MA, a, 0);
+        __builtin_amdgcn_sched_group_barrier(MB, 1, 0);
+        sched_spread<MA, NA - a, MB, NB - 1>();
+    }
+}
+
+// RD LDS reads and MF MFMAs per K step, VM global loads and WR LDS writes per slice
+template <int RD, int MF, int VM, int WR>
+__device__ __forceinline__ void sched_slice() {
+    __builtin_amdgcn_sched_group_barrier(kSgDsRd, RD, 0);
+    if constexpr (VM > 0) __builtin_amdgcn_sched_group_barrier(kSgVmemRd, VM, 0);
+    __builtin_amdgcn_sched_group_barrier(kSgDsRd, RD, 0);
+    sched_spread<kSgMfma, MF, kSgDsRd, RD>();
+    sched_spread<kSgMfma, MF, kSgDsRd, RD>();
+    __builtin_amdgcn_sched_group_barrier(kSgMfma, MF, 0);
+    sched_spread<kSgMfma, MF, kSgDsWr, WR>();
+}
+
 // Load 16 bytes of TL elements [k, k + kElems) of a K-contiguous row, zero beyond k_end.
 template <typename TL>
 __device__ __forceinline__ v4u load_chunk(const TL* __restrict__ src, int k, int k_end) {

@@ -19,6 +19,8 @@
 #include "kernels.h"
 #include "mma.h"
 
+#include <algorithm>
+
 namespace mla {
 
 namespace {
@@ -63,25 +65,42 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
     const int nsl_r = (a.R + KS - 1) / KS;
     const int nsl = nsl_r + (a.D + KS - 1) / KS;
 
+    // Staging geometry, fixed for the whole tile: thread tid loads 16-byte chunk tid%8 of
+    // tile rows i*32 + tid/8 (i = 0..3) of Q and of K.  Byte offsets are relative to the
+    // slice's first column of the tile's first row, kOob for rows beyond the tile; the
+    // latent (R-wide) and rope (D-wide) rows have their own strides.
+    const TL* qa_t = static_cast<const TL*>(a.qa) + (row_base + r0) * a.R;
+    const TL* qr_t = static_cast<const TL*>(a.qr) + (row_base + r0) * a.D;
+    const int64_t key_row0 = (int64_t)b * a.key_stride + k0;
+    const TL* ckv_t = static_cast<const TL*>(a.ckv) + key_row0 * a.R;
+    const TL* pe_t = static_cast<const TL*>(a.pe) + key_row0 * a.D;
+    uint32_t oq_r[4], oq_d[4], ok_r[4], ok_d[4];
+    #pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t row = i * 32 + (tid >> 3), cb = 16u * (tid & 7);
+        const bool qv = r0 + (int)row < rows_b, kv = k0 + (int)row < a.Sk;
+        oq_r[i] = qv ? row * (uint32_t)(a.R * sizeof(TL)) + cb : kOob;
+        oq_d[i] = qv ? row * (uint32_t)(a.D * sizeof(TL)) + cb : kOob;
+        ok_r[i] = kv ? row * (uint32_t)(a.R * sizeof(TL)) + cb : kOob;
+        ok_d[i] = kv ? row * (uint32_t)(a.D * sizeof(TL)) + cb : kOob;
+    }
+
+    // Slices at or past nsl load zeros (their column test fails), so the ring needs no
+    // bounds branches; the zeros land in an LDS buffer nobody reads.
     v4u rq[PD][4], rk[PD][4];
     auto load_slice = [&](int s, int slot) {
         const bool rope = s >= nsl_r;
         const int c0 = rope ? (s - nsl_r) * KS : s * KS;
         const int cw = rope ? a.D : a.R;
-        const TL* qsrc = static_cast<const TL*>(rope ? a.qr : a.qa);
-        const TL* ksrc = static_cast<const TL*>(rope ? a.pe : a.ckv);
-        const int c = c0 + E * (tid & 7);
+        const __amdgpu_buffer_rsrc_t rsq = make_rsrc((rope ? qr_t : qa_t) + c0);
+        const __amdgpu_buffer_rsrc_t rsk = make_rsrc((rope ? pe_t : ckv_t) + c0);
+        // column chunks at or past the row width (a partial last slice, or a slice past
+        // nsl) get the kOob bit OR-ed into their offsets
+        const uint32_t cmask = oob_mask(E * (tid & 7), cw - c0);
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = r0 + i * 32 + (tid >> 3);
-            v4u v = {0u, 0u, 0u, 0u};
-            if (r < rows_b && c < cw) v = load_chunk<TL>(qsrc + (row_base + r) * cw + c, c, cw);
-            rq[slot][i] = v;
-            const int k = k0 + i * 32 + (tid >> 3);
-            v4u w = {0u, 0u, 0u, 0u};
-            if (k < a.Sk && c < cw)
-                w = load_chunk<TL>(ksrc + ((int64_t)b * a.key_stride + k) * cw + c, c, cw);
-            rk[slot][i] = w;
+            rq[slot][i] = load16(rsq, (rope ? oq_d[i] : oq_r[i]) | cmask);
+            rk[slot][i] = load16(rsk, (rope ? ok_d[i] : ok_r[i]) | cmask);
         }
     };
     auto store_slice = [&](int buf, int slot) {
@@ -99,8 +118,7 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
 
     #pragma unroll
-    for (int u = 0; u < PD; ++u)
-        if (u < nsl) load_slice(u, u);
+    for (int u = 0; u < PD; ++u) load_slice(u, u);
     store_slice(0, 0);
     __syncthreads();
     // slice s sits in LDS buffer s&1 and came from ring slot s%PD; the loop is unrolled by
@@ -109,9 +127,9 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         #pragma unroll
         for (int u = 0; u < PD; ++u) {
             const int s = s0 + u;
-            if (s < nsl) {
+            if (PD == 1 || s < nsl) {
                 const int buf = (PD == 1) ? (s & 1) : (u & 1);
-                if (s + PD < nsl) load_slice(s + PD, u);
+                load_slice(s + PD, u);
                 #pragma unroll
                 for (int st = 0; st < 4; ++st) {
                     const v4u fq = *reinterpret_cast<const v4u*>(&Qs[buf][wave * 32 + l32][8 * st + 4 * half]);
@@ -124,7 +142,8 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
                         #pragma unroll
                         for (int j = 0; j < 4; ++j) acc[j] = MM::sub(fq, fk[j], q, acc[j]);
                 }
-                if (s + 1 < nsl) store_slice(buf ^ 1, (u + 1) % PD);
+                store_slice(buf ^ 1, (u + 1) % PD);
+                sched_slice<5, 4 * MM::kSub, 8, 8>();
                 __syncthreads();
             }
         }
@@ -181,6 +200,9 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     a.causal_base = (p.sk_total ? p.sk_total : p.Sk) - p.Sq - p.key_offset;
     a.scale_log2 = p.inv_scale * 1.4426950408889634f;
     a.causal = p.causal ? 1 : 0;
+    // every staging offset (a row of the 128-row tile) must stay below the buffer range
+    const int64_t row_bytes = (int64_t)std::max(p.R, p.D) * (p.bf16 ? 2 : 4);
+    if (kBM * row_bytes >= kRsrcRange) return hipErrorInvalidValue;
     const int64_t nblocks = (int64_t)p.B * a.tiles_r * a.P;
     if (nblocks <= 0 || nblocks > 0x7fffffff) return hipErrorInvalidValue;
     if (p.bf16)
