@@ -32,16 +32,20 @@ __device__ __forceinline__ int acc_row(int i, int lane) {
 
 // ----------------------------------------------------------------------------------
 // Wave reductions.  Steps 1..8 move data with DPP (quad_perm, row_half_mirror,
-// row_mirror); step 16 with ds_swizzle's bitmask mode; the two 32-lane halves meet
-// through readlane.  Each step leaves the partial result in every lane of its group.
+// row_mirror); step 16 with gfx950's v_permlane16_swap, which exchanges the odd 16-lane
+// rows of one register with the even rows of another -- given the same value twice it
+// returns, in every lane, the value of its own row pair's even row and odd row.  The two
+// 32-lane halves meet through readlane.  Each step leaves the partial result in every
+// lane of its group, and every step combines its two operands in the same order in all
+// lanes, so sums are bitwise identical across the group.
 // ----------------------------------------------------------------------------------
+// bound_ctrl is set: every control used here reads a lane inside the same row, so it
+// changes nothing but lets the compiler fold the move into the consuming VALU op (one
+// v_max_f32_dpp / v_add_f32_dpp per step).
 template <int kCtrl>
 __device__ __forceinline__ float dpp_move(float v) {
     return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF,
-                                                      false));
-}
-__device__ __forceinline__ float swizzle_xor16(float v) {
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+                                                      true));
 }
 
 struct OpMax {
@@ -58,8 +62,9 @@ __device__ __forceinline__ float half_wave_reduce(float v, Op op) {
     v = op(v, dpp_move<0x4E>(v));   // quad_perm [2,3,0,1]  (lane ^ 2)
     v = op(v, dpp_move<0x141>(v));  // row_half_mirror      (other quad of 8)
     v = op(v, dpp_move<0x140>(v));  // row_mirror           (other half of 16)
-    v = op(v, swizzle_xor16(v));    // ds_swizzle xor 16    (other row of 32)
-    return v;
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return op(__uint_as_float(r[0]), __uint_as_float(r[1]));   // (even row, odd row)
 }
 
 // Reduce across the whole wave; the result is wave-uniform.

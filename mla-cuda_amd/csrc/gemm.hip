@@ -58,11 +58,12 @@ constexpr int nn_row_words() {
 // TL: LDS / MFMA element type (float or bf16_t).  TA: global element type of A (float,
 // or bf16_t when TL is bf16).  B is always TL in global memory.
 // PD = depth of the register prefetch ring (slices in flight while one feeds the MFMAs):
-// 1 for fp32 (MFMA-bound, ~4K MFMA cycles per slice), 2 for bf16 (8x less MFMA work per
-// slice, so more HBM latency to cover).
+// 2 -- one slice of MFMA work (~4K cycles per wave in fp32, 8x less in bf16) does not
+// cover the HBM latency of a long-K stream such as 3c's scores x c_kv; with two slices in
+// flight 3c runs at ~83% of the fp32 MFMA peak instead of ~78%.
 template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
-    constexpr int PD = sizeof(TL) == 2 ? 2 : 1;
+    constexpr int PD = 2;
     using MM = Mma<TL>;
     constexpr int E = MM::kElems;          // elements per 16-byte chunk
     constexpr int KS = MM::kSlice;         // K elements per slice

@@ -13,13 +13,20 @@
 // Epilogue per row and 128-key tile j (mla_kernels.cu:971-1032 computes the same
 // quantities): m_j = max over visible keys of t = s/scale, p = exp(t - m_j) stored into
 // `scores` (0 for masked keys and for the row padding [Sk, ld_p)), l_j = sum p.
-// Grid: batch x row tiles x key tiles, XCD-ordered so one XCD streams one batch's keys
-// while its L2 keeps that batch's Q rows.
+// Persistent grid: at most two workgroups per CU (the LDS and register budget), each walking
+// a strided list of 128x128 tiles.  XCD x owns a contiguous range of the batch-major tile
+// order and its workgroups interleave over it, so the tiles in flight on an XCD share one
+// or two batches' Q rows in that XCD's L2.  The register prefetch ring runs straight
+// across tile boundaries: the next tile's first slices are loaded while the current
+// tile's last slices compute, so a tile switch exposes neither launch overhead nor the
+// first slice's memory latency -- only the epilogue, which the CU's other workgroup
+// covers with MFMA work.
 
 #include "kernels.h"
 #include "mma.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace mla {
 
@@ -30,80 +37,115 @@ constexpr int kBM = 128, kBN = 128, kRowWords = 36, kThreads = 256;
 struct ScoresArgs {
     const void* qa; const void* qr; const void* ckv; const void* pe;
     float* p; float* m_part; float* l_part;
-    int B, Sq, Sk, H, R, D, ld_p, P, tiles_r;
+    int B, Sq, Sk, H, R, D, ld_p, P, tiles_r, tiles;
     int64_t key_stride;   // key rows between batches
     int causal_base;      // sk_total - Sq - key_offset: query s sees local keys <= base + s
     float scale_log2;   // log2(e) / scale
     int causal;
 };
 
+// Tile t of the batch-major order: key tile kt = t % P, row tile tr = (t / P) % tiles_r,
+// batch b = t / (P * tiles_r).
+struct TileId {
+    int b, r0, k0, kt;
+};
+__device__ __forceinline__ TileId tile_id(const ScoresArgs& a, int t) {
+    TileId id;
+    id.kt = t % a.P;
+    const int u = t / a.P;
+    id.r0 = (u % a.tiles_r) * kBM;
+    id.b = u / a.tiles_r;
+    id.k0 = id.kt * kBN;
+    return id;
+}
+
 // PD = depth of the register prefetch ring: while slice s feeds the MFMAs from LDS, slices
 // s+1 .. s+PD are in flight from global memory.  fp32 is MFMA-bound with ~4K MFMA cycles
-// per slice and uses PD = 1; bf16 slices hold 8x less MFMA work, so HBM latency is only
-// hidden with several slices in flight (PD = 4).
-template <typename TL, int PD>
+// per slice and uses PD = 1; bf16 slices hold 8x less MFMA work and keep two slices in
+// flight (PD = 2).
+// PARTIAL: R or D is not a whole number of slices, so a slice's column chunks past the row
+// width must read as zeros (a per-load mask that whole slices do without).
+template <typename TL, int PD, bool PARTIAL>
 __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
     using MM = Mma<TL>;
     constexpr int E = MM::kElems, KS = MM::kSlice;
-    static_assert(PD == 1 || PD % 2 == 0, "ring depth 1 or even (LDS buffer index is slot parity)");
     __shared__ __attribute__((aligned(16))) uint32_t Qs[2][kBM][kRowWords];
     __shared__ __attribute__((aligned(16))) uint32_t Ks[2][kBN][kRowWords];
 
-    int t = xcd_logical_block(blockIdx.x, gridDim.x);
-    const int kt = t % a.P; t /= a.P;
-    const int tr = t % a.tiles_r;
-    const int b = t / a.tiles_r;
+    // this workgroup's tiles: t_first, t_first + nbx, ... below x_hi
+    const int x = blockIdx.x % kNumXCDs, jx = blockIdx.x / kNumXCDs;
+    const int nbx = gridDim.x / kNumXCDs + (x < (int)(gridDim.x % kNumXCDs) ? 1 : 0);
+    const int per_x = a.tiles / kNumXCDs, rem_x = a.tiles % kNumXCDs;
+    const int x_lo = x * per_x + min(x, rem_x);
+    const int x_hi = x_lo + per_x + (x < rem_x ? 1 : 0);
+    if (x_lo + jx >= x_hi) return;   // whole workgroup: no barrier is left waiting
 
-    const int rows_b = a.Sq * a.H;             // rows of this batch
-    const int r0 = tr * kBM;                   // first row (within the batch)
-    const int k0 = kt * kBN;                   // first key
-    const int64_t row_base = (int64_t)b * rows_b;
-
+    const int rows_b = a.Sq * a.H;             // rows of a batch
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, half = lane >> 5;
 
     const int nsl_r = (a.R + KS - 1) / KS;
     const int nsl = nsl_r + (a.D + KS - 1) / KS;
 
-    // Staging geometry, fixed for the whole tile: thread tid loads 16-byte chunk tid%8 of
-    // tile rows i*32 + tid/8 (i = 0..3) of Q and of K.  Byte offsets are relative to the
-    // slice's first column of the tile's first row, kOob for rows beyond the tile; the
-    // latent (R-wide) and rope (D-wide) rows have their own strides.
-    const TL* qa_t = static_cast<const TL*>(a.qa) + (row_base + r0) * a.R;
-    const TL* qr_t = static_cast<const TL*>(a.qr) + (row_base + r0) * a.D;
-    const int64_t key_row0 = (int64_t)b * a.key_stride + k0;
-    const TL* ckv_t = static_cast<const TL*>(a.ckv) + key_row0 * a.R;
-    const TL* pe_t = static_cast<const TL*>(a.pe) + key_row0 * a.D;
-    uint32_t oq_r[4], oq_d[4], ok_r[4], ok_d[4];
+    // Staging geometry: thread tid loads 16-byte chunk tid%8 of tile rows i*32 + tid/8
+    // (i = 0..3) of Q and of K.  Byte offsets are relative to the slice's first column of
+    // the tile's first row; latent (R-wide) and rope (D-wide) rows have their own strides.
+    // Rows beyond a tile's valid count carry the kOob bit, folded in once per tile.
+    uint32_t o_r[4], o_d[4];
     #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const uint32_t row = i * 32 + (tid >> 3), cb = 16u * (tid & 7);
-        const bool qv = r0 + (int)row < rows_b, kv = k0 + (int)row < a.Sk;
-        oq_r[i] = qv ? row * (uint32_t)(a.R * sizeof(TL)) + cb : kOob;
-        oq_d[i] = qv ? row * (uint32_t)(a.D * sizeof(TL)) + cb : kOob;
-        ok_r[i] = kv ? row * (uint32_t)(a.R * sizeof(TL)) + cb : kOob;
-        ok_d[i] = kv ? row * (uint32_t)(a.D * sizeof(TL)) + cb : kOob;
+        o_r[i] = row * (uint32_t)(a.R * sizeof(TL)) + cb;
+        o_d[i] = row * (uint32_t)(a.D * sizeof(TL)) + cb;
     }
 
-    // Slices at or past nsl load zeros (their column test fails), so the ring needs no
-    // bounds branches; the zeros land in an LDS buffer nobody reads.
+    // load cursor: tile lt, slice ls; its operand tile origins and per-row offsets (every
+    // row masked once lt runs past the list, so the ring's surplus loads return zeros)
+    int lt = x_lo + jx, ls = 0;
+    const TL *lqa, *lqr, *lka, *lkr;
+    uint32_t oq_r[4], oq_d[4], ok_r[4], ok_d[4];
+    auto set_load_tile = [&]() __attribute__((always_inline)) {
+        const bool live = lt < x_hi;
+        const TileId id = tile_id(a, live ? lt : x_lo);
+        const int64_t qrow = (int64_t)id.b * rows_b + id.r0;
+        const int64_t krow = (int64_t)id.b * a.key_stride + id.k0;
+        lqa = static_cast<const TL*>(a.qa) + qrow * a.R;
+        lqr = static_cast<const TL*>(a.qr) + qrow * a.D;
+        lka = static_cast<const TL*>(a.ckv) + krow * a.R;
+        lkr = static_cast<const TL*>(a.pe) + krow * a.D;
+        const int qv = live ? min(kBM, rows_b - id.r0) : 0;
+        const int kv = live ? min(kBN, a.Sk - id.k0) : 0;
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int row = i * 32 + (tid >> 3);
+            const uint32_t mq = oob_mask(row, qv), mk = oob_mask(row, kv);
+            oq_r[i] = o_r[i] | mq; oq_d[i] = o_d[i] | mq;
+            ok_r[i] = o_r[i] | mk; ok_d[i] = o_d[i] | mk;
+        }
+    };
+    auto advance_load = [&]() __attribute__((always_inline)) {
+        if (++ls == nsl) {
+            ls = 0;
+            lt += nbx;
+            set_load_tile();
+        }
+    };
+
     v4u rq[PD][4], rk[PD][4];
-    auto load_slice = [&](int s, int slot) {
-        const bool rope = s >= nsl_r;
-        const int c0 = rope ? (s - nsl_r) * KS : s * KS;
-        const int cw = rope ? a.D : a.R;
-        const __amdgpu_buffer_rsrc_t rsq = make_rsrc((rope ? qr_t : qa_t) + c0);
-        const __amdgpu_buffer_rsrc_t rsk = make_rsrc((rope ? pe_t : ckv_t) + c0);
-        // column chunks at or past the row width (a partial last slice, or a slice past
-        // nsl) get the kOob bit OR-ed into their offsets
-        const uint32_t cmask = oob_mask(E * (tid & 7), cw - c0);
+    auto load_slice = [&](int slot) __attribute__((always_inline)) {
+        const bool rope = ls >= nsl_r;
+        const int c0 = rope ? (ls - nsl_r) * KS : ls * KS;
+        const __amdgpu_buffer_rsrc_t rsq = make_rsrc((rope ? lqr : lqa) + c0);
+        const __amdgpu_buffer_rsrc_t rsk = make_rsrc((rope ? lkr : lka) + c0);
+        uint32_t cmask = 0;
+        if constexpr (PARTIAL) cmask = oob_mask(E * (tid & 7), (rope ? a.D : a.R) - c0);
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
             rq[slot][i] = load16(rsq, (rope ? oq_d[i] : oq_r[i]) | cmask);
             rk[slot][i] = load16(rsk, (rope ? ok_d[i] : ok_r[i]) | cmask);
         }
     };
-    auto store_slice = [&](int buf, int slot) {
+    auto store_slice = [&](int buf, int slot) __attribute__((always_inline)) {
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
             *reinterpret_cast<v4u*>(&Qs[buf][i * 32 + (tid >> 3)][4 * (tid & 7)]) = rq[slot][i];
@@ -117,73 +159,126 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         #pragma unroll
         for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
 
+    // ---- epilogue of tile t: per accumulator register e the lane holds tile row
+    // rr(e) = wave*32 + acc_row(e, lane) and keys k0 + 32*j + l32 (j = 0..3).  Work in the
+    // log2 domain with c = log2(e)/scale: m2 = c * (row max of the raw scores) equals the
+    // max of the scaled scores exactly (c > 0 and rounding are monotonic), p = 2^(s*c - m2)
+    // is one fma and one v_exp_f32, and m = m2 * ln(2) is stored in the natural units of
+    // s/scale.  Every instruction here costs MFMA time -- fp32 MFMAs and VALU work do not
+    // overlap on a SIMD -- so full non-causal tiles take a path without visibility masks.
+    // Stores are buffer stores whose offsets carry the kOob bit for rows past the tile and
+    // for lanes that do not own a row's m / l, so no store branches.
+    auto epilogue = [&](int t, auto causal_tag, auto full_tag) __attribute__((always_inline)) {
+        constexpr bool kCausal = decltype(causal_tag)::value;
+        constexpr bool kFull = decltype(full_tag)::value;     // all 128 keys visible
+        const TileId id = tile_id(a, t);
+        const int64_t row0 = (int64_t)id.b * rows_b + id.r0;   // first row of the tile
+        const int rv = min(kBM, rows_b - id.r0);                // valid rows
+        const int kvis = min(kBN, a.Sk - id.k0);                // keys before the padding
+        const int kcols = min(kBN, a.ld_p - id.k0);             // columns inside the p row
+        const float c = a.scale_log2;
+        const __amdgpu_buffer_rsrc_t rsp = make_rsrc(a.p + row0 * a.ld_p + id.k0);
+        const __amdgpu_buffer_rsrc_t rsm = make_rsrc(a.m_part + row0 * a.P + id.kt);
+        const __amdgpu_buffer_rsrc_t rsl = make_rsrc(a.l_part + row0 * a.P + id.kt);
+        const uint32_t ml_lane = oob_mask(l32, 1);              // lane 0 of each half-wave
+        // the lane's first tile row, made opaque here so the compiler does not hoist the
+        // sixteen rows' offsets out of the tile loop (they would stay live through it)
+        int rr0 = wave * 32 + 4 * half;
+        asm volatile("" : "+v"(rr0));
+        #pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int rr = rr0 + 8 * (e >> 2) + (e & 3);       // wave*32 + acc_row(e, lane)
+            const uint32_t rmask = oob_mask(rr, rv);
+            int klast = kvis - 1;                               // last visible key, tile-relative
+            if constexpr (kCausal) {
+                // query index s = r / H sees absolute keys <= Sk_total - Sq + s
+                const int r = min(id.r0 + rr, rows_b - 1);
+                klast = min(klast, a.causal_base + r / a.H - id.k0);
+            }
+            float mx;
+            if constexpr (kFull) {
+                mx = fmaxf(fmaxf(acc[0][e], acc[1][e]), fmaxf(acc[2][e], acc[3][e]));
+            } else {
+                mx = -INFINITY;
+                #pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (32 * j + l32 <= klast) mx = fmaxf(mx, acc[j][e]);
+            }
+            const float m2 = half_wave_reduce(mx, OpMax()) * c;
+            float sum = 0.f;
+            const uint32_t prow = ((uint32_t)(rr * a.ld_p + l32) * 4u) | rmask;
+            #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float pv = __builtin_amdgcn_exp2f(__builtin_fmaf(acc[j][e], c, -m2));
+                if constexpr (!kFull) pv = (32 * j + l32 <= klast) ? pv : 0.f;
+                sum += pv;
+                // ld_p and k0 are multiples of 32: a 32-key group is all in or all out
+                if (kFull || 32 * j < kcols)
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(pv), rsp,
+                                                          (int)(prow + 128u * j), 0, 0);
+            }
+            sum = half_wave_reduce(sum, OpSum());
+            const uint32_t mloff = ((uint32_t)(rr * a.P) * 4u) | rmask | ml_lane;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m2 * 0.69314718055994531f), rsm,
+                                                  (int)mloff, 0, 0);   // * ln 2
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(sum), rsl, (int)mloff, 0, 0);
+        }
+    };
+
+    set_load_tile();
     #pragma unroll
-    for (int u = 0; u < PD; ++u) load_slice(u, u);
+    for (int u = 0; u < PD; ++u) {
+        load_slice(u);
+        advance_load();
+    }
     store_slice(0, 0);
     __syncthreads();
-    // slice s sits in LDS buffer s&1 and came from ring slot s%PD; the loop is unrolled by
-    // PD so every slot index is a compile-time constant
-    for (int s0 = 0; s0 < nsl; s0 += PD) {
-        #pragma unroll
-        for (int u = 0; u < PD; ++u) {
-            const int s = s0 + u;
-            if (PD == 1 || s < nsl) {
-                const int buf = (PD == 1) ? (s & 1) : (u & 1);
-                load_slice(s + PD, u);
-                #pragma unroll
-                for (int st = 0; st < 4; ++st) {
-                    const v4u fq = *reinterpret_cast<const v4u*>(&Qs[buf][wave * 32 + l32][8 * st + 4 * half]);
-                    v4u fk[4];
-                    #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        fk[j] = *reinterpret_cast<const v4u*>(&Ks[buf][j * 32 + l32][8 * st + 4 * half]);
-                    #pragma unroll
-                    for (int q = 0; q < MM::kSub; ++q)
-                        #pragma unroll
-                        for (int j = 0; j < 4; ++j) acc[j] = MM::sub(fq, fk[j], q, acc[j]);
-                }
-                store_slice(buf ^ 1, (u + 1) % PD);
-                sched_slice<5, 4 * MM::kSub, 8, 8>();
-                __syncthreads();
-            }
-        }
-    }
 
-    // ---- epilogue: per accumulator register e the lane holds row acc_row(e, lane) and
-    // keys k0 + 32*j + l32 (j = 0..3).  Work in the log2 domain: t2 = s * (log2(e)/scale),
-    // p = 2^(t2 - max t2) is one v_exp_f32, and m = max t2 * ln(2) is stored in the natural
-    // units of s/scale.  (The exponent's rounding differs from exp(s/scale - m) by ~1e-7
-    // relative to |s/scale|, i.e. ~1e-6 relative in p.)
-    #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int r = r0 + wave * 32 + acc_row(e, lane);   // row within the batch
-        const bool row_ok = r < rows_b;
-        // causal: query index s = r / H sees absolute keys <= Sk_total - Sq + s
-        const int kmax = a.causal ? (a.causal_base + (row_ok ? r / a.H : 0)) : (a.Sk - 1);
-        float tv[4];
-        float mx = -INFINITY;
+    // compute cursor: tile ct, slice cs.  Global slice g sits in LDS buffer g&1 and came
+    // from ring slot g%PD.  One slice step per ring slot, instantiated with the slot as a
+    // compile-time constant (a runtime slot index would turn the ring into indexed
+    // register moves that wait for every load).  Returns true when the list is done.
+    int ct = x_lo + jx, cs = 0;
+    auto slice_step = [&](int g, auto slot_tag) __attribute__((always_inline)) -> bool {
+        constexpr int u = decltype(slot_tag)::value;
+        const int buf = g & 1;
+        load_slice(u);   // global slice g + PD
         #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = k0 + 32 * j + l32;
-            tv[j] = acc[j][e] * a.scale_log2;
-            if (k <= kmax && k < a.Sk) mx = fmaxf(mx, tv[j]);
+        for (int st = 0; st < 4; ++st) {
+            const v4u fq = *reinterpret_cast<const v4u*>(&Qs[buf][wave * 32 + l32][8 * st + 4 * half]);
+            v4u fk[4];
+            #pragma unroll
+            for (int j = 0; j < 4; ++j)
+                fk[j] = *reinterpret_cast<const v4u*>(&Ks[buf][j * 32 + l32][8 * st + 4 * half]);
+            #pragma unroll
+            for (int q = 0; q < MM::kSub; ++q)
+                #pragma unroll
+                for (int j = 0; j < 4; ++j) acc[j] = MM::sub(fq, fk[j], q, acc[j]);
         }
-        mx = half_wave_reduce(mx, OpMax());
-        float sum = 0.f;
-        float* prow = a.p + (row_base + r) * (int64_t)a.ld_p;
+        store_slice(buf ^ 1, (u + 1) % PD);
+        sched_slice<5, 4 * MM::kSub, 8, 8>();
+        __syncthreads();
+        advance_load();
+        if (++cs < nsl) return false;
+        if (a.causal)
+            epilogue(ct, std::true_type(), std::false_type());
+        else if ((ct % a.P + 1) * kBN <= a.Sk)
+            epilogue(ct, std::false_type(), std::true_type());
+        else
+            epilogue(ct, std::false_type(), std::false_type());
         #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int k = k0 + 32 * j + l32;
-            const bool vis = (k <= kmax) && (k < a.Sk);
-            const float pv = vis ? __builtin_amdgcn_exp2f(tv[j] - mx) : 0.f;
-            sum += pv;
-            if (row_ok && k < a.ld_p) prow[k] = pv;
-        }
-        sum = half_wave_reduce(sum, OpSum());
-        if (row_ok && l32 == 0) {
-            a.m_part[(row_base + r) * a.P + kt] = mx * 0.69314718055994531f;  // ln 2
-            a.l_part[(row_base + r) * a.P + kt] = sum;
-        }
+        for (int j = 0; j < 4; ++j)
+            #pragma unroll
+            for (int e = 0; e < 16; ++e) acc[j][e] = 0.f;
+        cs = 0;
+        ct += nbx;
+        return ct >= x_hi;
+    };
+    static_assert(PD == 1 || PD == 2, "ring depth 1 or 2");
+    for (int g = 0;; g += PD) {
+        if (slice_step(g, std::integral_constant<int, 0>())) break;
+        if constexpr (PD == 2)
+            if (slice_step(g + 1, std::integral_constant<int, 1>())) break;
     }
 }
 
@@ -202,13 +297,23 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     a.causal = p.causal ? 1 : 0;
     // every staging offset (a row of the 128-row tile) must stay below the buffer range
     const int64_t row_bytes = (int64_t)std::max(p.R, p.D) * (p.bf16 ? 2 : 4);
-    if (kBM * row_bytes >= kRsrcRange) return hipErrorInvalidValue;
-    const int64_t nblocks = (int64_t)p.B * a.tiles_r * a.P;
-    if (nblocks <= 0 || nblocks > 0x7fffffff) return hipErrorInvalidValue;
-    if (p.bf16)
-        hipLaunchKernelGGL((scores_kernel<bf16_t, 4>), dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
-    else
-        hipLaunchKernelGGL((scores_kernel<float, 1>), dim3((unsigned)nblocks), dim3(kThreads), 0, stream, a);
+    if (kBM * row_bytes >= kRsrcRange || (int64_t)kBM * p.ld_p * 4 >= kRsrcRange)
+        return hipErrorInvalidValue;
+    const int64_t tiles = (int64_t)p.B * a.tiles_r * a.P;
+    if (tiles <= 0 || tiles > 0x7fffffff) return hipErrorInvalidValue;
+    a.tiles = (int)tiles;
+    // two resident workgroups per CU (launch bounds and 74 KB of LDS each)
+    const int64_t nblocks = std::min<int64_t>(tiles, 2 * kNumCUs);
+    const dim3 grid((unsigned)nblocks), block(kThreads);
+    const int ks = p.bf16 ? 64 : 32;   // slice width
+    const bool partial = p.R % ks != 0 || p.D % ks != 0;
+    if (p.bf16) {
+        if (partial) hipLaunchKernelGGL((scores_kernel<bf16_t, 2, true>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((scores_kernel<bf16_t, 2, false>), grid, block, 0, stream, a);
+    } else {
+        if (partial) hipLaunchKernelGGL((scores_kernel<float, 1, true>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((scores_kernel<float, 1, false>), grid, block, 0, stream, a);
+    }
     return hipGetLastError();
 }
 
