@@ -46,7 +46,7 @@ struct GemmArgs {
     int M, N, K, G;
     int split, k_chunk, tiles_m, tiles_n;
     const float* rs; int64_t rs_m, rs_g;
-    const float* alpha; int alpha_ld, alpha_tile;
+    const float* alpha; int alpha_ld, alpha_shift;   // alpha column of k: k >> alpha_shift
 };
 
 template <typename TL, int BN>
@@ -186,7 +186,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             float sc = row_scale[i];
             if constexpr (AMODE == kAAlpha) {
                 // one alpha per 128-key tile: every chunk of a slice shares k0 / alpha_tile
-                const __amdgpu_buffer_rsrc_t rsl = make_rsrc(al_t + k0 / a.alpha_tile);
+                const __amdgpu_buffer_rsrc_t rsl = make_rsrc(al_t + (k0 >> a.alpha_shift));
                 sc = load_f32(rsl, oal[i] | oob_mask(kc, klim));
             }
             rsc[slot][i] = sc;
@@ -527,7 +527,18 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     a.tiles_m = cdiv(p.M, plan.bm);
     a.tiles_n = cdiv(p.N, plan.bn);
     a.rs = p.rs; a.rs_m = p.rs_m; a.rs_g = p.rs_g;
-    a.alpha = p.alpha; a.alpha_ld = p.alpha_ld; a.alpha_tile = p.alpha_tile;
+    a.alpha = p.alpha; a.alpha_ld = p.alpha_ld;
+    a.alpha_shift = 0;
+    if (p.amode == kAAlpha) {
+        // one alpha per slice: the tile is a power of two and a multiple of the slice
+        const int ks = p.bf16 ? 64 : 32;
+        if (p.alpha_tile < ks || (p.alpha_tile & (p.alpha_tile - 1)) != 0) return hipErrorInvalidValue;
+        while ((1 << a.alpha_shift) < p.alpha_tile) ++a.alpha_shift;
+    }
+    // every staging offset (a row of a 128-row tile) must stay below the buffer range
+    const int64_t ea = (p.a_f32 || !p.bf16) ? 4 : 2, eb = p.bf16 ? 2 : 4;
+    if (128 * std::max({p.lda * ea, p.ldb * eb, (int64_t)p.alpha_ld * 4}) >= kRsrcRange)
+        return hipErrorInvalidValue;
     const int64_t nblocks64 = (int64_t)a.tiles_m * a.tiles_n * a.G * a.split;
     if (nblocks64 <= 0 || nblocks64 > 0x7fffffff) return hipErrorInvalidValue;
     const int nblocks = (int)nblocks64;

@@ -17,19 +17,19 @@ namespace mla {
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
 
-// bf16 storage is raw 16-bit words; conversion rounds to nearest even (as torch does).
+// bf16 storage is raw 16-bit words.  Conversion is gfx950's v_cvt_pk_bf16_f32: IEEE
+// round to nearest even, two values per instruction (as torch rounds; a NaN stays a NaN).
 typedef uint16_t bf16_t;
-
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    const uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 template <typename TL> struct Mma;
 
@@ -121,25 +121,6 @@ __device__ __forceinline__ void sched_slice() {
     sched_spread<kSgMfma, MF, kSgDsRd, RD>();
     __builtin_amdgcn_sched_group_barrier(kSgMfma, MF, 0);
     sched_spread<kSgMfma, MF, kSgDsWr, WR>();
-}
-
-// Load 16 bytes of TL elements [k, k + kElems) of a K-contiguous row, zero beyond k_end.
-template <typename TL>
-__device__ __forceinline__ v4u load_chunk(const TL* __restrict__ src, int k, int k_end) {
-    constexpr int E = Mma<TL>::kElems;
-    if (k + E <= k_end) return *reinterpret_cast<const v4u*>(src);
-    v4u r = {0u, 0u, 0u, 0u};
-    if constexpr (sizeof(TL) == 4) {
-        #pragma unroll
-        for (int j = 0; j < 4; ++j) r[j] = (k + j < k_end) ? __float_as_uint(src[j]) : 0u;
-    } else {
-        #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t h = (k + j < k_end) ? (uint32_t)src[j] : 0u;
-            r[j >> 1] |= h << (16 * (j & 1));
-        }
-    }
-    return r;
 }
 
 }  // namespace mla
