@@ -272,6 +272,48 @@ def main():
         traffic = None
     roofline.update({"traffic": traffic, "algorithmic_flop": fl, "algorithmic_bytes": by})
 
+    # ---- the path's neighbours, timed separately (not part of the layer's value):
+    # the wkv_b split (weight prep), the KV-cache append of this step's Sq tokens per
+    # sequence, and the output projection wo of the layer's output.
+    nb = {}
+    e_b = 2 if dname == "bf16" else 4
+    H, R_, D_, V_, hid = dims.n_heads, dims.kv_rank, dims.rope, dims.v, dims.hidden
+    bq = B * Sq
+    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+    W_kv_a = (torch.randn(hid, R_ + D_, device=dev, generator=gen) / math.sqrt(hid)).to(dt)
+    kv_gain = (1.0 + 0.1 * torch.randn(R_, device=dev, generator=gen)).to(dt)
+    W_o = (torch.randn(H * V_, hid, device=dev, generator=gen) / math.sqrt(H * V_)).to(dt)
+    kv_pos = torch.arange(Sk - Sq, Sk, device=dev)
+    nb_calls = {
+        "split_wkv_b": (lambda: ext.split_wkv_b(g["wkv_b"], dims.nope),
+                        0, 2 * e_b * H * (dims.nope + V_) * R_),
+        "kv_append": (lambda: ext.kv_append(g["x"], W_kv_a, kv_gain, kv_pos, g["c_kv"],
+                                            g["pe_cache"], Sk - Sq, eps),
+                      2 * bq * hid * (R_ + D_),
+                      e_b * (bq * hid + hid * (R_ + D_) + R_ + bq * (R_ + D_)) + 8 * Sq),
+        "o_proj": (lambda: ext.o_proj(out, W_o), 2 * bq * H * V_ * hid,
+                   e_b * (bq * H * V_ + H * V_ * hid + bq * hid)),
+    }
+    for name, (fn, fl, by) in nb_calls.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / args.steps * 1e-3
+        mfma_bound = fl > 0 and fl / by > peak_mfma / PEAK_HBM
+        frac = (fl / t / peak_mfma) if mfma_bound else (by / t / PEAK_HBM)
+        nb[name] = {"us": round(t * 1e6, 2), "gflop": round(fl / 1e9, 3),
+                    "mbytes": round(by / 1e6, 2), "tflops": round(fl / t / 1e12, 2),
+                    "gbps": round(by / t / 1e9, 1), "bound": "mfma" if mfma_bound else "hbm",
+                    "frac": round(frac, 4)}
+    print(f"[bench] neighbours: " + ", ".join(f"{k} {v['us']} µs" for k, v in nb.items()),
+          file=sys.stderr, flush=True)
+
     value_us = ms_per_step * 1e3
     rec = {
         "metric": METRIC,
@@ -295,6 +337,7 @@ def main():
         "steps_us": per_step,
         "per_step_sum_us": round(steps_sum, 2),
         "per_step_vs_fused_max_abs": same,
+        "neighbours": nb,
         "wall_s_timed": round(t_wall, 3),
     }
 

@@ -191,6 +191,41 @@ int mla_out(mla_dtype_t dtype, const mla_dims_t* dims, const float* ctx,
             const float* row_sum, const void* W_uv, void* out,
             void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* ======================================================================================
+ * Neighbours of the path: the caller's weight prep before it, the KV-cache write beside
+ * it, and the output projection after it.  None is in the reference; the reference names
+ * the weight split its callers repeat per call (exhaustive_benchmark_suite.py:261-265,
+ * 320, 334) and wkv_a's cache write (exhaustive_benchmark_suite.py:188-196).
+ * ==================================================================================== */
+
+/* Weight prep, once at load: split wkv_b [H, nope + v, kv_rank] into contiguous
+ * W_uk [H, nope, kv_rank] = wkv_b[:, :nope, :] and W_uv [H, v, kv_rank] = wkv_b[:, nope:, :]
+ * (the copies the reference's callers make with .contiguous() on every call).  Uses
+ * dims->heads, nope, v, kv_rank.  Bit-exact copy. */
+int mla_split_wkv_b(mla_dtype_t dtype, const mla_dims_t* dims, const void* wkv_b,
+                    void* W_uk, void* W_uv, hipStream_t stream);
+
+/* KV-cache append for dims->sq new tokens of each of dims->batch sequences, as DeepSeek-V3
+ * writes its absorbed-layout cache (deepseek-ai/DeepSeek-V3 inference/model.py, MLA.forward):
+ *   kv = x @ W_kv_a                                  x [B, Sq, hidden], W_kv_a [hidden, kv_rank + rope]
+ *   c_kv[b, start_row + s, :]     = RMSNorm(kv[b, s, :kv_rank]) * kv_norm_w     (eps)
+ *   pe_cache[b, start_row + s, :] = RoPE(kv[b, s, kv_rank:], positions[s])       (interleaved pairs)
+ * with the same RMSNorm and RoPE arithmetic as mla_q_absorbed (inv_freq as there).
+ * c_kv [B, cache_rows, kv_rank] and pe_cache [B, cache_rows, rope] are updated in place;
+ * rows outside [start_row, start_row + Sq) are untouched.  start_row + Sq <= cache_rows. */
+size_t mla_kv_append_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims);
+int mla_kv_append(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_kv_a,
+                  const void* kv_norm_w, const int64_t* positions, const float* inv_freq,
+                  double eps, int32_t start_row, int32_t cache_rows, void* c_kv,
+                  void* pe_cache, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream);
+
+/* Output projection wo: out [B*Sq, hidden] = attn [B*Sq, H*v] @ W_o [H*v, hidden], all in
+ * dtype (fp32 accumulation).  attn is mla_attention's output [B, Sq, H, v]. */
+size_t mla_o_proj_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims);
+int mla_o_proj(mla_dtype_t dtype, const mla_dims_t* dims, const void* attn, const void* W_o,
+               void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

@@ -7,7 +7,8 @@
 //       -> out [B,Sq,H,v]                                         (mla_kernels.cu:1479-1682)
 //
 // plus one op per step (gemm, rmsnorm, rope, absorb, scores, combine, ctx, out) that runs
-// the very kernels the fused calls run.  This file only validates tensors, allocates
+// the very kernels the fused calls run, and the path's neighbours: split_wkv_b (weight
+// prep), kv_append (the cache write) and o_proj (wo).  This file only validates tensors, allocates
 // outputs and workspace from torch's caching allocator and passes raw pointers and the
 // current HIP stream to the C ABI; all device work lives in libmla_amd.so.
 //
@@ -425,6 +426,104 @@ torch::Tensor step_out(torch::Tensor ctx, torch::Tensor row_sum, torch::Tensor W
     return out;
 }
 
+// ------------------------------------------------------------------ neighbours of the path
+
+// Weight prep once at load: the W_uk / W_uv halves of wkv_b as contiguous tensors.
+std::vector<torch::Tensor> op_split_wkv_b(torch::Tensor wkv_b, int64_t nope_dim) {
+    check_dim(wkv_b, 3, "wkv_b", "[H, nope + v, kv_rank]");
+    const int64_t H = wkv_b.size(0), rows = wkv_b.size(1), R = wkv_b.size(2);
+    TORCH_CHECK(nope_dim > 0 && nope_dim < rows, "MLA: nope_dim must lie in (0, ", rows, ")");
+    const mla_dtype_t dt = to_mla_dtype(wkv_b, "wkv_b");
+    check_device({&wkv_b});
+    c10::DeviceGuard guard(wkv_b.device());
+    auto w = wkv_b.contiguous();
+    mla_dims_t d{};
+    d.heads = (int32_t)H; d.nope = (int32_t)nope_dim; d.v = (int32_t)(rows - nope_dim);
+    d.kv_rank = (int32_t)R;
+    auto uk = torch::empty({H, nope_dim, R}, w.options());
+    auto uv = torch::empty({H, rows - nope_dim, R}, w.options());
+    check_status(mla_split_wkv_b(dt, &d, w.data_ptr(), uk.data_ptr(), uv.data_ptr(),
+                                 current_stream()),
+                 "split_wkv_b");
+    return {uk, uv};
+}
+
+// KV-cache append: writes rows [start_row, start_row + Sq) of c_kv and pe_cache in place.
+void op_kv_append(torch::Tensor x, torch::Tensor W_kv_a, torch::Tensor kv_norm_w,
+                  torch::Tensor positions, torch::Tensor c_kv, torch::Tensor pe_cache,
+                  int64_t start_row, double eps) {
+    check_dim(x, 3, "x", "[B, Sq, hidden]");
+    check_dim(W_kv_a, 2, "W_kv_a", "[hidden, kv_rank + rope]");
+    check_dim(c_kv, 3, "c_kv", "[B, cache_rows, kv_rank]");
+    check_dim(pe_cache, 3, "pe_cache", "[B, cache_rows, rope]");
+    const int64_t B = x.size(0), Sq = x.size(1), hidden = x.size(2);
+    const int64_t rows = c_kv.size(1), R = c_kv.size(2), D = pe_cache.size(2);
+    TORCH_CHECK(W_kv_a.size(0) == hidden && W_kv_a.size(1) == R + D,
+                "W_kv_a must be [hidden, kv_rank + rope] (got ", W_kv_a.sizes(), ")");
+    TORCH_CHECK(c_kv.size(0) == B && pe_cache.size(0) == B && pe_cache.size(1) == rows,
+                "c_kv [B, cache_rows, kv_rank] and pe_cache [B, cache_rows, rope] must agree "
+                "with x (got ", c_kv.sizes(), " and ", pe_cache.sizes(), ")");
+    TORCH_CHECK(kv_norm_w.dim() == 1 && kv_norm_w.size(0) == R,
+                "kv_norm_w must be a 1-D tensor of length kv_rank (got ", kv_norm_w.sizes(), ")");
+    TORCH_CHECK(positions.dim() == 1 && positions.size(0) == Sq,
+                "positions must be a 1-D tensor of length Sq (got ", positions.sizes(), ")");
+    TORCH_CHECK(!positions.is_floating_point() && !positions.is_complex(),
+                "positions must be an integer tensor");
+    TORCH_CHECK(D > 0 && D % 2 == 0, "MLA: the rope width must be positive and even");
+    TORCH_CHECK(c_kv.is_contiguous() && pe_cache.is_contiguous(),
+                "MLA: c_kv and pe_cache are updated in place and must be contiguous");
+    const mla_dtype_t dt = to_mla_dtype(x, "x");
+    check_same_dtype(x, W_kv_a, "W_kv_a");
+    check_same_dtype(x, kv_norm_w, "kv_norm_w");
+    check_same_dtype(x, c_kv, "c_kv");
+    check_same_dtype(x, pe_cache, "pe_cache");
+    check_device({&x, &W_kv_a, &kv_norm_w, &positions, &c_kv, &pe_cache});
+
+    c10::DeviceGuard guard(x.device());
+    auto xc = x.contiguous();
+    auto wa = W_kv_a.contiguous();
+    auto g = kv_norm_w.contiguous();
+    auto pos = positions.to(torch::kLong).contiguous();
+    auto inv_freq = device_inv_freq(D, x.device());
+    mla_dims_t d{};
+    d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.hidden = (int32_t)hidden;
+    d.kv_rank = (int32_t)R; d.rope = (int32_t)D;
+    TORCH_CHECK(start_row >= 0 && rows < INT32_MAX && start_row + Sq <= rows,
+                "MLA: start_row + Sq must not exceed the cache rows");
+    const size_t wsb = mla_kv_append_workspace_bytes(dt, &d);
+    auto ws = workspace(wsb, x);
+    check_status(mla_kv_append(dt, &d, xc.data_ptr(), wa.data_ptr(), g.data_ptr(),
+                               pos.data_ptr<int64_t>(), inv_freq.data_ptr<float>(), eps,
+                               (int32_t)start_row, (int32_t)rows, c_kv.data_ptr(),
+                               pe_cache.data_ptr(), ws.data_ptr(), wsb, current_stream()),
+                 "kv_append");
+}
+
+// Output projection wo: [B, Sq, H, v] @ [H*v, hidden] -> [B, Sq, hidden].
+torch::Tensor op_o_proj(torch::Tensor attn, torch::Tensor W_o) {
+    check_dim(attn, 4, "attn", "[B, Sq, H, v]");
+    check_dim(W_o, 2, "W_o", "[H*v, hidden]");
+    const int64_t B = attn.size(0), Sq = attn.size(1), H = attn.size(2), v = attn.size(3);
+    const int64_t hidden = W_o.size(1);
+    TORCH_CHECK(W_o.size(0) == H * v, "W_o must be [H*v, hidden] (got ", W_o.sizes(), ")");
+    const mla_dtype_t dt = to_mla_dtype(attn, "attn");
+    check_same_dtype(attn, W_o, "W_o");
+    check_device({&attn, &W_o});
+    c10::DeviceGuard guard(attn.device());
+    auto a = attn.contiguous();
+    auto w = W_o.contiguous();
+    mla_dims_t d{};
+    d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.heads = (int32_t)H; d.v = (int32_t)v;
+    d.hidden = (int32_t)hidden;
+    auto out = torch::empty({B, Sq, hidden}, a.options());
+    const size_t wsb = mla_o_proj_workspace_bytes(dt, &d);
+    auto ws = workspace(wsb, a);
+    check_status(mla_o_proj(dt, &d, a.data_ptr(), w.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                            wsb, current_stream()),
+                 "o_proj");
+    return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
@@ -459,4 +558,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("score_tile", []() { return mla_score_tile(); });
     m.def("score_ld", [](int32_t sk) { return mla_score_ld(sk); });
     m.def("version", []() { return std::string(mla_version()); });
+    m.def("split_wkv_b", &op_split_wkv_b,
+          "Weight prep: contiguous [W_uk, W_uv] halves of wkv_b [H, nope + v, kv_rank]",
+          py::arg("wkv_b"), py::arg("nope_dim"));
+    m.def("kv_append", &op_kv_append,
+          "KV-cache append in place: c_kv rows = RMSNorm((x @ W_kv_a)[..., :kv_rank]), "
+          "pe_cache rows = RoPE((x @ W_kv_a)[..., kv_rank:])",
+          py::arg("x"), py::arg("W_kv_a"), py::arg("kv_norm_w"), py::arg("positions"),
+          py::arg("c_kv"), py::arg("pe_cache"), py::arg("start_row"), py::arg("eps"));
+    m.def("o_proj", &op_o_proj, "Output projection: [B, Sq, H, v] @ W_o [H*v, hidden]",
+          py::arg("attn"), py::arg("W_o"));
 }

@@ -385,6 +385,82 @@ int check_scale(double scale) {
     return MLA_OK;
 }
 
+// ------------------------------------------------------------------ neighbours of the path
+
+// wkv_b split reads heads, nope, v, kv_rank.
+int check_split_dims(mla_dtype_t dt, const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_pos(d->nope, "dims.nope"));
+    MLA_CHECK(check_pos(d->v, "dims.v"));
+    MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
+    if ((int64_t)d->heads * (d->nope + d->v) * (int64_t)d->kv_rank > ((int64_t)1 << 40))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "wkv_b too large");
+    return MLA_OK;
+}
+
+// KV append reads batch, sq, hidden, kv_rank, rope.
+int check_kv_dims(mla_dtype_t dt, const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_row(dt, d->hidden, "dims.hidden"));
+    MLA_CHECK(check_row(dt, d->kv_rank, "dims.kv_rank"));
+    MLA_CHECK(check_row(dt, d->rope, "dims.rope"));
+    if ((int64_t)d->batch * d->sq * (int64_t)(d->kv_rank + d->rope) > kMaxI32 ||
+        (int64_t)d->batch * d->sq * (int64_t)d->hidden > kMaxI32)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq too large");
+    return MLA_OK;
+}
+
+// wo reads batch, sq, heads, v, hidden.
+int check_oproj_dims(mla_dtype_t dt, const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_row(dt, d->v, "dims.v"));
+    MLA_CHECK(check_row(dt, d->hidden, "dims.hidden"));
+    const int64_t bq = (int64_t)d->batch * d->sq;
+    if (bq * d->heads * (int64_t)d->v > kMaxI32 || bq * (int64_t)d->hidden > kMaxI32 ||
+        (int64_t)d->heads * d->v > kMaxI32 / 8)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads*v too large");
+    return MLA_OK;
+}
+
+GemmProblem kv_problem(mla_dtype_t dt, const mla_dims_t* d, const void* x, const void* W,
+                       float* C) {
+    const int n = d->kv_rank + d->rope;
+    GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt);
+    p.A = x; p.lda = d->hidden;
+    p.B = W; p.ldb = n;
+    p.C = C; p.ldc = n;
+    p.M = d->batch * d->sq; p.N = n; p.K = d->hidden;
+    return p;
+}
+
+GemmProblem oproj_problem(mla_dtype_t dt, const mla_dims_t* d, const void* attn, const void* W,
+                          void* out) {
+    const int k = d->heads * d->v;
+    GemmProblem p;
+    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt); p.out_type = storage_out(dt);
+    p.A = attn; p.lda = k;
+    p.B = W; p.ldb = d->hidden;
+    p.C = out; p.ldc = d->hidden;
+    p.M = d->batch * d->sq; p.N = d->hidden; p.K = k;
+    return p;
+}
+
+// x @ W_kv_a lands in one fp32 buffer: the product itself, or its split-K partials for the
+// append kernel to sum.
+size_t kv_ws_bytes(mla_dtype_t dt, const mla_dims_t* d, GemmPlan* plan_out) {
+    const GemmPlan plan = plan_gemm(kv_problem(dt, d, nullptr, nullptr, nullptr));
+    if (plan_out) *plan_out = plan;
+    return align_up((size_t)std::max(1, plan.split) * d->batch * d->sq *
+                    (size_t)(d->kv_rank + d->rope) * sizeof(float));
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -725,6 +801,89 @@ int mla_attention_streaming(mla_dtype_t dtype, const mla_dims_t* dims, const voi
     GemmProblem op = out_problem(dtype, dims, ctx, run_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
                 "stream 3d launch");
+    return ok();
+}
+
+int mla_split_wkv_b(mla_dtype_t dtype, const mla_dims_t* dims, const void* wkv_b, void* W_uk,
+                    void* W_uv, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_split_dims(dtype, dims));
+    MLA_CHECK(check_ptr(wkv_b, "wkv_b"));
+    MLA_CHECK(check_ptr(W_uk, "W_uk"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    const int64_t row_bytes = (int64_t)dims->kv_rank * (is_bf16(dtype) ? 2 : 4);
+    MLA_TRY_HIP(launch_split_rows(wkv_b, W_uk, W_uv, dims->heads, dims->nope, dims->v, row_bytes,
+                                  stream),
+                "wkv_b split launch");
+    return ok();
+}
+
+size_t mla_kv_append_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
+    if (!dims || check_dtype(dtype) != MLA_OK || check_kv_dims(dtype, dims) != MLA_OK) return 0;
+    return kv_ws_bytes(dtype, dims, nullptr);
+}
+
+int mla_kv_append(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_kv_a,
+                  const void* kv_norm_w, const int64_t* positions, const float* inv_freq,
+                  double eps, int32_t start_row, int32_t cache_rows, void* c_kv, void* pe_cache,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_kv_dims(dtype, dims));
+    MLA_CHECK(check_ptr(x, "x"));
+    MLA_CHECK(check_ptr(W_kv_a, "W_kv_a"));
+    MLA_CHECK(check_ptr(kv_norm_w, "kv_norm_w"));
+    MLA_CHECK(check_ptr(positions, "positions"));
+    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    if (cache_rows <= 0 || start_row < 0 || (int64_t)start_row + dims->sq > cache_rows)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "cache rows [start_row, start_row + sq) = [%d, %lld) must lie in [0, %d)",
+                    start_row, (long long)start_row + dims->sq, cache_rows);
+    if ((int64_t)dims->batch * cache_rows * (int64_t)dims->kv_rank > ((int64_t)1 << 40))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "cache too large");
+    GemmPlan plan;
+    const size_t need = kv_ws_bytes(dtype, dims, &plan);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, need));
+
+    const int bq = dims->batch * dims->sq;
+    const int n = dims->kv_rank + dims->rope;
+    float* acc = at<float>(workspace, 0);
+    GemmProblem gp = kv_problem(dtype, dims, x, W_kv_a, acc);
+    int nsplit = 1;
+    if (plan.split > 1) {
+        nsplit = plan.split;
+        plan.workspace_bytes = 0;
+        MLA_TRY_HIP(launch_gemm_partials(gp, plan, acc, stream), "kv GEMM launch");
+    } else {
+        MLA_TRY_HIP(launch_gemm(gp, plan, nullptr, stream), "kv GEMM launch");
+    }
+    MLA_TRY_HIP(launch_kv_append(acc, nsplit, (int64_t)bq * n, kv_norm_w, positions, inv_freq,
+                                 c_kv, pe_cache, storage_out(dtype), dims->batch, dims->sq,
+                                 dims->kv_rank, dims->rope, start_row, cache_rows, (float)eps,
+                                 stream),
+                "kv append launch");
+    return ok();
+}
+
+size_t mla_o_proj_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
+    if (!dims || check_dtype(dtype) != MLA_OK || check_oproj_dims(dtype, dims) != MLA_OK) return 0;
+    return align_up(plan_gemm(oproj_problem(dtype, dims, nullptr, nullptr, nullptr)).workspace_bytes);
+}
+
+int mla_o_proj(mla_dtype_t dtype, const mla_dims_t* dims, const void* attn, const void* W_o,
+               void* out, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_oproj_dims(dtype, dims));
+    MLA_CHECK(check_ptr(attn, "attn"));
+    MLA_CHECK(check_ptr(W_o, "W_o"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const GemmProblem gp = oproj_problem(dtype, dims, attn, W_o, out);
+    const GemmPlan plan = plan_gemm(gp);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, align_up(plan.workspace_bytes)));
+    MLA_TRY_HIP(launch_gemm(gp, plan, workspace, stream), "wo GEMM launch");
     return ok();
 }
 

@@ -376,7 +376,7 @@ hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipSt
 
 // The operand/epilogue combinations the layer uses (others are rejected):
 //   fp32:  NN plain  -> f32 (2a1, 2a2, 2c) | NN alpha -> f32 (3c) | NT rowrecip -> f32 (3d)
-//   bf16:  NN plain, A bf16 -> f32 (2a1, 2a2) | NN plain, A f32 -> bf16 (2c)
+//   bf16:  NN plain, A bf16 -> f32 (2a1, 2a2) or -> bf16 (wo) | NN plain, A f32 -> bf16 (2c)
 //          NN alpha, A f32 -> f32 (3c)         | NT rowrecip, A f32 -> bf16 (3d)
 // A split-K launch writes fp32 partials whatever the output type.
 hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
@@ -391,8 +391,11 @@ hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int
             return launch_tiles<float, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
         return hipErrorInvalidValue;
     }
-    if (!p.b_nt && p.amode == kAPlain && !p.a_f32 && (p.out_type == kOutF32 || split))
-        return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+    if (!p.b_nt && p.amode == kAPlain && !p.a_f32) {
+        if (split || p.out_type == kOutF32)
+            return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutBF16>(a, bm, bn, nblocks, stream);
+    }
     if (!p.b_nt && p.amode == kAPlain && p.a_f32) {
         if (split || p.out_type == kOutF32)
             return launch_tiles<bf16_t, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);

@@ -67,6 +67,17 @@ hipError_t launch_stream_merge(float* ctx, float* run_max, float* run_sum, const
                                const float* max_c, const float* sum_c, int rows, int R,
                                bool first, hipStream_t stream);
 
+// KV-cache append: in = x @ W_kv_a rows [B*Sq][R + D] (or nsplit split-K partials);
+// c_kv[b][start_row + s] = RMSNorm(row[:R]) * gain (as launch_rmsnorm),
+// pe[b][start_row + s] = RoPE(row[R:], positions[s]) (as launch_rope).
+hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, const void* gain,
+                            const int64_t* positions, const float* inv_freq, void* c_kv,
+                            void* pe, OutType out_type, int B, int Sq, int R, int D,
+                            int start_row, int cache_rows, float eps, hipStream_t stream);
+// Split each group of rows_a + rows_b rows (row_bytes each) of src into dst_a / dst_b.
+hipError_t launch_split_rows(const void* src, void* dst_a, void* dst_b, int64_t groups,
+                             int rows_a, int rows_b, int64_t row_bytes, hipStream_t stream);
+
 // ---------------------------------------------------------------- 3a scores
 struct ScoresProblem {
     const void* qa = nullptr;    // [B*Sq*H, R]   storage dtype

@@ -1,4 +1,5 @@
-// Row-wise steps of the layer: 2a-n RMSNorm, 2b RoPE, 3b softmax-partial combine.
+// Row-wise steps of the layer: 2a-n RMSNorm, 2b RoPE, 3b softmax-partial combine, the
+// streaming merge, and the KV-cache append and wkv_b split beside the layer.
 // All three are HBM/latency bound and tiny next to the contractions; they use 128-bit
 // loads where the row is contiguous and wave64 DPP reductions.
 
@@ -11,50 +12,53 @@ namespace mla {
 
 namespace {
 
+typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));   // 16 raw bytes
+
 // ---- 2a-n: one 256-thread workgroup per row.  The input may be nsplit fp32 partial
 // sums of 2a1 (split-K); they are added here in slice order, which is what makes the
 // split-K of 2a1 free of a separate reduction pass.  Each thread keeps its summed
 // elements in registers between the sum-of-squares pass and the output pass (rows up to
 // 4096 wide), so the partials are read once; the partial loop is unrolled so the loads
-// of all slices are in flight together.
+// of all slices are in flight together.  The row body is shared with the KV-cache append,
+// so both normalise with the same arithmetic and summation order.
 constexpr int kNormCache = 4;  // float4 per thread kept in registers (256*4*4 = 4096 wide)
 
+// Sum of nsplit partial rows (slice order) at float4 column c4.
+__device__ __forceinline__ v4f sum_partials4(const float* base, int nsplit, int64_t split_stride,
+                                             int c4) {
+    v4f v = *reinterpret_cast<const v4f*>(base + 4 * c4);
+    int s = 1;
+    for (; s + 4 <= nsplit; s += 4) {
+        const v4f a = *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
+        const v4f b = *reinterpret_cast<const v4f*>(base + (s + 1) * split_stride + 4 * c4);
+        const v4f c = *reinterpret_cast<const v4f*>(base + (s + 2) * split_stride + 4 * c4);
+        const v4f d = *reinterpret_cast<const v4f*>(base + (s + 3) * split_stride + 4 * c4);
+        v += a; v += b; v += c; v += d;
+    }
+    for (; s < nsplit; ++s)
+        v += *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
+    return v;
+}
+
+// out_row[0:N] = row * rsqrt(mean(row^2) + eps) * gain, row = summed partials at `base`.
+// Called by all 256 threads of the workgroup (it synchronises through `red`).
 template <int OUT>
-__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ in, int nsplit,
-                                                      int64_t split_stride, const void* gain_v,
-                                                      void* out_v, int N, float eps) {
-    __shared__ float red[4];
-    const int row = blockIdx.x;
+__device__ __forceinline__ void rms_row(const float* base, int nsplit, int64_t split_stride,
+                                        const void* gain_v, void* out_row, int N, float eps,
+                                        float* red) {
     const int tid = threadIdx.x;
     const int n4 = N >> 2;
-    const float* base = in + (int64_t)row * N;
-
-    auto load4 = [&](int c4) {
-        v4f v = *reinterpret_cast<const v4f*>(base + 4 * c4);
-        int s = 1;
-        for (; s + 4 <= nsplit; s += 4) {
-            const v4f a = *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
-            const v4f b = *reinterpret_cast<const v4f*>(base + (s + 1) * split_stride + 4 * c4);
-            const v4f c = *reinterpret_cast<const v4f*>(base + (s + 2) * split_stride + 4 * c4);
-            const v4f d = *reinterpret_cast<const v4f*>(base + (s + 3) * split_stride + 4 * c4);
-            v += a; v += b; v += c; v += d;
-        }
-        for (; s < nsplit; ++s)
-            v += *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
-        return v;
-    };
-
     v4f cache[kNormCache];
     float ss = 0.f;
     #pragma unroll
     for (int j = 0; j < kNormCache; ++j) {
         const int c4 = tid + 256 * j;
-        cache[j] = (c4 < n4) ? load4(c4) : v4f{0.f, 0.f, 0.f, 0.f};
+        cache[j] = (c4 < n4) ? sum_partials4(base, nsplit, split_stride, c4) : v4f{0.f, 0.f, 0.f, 0.f};
         ss += cache[j][0] * cache[j][0] + cache[j][1] * cache[j][1] +
               cache[j][2] * cache[j][2] + cache[j][3] * cache[j][3];
     }
     for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256) {
-        const v4f v = load4(c4);
+        const v4f v = sum_partials4(base, nsplit, split_stride, c4);
         ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     }
     ss = wave_reduce(ss, OpSum());
@@ -69,10 +73,10 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
             v4f o;
             #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = v[j] * inv * g[j];
-            *reinterpret_cast<v4f*>(static_cast<float*>(out_v) + (int64_t)row * N + 4 * c4) = o;
+            *reinterpret_cast<v4f*>(static_cast<float*>(out_row) + 4 * c4) = o;
         } else {
             const __hip_bfloat16* g = static_cast<const __hip_bfloat16*>(gain_v) + 4 * c4;
-            __hip_bfloat16* o = static_cast<__hip_bfloat16*>(out_v) + (int64_t)row * N + 4 * c4;
+            __hip_bfloat16* o = static_cast<__hip_bfloat16*>(out_row) + 4 * c4;
             #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = __float2bfloat16(v[j] * inv * __bfloat162float(g[j]));
         }
@@ -82,7 +86,20 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
         const int c4 = tid + 256 * j;
         if (c4 < n4) emit(c4, cache[j]);
     }
-    for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256) emit(c4, load4(c4));
+    for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256)
+        emit(c4, sum_partials4(base, nsplit, split_stride, c4));
+}
+
+template <int OUT>
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ in, int nsplit,
+                                                      int64_t split_stride, const void* gain_v,
+                                                      void* out_v, int N, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    void* out_row = OUT == kOutF32
+                        ? static_cast<void*>(static_cast<float*>(out_v) + (int64_t)row * N)
+                        : static_cast<void*>(static_cast<__hip_bfloat16*>(out_v) + (int64_t)row * N);
+    rms_row<OUT>(in + (int64_t)row * N, nsplit, split_stride, gain_v, out_row, N, eps, red);
 }
 
 // ---- 2b: one workgroup per (query row bq, chunk of 32 heads).  Every head of a row uses
@@ -93,6 +110,13 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
 // elements of the chunk with 64-bit loads and stores.
 constexpr int kRopeHeads = 32;
 constexpr int kRopeMaxHalf = 256;
+
+// Rotation of the interleaved pair (x0, x1) = (x[2i], x[2i+1]) by angle pos * inv_freq[i].
+__device__ __forceinline__ float rope_angle(int64_t pos, float inv_freq) {
+    return (float)pos * inv_freq;
+}
+__device__ __forceinline__ float rope_even(float x0, float x1, float c, float s) { return x0 * c - x1 * s; }
+__device__ __forceinline__ float rope_odd(float x0, float x1, float c, float s) { return x0 * s + x1 * c; }
 
 template <int OUT>
 __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_raw,
@@ -106,9 +130,9 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
     const int bq = blockIdx.x;
     const int h0 = blockIdx.y * kRopeHeads;
     const int nh = min(kRopeHeads, H - h0);
-    const float pos = (float)positions[bq % Sq];
+    const int64_t pos = positions[bq % Sq];
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
-        const float ang = pos * inv_freq[i];
+        const float ang = rope_angle(pos, inv_freq[i]);
         cs[i] = cosf(ang);
         sn[i] = sinf(ang);
     }
@@ -118,8 +142,8 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
         const int h = h0 + idx / half;
         const int i = idx % half;
         const float2 x = *reinterpret_cast<const float2*>(src + (int64_t)h * qk + 2 * i);
-        const float e = x.x * cs[i] - x.y * sn[i];
-        const float o = x.x * sn[i] + x.y * cs[i];
+        const float e = rope_even(x.x, x.y, cs[i], sn[i]);
+        const float o = rope_odd(x.x, x.y, cs[i], sn[i]);
         const int64_t dst = ((int64_t)bq * H + h) * rope + 2 * i;
         if (OUT == kOutF32) {
             *reinterpret_cast<float2*>(static_cast<float*>(out_v) + dst) = make_float2(e, o);
@@ -192,6 +216,70 @@ __global__ void __launch_bounds__(256) stream_merge_kernel(float* __restrict__ c
     }
 }
 
+// ---- KV-cache append: one 256-thread workgroup per new token row (b, s).  The row's
+// kv_rank latent columns are normalised exactly as 2a-n normalises (rms_row), its rope
+// columns rotated exactly as 2b rotates, and both land in cache row start_row + s of
+// batch b.  The input is the GEMM output x @ W_kv_a or its nsplit split-K partials, rows
+// of ld = kv_rank + rope floats; partials are summed in slice order.
+template <int OUT>
+__global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict__ in, int nsplit,
+                                                        int64_t split_stride, const void* gain,
+                                                        const int64_t* __restrict__ positions,
+                                                        const float* __restrict__ inv_freq,
+                                                        void* c_kv, void* pe, int Sq, int R, int D,
+                                                        int start_row, int cache_rows, float eps) {
+    __shared__ float red[4];
+    const int row = blockIdx.x;
+    const int b = row / Sq, s = row % Sq;
+    const int ld = R + D;
+    const float* base = in + (int64_t)row * ld;
+    const int64_t crow = (int64_t)b * cache_rows + start_row + s;
+    // rope pairs first (no barrier inside), then the workgroup-wide norm
+    const int64_t pos = positions[s];
+    for (int i = threadIdx.x; i < D / 2; i += blockDim.x) {
+        float x0 = base[R + 2 * i], x1 = base[R + 2 * i + 1];
+        for (int q = 1; q < nsplit; ++q) {
+            x0 += base[q * split_stride + R + 2 * i];
+            x1 += base[q * split_stride + R + 2 * i + 1];
+        }
+        const float ang = rope_angle(pos, inv_freq[i]);
+        const float c = cosf(ang), sn = sinf(ang);
+        const float e = rope_even(x0, x1, c, sn), o = rope_odd(x0, x1, c, sn);
+        if (OUT == kOutF32) {
+            float* dst = static_cast<float*>(pe) + crow * D + 2 * i;
+            dst[0] = e; dst[1] = o;
+        } else {
+            __hip_bfloat16* dst = static_cast<__hip_bfloat16*>(pe) + crow * D + 2 * i;
+            dst[0] = __float2bfloat16(e); dst[1] = __float2bfloat16(o);
+        }
+    }
+    void* out_row = OUT == kOutF32
+                        ? static_cast<void*>(static_cast<float*>(c_kv) + crow * R)
+                        : static_cast<void*>(static_cast<__hip_bfloat16*>(c_kv) + crow * R);
+    rms_row<OUT>(base, nsplit, split_stride, gain, out_row, R, eps, red);
+}
+
+// ---- wkv_b split: row r of wkv_b [H, nope + v, R] goes to W_uk (j < nope) or W_uv.
+// One thread per 16-byte chunk; rows are whole chunks (R * element size % 16 == 0).
+__global__ void __launch_bounds__(256) split_rows_kernel(const v4u_t* __restrict__ src,
+                                                         v4u_t* __restrict__ dst_a,
+                                                         v4u_t* __restrict__ dst_b, int64_t rows,
+                                                         int rows_a, int rows_per_group,
+                                                         int chunks_per_row) {
+    const int64_t total = rows * chunks_per_row;
+    for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
+         idx += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = idx / chunks_per_row;
+        const int c = (int)(idx - r * chunks_per_row);
+        const int64_t h = r / rows_per_group;
+        const int j = (int)(r - h * rows_per_group);
+        const int rows_b = rows_per_group - rows_a;
+        v4u_t* dst = j < rows_a ? dst_a + ((h * rows_a + j) * chunks_per_row + c)
+                                : dst_b + ((h * rows_b + (j - rows_a)) * chunks_per_row + c);
+        *dst = src[idx];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, const void* gain,
@@ -236,6 +324,37 @@ hipError_t launch_stream_merge(float* ctx, float* run_max, float* run_sum, const
     if (rows <= 0) return hipSuccess;
     hipLaunchKernelGGL(stream_merge_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, ctx,
                        run_max, run_sum, ctx_c, max_c, sum_c, rows, R, first ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, const void* gain,
+                            const int64_t* positions, const float* inv_freq, void* c_kv,
+                            void* pe, OutType out_type, int B, int Sq, int R, int D,
+                            int start_row, int cache_rows, float eps, hipStream_t stream) {
+    const int64_t rows = (int64_t)B * Sq;
+    if (rows <= 0) return hipSuccess;
+    if (rows > 0x7fffffff) return hipErrorInvalidValue;
+    if (out_type == kOutF32)
+        hipLaunchKernelGGL(kv_append_kernel<kOutF32>, dim3((unsigned)rows), dim3(256), 0, stream,
+                           in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
+                           D, start_row, cache_rows, eps);
+    else
+        hipLaunchKernelGGL(kv_append_kernel<kOutBF16>, dim3((unsigned)rows), dim3(256), 0, stream,
+                           in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
+                           D, start_row, cache_rows, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_split_rows(const void* src, void* dst_a, void* dst_b, int64_t groups,
+                             int rows_a, int rows_b, int64_t row_bytes, hipStream_t stream) {
+    if (groups <= 0 || row_bytes % 16 != 0) return hipErrorInvalidValue;
+    const int chunks = (int)(row_bytes / 16);
+    const int64_t rows = groups * (rows_a + rows_b);
+    const int64_t total = rows * chunks;
+    const int blocks = (int)std::min<int64_t>((total + 255) / 256, 16 * kNumCUs);
+    hipLaunchKernelGGL(split_rows_kernel, dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const v4u_t*>(src), static_cast<v4u_t*>(dst_a),
+                       static_cast<v4u_t*>(dst_b), rows, rows_a, rows_a + rows_b, chunks);
     return hipGetLastError();
 }
 

@@ -16,7 +16,9 @@ What it restates (reference = pgangwar-ucsd/mla-cuda):
   (``mla_kernels.cu:971-1032, 1058-1079``), the unnormalised ctx of 3c
   (``:1101-1118``) and the deferred divide in 3d (``:1385-1415``);
 * one extension the reference does not have: a causal mask (key j visible to query i iff
-  j <= Sk - Sq + i), used by the chunked-prefill configuration.
+  j <= Sk - Sq + i), used by the chunked-prefill configuration;
+* the path's neighbours, which the reference names but does not implement: the KV-cache
+  append (``kv_append``) and the output projection (``o_proj``).
 
 Arithmetic runs in torch on the CPU, in float32 for float32/bfloat16/float16 inputs and in
 float64 for float64 inputs -- the reference's accumulate-dtype policy
@@ -317,6 +319,47 @@ def layer_by_steps(inp: Dict[str, torch.Tensor], dims: MLADims = DSV3,
     r["ctx"] = step_ctx(r["p"], r["alpha"], inp["c_kv"], B, Sq, H, tile)
     r["out"] = step_out(r["ctx"], r["row_sum"], W_uv, dt)
     return r
+
+
+# ---------------------------------------------------------------------------
+# Neighbours of the path (not in the reference's kernels)
+# ---------------------------------------------------------------------------
+
+
+def kv_append(x: torch.Tensor, W_kv_a: torch.Tensor, kv_norm_w: torch.Tensor,
+              positions: torch.Tensor, c_kv: torch.Tensor, pe_cache: torch.Tensor,
+              start_row: int, eps: float = RMS_NORM_EPS) -> Tuple[torch.Tensor, torch.Tensor]:
+    """KV-cache write of the absorbed layout.  The reference describes it without
+    implementing it (exhaustive_benchmark_suite.py:188-196): ``wkv_a`` maps x to
+    [c_kv, k_pe_raw] for the cache write, and pe_cache holds K_rope after RoPE.  The
+    algorithm is DeepSeek-V3's published one (deepseek-ai/DeepSeek-V3, inference/model.py,
+    MLA.forward, absorb branch; a third-party source the reference does not vendor, no
+    pinned version): kv = x @ wkv_a; kv_cache[:, start:end] = kv_norm(kv[..., :kv_rank]);
+    pe_cache[:, start:end] = rotary(kv[..., kv_rank:]) at the token positions.
+
+    Arithmetic follows this path's Q-side steps: the product in the acc dtype
+    (``step_gemm``), the norm of the acc-dtype latent with the gain applied before
+    narrowing (``step_norm``), and the interleaved-pair rotation of the acc-dtype rope
+    columns (``step_rope`` with one head).  Returns updated copies of the two caches."""
+    B, Sq, hidden = x.shape
+    R, D = c_kv.shape[-1], pe_cache.shape[-1]
+    dt = x.dtype
+    kv = step_gemm(x.reshape(B * Sq, hidden), W_kv_a)                    # [B*Sq, R + D]
+    lat = step_norm(kv[:, :R], kv_norm_w, eps, dt).reshape(B, Sq, R)
+    inv_freq = rope_inv_freq(D, acc_dtype(dt))
+    kpe = step_rope(kv, positions, inv_freq, B, Sq, 1, R, D, dt).reshape(B, Sq, D)
+    c2, p2 = c_kv.clone(), pe_cache.clone()
+    c2[:, start_row:start_row + Sq] = lat
+    p2[:, start_row:start_row + Sq] = kpe
+    return c2, p2
+
+
+def o_proj(attn: torch.Tensor, W_o: torch.Tensor) -> torch.Tensor:
+    """Output projection wo, the step after the layer's output [B, Sq, H, v] (named by the
+    reference's scope, not implemented there): [B*Sq, H*v] @ W_o [H*v, hidden] in the acc
+    dtype, narrowed to the input dtype."""
+    B, Sq, H, v = attn.shape
+    return step_gemm(attn.reshape(B * Sq, H * v), W_o).to(attn.dtype).reshape(B, Sq, -1)
 
 
 # ---------------------------------------------------------------------------

@@ -60,3 +60,36 @@ def layer(x, W_q_a, gain, W_q_b, wkv_b, c_kv, pe, positions, H, nope, rope, v,
                 for d in range(v):
                     out[b][s][h][d] = sum(ctx[r] * wkv_b[h][nope + d][r] for r in range(R))
     return out
+
+
+def kv_append(x, W_kv_a, gain, positions, R, eps=1e-6):
+    """New cache rows for x[b][s]: (c_kv_row [R], pe_row [D]) per (b, s), from the
+    mathematics: kv = x W_kv_a; c = kv[:R] / sqrt(mean(kv[:R]^2) + eps) * gain;
+    pe pair i of kv[R:] rotated by positions[s] / 10000^(2i/D)."""
+    B, Sq, hidden = len(x), len(x[0]), len(x[0][0])
+    N = len(W_kv_a[0])
+    D = N - R
+    rows = {}
+    for b in range(B):
+        for s in range(Sq):
+            kv = [sum(x[b][s][c] * W_kv_a[c][j] for c in range(hidden)) for j in range(N)]
+            lat = kv[:R]
+            inv = 1.0 / math.sqrt(sum(t * t for t in lat) / R + eps)
+            crow = [lat[j] * inv * gain[j] for j in range(R)]
+            ang = rope_angles(positions[s], D)
+            prow = [0.0] * D
+            for i in range(D // 2):
+                e, o = kv[R + 2 * i], kv[R + 2 * i + 1]
+                prow[2 * i] = e * math.cos(ang[i]) - o * math.sin(ang[i])
+                prow[2 * i + 1] = e * math.sin(ang[i]) + o * math.cos(ang[i])
+            rows[(b, s)] = (crow, prow)
+    return rows
+
+
+def o_proj(attn, W_o):
+    """out[b][s][n] = sum over (h, d) of attn[b][s][h][d] * W_o[h*v + d][n]."""
+    B, Sq, H, v = len(attn), len(attn[0]), len(attn[0][0]), len(attn[0][0][0])
+    N = len(W_o[0])
+    return [[[sum(attn[b][s][h][d] * W_o[h * v + d][n] for h in range(H) for d in range(v))
+              for n in range(N)] for s in range(Sq)] for b in range(B)]
+

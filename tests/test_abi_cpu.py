@@ -40,7 +40,8 @@ def lib():
     L.mla_version.restype = ctypes.c_char_p
     for n in ("mla_q_absorbed_workspace_bytes", "mla_attention_workspace_bytes",
               "mla_gemm_workspace_bytes", "mla_ctx_workspace_bytes", "mla_out_workspace_bytes",
-              "mla_attention_streaming_workspace_bytes"):
+              "mla_attention_streaming_workspace_bytes", "mla_kv_append_workspace_bytes",
+              "mla_o_proj_workspace_bytes"):
         getattr(L, n).restype = ctypes.c_size_t
     return L
 
@@ -190,6 +191,49 @@ def test_scores_validation(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "ld_scores" in _err(lib)
 
 
+def test_split_wkv_b_validation(lib):
+    d = dsv3()
+    st = lib.mla_split_wkv_b(F32, ctypes.byref(d), P16, P16, None, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "W_uv must not be NULL" in _err(lib)
+    d.v = 0
+    st = lib.mla_split_wkv_b(F32, ctypes.byref(d), P16, P16, P16, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "dims.v" in _err(lib)
+    d = dsv3()
+    d.kv_rank = 500
+    st = lib.mla_split_wkv_b(BF16, ctypes.byref(d), P16, P16, P16, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "multiple of 8 for bf16" in _err(lib)
+
+
+def test_kv_append_validation_and_workspace(lib):
+    d = dsv3(128, 1, 4989)
+    need = lib.mla_kv_append_workspace_bytes(F32, ctypes.byref(d))
+    assert need >= 128 * 576 * 4, "x @ W_kv_a lands in the workspace"
+    ptrs = [P16] * 5
+    st = lib.mla_kv_append(F32, ctypes.byref(d), *ptrs, ctypes.c_double(1e-6), 4989, 4989, P16,
+                           P16, P16, ctypes.c_size_t(need), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "start_row" in _err(lib)
+    st = lib.mla_kv_append(F32, ctypes.byref(d), *ptrs, ctypes.c_double(float("nan")), 0, 4989,
+                           P16, P16, P16, ctypes.c_size_t(need), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "eps" in _err(lib)
+    st = lib.mla_kv_append(F32, ctypes.byref(d), *ptrs, ctypes.c_double(1e-6), 4988, 4989, P16,
+                           P16, P16, ctypes.c_size_t(need - 1), None)
+    assert st == MLA_ERR_WORKSPACE
+    st = lib.mla_kv_append(F32, ctypes.byref(d), *ptrs, ctypes.c_double(1e-6), 4988, 4989, P16,
+                           None, P16, ctypes.c_size_t(need), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "pe_cache must not be NULL" in _err(lib)
+
+
+def test_o_proj_validation_and_workspace(lib):
+    d = dsv3(128, 1, 1)
+    need = lib.mla_o_proj_workspace_bytes(F32, ctypes.byref(d))
+    assert need > 0, "K = H*v = 16384 against 56 output tiles is split over K"
+    st = lib.mla_o_proj(F32, ctypes.byref(d), P16, P16, P16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_WORKSPACE
+    d.hidden = 7166
+    st = lib.mla_o_proj(F32, ctypes.byref(d), P16, P16, P16, P16, ctypes.c_size_t(need), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "dims.hidden" in _err(lib)
+
+
 # ------------------------------------------------------------------ torch binding
 
 
@@ -253,3 +297,24 @@ def test_binding_q_absorbed_shape_errors(ext):
         ext.q_absorbed(x, wa, g, wb, wuk, torch.zeros(2, dtype=torch.int64), 16, 8, 1e-6)
     with pytest.raises(RuntimeError, match="ROCm GPU device"):
         ext.q_absorbed(x, wa, g, wb, wuk, pos, 16, 8, 1e-6)
+
+
+def test_binding_neighbour_shape_errors(ext):
+    with pytest.raises(RuntimeError, match="nope_dim must lie"):
+        ext.split_wkv_b(torch.zeros(2, 8, 16), 8)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        ext.split_wkv_b(torch.zeros(2, 8, 16), 4)
+    x, W = torch.zeros(2, 1, 32), torch.zeros(32, 24)
+    g, pos = torch.zeros(16), torch.zeros(1, dtype=torch.int64)
+    ck, pe = torch.zeros(2, 5, 16), torch.zeros(2, 5, 8)
+    with pytest.raises(RuntimeError, match="W_kv_a must be"):
+        ext.kv_append(x, W[:, :20], g, pos, ck, pe, 0, 1e-6)
+    with pytest.raises(RuntimeError, match="kv_norm_w must be"):
+        ext.kv_append(x, W, g[:8], pos, ck, pe, 0, 1e-6)
+    with pytest.raises(RuntimeError, match="must be contiguous"):
+        ext.kv_append(x, W, g, pos, ck.transpose(1, 2).contiguous().transpose(1, 2), pe, 0, 1e-6)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        ext.kv_append(x, W, g, pos, ck, pe, 0, 1e-6)
+    with pytest.raises(RuntimeError, match="W_o must be"):
+        ext.o_proj(torch.zeros(2, 1, 4, 8), torch.zeros(30, 16))
+

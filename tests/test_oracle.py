@@ -271,3 +271,84 @@ def test_planted_combine_without_alpha_is_caught():
     ctx_bad = R.step_ctx(r["p"], torch.ones_like(r["alpha"]), inp["c_kv"], 1, 2, 2, tile=2)
     bad = R.step_out(ctx_bad, r["row_sum"], W_uv, torch.float64)
     assert (bad - _oracle(inp, dims, False)).abs().max().item() > 1e-6
+
+
+# --------------------------------------------------------------------------- neighbours
+
+
+def _kv_case(seed=11):
+    g = torch.Generator().manual_seed(seed)
+    B, Sq, hidden, Rk, D, rows, start = 2, 3, 6, 4, 4, 7, 2
+    x = torch.randn(B, Sq, hidden, generator=g, dtype=torch.float64)
+    W = torch.randn(hidden, Rk + D, generator=g, dtype=torch.float64) / math.sqrt(hidden)
+    gain = 1.0 + 0.1 * torch.randn(Rk, generator=g, dtype=torch.float64)
+    pos = torch.tensor([3, 40, 977])
+    c_kv = torch.randn(B, rows, Rk, generator=g, dtype=torch.float64)
+    pe = torch.randn(B, rows, D, generator=g, dtype=torch.float64)
+    return x, W, gain, pos, c_kv, pe, start
+
+
+def _kv_brute_check(c2, p2, x, W, gain, pos, c_kv, pe, start):
+    Rk = c_kv.shape[-1]
+    rows = brute_mla.kv_append(x.tolist(), W.tolist(), gain.tolist(), pos.tolist(), Rk)
+    err = 0.0
+    for (b, s), (crow, prow) in rows.items():
+        err = max(err, (c2[b, start + s] - torch.tensor(crow, dtype=torch.float64)).abs().max().item())
+        err = max(err, (p2[b, start + s] - torch.tensor(prow, dtype=torch.float64)).abs().max().item())
+    Sq = x.shape[1]
+    keep = [r for r in range(c_kv.shape[1]) if not start <= r < start + Sq]
+    err = max(err, (c2[:, keep] - c_kv[:, keep]).abs().max().item(),
+              (p2[:, keep] - pe[:, keep]).abs().max().item())
+    return err
+
+
+def test_kv_append_matches_brute_force():
+    x, W, gain, pos, c_kv, pe, start = _kv_case()
+    c2, p2 = R.kv_append(x, W, gain, pos, c_kv, pe, start, eps=1e-6)
+    assert _kv_brute_check(c2, p2, x, W, gain, pos, c_kv, pe, start) < 1e-12
+    # the written latent rows have unit RMS before the gain
+    lat = c2[:, start:start + 3] / gain
+    torch.testing.assert_close(lat.square().mean(-1), torch.ones(2, 3, dtype=torch.float64),
+                               rtol=1e-5, atol=1e-5)
+
+
+def _kvmut_no_gain(mp):
+    orig = R.step_norm
+    mp.setattr(R, "step_norm", lambda q, g, eps, dt: orig(q, torch.ones_like(g), eps, dt))
+
+
+def _kvmut_rope_sign(mp):
+    orig = R.step_rope
+    mp.setattr(R, "step_rope", lambda q, p, f, B, Sq, H, n, r, dt: orig(q, -p, f, B, Sq, H, n, r, dt))
+
+
+def _kvmut_swapped_split(mp):
+    # rope on the first columns and the norm on the rest: the split of kv read backwards
+    orig = R.step_gemm
+    mp.setattr(R, "step_gemm", lambda a, w: orig(a, torch.roll(w, shifts=4, dims=1)))
+
+
+KV_MUTANTS = {"no_gain": _kvmut_no_gain, "rope_sign": _kvmut_rope_sign,
+              "swapped_split": _kvmut_swapped_split}
+
+
+@pytest.mark.parametrize("name", sorted(KV_MUTANTS))
+def test_kv_append_planted_mistakes_are_caught(name, monkeypatch):
+    x, W, gain, pos, c_kv, pe, start = _kv_case(12)
+    KV_MUTANTS[name](monkeypatch)
+    c2, p2 = R.kv_append(x, W, gain, pos, c_kv, pe, start, eps=1e-6)
+    assert _kv_brute_check(c2, p2, x, W, gain, pos, c_kv, pe, start) > 1e-6
+
+
+def test_o_proj_matches_brute_force_and_identity():
+    g = torch.Generator().manual_seed(13)
+    attn = torch.randn(2, 3, 2, 3, generator=g, dtype=torch.float64)
+    W = torch.randn(6, 5, generator=g, dtype=torch.float64)
+    ref = torch.tensor(brute_mla.o_proj(attn.tolist(), W.tolist()), dtype=torch.float64)
+    torch.testing.assert_close(R.o_proj(attn, W), ref, rtol=1e-12, atol=1e-12)
+    # closed form: an identity W_o returns the heads flattened in (h, d) order
+    eye = torch.eye(6, dtype=torch.float64)
+    torch.testing.assert_close(R.o_proj(attn, eye), attn.reshape(2, 3, 6), rtol=0, atol=0)
+    # a transposed head/dim flattening is caught
+    bad = attn.permute(0, 1, 3, 2).reshape(2, 3, 6) @ W
+    assert (bad - ref).abs().max().item() > 1e-6
