@@ -436,6 +436,51 @@ int lds_bytes(int bm, int bn, bool nt, bool bf16) {
     return a + b;
 }
 
+// Measured-best plans for the GEMM shapes of the DeepSeek-V3 layer and its neighbours on
+// MI355X: a sweep of every tile x power-of-two split per shape, keeping the fastest (ties
+// within ~1% go to the model's choice).  Exact shape matches only; every other shape goes
+// through the time model below.  M = B*Sq for the Q path / wo / KV append, M = H for 3c.
+struct TunedPlan { int M, N, K, G; bool nt, bf16; int bm, bn, split; };
+constexpr TunedPlan kTuned[] = {
+    // B = 128 decode, fp32: 2a1, 2a2, 2c, 3d, wo, kv
+    {128, 1536, 7168, 1, false, false, 64, 64, 16},
+    {128, 24576, 1536, 1, false, false, 64, 64, 1},
+    {128, 512, 128, 128, false, false, 128, 128, 1},
+    {128, 128, 512, 128, true, false, 64, 64, 1},
+    {128, 7168, 16384, 1, false, false, 128, 32, 8},
+    {128, 576, 7168, 1, false, false, 64, 64, 8},
+    // B = 128 decode, bf16
+    {128, 1536, 7168, 1, false, true, 128, 64, 8},
+    {128, 24576, 1536, 1, false, true, 128, 96, 1},
+    {128, 512, 128, 128, false, true, 128, 128, 1},
+    {128, 128, 512, 128, true, true, 32, 128, 1},
+    {128, 7168, 16384, 1, false, true, 128, 128, 8},
+    {128, 576, 7168, 1, false, true, 64, 64, 8},
+    // B = 1, 8, 32 decode, fp32: 2a1, 2a2, 2c, 3d
+    {1, 1536, 7168, 1, false, false, 32, 128, 16},
+    {1, 24576, 1536, 1, false, false, 32, 128, 4},
+    {1, 512, 128, 128, false, false, 32, 128, 1},
+    {1, 128, 512, 128, true, false, 32, 128, 2},
+    {8, 1536, 7168, 1, false, false, 32, 128, 16},
+    {8, 24576, 1536, 1, false, false, 32, 128, 4},
+    {8, 512, 128, 128, false, false, 32, 128, 1},
+    {8, 128, 512, 128, true, false, 32, 128, 2},
+    {32, 1536, 7168, 1, false, false, 32, 128, 16},
+    {32, 24576, 1536, 1, false, false, 32, 128, 2},
+    {32, 512, 128, 128, false, false, 32, 128, 1},
+    {32, 128, 512, 128, true, false, 64, 64, 1},
+};
+
+bool tuned_plan(const GemmProblem& p, GemmPlan* out) {
+    for (const auto& t : kTuned)
+        if (t.M == p.M && t.N == p.N && t.K == p.K && t.G == p.G && t.nt == p.b_nt &&
+            t.bf16 == p.bf16) {
+            out->bm = t.bm; out->bn = t.bn; out->split = t.split;
+            return true;
+        }
+    return false;
+}
+
 bool tile_supported(int bm, int bn) {
     for (const auto& t : kTiles)
         if (t.bm == bm && t.bn == bn) return true;
@@ -477,7 +522,7 @@ GemmPlan plan_gemm(const GemmProblem& p) {
     const int kslices = cdiv(p.K, kBK);
     GemmPlan best;
     double best_t = 1e300;
-    if (!plan_override(p, &best)) {
+    if (!plan_override(p, &best) && !tuned_plan(p, &best)) {
         for (const auto& t : kTiles) {
             const int tm = cdiv(p.M, t.bm), tn = cdiv(p.N, t.bn);
             const int64_t tiles = (int64_t)tm * tn * p.G;
@@ -491,13 +536,18 @@ GemmPlan plan_gemm(const GemmProblem& p) {
                 // side; a lone workgroup per CU hides latency worse than two
                 const int64_t per_cu = (blocks + kNumCUs - 1) / kNumCUs;
                 const double hide = std::min<int64_t>(per_cu, occ) >= 2 ? 1.0 : 0.8;
+                // a workgroup's first slices and its epilogue are not overlapped with MFMA
+                // work: about four slices' worth of pipeline fill and drain
+                const double fill = per / (per + 4.0);
                 const double wg_flops = 2.0 * t.bm * t.bn * (double)per * kBK;
-                const double t_mfma = per_cu * wg_flops / (kCuRate * t.eff * hide);
+                const double t_mfma = per_cu * wg_flops / (kCuRate * t.eff * hide * fill);
+                // HBM reaches its sustained rate only with ~2 workgroups per CU streaming
+                const double conc = std::min(1.0, (double)blocks / (2.0 * kNumCUs));
                 // B operand streamed once per M tile (weights / cache), A once per N tile
                 // (small, mostly L2), C written once
                 const double bytes = eb * (double)p.K * p.N * p.G * std::min(tm, 2) +
                                      ea * (double)p.M * p.K * p.G + 4.0 * (double)p.M * p.N * p.G;
-                double tt = std::max(t_mfma, bytes / kHbm);
+                double tt = std::max(t_mfma, bytes / (kHbm * conc));
                 if (split > 1)
                     tt += 4.0 * (split + 1) * (double)p.M * p.N * p.G / kHbm + kReduceLaunch;
                 if (tt < best_t * 0.999) {
