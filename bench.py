@@ -311,6 +311,54 @@ def main():
                     "mbytes": round(by / 1e6, 2), "tflops": round(fl / t / 1e12, 2),
                     "gbps": round(by / t / 1e9, 1), "bound": "mfma" if mfma_bound else "hbm",
                     "frac": round(frac, 4)}
+    # attention alone over the same keys: dense, then through a shuffled pool of 64-key
+    # pages (full lengths: the dense work, plus the page-table indirection), then with
+    # ragged lengths U[1, Sk] (work is still that of the longest sequence: masked tiles
+    # are computed)
+    if not causal:
+        page = 64
+        mp = -(-Sk // page)
+        gp = torch.Generator().manual_seed(args.seed + 2)
+        perm = torch.randperm(B * mp, generator=gp)
+        pad = mp * page - Sk
+        def pool(t):
+            tp = torch.nn.functional.pad(t, (0, 0, 0, pad)).reshape(B * mp, page, t.shape[-1])
+            out_pool = torch.empty_like(tp)
+            out_pool[perm.to(dev)] = tp
+            return out_pool
+        ck_pool, pe_pool = pool(g["c_kv"]), pool(g["pe_cache"])
+        table = perm.reshape(B, mp).int().to(dev)
+        full = torch.full((B,), Sk, dtype=torch.int32, device=dev)
+        ragged = torch.randint(1, Sk + 1, (B,), generator=gp, dtype=torch.int32).to(dev)
+        qa_b, qr_b = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
+                                    g["positions"], dims.nope, dims.rope, eps)
+        fl_attn = work["3a"][0] + work["3c"][0] + work["3d"][0]
+        keys_ragged = int(ragged.sum().item())
+        att_calls = {
+            "attention_dense": (lambda: ext.mla_attention(qa_b, qr_b, g["c_kv"], g["pe_cache"],
+                                                          W_uv_d, scale), fl_attn),
+            "attention_paged": (lambda: ext.mla_attention_paged(
+                qa_b, qr_b, ck_pool, pe_pool, table, full, W_uv_d, scale), fl_attn),
+            "attention_paged_ragged": (lambda: ext.mla_attention_paged(
+                qa_b, qr_b, ck_pool, pe_pool, table, ragged, W_uv_d, scale),
+                fl_attn * keys_ragged / (B * Sk)),
+        }
+        for name, (fn, fl) in att_calls.items():
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) / args.steps * 1e-3
+            nb[name] = {"us": round(t * 1e6, 2), "gflop": round(fl / 1e9, 3),
+                        "tflops": round(fl / t / 1e12, 2), "bound": "mfma" if dname == "f32" else "hbm",
+                        "mfma_pct": round(100 * fl / t / peak_mfma, 1)}
+        nb["attention_paged_ragged"]["mean_keys"] = round(keys_ragged / B, 1)
+        del ck_pool, pe_pool
     print(f"[bench] neighbours: " + ", ".join(f"{k} {v['us']} µs" for k, v in nb.items()),
           file=sys.stderr, flush=True)
 

@@ -220,6 +220,47 @@ int mla_kv_append(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, cons
                   void* pe_cache, void* workspace, size_t workspace_bytes,
                   hipStream_t stream);
 
+/* ---- Ragged, paged KV cache (the reference has one dense [B, Sk, kv_rank] cache with one
+ * Sk for the whole batch and query positions shared by the batch, mla_kernels.cu:1489,
+ * 847-848, 449).  Keys live in a pool of pages:
+ *   c_kv_pages [num_pages, page_size, kv_rank], pe_pages [num_pages, page_size, rope]
+ *   block_table [B, max_pages] int32: sequence b's keys [j*page_size, (j+1)*page_size)
+ *               are page block_table[b*max_pages + j] of the pool
+ *   seq_lens    [B] int32: keys of sequence b, 1 <= seq_lens[b] <= max_pages*page_size
+ * page_size is a multiple of 64; dims->sk = max_pages * page_size (the table's key span).
+ * Both tables are device memory, read by the kernels (no host synchronisation). */
+
+/* mla_q_absorbed with per-sequence positions: positions [B, Sq] (int64, row b = sequence b's
+ * absolute query positions) instead of one [Sq] row shared by the batch.  Same workspace as
+ * mla_q_absorbed. */
+int mla_q_absorbed_ragged(mla_dtype_t dtype, const mla_dims_t* dims, const void* x,
+                          const void* W_q_a, const void* q_norm_w, const void* W_q_b,
+                          const void* W_uk, const int64_t* positions, const float* inv_freq,
+                          double eps, void* q_absorbed, void* q_rope, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream);
+
+/* Attention over the paged cache: sequence b attends to its first seq_lens[b] keys; with
+ * causal, key j is visible to query i iff j <= seq_lens[b] - Sq + i (seq_lens[b] >= Sq).
+ * Same queries, W_uv, scale and output as mla_attention. */
+size_t mla_attention_paged_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                           int causal, int32_t page_size);
+int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                        const void* q_rope, const void* c_kv_pages, const void* pe_pages,
+                        const int32_t* block_table, const int32_t* seq_lens, int32_t page_size,
+                        const void* W_uv, double scale, int causal, void* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
+/* KV-cache append into the paged cache: as mla_kv_append, but token (b, s) is written to
+ * logical slot positions[b*Sq + s] of sequence b (positions [B, Sq], int64): pool row
+ * block_table[b*max_pages + slot/page_size]*page_size + slot%page_size.  Slots outside
+ * [0, max_pages*page_size) are skipped.  Uses dims->batch, sq, hidden, kv_rank, rope, sk
+ * (= max_pages * page_size).  Same workspace as mla_kv_append. */
+int mla_kv_append_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* x,
+                        const void* W_kv_a, const void* kv_norm_w, const int64_t* positions,
+                        const float* inv_freq, double eps, const int32_t* block_table,
+                        int32_t page_size, void* c_kv_pages, void* pe_pages, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+
 /* Output projection wo: out [B*Sq, hidden] = attn [B*Sq, H*v] @ W_o [H*v, hidden], all in
  * dtype (fp32 accumulation).  attn is mla_attention's output [B, Sq, H, v]. */
 size_t mla_o_proj_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims);

@@ -8,7 +8,8 @@
 //
 // plus one op per step (gemm, rmsnorm, rope, absorb, scores, combine, ctx, out) that runs
 // the very kernels the fused calls run, and the path's neighbours: split_wkv_b (weight
-// prep), kv_append (the cache write) and o_proj (wo).  This file only validates tensors, allocates
+// prep), kv_append (the cache write) and o_proj (wo); mla_attention_paged and
+// kv_append_paged for a ragged, paged cache (q_absorbed takes [B, Sq] positions for it).  This file only validates tensors, allocates
 // outputs and workspace from torch's caching allocator and passes raw pointers and the
 // current HIP stream to the C ABI; all device work lives in libmla_amd.so.
 //
@@ -109,8 +110,11 @@ std::vector<torch::Tensor> op_q_absorbed(torch::Tensor x, torch::Tensor W_q_a, t
     TORCH_CHECK(W_uk.size(1) == nope_dim, "W_uk must be [H, nope, kv_rank]");
     TORCH_CHECK(q_norm_w.dim() == 1 && q_norm_w.size(0) == q_lora,
                 "q_norm_w must be a 1-D tensor of length q_lora (got ", q_norm_w.sizes(), ")");
-    TORCH_CHECK(positions.dim() == 1 && positions.size(0) == Sq,
-                "positions must be a 1-D tensor of length Sq (got ", positions.sizes(), ")");
+    const bool per_seq = positions.dim() == 2;
+    TORCH_CHECK((positions.dim() == 1 && positions.size(0) == Sq) ||
+                    (per_seq && positions.size(0) == B && positions.size(1) == Sq),
+                "positions must be [Sq] (shared by the batch) or [B, Sq] (per sequence) (got ",
+                positions.sizes(), ")");
     TORCH_CHECK(!positions.is_floating_point() && !positions.is_complex(),
                 "positions must be an integer tensor");
     const mla_dtype_t dt = to_mla_dtype(x, "x");
@@ -138,10 +142,10 @@ std::vector<torch::Tensor> op_q_absorbed(torch::Tensor x, torch::Tensor W_q_a, t
     auto qr = torch::empty({B, Sq, H, rope_dim}, x.options());
     const size_t wsb = mla_q_absorbed_workspace_bytes(dt, &d);
     auto ws = workspace(wsb, x);
-    check_status(mla_q_absorbed(dt, &d, xc.data_ptr(), wa.data_ptr(), g.data_ptr(), wb.data_ptr(),
-                                wuk.data_ptr(), pos.data_ptr<int64_t>(),
-                                inv_freq.data_ptr<float>(), eps, qa.data_ptr(), qr.data_ptr(),
-                                ws.data_ptr(), wsb, current_stream()),
+    auto q_fn = per_seq ? mla_q_absorbed_ragged : mla_q_absorbed;
+    check_status(q_fn(dt, &d, xc.data_ptr(), wa.data_ptr(), g.data_ptr(), wb.data_ptr(),
+                      wuk.data_ptr(), pos.data_ptr<int64_t>(), inv_freq.data_ptr<float>(), eps,
+                      qa.data_ptr(), qr.data_ptr(), ws.data_ptr(), wsb, current_stream()),
                  "q_absorbed");
     return {qa, qr};
 }
@@ -426,6 +430,140 @@ torch::Tensor step_out(torch::Tensor ctx, torch::Tensor row_sum, torch::Tensor W
     return out;
 }
 
+// ------------------------------------------------------------------ ragged, paged cache
+
+// Shapes of a paged call: q [B, Sq, H, ·], pools [pages, page_size, ·], block_table
+// [B, max_pages] int32, seq_lens [B] int32.
+mla_dims_t paged_dims(const torch::Tensor& qa, const torch::Tensor& qr, const torch::Tensor& ckv,
+                      const torch::Tensor& pe, const torch::Tensor& table,
+                      const torch::Tensor* seq_lens, const torch::Tensor* W_uv, int64_t* page) {
+    check_dim(qa, 4, "q_absorbed", "[B, Sq, H, kv_rank]");
+    check_dim(qr, 4, "q_rope", "[B, Sq, H, rope]");
+    check_dim(ckv, 3, "c_kv_pages", "[num_pages, page_size, kv_rank]");
+    check_dim(pe, 3, "pe_pages", "[num_pages, page_size, rope]");
+    check_dim(table, 2, "block_table", "[B, max_pages]");
+    const int64_t B = qa.size(0), Sq = qa.size(1), H = qa.size(2), R = qa.size(3);
+    const int64_t D = qr.size(3);
+    TORCH_CHECK(qr.size(0) == B && qr.size(1) == Sq && qr.size(2) == H,
+                "q_rope must be [B, Sq, H, rope] matching q_absorbed (got ", qr.sizes(), ")");
+    TORCH_CHECK(ckv.size(2) == R, "c_kv_pages must be [num_pages, page_size, kv_rank] (got ",
+                ckv.sizes(), ")");
+    TORCH_CHECK(pe.size(0) == ckv.size(0) && pe.size(1) == ckv.size(1) && pe.size(2) == D,
+                "pe_pages must be [num_pages, page_size, rope] matching c_kv_pages (got ",
+                pe.sizes(), ")");
+    TORCH_CHECK(table.size(0) == B, "block_table must be [B, max_pages] (got ", table.sizes(), ")");
+    TORCH_CHECK(table.scalar_type() == torch::kInt32, "block_table must be int32");
+    if (seq_lens) {
+        TORCH_CHECK(seq_lens->dim() == 1 && seq_lens->size(0) == B,
+                    "seq_lens must be a 1-D tensor of length B (got ", seq_lens->sizes(), ")");
+        TORCH_CHECK(seq_lens->scalar_type() == torch::kInt32, "seq_lens must be int32");
+    }
+    *page = ckv.size(1);
+    mla_dims_t d{};
+    d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.heads = (int32_t)H;
+    d.kv_rank = (int32_t)R; d.rope = (int32_t)D;
+    TORCH_CHECK(table.size(1) * *page < INT32_MAX, "MLA: block_table spans too many keys");
+    d.sk = (int32_t)(table.size(1) * *page);
+    if (W_uv) {
+        check_dim(*W_uv, 3, "W_uv", "[H, v, kv_rank]");
+        TORCH_CHECK(W_uv->size(0) == H && W_uv->size(2) == R,
+                    "W_uv must be [H, v, kv_rank] (got ", W_uv->sizes(), ")");
+        d.v = (int32_t)W_uv->size(1);
+    }
+    return d;
+}
+
+// Attention over a paged, ragged cache: sequence b attends to its first seq_lens[b] keys,
+// found through its row of block_table.
+torch::Tensor op_mla_attention_paged(torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                     torch::Tensor c_kv_pages, torch::Tensor pe_pages,
+                                     torch::Tensor block_table, torch::Tensor seq_lens,
+                                     torch::Tensor W_uv, double scale, bool causal) {
+    int64_t page = 0;
+    mla_dims_t d = paged_dims(q_absorbed, q_rope, c_kv_pages, pe_pages, block_table, &seq_lens,
+                              &W_uv, &page);
+    const mla_dtype_t dt = to_mla_dtype(q_absorbed, "q_absorbed");
+    check_same_dtype(q_absorbed, q_rope, "q_rope");
+    check_same_dtype(q_absorbed, c_kv_pages, "c_kv_pages");
+    check_same_dtype(q_absorbed, pe_pages, "pe_pages");
+    check_same_dtype(q_absorbed, W_uv, "W_uv");
+    check_device({&q_absorbed, &q_rope, &c_kv_pages, &pe_pages, &block_table, &seq_lens, &W_uv});
+
+    c10::DeviceGuard guard(q_absorbed.device());
+    auto qa = q_absorbed.contiguous();
+    auto qr = q_rope.contiguous();
+    auto ck = c_kv_pages.contiguous();
+    auto pe = pe_pages.contiguous();
+    auto tab = block_table.contiguous();
+    auto lens = seq_lens.contiguous();
+    auto wuv = W_uv.contiguous();
+    auto out = torch::empty({d.batch, d.sq, d.heads, d.v}, qa.options());
+    const size_t wsb = mla_attention_paged_workspace_bytes(dt, &d, causal ? 1 : 0, (int32_t)page);
+    auto ws = workspace(wsb, qa);
+    check_status(mla_attention_paged(dt, &d, qa.data_ptr(), qr.data_ptr(), ck.data_ptr(),
+                                     pe.data_ptr(), tab.data_ptr<int32_t>(),
+                                     lens.data_ptr<int32_t>(), (int32_t)page, wuv.data_ptr(),
+                                     scale, causal ? 1 : 0, out.data_ptr(), ws.data_ptr(), wsb,
+                                     current_stream()),
+                 "mla_attention_paged");
+    return out;
+}
+
+// KV-cache append into the paged cache: token (b, s) goes to slot positions[b, s] of
+// sequence b (pool row through block_table).
+void op_kv_append_paged(torch::Tensor x, torch::Tensor W_kv_a, torch::Tensor kv_norm_w,
+                        torch::Tensor positions, torch::Tensor block_table,
+                        torch::Tensor c_kv_pages, torch::Tensor pe_pages, double eps) {
+    check_dim(x, 3, "x", "[B, Sq, hidden]");
+    check_dim(W_kv_a, 2, "W_kv_a", "[hidden, kv_rank + rope]");
+    check_dim(c_kv_pages, 3, "c_kv_pages", "[num_pages, page_size, kv_rank]");
+    check_dim(pe_pages, 3, "pe_pages", "[num_pages, page_size, rope]");
+    check_dim(block_table, 2, "block_table", "[B, max_pages]");
+    const int64_t B = x.size(0), Sq = x.size(1), hidden = x.size(2);
+    const int64_t page = c_kv_pages.size(1), R = c_kv_pages.size(2), D = pe_pages.size(2);
+    TORCH_CHECK(W_kv_a.size(0) == hidden && W_kv_a.size(1) == R + D,
+                "W_kv_a must be [hidden, kv_rank + rope] (got ", W_kv_a.sizes(), ")");
+    TORCH_CHECK(pe_pages.size(0) == c_kv_pages.size(0) && pe_pages.size(1) == page,
+                "pe_pages must be [num_pages, page_size, rope] matching c_kv_pages");
+    TORCH_CHECK(block_table.size(0) == B && block_table.scalar_type() == torch::kInt32,
+                "block_table must be an int32 [B, max_pages] tensor");
+    TORCH_CHECK(kv_norm_w.dim() == 1 && kv_norm_w.size(0) == R,
+                "kv_norm_w must be a 1-D tensor of length kv_rank (got ", kv_norm_w.sizes(), ")");
+    TORCH_CHECK(positions.dim() == 2 && positions.size(0) == B && positions.size(1) == Sq,
+                "positions must be [B, Sq] (got ", positions.sizes(), ")");
+    TORCH_CHECK(!positions.is_floating_point() && !positions.is_complex(),
+                "positions must be an integer tensor");
+    TORCH_CHECK(D > 0 && D % 2 == 0, "MLA: the rope width must be positive and even");
+    TORCH_CHECK(c_kv_pages.is_contiguous() && pe_pages.is_contiguous(),
+                "MLA: c_kv_pages and pe_pages are updated in place and must be contiguous");
+    const mla_dtype_t dt = to_mla_dtype(x, "x");
+    check_same_dtype(x, W_kv_a, "W_kv_a");
+    check_same_dtype(x, kv_norm_w, "kv_norm_w");
+    check_same_dtype(x, c_kv_pages, "c_kv_pages");
+    check_same_dtype(x, pe_pages, "pe_pages");
+    check_device({&x, &W_kv_a, &kv_norm_w, &positions, &block_table, &c_kv_pages, &pe_pages});
+
+    c10::DeviceGuard guard(x.device());
+    auto xc = x.contiguous();
+    auto wa = W_kv_a.contiguous();
+    auto g = kv_norm_w.contiguous();
+    auto pos = positions.to(torch::kLong).contiguous();
+    auto tab = block_table.contiguous();
+    auto inv_freq = device_inv_freq(D, x.device());
+    mla_dims_t d{};
+    d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.hidden = (int32_t)hidden;
+    d.kv_rank = (int32_t)R; d.rope = (int32_t)D;
+    TORCH_CHECK(block_table.size(1) * page < INT32_MAX, "MLA: block_table spans too many keys");
+    d.sk = (int32_t)(block_table.size(1) * page);
+    const size_t wsb = mla_kv_append_workspace_bytes(dt, &d);
+    auto ws = workspace(wsb, x);
+    check_status(mla_kv_append_paged(dt, &d, xc.data_ptr(), wa.data_ptr(), g.data_ptr(),
+                                     pos.data_ptr<int64_t>(), inv_freq.data_ptr<float>(), eps,
+                                     tab.data_ptr<int32_t>(), (int32_t)page, c_kv_pages.data_ptr(),
+                                     pe_pages.data_ptr(), ws.data_ptr(), wsb, current_stream()),
+                 "kv_append_paged");
+}
+
 // ------------------------------------------------------------------ neighbours of the path
 
 // Weight prep once at load: the W_uk / W_uv halves of wkv_b as contiguous tensors.
@@ -568,4 +706,13 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("c_kv"), py::arg("pe_cache"), py::arg("start_row"), py::arg("eps"));
     m.def("o_proj", &op_o_proj, "Output projection: [B, Sq, H, v] @ W_o [H*v, hidden]",
           py::arg("attn"), py::arg("W_o"));
+    m.def("mla_attention_paged", &op_mla_attention_paged,
+          "Attention over a paged, ragged KV cache: returns out [B, Sq, H, v]",
+          py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv_pages"), py::arg("pe_pages"),
+          py::arg("block_table"), py::arg("seq_lens"), py::arg("W_uv"), py::arg("scale"),
+          py::arg("causal") = false);
+    m.def("kv_append_paged", &op_kv_append_paged,
+          "KV-cache append into a paged cache: token (b, s) to slot positions[b, s]",
+          py::arg("x"), py::arg("W_kv_a"), py::arg("kv_norm_w"), py::arg("positions"),
+          py::arg("block_table"), py::arg("c_kv_pages"), py::arg("pe_pages"), py::arg("eps"));
 }

@@ -365,7 +365,8 @@ template <typename T> T* at(void* base, size_t off) {
 int run_scores(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* qr, const void* ckv,
                const void* pe, double scale, int causal, float* p, int ld_p, float* m_part,
                float* l_part, hipStream_t stream, int64_t key_stride = 0, int key_offset = 0,
-               int sk_total = 0) {
+               int sk_total = 0, const int* seq_lens = nullptr, const int* block_table = nullptr,
+               int page_size = 0) {
     ScoresProblem sp;
     sp.qa = qa; sp.qr = qr; sp.ckv = ckv; sp.pe = pe;
     sp.bf16 = is_bf16(dt);
@@ -375,6 +376,8 @@ int run_scores(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* 
     sp.inv_scale = 1.0f / (float)scale;
     sp.causal = causal != 0;
     sp.key_stride = key_stride; sp.key_offset = key_offset; sp.sk_total = sk_total;
+    sp.seq_lens = seq_lens; sp.block_table = block_table; sp.page_size = page_size;
+    sp.max_pages = page_size > 0 ? d->sk / page_size : 0;
     MLA_TRY_HIP(launch_scores(sp, stream), "scores kernel launch");
     return MLA_OK;
 }
@@ -459,6 +462,129 @@ size_t kv_ws_bytes(mla_dtype_t dt, const mla_dims_t* d, GemmPlan* plan_out) {
     if (plan_out) *plan_out = plan;
     return align_up((size_t)std::max(1, plan.split) * d->batch * d->sq *
                     (size_t)(d->kv_rank + d->rope) * sizeof(float));
+}
+
+int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_q_a,
+                   const void* q_norm_w, const void* W_q_b, const void* W_uk,
+                   const int64_t* positions, const float* inv_freq, double eps,
+                   void* q_absorbed, void* q_rope, void* workspace, size_t workspace_bytes,
+                   hipStream_t stream, bool pos_per_batch) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_q_dims(dtype, dims));
+    MLA_CHECK(check_ptr(x, "x"));
+    MLA_CHECK(check_ptr(W_q_a, "W_q_a"));
+    MLA_CHECK(check_ptr(q_norm_w, "q_norm_w"));
+    MLA_CHECK(check_ptr(W_q_b, "W_q_b"));
+    MLA_CHECK(check_ptr(W_uk, "W_uk"));
+    MLA_CHECK(check_ptr(positions, "positions"));
+    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    const QLayout L = q_layout(dtype, dims);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+
+    const int bq = dims->batch * dims->sq;
+    float* lat_acc = at<float>(workspace, L.off_lat_acc);
+    void* lat = at<void>(workspace, L.off_lat);  // storage dtype
+    float* raw = at<float>(workspace, L.off_raw);
+
+    // 2a1: split-K partials land in lat_acc[split][bq][q_lora]; 2a-n sums them.
+    GemmProblem down = q_down_problem(dtype, dims, x, W_q_a, lat_acc);
+    GemmPlan down_plan = L.down;
+    int nsplit = 1;
+    if (down_plan.split > 1) {
+        nsplit = down_plan.split;
+        down_plan.workspace_bytes = 0;
+        MLA_TRY_HIP(launch_gemm_partials(down, down_plan, lat_acc, stream), "2a1 launch");
+    } else {
+        MLA_TRY_HIP(launch_gemm(down, down_plan, nullptr, stream), "2a1 launch");
+    }
+    // 2a-n
+    MLA_TRY_HIP(launch_rmsnorm(lat_acc, nsplit, (int64_t)bq * dims->q_lora, q_norm_w, lat,
+                               storage_out(dtype), bq, dims->q_lora, (float)eps, stream),
+                "2a-n launch");
+    // 2a2
+    GemmProblem up = q_up_problem(dtype, dims, lat, W_q_b, raw);
+    MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
+    // 2b
+    MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch, dims->sq,
+                            dims->heads, dims->nope, dims->rope, stream, pos_per_batch),
+                "2b launch");
+    // 2c
+    GemmProblem ab = absorb_problem(dtype, dims, raw, W_uk, q_absorbed);
+    MLA_TRY_HIP(launch_gemm(ab, L.absorb, at<void>(workspace, L.off_abs_ws), stream),
+                "2c launch");
+    return ok();
+}
+
+// Paged cache: page_size a positive multiple of 64 that divides dims->sk (the table span).
+int check_pages(const mla_dims_t* d, int32_t page_size) {
+    if (page_size <= 0 || page_size % 64 != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "page_size must be a positive multiple of 64 (got %d)",
+                    page_size);
+    if (d->sk <= 0 || d->sk % page_size != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "dims.sk must be max_pages * page_size, a positive multiple of page_size "
+                    "(got sk=%d, page_size=%d)", d->sk, page_size);
+    return MLA_OK;
+}
+
+// KV append: x @ W_kv_a into the workspace, then the fused norm / RoPE / scatter kernel.
+// Dense: rows start_row + s of a [B, cache_rows] cache.  Paged (block_table): the rows of
+// slots positions[b*Sq + s] through the table.
+int kv_append_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_kv_a,
+                   const void* kv_norm_w, const int64_t* positions, const float* inv_freq,
+                   double eps, int32_t start_row, int32_t cache_rows, const int32_t* block_table,
+                   int32_t page_size, void* c_kv, void* pe_cache, void* workspace,
+                   size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_kv_dims(dtype, dims));
+    MLA_CHECK(check_ptr(x, "x"));
+    MLA_CHECK(check_ptr(W_kv_a, "W_kv_a"));
+    MLA_CHECK(check_ptr(kv_norm_w, "kv_norm_w"));
+    MLA_CHECK(check_ptr(positions, "positions"));
+    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
+    MLA_CHECK(check_ptr(c_kv, block_table ? "c_kv_pages" : "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, block_table ? "pe_pages" : "pe_cache"));
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    int max_pages = 0;
+    if (block_table) {
+        MLA_CHECK(check_pages(dims, page_size));
+        max_pages = dims->sk / page_size;
+    } else {
+        if (cache_rows <= 0 || start_row < 0 || (int64_t)start_row + dims->sq > cache_rows)
+            return fail(MLA_ERR_INVALID_ARGUMENT,
+                        "cache rows [start_row, start_row + sq) = [%d, %lld) must lie in [0, %d)",
+                        start_row, (long long)start_row + dims->sq, cache_rows);
+        if ((int64_t)dims->batch * cache_rows * (int64_t)dims->kv_rank > ((int64_t)1 << 40))
+            return fail(MLA_ERR_INVALID_ARGUMENT, "cache too large");
+    }
+    GemmPlan plan;
+    const size_t need = kv_ws_bytes(dtype, dims, &plan);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, need));
+
+    const int bq = dims->batch * dims->sq;
+    const int n = dims->kv_rank + dims->rope;
+    float* acc = at<float>(workspace, 0);
+    GemmProblem gp = kv_problem(dtype, dims, x, W_kv_a, acc);
+    int nsplit = 1;
+    if (plan.split > 1) {
+        nsplit = plan.split;
+        plan.workspace_bytes = 0;
+        MLA_TRY_HIP(launch_gemm_partials(gp, plan, acc, stream), "kv GEMM launch");
+    } else {
+        MLA_TRY_HIP(launch_gemm(gp, plan, nullptr, stream), "kv GEMM launch");
+    }
+    MLA_TRY_HIP(launch_kv_append(acc, nsplit, (int64_t)bq * n, kv_norm_w, positions, inv_freq,
+                                 c_kv, pe_cache, storage_out(dtype), dims->batch, dims->sq,
+                                 dims->kv_rank, dims->rope, start_row, cache_rows, (float)eps,
+                                 stream, block_table != nullptr, block_table, page_size,
+                                 max_pages),
+                "kv append launch");
+    return ok();
 }
 
 }  // namespace
@@ -641,54 +767,17 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, con
                    const int64_t* positions, const float* inv_freq, double eps,
                    void* q_absorbed, void* q_rope, void* workspace, size_t workspace_bytes,
                    hipStream_t stream) {
-    MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_q_dims(dtype, dims));
-    MLA_CHECK(check_ptr(x, "x"));
-    MLA_CHECK(check_ptr(W_q_a, "W_q_a"));
-    MLA_CHECK(check_ptr(q_norm_w, "q_norm_w"));
-    MLA_CHECK(check_ptr(W_q_b, "W_q_b"));
-    MLA_CHECK(check_ptr(W_uk, "W_uk"));
-    MLA_CHECK(check_ptr(positions, "positions"));
-    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
-    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
-    MLA_CHECK(check_ptr(q_rope, "q_rope"));
-    if (!(eps >= 0.0) || !std::isfinite(eps))
-        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
-    const QLayout L = q_layout(dtype, dims);
-    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+    return q_absorbed_impl(dtype, dims, x, W_q_a, q_norm_w, W_q_b, W_uk, positions, inv_freq, eps,
+                           q_absorbed, q_rope, workspace, workspace_bytes, stream, false);
+}
 
-    const int bq = dims->batch * dims->sq;
-    float* lat_acc = at<float>(workspace, L.off_lat_acc);
-    void* lat = at<void>(workspace, L.off_lat);  // storage dtype
-    float* raw = at<float>(workspace, L.off_raw);
-
-    // 2a1: split-K partials land in lat_acc[split][bq][q_lora]; 2a-n sums them.
-    GemmProblem down = q_down_problem(dtype, dims, x, W_q_a, lat_acc);
-    GemmPlan down_plan = L.down;
-    int nsplit = 1;
-    if (down_plan.split > 1) {
-        nsplit = down_plan.split;
-        down_plan.workspace_bytes = 0;
-        MLA_TRY_HIP(launch_gemm_partials(down, down_plan, lat_acc, stream), "2a1 launch");
-    } else {
-        MLA_TRY_HIP(launch_gemm(down, down_plan, nullptr, stream), "2a1 launch");
-    }
-    // 2a-n
-    MLA_TRY_HIP(launch_rmsnorm(lat_acc, nsplit, (int64_t)bq * dims->q_lora, q_norm_w, lat,
-                               storage_out(dtype), bq, dims->q_lora, (float)eps, stream),
-                "2a-n launch");
-    // 2a2
-    GemmProblem up = q_up_problem(dtype, dims, lat, W_q_b, raw);
-    MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
-    // 2b
-    MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch, dims->sq,
-                            dims->heads, dims->nope, dims->rope, stream),
-                "2b launch");
-    // 2c
-    GemmProblem ab = absorb_problem(dtype, dims, raw, W_uk, q_absorbed);
-    MLA_TRY_HIP(launch_gemm(ab, L.absorb, at<void>(workspace, L.off_abs_ws), stream),
-                "2c launch");
-    return ok();
+int mla_q_absorbed_ragged(mla_dtype_t dtype, const mla_dims_t* dims, const void* x,
+                          const void* W_q_a, const void* q_norm_w, const void* W_q_b,
+                          const void* W_uk, const int64_t* positions, const float* inv_freq,
+                          double eps, void* q_absorbed, void* q_rope, void* workspace,
+                          size_t workspace_bytes, hipStream_t stream) {
+    return q_absorbed_impl(dtype, dims, x, W_q_a, q_norm_w, W_q_b, W_uk, positions, inv_freq, eps,
+                           q_absorbed, q_rope, workspace, workspace_bytes, stream, true);
 }
 
 size_t mla_attention_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal) {
@@ -827,44 +916,72 @@ int mla_kv_append(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, cons
                   const void* kv_norm_w, const int64_t* positions, const float* inv_freq,
                   double eps, int32_t start_row, int32_t cache_rows, void* c_kv, void* pe_cache,
                   void* workspace, size_t workspace_bytes, hipStream_t stream) {
-    MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_kv_dims(dtype, dims));
-    MLA_CHECK(check_ptr(x, "x"));
-    MLA_CHECK(check_ptr(W_kv_a, "W_kv_a"));
-    MLA_CHECK(check_ptr(kv_norm_w, "kv_norm_w"));
-    MLA_CHECK(check_ptr(positions, "positions"));
-    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
-    MLA_CHECK(check_ptr(c_kv, "c_kv"));
-    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
-    if (!(eps >= 0.0) || !std::isfinite(eps))
-        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
-    if (cache_rows <= 0 || start_row < 0 || (int64_t)start_row + dims->sq > cache_rows)
-        return fail(MLA_ERR_INVALID_ARGUMENT,
-                    "cache rows [start_row, start_row + sq) = [%d, %lld) must lie in [0, %d)",
-                    start_row, (long long)start_row + dims->sq, cache_rows);
-    if ((int64_t)dims->batch * cache_rows * (int64_t)dims->kv_rank > ((int64_t)1 << 40))
-        return fail(MLA_ERR_INVALID_ARGUMENT, "cache too large");
-    GemmPlan plan;
-    const size_t need = kv_ws_bytes(dtype, dims, &plan);
-    MLA_CHECK(check_ws(workspace, workspace_bytes, need));
+    return kv_append_impl(dtype, dims, x, W_kv_a, kv_norm_w, positions, inv_freq, eps, start_row,
+                          cache_rows, nullptr, 0, c_kv, pe_cache, workspace, workspace_bytes,
+                          stream);
+}
 
-    const int bq = dims->batch * dims->sq;
-    const int n = dims->kv_rank + dims->rope;
-    float* acc = at<float>(workspace, 0);
-    GemmProblem gp = kv_problem(dtype, dims, x, W_kv_a, acc);
-    int nsplit = 1;
-    if (plan.split > 1) {
-        nsplit = plan.split;
-        plan.workspace_bytes = 0;
-        MLA_TRY_HIP(launch_gemm_partials(gp, plan, acc, stream), "kv GEMM launch");
-    } else {
-        MLA_TRY_HIP(launch_gemm(gp, plan, nullptr, stream), "kv GEMM launch");
-    }
-    MLA_TRY_HIP(launch_kv_append(acc, nsplit, (int64_t)bq * n, kv_norm_w, positions, inv_freq,
-                                 c_kv, pe_cache, storage_out(dtype), dims->batch, dims->sq,
-                                 dims->kv_rank, dims->rope, start_row, cache_rows, (float)eps,
-                                 stream),
-                "kv append launch");
+int mla_kv_append_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* x,
+                        const void* W_kv_a, const void* kv_norm_w, const int64_t* positions,
+                        const float* inv_freq, double eps, const int32_t* block_table,
+                        int32_t page_size, void* c_kv_pages, void* pe_pages, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_ptr(block_table, "block_table"));
+    return kv_append_impl(dtype, dims, x, W_kv_a, kv_norm_w, positions, inv_freq, eps, 0, 0,
+                          block_table, page_size, c_kv_pages, pe_pages, workspace,
+                          workspace_bytes, stream);
+}
+
+size_t mla_attention_paged_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                           int causal, int32_t page_size) {
+    if (!dims || check_dtype(dtype) != MLA_OK || check_attn_dims(dtype, dims, causal) != MLA_OK ||
+        check_pages(dims, page_size) != MLA_OK)
+        return 0;
+    return attn_layout(dtype, dims).total;
+}
+
+int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                        const void* q_rope, const void* c_kv_pages, const void* pe_pages,
+                        const int32_t* block_table, const int32_t* seq_lens, int32_t page_size,
+                        const void* W_uv, double scale, int causal, void* out, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    MLA_CHECK(check_pages(dims, page_size));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv_pages, "c_kv_pages"));
+    MLA_CHECK(check_ptr(pe_pages, "pe_pages"));
+    MLA_CHECK(check_ptr(block_table, "block_table"));
+    MLA_CHECK(check_ptr(seq_lens, "seq_lens"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const AttnLayout L = attn_layout(dtype, dims);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+
+    float* p = at<float>(workspace, L.off_p);
+    float* m = at<float>(workspace, L.off_m);
+    float* l = at<float>(workspace, L.off_l);
+    float* alpha = at<float>(workspace, L.off_alpha);
+    float* row_sum = at<float>(workspace, L.off_rowsum);
+    float* ctx = at<float>(workspace, L.off_ctx);
+    const int rows = dims->batch * dims->sq * dims->heads;
+
+    // 3a over the pages, each sequence to its own length (keys past it score as masked)
+    MLA_CHECK(run_scores(dtype, dims, q_absorbed, q_rope, c_kv_pages, pe_pages, scale, causal, p,
+                         L.ld_p, m, l, stream, 0, 0, 0, seq_lens, block_table, page_size));
+    // 3b: a tile past a sequence's keys has m = -inf, l = 0 and gets alpha 0
+    MLA_TRY_HIP(launch_combine(m, l, alpha, row_sum, nullptr, rows, L.P, stream), "3b launch");
+    // 3c: K rows through the block table, K limited to each sequence's length
+    GemmProblem cp = ctx_problem(dtype, dims, p, L.ld_p, alpha, c_kv_pages, ctx);
+    cp.sBg = 0;
+    cp.k_len = seq_lens;
+    cp.b_pages = block_table; cp.page_size = page_size; cp.max_pages = dims->sk / page_size;
+    MLA_TRY_HIP(launch_gemm(cp, L.ctx, at<void>(workspace, L.off_ctx_ws), stream), "3c launch");
+    // 3d
+    GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
+    MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
     return ok();
 }
 

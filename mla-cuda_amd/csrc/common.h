@@ -76,6 +76,14 @@ __device__ __forceinline__ float wave_reduce(float v, Op op) {
     return op(lo, hi);
 }
 
+// A wave-uniform read of kernel-lifetime read-only data (sequence lengths, page tables):
+// through the constant address space it is an s_load into SGPRs, so waiting for it does
+// not drain the vector-memory queue the staging pipeline keeps full.
+__device__ __forceinline__ int load_uniform(const int* p) {
+    typedef const __attribute__((address_space(4))) int ConstInt;
+    return *(ConstInt*)p;
+}
+
 // ----------------------------------------------------------------------------------
 // XCD-aware block order.  The dispatcher hands workgroup b to XCD b % 8; this maps the
 // hardware id to a logical tile id so that each XCD walks a CONTIGUOUS run of logical

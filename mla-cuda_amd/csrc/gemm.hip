@@ -47,6 +47,8 @@ struct GemmArgs {
     int split, k_chunk, tiles_m, tiles_n;
     const float* rs; int64_t rs_m, rs_g;
     const float* alpha; int alpha_ld, alpha_shift;   // alpha column of k: k >> alpha_shift
+    const int* k_len;                                  // per-group K limit (optional)
+    const int* b_pages; int page_size, max_pages;      // paged NN B (PAGED kernels)
 };
 
 template <typename TL, int BN>
@@ -61,7 +63,11 @@ constexpr int nn_row_words() {
 // 2 -- one slice of MFMA work (~4K cycles per wave in fp32, 8x less in bf16) does not
 // cover the HBM latency of a long-K stream such as 3c's scores x c_kv; with two slices in
 // flight 3c runs at ~83% of the fp32 MFMA peak instead of ~78%.
-template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
+// PAGED: the NN B operand is a paged row pool -- K row k of group g is row
+// b_pages[g*max_pages + k/page_size]*page_size + k%page_size (page_size a multiple of 64,
+// so a K slice never straddles a page); used by 3c over a paged KV cache.
+template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT,
+          bool PAGED = false>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     constexpr int PD = 2;
     using MM = Mma<TL>;
@@ -98,7 +104,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
 
     const int m0 = tm * BM, n0 = tn * BN;
     const int k_begin = sp * a.k_chunk;
-    const int k_end = min(a.K, k_begin + a.k_chunk);
+    const int k_end = min(a.k_len ? min(a.K, load_uniform(a.k_len + g)) : a.K,
+                          k_begin + a.k_chunk);
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -168,11 +175,24 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
 
     // Slices at or past k_end load zeros (every column or K-row test fails), so the ring
     // needs no bounds branches; the zeros land in an LDS buffer nobody reads.
+    // paged B: the pool row of the next slice to load, looked up one slice ahead so the
+    // scalar load's latency hides behind a slice of MFMA work
+    int64_t page_row = 0;
+    auto lookup_row = [&](int k0) -> int64_t {
+        if constexpr (!PAGED) return 0;
+        const int pg = k0 < k_end
+                           ? load_uniform(a.b_pages + (int64_t)g * a.max_pages + k0 / a.page_size)
+                           : 0;
+        return (int64_t)pg * a.page_size + k0 % a.page_size;
+    };
+    if constexpr (PAGED) page_row = lookup_row(k_begin);
+
     auto load_slice = [&](int k0, int slot) {
         const int klim = k_end - k0;               // valid K columns / rows of this slice
         const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A_t + k0);
         const __amdgpu_buffer_rsrc_t rsb =
-            make_rsrc(NT ? B_t + k0 : B_t + (int64_t)k0 * a.ldb);
+            make_rsrc(NT ? B_t + k0 : B_t + (PAGED ? page_row : (int64_t)k0) * a.ldb);
+        if constexpr (PAGED) page_row = lookup_row(k0 + KS);
         #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             if constexpr (A_F32) {
@@ -351,18 +371,20 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
     }
 }
 
-template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT>
+template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT,
+          bool PAGED>
 hipError_t launch_cfg(const GemmArgs& args, int nblocks, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT>), dim3(nblocks),
-                       dim3(kThreads), 0, stream, args);
+    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT, PAGED>),
+                       dim3(nblocks), dim3(kThreads), 0, stream, args);
     return hipGetLastError();
 }
 
-template <typename TL, typename TA, bool NT, int AMODE, int OUT>
+template <typename TL, typename TA, bool NT, int AMODE, int OUT, bool PAGED = false>
 hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipStream_t stream) {
 #define MLA_TILE(BM_, BN_, WM_, WN_)                                                       \
     if (bm == BM_ && bn == BN_)                                                             \
-        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT>(args, nblocks, stream);
+        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT, PAGED>(args, nblocks,  \
+                                                                             stream);
     MLA_TILE(128, 128, 2, 2)
     MLA_TILE(128, 96, 4, 1)
     MLA_TILE(128, 64, 2, 2)
@@ -382,6 +404,15 @@ hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipSt
 hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
                     hipStream_t stream) {
     const bool split = a.split > 1;
+    if (p.b_pages) {   // paged NN B: 3c over a paged cache only
+        if (p.b_nt || p.amode != kAAlpha || !(p.out_type == kOutF32 || split))
+            return hipErrorInvalidValue;
+        if (!p.bf16)
+            return launch_tiles<float, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
+        if (p.a_f32)
+            return launch_tiles<bf16_t, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
+        return hipErrorInvalidValue;
+    }
     if (!p.bf16) {
         if (!p.b_nt && p.amode == kAPlain && (p.out_type == kOutF32 || split))
             return launch_tiles<float, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
@@ -581,6 +612,10 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     a.tiles_n = cdiv(p.N, plan.bn);
     a.rs = p.rs; a.rs_m = p.rs_m; a.rs_g = p.rs_g;
     a.alpha = p.alpha; a.alpha_ld = p.alpha_ld;
+    a.k_len = p.k_len; a.b_pages = p.b_pages; a.page_size = p.page_size; a.max_pages = p.max_pages;
+    if (p.b_pages && (p.page_size <= 0 || p.page_size % 64 != 0 ||
+                      (int64_t)p.max_pages * p.page_size < p.K))
+        return hipErrorInvalidValue;
     a.alpha_shift = 0;
     if (p.amode == kAAlpha) {
         // one alpha per slice: the tile is a power of two and a multiple of the slice

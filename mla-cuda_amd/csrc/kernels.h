@@ -30,6 +30,12 @@ struct GemmProblem {
     const float* rs = nullptr; int64_t rs_m = 0, rs_g = 0;
     const float* alpha = nullptr; int alpha_ld = 0, alpha_tile = 1;
     OutType out_type = kOutF32;
+    // optional: per-group K limit k_len[g] (<= K), and a paged NN B operand -- K row k of
+    // group g is pool row b_pages[g*max_pages + k/page_size]*page_size + k%page_size of B
+    // (sBg unused; page_size a multiple of 64; only the alpha-scaled NN form)
+    const int* k_len = nullptr;
+    const int* b_pages = nullptr;
+    int page_size = 0, max_pages = 0;
 };
 
 // Tile/split plan chosen for a problem (pure function of the shape; see plan_gemm).
@@ -54,9 +60,10 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride,
                           const void* gain, void* out, OutType out_type, int M, int N,
                           float eps, hipStream_t stream);
 // 2b
+// positions [Sq] shared by the batch, or [B*Sq] per sequence (pos_per_batch)
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope,
-                       int rope, hipStream_t stream);
+                       int rope, hipStream_t stream, bool pos_per_batch = false);
 // 3b (row_max may be null; when given it receives M = max_j m_part[row, j])
 hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
                           float* row_sum, float* row_max, int rows, int P, hipStream_t stream);
@@ -70,10 +77,15 @@ hipError_t launch_stream_merge(float* ctx, float* run_max, float* run_sum, const
 // KV-cache append: in = x @ W_kv_a rows [B*Sq][R + D] (or nsplit split-K partials);
 // c_kv[b][start_row + s] = RMSNorm(row[:R]) * gain (as launch_rmsnorm),
 // pe[b][start_row + s] = RoPE(row[R:], positions[s]) (as launch_rope).
+// Paged form (block_table given): token (b, s) goes to logical slot positions[b*Sq + s]
+// (pos_per_batch) of sequence b, i.e. pool row table[b][slot/page_size]*page_size +
+// slot%page_size; slots outside the table are skipped.
 hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, const void* gain,
                             const int64_t* positions, const float* inv_freq, void* c_kv,
                             void* pe, OutType out_type, int B, int Sq, int R, int D,
-                            int start_row, int cache_rows, float eps, hipStream_t stream);
+                            int start_row, int cache_rows, float eps, hipStream_t stream,
+                            bool pos_per_batch = false, const int* block_table = nullptr,
+                            int page_size = 0, int max_pages = 0);
 // Split each group of rows_a + rows_b rows (row_bytes each) of src into dst_a / dst_b.
 hipError_t launch_split_rows(const void* src, void* dst_a, void* dst_b, int64_t groups,
                              int rows_a, int rows_b, int64_t row_bytes, hipStream_t stream);
@@ -94,6 +106,11 @@ struct ScoresProblem {
     int sk_total = 0;            // keys in the whole sequence (causal rule)
     float inv_scale = 1.f;
     bool causal = false;
+    // ragged / paged keys (optional): per-batch key counts (<= Sk) and a block table
+    // [B][max_pages] of page_size-row pages of ckv / pe (page_size a multiple of 64)
+    const int* seq_lens = nullptr;
+    const int* block_table = nullptr;
+    int page_size = 0, max_pages = 0;
 };
 hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream);
 

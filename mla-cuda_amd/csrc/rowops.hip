@@ -123,14 +123,14 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
                                                    const int64_t* __restrict__ positions,
                                                    const float* __restrict__ inv_freq,
                                                    void* out_v, int Sq, int H, int nope,
-                                                   int rope) {
+                                                   int rope, int pos_per_batch) {
     __shared__ float cs[kRopeMaxHalf], sn[kRopeMaxHalf];
     const int half = rope >> 1;
     const int qk = nope + rope;
     const int bq = blockIdx.x;
     const int h0 = blockIdx.y * kRopeHeads;
     const int nh = min(kRopeHeads, H - h0);
-    const int64_t pos = positions[bq % Sq];
+    const int64_t pos = positions[pos_per_batch ? bq : bq % Sq];
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const float ang = rope_angle(pos, inv_freq[i]);
         cs[i] = cosf(ang);
@@ -227,15 +227,26 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict_
                                                         const int64_t* __restrict__ positions,
                                                         const float* __restrict__ inv_freq,
                                                         void* c_kv, void* pe, int Sq, int R, int D,
-                                                        int start_row, int cache_rows, float eps) {
+                                                        int start_row, int cache_rows,
+                                                        int pos_per_batch, const int* block_table,
+                                                        int page_size, int max_pages, float eps) {
     __shared__ float red[4];
     const int row = blockIdx.x;
     const int b = row / Sq, s = row % Sq;
     const int ld = R + D;
     const float* base = in + (int64_t)row * ld;
-    const int64_t crow = (int64_t)b * cache_rows + start_row + s;
+    const int64_t pos = positions[pos_per_batch ? row : s];
+    // destination row: dense cache row b*cache_rows + start_row + s, or in a paged cache
+    // the row of logical slot `pos` (the token's position) through the block table
+    int64_t crow;
+    if (block_table) {
+        if (pos < 0 || pos / page_size >= max_pages) return;   // outside the table: skip
+        const int page = block_table[(int64_t)b * max_pages + pos / page_size];
+        crow = (int64_t)page * page_size + pos % page_size;
+    } else {
+        crow = (int64_t)b * cache_rows + start_row + s;
+    }
     // rope pairs first (no barrier inside), then the workgroup-wide norm
-    const int64_t pos = positions[s];
     for (int i = threadIdx.x; i < D / 2; i += blockDim.x) {
         float x0 = base[R + 2 * i], x1 = base[R + 2 * i + 1];
         for (int q = 1; q < nsplit; ++q) {
@@ -297,16 +308,16 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, con
 
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope, int rope,
-                       hipStream_t stream) {
+                       hipStream_t stream, bool pos_per_batch) {
     if ((int64_t)B * Sq <= 0 || H <= 0) return hipSuccess;
     if (rope / 2 > kRopeMaxHalf) return hipErrorInvalidValue;
     const dim3 grid(B * Sq, (H + kRopeHeads - 1) / kRopeHeads);
     if (out_type == kOutF32)
         hipLaunchKernelGGL(rope_kernel<kOutF32>, grid, dim3(256), 0, stream, q_raw, positions,
-                           inv_freq, q_rope, Sq, H, nope, rope);
+                           inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
     else
         hipLaunchKernelGGL(rope_kernel<kOutBF16>, grid, dim3(256), 0, stream, q_raw, positions,
-                           inv_freq, q_rope, Sq, H, nope, rope);
+                           inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -330,18 +341,23 @@ hipError_t launch_stream_merge(float* ctx, float* run_max, float* run_sum, const
 hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, const void* gain,
                             const int64_t* positions, const float* inv_freq, void* c_kv,
                             void* pe, OutType out_type, int B, int Sq, int R, int D,
-                            int start_row, int cache_rows, float eps, hipStream_t stream) {
+                            int start_row, int cache_rows, float eps, hipStream_t stream,
+                            bool pos_per_batch, const int* block_table, int page_size,
+                            int max_pages) {
+    if (block_table && (page_size <= 0 || max_pages <= 0)) return hipErrorInvalidValue;
     const int64_t rows = (int64_t)B * Sq;
     if (rows <= 0) return hipSuccess;
     if (rows > 0x7fffffff) return hipErrorInvalidValue;
     if (out_type == kOutF32)
         hipLaunchKernelGGL(kv_append_kernel<kOutF32>, dim3((unsigned)rows), dim3(256), 0, stream,
                            in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
-                           D, start_row, cache_rows, eps);
+                           D, start_row, cache_rows, pos_per_batch ? 1 : 0, block_table,
+                           page_size, max_pages, eps);
     else
         hipLaunchKernelGGL(kv_append_kernel<kOutBF16>, dim3((unsigned)rows), dim3(256), 0, stream,
                            in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
-                           D, start_row, cache_rows, eps);
+                           D, start_row, cache_rows, pos_per_batch ? 1 : 0, block_table,
+                           page_size, max_pages, eps);
     return hipGetLastError();
 }
 

@@ -42,7 +42,27 @@ struct ScoresArgs {
     int causal_base;      // sk_total - Sq - key_offset: query s sees local keys <= base + s
     float scale_log2;   // log2(e) / scale
     int causal;
+    // ragged / paged keys (both optional): batch b has seq_lens[b] keys, and its key rows
+    // [j*page_size, (j+1)*page_size) live in page block_table[b*max_pages + j] of ckv / pe
+    const int* seq_lens;
+    const int* block_table;
+    int page_size, max_pages;
 };
+
+// Keys of batch b (Sk for a uniform batch).
+__device__ __forceinline__ int batch_keys(const ScoresArgs& a, int b) {
+    return a.seq_lens ? min(load_uniform(a.seq_lens + b), a.Sk) : a.Sk;
+}
+
+// First key row (in rows of ckv / pe) of the 64 keys [k, k + 64) of batch b: dense rows
+// are b*key_stride + k; paged rows go through the block table (page_size is a multiple of
+// 64, so 64 keys never straddle a page).  Keys at or past Sk read no table entry.
+__device__ __forceinline__ int64_t key_row(const ScoresArgs& a, int b, int k) {
+    if (!a.block_table) return (int64_t)b * a.key_stride + k;
+    const int page =
+        k < a.Sk ? load_uniform(a.block_table + (int64_t)b * a.max_pages + k / a.page_size) : 0;
+    return (int64_t)page * a.page_size + k % a.page_size;
+}
 
 // Tile t of the batch-major order: key tile kt = t % P, row tile tr = (t / P) % tiles_r,
 // batch b = t / (P * tiles_r).
@@ -101,26 +121,31 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
 
     // load cursor: tile lt, slice ls; its operand tile origins and per-row offsets (every
     // row masked once lt runs past the list, so the ring's surplus loads return zeros)
+    // K rows come in two 64-row halves (staging rows i = 0,1 and i = 2,3), each with its
+    // own origin, so a paged cache with 64-key pages needs no per-lane address math.
     int lt = x_lo + jx, ls = 0;
-    const TL *lqa, *lqr, *lka, *lkr;
+    const TL *lqa, *lqr, *lka[2], *lkr[2];
     uint32_t oq_r[4], oq_d[4], ok_r[4], ok_d[4];
     auto set_load_tile = [&]() __attribute__((always_inline)) {
         const bool live = lt < x_hi;
         const TileId id = tile_id(a, live ? lt : x_lo);
         const int64_t qrow = (int64_t)id.b * rows_b + id.r0;
-        const int64_t krow = (int64_t)id.b * a.key_stride + id.k0;
         lqa = static_cast<const TL*>(a.qa) + qrow * a.R;
         lqr = static_cast<const TL*>(a.qr) + qrow * a.D;
-        lka = static_cast<const TL*>(a.ckv) + krow * a.R;
-        lkr = static_cast<const TL*>(a.pe) + krow * a.D;
+        #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int64_t krow = key_row(a, id.b, id.k0 + 64 * h);
+            lka[h] = static_cast<const TL*>(a.ckv) + krow * a.R;
+            lkr[h] = static_cast<const TL*>(a.pe) + krow * a.D;
+        }
         const int qv = live ? min(kBM, rows_b - id.r0) : 0;
-        const int kv = live ? min(kBN, a.Sk - id.k0) : 0;
+        const int kv = live ? min(kBN, batch_keys(a, id.b) - id.k0) : 0;
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int row = i * 32 + (tid >> 3);
             const uint32_t mq = oob_mask(row, qv), mk = oob_mask(row, kv);
             oq_r[i] = o_r[i] | mq; oq_d[i] = o_d[i] | mq;
-            ok_r[i] = o_r[i] | mk; ok_d[i] = o_d[i] | mk;
+            ok_r[i] = o_r[i & 1] | mk; ok_d[i] = o_d[i & 1] | mk;   // offsets within the half
         }
     };
     auto advance_load = [&]() __attribute__((always_inline)) {
@@ -136,13 +161,14 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         const bool rope = ls >= nsl_r;
         const int c0 = rope ? (ls - nsl_r) * KS : ls * KS;
         const __amdgpu_buffer_rsrc_t rsq = make_rsrc((rope ? lqr : lqa) + c0);
-        const __amdgpu_buffer_rsrc_t rsk = make_rsrc((rope ? lkr : lka) + c0);
+        const __amdgpu_buffer_rsrc_t rsk0 = make_rsrc((rope ? lkr[0] : lka[0]) + c0);
+        const __amdgpu_buffer_rsrc_t rsk1 = make_rsrc((rope ? lkr[1] : lka[1]) + c0);
         uint32_t cmask = 0;
         if constexpr (PARTIAL) cmask = oob_mask(E * (tid & 7), (rope ? a.D : a.R) - c0);
         #pragma unroll
         for (int i = 0; i < 4; ++i) {
             rq[slot][i] = load16(rsq, (rope ? oq_d[i] : oq_r[i]) | cmask);
-            rk[slot][i] = load16(rsk, (rope ? ok_d[i] : ok_r[i]) | cmask);
+            rk[slot][i] = load16(i < 2 ? rsk0 : rsk1, (rope ? ok_d[i] : ok_r[i]) | cmask);
         }
     };
     auto store_slice = [&](int buf, int slot) __attribute__((always_inline)) {
@@ -174,7 +200,8 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         const TileId id = tile_id(a, t);
         const int64_t row0 = (int64_t)id.b * rows_b + id.r0;   // first row of the tile
         const int rv = min(kBM, rows_b - id.r0);                // valid rows
-        const int kvis = min(kBN, a.Sk - id.k0);                // keys before the padding
+        const int skb = batch_keys(a, id.b);
+        const int kvis = min(kBN, skb - id.k0);                 // keys before the padding
         const int kcols = min(kBN, a.ld_p - id.k0);             // columns inside the p row
         const float c = a.scale_log2;
         const __amdgpu_buffer_rsrc_t rsp = make_rsrc(a.p + row0 * a.ld_p + id.k0);
@@ -193,7 +220,8 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
             if constexpr (kCausal) {
                 // query index s = r / H sees absolute keys <= Sk_total - Sq + s
                 const int r = min(id.r0 + rr, rows_b - 1);
-                klast = min(klast, a.causal_base + r / a.H - id.k0);
+                const int cbase = a.seq_lens ? skb - a.Sq : a.causal_base;
+                klast = min(klast, cbase + r / a.H - id.k0);
             }
             float mx;
             if constexpr (kFull) {
@@ -262,7 +290,7 @@ __global__ void __launch_bounds__(kThreads, 2) scores_kernel(ScoresArgs a) {
         if (++cs < nsl) return false;
         if (a.causal)
             epilogue(ct, std::true_type(), std::false_type());
-        else if ((ct % a.P + 1) * kBN <= a.Sk)
+        else if ((ct % a.P + 1) * kBN <= batch_keys(a, ct / (a.P * a.tiles_r)))
             epilogue(ct, std::false_type(), std::true_type());
         else
             epilogue(ct, std::false_type(), std::false_type());
@@ -295,6 +323,11 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     a.causal_base = (p.sk_total ? p.sk_total : p.Sk) - p.Sq - p.key_offset;
     a.scale_log2 = p.inv_scale * 1.4426950408889634f;
     a.causal = p.causal ? 1 : 0;
+    a.seq_lens = p.seq_lens; a.block_table = p.block_table;
+    a.page_size = p.page_size; a.max_pages = p.max_pages;
+    if (p.block_table && (p.page_size <= 0 || p.page_size % 64 != 0 ||
+                          (int64_t)p.max_pages * p.page_size < p.Sk))
+        return hipErrorInvalidValue;
     // every staging offset (a row of the 128-row tile) must stay below the buffer range
     const int64_t row_bytes = (int64_t)std::max(p.R, p.D) * (p.bf16 ? 2 : 4);
     if (kBM * row_bytes >= kRsrcRange || (int64_t)kBM * p.ld_p * 4 >= kRsrcRange)

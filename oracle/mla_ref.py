@@ -18,7 +18,9 @@ What it restates (reference = pgangwar-ucsd/mla-cuda):
 * one extension the reference does not have: a causal mask (key j visible to query i iff
   j <= Sk - Sq + i), used by the chunked-prefill configuration;
 * the path's neighbours, which the reference names but does not implement: the KV-cache
-  append (``kv_append``) and the output projection (``o_proj``).
+  append (``kv_append``) and the output projection (``o_proj``);
+* a ragged, paged cache (``gather_pages``, ``mla_attention_paged``, ``prepare_q_ragged``,
+  ``kv_append_paged``): the same per-sequence math over keys found through a page table.
 
 Arithmetic runs in torch on the CPU, in float32 for float32/bfloat16/float16 inputs and in
 float64 for float64 inputs -- the reference's accumulate-dtype policy
@@ -360,6 +362,70 @@ def o_proj(attn: torch.Tensor, W_o: torch.Tensor) -> torch.Tensor:
     dtype, narrowed to the input dtype."""
     B, Sq, H, v = attn.shape
     return step_gemm(attn.reshape(B * Sq, H * v), W_o).to(attn.dtype).reshape(B, Sq, -1)
+
+
+# ---------------------------------------------------------------------------
+# Ragged, paged KV cache (the reference's cache is one dense [B, Sk] block with one Sk
+# and query positions shared by the batch: mla_kernels.cu:1489, 847-848, 449)
+# ---------------------------------------------------------------------------
+
+
+def gather_pages(pages: torch.Tensor, table_row: torch.Tensor, n: int) -> torch.Tensor:
+    """Keys [0, n) of one sequence from a paged pool [num_pages, page_size, width]: key k
+    is row k % page_size of page table_row[k // page_size]."""
+    page = pages.shape[1]
+    k = torch.arange(n)
+    return pages[table_row.long()[k // page], k % page]
+
+
+def mla_attention_paged(q_absorbed, q_rope, c_kv_pages, pe_pages, block_table, seq_lens,
+                        W_uv, scale: float, causal: bool = False) -> torch.Tensor:
+    """Each sequence b attends, exactly as ``mla_attention_official`` (the reference's
+    formulation, exhaustive_benchmark_suite.py:282-304), to its own seq_lens[b] keys
+    gathered from the pages; the causal rule is relative to that length."""
+    outs = []
+    for b in range(q_absorbed.shape[0]):
+        n = int(seq_lens[b])
+        ck = gather_pages(c_kv_pages, block_table[b], n).unsqueeze(0)
+        pe = gather_pages(pe_pages, block_table[b], n).unsqueeze(0)
+        outs.append(mla_attention_official(q_absorbed[b:b + 1], q_rope[b:b + 1], ck, pe, W_uv,
+                                           scale, causal))
+    return torch.cat(outs)
+
+
+def prepare_q_ragged(x, W_q_a, q_norm_w, W_q_b, W_uk, positions, nope: int, rope: int,
+                     eps: float = RMS_NORM_EPS):
+    """``prepare_q_mla_absorbed`` with per-sequence positions [B, Sq]: sequence b's query
+    rows use row b of positions."""
+    qa, qr = [], []
+    for b in range(x.shape[0]):
+        a, r = prepare_q_mla_absorbed(x[b:b + 1], W_q_a, q_norm_w, W_q_b, W_uk, positions[b],
+                                      nope, rope, eps)
+        qa.append(a); qr.append(r)
+    return torch.cat(qa), torch.cat(qr)
+
+
+def kv_append_paged(x, W_kv_a, kv_norm_w, positions, block_table, c_kv_pages, pe_pages,
+                    eps: float = RMS_NORM_EPS) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``kv_append`` into a paged cache: token (b, s) goes to slot positions[b, s] of
+    sequence b, i.e. row slot % page_size of page block_table[b, slot // page_size];
+    slots outside the table are skipped.  Returns updated copies of the two pools."""
+    B, Sq, _ = x.shape
+    R, D = c_kv_pages.shape[-1], pe_pages.shape[-1]
+    page, max_pages = c_kv_pages.shape[1], block_table.shape[1]
+    c2, p2 = c_kv_pages.clone(), pe_pages.clone()
+    for b in range(B):
+        dc = torch.zeros(1, Sq, R, dtype=c_kv_pages.dtype)
+        dp = torch.zeros(1, Sq, D, dtype=pe_pages.dtype)
+        rc, rp = kv_append(x[b:b + 1], W_kv_a, kv_norm_w, positions[b], dc, dp, 0, eps)
+        for s in range(Sq):
+            slot = int(positions[b, s])
+            if slot < 0 or slot // page >= max_pages:
+                continue
+            pg = int(block_table[b, slot // page])
+            c2[pg, slot % page] = rc[0, s]
+            p2[pg, slot % page] = rp[0, s]
+    return c2, p2
 
 
 # ---------------------------------------------------------------------------

@@ -41,7 +41,7 @@ def lib():
     for n in ("mla_q_absorbed_workspace_bytes", "mla_attention_workspace_bytes",
               "mla_gemm_workspace_bytes", "mla_ctx_workspace_bytes", "mla_out_workspace_bytes",
               "mla_attention_streaming_workspace_bytes", "mla_kv_append_workspace_bytes",
-              "mla_o_proj_workspace_bytes"):
+              "mla_o_proj_workspace_bytes", "mla_attention_paged_workspace_bytes"):
         getattr(L, n).restype = ctypes.c_size_t
     return L
 
@@ -234,6 +234,28 @@ def test_o_proj_validation_and_workspace(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "dims.hidden" in _err(lib)
 
 
+def test_paged_validation(lib):
+    d = dsv3(128, 1, 4992)
+    ws = lib.mla_attention_paged_workspace_bytes(F32, ctypes.byref(d), 0, 64)
+    assert ws == lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0) > 0
+    assert lib.mla_attention_paged_workspace_bytes(F32, ctypes.byref(d), 0, 96) == 0
+    args = [P16] * 6
+    st = lib.mla_attention_paged(F32, ctypes.byref(d), *args, 100, P16, ctypes.c_double(13.85), 0,
+                                 P16, P16, ctypes.c_size_t(ws), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "page_size" in _err(lib)
+    d.sk = 4989
+    st = lib.mla_attention_paged(F32, ctypes.byref(d), *args, 64, P16, ctypes.c_double(13.85), 0,
+                                 P16, P16, ctypes.c_size_t(ws), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "max_pages * page_size" in _err(lib)
+    d.sk = 4992
+    st = lib.mla_attention_paged(F32, ctypes.byref(d), P16, P16, P16, P16, P16, None, 64, P16,
+                                 ctypes.c_double(13.85), 0, P16, P16, ctypes.c_size_t(ws), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "seq_lens must not be NULL" in _err(lib)
+    st = lib.mla_kv_append_paged(F32, ctypes.byref(d), *([P16] * 5), ctypes.c_double(1e-6), None,
+                                 64, P16, P16, P16, ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "block_table must not be NULL" in _err(lib)
+
+
 # ------------------------------------------------------------------ torch binding
 
 
@@ -317,4 +339,25 @@ def test_binding_neighbour_shape_errors(ext):
         ext.kv_append(x, W, g, pos, ck, pe, 0, 1e-6)
     with pytest.raises(RuntimeError, match="W_o must be"):
         ext.o_proj(torch.zeros(2, 1, 4, 8), torch.zeros(30, 16))
+
+
+def test_binding_paged_shape_errors(ext):
+    qa, qr = torch.zeros(2, 1, 4, 16), torch.zeros(2, 1, 4, 8)
+    ck, pe = torch.zeros(5, 64, 16), torch.zeros(5, 64, 8)
+    tab, sl, wuv = torch.zeros(2, 2, dtype=torch.int32), torch.ones(2, dtype=torch.int32), torch.zeros(4, 8, 16)
+    with pytest.raises(RuntimeError, match="block_table must be int32"):
+        ext.mla_attention_paged(qa, qr, ck, pe, tab.long(), sl, wuv, 1.0)
+    with pytest.raises(RuntimeError, match="seq_lens must be a 1-D"):
+        ext.mla_attention_paged(qa, qr, ck, pe, tab, sl[:1], wuv, 1.0)
+    with pytest.raises(RuntimeError, match="pe_pages must be"):
+        ext.mla_attention_paged(qa, qr, ck, pe[:, :32], tab, sl, wuv, 1.0)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        ext.mla_attention_paged(qa, qr, ck, pe, tab, sl, wuv, 1.0)
+    with pytest.raises(RuntimeError, match=r"positions must be \[B, Sq\]"):
+        ext.kv_append_paged(torch.zeros(2, 1, 32), torch.zeros(32, 24), torch.zeros(16),
+                            torch.zeros(1, dtype=torch.int64), tab, ck, pe, 1e-6)
+    with pytest.raises(RuntimeError, match="positions must be"):
+        ext.q_absorbed(torch.zeros(2, 1, 64), torch.zeros(64, 32), torch.zeros(32),
+                       torch.zeros(32, 4 * 24), torch.zeros(4, 16, 16),
+                       torch.zeros(3, 1, dtype=torch.int64), 16, 8, 1e-6)
 

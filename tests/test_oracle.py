@@ -352,3 +352,70 @@ def test_o_proj_matches_brute_force_and_identity():
     # a transposed head/dim flattening is caught
     bad = attn.permute(0, 1, 3, 2).reshape(2, 3, 6) @ W
     assert (bad - ref).abs().max().item() > 1e-6
+
+
+# --------------------------------------------------------------------------- paged cache
+
+
+def _paged_case(seed, B=3, Sq=2, page=4, max_pages=3, dims=None):
+    dims = dims or R.MLADims(hidden=6, n_heads=2, q_lora=4, kv_rank=4, nope=2, rope=4, v=3)
+    g = torch.Generator().manual_seed(seed)
+    n_pages = B * max_pages + 2
+    perm = torch.randperm(n_pages, generator=g)[:B * max_pages].reshape(B, max_pages).int()
+    ck = torch.randn(n_pages, page, dims.kv_rank, generator=g, dtype=torch.float64)
+    pe = torch.randn(n_pages, page, dims.rope, generator=g, dtype=torch.float64)
+    qa = torch.randn(B, Sq, dims.n_heads, dims.kv_rank, generator=g, dtype=torch.float64)
+    qr = torch.randn(B, Sq, dims.n_heads, dims.rope, generator=g, dtype=torch.float64)
+    wuv = torch.randn(dims.n_heads, dims.v, dims.kv_rank, generator=g, dtype=torch.float64)
+    lens = torch.tensor([max_pages * page, 5, Sq], dtype=torch.int32)[:B]
+    return qa, qr, ck, pe, perm, lens, wuv
+
+
+def test_gather_pages_matches_loop():
+    _, _, ck, _, perm, _, _ = _paged_case(21)
+    got = R.gather_pages(ck, perm[1], 10)
+    for k in range(10):
+        assert torch.equal(got[k], ck[int(perm[1][k // 4]), k % 4])
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_paged_attention_reduces_to_dense(causal):
+    """Identity table and full lengths: exactly the dense formulation on the whole batch."""
+    qa, qr, _, _, _, _, wuv = _paged_case(22)
+    B, page, max_pages = 3, 4, 3
+    g = torch.Generator().manual_seed(23)
+    dense_c = torch.randn(B, page * max_pages, 4, generator=g, dtype=torch.float64)
+    dense_p = torch.randn(B, page * max_pages, 4, generator=g, dtype=torch.float64)
+    table = torch.arange(B * max_pages, dtype=torch.int32).reshape(B, max_pages)
+    got = R.mla_attention_paged(qa, qr, dense_c.reshape(-1, page, 4), dense_p.reshape(-1, page, 4),
+                                table, torch.full((B,), page * max_pages, dtype=torch.int32),
+                                wuv, 2.5, causal)
+    ref = R.mla_attention_official(qa, qr, dense_c, dense_p, wuv, 2.5, causal)
+    torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_paged_attention_uses_each_length():
+    """A sequence's result depends on its own keys only; one key more or less is caught."""
+    qa, qr, ck, pe, perm, lens, wuv = _paged_case(24)
+    got = R.mla_attention_paged(qa, qr, ck, pe, perm, lens, wuv, 2.5)
+    for b in range(3):
+        n = int(lens[b])
+        ref = R.mla_attention_official(qa[b:b + 1], qr[b:b + 1],
+                                       R.gather_pages(ck, perm[b], n)[None],
+                                       R.gather_pages(pe, perm[b], n)[None], wuv, 2.5)
+        torch.testing.assert_close(got[b:b + 1], ref, rtol=1e-12, atol=1e-12)
+    wrong = R.mla_attention_paged(qa, qr, ck, pe, perm, lens - 1, wuv, 2.5)
+    assert (wrong - got).abs().max().item() > 1e-6
+
+
+def test_kv_append_paged_reduces_to_dense():
+    x, W, gain, pos1, c_kv, pe, start = _kv_case(25)
+    B, rows = x.shape[0], c_kv.shape[1]
+    page = 7
+    table = torch.arange(B, dtype=torch.int32).reshape(B, 1)   # one page of 7 rows per sequence
+    pos = torch.stack([torch.arange(start, start + 3)] * B)
+    c2, p2 = R.kv_append_paged(x, W, gain, pos, table, c_kv, pe, eps=1e-6)
+    rc, rp = R.kv_append(x, W, gain, pos[0], c_kv, pe, start, eps=1e-6)
+    torch.testing.assert_close(c2, rc, rtol=0, atol=0)
+    torch.testing.assert_close(p2, rp, rtol=0, atol=0)
+    assert _kv_brute_check(c2, p2, x, W, gain, pos[0], c_kv, pe, start) < 1e-12
