@@ -10,6 +10,8 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <cstring>
 #include <string>
 
 #include "../../include/mla/mla.h"
@@ -278,12 +280,46 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     return L;
 }
 
+// 3a+3b+3c as one fused pass over the cache (flash.hip), for bf16 storage at the
+// DeepSeek-V3 widths.  MLA_ATTENTION_PATH=split selects the per-step kernels instead.
+FlashProblem flash_problem(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* qr,
+                           const void* ckv, const void* pe, double scale, int causal) {
+    (void)dt;
+    FlashProblem p;
+    p.qa = qa; p.qr = qr; p.ckv = ckv; p.pe = pe;
+    p.B = d->batch; p.Sq = d->sq; p.Sk = d->sk; p.H = d->heads; p.R = d->kv_rank;
+    p.D = d->rope; p.key_stride = d->sk;
+    p.scale = (float)scale;
+    p.causal = causal != 0;
+    return p;
+}
+
+bool flash_eligible(mla_dtype_t dt, const mla_dims_t* d) {
+    if (!is_bf16(dt)) return false;
+    // per-lane 32-bit buffer offsets: a batch's query rows and key rows (1 KB each)
+    constexpr int64_t kRange = 0x7fffffff;
+    if ((int64_t)d->sq * d->heads * 1024 >= kRange || (int64_t)d->sk * 1024 >= kRange)
+        return false;
+    return flash_supported(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
+}
+
+bool use_flash(mla_dtype_t dt, const mla_dims_t* d) {
+    const char* e = std::getenv("MLA_ATTENTION_PATH");
+    if (e && std::strcmp(e, "split") == 0) return false;
+    return flash_eligible(dt, d);
+}
+
 struct AttnLayout {
     int ld_p, P;
     GemmPlan ctx, out;
-    size_t off_p, off_m, off_l, off_alpha, off_rowsum, off_ctx, off_ctx_ws, off_out_ws, total;
+    FlashPlan flash;
+    size_t off_p, off_m, off_l, off_alpha, off_rowsum, off_ctx, off_ctx_ws, off_out_ws, off_part,
+        total;
 };
 
+// Both attention paths fit in one layout (the path is chosen per call): the fused path
+// uses ctx, row_sum and 3d's workspace like the per-step path, and puts its split partials
+// into the scores region when they fit there.
 AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     AttnLayout L;
     const size_t rows = (size_t)d->batch * d->sq * d->heads;
@@ -300,6 +336,14 @@ AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
     L.off_ctx_ws = o; o = align_up(o + L.ctx.workspace_bytes);
     L.off_out_ws = o; o = align_up(o + L.out.workspace_bytes);
+    L.off_part = L.off_p;
+    if (flash_eligible(dt, d)) {
+        L.flash = plan_flash(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
+        if (L.flash.partial_bytes > rows * L.ld_p * sizeof(float)) {
+            L.off_part = o;
+            o = align_up(o + L.flash.partial_bytes);
+        }
+    }
     L.total = o;
     return L;
 }
@@ -808,6 +852,19 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     float* row_sum = at<float>(workspace, L.off_rowsum);
     float* ctx = at<float>(workspace, L.off_ctx);
     const int rows = dims->batch * dims->sq * dims->heads;
+
+    if (use_flash(dtype, dims)) {
+        // 3a+3b+3c fused, then 3d
+        const FlashProblem fp = flash_problem(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache,
+                                              scale, causal);
+        MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part),
+                                 stream),
+                    "fused attention launch");
+        GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
+        MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
+                    "3d launch");
+        return ok();
+    }
 
     // 3a
     MLA_CHECK(run_scores(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal, p, L.ld_p, m,

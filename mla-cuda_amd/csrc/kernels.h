@@ -116,4 +116,28 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream);
 
 constexpr int kScoreTile = 128;  // keys per softmax partial (one 3a workgroup's key tile)
 
+// ---------------------------------------------------------------- 3a+3b+3c fused (bf16)
+// One pass over the cache per key split: ctx [rows, R] (unnormalised) and row_sum [rows]
+// for 3d, as 3c and 3b produce them.  bf16 storage, R = 512, D = 64 only.
+struct FlashProblem {
+    const void* qa = nullptr;    // [B*Sq*H, R]   bf16
+    const void* qr = nullptr;    // [B*Sq*H, D]
+    const void* ckv = nullptr;   // [B, key_stride, R]
+    const void* pe = nullptr;    // [B, key_stride, D]
+    int B = 0, Sq = 0, Sk = 0, H = 0, R = 0, D = 0;
+    int64_t key_stride = 0;      // key rows between batches (0: Sk)
+    float scale = 1.f;           // divisor of the scores
+    bool causal = false;
+};
+struct FlashPlan {
+    int row_tiles = 1;           // 128-row tiles per batch
+    int n_split = 1;             // key splits (one workgroup each)
+    int keys_per_split = 0;      // multiple of 32
+    size_t partial_bytes = 0;    // scratch: split partials, merged into ctx / row_sum
+};
+bool flash_supported(const FlashProblem& p);
+FlashPlan plan_flash(const FlashProblem& p);
+hipError_t launch_flash(const FlashProblem& p, const FlashPlan& plan, float* ctx, float* row_sum,
+                        float* partials, hipStream_t stream);
+
 }  // namespace mla

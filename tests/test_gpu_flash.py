@@ -1,0 +1,134 @@
+"""GPU parity of the fused bf16 attention (3a+3b+3c in one pass over the cache, flash.hip).
+
+mla_attention takes the fused path for bf16 at R = 512, D = 64; MLA_ATTENTION_PATH=split
+selects the per-step kernels.  Both are held to the fp32 oracle on the very bf16 values
+the kernels read, at the bf16 tolerance rtol 2e-2 (atol 2e-2 on O(1) outputs), and to each
+other.  Shapes cover a partial last key block, a single key, key splits merged across
+workgroups (small B), causal masks with Sq > 1, splits that a tile's causal limit leaves
+empty, row tiles that do not fill 64 rows (H = 40, H = 1), and a row maximum that keeps
+rising by more than the kernel's rescale slack.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import mla_ref as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+D = R.DSV3
+SCALE = math.sqrt(D.qk_head)
+BF = torch.bfloat16
+TOL = dict(rtol=2e-2, atol=2e-2)
+
+
+@pytest.fixture(scope="module")
+def ext():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import mla_custom_cuda
+    return mla_custom_cuda
+
+
+def gpu(t):
+    return t.to(DEV)
+
+
+def inputs(B, Sq, Sk, H=D.n_heads, seed=0, qs=0.05):
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(BF)  # noqa: E731
+    return (mk(B, Sq, H, D.kv_rank, sc=qs), mk(B, Sq, H, D.rope, sc=qs), mk(B, Sk, D.kv_rank),
+            mk(B, Sk, D.rope), mk(H, D.v, D.kv_rank, sc=1 / math.sqrt(D.kv_rank)))
+
+
+def oracle(args, causal):
+    qa, qr, ck, pe, wuv = (t.double() for t in args)
+    return R.mla_attention_official(qa, qr, ck, pe, wuv, SCALE, causal=causal).float()
+
+
+def run(ext, args, causal, path=None, monkeypatch=None):
+    if path is not None:
+        monkeypatch.setenv("MLA_ATTENTION_PATH", path)
+    try:
+        out = ext.mla_attention(*(gpu(t) for t in args), SCALE, causal)
+        torch.cuda.synchronize()
+    finally:
+        if path is not None:
+            monkeypatch.delenv("MLA_ATTENTION_PATH")
+    assert out.dtype == BF
+    return out.float().cpu()
+
+
+SHAPES = [
+    # B, Sq, Sk, causal
+    (1, 1, 1, False),
+    (1, 1, 5, False),
+    (2, 1, 32, False),
+    (2, 1, 33, False),
+    (3, 2, 300, True),
+    (1, 4, 700, True),
+    (1, 1, 4989, False),     # 39 key splits, merged
+    (4, 1, 4989, False),
+    (2, 16, 1000, True),
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", SHAPES)
+def test_fused_vs_oracle(ext, B, Sq, Sk, causal):
+    args = inputs(B, Sq, Sk, seed=Sk + B)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOL)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", SHAPES[2:7])
+def test_fused_vs_split_path(ext, monkeypatch, B, Sq, Sk, causal):
+    args = inputs(B, Sq, Sk, seed=7 * Sk + B)
+    fused = run(ext, args, causal)
+    split = run(ext, args, causal, "split", monkeypatch)
+    torch.testing.assert_close(fused, split, rtol=1e-2, atol=1e-2)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,H,causal", [(2, 3, 257, 40, False), (1, 512, 1024, 1, True),
+                                              (3, 1, 100, 1, False)])
+def test_fused_partial_row_tiles(ext, B, Sq, Sk, H, causal):
+    args = inputs(B, Sq, Sk, H=H, seed=H + Sk)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOL)
+
+
+def test_fused_rising_row_max(ext):
+    """Scores grow along the keys by ~0.35 (log2 units) per key, so every 32-key block
+    raises the row maximum by more than the kernel's slack and rescales its state."""
+    B, Sq, Sk = 2, 1, 640
+    qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=11)
+    u = torch.randn(D.kv_rank, generator=torch.Generator().manual_seed(12))
+    u = u / u.norm()
+    qa = (u * 64.0).expand(B, Sq, D.n_heads, D.kv_rank).to(BF)
+    # s_k = 64 * 0.0525 k = 3.36 k, i.e. t_k = s_k / sqrt(192) * log2(e) = 0.35 k; the
+    # keys stay O(10), so the bf16 rounding of p stays within the tolerance
+    ramp = torch.arange(Sk, dtype=torch.float32) * 0.0525
+    ck = (ck.float() * 0.05 + ramp[None, :, None] * u).to(BF)
+    args = (qa, qr, ck, pe, wuv)
+    torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOL)
+
+
+def test_fused_deterministic(ext):
+    args = [gpu(t) for t in inputs(3, 1, 2000, seed=5)]
+    a = ext.mla_attention(*args, SCALE)
+    b = ext.mla_attention(*args, SCALE)
+    assert torch.equal(a, b)
+
+
+def test_fused_cfg4_full_size_vs_split_path(ext, monkeypatch):
+    """B=128, Sq=1, Sk=4989 (cfg4 attention): the fused and per-step paths agree on every
+    sequence; the oracle checks three of them."""
+    args = inputs(128, 1, 4989, seed=0, qs=0.1)
+    fused = run(ext, args, False)
+    split = run(ext, args, False, "split", monkeypatch)
+    torch.testing.assert_close(fused, split, rtol=1e-2, atol=1e-2)
+    pick = [0, 77, 127]
+    ref = oracle(tuple(t[pick] for t in args[:4]) + (args[4],), False)
+    torch.testing.assert_close(fused[pick], ref, **TOL)
