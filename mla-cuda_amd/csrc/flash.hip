@@ -62,6 +62,7 @@ constexpr int kStageBytes = kPeOff + kFKeys * kPeBytes;
 constexpr int kXBytes = 4 * 4 * 64 * 16;            // S^T exchange: [wave][quarter][lane] x 16 B
 constexpr int kLoadsPerBlock = 9;                   // per wave: 8 latent rows, 8 rope rows
 constexpr float kSlack = 8.f;                       // log2 units
+constexpr int kSgValu = 0x002;                      // sched_group_barrier class: VALU
 
 typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_t;
@@ -79,8 +80,14 @@ struct FlashArgs {
     int causal;
 };
 
-// chunk permutation of key k's row (see the header)
-__device__ __forceinline__ int swz(int k) { return ((k & 3) << 1) | ((k >> 2) & 1); }
+// Chunk permutations (see the header).  gfx950 serves a 128-bit LDS read 16 lanes per
+// cycle (256 bytes, all 64 banks) and a 64-bit read 32 lanes per cycle.  Latent rows (1 KB):
+// the 16-byte chunk c of key k sits at c ^ swz(k & 15) within its 256-byte group, so the
+// 16 keys of a K fragment read hit 16 distinct chunks, and the 4 keys x 64 bytes of a
+// transposing read's half-wave hit 4 distinct 64-byte quarters.  Rope rows (128 B, two per
+// 256 bytes): chunk c of key k sits at c ^ ((k >> 1) & 7).
+__device__ __forceinline__ int swz(int k) { return ((k & 3) << 2) | ((k >> 2) & 3); }
+__device__ __forceinline__ int swz_pe(int k) { return (k >> 1) & 7; }
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -93,10 +100,12 @@ __device__ __forceinline__ void wait_vm() {
 // (vmcnt(0)), i.e. drain the ring of direct-to-LDS prefetches.  The empty asm statements
 // keep the compiler from moving memory accesses across the barrier.
 __device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt/expcnt at their maxima
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
@@ -155,6 +164,8 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
         k_hi = min(k_hi, a.Sk - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
     }
     const int nb = k_hi > k_lo ? (k_hi - k_lo + kFKeys - 1) / kFKeys : 0;
+    // the smallest row limit of the wave: its first row's (rows ascend with the lanes)
+    const int lim_wave = __builtin_amdgcn_readfirstlane(lim);
 
     // ---- Q^T fragments of depth half CW: lane l holds row l%32's depth 16s + 8h .. +7
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qa + (int64_t)b * rows_b * kFR);
@@ -174,7 +185,14 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
     const v4i rp = rsrc_words(a.pe + (int64_t)b * a.key_stride * kFD);
     const uint32_t lds0 = lds_addr(smem);
     // rope rows of keys 8w .. 8w+7: lane i fills chunk i%8 of key 8w + i/8
-    const uint32_t pe_lane = (uint32_t)(lane >> 3) * kPeBytes + 16u * ((lane & 7) ^ swz(lane >> 3));
+    const uint32_t pe_lane = (uint32_t)(lane >> 3) * kPeBytes +
+                             16u * ((lane & 7) ^ swz_pe(8 * wave + (lane >> 3)));
+    // latent row of key 8w + q: lane i fills LDS chunk i, i.e. loads logical chunk
+    // i ^ swz(key & 15) of its 256-byte group (blocks start at multiples of 32 keys)
+    uint32_t lat_lane[8];
+    #pragma unroll
+    for (int q = 0; q < 8; ++q)
+        lat_lane[q] = 16u * ((lane & ~15) | ((lane ^ swz((8 * wave + q) & 15)) & 15));
 
     auto issue = [&](int j, int stage) __attribute__((always_inline)) {
         const int kb = k_lo + kFKeys * j + 8 * wave;     // this wave's first key
@@ -184,10 +202,7 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
         const uint32_t kb_s = __builtin_amdgcn_readfirstlane(kb);
         #pragma unroll
         for (int q = 0; q < 8; ++q) {
-            // latent row of key kb + q: lane i fills LDS chunk i, i.e. loads logical chunk
-            // i ^ f(q) of its group of 8 chunks
-            const uint32_t lat = 16u * ((lane & ~7) | ((lane ^ swz(q)) & 7));
-            const uint32_t voff = (int)kb_s + q < k_hi ? lat : kOob;
+            const uint32_t voff = (int)kb_s + q < k_hi ? lat_lane[q] : kOob;
             dma16(rk, st + q * kLatBytes, voff, (kb_s + q) * kLatBytes);
         }
         const uint32_t voff = kb + (lane >> 3) < k_hi ? pe_lane : kOob;
@@ -195,22 +210,30 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
     };
 
     // ---- per-lane LDS offsets of the fragments
-    // K fragment of step s: key l32, logical chunk 2s + h, i.e. 8(s/4) + ((2(s%4)+h) ^ f)
-    const int fk = swz(l32 & 7);
-    uint32_t k_off[4];
+    // K fragment of step s: key l32, logical chunk 2s + h = 16(s/8) + (2(s%8) + h), the low
+    // four bits permuted by swz(l32 & 15); rope step s' reads chunk 2s' + h of the rope row
+    const int fk = swz(l32 & 15);
+    uint32_t k_off[8];
     #pragma unroll
-    for (int q = 0; q < 4; ++q) k_off[q] = l32 * kLatBytes + 16u * ((2 * q + h) ^ fk);
-    const uint32_t p_base = kPeOff + l32 * (kPeBytes - kLatBytes);   // rope row minus latent row
+    for (int q = 0; q < 8; ++q) k_off[q] = l32 * kLatBytes + 16u * ((2 * q + h) ^ fk);
+    uint32_t p_off[4];
+    #pragma unroll
+    for (int q = 0; q < 4; ++q)
+        p_off[q] = kPeOff + l32 * kPeBytes + 16u * ((2 * q + h) ^ swz_pe(l32));
     // V^T fragment of 32-col block mb, K step t, half r2: lane (group G = l/16, j = l%16,
-    // q = j/4, c = j%4) addresses key 16t + 8r2 + 4h + q, cols 32mb + 16(G%2) + 4c .. +3
-    uint32_t v_off[2];
+    // q = j/4, c = j%4) addresses key 16t + 8r2 + 4h + q, cols 32mb + 16(G%2) + 4c .. +3,
+    // i.e. logical chunk 4mb + 2(G%2) + c/2 = 16(mb/4) + (4(mb%4) + 2(G%2) + c/2)
+    uint32_t v_off[8];   // [r2][mb % 4]
     {
         const int G = lane >> 4, j = lane & 15, q = j >> 2, c = j & 3;
-        const int kx = 4 * h + q, fv = swz(kx);
         #pragma unroll
-        for (int odd = 0; odd < 2; ++odd) {
-            const int chunk = 4 * odd + 2 * (G & 1) + (c >> 1);   // low 3 bits of col/8
-            v_off[odd] = kx * kLatBytes + 16u * (chunk ^ fv) + 8u * (c & 1);
+        for (int r2 = 0; r2 < 2; ++r2) {
+            const int kx = 8 * r2 + 4 * h + q, fv = swz(kx);
+            #pragma unroll
+            for (int m4 = 0; m4 < 4; ++m4) {
+                const int chunk = 4 * m4 + 2 * (G & 1) + (c >> 1);   // low 4 bits of col/8
+                v_off[4 * r2 + m4] = kx * kLatBytes + 16u * (chunk ^ fv) + 8u * (c & 1);
+            }
         }
     }
     v4f* xw = reinterpret_cast<v4f*>(smem + NS * kStageBytes) + wave * 256 + lane;
@@ -220,11 +243,45 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
     #pragma unroll
     for (int i = 0; i < kColBlocks; ++i) O[i] = v16f{};
     float m_run = -INFINITY, l_run = 0.f;
+    uint32_t pk[8] = {0, 0, 0, 0, 0, 0, 0, 0};   // P^T of the previous block, bf16 pairs
 
-    // one 32-key block j held in ring stage ST
-    auto step = [&](int j, auto st_tag) __attribute__((always_inline)) {
+    // V^T fragments of the block in stage ST for K step tk (keys 16tk + {0..3, 8..11} + 4h),
+    // and the MFMAs that fold them into O^T with P^T of that block
+    auto read_v = [&](auto st_tag, int tk, v8bf* va) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
-        const int ahead = min(nb - 1, j + NS - 2) - j;   // blocks issued after block j
+        const uint8_t* st = smem + ST * kStageBytes;
+        #pragma unroll
+        for (int i = 0; i < kColBlocks; ++i) {
+            const int mb = kColBlocks * CW + i;
+            const uint32_t imm = 256u * (mb >> 2) + 16384u * tk;
+            const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                (lds_v4bf*)(st + v_off[mb & 3] + imm));
+            const v4bf hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                (lds_v4bf*)(st + v_off[4 + (mb & 3)] + imm));   // row offset includes 8r2
+            va[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+    };
+    auto mma_v = [&](int tk, const v8bf* va) __attribute__((always_inline)) {
+        const v4u pb = {pk[4 * tk], pk[4 * tk + 1], pk[4 * tk + 2], pk[4 * tk + 3]};
+        #pragma unroll
+        for (int i = 0; i < kColBlocks; ++i)
+            O[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[i], __builtin_bit_cast(v8bf, pb),
+                                                           O[i], 0, 0, 0);
+    };
+    auto pv = [&](auto st_tag, int tk) __attribute__((always_inline)) {
+        v8bf va[kColBlocks];
+        read_v(st_tag, tk, va);
+        mma_v(tk, va);
+    };
+
+    // One 32-key block j held in ring stage ST.  Block j's scores, exchange and softmax run
+    // together with block j-1's P.V (stage ST-1): the first half of that P.V covers the
+    // exchange writes before the barrier, the second half interleaves with the softmax.
+    auto step = [&](int j, auto st_tag, auto has_prev) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_tag)::value;
+        constexpr bool PREV = decltype(has_prev)::value;
+        constexpr int SP = (ST + NS - 1) % NS;
+        const int ahead = min(nb - 1, j + NS - 3) - j;   // blocks issued after block j
         if constexpr (NS >= 4) {
             if (ahead >= 2) wait_vm<2 * kLoadsPerBlock>();
             else if (ahead == 1) wait_vm<kLoadsPerBlock>();
@@ -233,23 +290,24 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
             if (ahead >= 1) wait_vm<kLoadsPerBlock>();
             else wait_vm<0>();
         }
-        lds_barrier();   // block j is in LDS for every wave; every wave is past block j-1
-        if (j + NS - 1 < nb) issue(j + NS - 1, (ST + NS - 1) % NS);
+        lds_barrier();   // block j is in LDS for every wave; every wave is past block j-2's P.V
+        if (j + NS - 2 < nb) issue(j + NS - 2, (ST + NS - 2) % NS);
 
         const uint8_t* st = smem + ST * kStageBytes;
 
-        // partial S^T over this wave's 18 depth steps; K fragment reads run kWin steps
-        // ahead of the MFMAs that consume them
+        // partial S^T over this wave's 18 depth steps; K fragment reads run kWin steps ahead
         constexpr int kWin = 6;
         auto read_k = [&](int i) __attribute__((always_inline)) {
             const int s = kHSteps * CW + i;
-            const uint32_t off = s < kRSteps ? k_off[s & 3] + 128u * (s >> 2)
-                                             : p_base + k_off[(s - kRSteps) & 3];
+            const uint32_t off = s < kRSteps ? k_off[s & 7] + 256u * (s >> 3)
+                                             : p_off[(s - kRSteps) & 3];
             return *reinterpret_cast<const v4u*>(st + off);
         };
         v4u kf[kWin];
         #pragma unroll
         for (int i = 0; i < kWin; ++i) kf[i] = read_k(i);
+        v8bf va0[kColBlocks];
+        if constexpr (PREV) read_v(std::integral_constant<int, SP>{}, 0, va0);
         v16f sa = v16f{};
         #pragma unroll
         for (int i = 0; i < kHSteps; ++i) {
@@ -260,7 +318,23 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
         #pragma unroll
         for (int q = 0; q < 4; ++q)
             xw[64 * q] = v4f{sa[4 * q], sa[4 * q + 1], sa[4 * q + 2], sa[4 * q + 3]};
+        if constexpr (PREV) mma_v(0, va0);
+        // issue order of this region: the first K window, the V^T reads of block j-1, the
+        // score MFMAs with the remaining K reads between them, the exchange writes, then
+        // block j-1's first P.V half
+        __builtin_amdgcn_sched_group_barrier(kSgDsRd, kWin, 0);
+        if constexpr (PREV) __builtin_amdgcn_sched_group_barrier(kSgDsRd, 2 * kColBlocks, 0);
+        #pragma unroll
+        for (int i = 0; i < kHSteps - kWin; ++i) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRd, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, kWin, 0);
+        __builtin_amdgcn_sched_group_barrier(kSgDsWr, 4, 0);
+        if constexpr (PREV) __builtin_amdgcn_sched_group_barrier(kSgMfma, kColBlocks, 0);
         lds_barrier();   // both halves of every row block's S^T are in LDS
+        v8bf va1[kColBlocks];
+        if constexpr (PREV) read_v(std::integral_constant<int, SP>{}, 1, va1);
         v16f sc;
         #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -269,91 +343,88 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
             for (int e = 0; e < 4; ++e)   // the same operand order in both waves
                 sc[4 * q + e] = CW == 0 ? sa[4 * q + e] + o[e] : o[e] + sa[4 * q + e];
         }
+        if constexpr (PREV) mma_v(1, va1);
 
-        // V^T fragments of this wave's column blocks for K step tk
-        auto read_v = [&](int tk, v8bf* va) __attribute__((always_inline)) {
-            #pragma unroll
-            for (int i = 0; i < kColBlocks; ++i) {
-                const int mb = kColBlocks * CW + i;
-                const uint32_t base = v_off[mb & 1] + 128u * (mb >> 1) + 16384u * tk;
-                const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(st + base));
-                const v4bf hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                    (lds_v4bf*)(st + base + 8 * kLatBytes));
-                va[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-            }
-        };
-        v8bf va0[kColBlocks];
-        read_v(0, va0);
-
-        // online softmax; element i of lane l is key kb + 8(i/4) + 4h + i%4 of row l%32
+        // online softmax of block j; element i of lane l is key kb + 8(i/4) + 4h + i%4 of
+        // row l%32
+        // Work on the raw scores: c > 0, so max(s) * c is exactly max(s * c), and
+        // p = 2^(s c - m) is one fma and one v_exp_f32.  Masked keys get s = -inf.  Blocks
+        // whose every key is visible to every row of the wave skip the mask.
         const int kb = k_lo + kFKeys * j;
-        float t[16];
-        float bm = -INFINITY;
-        #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
-            t[i] = key <= lim ? sc[i] * a.c : -INFINITY;
-            bm = fmaxf(bm, t[i]);
+        if (kb + kFKeys - 1 > lim_wave) {
+            #pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
+                sc[i] = key <= lim ? sc[i] : -INFINITY;
+            }
         }
+        float bm = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+        #pragma unroll
+        for (int i = 3; i < 16; i += 2) bm = fmaxf(fmaxf(bm, sc[i]), sc[i + 1] );
         {
             const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm),
                                                              __float_as_uint(bm), false, false);
-            bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+            bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * a.c;
         }
         const bool raise = bm > m_run + kSlack;
-        if (__builtin_amdgcn_ballot_w64(raise)) {
-            // 2^(m_run - bm) is 0 on a row's first raise (m_run = -inf); other rows keep 1
-            const float f = raise ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
-            l_run *= f;
-            #pragma unroll
-            for (int mb = 0; mb < kColBlocks; ++mb) O[mb] *= f;
-            m_run = raise ? bm : m_run;
-        }
-        // a row with no visible key so far has m_run = -inf and every t = -inf: p = 0
-        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        // 2^(m_run - bm) is 0 on a row's first raise (m_run = -inf); other rows keep 1
+        const float f = raise ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
+        m_run = raise ? bm : m_run;
+        // a row with no visible key so far has m_run = -inf and every s = -inf: p = 0
+        const float m_neg = m_run == -INFINITY ? 0.f : -m_run;
         float ls = 0.f;
-        uint32_t pk[8];
         #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(t[i] - m_use);
-            const float p1 = __builtin_amdgcn_exp2f(t[i + 1] - m_use);
+            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.c, m_neg));
+            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i + 1], a.c, m_neg));
             ls += p0 + p1;
             pk[i >> 1] = pack_bf16x2(p0, p1);
         }
-        l_run += ls;
-
-        // O^T += V_blk^T . P^T over this wave's 8 column blocks; K step tk uses accumulator
-        // elements 8tk .. 8tk+7 (keys 16tk + {0..3, 8..11} + 4h).  The V^T fragments of a
-        // K step are read before its MFMAs (those of step 0 before the softmax above).
-        #pragma unroll
-        for (int tk = 0; tk < 2; ++tk) {
-            const v4u pb = {pk[4 * tk], pk[4 * tk + 1], pk[4 * tk + 2], pk[4 * tk + 3]};
-            v8bf va[kColBlocks];
-            if (tk == 0) {
-                #pragma unroll
-                for (int i = 0; i < kColBlocks; ++i) va[i] = va0[i];
-            } else {
-                read_v(1, va);
-            }
+        l_run = l_run * f + ls;
+        // the probabilities are computed here, between block j-1's MFMAs, not sunk past the
+        // rescale branch below
+        asm volatile("" ::"v"(pk[0]), "v"(pk[1]), "v"(pk[2]), "v"(pk[3]), "v"(pk[4]), "v"(pk[5]),
+                     "v"(pk[6]), "v"(pk[7]), "v"(l_run));
+        // issue order of this region: the exchange and V^T reads, then block j-1's second
+        // P.V half with the softmax VALU work spread between its MFMAs
+        __builtin_amdgcn_sched_group_barrier(kSgDsRd, PREV ? 4 + 2 * kColBlocks : 4, 0);
+        if constexpr (PREV) {
             #pragma unroll
-            for (int i = 0; i < kColBlocks; ++i)
-                O[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                    va[i], __builtin_bit_cast(v8bf, pb), O[i], 0, 0, 0);
+            for (int i = 0; i < kColBlocks; ++i) {
+                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgValu, 10, 0);
+            }
+        }
+        // rescale after block j-1's P.V (which is in the old scale) has been accumulated
+        if (__builtin_amdgcn_ballot_w64(raise)) {
+            #pragma unroll
+            for (int mb = 0; mb < kColBlocks; ++mb) O[mb] *= f;
         }
     };
 
-    // ---- prologue: blocks 0 .. NS-2 in flight; then the blocks, NS per trip so that each
-    // step's ring stage is a constant
+    // ---- prologue: blocks 0 .. NS-3 in flight; block 0 without a predecessor; then the
+    // blocks, NS per trip so that every step's ring stage is a constant; then the last
+    // block's P.V
     #pragma unroll
-    for (int j = 0; j < NS - 1; ++j)
+    for (int j = 0; j < NS - 2; ++j)
         if (j < nb) issue(j, j);
-    for (int j0 = 0; j0 < nb; j0 += NS) {
-        step(j0, std::integral_constant<int, 0>{});
-        if (j0 + 1 < nb) step(j0 + 1, std::integral_constant<int, 1 % NS>{});
+    if (nb > 0) step(0, std::integral_constant<int, 0>{}, std::false_type{});
+    for (int j0 = 1; j0 < nb; j0 += NS) {
+        step(j0, std::integral_constant<int, 1 % NS>{}, std::true_type{});
+        if (j0 + 1 < nb) step(j0 + 1, std::integral_constant<int, 2 % NS>{}, std::true_type{});
         if constexpr (NS > 2)
-            if (j0 + 2 < nb) step(j0 + 2, std::integral_constant<int, 2 % NS>{});
+            if (j0 + 2 < nb) step(j0 + 2, std::integral_constant<int, 3 % NS>{}, std::true_type{});
         if constexpr (NS > 3)
-            if (j0 + 3 < nb) step(j0 + 3, std::integral_constant<int, 3 % NS>{});
+            if (j0 + 3 < nb) step(j0 + 3, std::integral_constant<int, 4 % NS>{}, std::true_type{});
+    }
+    if (nb > 0) {
+        // block nb-1 sits in stage (nb-1) % NS; no later loads overwrite it
+        switch ((nb - 1) % NS) {
+            case 0: pv(std::integral_constant<int, 0>{}, 0); pv(std::integral_constant<int, 0>{}, 1); break;
+            case 1: pv(std::integral_constant<int, 1 % NS>{}, 0); pv(std::integral_constant<int, 1 % NS>{}, 1); break;
+            case 2: pv(std::integral_constant<int, 2 % NS>{}, 0); pv(std::integral_constant<int, 2 % NS>{}, 1); break;
+            default: pv(std::integral_constant<int, 3 % NS>{}, 0); pv(std::integral_constant<int, 3 % NS>{}, 1); break;
+        }
     }
 
     // ---- this split's partial state: O columns 256CW .., and (CW = 0) m and l
@@ -389,7 +460,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
     else flash_wave<NS, 1>(a, smem, wg);
 }
 
-constexpr int kFStages = 3;   // LDS ring depth
+constexpr int kFStages = 4;   // LDS ring depth
 
 // ctx = sum_s w_s O_s, row_sum = sum_s w_s l_s, w_s = 2^(m_s - max_s m_s); one thread per
 // (row, 4 columns)
