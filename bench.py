@@ -74,6 +74,10 @@ def step_work(B, Sq, Sk, dims, e=4):
         "3b": (3 * flat * P, 4 * (3 * flat * P + flat)),
         "3c": (2 * flat * Sk * R, 4 * (flat * Sk + flat * P) + e * (B * Sk * R) + 4 * flat * R),
         "3d": (2 * flat * R * V, 4 * flat * R + e * H * V * R + 4 * flat + e * flat * V),
+        # 3a+3b+3c fused (the bf16 layer's attention kernel): queries and cache read once,
+        # the unnormalised ctx and row sums written once
+        "3abc": (2 * flat * Sk * (R + D) + 2 * flat * Sk * R,
+                 e * (flat * (R + D) + B * Sk * (R + D)) + 4 * flat * R + 4 * flat),
     }
     return w
 
@@ -237,6 +241,25 @@ def main():
     steps_sum = sum(step_us.values())
     same = (o_steps - out).abs().max().item()
 
+    # bf16: the layer's attention runs 3a+3b+3c as one fused kernel (attn_ctx), timed here
+    # the same way; the per-step 3a/3b/3c above are the decomposed kernels
+    fused_attn = dname == "bf16"
+    if fused_attn:
+        qa_f, qr_f = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
+                                    g["positions"], dims.nope, dims.rope, eps)
+        for _ in range(2):
+            ext.attn_ctx(qa_f, qr_f, g["c_kv"], g["pe_cache"], scale, causal)
+        torch.cuda.synchronize()
+        fev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(args.steps)]
+        for e0, e1 in fev:
+            e0.record()
+            ext.attn_ctx(qa_f, qr_f, g["c_kv"], g["pe_cache"], scale, causal)
+            e1.record()
+        torch.cuda.synchronize()
+        step_us["3abc"] = statistics.mean(e0.elapsed_time(e1) for e0, e1 in fev) * 1e3
+        names = names + ["3abc"]
+
     work = step_work(B, Sq, Sk, dims, e=2 if dname == "bf16" else 4)
     peak_mfma = PEAK_BF16 if dname == "bf16" else PEAK_F32
     per_step = {}
@@ -248,7 +271,7 @@ def main():
                        "tflops": round(fl / t / 1e12, 2), "gbps": round(by / t / 1e9, 1),
                        "mfma_pct": round(100 * fl / t / peak_mfma, 1),
                        "hbm_pct": round(100 * by / t / PEAK_HBM, 1)}
-    dom = max(("3a", "3c"), key=lambda n: step_us[n])
+    dom = "3abc" if fused_attn else max(("3a", "3c"), key=lambda n: step_us[n])
     fl, by = work[dom]
     t_dom = step_us[dom] * 1e-6
     if fl / by > peak_mfma / PEAK_HBM:   # above the ridge: compute-bound
@@ -384,6 +407,9 @@ def main():
         "roofline": roofline,
         "steps_us": per_step,
         "per_step_sum_us": round(steps_sum, 2),
+        "fused_path_sum_us": (round(sum(step_us[n] for n in ("2a1", "2a-n", "2a2", "2b", "2c",
+                                                             "3abc", "3d")), 2)
+                              if fused_attn else None),
         "per_step_vs_fused_max_abs": same,
         "neighbours": nb,
         "wall_s_timed": round(t_wall, 3),

@@ -406,6 +406,33 @@ torch::Tensor step_ctx(torch::Tensor p, torch::Tensor alpha, torch::Tensor c_kv,
     return ctx;
 }
 
+// 3a+3b+3c fused (bf16): [ctx [B, Sq, H, kv_rank], row_sum [B*Sq*H]], float32, with
+// ctx / row_sum the softmax-weighted sum of the c_kv rows (the pair shares one per-row
+// factor that differs from the per-step path's)
+std::vector<torch::Tensor> step_attn_ctx(torch::Tensor qa, torch::Tensor qr, torch::Tensor ckv,
+                                         torch::Tensor pe, double scale, bool causal) {
+    mla_dims_t d = attn_dims(qa, qr, ckv, pe, nullptr);
+    d.v = 4;
+    const mla_dtype_t dt = to_mla_dtype(qa, "q_absorbed");
+    check_same_dtype(qa, qr, "q_rope");
+    check_same_dtype(qa, ckv, "c_kv");
+    check_same_dtype(qa, pe, "pe_cache");
+    TORCH_CHECK(!causal || d.sk >= d.sq, "MLA: causal attention needs Sk >= Sq");
+    for (auto* t : {&qa, &qr, &ckv, &pe}) check_contig(*t, "attn_ctx input");
+    check_device({&qa, &qr, &ckv, &pe});
+    c10::DeviceGuard guard(qa.device());
+    auto f32 = qa.options().dtype(torch::kFloat32);
+    auto ctx = torch::empty({d.batch, d.sq, d.heads, d.kv_rank}, f32);
+    auto rs = torch::empty({(int64_t)d.batch * d.sq * d.heads}, f32);
+    const size_t wsb = mla_attn_ctx_workspace_bytes(dt, &d, causal ? 1 : 0);
+    auto ws = workspace(wsb, qa);
+    check_status(mla_attn_ctx(dt, &d, qa.data_ptr(), qr.data_ptr(), ckv.data_ptr(), pe.data_ptr(),
+                              scale, causal ? 1 : 0, ctx.data_ptr<float>(), rs.data_ptr<float>(),
+                              ws.data_ptr(), wsb, current_stream()),
+                 "attn_ctx");
+    return {ctx, rs};
+}
+
 torch::Tensor step_out(torch::Tensor ctx, torch::Tensor row_sum, torch::Tensor W_uv) {
     check_dim(ctx, 4, "ctx", "[B, Sq, H, kv_rank]");
     check_dim(W_uv, 3, "W_uv", "[H, v, kv_rank]");
@@ -693,6 +720,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("ctx", &step_ctx, "3c: unnormalised ctx", py::arg("scores"), py::arg("alpha"),
           py::arg("c_kv"), py::arg("Sq"), py::arg("H"));
     m.def("out", &step_out, "3d", py::arg("ctx"), py::arg("row_sum"), py::arg("W_uv"));
+    m.def("attn_ctx", &step_attn_ctx, "3a+3b+3c fused (bf16): returns [ctx, row_sum]",
+          py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),
+          py::arg("scale"), py::arg("causal") = false);
     m.def("score_tile", []() { return mla_score_tile(); });
     m.def("score_ld", [](int32_t sk) { return mla_score_ld(sk); });
     m.def("version", []() { return std::string(mla_version()); });

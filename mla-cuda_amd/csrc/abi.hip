@@ -780,6 +780,39 @@ int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores, int3
     return ok();
 }
 
+size_t mla_attn_ctx_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal) {
+    if (!dims || check_attn_dims(dtype, dims, causal) != MLA_OK) return 0;
+    if (!flash_eligible(dtype, dims)) return 0;
+    return align_up(plan_flash(flash_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr, 1.0,
+                                             causal)).partial_bytes);
+}
+
+int mla_attn_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                 const void* q_rope, const void* c_kv, const void* pe_cache, double scale,
+                 int causal, float* ctx, float* row_sum, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    MLA_CHECK(check_scale(scale));
+    if (!flash_eligible(dtype, dims))
+        return fail(MLA_ERR_UNSUPPORTED,
+                    "fused attention needs bf16, kv_rank 512 and rope 64 (got %s, %d, %d)",
+                    is_bf16(dtype) ? "bf16" : "float32", dims->kv_rank, dims->rope);
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    MLA_CHECK(check_ptr(ctx, "ctx"));
+    MLA_CHECK(check_ptr(row_sum, "row_sum"));
+    const FlashProblem fp =
+        flash_problem(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache, scale, causal);
+    const FlashPlan plan = plan_flash(fp);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, align_up(plan.partial_bytes)));
+    MLA_TRY_HIP(launch_flash(fp, plan, ctx, row_sum, static_cast<float*>(workspace), stream),
+                "fused attention launch");
+    return ok();
+}
+
 size_t mla_out_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
     if (!dims || check_out_dims(dtype, dims) != MLA_OK) return 0;
     return plan_gemm(out_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr)).workspace_bytes;

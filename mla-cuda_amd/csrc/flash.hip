@@ -10,25 +10,29 @@
 // order of operations differs (an online softmax instead of per-tile partials).
 //
 // Workgroup: 4 waves over 64 rows (queries x heads) of one batch and one contiguous key
-// range (a split).  Wave w = (rb, cw) = (w & 1, w >> 1) owns rows 32rb .. 32rb+31; the two
-// waves of a row block split the work of each 32-key block between them:
-//   partial S^T[32 keys x 32 rows] over depth half cw (18 bf16 MFMA K steps of the
-//     576-deep row; that half of Q^T lives in 72 VGPRs for the whole kernel), exchanged
-//     through LDS and summed in the same order by both waves
-//   online softmax per row (duplicated in both waves): every lane holds one row (column
-//     l%32 of the accumulator) and 16 of the block's keys, its partner lane l^32 the other 16
-//   O^T[256 cols x 32 rows] += V_blk^T . P^T for column half cw (P^T is the S^T
-//     accumulator rounded to bf16, used in place as the B operand; O^T is 128 registers)
+// range (a split).  Wave w owns rows 16w .. 16w+15 and all 512 output columns, with the
+// gfx950 16x16x32 bf16 MFMA; per 32-key block:
+//   S^T[32 keys x 16 rows] = K_blk . Q^T   (2 key halves x 18 K steps; the wave's Q^T,
+//                                          576 deep, lives in 72 VGPRs for the whole kernel)
+//   online softmax per row: lane l holds 8 of the block's keys for row l%16; the other
+//                           24 sit in lanes l%16 + 16g (v_permlane16/32_swap reductions)
+//   O^T[512 cols x 16 rows] += V_blk^T . P^T (P^T is the S^T accumulator rounded to bf16,
+//                                          used in place as the B operand; O^T is 128
+//                                          accumulation registers)
+// No data moves between waves; one barrier per block guards the LDS ring.  Block j-1's
+// P.V is issued in block j's step, interleaved with block j's softmax.
 // V_blk^T fragments come from the same key-major LDS tile as K_blk through gfx950's
 // transposing ds_read_b64_tr_b16, so c_kv is staged once per workgroup, by direct
-// global->LDS loads (buffer_load_dwordx4 ... lds) into a ring of NS blocks: NS-1 blocks are
-// in flight while one is computed, with no VGPRs spent on staging.  The two 64-row tiles of
-// a batch are placed on one XCD, so the second read of every key block hits its L2.
+// global->LDS loads (buffer_load_dwordx4 ... lds) into a 4-block ring: two blocks are in
+// flight while two are in use, with no VGPRs spent on staging.  The two 64-row tiles of a
+// batch are placed on one XCD, so the second read of every key block hits its L2.
 //
 // LDS tile of a block (36 KB): 32 latent rows of 1 KB, then 32 rope rows of 128 B.  The
-// 16-byte chunk c of key k sits at chunk c ^ f(k & 7), f(k) = 2(k & 3) + (k >> 2), which
-// keeps both the 8-lane phases of the K fragment reads (8 keys, one chunk) and the 16-lane
-// groups of the transposing reads (4 keys, two chunks) on disjoint banks.
+// 16-byte chunk c of latent key k sits at c ^ swz(k & 15) within its 256-byte group
+// (swz: rotate left by one of four bits); chunk c of rope key k at c ^ ((k >> 1) & 7).
+// The K slots of the MFMAs are assigned so that the four lane groups of a K fragment read
+// four different 256-byte quarters of the key rows.  Both measured free of bank conflicts
+// (SQ_LDS_BANK_CONFLICT = 0) for the fragment reads of this kernel.
 //
 // Softmax: log2 domain, t = s * log2(e)/scale.  The running maximum m is only raised when
 // a block's maximum exceeds it by more than kSlack (= 8, so p <= 256): the rescale of the
@@ -49,17 +53,15 @@ namespace {
 
 constexpr int kFR = 512, kFD = 64;                  // latent and rope widths
 constexpr int kFKeys = 32;                          // keys per block
-constexpr int kFRows = 64;                          // rows per workgroup
+constexpr int kFRows = 64;                          // rows per workgroup (4 waves x 16)
 constexpr int kFThreads = 256;
-constexpr int kQSteps = (kFR + kFD) / 16;           // 36 MFMA K steps of 16
-constexpr int kRSteps = kFR / 16;                   // 32 of them over the latent part
-constexpr int kHSteps = kQSteps / 2;                // 18 per wave of a row block
-constexpr int kColBlocks = kFR / 64;                // 8 blocks of 32 columns per wave
+constexpr int kQSteps = (kFR + kFD) / 32;           // 18 MFMA K steps of 32
+constexpr int kRSteps = kFR / 32;                   // 16 of them over the latent part
+constexpr int kColBlocks = kFR / 16;                // 32 blocks of 16 columns
 constexpr int kLatBytes = kFR * 2;                  // one key's latent row
 constexpr int kPeBytes = kFD * 2;                   // one key's rope row
 constexpr int kPeOff = kFKeys * kLatBytes;          // rope rows follow the latent rows
 constexpr int kStageBytes = kPeOff + kFKeys * kPeBytes;
-constexpr int kXBytes = 4 * 4 * 64 * 16;            // S^T exchange: [wave][quarter][lane] x 16 B
 constexpr int kLoadsPerBlock = 9;                   // per wave: 8 latent rows, 8 rope rows
 constexpr float kSlack = 8.f;                       // log2 units
 constexpr int kSgValu = 0x002;                      // sched_group_barrier class: VALU
@@ -80,13 +82,10 @@ struct FlashArgs {
     int causal;
 };
 
-// Chunk permutations (see the header).  gfx950 serves a 128-bit LDS read 16 lanes per
-// cycle (256 bytes, all 64 banks) and a 64-bit read 32 lanes per cycle.  Latent rows (1 KB):
-// the 16-byte chunk c of key k sits at c ^ swz(k & 15) within its 256-byte group, so the
-// 16 keys of a K fragment read hit 16 distinct chunks, and the 4 keys x 64 bytes of a
-// transposing read's half-wave hit 4 distinct 64-byte quarters.  Rope rows (128 B, two per
-// 256 bytes): chunk c of key k sits at c ^ ((k >> 1) & 7).
-__device__ __forceinline__ int swz(int k) { return ((k & 3) << 2) | ((k >> 2) & 3); }
+// Chunk permutations (see the header): latent rows (1 KB) keep chunk c of key k at
+// c ^ swz(k & 15) within its 256-byte group, swz = rotate left by one bit of four; rope
+// rows (128 B) keep chunk c of key k at c ^ ((k >> 1) & 7).
+__device__ __forceinline__ int swz(int k) { return ((k << 1) | (k >> 3)) & 15; }
 __device__ __forceinline__ int swz_pe(int k) { return (k >> 1) & 7; }
 
 template <int N>
@@ -98,7 +97,7 @@ __device__ __forceinline__ void wait_vm() {
 // Workgroup barrier for LDS data only: this wave's LDS accesses are complete (lgkmcnt(0)),
 // then s_barrier.  __syncthreads() would also wait for every outstanding global load
 // (vmcnt(0)), i.e. drain the ring of direct-to-LDS prefetches.  The empty asm statements
-// keep the compiler from moving memory accesses across the barrier.
+// and scheduling barriers keep the compiler from moving instructions across the barrier.
 __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
@@ -138,20 +137,40 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)reinterpret_cast<uintptr_t>((const lds_t*)p);
 }
 
-// The work of wave (rb, CW) of the workgroup; CW (depth half of S, column half of O) is a
-// template parameter, and so is the ring stage of each block step, so that every LDS
-// offset is an immediate.
-template <int NS, int CW>
-__device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, int wg) {
+// 16x16x32 bf16 MFMA: lane l supplies A[l%16][8(l/16) .. +7] and B[8(l/16) .. +7][l%16];
+// accumulator element i of lane l is D[4(l/16) + i][l%16].
+__device__ __forceinline__ v4f mfma16(v4u a, v4u b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a),
+                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+}
+
+// Max / sum over the 4 lanes l%16 + 16g (g = 0..3) that hold one row: v_permlane16_swap
+// pairs the rows of 16 lanes (0,1) and (2,3), v_permlane32_swap the two halves; given the
+// same value twice each returns the pair's two values in every lane, combined in one order.
+template <class Op>
+__device__ __forceinline__ float row4_reduce(float v, Op op) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    v = op(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                    false, false);
+    return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+template <int NS>
+__global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStageBytes];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l32 = lane & 31, h = lane >> 5, rb = wave & 1;
+    const int l16 = lane & 15, g = lane >> 4;
+    // the two row tiles of a batch are consecutive logical workgroups on one XCD
+    const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
 
     const int sp = wg % a.n_split;
     const int rt = (wg / a.n_split) % a.row_tiles;
     const int b = wg / (a.n_split * a.row_tiles);
     const int rows_b = a.Sq * a.H;
     const int r0 = rt * kFRows;
-    const int row = r0 + 32 * rb + l32;              // this lane's row within the batch
+    const int row = r0 + 16 * wave + l16;            // this lane's row within the batch
     const int rows_total = a.B * rows_b;
 
     // keys of this split; the causal rule (query s sees keys <= Sk - Sq + s) also trims
@@ -167,18 +186,19 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
     // the smallest row limit of the wave: its first row's (rows ascend with the lanes)
     const int lim_wave = __builtin_amdgcn_readfirstlane(lim);
 
-    // ---- Q^T fragments of depth half CW: lane l holds row l%32's depth 16s + 8h .. +7
+    // ---- Q^T fragments: lane l holds row l%16's K slots of group g for every step s:
+    // latent step s < 16 is depth 8(16g + s) .. +7 (the groups read four separate 256-byte
+    // quarters of a key row, which keeps the K fragment reads free of bank conflicts),
+    // rope step 16 + q is rope depth 8(4q + g) .. +7
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qa + (int64_t)b * rows_b * kFR);
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.qr + (int64_t)b * rows_b * kFD);
     const uint32_t qmask = oob_mask(row, rows_b);
-    v4u qf[kHSteps];
+    v4u qf[kQSteps];
     #pragma unroll
-    for (int i = 0; i < kHSteps; ++i) {
-        const int s = kHSteps * CW + i;
-        qf[i] = s < kRSteps
-                    ? load16(rq, ((uint32_t)row * kLatBytes + 32u * s + 16u * h) | qmask)
-                    : load16(rr, ((uint32_t)row * kPeBytes + 32u * (s - kRSteps) + 16u * h) | qmask);
-    }
+    for (int s = 0; s < kQSteps; ++s)
+        qf[s] = s < kRSteps
+                    ? load16(rq, ((uint32_t)row * kLatBytes + 256u * g + 16u * s) | qmask)
+                    : load16(rr, ((uint32_t)row * kPeBytes + 64u * (s - kRSteps) + 16u * g) | qmask);
 
     // ---- direct global->LDS staging of key blocks: wave w loads keys 8w .. 8w+7
     const v4i rk = rsrc_words(a.ckv + (int64_t)b * a.key_stride * kFR);
@@ -210,73 +230,57 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
     };
 
     // ---- per-lane LDS offsets of the fragments
-    // K fragment of step s: key l32, logical chunk 2s + h = 16(s/8) + (2(s%8) + h), the low
-    // four bits permuted by swz(l32 & 15); rope step s' reads chunk 2s' + h of the rope row
-    const int fk = swz(l32 & 15);
-    uint32_t k_off[8];
+    // K fragment (A operand) of key half kh (keys 16kh + l%16), latent step s: logical chunk
+    // 16g + s of the latent row (held at 16g + (s ^ swz(key & 15))); rope step 16 + q:
+    // chunk 4q + g of the rope row
+    const int fk = swz(l16);   // (16kh + l16) & 15 == l16
+    uint32_t k_off[16];
     #pragma unroll
-    for (int q = 0; q < 8; ++q) k_off[q] = l32 * kLatBytes + 16u * ((2 * q + h) ^ fk);
-    uint32_t p_off[4];
+    for (int s = 0; s < 16; ++s) k_off[s] = l16 * kLatBytes + 256u * g + 16u * (s ^ fk);
+    uint32_t p_off[2];
     #pragma unroll
-    for (int q = 0; q < 4; ++q)
-        p_off[q] = kPeOff + l32 * kPeBytes + 16u * ((2 * q + h) ^ swz_pe(l32));
-    // V^T fragment of 32-col block mb, K step t, half r2: lane (group G = l/16, j = l%16,
-    // q = j/4, c = j%4) addresses key 16t + 8r2 + 4h + q, cols 32mb + 16(G%2) + 4c .. +3,
-    // i.e. logical chunk 4mb + 2(G%2) + c/2 = 16(mb/4) + (4(mb%4) + 2(G%2) + c/2)
-    uint32_t v_off[8];   // [r2][mb % 4]
+    for (int q = 0; q < 2; ++q)
+        p_off[q] = kPeOff + l16 * kPeBytes + 16u * ((4 * q + g) ^ swz_pe(l16));
+    // V^T fragment (A operand) of 16-col block mb, half r2: lane (g, j = l%16, q = j/4,
+    // c = j%4) addresses key 16r2 + 4g + q, cols 16mb + 4c .. +3, i.e. logical chunk
+    // 2mb + c/2 = 16(mb/8) + (2(mb%8) + c/2), half c%2
+    uint32_t v_off[8];   // [mb % 8]
     {
-        const int G = lane >> 4, j = lane & 15, q = j >> 2, c = j & 3;
+        const int j = lane & 15, q = j >> 2, c = j & 3;
+        const int kx = 4 * g + q, fv = swz(kx);   // (16r2 + kx) & 15 == kx
         #pragma unroll
-        for (int r2 = 0; r2 < 2; ++r2) {
-            const int kx = 8 * r2 + 4 * h + q, fv = swz(kx);
-            #pragma unroll
-            for (int m4 = 0; m4 < 4; ++m4) {
-                const int chunk = 4 * m4 + 2 * (G & 1) + (c >> 1);   // low 4 bits of col/8
-                v_off[4 * r2 + m4] = kx * kLatBytes + 16u * (chunk ^ fv) + 8u * (c & 1);
-            }
+        for (int m8 = 0; m8 < 8; ++m8) {
+            const int chunk = 2 * m8 + (c >> 1);
+            v_off[m8] = kx * kLatBytes + 16u * (chunk ^ fv) + 8u * (c & 1);
         }
     }
-    v4f* xw = reinterpret_cast<v4f*>(smem + NS * kStageBytes) + wave * 256 + lane;
-    const v4f* xr = reinterpret_cast<const v4f*>(smem + NS * kStageBytes) + (wave ^ 2) * 256 + lane;
 
-    v16f O[kColBlocks];
+    v4f O[kColBlocks];
     #pragma unroll
-    for (int i = 0; i < kColBlocks; ++i) O[i] = v16f{};
+    for (int i = 0; i < kColBlocks; ++i) O[i] = v4f{};
     float m_run = -INFINITY, l_run = 0.f;
-    uint32_t pk[8] = {0, 0, 0, 0, 0, 0, 0, 0};   // P^T of the previous block, bf16 pairs
+    uint32_t pk[4] = {0, 0, 0, 0};   // P^T of the previous block, bf16 pairs
 
-    // V^T fragments of the block in stage ST for K step tk (keys 16tk + {0..3, 8..11} + 4h),
-    // and the MFMAs that fold them into O^T with P^T of that block
-    auto read_v = [&](auto st_tag, int tk, v8bf* va) __attribute__((always_inline)) {
+    // V^T fragments of column blocks [c0, c0 + N) of the block in stage ST (K slots: keys
+    // 4g + 0..3, then 16 + 4g + 0..3)
+    auto read_v = [&](auto st_tag, int c0, auto n_tag, v4u* va) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
+        constexpr int N = decltype(n_tag)::value;
         const uint8_t* st = smem + ST * kStageBytes;
         #pragma unroll
-        for (int i = 0; i < kColBlocks; ++i) {
-            const int mb = kColBlocks * CW + i;
-            const uint32_t imm = 256u * (mb >> 2) + 16384u * tk;
-            const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                (lds_v4bf*)(st + v_off[mb & 3] + imm));
+        for (int i = 0; i < N; ++i) {
+            const int mb = c0 + i;
+            const uint32_t off = v_off[mb & 7] + 256u * (mb >> 3);
+            const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(st + off));
             const v4bf hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                (lds_v4bf*)(st + v_off[4 + (mb & 3)] + imm));   // row offset includes 8r2
-            va[i] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+                (lds_v4bf*)(st + off + 16 * kLatBytes));
+            va[i] = __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
         }
     };
-    auto mma_v = [&](int tk, const v8bf* va) __attribute__((always_inline)) {
-        const v4u pb = {pk[4 * tk], pk[4 * tk + 1], pk[4 * tk + 2], pk[4 * tk + 3]};
-        #pragma unroll
-        for (int i = 0; i < kColBlocks; ++i)
-            O[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va[i], __builtin_bit_cast(v8bf, pb),
-                                                           O[i], 0, 0, 0);
-    };
-    auto pv = [&](auto st_tag, int tk) __attribute__((always_inline)) {
-        v8bf va[kColBlocks];
-        read_v(st_tag, tk, va);
-        mma_v(tk, va);
-    };
+    using Half = std::integral_constant<int, kColBlocks / 2>;
 
-    // One 32-key block j held in ring stage ST.  Block j's scores, exchange and softmax run
-    // together with block j-1's P.V (stage ST-1): the first half of that P.V covers the
-    // exchange writes before the barrier, the second half interleaves with the softmax.
+    // One 32-key block j held in ring stage ST: its scores, then block j-1's P.V with
+    // block j's softmax spread between the MFMAs.
     auto step = [&](int j, auto st_tag, auto has_prev) __attribute__((always_inline)) {
         constexpr int ST = decltype(st_tag)::value;
         constexpr bool PREV = decltype(has_prev)::value;
@@ -295,106 +299,88 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
 
         const uint8_t* st = smem + ST * kStageBytes;
 
-        // partial S^T over this wave's 18 depth steps; K fragment reads run kWin steps ahead
+        // S^T of block j: two 16-key halves x 18 K steps; K fragment reads kWin ahead
         constexpr int kWin = 6;
         auto read_k = [&](int i) __attribute__((always_inline)) {
-            const int s = kHSteps * CW + i;
-            const uint32_t off = s < kRSteps ? k_off[s & 7] + 256u * (s >> 3)
-                                             : p_off[(s - kRSteps) & 3];
+            const int kh = i & 1, s = i >> 1;
+            const uint32_t off = s < kRSteps ? k_off[s] + kh * 16 * kLatBytes
+                                             : p_off[s - kRSteps] + kh * 16 * kPeBytes;
             return *reinterpret_cast<const v4u*>(st + off);
         };
         v4u kf[kWin];
         #pragma unroll
         for (int i = 0; i < kWin; ++i) kf[i] = read_k(i);
-        v8bf va0[kColBlocks];
-        if constexpr (PREV) read_v(std::integral_constant<int, SP>{}, 0, va0);
-        v16f sa = v16f{};
+        // the first half of block j-1's V^T fragments are read during the score MFMAs
+        v4u va[kColBlocks / 2];
+        if constexpr (PREV) read_v(std::integral_constant<int, SP>{}, 0, Half{}, va);
+        v4f s0 = v4f{}, s1 = v4f{};
         #pragma unroll
-        for (int i = 0; i < kHSteps; ++i) {
+        for (int i = 0; i < 2 * kQSteps; ++i) {
             const v4u cur = kf[i % kWin];
-            if (i + kWin < kHSteps) kf[i % kWin] = read_k(i + kWin);
-            sa = Mma<bf16_t>::sub(cur, qf[i], 0, sa);
+            if (i + kWin < 2 * kQSteps) kf[i % kWin] = read_k(i + kWin);
+            if (i & 1) s1 = mfma16(cur, qf[i >> 1], s1);
+            else s0 = mfma16(cur, qf[i >> 1], s0);
         }
-        #pragma unroll
-        for (int q = 0; q < 4; ++q)
-            xw[64 * q] = v4f{sa[4 * q], sa[4 * q + 1], sa[4 * q + 2], sa[4 * q + 3]};
-        if constexpr (PREV) mma_v(0, va0);
-        // issue order of this region: the first K window, the V^T reads of block j-1, the
-        // score MFMAs with the remaining K reads between them, the exchange writes, then
-        // block j-1's first P.V half
         __builtin_amdgcn_sched_group_barrier(kSgDsRd, kWin, 0);
-        if constexpr (PREV) __builtin_amdgcn_sched_group_barrier(kSgDsRd, 2 * kColBlocks, 0);
+        if constexpr (PREV) __builtin_amdgcn_sched_group_barrier(kSgDsRd, kColBlocks, 0);
         #pragma unroll
-        for (int i = 0; i < kHSteps - kWin; ++i) {
+        for (int i = 0; i < 2 * kQSteps - kWin; ++i) {
             __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
             __builtin_amdgcn_sched_group_barrier(kSgDsRd, 1, 0);
         }
         __builtin_amdgcn_sched_group_barrier(kSgMfma, kWin, 0);
-        __builtin_amdgcn_sched_group_barrier(kSgDsWr, 4, 0);
-        if constexpr (PREV) __builtin_amdgcn_sched_group_barrier(kSgMfma, kColBlocks, 0);
-        lds_barrier();   // both halves of every row block's S^T are in LDS
-        v8bf va1[kColBlocks];
-        if constexpr (PREV) read_v(std::integral_constant<int, SP>{}, 1, va1);
-        v16f sc;
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const v4f o = xr[64 * q];
-            #pragma unroll
-            for (int e = 0; e < 4; ++e)   // the same operand order in both waves
-                sc[4 * q + e] = CW == 0 ? sa[4 * q + e] + o[e] : o[e] + sa[4 * q + e];
-        }
-        if constexpr (PREV) mma_v(1, va1);
+        __builtin_amdgcn_sched_barrier(0);
 
-        // online softmax of block j; element i of lane l is key kb + 8(i/4) + 4h + i%4 of
-        // row l%32
-        // Work on the raw scores: c > 0, so max(s) * c is exactly max(s * c), and
-        // p = 2^(s c - m) is one fma and one v_exp_f32.  Masked keys get s = -inf.  Blocks
-        // whose every key is visible to every row of the wave skip the mask.
+        // online softmax of block j: lane l holds keys 4g + i (s0) and 16 + 4g + i (s1) of
+        // row l%16.  Raw scores: c > 0, so max(s) * c is exactly max(s * c), and
+        // p = 2^(s c - m) is one fma and one v_exp_f32.  Masked keys get s = -inf.
         const int kb = k_lo + kFKeys * j;
         if (kb + kFKeys - 1 > lim_wave) {
             #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int key = kb + 8 * (i >> 2) + 4 * h + (i & 3);
-                sc[i] = key <= lim ? sc[i] : -INFINITY;
+            for (int i = 0; i < 4; ++i) {
+                s0[i] = kb + 4 * g + i <= lim ? s0[i] : -INFINITY;
+                s1[i] = kb + 16 + 4 * g + i <= lim ? s1[i] : -INFINITY;
             }
         }
-        float bm = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
-        #pragma unroll
-        for (int i = 3; i < 16; i += 2) bm = fmaxf(fmaxf(bm, sc[i]), sc[i + 1] );
-        {
-            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm),
-                                                             __float_as_uint(bm), false, false);
-            bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * a.c;
-        }
+        float bm = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                         fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+        bm = row4_reduce(bm, OpMax{}) * a.c;
         const bool raise = bm > m_run + kSlack;
         // 2^(m_run - bm) is 0 on a row's first raise (m_run = -inf); other rows keep 1
         const float f = raise ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
+        // the second half of block j-1's V^T fragments, then its P.V (old scale)
+        v4u vb[kColBlocks / 2];
+        if constexpr (PREV) {
+            read_v(std::integral_constant<int, SP>{}, kColBlocks / 2, Half{}, vb);
+            const v4u pb = {pk[0], pk[1], pk[2], pk[3]};
+            #pragma unroll
+            for (int i = 0; i < kColBlocks / 2; ++i) O[i] = mfma16(va[i], pb, O[i]);
+            #pragma unroll
+            for (int i = 0; i < kColBlocks / 2; ++i)
+                O[kColBlocks / 2 + i] = mfma16(vb[i], pb, O[kColBlocks / 2 + i]);
+        }
         m_run = raise ? bm : m_run;
         // a row with no visible key so far has m_run = -inf and every s = -inf: p = 0
         const float m_neg = m_run == -INFINITY ? 0.f : -m_run;
-        float ls = 0.f;
+        float p[8];
         #pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-            const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.c, m_neg));
-            const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i + 1], a.c, m_neg));
-            ls += p0 + p1;
-            pk[i >> 1] = pack_bf16x2(p0, p1);
+        for (int i = 0; i < 4; ++i) {
+            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], a.c, m_neg));
+            p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], a.c, m_neg));
         }
+        const float ls = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
         l_run = l_run * f + ls;
-        // the probabilities are computed here, between block j-1's MFMAs, not sunk past the
-        // rescale branch below
-        asm volatile("" ::"v"(pk[0]), "v"(pk[1]), "v"(pk[2]), "v"(pk[3]), "v"(pk[4]), "v"(pk[5]),
-                     "v"(pk[6]), "v"(pk[7]), "v"(l_run));
-        // issue order of this region: the exchange and V^T reads, then block j-1's second
-        // P.V half with the softmax VALU work spread between its MFMAs
-        __builtin_amdgcn_sched_group_barrier(kSgDsRd, PREV ? 4 + 2 * kColBlocks : 4, 0);
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
         if constexpr (PREV) {
+            __builtin_amdgcn_sched_group_barrier(kSgDsRd, kColBlocks, 0);
             #pragma unroll
             for (int i = 0; i < kColBlocks; ++i) {
                 __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgValu, 10, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgValu, 2, 0);
             }
         }
+        asm volatile("" ::"v"(pk[0]), "v"(pk[1]), "v"(pk[2]), "v"(pk[3]), "v"(l_run));
         // rescale after block j-1's P.V (which is in the old scale) has been accumulated
         if (__builtin_amdgcn_ballot_w64(raise)) {
             #pragma unroll
@@ -419,45 +405,34 @@ __device__ __forceinline__ void flash_wave(const FlashArgs& a, uint8_t* smem, in
     }
     if (nb > 0) {
         // block nb-1 sits in stage (nb-1) % NS; no later loads overwrite it
+        auto last = [&](auto st_tag) __attribute__((always_inline)) {
+            v4u va[kColBlocks];
+            read_v(st_tag, 0, std::integral_constant<int, kColBlocks>{}, va);
+            const v4u pb = {pk[0], pk[1], pk[2], pk[3]};
+            #pragma unroll
+            for (int i = 0; i < kColBlocks; ++i) O[i] = mfma16(va[i], pb, O[i]);
+        };
         switch ((nb - 1) % NS) {
-            case 0: pv(std::integral_constant<int, 0>{}, 0); pv(std::integral_constant<int, 0>{}, 1); break;
-            case 1: pv(std::integral_constant<int, 1 % NS>{}, 0); pv(std::integral_constant<int, 1 % NS>{}, 1); break;
-            case 2: pv(std::integral_constant<int, 2 % NS>{}, 0); pv(std::integral_constant<int, 2 % NS>{}, 1); break;
-            default: pv(std::integral_constant<int, 3 % NS>{}, 0); pv(std::integral_constant<int, 3 % NS>{}, 1); break;
+            case 0: last(std::integral_constant<int, 0>{}); break;
+            case 1: last(std::integral_constant<int, 1 % NS>{}); break;
+            case 2: last(std::integral_constant<int, 2 % NS>{}); break;
+            default: last(std::integral_constant<int, 3 % NS>{}); break;
         }
     }
 
-    // ---- this split's partial state: O columns 256CW .., and (CW = 0) m and l
-    {
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run),
-                                                         __float_as_uint(l_run), false, false);
-        l_run = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    }
+    // ---- this split's partial state: O (lane l: row l%16, columns 16mb + 4g .. +3), m, l
+    l_run = row4_reduce(l_run, OpSum{});
     if (row < rows_b) {
         const int64_t slot = (int64_t)sp * rows_total + (int64_t)b * rows_b + row;
-        if (CW == 0 && h == 0) {
+        if (g == 0) {
             a.m[slot] = m_run;
             a.l[slot] = l_run;
         }
-        float* orow = a.o + slot * kFR + 256 * CW;
+        float* orow = a.o + slot * kFR;
         #pragma unroll
-        for (int i = 0; i < kColBlocks; ++i) {
-            #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const v4f v = {O[i][4 * g], O[i][4 * g + 1], O[i][4 * g + 2], O[i][4 * g + 3]};
-                *reinterpret_cast<v4f*>(orow + 32 * i + 8 * g + 4 * h) = v;
-            }
-        }
+        for (int i = 0; i < kColBlocks; ++i)
+            *reinterpret_cast<v4f*>(orow + 16 * i + 4 * g) = O[i];
     }
-}
-
-template <int NS>
-__global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStageBytes + kXBytes];
-    // the two row tiles of a batch are consecutive logical workgroups on one XCD
-    const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
-    if ((threadIdx.x >> 6) < 2) flash_wave<NS, 0>(a, smem, wg);
-    else flash_wave<NS, 1>(a, smem, wg);
 }
 
 constexpr int kFStages = 4;   // LDS ring depth

@@ -41,7 +41,8 @@ def lib():
     for n in ("mla_q_absorbed_workspace_bytes", "mla_attention_workspace_bytes",
               "mla_gemm_workspace_bytes", "mla_ctx_workspace_bytes", "mla_out_workspace_bytes",
               "mla_attention_streaming_workspace_bytes", "mla_kv_append_workspace_bytes",
-              "mla_o_proj_workspace_bytes", "mla_attention_paged_workspace_bytes"):
+              "mla_o_proj_workspace_bytes", "mla_attention_paged_workspace_bytes",
+              "mla_attn_ctx_workspace_bytes"):
         getattr(L, n).restype = ctypes.c_size_t
     return L
 
@@ -143,6 +144,34 @@ def test_attention_validation(lib):
     st = lib.mla_attention(F32, None, *args, ctypes.c_double(13.85), 0, P16, P16,
                            ctypes.c_size_t(1 << 30), None)
     assert st == MLA_ERR_INVALID_ARGUMENT and "dims" in _err(lib)
+
+
+def test_attn_ctx_validation_and_workspace(lib):
+    """The fused 3a+3b+3c entry point: bf16 at kv_rank 512 / rope 64 only; its workspace
+    is the split partials (a scratch row when one split covers the keys)."""
+    d = dsv3(128, 1, 4989)
+    assert lib.mla_attn_ctx_workspace_bytes(F32, ctypes.byref(d), 0) == 0
+    ws = lib.mla_attn_ctx_workspace_bytes(BF16, ctypes.byref(d), 0)
+    assert 0 < ws <= 128 * 128 * 4 + 256          # one split: the row-maximum scratch only
+    d1 = dsv3(1, 1, 4989)
+    ws1 = lib.mla_attn_ctx_workspace_bytes(BF16, ctypes.byref(d1), 0)
+    assert ws1 >= 2 * 128 * (512 + 2) * 4          # several splits: partial ctx, m, l
+    args = [P16] * 4
+    st = lib.mla_attn_ctx(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, P16,
+                          P16, ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_UNSUPPORTED and "bf16" in _err(lib)
+    d.kv_rank = 256
+    st = lib.mla_attn_ctx(BF16, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, P16,
+                          P16, ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_UNSUPPORTED
+    d = dsv3(2, 3, 2)
+    st = lib.mla_attn_ctx(BF16, ctypes.byref(d), *args, ctypes.c_double(13.85), 1, P16, P16,
+                          P16, ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "sk >= sq" in _err(lib)
+    d = dsv3(1, 1, 4989)
+    st = lib.mla_attn_ctx(BF16, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, P16,
+                          P16, ctypes.c_size_t(ws1 - 1), None)
+    assert st == MLA_ERR_WORKSPACE and "too small" in _err(lib)
 
 
 def test_q_absorbed_validation(lib):
@@ -267,7 +296,7 @@ def ext():
 
 def test_binding_surface(ext):
     for name in ("q_absorbed", "mla_attention", "gemm", "rmsnorm", "rope", "absorb", "scores",
-                 "combine", "ctx", "out", "rope_inv_freq"):
+                 "combine", "ctx", "out", "rope_inv_freq", "attn_ctx"):
         assert callable(getattr(ext, name))
 
 

@@ -132,3 +132,25 @@ def test_fused_cfg4_full_size_vs_split_path(ext, monkeypatch):
     pick = [0, 77, 127]
     ref = oracle(tuple(t[pick] for t in args[:4]) + (args[4],), False)
     torch.testing.assert_close(fused[pick], ref, **TOL)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", [(2, 1, 300, False), (1, 1, 4989, False),
+                                            (2, 4, 500, True)])
+def test_attn_ctx_step_vs_oracle(ext, B, Sq, Sk, causal):
+    """The per-step fused entry point: ctx / row_sum equals the oracle's softmax-weighted
+    c_kv (fp32 reference on the bf16 values, P rounded to bf16 only in the kernel), and
+    feeding (ctx, row_sum) to the 3d step gives mla_attention's output bit for bit."""
+    qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=3 * Sk + B)
+    ctx, rs = ext.attn_ctx(gpu(qa), gpu(qr), gpu(ck), gpu(pe), SCALE, causal)
+    assert ctx.dtype == torch.float32 and ctx.shape == (B, Sq, D.n_heads, D.kv_rank)
+    assert rs.shape == (B * Sq * D.n_heads,) and bool((rs > 0).all())
+    got = (ctx / rs.reshape(B, Sq, D.n_heads, 1)).cpu()
+    s = (torch.einsum("bqhr,bkr->bqhk", qa.double(), ck.double())
+         + torch.einsum("bqhd,bkd->bqhk", qr.double(), pe.double())) / SCALE
+    if causal:
+        s = s.masked_fill(~R.causal_mask(Sq, Sk)[None, :, None, :], float("-inf"))
+    ref = torch.einsum("bqhk,bkr->bqhr", torch.softmax(s, dim=-1), ck.double()).float()
+    torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
+    out = ext.out(ctx, rs, gpu(wuv))
+    full = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
+    assert torch.equal(out, full)
