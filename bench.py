@@ -74,8 +74,8 @@ def step_work(B, Sq, Sk, dims, e=4):
         "3b": (3 * flat * P, 4 * (3 * flat * P + flat)),
         "3c": (2 * flat * Sk * R, 4 * (flat * Sk + flat * P) + e * (B * Sk * R) + 4 * flat * R),
         "3d": (2 * flat * R * V, 4 * flat * R + e * H * V * R + 4 * flat + e * flat * V),
-        # 3a+3b+3c fused (the bf16 layer's attention kernel): queries and cache read once,
-        # the unnormalised ctx and row sums written once
+        # 3a+3b+3c fused (the layer's attention kernel at kv_rank 512 / rope 64): queries
+        # and cache read once, the unnormalised ctx and row sums written once
         "3abc": (2 * flat * Sk * (R + D) + 2 * flat * Sk * R,
                  e * (flat * (R + D) + B * Sk * (R + D)) + 4 * flat * R + 4 * flat),
     }
@@ -241,9 +241,12 @@ def main():
     steps_sum = sum(step_us.values())
     same = (o_steps - out).abs().max().item()
 
-    # bf16: the layer's attention runs 3a+3b+3c as one fused kernel (attn_ctx), timed here
-    # the same way; the per-step 3a/3b/3c above are the decomposed kernels
-    fused_attn = dname == "bf16"
+    # the layer's attention runs 3a+3b+3c as one fused kernel (attn_ctx) at the
+    # DeepSeek-V3 widths (mla_attention; the causal streaming path keeps the per-step
+    # kernels), timed here the same way; the per-step 3a/3b/3c above are the decomposed
+    # kernels
+    fused_attn = (not causal and dims.kv_rank == 512 and dims.rope == 64
+                  and os.environ.get("MLA_ATTENTION_PATH") != "split")
     if fused_attn:
         qa_f, qr_f = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
                                     g["positions"], dims.nope, dims.rope, eps)

@@ -720,7 +720,7 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
     m.def("ctx", &step_ctx, "3c: unnormalised ctx", py::arg("scores"), py::arg("alpha"),
           py::arg("c_kv"), py::arg("Sq"), py::arg("H"));
     m.def("out", &step_out, "3d", py::arg("ctx"), py::arg("row_sum"), py::arg("W_uv"));
-    m.def("attn_ctx", &step_attn_ctx, "3a+3b+3c fused (bf16): returns [ctx, row_sum]",
+    m.def("attn_ctx", &step_attn_ctx, "3a+3b+3c fused (bf16 or fp32): returns [ctx, row_sum]",
           py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),
           py::arg("scale"), py::arg("causal") = false);
     m.def("score_tile", []() { return mla_score_tile(); });

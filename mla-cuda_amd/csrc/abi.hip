@@ -280,12 +280,12 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     return L;
 }
 
-// 3a+3b+3c as one fused pass over the cache (flash.hip), for bf16 storage at the
+// 3a+3b+3c as one fused pass over the cache (flash.hip), for bf16 and fp32 storage at the
 // DeepSeek-V3 widths.  MLA_ATTENTION_PATH=split selects the per-step kernels instead.
 FlashProblem flash_problem(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* qr,
                            const void* ckv, const void* pe, double scale, int causal) {
-    (void)dt;
     FlashProblem p;
+    p.bf16 = is_bf16(dt);
     p.qa = qa; p.qr = qr; p.ckv = ckv; p.pe = pe;
     p.B = d->batch; p.Sq = d->sq; p.Sk = d->sk; p.H = d->heads; p.R = d->kv_rank;
     p.D = d->rope; p.key_stride = d->sk;
@@ -295,10 +295,10 @@ FlashProblem flash_problem(mla_dtype_t dt, const mla_dims_t* d, const void* qa, 
 }
 
 bool flash_eligible(mla_dtype_t dt, const mla_dims_t* d) {
-    if (!is_bf16(dt)) return false;
-    // per-lane 32-bit buffer offsets: a batch's query rows and key rows (1 KB each)
+    // per-lane 32-bit buffer offsets: a batch's query rows and key rows (R elements each)
     constexpr int64_t kRange = 0x7fffffff;
-    if ((int64_t)d->sq * d->heads * 1024 >= kRange || (int64_t)d->sk * 1024 >= kRange)
+    const int64_t row_bytes = 512 * (is_bf16(dt) ? 2 : 4);
+    if ((int64_t)d->sq * d->heads * row_bytes >= kRange || (int64_t)d->sk * row_bytes >= kRange)
         return false;
     return flash_supported(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
 }
@@ -796,8 +796,8 @@ int mla_attn_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorb
     MLA_CHECK(check_scale(scale));
     if (!flash_eligible(dtype, dims))
         return fail(MLA_ERR_UNSUPPORTED,
-                    "fused attention needs bf16, kv_rank 512 and rope 64 (got %s, %d, %d)",
-                    is_bf16(dtype) ? "bf16" : "float32", dims->kv_rank, dims->rope);
+                    "fused attention needs kv_rank 512 and rope 64 (got %d, %d)",
+                    dims->kv_rank, dims->rope);
     MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
     MLA_CHECK(check_ptr(q_rope, "q_rope"));
     MLA_CHECK(check_ptr(c_kv, "c_kv"));

@@ -131,6 +131,16 @@ __device__ __forceinline__ void dma16(v4i rsrc, uint32_t lds, uint32_t voff, uin
                  : "s"(lds), "v"(voff), "s"(rsrc), "s"(soff)
                  : "memory", "m0");
 }
+// The same with soffset 0 and an immediate offset OFF (< 4096), which the instruction adds
+// to both addresses: the bytes at voff + OFF land at lds + OFF + 16*lane.
+template <int OFF>
+__device__ __forceinline__ void dma16_imm(v4i rsrc, uint32_t lds, uint32_t voff) {
+    static_assert(OFF >= 0 && OFF < 4096, "12-bit buffer offset");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen offset:%3 lds"
+                 :
+                 : "s"(lds), "v"(voff), "s"(rsrc), "i"(OFF)
+                 : "memory", "m0");
+}
 #pragma clang diagnostic pop
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -199,6 +209,10 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
         qf[s] = s < kRSteps
                     ? load16(rq, ((uint32_t)row * kLatBytes + 256u * g + 16u * s) | qmask)
                     : load16(rr, ((uint32_t)row * kPeBytes + 64u * (s - kRSteps) + 16u * g) | qmask);
+    // Q is in registers before the first key block is requested: the cache loads are not
+    // seen by the compiler's wait-count tracking, which would otherwise keep waiting on Q
+    // (and so on every cache load issued since) inside the key loop
+    wait_vm<0>();
 
     // ---- direct global->LDS staging of key blocks: wave w loads keys 8w .. 8w+7
     const v4i rk = rsrc_words(a.ckv + (int64_t)b * a.key_stride * kFR);
@@ -435,6 +449,307 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ fp32 variant
+// Same pass with fp32 storage on the 16x16x4 fp32 MFMA (lane l supplies A[l%16][l/16] and
+// B[l/16][l%16]; accumulator element i of lane l is D[4(l/16) + i][l%16]).  A 16-key block
+// is 272 MFMAs of 32 cycles per wave, and a SIMD runs fp32 MFMAs and VALU instructions one
+// after the other (they do not overlap, and every switch between the two costs a drain of
+// the MFMA pipeline), so the kernel keeps VALU work per block to a few dozen instructions:
+//   S^T[16 keys x 16 rows]: lane group g reads the depth quarter [128g, 128g + 128) of the
+//     latent row in 16-byte chunks (4 depths per read feed 4 MFMAs) and the rope depths
+//     [16g, 16g + 16); the wave's Q^T lives in 144 VGPRs
+//   P^T: element i of lane l is key 4(l/16) + i of row l%16 -- the B operand of K step i
+//   O^T[512 x 16]: 32 accumulator blocks; block (mh, r) holds columns 32mh + 2j + r, so a
+//     64-bit read of V gives two blocks' A operands
+//   exponentials against a fixed per-row reference (k32Headroom): no O rescaling, no row
+//     reductions per block
+//   cache loads: the buffer descriptor is rebased on each block's first key in scalar
+//     registers and its range ends at the split's last key, so out-of-range keys read as
+//     zeros with no per-lane address work
+// LDS per stage: the rope rows of the NS stages first (16 x 256 B each, chunk c of key k at
+// c ^ swz(k & 15)), then the latent rows (16 keys x 2 KB at a pitch of 2064 bytes).  The K
+// reads (16 keys at one offset) and the 64-bit V reads (4 keys x 16 consecutive column
+// pairs) are free of bank conflicts (measured), and every LDS read is a per-lane base plus
+// an immediate offset: stages 0-1 and 2-3 of the latent region each have their own base.
+constexpr int k32Keys = 16;
+constexpr int k32Pitch = kFR * 4 + 16;
+constexpr int k32PeBytes = kFD * 4;
+constexpr int k32PeStage = k32Keys * k32PeBytes;     // 4 KB
+constexpr int k32LatStage = k32Keys * k32Pitch;      // 33024 B
+constexpr int k32StageBytes = k32PeStage + k32LatStage;
+constexpr int k32LatReads = kFR / 16;               // 32: 16-byte K reads per lane, latent
+constexpr int k32PeReads = kFD / 16;                // 4: rope
+constexpr int k32Loads = 9;                         // cache loads per wave and block
+
+__device__ __forceinline__ v4f mfma16f(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Reference point of a row's exponentials in the fp32 pass: p = 2^(s*c - m_ref) with m_ref
+// the first visible block's maximum, kept while the row's maximum stays below
+// m_ref + k32Headroom.  P then stays below 2^64, the row sum below 2^64 times the key count,
+// and O needs no rescaling (a rescale of the 128 accumulator registers costs more in the
+// compiler's register assignment for every block than the multiplies themselves).  A row
+// that outgrows its reference restarts the workgroup's pass with the larger reference.
+constexpr float k32Headroom = 64.f;
+constexpr int k32MaxPasses = 8;
+
+// Descriptor words of `bytes` bytes at base + off (off in bytes); wave-uniform arguments
+// (readfirstlane keeps the words in scalar registers, as the load instruction needs).
+__device__ __forceinline__ v4i rsrc_span(uint64_t base, uint32_t off, uint32_t bytes) {
+    const uint64_t p = base + off;
+    return v4i{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)p),
+               __builtin_amdgcn_readfirstlane((int32_t)((uint32_t)(p >> 32) & 0xffff)),
+               __builtin_amdgcn_readfirstlane((int32_t)bytes), 0x00020000};
+}
+
+template <int NS>
+__global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
+    static_assert(NS == 4, "two latent bases cover stages 0-1 and 2-3");
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * k32StageBytes];
+    __shared__ int restart[2];   // [block parity]: some row outgrew its reference
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, g = lane >> 4;
+    const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
+    if (tid < 2) restart[tid] = 0;   // read only after the first block's barrier
+    const float* qa = reinterpret_cast<const float*>(a.qa);
+    const float* qr = reinterpret_cast<const float*>(a.qr);
+
+    const int sp = wg % a.n_split;
+    const int rt = (wg / a.n_split) % a.row_tiles;
+    const int b = wg / (a.n_split * a.row_tiles);
+    const int rows_b = a.Sq * a.H;
+    const int r0 = rt * kFRows;
+    const int row = r0 + 16 * wave + l16;
+    const int rows_total = a.B * rows_b;
+
+    const int k_lo = sp * a.keys_per_split;
+    int k_hi = min(a.Sk, k_lo + a.keys_per_split);
+    int lim = k_hi - 1;
+    if (a.causal) {
+        lim = min(lim, a.Sk - a.Sq + min(row, rows_b - 1) / a.H);
+        k_hi = min(k_hi, a.Sk - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
+    }
+    const int nb = k_hi > k_lo ? (k_hi - k_lo + k32Keys - 1) / k32Keys : 0;
+    const int lim_wave = __builtin_amdgcn_readfirstlane(lim);
+    const int k_hi_s = __builtin_amdgcn_readfirstlane(k_hi);
+
+    // ---- Q^T: read r of lane group g is depths 128g + 4r .. +3 (latent), 16g + 4r' (rope)
+    const __amdgpu_buffer_rsrc_t rq = make_rsrc(qa + (int64_t)b * rows_b * kFR);
+    const __amdgpu_buffer_rsrc_t rr = make_rsrc(qr + (int64_t)b * rows_b * kFD);
+    const uint32_t qmask = oob_mask(row, rows_b);
+    v4u qf[k32LatReads + k32PeReads];
+    #pragma unroll
+    for (int r = 0; r < k32LatReads; ++r)
+        qf[r] = load16(rq, ((uint32_t)row * (kFR * 4) + 512u * g + 16u * r) | qmask);
+    #pragma unroll
+    for (int r = 0; r < k32PeReads; ++r)
+        qf[k32LatReads + r] = load16(rr, ((uint32_t)row * k32PeBytes + 64u * g + 16u * r) | qmask);
+    wait_vm<0>();   // as in flash_kernel: no wait on Q inside the key loop
+
+    // ---- direct global->LDS staging: wave w loads keys 4w .. 4w+3 of a block
+    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv) +
+                             (uint64_t)b * a.key_stride * (kFR * 4);
+    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe) +
+                             (uint64_t)b * a.key_stride * k32PeBytes;
+    const uint32_t lds0 = lds_addr(smem);
+    // latent: instruction q fills half q%2 of key q/2's row; rope (one instruction for the
+    // 4 keys): lane i fills chunk i%16 of key 4w + i/16, i.e. loads its logical chunk
+    // (i%16) ^ swz(key & 15)
+    uint32_t lat_lane[4];
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) lat_lane[k] = 16u * lane + (uint32_t)k * (kFR * 4);
+    const uint32_t pe_lane = (uint32_t)(lane >> 4) * k32PeBytes +
+                             16u * ((lane & 15) ^ swz((4 * wave + (lane >> 4)) & 15));
+    auto issue = [&](int j, int stage) __attribute__((always_inline)) {
+        const int kb = __builtin_amdgcn_readfirstlane(k_lo + k32Keys * j + 4 * wave);
+        const uint32_t left = (uint32_t)max(0, k_hi_s - kb);   // keys of this wave in range
+        const v4i rk = rsrc_span(ck_base, (uint32_t)kb * (kFR * 4), min(left, 4u) * (kFR * 4));
+        const v4i rp = rsrc_span(pe_base, (uint32_t)kb * k32PeBytes, min(left, 4u) * k32PeBytes);
+        const uint32_t st = __builtin_amdgcn_readfirstlane(
+            lds0 + NS * k32PeStage + stage * k32LatStage + 4 * wave * k32Pitch);
+        const uint32_t st_pe = __builtin_amdgcn_readfirstlane(
+            lds0 + stage * k32PeStage + 4 * wave * k32PeBytes);
+        #pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            dma16_imm<0>(rk, st + k * k32Pitch, lat_lane[k]);
+            dma16_imm<1024>(rk, st + k * k32Pitch, lat_lane[k]);   // second KB of the row
+        }
+        dma16_imm<0>(rp, st_pe, pe_lane);
+    };
+
+    // ---- per-lane LDS bases (byte offsets from smem)
+    // (the asm statements hide that the second base is the first plus a constant, which
+    // the compiler would otherwise add back per read: the sum exceeds the 16-bit offset)
+    const uint32_t lat0 = NS * k32PeStage;
+    uint32_t k_base[2] = {lat0 + l16 * k32Pitch + 512u * g,
+                          lat0 + 2 * k32LatStage + l16 * k32Pitch + 512u * g};
+    uint32_t v_base[2] = {lat0 + 4 * g * k32Pitch + 8u * l16,
+                          lat0 + 2 * k32LatStage + 4 * g * k32Pitch + 8u * l16};
+    asm volatile("" : "+v"(k_base[1]), "+v"(v_base[1]));
+    uint32_t p_off[k32PeReads];
+    #pragma unroll
+    for (int r = 0; r < k32PeReads; ++r)
+        p_off[r] = l16 * k32PeBytes + 16u * ((4 * g + r) ^ swz(l16));
+
+    v4f O[2 * 16];   // [mh][r]
+    float m_ref = -INFINITY, m_neg = 0.f, thr = -INFINITY, l_run = 0.f;
+    int pass = 1;
+
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    auto k_read = [&](auto st_tag, int r) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_tag)::value;
+        const uint32_t off = r < k32LatReads
+                                 ? k_base[ST >> 1] + (ST & 1) * k32LatStage + 16u * r
+                                 : p_off[r - k32LatReads] + ST * k32PeStage;
+        return *reinterpret_cast<const v4u*>(smem + off);
+    };
+    // V read t: K step i = t / 16 (keys 4g + i), column pair 32mh + 2*l16 with mh = t % 16
+    auto v_read = [&](auto st_tag, int t) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_tag)::value;
+        return *reinterpret_cast<const v2u*>(smem + v_base[ST >> 1] + (ST & 1) * k32LatStage +
+                                             (t >> 4) * k32Pitch + 128u * (t & 15));
+    };
+
+    // One block; returns true (before any work) when a row asked for a restart in block j-1.
+    auto step = [&](int j, auto st_tag) __attribute__((always_inline)) {
+        constexpr int ST = decltype(st_tag)::value;
+        constexpr int KW = 4;    // K reads in flight ahead of the MFMAs that use them
+        constexpr int VW = 8;    // V reads in flight
+        constexpr int KR = k32LatReads + k32PeReads;
+        const int ahead = min(nb - 1, j + NS - 2) - j;   // blocks issued after block j
+        if (ahead >= 2) wait_vm<2 * k32Loads>();
+        else if (ahead == 1) wait_vm<k32Loads>();
+        else wait_vm<0>();
+        lds_barrier();   // block j is in LDS for every wave; every wave is past block j-1
+        if (j > 0 && __builtin_amdgcn_readfirstlane(restart[(j - 1) & 1])) return true;
+        if (j + NS - 1 < nb) issue(j + NS - 1, (ST + NS - 1) % NS);
+
+        // S^T: 36 16-byte K reads per lane, 4 MFMAs each, alternating two accumulators
+        v4u kq[KW];
+        #pragma unroll
+        for (int r = 0; r < KW; ++r) kq[r] = k_read(st_tag, r);
+        v4f s2[2] = {v4f{}, v4f{}};
+        #pragma unroll
+        for (int r = 0; r < KR; ++r) {
+            const v4u cur = kq[r % KW];
+            if (r + KW < KR) kq[r % KW] = k_read(st_tag, r + KW);
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+                s2[q & 1] = mfma16f(__uint_as_float(cur[q]), __uint_as_float(qf[r][q]), s2[q & 1]);
+        }
+        // the first V reads of the P.V pass go out under the last score MFMAs
+        v2u vq[VW];
+        #pragma unroll
+        for (int t = 0; t < VW; ++t) vq[t] = v_read(st_tag, t);
+        __builtin_amdgcn_sched_group_barrier(kSgDsRd, KW, 0);
+        #pragma unroll
+        for (int r = 0; r < KR - KW; ++r) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRd, 1, 0);
+        }
+        #pragma unroll
+        for (int r = 0; r < KW; ++r) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 4, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRd, VW / KW, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        v4f sc = s2[0] + s2[1];
+
+        // softmax numerators: element i of lane l is key kb + 4g + i of row l%16
+        const int kb = k_lo + k32Keys * j;
+        if (kb + k32Keys - 1 > lim_wave) {
+            #pragma unroll
+            for (int i = 0; i < 4; ++i) sc[i] = kb + 4 * g + i <= lim ? sc[i] : -INFINITY;
+        }
+        const float smax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+        // a row's first visible keys set its reference (O is still zero for it); a row
+        // whose maximum passes reference + headroom asks for a restart (rows are uniform
+        // over their 4 lanes after the reduction, and NaN scores take this path too)
+        if (__builtin_amdgcn_ballot_w64(!(smax * a.c <= thr))) {
+            const float bm = row4_reduce(smax, OpMax{}) * a.c;
+            const bool over = pass < k32MaxPasses && m_ref != -INFINITY && bm > thr;
+            if (__builtin_amdgcn_ballot_w64(over) && lane == 0) restart[j & 1] = 1;
+            if (m_ref == -INFINITY || over) {
+                m_ref = bm;
+                m_neg = bm == -INFINITY ? 0.f : -bm;
+                thr = bm + k32Headroom;
+            }
+        }
+        float p[4];
+        #pragma unroll
+        for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.c, m_neg));
+        l_run += (p[0] + p[1]) + (p[2] + p[3]);
+        __builtin_amdgcn_sched_barrier(0);   // all VALU work of the block before its P.V
+
+        // O^T += V^T . P^T: K step i (keys 4g + i) is 16 64-bit V reads x 2 MFMAs
+        #pragma unroll
+        for (int t = 0; t < 64; ++t) {
+            const v2u cur = vq[t % VW];
+            if (t + VW < 64) vq[t % VW] = v_read(st_tag, t + VW);
+            const int mh = t & 15, i = t >> 4;
+            O[2 * mh] = mfma16f(__uint_as_float(cur[0]), p[i], O[2 * mh]);
+            O[2 * mh + 1] = mfma16f(__uint_as_float(cur[1]), p[i], O[2 * mh + 1]);
+        }
+        #pragma unroll
+        for (int t = 0; t < 64 - VW; ++t) {
+            __builtin_amdgcn_sched_group_barrier(kSgMfma, 2, 0);
+            __builtin_amdgcn_sched_group_barrier(kSgDsRd, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(kSgMfma, 2 * VW, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        return false;
+    };
+
+    // A pass over the split's keys; repeated (from the first key, every wave) only when a
+    // row's maximum outgrew its reference point.  Each repeat raises that row's reference by
+    // more than k32Headroom; after k32MaxPasses passes the last one stands (exponents past
+    // 2^128 then overflow to inf, as a plain softmax without the max subtraction would).
+    for (;; ++pass) {
+        #pragma unroll
+        for (int i = 0; i < 32; ++i) O[i] = v4f{};
+        l_run = 0.f;
+        #pragma unroll
+        for (int j = 0; j < NS - 1; ++j)
+            if (j < nb) issue(j, j);
+        bool again = false;
+        for (int j0 = 0; j0 < nb && !again; j0 += NS) {
+            again = step(j0, std::integral_constant<int, 0>{});
+            if (!again && j0 + 1 < nb) again = step(j0 + 1, std::integral_constant<int, 1>{});
+            if (!again && j0 + 2 < nb) again = step(j0 + 2, std::integral_constant<int, 2>{});
+            if (!again && j0 + 3 < nb) again = step(j0 + 3, std::integral_constant<int, 3>{});
+        }
+        if (nb == 0) break;
+        if (!again) {   // the last block's request
+            lds_barrier();
+            again = __builtin_amdgcn_readfirstlane(restart[(nb - 1) & 1]) != 0;
+            if (!again) break;
+        }
+        wait_vm<0>();    // no cache load still writes the ring
+        lds_barrier();   // every wave has read the request
+        if (tid < 2) restart[tid] = 0;
+        lds_barrier();
+    }
+
+    // ---- partial state: lane l holds row l%16, columns 32mh + 8g + 2i + r of O[mh][r][i]
+    l_run = row4_reduce(l_run, OpSum{});
+    if (row < rows_b) {
+        const int64_t slot = (int64_t)sp * rows_total + (int64_t)b * rows_b + row;
+        if (g == 0) {
+            a.m[slot] = m_ref;
+            a.l[slot] = l_run;
+        }
+        float* orow = a.o + slot * kFR;
+        #pragma unroll
+        for (int mh = 0; mh < 16; ++mh) {
+            const v4f lo = {O[2 * mh][0], O[2 * mh + 1][0], O[2 * mh][1], O[2 * mh + 1][1]};
+            const v4f hi = {O[2 * mh][2], O[2 * mh + 1][2], O[2 * mh][3], O[2 * mh + 1][3]};
+            *reinterpret_cast<v4f*>(orow + 32 * mh + 8 * g) = lo;
+            *reinterpret_cast<v4f*>(orow + 32 * mh + 8 * g + 4) = hi;
+        }
+    }
+}
+
 constexpr int kFStages = 4;   // LDS ring depth
 
 // ctx = sum_s w_s O_s, row_sum = sum_s w_s l_s, w_s = 2^(m_s - max_s m_s); one thread per
@@ -474,13 +789,14 @@ FlashPlan plan_flash(const FlashProblem& p) {
     FlashPlan f;
     f.row_tiles = (p.Sq * p.H + kFRows - 1) / kFRows;
     const int base = p.B * f.row_tiles;
-    const int blocks = (p.Sk + kFKeys - 1) / kFKeys;
+    const int block_keys = p.bf16 ? kFKeys : k32Keys;
+    const int blocks = (p.Sk + block_keys - 1) / block_keys;
     // about one workgroup per CU (the LDS ring admits one per CU), at least 4 key blocks
     // per split
     int split = std::max(1, (kNumCUs + base / 2) / base);
     split = std::min(split, std::max(1, blocks / 4));
     const int per = (blocks + split - 1) / split;
-    f.keys_per_split = per * kFKeys;
+    f.keys_per_split = per * block_keys;
     f.n_split = (blocks + per - 1) / per;
     const size_t rows = (size_t)p.B * p.Sq * p.H;
     // split partials (O, m, l); with one split O and l go straight to ctx / row_sum and
@@ -516,7 +832,10 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     a.c = 1.4426950408889634f / p.scale;
     a.causal = p.causal ? 1 : 0;
     const int grid = p.B * f.row_tiles * f.n_split;
-    hipLaunchKernelGGL(flash_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
+    if (p.bf16)
+        hipLaunchKernelGGL(flash_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
+    else
+        hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || f.n_split == 1) return e;
     const int64_t n = (int64_t)rows * (kFR / 4);

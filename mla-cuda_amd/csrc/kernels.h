@@ -116,11 +116,12 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream);
 
 constexpr int kScoreTile = 128;  // keys per softmax partial (one 3a workgroup's key tile)
 
-// ---------------------------------------------------------------- 3a+3b+3c fused (bf16)
+// ---------------------------------------------------------------- 3a+3b+3c fused
 // One pass over the cache per key split: ctx [rows, R] (unnormalised) and row_sum [rows]
-// for 3d, as 3c and 3b produce them.  bf16 storage, R = 512, D = 64 only.
+// for 3d, as 3c and 3b produce them.  bf16 or fp32 storage, R = 512, D = 64 only.
 struct FlashProblem {
-    const void* qa = nullptr;    // [B*Sq*H, R]   bf16
+    bool bf16 = true;            // storage dtype (else fp32)
+    const void* qa = nullptr;    // [B*Sq*H, R]
     const void* qr = nullptr;    // [B*Sq*H, D]
     const void* ckv = nullptr;   // [B, key_stride, R]
     const void* pe = nullptr;    // [B, key_stride, D]

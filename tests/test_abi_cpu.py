@@ -147,20 +147,22 @@ def test_attention_validation(lib):
 
 
 def test_attn_ctx_validation_and_workspace(lib):
-    """The fused 3a+3b+3c entry point: bf16 at kv_rank 512 / rope 64 only; its workspace
-    is the split partials (a scratch row when one split covers the keys)."""
+    """The fused 3a+3b+3c entry point: kv_rank 512 / rope 64 only (bf16 or fp32); its
+    workspace is the split partials (a scratch row when one split covers the keys)."""
     d = dsv3(128, 1, 4989)
-    assert lib.mla_attn_ctx_workspace_bytes(F32, ctypes.byref(d), 0) == 0
-    ws = lib.mla_attn_ctx_workspace_bytes(BF16, ctypes.byref(d), 0)
-    assert 0 < ws <= 128 * 128 * 4 + 256          # one split: the row-maximum scratch only
+    for dt in (F32, BF16):
+        ws = lib.mla_attn_ctx_workspace_bytes(dt, ctypes.byref(d), 0)
+        assert 0 < ws <= 128 * 128 * 4 + 256      # one split: the row-maximum scratch only
     d1 = dsv3(1, 1, 4989)
     ws1 = lib.mla_attn_ctx_workspace_bytes(BF16, ctypes.byref(d1), 0)
     assert ws1 >= 2 * 128 * (512 + 2) * 4          # several splits: partial ctx, m, l
+    assert lib.mla_attn_ctx_workspace_bytes(F32, ctypes.byref(d1), 0) >= 2 * 128 * 514 * 4
     args = [P16] * 4
+    d.kv_rank = 256
+    assert lib.mla_attn_ctx_workspace_bytes(F32, ctypes.byref(d), 0) == 0
     st = lib.mla_attn_ctx(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, P16,
                           P16, ctypes.c_size_t(1 << 30), None)
-    assert st == MLA_ERR_UNSUPPORTED and "bf16" in _err(lib)
-    d.kv_rank = 256
+    assert st == MLA_ERR_UNSUPPORTED and "kv_rank 512" in _err(lib)
     st = lib.mla_attn_ctx(BF16, ctypes.byref(d), *args, ctypes.c_double(13.85), 0, P16, P16,
                           P16, ctypes.c_size_t(1 << 30), None)
     assert st == MLA_ERR_UNSUPPORTED

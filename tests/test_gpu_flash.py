@@ -1,12 +1,13 @@
-"""GPU parity of the fused bf16 attention (3a+3b+3c in one pass over the cache, flash.hip).
+"""GPU parity of the fused attention (3a+3b+3c in one pass over the cache, flash.hip).
 
-mla_attention takes the fused path for bf16 at R = 512, D = 64; MLA_ATTENTION_PATH=split
-selects the per-step kernels.  Both are held to the fp32 oracle on the very bf16 values
-the kernels read, at the bf16 tolerance rtol 2e-2 (atol 2e-2 on O(1) outputs), and to each
-other.  Shapes cover a partial last key block, a single key, key splits merged across
-workgroups (small B), causal masks with Sq > 1, splits that a tile's causal limit leaves
-empty, row tiles that do not fill 64 rows (H = 40, H = 1), and a row maximum that keeps
-rising by more than the kernel's rescale slack.
+mla_attention takes the fused path for bf16 and fp32 at R = 512, D = 64;
+MLA_ATTENTION_PATH=split selects the per-step kernels.  Both are held to the float64
+oracle on the very values the kernels read -- bf16 at rtol/atol 2e-2 (P is rounded to bf16
+inside the kernel), fp32 at rtol/atol 1e-4 -- and to each other.  Shapes cover a partial
+last key block, a single key, key splits merged across workgroups (small B), causal masks
+with Sq > 1, splits that a tile's causal limit leaves empty, row tiles that do not fill 64
+rows (H = 40, H = 1), and a row maximum that keeps rising: past the bf16 kernel's rescale
+slack, and past the fp32 kernel's exponent headroom (which restarts its pass).
 """
 
 from __future__ import annotations
@@ -24,7 +25,10 @@ DEV = "cuda:0"
 D = R.DSV3
 SCALE = math.sqrt(D.qk_head)
 BF = torch.bfloat16
-TOL = dict(rtol=2e-2, atol=2e-2)
+F32 = torch.float32
+TOLS = {BF: dict(rtol=2e-2, atol=2e-2), F32: dict(rtol=1e-4, atol=1e-4)}
+TOL = TOLS[BF]
+DTYPES = pytest.mark.parametrize("dt", [BF, F32], ids=["bf16", "f32"])
 
 
 @pytest.fixture(scope="module")
@@ -39,9 +43,9 @@ def gpu(t):
     return t.to(DEV)
 
 
-def inputs(B, Sq, Sk, H=D.n_heads, seed=0, qs=0.05):
+def inputs(B, Sq, Sk, H=D.n_heads, seed=0, qs=0.05, dt=BF):
     g = torch.Generator().manual_seed(seed)
-    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(BF)  # noqa: E731
+    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(dt)  # noqa: E731
     return (mk(B, Sq, H, D.kv_rank, sc=qs), mk(B, Sq, H, D.rope, sc=qs), mk(B, Sk, D.kv_rank),
             mk(B, Sk, D.rope), mk(H, D.v, D.kv_rank, sc=1 / math.sqrt(D.kv_rank)))
 
@@ -60,7 +64,7 @@ def run(ext, args, causal, path=None, monkeypatch=None):
     finally:
         if path is not None:
             monkeypatch.delenv("MLA_ATTENTION_PATH")
-    assert out.dtype == BF
+    assert out.dtype == args[0].dtype
     return out.float().cpu()
 
 
@@ -78,25 +82,29 @@ SHAPES = [
 ]
 
 
+@DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,causal", SHAPES)
-def test_fused_vs_oracle(ext, B, Sq, Sk, causal):
-    args = inputs(B, Sq, Sk, seed=Sk + B)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOL)
+def test_fused_vs_oracle(ext, dt, B, Sq, Sk, causal):
+    args = inputs(B, Sq, Sk, seed=Sk + B, dt=dt)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[dt])
 
 
+@DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,causal", SHAPES[2:7])
-def test_fused_vs_split_path(ext, monkeypatch, B, Sq, Sk, causal):
-    args = inputs(B, Sq, Sk, seed=7 * Sk + B)
+def test_fused_vs_split_path(ext, monkeypatch, dt, B, Sq, Sk, causal):
+    args = inputs(B, Sq, Sk, seed=7 * Sk + B, dt=dt)
     fused = run(ext, args, causal)
     split = run(ext, args, causal, "split", monkeypatch)
-    torch.testing.assert_close(fused, split, rtol=1e-2, atol=1e-2)
+    tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
+    torch.testing.assert_close(fused, split, **tol)
 
 
+@DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,H,causal", [(2, 3, 257, 40, False), (1, 512, 1024, 1, True),
                                               (3, 1, 100, 1, False)])
-def test_fused_partial_row_tiles(ext, B, Sq, Sk, H, causal):
-    args = inputs(B, Sq, Sk, H=H, seed=H + Sk)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOL)
+def test_fused_partial_row_tiles(ext, dt, B, Sq, Sk, H, causal):
+    args = inputs(B, Sq, Sk, H=H, seed=H + Sk, dt=dt)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[dt])
 
 
 def test_fused_rising_row_max(ext):
@@ -115,32 +123,59 @@ def test_fused_rising_row_max(ext):
     torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOL)
 
 
-def test_fused_deterministic(ext):
-    args = [gpu(t) for t in inputs(3, 1, 2000, seed=5)]
+@pytest.mark.parametrize("jump", [100.0, 400.0])
+def test_fused_f32_restart(ext, jump):
+    """fp32 keeps each row's exponentials against the first visible block's maximum; a
+    row whose later maximum passes it by the 2^64 headroom restarts the pass.  Here the
+    scores rise by `jump` (log2 units) over the keys in steps of ~0.35 per key, so the
+    kernel restarts one (100) or several (400) times; a one-key spike at key 900 of
+    another sequence restarts from a late block."""
+    B, Sq, Sk = 2, 1, 1200
+    qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=13, dt=F32)
+    u = torch.randn(D.kv_rank, generator=torch.Generator().manual_seed(14))
+    u = u / u.norm()
+    qa = (u * 64.0).expand(B, Sq, D.n_heads, D.kv_rank).contiguous()
+    # t_k = s_k / sqrt(192) * log2(e); s_k = 64 * a * k with a chosen so t_(Sk-1) = jump
+    a = jump / (Sk - 1) * SCALE / math.log2(math.e) / 64.0
+    ramp = torch.arange(Sk, dtype=torch.float32) * a
+    ck = ck * 0.05
+    ck[0] += ramp[:, None] * u
+    ck[1, 900] += (jump / math.log2(math.e) * SCALE / 64.0) * u
+    args = (qa, qr, ck, pe, wuv)
+    torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOLS[F32])
+
+
+@DTYPES
+def test_fused_deterministic(ext, dt):
+    args = [gpu(t) for t in inputs(3, 1, 2000, seed=5, dt=dt)]
     a = ext.mla_attention(*args, SCALE)
     b = ext.mla_attention(*args, SCALE)
     assert torch.equal(a, b)
 
 
-def test_fused_cfg4_full_size_vs_split_path(ext, monkeypatch):
-    """B=128, Sq=1, Sk=4989 (cfg4 attention): the fused and per-step paths agree on every
-    sequence; the oracle checks three of them."""
-    args = inputs(128, 1, 4989, seed=0, qs=0.1)
+@DTYPES
+def test_fused_full_size_vs_split_path(ext, monkeypatch, dt):
+    """B=128, Sq=1, Sk=4989 (the cfg2 / cfg4 attention): the fused and per-step paths agree
+    on every sequence; the oracle checks three of them."""
+    args = inputs(128, 1, 4989, seed=0, qs=0.1, dt=dt)
     fused = run(ext, args, False)
     split = run(ext, args, False, "split", monkeypatch)
-    torch.testing.assert_close(fused, split, rtol=1e-2, atol=1e-2)
+    tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
+    torch.testing.assert_close(fused, split, **tol)
     pick = [0, 77, 127]
     ref = oracle(tuple(t[pick] for t in args[:4]) + (args[4],), False)
-    torch.testing.assert_close(fused[pick], ref, **TOL)
+    torch.testing.assert_close(fused[pick], ref, **TOLS[dt])
 
 
+@DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,causal", [(2, 1, 300, False), (1, 1, 4989, False),
                                             (2, 4, 500, True)])
-def test_attn_ctx_step_vs_oracle(ext, B, Sq, Sk, causal):
+def test_attn_ctx_step_vs_oracle(ext, dt, B, Sq, Sk, causal):
     """The per-step fused entry point: ctx / row_sum equals the oracle's softmax-weighted
-    c_kv (fp32 reference on the bf16 values, P rounded to bf16 only in the kernel), and
-    feeding (ctx, row_sum) to the 3d step gives mla_attention's output bit for bit."""
-    qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=3 * Sk + B)
+    c_kv (float64 reference on the values the kernel reads; bf16 P is rounded only in the
+    kernel), and feeding (ctx, row_sum) to the 3d step gives mla_attention's output bit
+    for bit."""
+    qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=3 * Sk + B, dt=dt)
     ctx, rs = ext.attn_ctx(gpu(qa), gpu(qr), gpu(ck), gpu(pe), SCALE, causal)
     assert ctx.dtype == torch.float32 and ctx.shape == (B, Sq, D.n_heads, D.kv_rank)
     assert rs.shape == (B * Sq * D.n_heads,) and bool((rs > 0).all())
@@ -150,7 +185,8 @@ def test_attn_ctx_step_vs_oracle(ext, B, Sq, Sk, causal):
     if causal:
         s = s.masked_fill(~R.causal_mask(Sq, Sk)[None, :, None, :], float("-inf"))
     ref = torch.einsum("bqhk,bkr->bqhr", torch.softmax(s, dim=-1), ck.double()).float()
-    torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
+    tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
+    torch.testing.assert_close(got, ref, **tol)
     out = ext.out(ctx, rs, gpu(wuv))
     full = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
     assert torch.equal(out, full)

@@ -69,8 +69,9 @@ def test_paged_attention_matches_oracle(ext, page, lens, causal, Sq):
     torch.testing.assert_close(out, ref, **TOL)
 
 
-def test_paged_equals_dense_bitwise(ext):
-    """Full lengths and pages laid out in sequence order: the dense cache, the same answer."""
+def test_paged_equals_dense_bitwise(ext, monkeypatch):
+    """Full lengths and pages laid out in sequence order: the dense cache's per-step path
+    gives the same answer bit for bit (the dense fused path agrees to fp32 rounding)."""
     B, Sk, page = 3, 4992, 64
     g = torch.Generator().manual_seed(31)
     qa = torch.randn(B, 1, D.n_heads, D.kv_rank, generator=g)
@@ -81,11 +82,15 @@ def test_paged_equals_dense_bitwise(ext):
     mp = Sk // page
     table = torch.arange(B * mp, dtype=torch.int32).reshape(B, mp)
     sl = torch.full((B,), Sk, dtype=torch.int32)
+    fused = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
+    monkeypatch.setenv("MLA_ATTENTION_PATH", "split")
     dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
+    monkeypatch.delenv("MLA_ATTENTION_PATH")
     paged = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck.reshape(-1, page, D.kv_rank)),
                                     gpu(pe.reshape(-1, page, D.rope)), gpu(table), gpu(sl),
                                     gpu(wuv), SCALE)
     assert torch.equal(dense.cpu(), paged.cpu())
+    torch.testing.assert_close(fused.cpu(), paged.cpu(), rtol=1e-4, atol=1e-4)
 
 
 def test_paged_attention_bf16(ext):
