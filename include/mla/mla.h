@@ -183,11 +183,12 @@ int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores,
             int32_t ld_scores, const float* alpha, const void* c_kv, float* ctx,
             void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* 3a + 3b + 3c as one pass over the cache (bf16 with kv_rank = 512 and rope = 64 only;
- * MLA_ERR_UNSUPPORTED otherwise): ctx [B*Sq*H, kv_rank] and row_sum [B*Sq*H], float32,
- * such that ctx[f] / row_sum[f] = sum_k softmax_k(t[f, :]) c_kv[b, k] -- what mla_ctx and
- * mla_combine produce, up to one positive factor per row shared by ctx[f] and row_sum[f]
- * (an online softmax keeps its own running maximum).  mla_attention runs this for bf16.
+/* 3a + 3b + 3c as one pass over the cache (bf16 or float32 with kv_rank = 512 and
+ * rope = 64 only; MLA_ERR_UNSUPPORTED otherwise): ctx [B*Sq*H, kv_rank] and row_sum
+ * [B*Sq*H], float32, such that ctx[f] / row_sum[f] = sum_k softmax_k(t[f, :]) c_kv[b, k]
+ * -- what mla_ctx and mla_combine produce, up to one positive factor per row shared by
+ * ctx[f] and row_sum[f] (the kernels keep their own per-row reference maximum).
+ * mla_attention runs this at those widths.
  * Fuses the reference's mla_scores_kernel, mla_combine_kernel and mla_ctx_kernel
  * (mla_kernels.cu:808-1326). */
 size_t mla_attn_ctx_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal);

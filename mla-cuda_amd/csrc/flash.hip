@@ -1,10 +1,13 @@
-// 3a + 3b + 3c fused for bf16 storage: one pass over the latent cache per key split.
+// 3a + 3b + 3c fused: one pass over the latent cache per key split, for bf16 storage
+// (flash_kernel) and fp32 storage (flash32_kernel, further below).
 //
 // The per-step path materialises fp32 scores (3a), reduces per-tile softmax partials
 // (3b) and streams c_kv a second time for ctx (3c).  With bf16 storage that path is
 // HBM-bound on traffic it creates itself: at B=128, Sk=4989 it moves ~2.0 GB, of which
-// only 0.74 GB is the cache.  This kernel reads every key row once, keeps the softmax
-// state in registers and writes only the unnormalised ctx, its row sums and row maxima.
+// only 0.74 GB is the cache; in fp32 it is MFMA-bound and the extra passes cost the
+// score epilogue, the combine and a second launch tail.  These kernels read every key row
+// once, keep the softmax state in registers and write only the unnormalised ctx, its row
+// sums and row maxima.
 // The arithmetic is the reference's (mla_kernels.cu:971-1032, 1058-1079, 1247-1254):
 // s = q_absorbed.c_kv + q_rope.pe, softmax over s/scale, ctx = sum_k p_k c_kv[k]; only the
 // order of operations differs (an online softmax instead of per-tile partials).
