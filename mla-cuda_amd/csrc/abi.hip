@@ -1058,6 +1058,22 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
     float* ctx = at<float>(workspace, L.off_ctx);
     const int rows = dims->batch * dims->sq * dims->heads;
 
+    if (use_flash(dtype, dims)) {
+        // 3a+3b+3c fused over the pages (each sequence to its own length), then 3d
+        FlashProblem fp = flash_problem(dtype, dims, q_absorbed, q_rope, c_kv_pages, pe_pages,
+                                        scale, causal);
+        fp.seq_lens = seq_lens;
+        fp.block_table = block_table;
+        fp.page_size = page_size;
+        MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part),
+                                 stream),
+                    "fused paged attention launch");
+        GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
+        MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
+                    "3d launch");
+        return ok();
+    }
+
     // 3a over the pages, each sequence to its own length (keys past it score as masked)
     MLA_CHECK(run_scores(dtype, dims, q_absorbed, q_rope, c_kv_pages, pe_pages, scale, causal, p,
                          L.ld_p, m, l, stream, 0, 0, 0, seq_lens, block_table, page_size));

@@ -83,7 +83,25 @@ struct FlashArgs {
     int64_t key_stride;
     float c;           // log2(e) / scale
     int causal;
+    // ragged / paged keys (both optional): batch b has min(seq_lens[b], Sk) keys, and its
+    // key rows [j*page_size, (j+1)*page_size) are rows of page block_table[b*max_pages + j]
+    // of ckv / pe (page_size a multiple of 64, so no key block straddles a page)
+    const int* seq_lens;
+    const int* block_table;
+    int page_size, max_pages;
 };
+
+// Keys of batch b, and the cache row of key k (a wave-uniform key inside the sequence; a
+// key past it maps to row 0, which only out-of-range loads then address).
+__device__ __forceinline__ int flash_batch_keys(const FlashArgs& a, int b) {
+    return a.seq_lens ? min(load_uniform(a.seq_lens + b), a.Sk) : a.Sk;
+}
+__device__ __forceinline__ int64_t flash_key_row(const FlashArgs& a, int b, int k, int k_end) {
+    if (!a.block_table) return (int64_t)b * a.key_stride + k;
+    if (k >= k_end) return 0;
+    const int page = load_uniform(a.block_table + (int64_t)b * a.max_pages + k / a.page_size);
+    return (int64_t)page * a.page_size + k % a.page_size;
+}
 
 // Chunk permutations (see the header): latent rows (1 KB) keep chunk c of key k at
 // c ^ swz(k & 15) within its 256-byte group, swz = rotate left by one bit of four; rope
@@ -186,14 +204,15 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
     const int row = r0 + 16 * wave + l16;            // this lane's row within the batch
     const int rows_total = a.B * rows_b;
 
-    // keys of this split; the causal rule (query s sees keys <= Sk - Sq + s) also trims
+    // keys of this split; the causal rule (query s sees keys <= Sk_b - Sq + s) also trims
     // the range to the tile's last query
+    const int skb = flash_batch_keys(a, b);
     const int k_lo = sp * a.keys_per_split;
-    int k_hi = min(a.Sk, k_lo + a.keys_per_split);
+    int k_hi = min(skb, k_lo + a.keys_per_split);
     int lim = k_hi - 1;                              // last visible key of this lane's row
     if (a.causal) {
-        lim = min(lim, a.Sk - a.Sq + min(row, rows_b - 1) / a.H);
-        k_hi = min(k_hi, a.Sk - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
+        lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
+        k_hi = min(k_hi, skb - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
     }
     const int nb = k_hi > k_lo ? (k_hi - k_lo + kFKeys - 1) / kFKeys : 0;
     // the smallest row limit of the wave: its first row's (rows ascend with the lanes)
@@ -218,8 +237,6 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
     wait_vm<0>();
 
     // ---- direct global->LDS staging of key blocks: wave w loads keys 8w .. 8w+7
-    const v4i rk = rsrc_words(a.ckv + (int64_t)b * a.key_stride * kFR);
-    const v4i rp = rsrc_words(a.pe + (int64_t)b * a.key_stride * kFD);
     const uint32_t lds0 = lds_addr(smem);
     // rope rows of keys 8w .. 8w+7: lane i fills chunk i%8 of key 8w + i/8
     const uint32_t pe_lane = (uint32_t)(lane >> 3) * kPeBytes +
@@ -237,13 +254,17 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
         const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + stage * kStageBytes + 8 * wave * kLatBytes);
         const uint32_t st_pe = __builtin_amdgcn_readfirstlane(lds0 + stage * kStageBytes + kPeOff + 8 * wave * kPeBytes);
         const uint32_t kb_s = __builtin_amdgcn_readfirstlane(kb);
+        // descriptors at the cache row of the wave's first key (its 8 keys share a page)
+        const int64_t row0 = flash_key_row(a, b, (int)kb_s, __builtin_amdgcn_readfirstlane(k_hi));
+        const v4i rk = rsrc_words(a.ckv + row0 * kFR);
+        const v4i rp = rsrc_words(a.pe + row0 * kFD);
         #pragma unroll
         for (int q = 0; q < 8; ++q) {
             const uint32_t voff = (int)kb_s + q < k_hi ? lat_lane[q] : kOob;
-            dma16(rk, st + q * kLatBytes, voff, (kb_s + q) * kLatBytes);
+            dma16(rk, st + q * kLatBytes, voff, q * kLatBytes);
         }
         const uint32_t voff = kb + (lane >> 3) < k_hi ? pe_lane : kOob;
-        dma16(rp, st_pe, voff, kb_s * kPeBytes);
+        dma16(rp, st_pe, voff, 0);
     };
 
     // ---- per-lane LDS offsets of the fragments
@@ -526,12 +547,13 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     const int row = r0 + 16 * wave + l16;
     const int rows_total = a.B * rows_b;
 
+    const int skb = flash_batch_keys(a, b);
     const int k_lo = sp * a.keys_per_split;
-    int k_hi = min(a.Sk, k_lo + a.keys_per_split);
+    int k_hi = min(skb, k_lo + a.keys_per_split);
     int lim = k_hi - 1;
     if (a.causal) {
-        lim = min(lim, a.Sk - a.Sq + min(row, rows_b - 1) / a.H);
-        k_hi = min(k_hi, a.Sk - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
+        lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
+        k_hi = min(k_hi, skb - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
     }
     const int nb = k_hi > k_lo ? (k_hi - k_lo + k32Keys - 1) / k32Keys : 0;
     const int lim_wave = __builtin_amdgcn_readfirstlane(lim);
@@ -551,10 +573,8 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     wait_vm<0>();   // as in flash_kernel: no wait on Q inside the key loop
 
     // ---- direct global->LDS staging: wave w loads keys 4w .. 4w+3 of a block
-    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv) +
-                             (uint64_t)b * a.key_stride * (kFR * 4);
-    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe) +
-                             (uint64_t)b * a.key_stride * k32PeBytes;
+    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
+    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe);
     const uint32_t lds0 = lds_addr(smem);
     // latent: instruction q fills half q%2 of key q/2's row; rope (one instruction for the
     // 4 keys): lane i fills chunk i%16 of key 4w + i/16, i.e. loads its logical chunk
@@ -567,8 +587,10 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     auto issue = [&](int j, int stage) __attribute__((always_inline)) {
         const int kb = __builtin_amdgcn_readfirstlane(k_lo + k32Keys * j + 4 * wave);
         const uint32_t left = (uint32_t)max(0, k_hi_s - kb);   // keys of this wave in range
-        const v4i rk = rsrc_span(ck_base, (uint32_t)kb * (kFR * 4), min(left, 4u) * (kFR * 4));
-        const v4i rp = rsrc_span(pe_base, (uint32_t)kb * k32PeBytes, min(left, 4u) * k32PeBytes);
+        // the wave's 4 keys are consecutive cache rows (one page)
+        const uint64_t row0 = (uint64_t)flash_key_row(a, b, kb, k_hi_s);
+        const v4i rk = rsrc_span(ck_base + row0 * (kFR * 4), 0, min(left, 4u) * (kFR * 4));
+        const v4i rp = rsrc_span(pe_base + row0 * k32PeBytes, 0, min(left, 4u) * k32PeBytes);
         const uint32_t st = __builtin_amdgcn_readfirstlane(
             lds0 + NS * k32PeStage + stage * k32LatStage + 4 * wave * k32Pitch);
         const uint32_t st_pe = __builtin_amdgcn_readfirstlane(
@@ -795,7 +817,9 @@ FlashPlan plan_flash(const FlashProblem& p) {
     const int block_keys = p.bf16 ? kFKeys : k32Keys;
     const int blocks = (p.Sk + block_keys - 1) / block_keys;
     // about one workgroup per CU (the LDS ring admits one per CU), at least 4 key blocks
-    // per split
+    // per split.  (Ragged batches keep this plan: four splits per sequence at B=128 were
+    // measured slower -- the partials' write and merge cost more than the shorter
+    // sequences' idle CUs.)
     int split = std::max(1, (kNumCUs + base / 2) / base);
     split = std::min(split, std::max(1, blocks / 4));
     const int per = (blocks + split - 1) / split;
@@ -834,6 +858,12 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     a.key_stride = p.key_stride > 0 ? p.key_stride : p.Sk;
     a.c = 1.4426950408889634f / p.scale;
     a.causal = p.causal ? 1 : 0;
+    a.seq_lens = p.seq_lens;
+    a.block_table = p.block_table;
+    a.page_size = p.page_size;
+    a.max_pages = p.page_size > 0 ? p.Sk / p.page_size : 0;
+    if (p.block_table && (p.page_size <= 0 || p.page_size % 64 != 0 || p.Sk % p.page_size != 0))
+        return hipErrorInvalidValue;
     const int grid = p.B * f.row_tiles * f.n_split;
     if (p.bf16)
         hipLaunchKernelGGL(flash_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);

@@ -129,6 +129,13 @@ struct FlashProblem {
     int64_t key_stride = 0;      // key rows between batches (0: Sk)
     float scale = 1.f;           // divisor of the scores
     bool causal = false;
+    // ragged / paged keys (optional): batch b has min(seq_lens[b], Sk) keys; with a block
+    // table, ckv / pe are pools of pages of page_size rows (a multiple of 64, Sk a multiple
+    // of it) and key k of batch b is row k % page_size of page block_table[b*Sk/page_size
+    // + k/page_size]
+    const int32_t* seq_lens = nullptr;
+    const int32_t* block_table = nullptr;
+    int page_size = 0;
 };
 struct FlashPlan {
     int row_tiles = 1;           // 128-row tiles per batch

@@ -6,7 +6,9 @@ Pools are shuffled (a sequence's pages are scattered through the pool, interleav
 other sequences' pages and unused ones), lengths are ragged and not multiples of the page
 or tile sizes.  Tolerances: fp32 rtol/atol 1e-4, bf16 2e-2 against the fp32 oracle on the
 rounded inputs; a paged cache laid out like the dense one must give the dense result
-bit for bit.
+bit for bit.  mla_attention_paged runs the fused 3a+3b+3c kernels at the DeepSeek-V3
+widths (the block table read per key block); MLA_ATTENTION_PATH=split selects the per-step
+kernels, and both paths are checked.
 """
 
 from __future__ import annotations
@@ -39,6 +41,16 @@ def gpu(t):
     return t.to(DEV)
 
 
+PATHS = pytest.mark.parametrize("path", ["fused", "split"])
+
+
+def set_path(monkeypatch, path):
+    if path == "split":
+        monkeypatch.setenv("MLA_ATTENTION_PATH", "split")
+    else:
+        monkeypatch.delenv("MLA_ATTENTION_PATH", raising=False)
+
+
 def paged_inputs(B, Sq, lens, page, max_pages, seed, dtype=torch.float32, spare=5):
     """Queries ~ N(0,1); a shuffled pool of B*max_pages + spare pages ~ N(0,1)."""
     g = torch.Generator().manual_seed(seed)
@@ -53,13 +65,15 @@ def paged_inputs(B, Sq, lens, page, max_pages, seed, dtype=torch.float32, spare=
     return qa, qr, ck, pe, table, torch.tensor(lens, dtype=torch.int32), wuv
 
 
+@PATHS
 @pytest.mark.parametrize("page,lens,causal,Sq", [
     (64, [640, 1, 333, 65], False, 1),
     (128, [1000, 129, 500], False, 1),
     (64, [200, 77, 640], True, 4),
     (192, [576, 300], True, 2),
 ])
-def test_paged_attention_matches_oracle(ext, page, lens, causal, Sq):
+def test_paged_attention_matches_oracle(ext, monkeypatch, path, page, lens, causal, Sq):
+    set_path(monkeypatch, path)
     B = len(lens)
     max_pages = -(-max(lens) // page)
     qa, qr, ck, pe, table, sl, wuv = paged_inputs(B, Sq, lens, page, max_pages, seed=page + B)
@@ -69,9 +83,11 @@ def test_paged_attention_matches_oracle(ext, page, lens, causal, Sq):
     torch.testing.assert_close(out, ref, **TOL)
 
 
-def test_paged_equals_dense_bitwise(ext, monkeypatch):
-    """Full lengths and pages laid out in sequence order: the dense cache's per-step path
-    gives the same answer bit for bit (the dense fused path agrees to fp32 rounding)."""
+@PATHS
+def test_paged_equals_dense_bitwise(ext, monkeypatch, path):
+    """Full lengths and pages laid out in sequence order: the dense cache gives the same
+    answer bit for bit on either path."""
+    set_path(monkeypatch, path)
     B, Sk, page = 3, 4992, 64
     g = torch.Generator().manual_seed(31)
     qa = torch.randn(B, 1, D.n_heads, D.kv_rank, generator=g)
@@ -82,20 +98,18 @@ def test_paged_equals_dense_bitwise(ext, monkeypatch):
     mp = Sk // page
     table = torch.arange(B * mp, dtype=torch.int32).reshape(B, mp)
     sl = torch.full((B,), Sk, dtype=torch.int32)
-    fused = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
-    monkeypatch.setenv("MLA_ATTENTION_PATH", "split")
     dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
-    monkeypatch.delenv("MLA_ATTENTION_PATH")
     paged = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck.reshape(-1, page, D.kv_rank)),
                                     gpu(pe.reshape(-1, page, D.rope)), gpu(table), gpu(sl),
                                     gpu(wuv), SCALE)
     assert torch.equal(dense.cpu(), paged.cpu())
-    torch.testing.assert_close(fused.cpu(), paged.cpu(), rtol=1e-4, atol=1e-4)
 
 
-def test_paged_attention_bf16(ext):
+@PATHS
+def test_paged_attention_bf16(ext, monkeypatch, path):
     """bf16 with the layer's scaling (q and W_uv ~ 1/sqrt(kv_rank)), so the outputs are
     O(1) like the layer's and the bf16 tolerance is meaningful."""
+    set_path(monkeypatch, path)
     lens, page = [700, 64, 1], 64
     qa, qr, ck, pe, table, sl, wuv = paged_inputs(3, 1, lens, page, 11, seed=9)
     s = 1 / math.sqrt(D.kv_rank)
@@ -152,9 +166,11 @@ def test_paged_decode_step_end_to_end(ext):
     torch.testing.assert_close(out, ref, **TOL)
 
 
-def test_paged_attention_full_size_ragged(ext):
+@PATHS
+def test_paged_attention_full_size_ragged(ext, monkeypatch, path):
     """B=128 decode over a shuffled 64-key-page pool, lengths ragged in [1, 4989];
     oracle on three sequences."""
+    set_path(monkeypatch, path)
     B, page, max_pages = 128, 64, 78                  # 78 * 64 = 4992 >= 4989
     g = torch.Generator().manual_seed(41)
     lens = torch.randint(1, 4990, (B,), generator=g, dtype=torch.int32)
