@@ -9,7 +9,10 @@ in HBM.  The default workload is the headline decode shape: B=128, Sq=1, Sk=4989
 DeepSeek-V3 dims.  Output: ONE JSON line on stdout.
 
 Timed region: W untimed warm-up layers, then exactly K layers bracketed by
-torch.cuda.synchronize() on both sides and HIP events on the current stream.  A second,
+torch.cuda.synchronize() on both sides, each layer between its own pair of HIP events on
+the current stream and preceded (outside the pair) by a 512 MB device write that evicts
+the MALL and L2s; `value` is the mean per-layer time (median and a back-to-back figure
+beside it).  A second,
 separately timed pass runs the same kernels through the per-step ops with an event
 between consecutive steps; it gives each step's average launch duration, from which the
 per-step GFLOP/s, GB/s, MFMA % and HBM % (algorithmic work, formulas below) and the
@@ -194,22 +197,39 @@ def main():
                                                True)
         return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale)
 
-    # ---- timed region: the fused boundary calls
+    # ---- timed region: the fused boundary calls.  Each timed layer is preceded by a 512 MB
+    # device write outside its event pair, so no layer finds the previous one's weights or
+    # cache in the 256 MB MALL or the L2s; value = mean over the layers (median beside it).
     for _ in range(args.warmup):
         out = layer()
+    flush = torch.empty(512 << 18, dtype=torch.float32, device=dev)   # 512 MB
     torch.cuda.synchronize()
+    lev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t_wall = time.perf_counter()
+    for e0, e1 in lev:
+        flush.zero_()
+        e0.record()
+        out = layer()
+        e1.record()
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter() - t_wall
+    layer_ms = [e0.elapsed_time(e1) for e0, e1 in lev]
+    ms_per_step = statistics.mean(layer_ms)
+    ms_median = statistics.median(layer_ms)
+    print(f"[bench] fused layer, eager launches, flushed caches: mean {ms_per_step * 1e3:.1f} "
+          f"µs, median {ms_median * 1e3:.1f} µs over {args.steps} layers", file=sys.stderr,
+          flush=True)
+    # the same calls back to back (caches warm from the previous layer)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    t_wall = time.perf_counter()
     start.record()
     for _ in range(args.steps):
         out = layer()
     end.record()
     torch.cuda.synchronize()
-    t_wall = time.perf_counter() - t_wall
-    ms_per_step = start.elapsed_time(end) / args.steps
-    print(f"[bench] fused layer, eager launches: {ms_per_step * 1e3:.1f} µs/step over "
-          f"{args.steps} steps", file=sys.stderr, flush=True)
+    b2b_us = round(start.elapsed_time(end) / args.steps * 1e3, 2)
+    del flush
 
     # The same layer replayed from a HIP graph (captured once; every replay runs all of the
     # layer's kernels), as a serving loop would launch it.  Reported beside the eager
@@ -425,6 +445,9 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 4),
+        "median_us_per_step": round(ms_median * 1e3, 2),
+        "min_max_us_per_step": [round(min(layer_ms) * 1e3, 2), round(max(layer_ms) * 1e3, 2)],
+        "back_to_back_us_per_step": b2b_us,
         "graph_replay_us_per_step": graph_us,
         "higher_is_better": False,
         "scaling": "weak",
