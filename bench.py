@@ -53,7 +53,7 @@ CONFIGS = {
     "b1": (1, 1, 4989, "B=1 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
     "b8": (8, 1, 4989, "B=8 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
     "b32": (32, 1, 4989, "B=32 Sq=1 Sk=4989 fp32 decode (small-batch sweep)"),
-    "cfg5": (4, 128, 32768, "B=4 Sq=128 Sk=32768 fp32 causal chunked prefill (streaming attention)"),
+    "cfg5": (4, 128, 32768, "B=4 Sq=128 Sk=32768 fp32 causal chunked prefill (online-softmax attention)"),
 }
 
 
@@ -192,10 +192,9 @@ def main():
     def layer():
         qa, qr = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
                                 g["positions"], dims.nope, dims.rope, eps)
-        if causal:
-            return ext.mla_attention_streaming(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale,
-                                               True)
-        return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale)
+        # causal (cfg5) too: the fused pass streams the keys through its online softmax
+        # and keeps no score matrix
+        return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale, causal)
 
     # ---- timed region: the fused boundary calls.  Each timed layer is preceded by a 512 MB
     # device write outside its event pair, so no layer finds the previous one's weights or
@@ -290,10 +289,9 @@ def main():
     same = (o_steps - out).abs().max().item()
 
     # the layer's attention runs 3a+3b+3c as one fused kernel (attn_ctx) at the
-    # DeepSeek-V3 widths (mla_attention; the causal streaming path keeps the per-step
-    # kernels), timed here the same way; the per-step 3a/3b/3c above are the decomposed
-    # kernels
-    fused_attn = (not causal and dims.kv_rank == 512 and dims.rope == 64
+    # DeepSeek-V3 widths, timed here the same way; the per-step 3a/3b/3c above are the
+    # decomposed kernels
+    fused_attn = (dims.kv_rank == 512 and dims.rope == 64
                   and os.environ.get("MLA_ATTENTION_PATH") != "split")
     if fused_attn:
         qa_f, qr_f = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
@@ -433,6 +431,27 @@ def main():
                         "mfma_pct": round(100 * fl / t / peak_mfma, 1)}
         nb["attention_paged_ragged"]["mean_keys"] = round(keys_ragged / B, 1)
         del ck_pool, pe_pool
+    else:
+        # causal: the key-chunked entry point (bounded score workspace) beside the layer's
+        # fused pass
+        qa_b, qr_b = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
+                                    g["positions"], dims.nope, dims.rope, eps)
+        fl_attn = work["3a"][0] + work["3c"][0] + work["3d"][0]
+        fn = lambda: ext.mla_attention_streaming(qa_b, qr_b, g["c_kv"], g["pe_cache"],  # noqa: E731
+                                                 W_uv_d, scale, True)
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / args.steps * 1e-3
+        nb["attention_streaming_chunks"] = {
+            "us": round(t * 1e6, 2), "gflop": round(fl_attn / 1e9, 3),
+            "tflops": round(fl_attn / t / 1e12, 2), "bound": "mfma",
+            "mfma_pct": round(100 * fl_attn / t / peak_mfma, 1)}
     print(f"[bench] neighbours: " + ", ".join(f"{k} {v['us']} µs" for k, v in nb.items()),
           file=sys.stderr, flush=True)
 

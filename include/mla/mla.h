@@ -105,6 +105,10 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims,
  *   scale      softmax DIVISOR (the reference passes sqrt(nope+rope))
  *   causal     0: every key visible; 1: key j visible to query i iff j <= Sk - Sq + i
  *              (not in the reference; used for chunked prefill)
+ * At kv_rank 512 / rope 64 this runs 3a+3b+3c as one fused pass (mla_attn_ctx), whose
+ * workspace holds no score matrix; MLA_ATTENTION_PATH=split selects the per-step kernels.
+ * The variable is read by the size query and by the call: a caller that changes it in
+ * between gets MLA_ERR_WORKSPACE when the workspace is too small.
  */
 size_t mla_attention_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal);
 int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims,

@@ -310,6 +310,7 @@ bool use_flash(mla_dtype_t dt, const mla_dims_t* d) {
 }
 
 struct AttnLayout {
+    bool fused = false;   // the path this layout is for
     int ld_p, P;
     GemmPlan ctx, out;
     FlashPlan flash;
@@ -317,17 +318,30 @@ struct AttnLayout {
         total;
 };
 
-// Both attention paths fit in one layout (the path is chosen per call): the fused path
-// uses ctx, row_sum and 3d's workspace like the per-step path, and puts its split partials
-// into the scores region when they fit there.
+// The workspace of the attention path a call takes (use_flash: read per call, so a caller
+// that changes MLA_ATTENTION_PATH between the size query and the call gets
+// MLA_ERR_WORKSPACE, never an overrun).  Fused: ctx, row_sum, the split partials and 3d's
+// workspace -- no score matrix.  Per-step: scores, tile partials, alpha, row_sum, ctx and
+// the 3c / 3d workspaces.
 AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     AttnLayout L;
     const size_t rows = (size_t)d->batch * d->sq * d->heads;
     L.ld_p = mla_score_ld(d->sk);
     L.P = cdiv(d->sk, kScoreTile);
-    L.ctx = plan_gemm(ctx_problem(dt, d, nullptr, L.ld_p, nullptr, nullptr, nullptr));
     L.out = plan_gemm(out_problem(dt, d, nullptr, nullptr, nullptr, nullptr));
     size_t o = 0;
+    L.fused = use_flash(dt, d);
+    if (L.fused) {
+        L.flash = plan_flash(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
+        L.off_p = L.off_m = L.off_l = L.off_alpha = L.off_ctx_ws = 0;
+        L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
+        L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
+        L.off_out_ws = o; o = align_up(o + L.out.workspace_bytes);
+        L.off_part = o;   o = align_up(o + L.flash.partial_bytes);
+        L.total = o;
+        return L;
+    }
+    L.ctx = plan_gemm(ctx_problem(dt, d, nullptr, L.ld_p, nullptr, nullptr, nullptr));
     L.off_p = o;      o = align_up(o + rows * L.ld_p * sizeof(float));
     L.off_m = o;      o = align_up(o + rows * L.P * sizeof(float));
     L.off_l = o;      o = align_up(o + rows * L.P * sizeof(float));
@@ -336,14 +350,7 @@ AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
     L.off_ctx_ws = o; o = align_up(o + L.ctx.workspace_bytes);
     L.off_out_ws = o; o = align_up(o + L.out.workspace_bytes);
-    L.off_part = L.off_p;
-    if (flash_eligible(dt, d)) {
-        L.flash = plan_flash(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
-        if (L.flash.partial_bytes > rows * L.ld_p * sizeof(float)) {
-            L.off_part = o;
-            o = align_up(o + L.flash.partial_bytes);
-        }
-    }
+    L.off_part = 0;
     L.total = o;
     return L;
 }
@@ -886,7 +893,7 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     float* ctx = at<float>(workspace, L.off_ctx);
     const int rows = dims->batch * dims->sq * dims->heads;
 
-    if (use_flash(dtype, dims)) {
+    if (L.fused) {
         // 3a+3b+3c fused, then 3d
         const FlashProblem fp = flash_problem(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache,
                                               scale, causal);
@@ -1058,7 +1065,7 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
     float* ctx = at<float>(workspace, L.off_ctx);
     const int rows = dims->batch * dims->sq * dims->heads;
 
-    if (use_flash(dtype, dims)) {
+    if (L.fused) {
         // 3a+3b+3c fused over the pages (each sequence to its own length), then 3d
         FlashProblem fp = flash_problem(dtype, dims, q_absorbed, q_rope, c_kv_pages, pe_pages,
                                         scale, causal);

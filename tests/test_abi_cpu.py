@@ -80,14 +80,19 @@ def test_version_and_layout_queries(lib):
     assert lib.mla_score_ld(0) == 0
 
 
-def test_workspace_queries_are_pure_host(lib):
+def test_workspace_queries_are_pure_host(lib, monkeypatch):
     d = dsv3(128, 1, 4989)
     wq = lib.mla_q_absorbed_workspace_bytes(F32, ctypes.byref(d))
-    wa = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0)
     rows = 128 * 128
-    # scores [rows, 4992] fp32 alone is 327 MB
-    assert wa >= rows * 4992 * 4 + rows * 512 * 4
-    assert wa < rows * 4992 * 4 * 1.3
+    # fused path (the default at these widths): ctx, row sums, 3d's workspace -- no scores
+    wa = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0)
+    assert rows * 512 * 4 <= wa < rows * 512 * 4 * 1.5
+    # per-step path: scores [rows, 4992] fp32 alone is 327 MB
+    monkeypatch.setenv("MLA_ATTENTION_PATH", "split")
+    ws = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0)
+    assert ws >= rows * 4992 * 4 + rows * 512 * 4
+    assert ws < rows * 4992 * 4 * 1.3
+    monkeypatch.delenv("MLA_ATTENTION_PATH")
     # q path: q_lat, q_raw at least
     assert wq >= 128 * (1536 + 128 * 192) * 4
     bad = dsv3(0, 1, 4989)
@@ -198,12 +203,16 @@ def test_bf16_needs_8_element_rows(lib):
     assert lib.mla_attention_workspace_bytes(BF16, ctypes.byref(dsv3(2, 1, 100)), 0) > 0
 
 
-def test_streaming_validation_and_bounded_workspace(lib):
+def test_streaming_validation_and_bounded_workspace(lib, monkeypatch):
     d = dsv3(4, 128, 32768)
+    fused = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 1)
+    monkeypatch.setenv("MLA_ATTENTION_PATH", "split")
     full = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 1)
+    monkeypatch.delenv("MLA_ATTENTION_PATH")
     stream = lib.mla_attention_streaming_workspace_bytes(F32, ctypes.byref(d), 1, 0)
     assert full > 8.5e9            # the materialised [65536 x 32768] fp32 scores
     assert 0 < stream < 1.6e9      # one <= 1 GiB chunk of scores plus the running state
+    assert 0 < fused < 0.2e9       # the fused pass keeps no scores: ctx and row sums
     small = lib.mla_attention_streaming_workspace_bytes(F32, ctypes.byref(d), 1, 128)
     assert 0 < small < stream
     assert lib.mla_attention_streaming_workspace_bytes(F32, ctypes.byref(d), 1, 100) == 0
