@@ -777,31 +777,57 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
 
 constexpr int kFStages = 4;   // LDS ring depth
 
-// ctx = sum_s w_s O_s, row_sum = sum_s w_s l_s, w_s = 2^(m_s - max_s m_s); one thread per
-// (row, 4 columns)
+// ctx = sum_s w_s O_s, row_sum = sum_s w_s l_s, w_s = 2^(m_s - max_s m_s).  One workgroup
+// per row: its threads take the row maximum over the splits, then wave w sums splits
+// w, w+4, ... (lane: 8 columns), and the four waves' sums are added in wave order -- a
+// fixed order, so the merge is deterministic.  Each wave keeps a split's 2 KB row in
+// flight per iteration, so many splits (small batches) do not serialise on latency.
 __global__ void __launch_bounds__(256) flash_merge_kernel(const float* __restrict__ o,
                                                           const float* __restrict__ m,
                                                           const float* __restrict__ l,
                                                           float* __restrict__ ctx,
                                                           float* __restrict__ row_sum, int rows,
                                                           int n_split) {
-    const int per_row = kFR / 4;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= (int64_t)rows * per_row) return;
-    const int r = (int)(idx / per_row), c4 = (int)(idx % per_row);
+    __shared__ float red[256];
+    __shared__ v4f part[4][64][2];
+    __shared__ float lpart[4];
+    const int r = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     float mx = -INFINITY;
-    for (int s = 0; s < n_split; ++s) mx = fmaxf(mx, m[(int64_t)s * rows + r]);
-    v4f acc = {0.f, 0.f, 0.f, 0.f};
-    float ls = 0.f;
-    for (int s = 0; s < n_split; ++s) {
-        const float ms = m[(int64_t)s * rows + r];
-        const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
-        const v4f v = *reinterpret_cast<const v4f*>(o + ((int64_t)s * rows + r) * kFR + 4 * c4);
-        acc += w * v;
-        ls += w * l[(int64_t)s * rows + r];
+    for (int s = tid; s < n_split; s += 256) mx = fmaxf(mx, m[(int64_t)s * rows + r]);
+    red[tid] = mx;
+    __syncthreads();
+    #pragma unroll
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) red[tid] = fmaxf(red[tid], red[tid + w]);
+        __syncthreads();
     }
-    *reinterpret_cast<v4f*>(ctx + (int64_t)r * kFR + 4 * c4) = acc;
-    if (c4 == 0) row_sum[r] = ls;
+    mx = red[0];
+    v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
+    float ls = 0.f;
+    for (int s = wave; s < n_split; s += 4) {
+        const int64_t slot = (int64_t)s * rows + r;
+        const float ms = m[slot];
+        const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+        const v4f* src = reinterpret_cast<const v4f*>(o + slot * kFR) + 2 * lane;
+        acc0 += w * src[0];
+        acc1 += w * src[1];
+        ls += w * l[slot];
+    }
+    part[wave][lane][0] = acc0;
+    part[wave][lane][1] = acc1;
+    if (lane == 0) lpart[wave] = ls;
+    __syncthreads();
+    if (wave == 0) {
+        #pragma unroll
+        for (int w = 1; w < 4; ++w) {
+            acc0 += part[w][lane][0];
+            acc1 += part[w][lane][1];
+        }
+        v4f* dst = reinterpret_cast<v4f*>(ctx + (int64_t)r * kFR) + 2 * lane;
+        dst[0] = acc0;
+        dst[1] = acc1;
+        if (lane == 0) row_sum[r] = ((lpart[0] + lpart[1]) + lpart[2]) + lpart[3];
+    }
 }
 
 }  // namespace
@@ -871,9 +897,8 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || f.n_split == 1) return e;
-    const int64_t n = (int64_t)rows * (kFR / 4);
-    hipLaunchKernelGGL(flash_merge_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                       stream, a.o, m_split, a.l, ctx, row_sum, rows, f.n_split);
+    hipLaunchKernelGGL(flash_merge_kernel, dim3((unsigned)rows), dim3(256), 0, stream, a.o,
+                       m_split, a.l, ctx, row_sum, rows, f.n_split);
     return hipGetLastError();
 }
 
