@@ -324,26 +324,40 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     }
 
     // epilogue: each accumulator register holds one row; lanes 0-31 / 32-63 write
-    // 32 consecutive columns of two rows.
-    #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    // 32 consecutive columns of two rows.  Buffer stores from one descriptor per tile:
+    // the lane's column (and its block's first row) is a per-lane offset fixed for the
+    // block, the register's row a wave-uniform offset, and rows or columns past the
+    // problem carry kOob -- no branches and no 64-bit address arithmetic per element.
+    {
+        const bool to_ws = a.split > 1;
+        const int64_t ld = to_ws ? a.N : a.ldc;
+        constexpr bool kF32Out = (OUT == kOutF32);
+        const int esz = (to_ws || kF32Out) ? 4 : 2;
+        const __amdgpu_buffer_rsrc_t rso =
+            to_ws ? make_rsrc(a.ws + (int64_t)sp * a.ws_split + ((int64_t)g * a.M + m0) * a.N + n0)
+                  : (kF32Out ? make_rsrc(static_cast<float*>(a.C) + (int64_t)g * a.sCg +
+                                         (int64_t)m0 * a.ldc + n0)
+                             : make_rsrc(static_cast<bf16_t*>(a.C) + (int64_t)g * a.sCg +
+                                         (int64_t)m0 * a.ldc + n0));
         #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * WTN + j * 32 + l32;
+        for (int i = 0; i < TM; ++i) {
             #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * WTM + i * 32 + acc_row(e, lane);
-                if (row < a.M && col < a.N) {
-                    if (a.split > 1) {
-                        a.ws[(int64_t)sp * a.ws_split + ((int64_t)g * a.M + row) * a.N + col] =
-                            acc[i][j][e];
-                    } else if (OUT == kOutF32) {
-                        static_cast<float*>(a.C)[(int64_t)g * a.sCg + (int64_t)row * a.ldc + col] =
-                            acc[i][j][e];
-                    } else {
-                        static_cast<bf16_t*>(a.C)[(int64_t)g * a.sCg + (int64_t)row * a.ldc + col] =
-                            (bf16_t)f32_to_bf16_bits(acc[i][j][e]);
-                    }
+            for (int j = 0; j < TN; ++j) {
+                const int c = wn * WTN + j * 32 + l32;              // tile column
+                const int r0 = wm * WTM + i * 32 + 4 * half;          // tile row of e = 0
+                const uint32_t lane_off =
+                    (uint32_t)((r0 * ld + c) * esz) | oob_mask(n0 + c, a.N);
+                #pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int re = 8 * (e >> 2) + (e & 3);
+                    const int soff = __builtin_amdgcn_readfirstlane((int)(re * ld * esz));
+                    const uint32_t off = lane_off | oob_mask(m0 + r0 + re, a.M);
+                    if (to_ws || kF32Out)
+                        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rso,
+                                                              (int)off, soff, 0);
+                    else
+                        __builtin_amdgcn_raw_buffer_store_b16(
+                            (uint16_t)f32_to_bf16_bits(acc[i][j][e]), rso, (int)off, soff, 0);
                 }
             }
         }
@@ -600,6 +614,9 @@ namespace {
 
 hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* workspace,
                             bool reduce, hipStream_t stream) {
+    // the epilogue addresses a tile's rows with 32-bit offsets from the tile's first row
+    const int64_t out_ld = plan.split > 1 ? p.N : p.ldc;
+    if ((int64_t)plan.bm * out_ld * 4 >= (int64_t)kRsrcRange) return hipErrorInvalidValue;
     GemmArgs a;
     a.A = p.A; a.lda = p.lda; a.sAg = p.sAg;
     a.B = p.B; a.ldb = p.ldb; a.sBg = p.sBg;
