@@ -66,8 +66,15 @@ constexpr int nn_row_words() {
 // PAGED: the NN B operand is a paged row pool -- K row k of group g is row
 // b_pages[g*max_pages + k/page_size]*page_size + k%page_size (page_size a multiple of 64,
 // so a K slice never straddles a page); used by 3c over a paged KV cache.
+// PERSIST: the grid holds fewer workgroups than tiles; workgroup w walks the tiles w',
+// w' + grid, ... (w' its XCD-aware logical index) and its load ring runs on across tile
+// boundaries, so the next tile's first slices are in flight during the current tile's
+// last ones and the epilogue's stores drain under the next tile's MFMA work.  Short-K
+// products (2c: K = 128, four slices) otherwise spend about a third of a tile in the
+// unoverlapped fill and epilogue.  Full tiles only, plain A, no per-group K limit or
+// paging (the launcher checks).
 template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT,
-          bool PAGED = false>
+          bool PAGED = false, bool PERSIST = false>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     constexpr int PD = 2;
     using MM = Mma<TL>;
@@ -92,6 +99,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     constexpr int kSliceLoads = A_LD * A_F4 + (TRN ? 4 : B_LD) + (AMODE == kAAlpha ? A_LD : 0);
     constexpr int kSliceWrites = A_LD + (TRN ? 8 : B_LD);
     static_assert(A_F32 || AMODE == kAPlain, "scaled A operands are fp32");
+    static_assert(!PERSIST || (AMODE == kAPlain && !PAGED), "persistent tiles: plain A only");
 
     __shared__ __attribute__((aligned(16))) uint32_t As[2][BM][kRowWords];
     __shared__ __attribute__((aligned(16))) uint32_t Bs[2][BROWS][BWORDS];
@@ -187,12 +195,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     };
     if constexpr (PAGED) page_row = lookup_row(k_begin);
 
-    auto load_slice = [&](int k0, int slot) {
-        const int klim = k_end - k0;               // valid K columns / rows of this slice
-        const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A_t + k0);
-        const __amdgpu_buffer_rsrc_t rsb =
-            make_rsrc(NT ? B_t + k0 : B_t + (PAGED ? page_row : (int64_t)k0) * a.ldb);
-        if constexpr (PAGED) page_row = lookup_row(k0 + KS);
+    // one slice's global loads into ring slot `slot`: A_s / B_s are the slice's origins,
+    // klim its valid K columns (A, NT B) or K rows (NN B); k0 indexes alpha
+    auto issue_loads = [&](const TA* A_s, const TL* B_s, int k0, int klim, int slot) {
+        const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A_s);
+        const __amdgpu_buffer_rsrc_t rsb = make_rsrc(B_s);
         #pragma unroll
         for (int i = 0; i < A_LD; ++i) {
             if constexpr (A_F32) {
@@ -214,6 +221,11 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
         #pragma unroll
         for (int i = 0; i < NB_LD; ++i)
             rb[slot][i] = load16(rsb, ob[i] | oob_mask(NT ? kc : bk[i], klim));
+    };
+    auto load_slice = [&](int k0, int slot) {
+        const TL* B_s = NT ? B_t + k0 : B_t + (PAGED ? page_row : (int64_t)k0) * a.ldb;
+        if constexpr (PAGED) page_row = lookup_row(k0 + KS);
+        issue_loads(A_t + k0, B_s, k0, k_end - k0, slot);
     };
 
     auto store_slice = [&](int buf, int slot) {
@@ -268,77 +280,58 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    const int nslices = (k_end > k_begin) ? (k_end - k_begin + KS - 1) / KS : 0;
-    #pragma unroll
-    for (int u = 0; u < PD; ++u) load_slice(k_begin + u * KS, u);
-    store_slice(0, 0);
-    __syncthreads();
-
     const int l32 = lane & 31;
     const int half = lane >> 5;
-    // slice s sits in LDS buffer s&1 and came from ring slot s%PD; the loop is unrolled by
-    // PD so every slot index is a compile-time constant
-    for (int s0 = 0; s0 < nslices; s0 += PD) {
+    // one slice of MFMA work from LDS buffer buf
+    auto mma_slice = [&](int buf) {
         #pragma unroll
-        for (int u = 0; u < PD; ++u) {
-            const int s = s0 + u;
-            if (PD > 1 && s >= nslices) break;
-            const int buf = (PD == 1) ? (s & 1) : (u & 1);
-            load_slice(k_begin + (s + PD) * KS, u);
-
+        for (int st = 0; st < 4; ++st) {
+            v4u fa[TM], fb[TN];
             #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                v4u fa[TM], fb[TN];
+            for (int i = 0; i < TM; ++i)
+                fa[i] = *reinterpret_cast<const v4u*>(&As[buf][wm * WTM + i * 32 + l32][8 * st + 4 * half]);
+            #pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int n = wn * WTN + j * 32 + l32;
+                if (NT || TRN) {
+                    fb[j] = *reinterpret_cast<const v4u*>(&Bs[buf][n][8 * st + 4 * half]);
+                } else if constexpr (sizeof(TL) == 4) {
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) fb[j][q] = Bs[buf][8 * st + 4 * half + q][n];
+                } else {
+                    const uint16_t* b16 = reinterpret_cast<const uint16_t*>(&Bs[buf][0][0]);
+                    const int r0 = 16 * st + 8 * half;
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        fb[j][q] = (uint32_t)b16[(r0 + 2 * q) * (2 * BWORDS) + n] |
+                                   ((uint32_t)b16[(r0 + 2 * q + 1) * (2 * BWORDS) + n] << 16);
+                }
+            }
+            #pragma unroll
+            for (int q = 0; q < MM::kSub; ++q)
                 #pragma unroll
                 for (int i = 0; i < TM; ++i)
-                    fa[i] = *reinterpret_cast<const v4u*>(&As[buf][wm * WTM + i * 32 + l32][8 * st + 4 * half]);
-                #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int n = wn * WTN + j * 32 + l32;
-                    if (NT || TRN) {
-                        fb[j] = *reinterpret_cast<const v4u*>(&Bs[buf][n][8 * st + 4 * half]);
-                    } else if constexpr (sizeof(TL) == 4) {
-                        #pragma unroll
-                        for (int q = 0; q < 4; ++q) fb[j][q] = Bs[buf][8 * st + 4 * half + q][n];
-                    } else {
-                        const uint16_t* b16 = reinterpret_cast<const uint16_t*>(&Bs[buf][0][0]);
-                        const int r0 = 16 * st + 8 * half;
-                        #pragma unroll
-                        for (int q = 0; q < 4; ++q)
-                            fb[j][q] = (uint32_t)b16[(r0 + 2 * q) * (2 * BWORDS) + n] |
-                                       ((uint32_t)b16[(r0 + 2 * q + 1) * (2 * BWORDS) + n] << 16);
-                    }
-                }
-                #pragma unroll
-                for (int q = 0; q < MM::kSub; ++q)
                     #pragma unroll
-                    for (int i = 0; i < TM; ++i)
-                        #pragma unroll
-                        for (int j = 0; j < TN; ++j) acc[i][j] = MM::sub(fa[i], fb[j], q, acc[i][j]);
-            }
-
-            store_slice(buf ^ 1, (u + 1) % PD);
-            sched_slice<kStepReads, MM::kSub * TM * TN, kSliceLoads, kSliceWrites>();
-            __syncthreads();
+                    for (int j = 0; j < TN; ++j) acc[i][j] = MM::sub(fa[i], fb[j], q, acc[i][j]);
         }
-    }
+    };
 
     // epilogue: each accumulator register holds one row; lanes 0-31 / 32-63 write
     // 32 consecutive columns of two rows.  Buffer stores from one descriptor per tile:
     // the lane's column (and its block's first row) is a per-lane offset fixed for the
     // block, the register's row a wave-uniform offset, and rows or columns past the
     // problem carry kOob -- no branches and no 64-bit address arithmetic per element.
-    {
+    auto epilogue = [&](int g_, int m0_, int n0_, int sp_) {
         const bool to_ws = a.split > 1;
         const int64_t ld = to_ws ? a.N : a.ldc;
         constexpr bool kF32Out = (OUT == kOutF32);
         const int esz = (to_ws || kF32Out) ? 4 : 2;
         const __amdgpu_buffer_rsrc_t rso =
-            to_ws ? make_rsrc(a.ws + (int64_t)sp * a.ws_split + ((int64_t)g * a.M + m0) * a.N + n0)
-                  : (kF32Out ? make_rsrc(static_cast<float*>(a.C) + (int64_t)g * a.sCg +
-                                         (int64_t)m0 * a.ldc + n0)
-                             : make_rsrc(static_cast<bf16_t*>(a.C) + (int64_t)g * a.sCg +
-                                         (int64_t)m0 * a.ldc + n0));
+            to_ws ? make_rsrc(a.ws + (int64_t)sp_ * a.ws_split + ((int64_t)g_ * a.M + m0_) * a.N + n0_)
+                  : (kF32Out ? make_rsrc(static_cast<float*>(a.C) + (int64_t)g_ * a.sCg +
+                                         (int64_t)m0_ * a.ldc + n0_)
+                             : make_rsrc(static_cast<bf16_t*>(a.C) + (int64_t)g_ * a.sCg +
+                                         (int64_t)m0_ * a.ldc + n0_));
         #pragma unroll
         for (int i = 0; i < TM; ++i) {
             #pragma unroll
@@ -346,18 +339,117 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                 const int c = wn * WTN + j * 32 + l32;              // tile column
                 const int r0 = wm * WTM + i * 32 + 4 * half;          // tile row of e = 0
                 const uint32_t lane_off =
-                    (uint32_t)((r0 * ld + c) * esz) | oob_mask(n0 + c, a.N);
+                    (uint32_t)((r0 * ld + c) * esz) | oob_mask(n0_ + c, a.N);
                 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int re = 8 * (e >> 2) + (e & 3);
                     const int soff = __builtin_amdgcn_readfirstlane((int)(re * ld * esz));
-                    const uint32_t off = lane_off | oob_mask(m0 + r0 + re, a.M);
+                    const uint32_t off = lane_off | oob_mask(m0_ + r0 + re, a.M);
                     if (to_ws || kF32Out)
                         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rso,
                                                               (int)off, soff, 0);
                     else
                         __builtin_amdgcn_raw_buffer_store_b16(
                             (uint16_t)f32_to_bf16_bits(acc[i][j][e]), rso, (int)off, soff, 0);
+                }
+            }
+        }
+    };
+
+    // Both loops below are unrolled by PD so every ring slot index is a compile-time
+    // constant, and run a multiple of PD slices: a slice past the end loads zeros (every
+    // offset fails its K test) and adds nothing.  An exit between the unrolled bodies would
+    // give the compiler a path back to the loop head with a slot's loads still in flight,
+    // and the wait counts it derives for the head would then drain the ring every slice.
+    if constexpr (!PERSIST) {
+        const int nslices = (k_end > k_begin) ? (k_end - k_begin + KS - 1) / KS : 0;
+        const int nslices_pd = (nslices + PD - 1) / PD * PD;
+        #pragma unroll
+        for (int u = 0; u < PD; ++u) load_slice(k_begin + u * KS, u);
+        store_slice(0, 0);
+        __syncthreads();
+
+        // slice s sits in LDS buffer s&1 and came from ring slot s%PD
+        for (int s0 = 0; s0 < nslices_pd; s0 += PD) {
+            #pragma unroll
+            for (int u = 0; u < PD; ++u) {
+                const int s = s0 + u;
+                const int buf = (PD == 1) ? (s & 1) : (u & 1);
+                load_slice(k_begin + (s + PD) * KS, u);
+                mma_slice(buf);
+                store_slice(buf ^ 1, (u + 1) % PD);
+                sched_slice<kStepReads, MM::kSub * TM * TN, kSliceLoads, kSliceWrites>();
+                __syncthreads();
+            }
+        }
+        epilogue(g, m0, n0, sp);
+    } else {
+        // Every tile has ns = k_chunk / KS slices (the last split's tail slices load
+        // zeros); the workgroup's tiles run as one stream of my_tiles * ns slices.  The load
+        // cursor (l_*) runs PD slices ahead of the compute cursor (c_*); past the last tile
+        // it loads zeros (klim 0: every offset gets kOob, nothing is read).
+        const int stride = gridDim.x;
+        const int n_tiles = a.tiles_m * a.tiles_n * a.split * a.G;
+        const int first = xcd_logical_block(blockIdx.x, gridDim.x);
+        const int my_tiles = (n_tiles - 1 - first) / stride + 1;   // grid <= n_tiles
+        const int ns = a.k_chunk / KS;
+        const int total = (my_tiles * ns + PD - 1) / PD * PD;
+        struct Tile { int g, m0, n0, sp; };
+        auto decode = [&](int tile) {
+            int t = tile;
+            const int tn_ = t % a.tiles_n; t /= a.tiles_n;
+            const int tm_ = t % a.tiles_m; t /= a.tiles_m;
+            return Tile{t / a.split, tm_ * BM, tn_ * BN, t % a.split};
+        };
+        int l_tile = first, l_s = 0;
+        const TA* l_A = A_t;
+        const TL* l_B = B_t;
+        int l_kb = k_begin, l_ke = k_end;
+        auto persist_load = [&](int slot) {
+            const int k0 = l_kb + l_s * KS;
+            const int klim = l_tile < n_tiles ? l_ke - k0 : 0;
+            issue_loads(l_A + k0, NT ? l_B + k0 : l_B + (int64_t)k0 * a.ldb, k0, klim, slot);
+            if (++l_s == ns) {
+                l_s = 0;
+                l_tile += stride;
+                if (l_tile < n_tiles) {
+                    const Tile t = decode(l_tile);
+                    l_A = static_cast<const TA*>(a.A) + (int64_t)t.g * a.sAg + (int64_t)t.m0 * a.lda;
+                    const TL* Bg_ = static_cast<const TL*>(a.B) + (int64_t)t.g * a.sBg;
+                    l_B = NT ? Bg_ + (int64_t)t.n0 * a.ldb : Bg_ + t.n0;
+                    l_kb = t.sp * a.k_chunk;
+                    l_ke = min(a.K, l_kb + a.k_chunk);
+                }
+            }
+        };
+        #pragma unroll
+        for (int u = 0; u < PD; ++u) persist_load(u);
+        store_slice(0, 0);
+        __syncthreads();
+
+        int c_tile = first, c_s = 0;
+        for (int v0 = 0; v0 < total; v0 += PD) {
+            #pragma unroll
+            for (int u = 0; u < PD; ++u) {
+                const int buf = u & 1;
+                persist_load(u);
+                mma_slice(buf);
+                store_slice(buf ^ 1, (u + 1) % PD);
+                sched_slice<kStepReads, MM::kSub * TM * TN, kSliceLoads, kSliceWrites>();
+                __syncthreads();
+                // after the barrier, so the slice body above stays one scheduling region;
+                // the stores drain while the next slices' MFMAs run
+                if (++c_s == ns && c_tile < n_tiles) {
+                    const Tile t = decode(c_tile);
+                    epilogue(t.g, t.m0, t.n0, t.sp);
+                    #pragma unroll
+                    for (int i = 0; i < TM; ++i)
+                        #pragma unroll
+                        for (int j = 0; j < TN; ++j)
+                            #pragma unroll
+                            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+                    c_s = 0;
+                    c_tile += stride;
                 }
             }
         }
@@ -386,19 +478,20 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
 }
 
 template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT,
-          bool PAGED>
+          bool PAGED, bool PERSIST>
 hipError_t launch_cfg(const GemmArgs& args, int nblocks, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT, PAGED>),
+    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT, PAGED, PERSIST>),
                        dim3(nblocks), dim3(kThreads), 0, stream, args);
     return hipGetLastError();
 }
 
-template <typename TL, typename TA, bool NT, int AMODE, int OUT, bool PAGED = false>
+template <typename TL, typename TA, bool NT, int AMODE, int OUT, bool PAGED = false,
+          bool PERSIST = false>
 hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipStream_t stream) {
 #define MLA_TILE(BM_, BN_, WM_, WN_)                                                       \
     if (bm == BM_ && bn == BN_)                                                             \
-        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT, PAGED>(args, nblocks,  \
-                                                                             stream);
+        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT, PAGED, PERSIST>(       \
+            args, nblocks, stream);
     MLA_TILE(128, 128, 2, 2)
     MLA_TILE(128, 96, 4, 1)
     MLA_TILE(128, 64, 2, 2)
@@ -416,8 +509,19 @@ hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipSt
 //          NN alpha, A f32 -> f32 (3c)         | NT rowrecip, A f32 -> bf16 (3d)
 // A split-K launch writes fp32 partials whatever the output type.
 hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
-                    hipStream_t stream) {
+                    bool persist, hipStream_t stream) {
     const bool split = a.split > 1;
+    if (persist) {   // NN plain with f32 output or partials (2c, 2a1, 2a2)
+        if (p.b_nt || p.amode != kAPlain || p.b_pages || !(p.out_type == kOutF32 || split))
+            return hipErrorInvalidValue;
+        if (!p.bf16)
+            return launch_tiles<float, float, false, kAPlain, kOutF32, false, true>(a, bm, bn,
+                                                                                   nblocks, stream);
+        if (!p.a_f32)
+            return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutF32, false, true>(
+                a, bm, bn, nblocks, stream);
+        return hipErrorInvalidValue;
+    }
     if (p.b_pages) {   // paged NN B: 3c over a paged cache only
         if (p.b_nt || p.amode != kAAlpha || !(p.out_type == kOutF32 || split))
             return hipErrorInvalidValue;
@@ -464,8 +568,9 @@ int cdiv(int a, int b) { return (a + b - 1) / b; }
 // split.  MFMA time = rounds of co-resident workgroups x the padded tile work (32x32
 // blocks waste rows/cols at small M or N) at a per-tile efficiency; memory time = the
 // operand bytes that must come from HBM; split-K adds its fp32 partial traffic and one
-// reduction launch.  MLA_GEMM_PLAN="M,N,K,G=bm,bn,split;..." forces a plan for a matching
-// problem (tuning aid; the chosen plan always goes through the same validity checks).
+// reduction launch.  MLA_GEMM_PLAN="M,N,K,G=bm,bn,split[,tiles_per_wg];..." forces a plan
+// for a matching problem (tuning aid; the chosen plan always goes through the same validity
+// checks).
 namespace {
 
 struct TileShape { int bm, bn; double eff; };
@@ -485,12 +590,15 @@ int lds_bytes(int bm, int bn, bool nt, bool bf16) {
 // MI355X: a sweep of every tile x power-of-two split per shape, keeping the fastest (ties
 // within ~1% go to the model's choice).  Exact shape matches only; every other shape goes
 // through the time model below.  M = B*Sq for the Q path / wo / KV append, M = H for 3c.
-struct TunedPlan { int M, N, K, G; bool nt, bf16; int bm, bn, split; };
+// The last column is the tiles per workgroup of a persistent grid (1: one per tile); 2c
+// at B = 128 runs 128x64 tiles two per workgroup, 30.5 us against 32.8 us for one 128x128
+// tile per workgroup.
+struct TunedPlan { int M, N, K, G; bool nt, bf16; int bm, bn, split, tiles_per_wg = 1; };
 constexpr TunedPlan kTuned[] = {
     // B = 128 decode, fp32: 2a1, 2a2, 2c, 3d, wo, kv
     {128, 1536, 7168, 1, false, false, 64, 64, 16},
     {128, 24576, 1536, 1, false, false, 64, 64, 1},
-    {128, 512, 128, 128, false, false, 128, 128, 1},
+    {128, 512, 128, 128, false, false, 128, 64, 1, 2},
     {128, 128, 512, 128, true, false, 64, 64, 1},
     {128, 7168, 16384, 1, false, false, 128, 32, 8},
     {128, 576, 7168, 1, false, false, 64, 64, 8},
@@ -521,6 +629,7 @@ bool tuned_plan(const GemmProblem& p, GemmPlan* out) {
         if (t.M == p.M && t.N == p.N && t.K == p.K && t.G == p.G && t.nt == p.b_nt &&
             t.bf16 == p.bf16) {
             out->bm = t.bm; out->bn = t.bn; out->split = t.split;
+            out->tiles_per_wg = t.tiles_per_wg;
             return true;
         }
     return false;
@@ -538,11 +647,12 @@ bool plan_override(const GemmProblem& p, GemmPlan* out) {
     const char* s = env;
     while (*s) {
         long M, N, K, G;
-        int bm, bn, split, used = 0;
+        int bm, bn, split, used = 0, per_wg = 1, used2 = 0;
         if (sscanf(s, "%ld,%ld,%ld,%ld=%d,%d,%d%n", &M, &N, &K, &G, &bm, &bn, &split, &used) == 7) {
+            if (sscanf(s + used, ",%d%n", &per_wg, &used2) == 1) used += used2;
             if (M == p.M && N == p.N && K == p.K && G == p.G && tile_supported(bm, bn) &&
-                split >= 1) {
-                out->bm = bm; out->bn = bn; out->split = split;
+                split >= 1 && per_wg >= 1) {
+                out->bm = bm; out->bn = bn; out->split = split; out->tiles_per_wg = per_wg;
                 return true;
             }
             s += used;
@@ -646,8 +756,15 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
         return hipErrorInvalidValue;
     const int64_t nblocks64 = (int64_t)a.tiles_m * a.tiles_n * a.G * a.split;
     if (nblocks64 <= 0 || nblocks64 > 0x7fffffff) return hipErrorInvalidValue;
-    const int nblocks = (int)nblocks64;
-    hipError_t e = dispatch(p, a, plan.bm, plan.bn, nblocks, stream);
+    int nblocks = (int)nblocks64;
+    // persistent grid: full tiles of a plain NN product with no per-group K limit; any
+    // other problem keeps one workgroup per tile
+    const bool persist = plan.tiles_per_wg > 1 && p.M % plan.bm == 0 && p.N % plan.bn == 0 &&
+                         !p.b_nt && p.amode == kAPlain && !p.k_len && !p.b_pages &&
+                         (p.out_type == kOutF32 || plan.split > 1) && (!p.bf16 || !p.a_f32) &&
+                         plan.k_chunk % (p.bf16 ? 64 : 32) == 0;
+    if (persist) nblocks = cdiv(nblocks, plan.tiles_per_wg);
+    hipError_t e = dispatch(p, a, plan.bm, plan.bn, nblocks, persist, stream);
     if (e != hipSuccess || plan.split == 1 || !reduce) return e;
     const int64_t total = (int64_t)p.G * p.M * p.N;
     const int rblocks = (int)std::min<int64_t>((total + 255) / 256, 8 * kNumCUs);

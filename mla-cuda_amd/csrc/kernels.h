@@ -43,6 +43,7 @@ struct GemmPlan {
     int bm = 128, bn = 128;   // workgroup tile
     int split = 1;            // K slices
     int k_chunk = 0;          // K elements per slice (multiple of 32)
+    int tiles_per_wg = 1;     // > 1: persistent grid of ceil(tiles / tiles_per_wg) workgroups
     size_t workspace_bytes = 0;  // fp32 partials when split > 1
 };
 

@@ -63,6 +63,21 @@ def test_gemm(ext, M, N, K):
     torch.testing.assert_close(got, ref, **TOL)
 
 
+@pytest.mark.parametrize("plan", ["64,64,1,3", "64,64,3,5", "128,128,1,7", "32,128,2,2"])
+def test_gemm_persistent_plans(ext, monkeypatch, plan):
+    """Forced persistent-grid plans (bm, bn, split, tiles per workgroup) of the 2a1 shape:
+    workgroups with unequal tile counts, a split whose last chunk is one slice short, and
+    slice streams of odd length (padded with a zero slice) all give the float64 product."""
+    M, N, K = 128, 1536, 7168
+    monkeypatch.setenv("MLA_GEMM_PLAN", f"{M},{N},{K},1={plan}")
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(M, K, generator=g)
+    W = torch.randn(K, N, generator=g) / math.sqrt(K)
+    got = ext.gemm(gpu(A), gpu(W)).cpu()
+    ref = (A.double() @ W.double()).float()
+    torch.testing.assert_close(got, ref, **TOL)
+
+
 @pytest.mark.parametrize("M", [1, 128, 300])
 def test_rmsnorm(ext, M):
     g = torch.Generator().manual_seed(M)
