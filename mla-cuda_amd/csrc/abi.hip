@@ -321,9 +321,10 @@ struct AttnLayout {
 // The workspace of the attention path a call takes (use_flash: read per call, so a caller
 // that changes MLA_ATTENTION_PATH between the size query and the call gets
 // MLA_ERR_WORKSPACE, never an overrun).  Fused: ctx, row_sum, the split partials and 3d's
-// workspace -- no score matrix.  Per-step: scores, tile partials, alpha, row_sum, ctx and
-// the 3c / 3d workspaces.
-AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
+// workspace -- no score matrix; `ragged` (the paged entry points) sizes the partials for
+// the work list that balances per-sequence key counts.  Per-step: scores, tile partials,
+// alpha, row_sum, ctx and the 3c / 3d workspaces.
+AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d, bool ragged = false) {
     AttnLayout L;
     const size_t rows = (size_t)d->batch * d->sq * d->heads;
     L.ld_p = mla_score_ld(d->sk);
@@ -332,7 +333,9 @@ AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d) {
     size_t o = 0;
     L.fused = use_flash(dt, d);
     if (L.fused) {
-        L.flash = plan_flash(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
+        FlashProblem fp = flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0);
+        fp.ragged = ragged;
+        L.flash = plan_flash(fp);
         L.off_p = L.off_m = L.off_l = L.off_alpha = L.off_ctx_ws = 0;
         L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
         L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
@@ -1034,7 +1037,7 @@ size_t mla_attention_paged_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* 
     if (!dims || check_dtype(dtype) != MLA_OK || check_attn_dims(dtype, dims, causal) != MLA_OK ||
         check_pages(dims, page_size) != MLA_OK)
         return 0;
-    return attn_layout(dtype, dims).total;
+    return attn_layout(dtype, dims, true).total;
 }
 
 int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
@@ -1054,7 +1057,7 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
     MLA_CHECK(check_ptr(seq_lens, "seq_lens"));
     MLA_CHECK(check_ptr(W_uv, "W_uv"));
     MLA_CHECK(check_ptr(out, "out"));
-    const AttnLayout L = attn_layout(dtype, dims);
+    const AttnLayout L = attn_layout(dtype, dims, true);
     MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
 
     float* p = at<float>(workspace, L.off_p);
@@ -1066,7 +1069,8 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
     const int rows = dims->batch * dims->sq * dims->heads;
 
     if (L.fused) {
-        // 3a+3b+3c fused over the pages (each sequence to its own length), then 3d
+        // 3a+3b+3c fused over the pages (each sequence to its own length, the key chunks
+        // balanced over the CUs by a work list built from seq_lens), then 3d
         FlashProblem fp = flash_problem(dtype, dims, q_absorbed, q_rope, c_kv_pages, pe_pages,
                                         scale, causal);
         fp.seq_lens = seq_lens;

@@ -89,7 +89,82 @@ struct FlashArgs {
     const int* seq_lens;
     const int* block_table;
     int page_size, max_pages;
+    // balanced work list of a ragged batch (optional; flash_worklist_kernel): workgroup
+    // (item, row tile) runs chunk c of batch b for item = {b, c}; a batch of one chunk
+    // writes o_direct / l_direct (ctx, row_sum), the others partial slot first[b] + c
+    const int* wl;
+    float* o_direct;
+    float* l_direct;
 };
+
+// Work-list layout (ints): item count, chunk keys, first partial slot [B], chunk count
+// [B], then the items {b, c} -- every full-length chunk first, then the shorter last
+// chunks, so the longest pieces are dispatched first.
+constexpr int kWlHead = 2;
+__host__ __device__ inline int wl_ints(int B, int max_items) {
+    return kWlHead + 2 * B + 2 * max_items;
+}
+// Items of a balanced list: at most 512 / row_tiles + B (either chunk rule below), rounded
+// up to a whole number per XCD.
+__host__ __device__ inline int wl_max_items(int B, int row_tiles) {
+    return (512 / row_tiles + B + 1 + kNumXCDs - 1) / kNumXCDs * kNumXCDs;
+}
+
+// Keys per split of a dense batch of Sk keys: about one workgroup per CU for base =
+// B * row_tiles workgroups per split, at least 4 key blocks per split.
+__host__ __device__ inline int dense_keys_per_split(int Sk, int base, int block_keys) {
+    const int blocks = (Sk + block_keys - 1) / block_keys;
+    int split = (kNumCUs + base / 2) / base;
+    split = split < 1 ? 1 : split;
+    const int cap = blocks / 4 < 1 ? 1 : blocks / 4;
+    split = split < cap ? split : cap;
+    return (blocks + split - 1) / split * block_keys;
+}
+
+// What one workgroup of the attention pass computes: batch b, row tile rt, keys
+// [k_lo, k_lo + k_len) (clipped to the batch), and where its state goes: partial slot
+// `slot` (rows slot * rows_b ..), or ctx / row_sum directly.
+struct FlashWork {
+    int b, rt, k_lo, k_len;
+    int64_t slot;
+    bool direct, skip;
+};
+// Uniform splits: the logical workgroup order is XCD-major (the two row tiles of a batch
+// are neighbours on one XCD, so the second read of a key block hits its L2).  Work list:
+// workgroup i runs on XCD i % 8 in the dispatcher's order, and item t's row tiles are
+// workgroups 8 (row_tiles (t / 8) + rt) + t % 8 -- one XCD per item, the items (longest
+// first) spread over the XCDs in list order, and the unused tail of the grid spread too.
+__device__ __forceinline__ FlashWork flash_work(const FlashArgs& a) {
+    FlashWork w;
+    w.direct = false;
+    w.skip = false;
+    if (!a.wl) {
+        const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
+        const int sp = wg % a.n_split;
+        w.rt = (wg / a.n_split) % a.row_tiles;
+        w.b = wg / (a.n_split * a.row_tiles);
+        w.k_lo = sp * a.keys_per_split;
+        w.k_len = a.keys_per_split;
+        w.slot = (int64_t)sp * a.B + w.b;
+        return w;
+    }
+    const int x = blockIdx.x % kNumXCDs, q = blockIdx.x / kNumXCDs;
+    const int it = (q / a.row_tiles) * kNumXCDs + x;
+    w.rt = q % a.row_tiles;
+    w.b = 0; w.k_lo = 0; w.k_len = 0; w.slot = 0;
+    if (it >= load_uniform(a.wl)) {
+        w.skip = true;
+        return w;
+    }
+    const int* items = a.wl + kWlHead + 2 * a.B;
+    w.b = load_uniform(items + 2 * it);
+    const int c = load_uniform(items + 2 * it + 1);
+    w.k_len = load_uniform(a.wl + 1);
+    w.k_lo = c * w.k_len;
+    w.direct = load_uniform(a.wl + kWlHead + a.B + w.b) == 1;
+    w.slot = (int64_t)load_uniform(a.wl + kWlHead + w.b) + c;
+    return w;
+}
 
 // Keys of batch b, and the cache row of key k (a wave-uniform key inside the sequence; a
 // key past it maps to row 0, which only out-of-range loads then address).
@@ -193,22 +268,20 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStageBytes];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    // the two row tiles of a batch are consecutive logical workgroups on one XCD
-    const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
+    const FlashWork work = flash_work(a);
+    if (work.skip) return;   // past the end of a work list: the whole workgroup leaves
 
-    const int sp = wg % a.n_split;
-    const int rt = (wg / a.n_split) % a.row_tiles;
-    const int b = wg / (a.n_split * a.row_tiles);
+    const int rt = work.rt;
+    const int b = work.b;
     const int rows_b = a.Sq * a.H;
     const int r0 = rt * kFRows;
     const int row = r0 + 16 * wave + l16;            // this lane's row within the batch
-    const int rows_total = a.B * rows_b;
 
     // keys of this split; the causal rule (query s sees keys <= Sk_b - Sq + s) also trims
     // the range to the tile's last query
     const int skb = flash_batch_keys(a, b);
-    const int k_lo = sp * a.keys_per_split;
-    int k_hi = min(skb, k_lo + a.keys_per_split);
+    const int k_lo = work.k_lo;
+    int k_hi = min(skb, k_lo + work.k_len);
     int lim = k_hi - 1;                              // last visible key of this lane's row
     if (a.causal) {
         lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
@@ -461,12 +534,12 @@ __global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
     // ---- this split's partial state: O (lane l: row l%16, columns 16mb + 4g .. +3), m, l
     l_run = row4_reduce(l_run, OpSum{});
     if (row < rows_b) {
-        const int64_t slot = (int64_t)sp * rows_total + (int64_t)b * rows_b + row;
+        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
         if (g == 0) {
-            a.m[slot] = m_run;
-            a.l[slot] = l_run;
+            if (!work.direct) a.m[slot] = m_run;
+            (work.direct ? a.l_direct : a.l)[slot] = l_run;
         }
-        float* orow = a.o + slot * kFR;
+        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR;
         #pragma unroll
         for (int i = 0; i < kColBlocks; ++i)
             *reinterpret_cast<v4f*>(orow + 16 * i + 4 * g) = O[i];
@@ -534,22 +607,22 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     __shared__ int restart[2];   // [block parity]: some row outgrew its reference
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, g = lane >> 4;
-    const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
     if (tid < 2) restart[tid] = 0;   // read only after the first block's barrier
     const float* qa = reinterpret_cast<const float*>(a.qa);
     const float* qr = reinterpret_cast<const float*>(a.qr);
 
-    const int sp = wg % a.n_split;
-    const int rt = (wg / a.n_split) % a.row_tiles;
-    const int b = wg / (a.n_split * a.row_tiles);
+    const FlashWork work = flash_work(a);
+    if (work.skip) return;   // as in flash_kernel (restart[] is not read before a barrier)
+
+    const int rt = work.rt;
+    const int b = work.b;
     const int rows_b = a.Sq * a.H;
     const int r0 = rt * kFRows;
     const int row = r0 + 16 * wave + l16;
-    const int rows_total = a.B * rows_b;
 
     const int skb = flash_batch_keys(a, b);
-    const int k_lo = sp * a.keys_per_split;
-    int k_hi = min(skb, k_lo + a.keys_per_split);
+    const int k_lo = work.k_lo;
+    int k_hi = min(skb, k_lo + work.k_len);
     int lim = k_hi - 1;
     if (a.causal) {
         lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
@@ -759,12 +832,12 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     // ---- partial state: lane l holds row l%16, columns 32mh + 8g + 2i + r of O[mh][r][i]
     l_run = row4_reduce(l_run, OpSum{});
     if (row < rows_b) {
-        const int64_t slot = (int64_t)sp * rows_total + (int64_t)b * rows_b + row;
+        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
         if (g == 0) {
-            a.m[slot] = m_ref;
-            a.l[slot] = l_run;
+            if (!work.direct) a.m[slot] = m_ref;
+            (work.direct ? a.l_direct : a.l)[slot] = l_run;
         }
-        float* orow = a.o + slot * kFR;
+        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR;
         #pragma unroll
         for (int mh = 0; mh < 16; ++mh) {
             const v4f lo = {O[2 * mh][0], O[2 * mh + 1][0], O[2 * mh][1], O[2 * mh + 1][1]};
@@ -782,18 +855,31 @@ constexpr int kFStages = 4;   // LDS ring depth
 // w, w+4, ... (lane: 8 columns), and the four waves' sums are added in wave order -- a
 // fixed order, so the merge is deterministic.  Each wave keeps a split's 2 KB row in
 // flight per iteration, so many splits (small batches) do not serialise on latency.
+// Split s of row r (batch b, row i of the batch) is partial slot unit(s) * rows_b + i:
+// unit(s) = s * B + b for the uniform splits, first[b] + s for a work list (whose batches
+// of one chunk were written straight to ctx / row_sum and are skipped here).
 __global__ void __launch_bounds__(256) flash_merge_kernel(const float* __restrict__ o,
                                                           const float* __restrict__ m,
                                                           const float* __restrict__ l,
                                                           float* __restrict__ ctx,
-                                                          float* __restrict__ row_sum, int rows,
-                                                          int n_split) {
+                                                          float* __restrict__ row_sum, int B,
+                                                          int rows_b, int n_split,
+                                                          const int* __restrict__ wl) {
     __shared__ float red[256];
     __shared__ v4f part[4][64][2];
     __shared__ float lpart[4];
     const int r = blockIdx.x, tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int b = r / rows_b, i = r - b * rows_b;
+    int64_t unit0 = b, unit_step = B;
+    if (wl) {
+        n_split = load_uniform(wl + kWlHead + B + b);
+        if (n_split == 1) return;
+        unit0 = load_uniform(wl + kWlHead + b);
+        unit_step = 1;
+    }
+    auto slot_of = [&](int s) { return (unit0 + s * unit_step) * rows_b + i; };
     float mx = -INFINITY;
-    for (int s = tid; s < n_split; s += 256) mx = fmaxf(mx, m[(int64_t)s * rows + r]);
+    for (int s = tid; s < n_split; s += 256) mx = fmaxf(mx, m[slot_of(s)]);
     red[tid] = mx;
     __syncthreads();
     #pragma unroll
@@ -805,7 +891,7 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(const float* __restric
     v4f acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = acc0;
     float ls = 0.f;
     for (int s = wave; s < n_split; s += 4) {
-        const int64_t slot = (int64_t)s * rows + r;
+        const int64_t slot = slot_of(s);
         const float ms = m[slot];
         const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
         const v4f* src = reinterpret_cast<const v4f*>(o + slot * kFR) + 2 * lane;
@@ -830,6 +916,97 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(const float* __restric
     }
 }
 
+// Work list of a ragged batch (one workgroup; key counts are device data).  Chunk rule:
+//   every batch the same length L -> the dense plan's keys per split for L, so the list
+//     reproduces the dense launch exactly (same key ranges, same merge order);
+//   otherwise -> the total key count spread over 2 workgroups per CU (at least 4 key
+//     blocks), so the grid's work is even and a long sequence no longer sets the kernel's
+//     duration; the dispatcher's in-order issue then balances the pieces across CUs.
+// Batch b gets max(1, ceil(len_b / chunk)) chunks; partial slots are batch-major; items
+// list the full chunks first, then the shorter last chunks.
+__global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restrict__ seq_lens,
+                                                             int B, int Sk, int row_tiles,
+                                                             int block_keys, int max_items,
+                                                             int* __restrict__ wl) {
+    __shared__ long long s_tot[256];
+    __shared__ int s_min[256], s_max[256];
+    __shared__ int s_cnt[256], s_full[256], s_rem[256];
+    const int tid = threadIdx.x;
+    const int per = (B + 255) / 256;
+    const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
+    auto len_of = [&](int b) { return max(0, min(seq_lens[b], Sk)); };
+    long long tot = 0;
+    int mn = 0x7fffffff, mx = 0;
+    for (int b = b0; b < b1; ++b) {
+        const int L = len_of(b);
+        tot += L;
+        mn = min(mn, L);
+        mx = max(mx, L);
+    }
+    s_tot[tid] = tot; s_min[tid] = mn; s_max[tid] = mx;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (tid < w) {
+            s_tot[tid] += s_tot[tid + w];
+            s_min[tid] = min(s_min[tid], s_min[tid + w]);
+            s_max[tid] = max(s_max[tid], s_max[tid + w]);
+        }
+        __syncthreads();
+    }
+    int chunk;
+    if (s_min[0] == s_max[0]) {
+        chunk = dense_keys_per_split(max(1, s_max[0]), B * row_tiles, block_keys);
+    } else {
+        const long long want = (s_tot[0] * row_tiles + 2 * kNumCUs - 1) / (2 * kNumCUs);
+        // a multiple of the key block (a wave's keys then never straddle a page)
+        const long long cap = (Sk + block_keys - 1) / block_keys * block_keys;
+        chunk = (int)min<long long>((want + block_keys - 1) / block_keys * block_keys, cap);
+        chunk = max(chunk, 4 * block_keys);
+    }
+    __syncthreads();   // the reductions' slots are reused below
+    int cnt = 0, full = 0, rem = 0;
+    for (int b = b0; b < b1; ++b) {
+        const int L = len_of(b);
+        cnt += max(1, (L + chunk - 1) / chunk);
+        full += L / chunk;
+        rem += (L % chunk != 0 || L == 0) ? 1 : 0;
+    }
+    s_cnt[tid] = cnt; s_full[tid] = full; s_rem[tid] = rem;
+    __syncthreads();
+    // exclusive prefix sums over the threads (Hillis-Steele on the inclusive sums)
+    for (int d = 1; d < 256; d <<= 1) {
+        int c = 0, f = 0, r = 0;
+        if (tid >= d) { c = s_cnt[tid - d]; f = s_full[tid - d]; r = s_rem[tid - d]; }
+        __syncthreads();
+        s_cnt[tid] += c; s_full[tid] += f; s_rem[tid] += r;
+        __syncthreads();
+    }
+    const int n_full = s_full[255];
+    int slot = s_cnt[tid] - cnt, fi = s_full[tid] - full, ri = n_full + s_rem[tid] - rem;
+    int* first = wl + kWlHead;
+    int* count = first + B;
+    int* items = count + B;
+    for (int b = b0; b < b1; ++b) {
+        const int L = len_of(b);
+        const int n = max(1, (L + chunk - 1) / chunk);
+        first[b] = slot;
+        count[b] = n;
+        slot += n;
+        for (int c = 0; c < n; ++c) {
+            const bool is_full = (c + 1) * chunk <= L;
+            const int it = is_full ? fi++ : ri++;
+            if (it < max_items) {   // always (wl_max_items bounds both rules); a guard
+                items[2 * it] = b;
+                items[2 * it + 1] = c;
+            }
+        }
+    }
+    if (tid == 0) {
+        wl[0] = min(s_cnt[255], max_items);
+        wl[1] = chunk;
+    }
+}
+
 }  // namespace
 
 bool flash_supported(const FlashProblem& p) {
@@ -842,16 +1019,25 @@ FlashPlan plan_flash(const FlashProblem& p) {
     const int base = p.B * f.row_tiles;
     const int block_keys = p.bf16 ? kFKeys : k32Keys;
     const int blocks = (p.Sk + block_keys - 1) / block_keys;
-    // about one workgroup per CU (the LDS ring admits one per CU), at least 4 key blocks
-    // per split.  (Ragged batches keep this plan: four splits per sequence at B=128 were
-    // measured slower -- the partials' write and merge cost more than the shorter
-    // sequences' idle CUs.)
-    int split = std::max(1, (kNumCUs + base / 2) / base);
-    split = std::min(split, std::max(1, blocks / 4));
-    const int per = (blocks + split - 1) / split;
-    f.keys_per_split = per * block_keys;
-    f.n_split = (blocks + per - 1) / per;
     const size_t rows = (size_t)p.B * p.Sq * p.H;
+    const size_t rows_b = (size_t)p.Sq * p.H;
+    if (p.seq_lens || p.ragged) {
+        // ragged keys: a work list built on the device from the key counts balances the
+        // grid (flash_worklist_kernel); the partial slots, the list and its grid are sized
+        // for its largest case
+        f.balanced = true;
+        f.max_items = wl_max_items(p.B, f.row_tiles);
+        f.n_split = 0;
+        f.keys_per_split = 0;
+        const size_t wl_bytes = ((size_t)wl_ints(p.B, f.max_items) * sizeof(int) + 255) / 256 * 256;
+        f.partial_bytes = wl_bytes + (size_t)f.max_items * rows_b * (kFR + 2) * sizeof(float);
+        return f;
+    }
+    // about one workgroup per CU (the LDS ring admits one per CU), at least 4 key blocks
+    // per split
+    f.keys_per_split = dense_keys_per_split(p.Sk, base, block_keys);
+    const int per = f.keys_per_split / block_keys;
+    f.n_split = (blocks + per - 1) / per;
     // split partials (O, m, l); with one split O and l go straight to ctx / row_sum and
     // only the row maxima need a scratch row
     f.partial_bytes = f.n_split > 1 ? rows * f.n_split * (kFR + 2) * sizeof(float)
@@ -862,25 +1048,43 @@ FlashPlan plan_flash(const FlashProblem& p) {
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, float* row_sum,
                         float* partials, hipStream_t stream) {
     const int rows = p.B * p.Sq * p.H;
+    const int rows_b = p.Sq * p.H;
     FlashArgs a;
     a.qa = static_cast<const uint16_t*>(p.qa);
     a.qr = static_cast<const uint16_t*>(p.qr);
     a.ckv = static_cast<const uint16_t*>(p.ckv);
     a.pe = static_cast<const uint16_t*>(p.pe);
-    float* m_split;
-    if (f.n_split > 1) {
+    a.wl = nullptr;
+    a.o_direct = ctx;
+    a.l_direct = row_sum;
+    int grid;
+    int* wl = nullptr;
+    if (f.balanced) {
+        if (!p.seq_lens) return hipErrorInvalidValue;
+        wl = reinterpret_cast<int*>(partials);
+        const size_t wl_bytes =
+            ((size_t)wl_ints(p.B, f.max_items) * sizeof(int) + 255) / 256 * 256;
+        float* slots = reinterpret_cast<float*>(reinterpret_cast<char*>(partials) + wl_bytes);
+        a.wl = wl;
+        a.o = slots;
+        a.m = slots + (size_t)f.max_items * rows_b * kFR;
+        a.l = a.m + (size_t)f.max_items * rows_b;
+        grid = f.max_items * f.row_tiles;
+    } else if (f.n_split > 1) {
         a.o = partials;
         a.m = partials + (size_t)f.n_split * rows * kFR;
         a.l = a.m + (size_t)f.n_split * rows;
-        m_split = a.m;
+        grid = p.B * f.row_tiles * f.n_split;
     } else {
         a.o = ctx;
         a.l = row_sum;
         a.m = partials;   // the row maxima are not needed: a small scratch row
-        m_split = nullptr;
+        grid = p.B * f.row_tiles;
     }
     a.B = p.B; a.Sq = p.Sq; a.Sk = p.Sk; a.H = p.H;
-    a.n_split = f.n_split; a.keys_per_split = f.keys_per_split; a.row_tiles = f.row_tiles;
+    a.n_split = f.balanced ? 1 : f.n_split;
+    a.keys_per_split = f.keys_per_split;
+    a.row_tiles = f.row_tiles;
     a.key_stride = p.key_stride > 0 ? p.key_stride : p.Sk;
     a.c = 1.4426950408889634f / p.scale;
     a.causal = p.causal ? 1 : 0;
@@ -890,15 +1094,21 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     a.max_pages = p.page_size > 0 ? p.Sk / p.page_size : 0;
     if (p.block_table && (p.page_size <= 0 || p.page_size % 64 != 0 || p.Sk % p.page_size != 0))
         return hipErrorInvalidValue;
-    const int grid = p.B * f.row_tiles * f.n_split;
+    if (f.balanced) {
+        hipLaunchKernelGGL(flash_worklist_kernel, dim3(1), dim3(256), 0, stream, p.seq_lens,
+                           p.B, p.Sk, f.row_tiles, p.bf16 ? kFKeys : k32Keys, f.max_items,
+                           wl);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     if (p.bf16)
         hipLaunchKernelGGL(flash_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || f.n_split == 1) return e;
+    if (e != hipSuccess || (!f.balanced && f.n_split == 1)) return e;
     hipLaunchKernelGGL(flash_merge_kernel, dim3((unsigned)rows), dim3(256), 0, stream, a.o,
-                       m_split, a.l, ctx, row_sum, rows, f.n_split);
+                       a.m, a.l, ctx, row_sum, p.B, rows_b, f.n_split, a.wl);
     return hipGetLastError();
 }
 

@@ -137,12 +137,16 @@ struct FlashProblem {
     const int32_t* seq_lens = nullptr;
     const int32_t* block_table = nullptr;
     int page_size = 0;
+    bool ragged = false;         // plan for per-batch key counts (a size query sets this
+                                 // without seq_lens; a launch with it needs seq_lens)
 };
 struct FlashPlan {
-    int row_tiles = 1;           // 128-row tiles per batch
+    int row_tiles = 1;           // 64-row tiles per batch
     int n_split = 1;             // key splits (one workgroup each)
-    int keys_per_split = 0;      // multiple of 32
-    size_t partial_bytes = 0;    // scratch: split partials, merged into ctx / row_sum
+    int keys_per_split = 0;      // multiple of the key block
+    bool balanced = false;       // ragged keys: a device-built work list of key chunks
+    int max_items = 0;           // its largest item count (grid = max_items * row_tiles)
+    size_t partial_bytes = 0;    // scratch: split partials (and the work list)
 };
 bool flash_supported(const FlashProblem& p);
 FlashPlan plan_flash(const FlashProblem& p);

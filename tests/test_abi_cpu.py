@@ -274,10 +274,21 @@ def test_o_proj_validation_and_workspace(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "dims.hidden" in _err(lib)
 
 
-def test_paged_validation(lib):
+def test_paged_validation(lib, monkeypatch):
     d = dsv3(128, 1, 4992)
     ws = lib.mla_attention_paged_workspace_bytes(F32, ctypes.byref(d), 0, 64)
-    assert ws == lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0) > 0
+    dense = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0)
+    # the fused paged pass adds the work list and the partial slots of its balanced grid:
+    # at most 512 / row_tiles + B + 1 items (rounded up to a multiple of the 8 XCDs) of
+    # 128 rows x (512 + 2) floats, plus the list
+    row_tiles, B = 2, 128
+    items = -(-(512 // row_tiles + B + 1) // 8) * 8
+    extra = items * 128 * (512 + 2) * 4 + (2 + 2 * B + 2 * items) * 4
+    assert dense > 0 and dense < ws <= dense + extra + 4096
+    monkeypatch.setenv("MLA_ATTENTION_PATH", "split")   # the per-step path: same layout
+    assert (lib.mla_attention_paged_workspace_bytes(F32, ctypes.byref(d), 0, 64) ==
+            lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0))
+    monkeypatch.delenv("MLA_ATTENTION_PATH")
     assert lib.mla_attention_paged_workspace_bytes(F32, ctypes.byref(d), 0, 96) == 0
     args = [P16] * 6
     st = lib.mla_attention_paged(F32, ctypes.byref(d), *args, 100, P16, ctypes.c_double(13.85), 0,

@@ -7,8 +7,9 @@ other sequences' pages and unused ones), lengths are ragged and not multiples of
 or tile sizes.  Tolerances: fp32 rtol/atol 1e-4, bf16 2e-2 against the fp32 oracle on the
 rounded inputs; a paged cache laid out like the dense one must give the dense result
 bit for bit.  mla_attention_paged runs the fused 3a+3b+3c kernels at the DeepSeek-V3
-widths (the block table read per key block); MLA_ATTENTION_PATH=split selects the per-step
-kernels, and both paths are checked.
+widths (the block table read per key block, the key chunks of a ragged batch balanced by a
+device-built work list); MLA_ATTENTION_PATH=split selects the per-step kernels, and both
+paths are checked.
 """
 
 from __future__ import annotations
@@ -101,6 +102,45 @@ def test_paged_equals_dense_bitwise(ext, monkeypatch, path):
     dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
     paged = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck.reshape(-1, page, D.kv_rank)),
                                     gpu(pe.reshape(-1, page, D.rope)), gpu(table), gpu(sl),
+                                    gpu(wuv), SCALE)
+    assert torch.equal(dense.cpu(), paged.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_paged_balanced_work_list(ext, dtype):
+    """One long sequence among short ones: the fused pass's work list cuts the long one into
+    many key chunks (merged per row) while the short ones are single chunks written
+    directly; every row against the oracle."""
+    lens, page = [4989, 1, 2, 3, 100, 64, 65, 700], 64
+    B = len(lens)
+    max_pages = -(-max(lens) // page)
+    qa, qr, ck, pe, table, sl, wuv = paged_inputs(B, 1, lens, page, max_pages, seed=77)
+    s = 1 / math.sqrt(D.kv_rank)
+    qa, qr, wuv = qa * s, qr * s, wuv * s
+    qa, qr, ck, pe, wuv = [t.to(dtype) for t in (qa, qr, ck, pe, wuv)]
+    out = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(table), gpu(sl),
+                                  gpu(wuv), SCALE).float().cpu()
+    f = lambda t: t.float()  # noqa: E731
+    ref = R.mla_attention_paged(f(qa), f(qr), f(ck), f(pe), table, sl, f(wuv), SCALE)
+    torch.testing.assert_close(out, ref, **(TOL if dtype == torch.float32 else TOL_BF16))
+
+
+def test_paged_equal_short_lengths_equal_dense(ext):
+    """Every sequence the same length L below the pool's capacity: the work list takes the
+    dense plan for L, so the result equals the dense call on [B, L] bit for bit."""
+    B, L, page, max_pages = 3, 3000, 64, 78
+    g = torch.Generator().manual_seed(8)
+    qa = torch.randn(B, 1, D.n_heads, D.kv_rank, generator=g)
+    qr = torch.randn(B, 1, D.n_heads, D.rope, generator=g)
+    ck = torch.randn(B * max_pages, page, D.kv_rank, generator=g)
+    pe = torch.randn(B * max_pages, page, D.rope, generator=g)
+    wuv = torch.randn(D.n_heads, D.v, D.kv_rank, generator=g)
+    table = torch.arange(B * max_pages, dtype=torch.int32).reshape(B, max_pages)
+    sl = torch.full((B,), L, dtype=torch.int32)
+    dense_ck = ck.reshape(B, max_pages * page, D.kv_rank)[:, :L].contiguous()
+    dense_pe = pe.reshape(B, max_pages * page, D.rope)[:, :L].contiguous()
+    dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(dense_ck), gpu(dense_pe), gpu(wuv), SCALE)
+    paged = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(table), gpu(sl),
                                     gpu(wuv), SCALE)
     assert torch.equal(dense.cpu(), paged.cpu())
 
