@@ -10,10 +10,9 @@ DeepSeek-V3 dims.  Output: ONE JSON line on stdout.
 
 Timed region: W untimed warm-up layers, then exactly K layers bracketed by
 torch.cuda.synchronize() on both sides, each layer between its own pair of HIP events on
-the current stream and preceded (outside the pair) by a 512 MB device write that evicts
-the MALL and L2s; `value` is the mean per-layer time (median and a back-to-back figure
-beside it).  A second,
-separately timed pass runs the same kernels through the per-step ops with an event
+the current stream and preceded (outside the pair) by a 512 MB device read that evicts
+the MALL and L2s (leaving clean lines); `value` is the mean per-layer time (median and a
+back-to-back figure beside it).  A second, separately timed pass runs the same kernels through the per-step ops with an event
 between consecutive steps; it gives each step's average launch duration, from which the
 per-step GFLOP/s, GB/s, MFMA % and HBM % (algorithmic work, formulas below) and the
 `roofline` object of the dominant kernel are computed.
@@ -197,17 +196,21 @@ def main():
         return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale, causal)
 
     # ---- timed region: the fused boundary calls.  Each timed layer is preceded by a 512 MB
-    # device write outside its event pair, so no layer finds the previous one's weights or
+    # device read outside its event pair, so no layer finds the previous one's weights or
     # cache in the 256 MB MALL or the L2s; value = mean over the layers (median beside it).
+    # The flush reads rather than writes: a write leaves ~256 MB of dirty lines whose
+    # write-back then competes with the timed layer's own reads (measured: the B=1 q
+    # up-projection's 151 MB weight stream takes 53 us after a write flush, 34 us after a
+    # read), a cost a decode loop, whose big traffic is weight and cache reads, does not pay.
     for _ in range(args.warmup):
         out = layer()
-    flush = torch.empty(512 << 18, dtype=torch.float32, device=dev)   # 512 MB
+    flush = torch.zeros(512 << 18, dtype=torch.float32, device=dev)   # 512 MB
     torch.cuda.synchronize()
     lev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
     t_wall = time.perf_counter()
     for e0, e1 in lev:
-        flush.zero_()
+        flush_sum = flush.sum()   # noqa: F841  (reads all 512 MB)
         e0.record()
         out = layer()
         e1.record()

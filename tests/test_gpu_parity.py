@@ -63,6 +63,19 @@ def test_gemm(ext, M, N, K):
     torch.testing.assert_close(got, ref, **TOL)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 1536, 7168), (3, 1000, 300), (5, 260, 4100),
+                                   (2, 4, 64), (8, 24576, 1536), (4, 512, 36), (6, 260, 100)])
+def test_gemm_small_m(ext, M, N, K):
+    """Decode-sized products (M <= 8, fp32): a tile mostly past M, ragged column tiles, K
+    splits with a short last chunk, K below one slice."""
+    g = torch.Generator().manual_seed(M * 1000 + K)
+    A = torch.randn(M, K, generator=g)
+    W = torch.randn(K, N, generator=g) / math.sqrt(K)
+    got = ext.gemm(gpu(A), gpu(W)).cpu()
+    ref = (A.double() @ W.double()).float()
+    torch.testing.assert_close(got, ref, **TOL)
+
+
 @pytest.mark.parametrize("plan", ["64,64,1,3", "64,64,3,5", "128,128,1,7", "32,128,2,2"])
 def test_gemm_persistent_plans(ext, monkeypatch, plan):
     """Forced persistent-grid plans (bm, bn, split, tiles per workgroup) of the 2a1 shape:
