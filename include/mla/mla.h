@@ -260,7 +260,11 @@ int mla_q_absorbed_ragged(mla_dtype_t dtype, const mla_dims_t* dims, const void*
 /* Attention over the paged cache: sequence b attends to its first seq_lens[b] keys; with
  * causal, key j is visible to query i iff j <= seq_lens[b] - Sq + i (seq_lens[b] >= Sq).
  * Same queries, W_uv, scale and output as mla_attention, and like it the fused 3a+3b+3c
- * pass at kv_rank 512 / rope 64 (MLA_ATTENTION_PATH=split: the per-step kernels). */
+ * pass at kv_rank 512 / rope 64 (MLA_ATTENTION_PATH=split: the per-step kernels).  The
+ * fused pass cuts the sequences into key chunks from a work list it builds on the device
+ * from seq_lens (the total key count spread over the CUs; equal lengths take the dense
+ * split), so the workspace is larger than mla_attention's by the list and its partial
+ * slots. */
 size_t mla_attention_paged_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
                                            int causal, int32_t page_size);
 int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
