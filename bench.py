@@ -134,7 +134,7 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16"],
                     help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
@@ -202,9 +202,14 @@ def main():
     # write-back then competes with the timed layer's own reads (measured: the B=1 q
     # up-projection's 151 MB weight stream takes 53 us after a write flush, 34 us after a
     # read), a cost a decode loop, whose big traffic is weight and cache reads, does not pay.
-    for _ in range(args.warmup):
-        out = layer()
+    # The warm-up layers follow the same flush-then-layer pattern.  The clock takes ~15
+    # layers (~25 ms) of this loop to settle: with 3 warm-up layers the first timed layer
+    # ran 13% slower than the tenth, with 10 (pattern-matched) 4%, so the default warm-up is
+    # 20 layers and the mean is not carried by the ramp.
     flush = torch.zeros(512 << 18, dtype=torch.float32, device=dev)   # 512 MB
+    for _ in range(args.warmup):
+        flush_sum = flush.sum()   # noqa: F841
+        out = layer()
     torch.cuda.synchronize()
     lev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
