@@ -963,14 +963,29 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         chunk = (int)min<long long>((want + block_keys - 1) / block_keys * block_keys, cap);
         chunk = max(chunk, 4 * block_keys);
     }
-    __syncthreads();   // the reductions' slots are reused below
-    int cnt = 0, full = 0, rem = 0;
-    for (int b = b0; b < b1; ++b) {
-        const int L = len_of(b);
-        cnt += max(1, (L + chunk - 1) / chunk);
-        full += L / chunk;
-        rem += (L % chunk != 0 || L == 0) ? 1 : 0;
+    // The list must fit max_items (the slots and the grid are sized for it): both rules
+    // above keep it under wl_max_items, and a chunk that would not is doubled until it
+    // does (a chunk of Sk keys gives B items), so no item or slot can fall outside.
+    int cnt, full, rem;
+    for (;;) {
+        cnt = 0; full = 0; rem = 0;
+        for (int b = b0; b < b1; ++b) {
+            const int L = len_of(b);
+            cnt += max(1, (L + chunk - 1) / chunk);
+            full += L / chunk;
+            rem += (L % chunk != 0 || L == 0) ? 1 : 0;
+        }
+        __syncthreads();   // every thread has read the previous round's totals
+        s_cnt[tid] = cnt;
+        __syncthreads();
+        for (int w = 128; w > 0; w >>= 1) {
+            if (tid < w) s_cnt[tid] += s_cnt[tid + w];
+            __syncthreads();
+        }
+        if (s_cnt[0] <= max_items || chunk >= Sk) break;
+        chunk *= 2;
     }
+    __syncthreads();   // the total has been read; the slots are reused by the scan
     s_cnt[tid] = cnt; s_full[tid] = full; s_rem[tid] = rem;
     __syncthreads();
     // exclusive prefix sums over the threads (Hillis-Steele on the inclusive sums)
