@@ -104,10 +104,14 @@ constexpr int kWlHead = 2;
 __host__ __device__ inline int wl_ints(int B, int max_items) {
     return kWlHead + 2 * B + 2 * max_items;
 }
-// Items of a balanced list: at most 512 / row_tiles + B (either chunk rule below), rounded
-// up to a whole number per XCD.
+// A ragged list spreads the total key count over kWlPerCu workgroups per CU: at B=128 with
+// lengths uniform in [1, 4989] (fp32), 1 per CU took 1185 us, 2: 950, 3: 901, 4: 870-905,
+// 6: 926, 8: 907 (more pieces shorten the tail; each piece costs its Q load and partials).
+constexpr int kWlPerCu = 4;
+// Items of a balanced list: at most kWlPerCu * CUs / row_tiles + B (either chunk rule
+// below), rounded up to a whole number per XCD.
 __host__ __device__ inline int wl_max_items(int B, int row_tiles) {
-    return (512 / row_tiles + B + 1 + kNumXCDs - 1) / kNumXCDs * kNumXCDs;
+    return (kWlPerCu * kNumCUs / row_tiles + B + 1 + kNumXCDs - 1) / kNumXCDs * kNumXCDs;
 }
 
 // Keys per split of a dense batch of Sk keys: about one workgroup per CU for base =
@@ -919,9 +923,9 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(const float* __restric
 // Work list of a ragged batch (one workgroup; key counts are device data).  Chunk rule:
 //   every batch the same length L -> the dense plan's keys per split for L, so the list
 //     reproduces the dense launch exactly (same key ranges, same merge order);
-//   otherwise -> the total key count spread over 2 workgroups per CU (at least 4 key
-//     blocks), so the grid's work is even and a long sequence no longer sets the kernel's
-//     duration; the dispatcher's in-order issue then balances the pieces across CUs.
+//   otherwise -> the total key count spread over kWlPerCu workgroups per CU (at least 4
+//     key blocks), so the grid's work is even and a long sequence no longer sets the
+//     kernel's duration; the dispatcher's in-order issue then balances the pieces.
 // Batch b gets max(1, ceil(len_b / chunk)) chunks; partial slots are batch-major; items
 // list the full chunks first, then the shorter last chunks.
 __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restrict__ seq_lens,
@@ -957,7 +961,8 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
     if (s_min[0] == s_max[0]) {
         chunk = dense_keys_per_split(max(1, s_max[0]), B * row_tiles, block_keys);
     } else {
-        const long long want = (s_tot[0] * row_tiles + 2 * kNumCUs - 1) / (2 * kNumCUs);
+        const long long wgs = (long long)kWlPerCu * kNumCUs;
+        const long long want = (s_tot[0] * row_tiles + wgs - 1) / wgs;
         // a multiple of the key block (a wave's keys then never straddle a page)
         const long long cap = (Sk + block_keys - 1) / block_keys * block_keys;
         chunk = (int)min<long long>((want + block_keys - 1) / block_keys * block_keys, cap);

@@ -279,10 +279,10 @@ def test_paged_validation(lib, monkeypatch):
     ws = lib.mla_attention_paged_workspace_bytes(F32, ctypes.byref(d), 0, 64)
     dense = lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 0)
     # the fused paged pass adds the work list and the partial slots of its balanced grid:
-    # at most 512 / row_tiles + B + 1 items (rounded up to a multiple of the 8 XCDs) of
-    # 128 rows x (512 + 2) floats, plus the list
+    # at most 4 * 256 / row_tiles + B + 1 items (rounded up to a multiple of the 8 XCDs)
+    # of 128 rows x (512 + 2) floats, plus the list
     row_tiles, B = 2, 128
-    items = -(-(512 // row_tiles + B + 1) // 8) * 8
+    items = -(-(4 * 256 // row_tiles + B + 1) // 8) * 8
     extra = items * 128 * (512 + 2) * 4 + (2 + 2 * B + 2 * items) * 4
     assert dense > 0 and dense < ws <= dense + extra + 4096
     monkeypatch.setenv("MLA_ATTENTION_PATH", "split")   # the per-step path: same layout
