@@ -115,13 +115,14 @@ __host__ __device__ inline int wl_max_items(int B, int row_tiles) {
 }
 
 // Keys per split of a dense batch of Sk keys: about one workgroup per CU for base =
-// B * row_tiles workgroups per split, at least 4 key blocks per split.
+// B * row_tiles workgroups per split, at least one key block per split.  (Measured at B=1:
+// Sk=512 takes 25.0 us in 32 one-block splits against 33.0 us in 8 four-block ones; at
+// Sk=4989 the split size leaves the time unchanged.)
 __host__ __device__ inline int dense_keys_per_split(int Sk, int base, int block_keys) {
     const int blocks = (Sk + block_keys - 1) / block_keys;
     int split = (kNumCUs + base / 2) / base;
     split = split < 1 ? 1 : split;
-    const int cap = blocks / 4 < 1 ? 1 : blocks / 4;
-    split = split < cap ? split : cap;
+    split = split < blocks ? split : blocks;
     return (blocks + split - 1) / split * block_keys;
 }
 
@@ -1053,7 +1054,7 @@ FlashPlan plan_flash(const FlashProblem& p) {
         f.partial_bytes = wl_bytes + (size_t)f.max_items * rows_b * (kFR + 2) * sizeof(float);
         return f;
     }
-    // about one workgroup per CU (the LDS ring admits one per CU), at least 4 key blocks
+    // about one workgroup per CU (the LDS ring admits one per CU), at least one key block
     // per split
     f.keys_per_split = dense_keys_per_split(p.Sk, base, block_keys);
     const int per = f.keys_per_split / block_keys;
