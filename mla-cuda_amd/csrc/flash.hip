@@ -933,13 +933,31 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
                                                              int B, int Sk, int row_tiles,
                                                              int block_keys, int max_items,
                                                              int* __restrict__ wl) {
-    __shared__ long long s_tot[256];
-    __shared__ int s_min[256], s_max[256];
-    __shared__ int s_cnt[256], s_full[256], s_rem[256];
-    const int tid = threadIdx.x;
+    // reductions and scans run within each wave (__shfl_*), then over the four waves'
+    // totals in LDS: a handful of barriers, since this one-workgroup kernel sits on the
+    // decode step's critical path
+    __shared__ long long w_tot[4];
+    __shared__ int w_min[4], w_max[4], w_cnt[4], w_full[4], w_rem[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int per = (B + 255) / 256;
     const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
-    auto len_of = [&](int b) { return max(0, min(seq_lens[b], Sk)); };
+    // a thread's lengths stay in registers (up to 8 batches per thread, B <= 2048); past
+    // that they are read again
+    constexpr int kRegLens = 8;
+    int lens_r[kRegLens];
+    #pragma unroll
+    for (int i = 0; i < kRegLens; ++i)
+        lens_r[i] = b0 + i < b1 ? max(0, min(seq_lens[b0 + i], Sk)) : 0;
+    auto len_of = [&](int b) {
+        const int i = b - b0;
+        if (i < kRegLens) {
+            int v = 0;
+            #pragma unroll
+            for (int j = 0; j < kRegLens; ++j) v = j == i ? lens_r[j] : v;
+            return v;
+        }
+        return max(0, min(seq_lens[b], Sk));
+    };
     long long tot = 0;
     int mn = 0x7fffffff, mx = 0;
     for (int b = b0; b < b1; ++b) {
@@ -948,22 +966,22 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         mn = min(mn, L);
         mx = max(mx, L);
     }
-    s_tot[tid] = tot; s_min[tid] = mn; s_max[tid] = mx;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if (tid < w) {
-            s_tot[tid] += s_tot[tid + w];
-            s_min[tid] = min(s_min[tid], s_min[tid + w]);
-            s_max[tid] = max(s_max[tid], s_max[tid + w]);
-        }
-        __syncthreads();
+    for (int d = 32; d > 0; d >>= 1) {
+        tot += __shfl_xor(tot, d);
+        mn = min(mn, __shfl_xor(mn, d));
+        mx = max(mx, __shfl_xor(mx, d));
     }
+    if (lane == 0) { w_tot[wave] = tot; w_min[wave] = mn; w_max[wave] = mx; }
+    __syncthreads();
+    tot = ((w_tot[0] + w_tot[1]) + w_tot[2]) + w_tot[3];
+    mn = min(min(w_min[0], w_min[1]), min(w_min[2], w_min[3]));
+    mx = max(max(w_max[0], w_max[1]), max(w_max[2], w_max[3]));
     int chunk;
-    if (s_min[0] == s_max[0]) {
-        chunk = dense_keys_per_split(max(1, s_max[0]), B * row_tiles, block_keys);
+    if (mn == mx) {
+        chunk = dense_keys_per_split(max(1, mx), B * row_tiles, block_keys);
     } else {
         const long long wgs = (long long)kWlPerCu * kNumCUs;
-        const long long want = (s_tot[0] * row_tiles + wgs - 1) / wgs;
+        const long long want = (tot * row_tiles + wgs - 1) / wgs;
         // a multiple of the key block (a wave's keys then never straddle a page)
         const long long cap = (Sk + block_keys - 1) / block_keys * block_keys;
         chunk = (int)min<long long>((want + block_keys - 1) / block_keys * block_keys, cap);
@@ -981,32 +999,54 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
             full += L / chunk;
             rem += (L % chunk != 0 || L == 0) ? 1 : 0;
         }
-        __syncthreads();   // every thread has read the previous round's totals
-        s_cnt[tid] = cnt;
+        int c = cnt;
+        for (int d = 32; d > 0; d >>= 1) c += __shfl_xor(c, d);
+        __syncthreads();   // every thread has read the previous round's w_cnt
+        if (lane == 0) w_cnt[wave] = c;
         __syncthreads();
-        for (int w = 128; w > 0; w >>= 1) {
-            if (tid < w) s_cnt[tid] += s_cnt[tid + w];
-            __syncthreads();
-        }
-        if (s_cnt[0] <= max_items || chunk >= Sk) break;
+        const int total = ((w_cnt[0] + w_cnt[1]) + w_cnt[2]) + w_cnt[3];
+        if (total <= max_items || chunk >= Sk) break;
         chunk *= 2;
     }
-    __syncthreads();   // the total has been read; the slots are reused by the scan
-    s_cnt[tid] = cnt; s_full[tid] = full; s_rem[tid] = rem;
-    __syncthreads();
-    // exclusive prefix sums over the threads (Hillis-Steele on the inclusive sums)
-    for (int d = 1; d < 256; d <<= 1) {
-        int c = 0, f = 0, r = 0;
-        if (tid >= d) { c = s_cnt[tid - d]; f = s_full[tid - d]; r = s_rem[tid - d]; }
-        __syncthreads();
-        s_cnt[tid] += c; s_full[tid] += f; s_rem[tid] += r;
-        __syncthreads();
+    // exclusive prefix sums over the threads: inclusive scans within each wave, then the
+    // totals of the waves before
+    int ic = cnt, ifl = full, ir = rem;
+    for (int d = 1; d < 64; d <<= 1) {
+        const int c = __shfl_up(ic, d), f = __shfl_up(ifl, d), r = __shfl_up(ir, d);
+        if (lane >= d) { ic += c; ifl += f; ir += r; }
     }
-    const int n_full = s_full[255];
-    int slot = s_cnt[tid] - cnt, fi = s_full[tid] - full, ri = n_full + s_rem[tid] - rem;
+    __syncthreads();   // w_cnt of the loop above has been read by every thread
+    if (lane == 63) { w_cnt[wave] = ic; w_full[wave] = ifl; w_rem[wave] = ir; }
+    __syncthreads();
+    int pc = 0, pf = 0, pr = 0, n_full = 0, n_all = 0;
+    for (int w = 0; w < 4; ++w) {
+        if (w < wave) { pc += w_cnt[w]; pf += w_full[w]; pr += w_rem[w]; }
+        n_full += w_full[w];
+        n_all += w_cnt[w];
+    }
+    int slot = pc + ic - cnt, fi = pf + ifl - full, ri = n_full + pr + ir - rem;
     int* first = wl + kWlHead;
     int* count = first + B;
     int* items = count + B;
+    if (mn == mx) {
+        // equal lengths: every batch has the same chunks, so item t is computed directly
+        // (all threads write; at B=1 one thread would otherwise write every item)
+        const int n = max(1, (mx + chunk - 1) / chunk), nf = mx / chunk;
+        for (int b = tid; b < B; b += 256) {
+            first[b] = b * n;
+            count[b] = n;
+        }
+        for (int it = tid; it < min(n_all, max_items); it += 256) {
+            const bool is_full = it < B * nf;
+            items[2 * it] = is_full ? it / max(1, nf) : it - B * nf;
+            items[2 * it + 1] = is_full ? it % max(1, nf) : nf;
+        }
+        if (tid == 0) {
+            wl[0] = min(n_all, max_items);
+            wl[1] = chunk;
+        }
+        return;
+    }
     for (int b = b0; b < b1; ++b) {
         const int L = len_of(b);
         const int n = max(1, (L + chunk - 1) / chunk);
@@ -1016,14 +1056,14 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         for (int c = 0; c < n; ++c) {
             const bool is_full = (c + 1) * chunk <= L;
             const int it = is_full ? fi++ : ri++;
-            if (it < max_items) {   // always (wl_max_items bounds both rules); a guard
+            if (it < max_items) {   // always (the loop above); a guard
                 items[2 * it] = b;
                 items[2 * it + 1] = c;
             }
         }
     }
     if (tid == 0) {
-        wl[0] = min(s_cnt[255], max_items);
+        wl[0] = min(n_all, max_items);
         wl[1] = chunk;
     }
 }
