@@ -126,8 +126,16 @@ def cpu_baseline(inp, gpu_out, budget_s=30.0, causal=False):
     err = (gpu_out[:b_use].float().cpu() - ref).abs().max().item()
     sample = (f"{'full batch' if b_use == B else f'first {b_use} of {B} sequences, scaled x{B / b_use:.1f}'}"
               f"; oracle layer on CPU, 1 warm-up + median of 3")
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f
+                          if ln.startswith("model name")), "")
+    except OSError:
+        pass
     return {"value": round(us, 1), "unit": "µs", "cores": threads, "kind": "port",
-            "sample": sample}, err, b_use
+            "sample": sample, "torch_threads": torch.get_num_threads(),
+            "os_cpu_count": os.cpu_count(), "cpu_model": model}, err, b_use
 
 
 def main():
