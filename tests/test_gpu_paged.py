@@ -125,6 +125,32 @@ def test_paged_balanced_work_list(ext, dtype):
     torch.testing.assert_close(out, ref, **(TOL if dtype == torch.float32 else TOL_BF16))
 
 
+@pytest.mark.parametrize("uniform", [False, True], ids=["ragged", "equal"])
+def test_paged_work_list_many_sequences(ext, uniform):
+    """More sequences than the work-list kernel has threads (B = 300: two per thread), with
+    ragged lengths against the oracle on sampled sequences, and with equal lengths bit for
+    bit against the dense call."""
+    B, page, max_pages = 300, 64, 4
+    g = torch.Generator().manual_seed(300)
+    lens = (torch.full((B,), 200, dtype=torch.int32) if uniform
+            else torch.randint(1, 257, (B,), generator=g, dtype=torch.int32))
+    qa, qr, ck, pe, table, _, wuv = paged_inputs(B, 1, [1] * B, page, max_pages, seed=301)
+    qa, qr = qa / math.sqrt(D.kv_rank), qr / math.sqrt(D.kv_rank)
+    out = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(table), gpu(lens),
+                                  gpu(wuv), SCALE).cpu()
+    if uniform:
+        gather = lambda pool: torch.stack([R.gather_pages(pool, table[b], 200)  # noqa: E731
+                                           for b in range(B)])
+        dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(gather(ck)), gpu(gather(pe)), gpu(wuv),
+                                  SCALE).cpu()
+        assert torch.equal(out, dense)
+    else:
+        pick = [0, 1, 150, 255, 256, 299]
+        ref = R.mla_attention_paged(qa[pick], qr[pick], ck, pe, table[pick], lens[pick], wuv,
+                                    SCALE)
+        torch.testing.assert_close(out[pick], ref, **TOL)
+
+
 def test_paged_equal_short_lengths_equal_dense(ext):
     """Every sequence the same length L below the pool's capacity: the work list takes the
     dense plan for L, so the result equals the dense call on [B, L] bit for bit."""
