@@ -1047,6 +1047,32 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         }
         return;
     }
+    // Ragged: the shorter last chunks follow the full ones longest first (a counting sort
+    // over 256 length buckets), so the dispatcher hands out the longest remaining pieces
+    // first; the order inside a bucket is the LDS atomics' and does not matter, since an
+    // item's partial slot (first[b] + c) and so the merge order depend on b and c only.
+    // (Simulated in-order dispatch at B=128, lengths uniform in [1, 4989]: the makespan
+    // drops from 2916 to 2621 key-times against a 2571 lower bound.)
+    __shared__ int hist[256], cursor[256];
+    hist[tid] = 0;
+    cursor[tid] = 0;
+    __syncthreads();
+    auto bucket = [&](int r) { return (int)(((long long)(chunk - 1 - r) * 256) / chunk); };
+    for (int b = b0; b < b1; ++b) {
+        const int L = len_of(b);
+        if (L % chunk != 0 || L == 0) atomicAdd(&hist[bucket(L % chunk)], 1);
+    }
+    __syncthreads();
+    int hb = hist[tid], hs = hb;   // exclusive scan of the buckets in order
+    for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(hs, d);
+        if (lane >= d) hs += v;
+    }
+    if (lane == 63) w_rem[wave] = hs;   // w_rem was last read before the barrier above
+    __syncthreads();
+    for (int w = 0; w < wave; ++w) hs += w_rem[w];
+    hist[tid] = hs - hb;              // bucket start among the last chunks
+    __syncthreads();
     for (int b = b0; b < b1; ++b) {
         const int L = len_of(b);
         const int n = max(1, (L + chunk - 1) / chunk);
@@ -1055,13 +1081,15 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         slot += n;
         for (int c = 0; c < n; ++c) {
             const bool is_full = (c + 1) * chunk <= L;
-            const int it = is_full ? fi++ : ri++;
+            const int q = bucket(L % chunk);
+            const int it = is_full ? fi++ : n_full + hist[q] + atomicAdd(&cursor[q], 1);
             if (it < max_items) {   // always (the loop above); a guard
                 items[2 * it] = b;
                 items[2 * it + 1] = c;
             }
         }
     }
+    (void)ri;
     if (tid == 0) {
         wl[0] = min(n_all, max_items);
         wl[1] = chunk;
