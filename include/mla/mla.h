@@ -244,7 +244,10 @@ int mla_kv_append(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, cons
  *   c_kv_pages [num_pages, page_size, kv_rank], pe_pages [num_pages, page_size, rope]
  *   block_table [B, max_pages] int32: sequence b's keys [j*page_size, (j+1)*page_size)
  *               are page block_table[b*max_pages + j] of the pool
- *   seq_lens    [B] int32: keys of sequence b, 1 <= seq_lens[b] <= max_pages*page_size
+ *   seq_lens    [B] int32: keys of sequence b, clamped to [0, max_pages*page_size]; a
+ *               sequence without keys (or, with causal, a query that sees none) gives
+ *               zero output rows, as a softmax over no keys does in the reference's
+ *               formulation
  * page_size is a multiple of 64; dims->sk = max_pages * page_size (the table's key span).
  * Both tables are device memory, read by the kernels (no host synchronisation). */
 
@@ -272,6 +275,18 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
                         const int32_t* block_table, const int32_t* seq_lens, int32_t page_size,
                         const void* W_uv, double scale, int causal, void* out, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
+
+/* The work list that mla_attention_paged's fused pass builds on the device from seq_lens,
+ * written to `work_list` for inspection (a per-step view of that kernel; no reference
+ * counterpart).  int32 layout: [0] item count, [1] keys per chunk, first partial slot [B],
+ * chunk count [B], then the items {b, c} (chunk c of sequence b covers keys [c*chunk,
+ * min((c+1)*chunk, seq_lens[b]))): the full-length chunks first, then the shorter last
+ * chunks, longest first.  Uses dims->batch, sq, heads and sk (= max_pages * page_size);
+ * dtype selects the key block (16 keys for float32, 32 for bf16).
+ * mla_attention_work_list_ints() gives the list's length in ints (0 if dims are invalid). */
+int32_t mla_attention_work_list_ints(mla_dtype_t dtype, const mla_dims_t* dims);
+int mla_attention_work_list(mla_dtype_t dtype, const mla_dims_t* dims, const int32_t* seq_lens,
+                            int32_t* work_list, int32_t ints, hipStream_t stream);
 
 /* KV-cache append into the paged cache: as mla_kv_append, but token (b, s) is written to
  * logical slot positions[b*Sq + s] of sequence b (positions [B, Sq], int64): pool row

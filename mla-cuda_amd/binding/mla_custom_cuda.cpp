@@ -536,6 +536,28 @@ torch::Tensor op_mla_attention_paged(torch::Tensor q_absorbed, torch::Tensor q_r
     return out;
 }
 
+// The work list the fused paged pass builds from seq_lens (int32, layout in mla.h).
+torch::Tensor op_attention_work_list(torch::Tensor seq_lens, int64_t Sq, int64_t H, int64_t Sk,
+                                     torch::ScalarType dtype) {
+    TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.scalar_type() == torch::kInt32,
+                "seq_lens must be a 1-D int32 tensor (got ", seq_lens.sizes(), ")");
+    TORCH_CHECK(Sq > 0 && H > 0 && Sk > 0 && Sk < INT32_MAX, "MLA: Sq, H and Sk must be positive");
+    const mla_dtype_t dt = to_mla_dtype(torch::empty({0}, torch::TensorOptions().dtype(dtype)),
+                                        "dtype");
+    check_device({&seq_lens});
+    c10::DeviceGuard guard(seq_lens.device());
+    auto lens = seq_lens.contiguous();
+    mla_dims_t d{};
+    d.batch = (int32_t)lens.size(0); d.sq = (int32_t)Sq; d.heads = (int32_t)H; d.sk = (int32_t)Sk;
+    const int32_t n = mla_attention_work_list_ints(dt, &d);
+    TORCH_CHECK(n > 0, "MLA: invalid work-list dims");
+    auto wl = torch::empty({n}, lens.options());
+    check_status(mla_attention_work_list(dt, &d, lens.data_ptr<int32_t>(), wl.data_ptr<int32_t>(),
+                                         n, current_stream()),
+                 "attention_work_list");
+    return wl;
+}
+
 // KV-cache append into the paged cache: token (b, s) goes to slot positions[b, s] of
 // sequence b (pool row through block_table).
 void op_kv_append_paged(torch::Tensor x, torch::Tensor W_kv_a, torch::Tensor kv_norm_w,
@@ -741,6 +763,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv_pages"), py::arg("pe_pages"),
           py::arg("block_table"), py::arg("seq_lens"), py::arg("W_uv"), py::arg("scale"),
           py::arg("causal") = false);
+    m.def("attention_work_list", &op_attention_work_list,
+          "The fused paged pass's device-built work list for seq_lens (int32)",
+          py::arg("seq_lens"), py::arg("Sq"), py::arg("H"), py::arg("Sk"), py::arg("dtype"));
     m.def("kv_append_paged", &op_kv_append_paged,
           "KV-cache append into a paged cache: token (b, s) to slot positions[b, s]",
           py::arg("x"), py::arg("W_kv_a"), py::arg("kv_norm_w"), py::arg("positions"),

@@ -117,6 +117,18 @@ int check_q_dims(mla_dtype_t dt, const mla_dims_t* d) {
     return MLA_OK;
 }
 
+// The fields the work list reads: batch, sq, heads and sk (the block table's key span).
+int check_work_list_dims(const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->sk, "dims.sk"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    if ((int64_t)d->sq * d->heads > kMaxI32 / 2 || (int64_t)d->sk > kMaxI32 / 1024)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "sq*heads or sk too large");
+    return MLA_OK;
+}
+
 // The fields the 2b / 2c steps read: batch, sq, heads, nope, rope (+ kv_rank for 2c).
 int check_qraw_dims(mla_dtype_t dt, const mla_dims_t* d, bool absorb) {
     if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
@@ -1099,6 +1111,30 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
     // 3d
     GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
+    return ok();
+}
+
+int32_t mla_attention_work_list_ints(mla_dtype_t dtype, const mla_dims_t* dims) {
+    if (!dims || check_dtype(dtype) != MLA_OK || check_work_list_dims(dims) != MLA_OK) return 0;
+    FlashProblem fp = flash_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr, 1.0, 0);
+    fp.ragged = true;
+    return flash_worklist_ints(fp, plan_flash(fp));
+}
+
+int mla_attention_work_list(mla_dtype_t dtype, const mla_dims_t* dims, const int32_t* seq_lens,
+                            int32_t* work_list, int32_t ints, hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_work_list_dims(dims));
+    MLA_CHECK(check_ptr(seq_lens, "seq_lens"));
+    MLA_CHECK(check_ptr(work_list, "work_list"));
+    FlashProblem fp = flash_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr, 1.0, 0);
+    fp.ragged = true;
+    fp.seq_lens = seq_lens;
+    const FlashPlan plan = plan_flash(fp);
+    const int need = flash_worklist_ints(fp, plan);
+    if (ints < need)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "work_list holds %d ints, %d required", ints, need);
+    MLA_TRY_HIP(launch_flash_worklist(fp, plan, work_list, stream), "work list launch");
     return ok();
 }
 

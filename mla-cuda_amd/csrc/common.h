@@ -6,15 +6,13 @@
 #include <hip/hip_bf16.h>
 #include <stdint.h>
 
+#include "gpu_shape.h"
+
 namespace mla {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
-
-constexpr int kWave = 64;      // CDNA wavefront width
-constexpr int kNumCUs = 256;   // MI355X: 8 XCDs x 32 CUs
-constexpr int kNumXCDs = 8;
 
 // ----------------------------------------------------------------------------------
 // fp32 MFMA: D(32x32) += A(32x2) * B(2x32).  Lane l supplies A[l%32][l/32] and

@@ -44,6 +44,7 @@
 
 #include "kernels.h"
 #include "mma.h"
+#include "worklist.h"
 
 #include <math.h>
 
@@ -96,35 +97,6 @@ struct FlashArgs {
     float* o_direct;
     float* l_direct;
 };
-
-// Work-list layout (ints): item count, chunk keys, first partial slot [B], chunk count
-// [B], then the items {b, c} -- every full-length chunk first, then the shorter last
-// chunks, so the longest pieces are dispatched first.
-constexpr int kWlHead = 2;
-__host__ __device__ inline int wl_ints(int B, int max_items) {
-    return kWlHead + 2 * B + 2 * max_items;
-}
-// A ragged list spreads the total key count over kWlPerCu workgroups per CU: at B=128 with
-// lengths uniform in [1, 4989] (fp32), 1 per CU took 1185 us, 2: 950, 3: 901, 4: 870-905,
-// 6: 926, 8: 907 (more pieces shorten the tail; each piece costs its Q load and partials).
-constexpr int kWlPerCu = 4;
-// Items of a balanced list: at most kWlPerCu * CUs / row_tiles + B (either chunk rule
-// below), rounded up to a whole number per XCD.
-__host__ __device__ inline int wl_max_items(int B, int row_tiles) {
-    return (kWlPerCu * kNumCUs / row_tiles + B + 1 + kNumXCDs - 1) / kNumXCDs * kNumXCDs;
-}
-
-// Keys per split of a dense batch of Sk keys: about one workgroup per CU for base =
-// B * row_tiles workgroups per split, at least one key block per split.  (Measured at B=1:
-// Sk=512 takes 25.0 us in 32 one-block splits against 33.0 us in 8 four-block ones; at
-// Sk=4989 the split size leaves the time unchanged.)
-__host__ __device__ inline int dense_keys_per_split(int Sk, int base, int block_keys) {
-    const int blocks = (Sk + block_keys - 1) / block_keys;
-    int split = (kNumCUs + base / 2) / base;
-    split = split < 1 ? 1 : split;
-    split = split < blocks ? split : blocks;
-    return (blocks + split - 1) / split * block_keys;
-}
 
 // What one workgroup of the attention pass computes: batch b, row tile rt, keys
 // [k_lo, k_lo + k_len) (clipped to the batch), and where its state goes: partial slot
@@ -921,33 +893,29 @@ __global__ void __launch_bounds__(256) flash_merge_kernel(const float* __restric
     }
 }
 
-// Work list of a ragged batch (one workgroup; key counts are device data).  Chunk rule:
-//   every batch the same length L -> the dense plan's keys per split for L, so the list
-//     reproduces the dense launch exactly (same key ranges, same merge order);
-//   otherwise -> the total key count spread over kWlPerCu workgroups per CU (at least 4
-//     key blocks), so the grid's work is even and a long sequence no longer sets the
-//     kernel's duration; the dispatcher's in-order issue then balances the pieces.
-// Batch b gets max(1, ceil(len_b / chunk)) chunks; partial slots are batch-major; items
-// list the full chunks first, then the shorter last chunks.
-__global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restrict__ seq_lens,
-                                                             int B, int Sk, int row_tiles,
-                                                             int block_keys, int max_items,
-                                                             int* __restrict__ wl) {
+// Work list of a ragged batch (one workgroup; key counts are device data).  The chunk rule,
+// the fit check, each batch's chunk counts and the order of the items are the functions of
+// worklist.h; this kernel spreads them over its threads (thread tid owns batches
+// [wl_thread_first(tid), wl_thread_first(tid + 1))) and turns the sums they need into
+// wave-level reductions and scans.
+__global__ void __launch_bounds__(kWlThreads) flash_worklist_kernel(const int* __restrict__ seq_lens,
+                                                                    int B, int Sk, int row_tiles,
+                                                                    int block_keys, int max_items,
+                                                                    int* __restrict__ wl) {
     // reductions and scans run within each wave (__shfl_*), then over the four waves'
     // totals in LDS: a handful of barriers, since this one-workgroup kernel sits on the
     // decode step's critical path
+    static_assert(kWlThreads == 256 && kWlBuckets == 256, "one bucket per thread, four waves");
     __shared__ long long w_tot[4];
     __shared__ int w_min[4], w_max[4], w_cnt[4], w_full[4], w_rem[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int per = (B + 255) / 256;
-    const int b0 = min(B, tid * per), b1 = min(B, b0 + per);
+    const int b0 = wl_thread_first(tid, B), b1 = wl_thread_first(tid + 1, B);
     // a thread's lengths stay in registers (up to 8 batches per thread, B <= 2048); past
     // that they are read again
     constexpr int kRegLens = 8;
     int lens_r[kRegLens];
     #pragma unroll
-    for (int i = 0; i < kRegLens; ++i)
-        lens_r[i] = b0 + i < b1 ? max(0, min(seq_lens[b0 + i], Sk)) : 0;
+    for (int i = 0; i < kRegLens; ++i) lens_r[i] = b0 + i < b1 ? wl_len(seq_lens[b0 + i], Sk) : 0;
     auto len_of = [&](int b) {
         const int i = b - b0;
         if (i < kRegLens) {
@@ -956,7 +924,7 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
             for (int j = 0; j < kRegLens; ++j) v = j == i ? lens_r[j] : v;
             return v;
         }
-        return max(0, min(seq_lens[b], Sk));
+        return wl_len(seq_lens[b], Sk);
     };
     long long tot = 0;
     int mn = 0x7fffffff, mx = 0;
@@ -976,28 +944,14 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
     tot = ((w_tot[0] + w_tot[1]) + w_tot[2]) + w_tot[3];
     mn = min(min(w_min[0], w_min[1]), min(w_min[2], w_min[3]));
     mx = max(max(w_max[0], w_max[1]), max(w_max[2], w_max[3]));
-    int chunk;
-    if (mn == mx) {
-        chunk = dense_keys_per_split(max(1, mx), B * row_tiles, block_keys);
-    } else {
-        const long long wgs = (long long)kWlPerCu * kNumCUs;
-        const long long want = (tot * row_tiles + wgs - 1) / wgs;
-        // a multiple of the key block (a wave's keys then never straddle a page)
-        const long long cap = (Sk + block_keys - 1) / block_keys * block_keys;
-        chunk = (int)min<long long>((want + block_keys - 1) / block_keys * block_keys, cap);
-        chunk = max(chunk, 4 * block_keys);
-    }
-    // The list must fit max_items (the slots and the grid are sized for it): both rules
-    // above keep it under wl_max_items, and a chunk that would not is doubled until it
-    // does (a chunk of Sk keys gives B items), so no item or slot can fall outside.
-    int cnt, full, rem;
+    int chunk = wl_initial_chunk(tot, mn, mx, B, Sk, row_tiles, block_keys);
+    int cnt, full;
     for (;;) {
-        cnt = 0; full = 0; rem = 0;
+        cnt = 0; full = 0;
         for (int b = b0; b < b1; ++b) {
             const int L = len_of(b);
-            cnt += max(1, (L + chunk - 1) / chunk);
-            full += L / chunk;
-            rem += (L % chunk != 0 || L == 0) ? 1 : 0;
+            cnt += wl_chunk_count(L, chunk);
+            full += wl_full_count(L, chunk);
         }
         int c = cnt;
         for (int d = 32; d > 0; d >>= 1) c += __shfl_xor(c, d);
@@ -1005,62 +959,59 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         if (lane == 0) w_cnt[wave] = c;
         __syncthreads();
         const int total = ((w_cnt[0] + w_cnt[1]) + w_cnt[2]) + w_cnt[3];
-        if (total <= max_items || chunk >= Sk) break;
+        if (wl_fits(total, max_items, chunk, Sk)) break;
         chunk *= 2;
     }
     // exclusive prefix sums over the threads: inclusive scans within each wave, then the
     // totals of the waves before
-    int ic = cnt, ifl = full, ir = rem;
+    int ic = cnt, ifl = full;
     for (int d = 1; d < 64; d <<= 1) {
-        const int c = __shfl_up(ic, d), f = __shfl_up(ifl, d), r = __shfl_up(ir, d);
-        if (lane >= d) { ic += c; ifl += f; ir += r; }
+        const int c = __shfl_up(ic, d), f = __shfl_up(ifl, d);
+        if (lane >= d) { ic += c; ifl += f; }
     }
     __syncthreads();   // w_cnt of the loop above has been read by every thread
-    if (lane == 63) { w_cnt[wave] = ic; w_full[wave] = ifl; w_rem[wave] = ir; }
+    if (lane == 63) { w_cnt[wave] = ic; w_full[wave] = ifl; }
     __syncthreads();
-    int pc = 0, pf = 0, pr = 0, n_full = 0, n_all = 0;
+    int pc = 0, pf = 0, n_full = 0, n_all = 0;
     for (int w = 0; w < 4; ++w) {
-        if (w < wave) { pc += w_cnt[w]; pf += w_full[w]; pr += w_rem[w]; }
+        if (w < wave) { pc += w_cnt[w]; pf += w_full[w]; }
         n_full += w_full[w];
         n_all += w_cnt[w];
     }
-    int slot = pc + ic - cnt, fi = pf + ifl - full, ri = n_full + pr + ir - rem;
+    int slot = pc + ic - cnt, fi = pf + ifl - full;
     int* first = wl + kWlHead;
     int* count = first + B;
     int* items = count + B;
+    const int n_items = min(n_all, max_items);
     if (mn == mx) {
         // equal lengths: every batch has the same chunks, so item t is computed directly
         // (all threads write; at B=1 one thread would otherwise write every item)
-        const int n = max(1, (mx + chunk - 1) / chunk), nf = mx / chunk;
-        for (int b = tid; b < B; b += 256) {
+        const int n = wl_chunk_count(mx, chunk), nf = wl_full_count(mx, chunk);
+        for (int b = tid; b < B; b += kWlThreads) {
             first[b] = b * n;
             count[b] = n;
         }
-        for (int it = tid; it < min(n_all, max_items); it += 256) {
-            const bool is_full = it < B * nf;
-            items[2 * it] = is_full ? it / max(1, nf) : it - B * nf;
-            items[2 * it + 1] = is_full ? it % max(1, nf) : nf;
-        }
+        for (int it = tid; it < n_items; it += kWlThreads)
+            wl_equal_item(it, B, nf, &items[2 * it], &items[2 * it + 1]);
         if (tid == 0) {
-            wl[0] = min(n_all, max_items);
+            wl[0] = n_items;
             wl[1] = chunk;
         }
         return;
     }
     // Ragged: the shorter last chunks follow the full ones longest first (a counting sort
-    // over 256 length buckets), so the dispatcher hands out the longest remaining pieces
+    // over the length buckets), so the dispatcher hands out the longest remaining pieces
     // first; the order inside a bucket is the LDS atomics' and does not matter, since an
     // item's partial slot (first[b] + c) and so the merge order depend on b and c only.
     // (Simulated in-order dispatch at B=128, lengths uniform in [1, 4989]: the makespan
     // drops from 2916 to 2621 key-times against a 2571 lower bound.)
-    __shared__ int hist[256], cursor[256];
+    __shared__ int hist[kWlBuckets], cursor[kWlBuckets];
     hist[tid] = 0;
     cursor[tid] = 0;
     __syncthreads();
-    auto bucket = [&](int r) { return (int)(((long long)(chunk - 1 - r) * 256) / chunk); };
     for (int b = b0; b < b1; ++b) {
         const int L = len_of(b);
-        if (L % chunk != 0 || L == 0) atomicAdd(&hist[bucket(L % chunk)], 1);
+        if (wl_has_short(L, chunk)) atomicAdd(&hist[wl_bucket(L, chunk)], 1);
     }
     __syncthreads();
     int hb = hist[tid], hs = hb;   // exclusive scan of the buckets in order
@@ -1068,30 +1019,29 @@ __global__ void __launch_bounds__(256) flash_worklist_kernel(const int* __restri
         const int v = __shfl_up(hs, d);
         if (lane >= d) hs += v;
     }
-    if (lane == 63) w_rem[wave] = hs;   // w_rem was last read before the barrier above
+    if (lane == 63) w_rem[wave] = hs;
     __syncthreads();
     for (int w = 0; w < wave; ++w) hs += w_rem[w];
     hist[tid] = hs - hb;              // bucket start among the last chunks
     __syncthreads();
     for (int b = b0; b < b1; ++b) {
         const int L = len_of(b);
-        const int n = max(1, (L + chunk - 1) / chunk);
+        const int n = wl_chunk_count(L, chunk);
         first[b] = slot;
         count[b] = n;
         slot += n;
         for (int c = 0; c < n; ++c) {
-            const bool is_full = (c + 1) * chunk <= L;
-            const int q = bucket(L % chunk);
+            const bool is_full = (long long)(c + 1) * chunk <= L;
+            const int q = wl_bucket(L, chunk);
             const int it = is_full ? fi++ : n_full + hist[q] + atomicAdd(&cursor[q], 1);
-            if (it < max_items) {   // always (the loop above); a guard
+            if (it < max_items) {   // always (the fit check above); a guard
                 items[2 * it] = b;
                 items[2 * it + 1] = c;
             }
         }
     }
-    (void)ri;
     if (tid == 0) {
-        wl[0] = min(n_all, max_items);
+        wl[0] = n_items;
         wl[1] = chunk;
     }
 }
@@ -1132,6 +1082,18 @@ FlashPlan plan_flash(const FlashProblem& p) {
     f.partial_bytes = f.n_split > 1 ? rows * f.n_split * (kFR + 2) * sizeof(float)
                                     : rows * sizeof(float);
     return f;
+}
+
+int flash_worklist_ints(const FlashProblem& p, const FlashPlan& f) {
+    return f.balanced ? wl_ints(p.B, f.max_items) : 0;
+}
+
+hipError_t launch_flash_worklist(const FlashProblem& p, const FlashPlan& f, int* wl,
+                                 hipStream_t stream) {
+    if (!f.balanced || !p.seq_lens) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(flash_worklist_kernel, dim3(1), dim3(kWlThreads), 0, stream, p.seq_lens,
+                       p.B, p.Sk, f.row_tiles, p.bf16 ? kFKeys : k32Keys, f.max_items, wl);
+    return hipGetLastError();
 }
 
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, float* row_sum,
@@ -1184,10 +1146,7 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     if (p.block_table && (p.page_size <= 0 || p.page_size % 64 != 0 || p.Sk % p.page_size != 0))
         return hipErrorInvalidValue;
     if (f.balanced) {
-        hipLaunchKernelGGL(flash_worklist_kernel, dim3(1), dim3(256), 0, stream, p.seq_lens,
-                           p.B, p.Sk, f.row_tiles, p.bf16 ? kFKeys : k32Keys, f.max_items,
-                           wl);
-        hipError_t e = hipGetLastError();
+        hipError_t e = launch_flash_worklist(p, f, wl, stream);
         if (e != hipSuccess) return e;
     }
     if (p.bf16)

@@ -130,7 +130,10 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
         row_scale[i] = 1.f;
         if (AMODE == kARowRecip) {
             const int m = m0 + i * 32 + (tid >> 3);
-            if (m < a.M) row_scale[i] = 1.f / a.rs[(int64_t)m * a.rs_m + (int64_t)g * a.rs_g];
+            // a row without visible keys (row sum 0, ctx 0) gives zeros, as the oracle's
+            // softmax over no keys does
+            const float rs = m < a.M ? a.rs[(int64_t)m * a.rs_m + (int64_t)g * a.rs_g] : 1.f;
+            row_scale[i] = rs == 0.f ? 0.f : 1.f / rs;
         }
     }
 

@@ -152,5 +152,10 @@ bool flash_supported(const FlashProblem& p);
 FlashPlan plan_flash(const FlashProblem& p);
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& plan, float* ctx, float* row_sum,
                         float* partials, hipStream_t stream);
+// The work list alone (plan.balanced, seq_lens given): wl receives flash_worklist_ints()
+// ints, laid out as worklist.h describes.
+int flash_worklist_ints(const FlashProblem& p, const FlashPlan& plan);
+hipError_t launch_flash_worklist(const FlashProblem& p, const FlashPlan& plan, int* wl,
+                                 hipStream_t stream);
 
 }  // namespace mla

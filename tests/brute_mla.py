@@ -93,3 +93,34 @@ def o_proj(attn, W_o):
     return [[[sum(attn[b][s][h][d] * W_o[h * v + d][n] for h in range(H) for d in range(v))
               for n in range(N)] for s in range(Sq)] for b in range(B)]
 
+
+
+def q_rows(x, W_q_a, gain, W_q_b, wkv_b, positions, H, nope, rope, eps=1e-6):
+    """The Q path alone, with per-sequence positions: positions[b][s] is query (b, s)'s
+    position.  Returns (q_absorbed[b][s][h][r], q_rope[b][s][h][d]) from the mathematics:
+    q = RMSNorm(x W_q_a) * gain . W_q_b; q_rope = interleaved-pair rotation of each head's
+    rope part; q_absorbed = each head's nope part times W_uk = wkv_b[h][:nope]."""
+    B, Sq, hidden = len(x), len(x[0]), len(x[0][0])
+    q_lora = len(gain)
+    R = len(wkv_b[0][0])
+    qk = nope + rope
+    qa_all = [[[None] * H for _ in range(Sq)] for _ in range(B)]
+    qr_all = [[[None] * H for _ in range(Sq)] for _ in range(B)]
+    for b in range(B):
+        for s in range(Sq):
+            lat = [sum(x[b][s][c] * W_q_a[c][j] for c in range(hidden)) for j in range(q_lora)]
+            inv = 1.0 / math.sqrt(sum(t * t for t in lat) / q_lora + eps)
+            lat = [lat[j] * inv * gain[j] for j in range(q_lora)]
+            q = [sum(lat[j] * W_q_b[j][n] for j in range(q_lora)) for n in range(H * qk)]
+            ang = rope_angles(float(positions[b][s]), rope)
+            for h in range(H):
+                qn, qp = q[h * qk:h * qk + nope], q[h * qk + nope:(h + 1) * qk]
+                qr = [0.0] * rope
+                for i in range(rope // 2):
+                    e, o = qp[2 * i], qp[2 * i + 1]
+                    qr[2 * i] = e * math.cos(ang[i]) - o * math.sin(ang[i])
+                    qr[2 * i + 1] = e * math.sin(ang[i]) + o * math.cos(ang[i])
+                qa_all[b][s][h] = [sum(qn[i] * wkv_b[h][i][r] for i in range(nope))
+                                   for r in range(R)]
+                qr_all[b][s][h] = qr
+    return qa_all, qr_all

@@ -412,3 +412,24 @@ def test_binding_paged_shape_errors(ext):
                        torch.zeros(32, 4 * 24), torch.zeros(4, 16, 16),
                        torch.zeros(3, 1, dtype=torch.int64), 16, 8, 1e-6)
 
+
+
+def test_work_list_validation_and_size(lib):
+    """The per-step view of the ragged work list: its length is wl_ints(B, max_items) and
+    it is validated before any HIP call."""
+    import wl_check as W
+    for B, Sq, dt, bk in [(1, 1, F32, 16), (128, 1, BF16, 32), (300, 4, F32, 16)]:
+        d = dsv3(B, Sq, 4992)
+        rt = W.row_tiles_of(Sq, 128)
+        n = lib.mla_attention_work_list_ints(dt, ctypes.byref(d))
+        assert n == W.harness().wl_harness_ints(B, W.max_items(B, rt))
+    d = dsv3(4, 1, 4992)
+    n = lib.mla_attention_work_list_ints(F32, ctypes.byref(d))
+    st = lib.mla_attention_work_list(F32, ctypes.byref(d), P16, P16, n - 1, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "ints" in _err(lib)
+    st = lib.mla_attention_work_list(F32, ctypes.byref(d), None, P16, n, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "seq_lens" in _err(lib)
+    d.batch = 0
+    assert lib.mla_attention_work_list_ints(F32, ctypes.byref(d)) == 0
+    st = lib.mla_attention_work_list(F32, ctypes.byref(d), P16, P16, n, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "batch" in _err(lib)

@@ -128,13 +128,12 @@ def test_layer_bf16_vs_fp32_oracle(ext, B, Sq, Sk):
 
 
 def test_layer_bf16_cfg4_full_size(ext):
-    """bf16 decode at B=128, Sq=1, Sk=4989; oracle on three sequences."""
+    """bf16 decode at B=128, Sq=1, Sk=4989; every sequence against the fp32 oracle on the
+    bf16-rounded inputs at the bf16 tolerance."""
     inp = R.make_inputs(128, 1, 4989, seed=0, dtype=BF)
     qa, qr, out = run_layer(ext, inp)
-    pick = [0, 64, 127]
+    assert torch.isfinite(out.float()).all()
     f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
-    for k in ("x", "c_kv", "pe_cache"):
-        f32[k] = f32[k][pick]
     ref = R.mla_layer(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], f32["wkv_b"],
                       f32["c_kv"], f32["pe_cache"], f32["positions"])
-    torch.testing.assert_close(out.float().cpu()[pick], ref, rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(out.float().cpu(), ref, rtol=2e-2, atol=2e-2)

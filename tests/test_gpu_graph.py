@@ -72,9 +72,13 @@ def test_layer_graph_replay(ext, dtype, B, Sk):
 
 
 def test_paged_attention_graph_replay(ext):
-    """The paged attention (block table, ragged lengths) replays the same way."""
+    """The paged attention (block table, ragged lengths) replays the same way.  The lengths
+    are device data read by the replayed kernels, so a captured decode step stays valid as
+    they change: between replays they grow by one key, then become equal (the dense split
+    rule), then ragged again; every replay equals an eager call on the same lengths bit for
+    bit."""
     B, page, lens = 3, 64, [700, 64, 1]
-    mp = -(-max(lens) // page)
+    mp = -(-max(lens) // page) + 1
     g = torch.Generator().manual_seed(21)
     qa = torch.randn(B, 1, D.n_heads, D.kv_rank, generator=g)
     qr = torch.randn(B, 1, D.n_heads, D.rope, generator=g)
@@ -84,15 +88,24 @@ def test_paged_attention_graph_replay(ext):
     table = torch.randperm(B * mp, generator=g).to(torch.int32).reshape(B, mp)
     sl = torch.tensor(lens, dtype=torch.int32)
     args = [t.to(DEV) for t in (qa, qr, ck, pe, table, sl, wuv)]
+    sl_dev = args[5]
     scale = math.sqrt(D.qk_head)
     eager = ext.mla_attention_paged(*args, scale)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         out_g = ext.mla_attention_paged(*args, scale)
-    for _ in range(3):
+    schedule = [lens, [n + 1 for n in lens], [300] * B, [5, 64 * mp, 100], lens]
+    for step_lens in schedule:
+        sl_dev.copy_(torch.tensor(step_lens, dtype=torch.int32))   # in place: same address
+        torch.cuda.synchronize()
+        eager = ext.mla_attention_paged(*args, scale).clone()
+        torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(out_g, eager)
-        ext.mla_attention_paged(*args[:6], args[6] * 2.0, scale)
+        assert torch.equal(out_g, eager), f"replay differs from eager at lengths {step_lens}"
+        ext.mla_attention_paged(*args[:6], args[6] * 2.0, scale)   # other eager work
         torch.cuda.synchronize()
+    ref = R.mla_attention_paged(qa, qr, ck, pe, table, torch.tensor(lens, dtype=torch.int32),
+                                wuv, scale)
+    torch.testing.assert_close(out_g.cpu(), ref, rtol=1e-4, atol=1e-4)

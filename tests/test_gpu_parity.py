@@ -8,8 +8,9 @@ copied to the GPU, so HIP path and oracle see identical values.  Tolerances:
   fp32-vs-fp64 noise of the same op (check_3d.py:40-44);
 * per-step fp32 intermediates: rtol/atol 1e-4 on O(1) quantities, 1e-5 on softmax factors.
 
-At the full decode sizes the oracle runs on a subset of sequences (each sequence's
-attention is independent), which keeps every test to seconds on the box's CPU.
+Layer tests compare every sequence with the oracle, the headline size (B=128, Sk=4989)
+included; the long-context causal shape compares its whole Q path and 16 query rows of the
+attention, each against the oracle on exactly the keys it sees.
 """
 
 from __future__ import annotations
@@ -248,27 +249,47 @@ def test_q_absorbed_cfg1(ext):
 def test_layer_cfg3_small_batch(ext, B):
     inp = R.make_inputs(B, 1, 4989, seed=0)
     qa, qr, out = run_layer(ext, inp)
-    pick = sorted({0, B // 2, B - 1})
-    rqa, rqr, rout = oracle_layer_rows(inp, pick)
-    torch.testing.assert_close(qa.cpu()[pick], rqa, **TOL)
-    torch.testing.assert_close(qr.cpu()[pick], rqr, **TOL)
-    torch.testing.assert_close(out.cpu()[pick], rout, **TOL)
+    rqa, rqr, rout = oracle_layer_rows(inp, list(range(B)))
+    torch.testing.assert_close(qa.cpu(), rqa, **TOL)
+    torch.testing.assert_close(qr.cpu(), rqr, **TOL)
+    torch.testing.assert_close(out.cpu(), rout, **TOL)
 
 
 def test_layer_cfg2_full_size(ext):
-    """Headline decode shape: B=128, Sq=1, Sk=4989, fp32, full DeepSeek-V3 dims."""
+    """Headline decode shape: B=128, Sq=1, Sk=4989, fp32, full DeepSeek-V3 dims; every
+    sequence against the oracle at the north-star tolerance."""
     inp = R.make_inputs(128, 1, 4989, seed=0)
     qa, qr, out = run_layer(ext, inp)
     assert torch.isfinite(out).all()
-    pick = [0, 63, 127]
-    rqa, rqr, rout = oracle_layer_rows(inp, pick)
-    torch.testing.assert_close(qa.cpu()[pick], rqa, **TOL)
-    torch.testing.assert_close(out.cpu()[pick], rout, **TOL)
-    # size-independent property over all 128 sequences: the output is linear in W_uv
+    rqa, rqr, rout = oracle_layer_rows(inp, list(range(128)))
+    torch.testing.assert_close(qa.cpu(), rqa, **TOL)
+    torch.testing.assert_close(qr.cpu(), rqr, **TOL)
+    torch.testing.assert_close(out.cpu(), rout, **TOL)
+
+
+def test_layer_cfg5_fused_causal_full_size(ext):
+    """The chunked-prefill configuration through the path bench.py times: q_absorbed at
+    Sq=128 with positions Sk-128 .. Sk-1, then the fused mla_attention(causal=True), B=4,
+    Sk=32768, fp32.  The Q path is compared whole; the attention on 16 (sequence, query)
+    rows -- each sequence's first and last query and two between -- against the oracle on
+    exactly the keys each query sees (key j visible to query s iff j <= Sk - Sq + s)."""
+    B, Sq, Sk = 4, 128, 32768
+    inp = R.make_inputs(B, Sq, Sk, seed=0)
+    qa, qr, out = run_layer(ext, inp, causal=True)
+    assert out.shape == (B, Sq, D.n_heads, D.v) and torch.isfinite(out).all()
     W_uk, W_uv = R.split_wkv_b(inp["wkv_b"], D.nope)
-    out2 = ext.mla_attention(qa, qr, gpu(inp["c_kv"]), gpu(inp["pe_cache"]),
-                             gpu((2.0 * W_uv).contiguous()), SCALE)
-    torch.testing.assert_close(out2, 2.0 * out, rtol=1e-6, atol=1e-6)
+    rqa, rqr = R.prepare_q_mla_absorbed(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
+                                        W_uk, inp["positions"], D.nope, D.rope)
+    torch.testing.assert_close(qa.cpu(), rqa, **TOL)
+    torch.testing.assert_close(qr.cpu(), rqr, **TOL)
+    qa_c, qr_c = qa.cpu(), qr.cpu()
+    for b in range(B):
+        for s in (0, 41 + 7 * b, 90 - 5 * b, Sq - 1):
+            lim = Sk - Sq + s + 1
+            ref = R.mla_attention_official(qa_c[b:b + 1, s:s + 1], qr_c[b:b + 1, s:s + 1],
+                                           inp["c_kv"][b:b + 1, :lim],
+                                           inp["pe_cache"][b:b + 1, :lim], W_uv, SCALE)
+            torch.testing.assert_close(out[b, s].cpu(), ref[0, 0], **TOL)
 
 
 def test_reference_input_convention(ext):
@@ -281,7 +302,6 @@ def test_reference_input_convention(ext):
     inp["pe_cache"] = inp["pe_cache"] / math.sqrt(D.rope)
     inp["wkv_b"] = inp["wkv_b"] * math.sqrt(D.kv_rank) / math.sqrt(D.nope)
     qa, qr, out = run_layer(ext, inp)
-    pick = [0, 31, 63]
-    _, _, rout = oracle_layer_rows(inp, pick)
-    torch.testing.assert_close(out.cpu()[pick], rout, rtol=3e-2, atol=3e-2)
-    torch.testing.assert_close(out.cpu()[pick], rout, **TOL)
+    _, _, rout = oracle_layer_rows(inp, list(range(64)))
+    torch.testing.assert_close(out.cpu(), rout, rtol=3e-2, atol=3e-2)
+    torch.testing.assert_close(out.cpu(), rout, **TOL)

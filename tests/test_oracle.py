@@ -419,3 +419,55 @@ def test_kv_append_paged_reduces_to_dense():
     torch.testing.assert_close(c2, rc, rtol=0, atol=0)
     torch.testing.assert_close(p2, rp, rtol=0, atol=0)
     assert _kv_brute_check(c2, p2, x, W, gain, pos[0], c_kv, pe, start) < 1e-12
+
+
+# --------------------------------------------------------------------------- ragged Q path
+
+
+def _ragged_q(inp, pos, dims=TINY):
+    W_uk = R.split_wkv_b(inp["wkv_b"], dims.nope)[0]
+    return R.prepare_q_ragged(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"], W_uk, pos,
+                              dims.nope, dims.rope)
+
+
+def test_prepare_q_ragged_matches_brute_force():
+    """Per-sequence positions (distinct per row, large ones included) against the scalar
+    brute force of the Q path."""
+    inp = R.make_inputs(3, 2, 4, TINY, seed=31, dtype=torch.float64)
+    pos = torch.tensor([[10, 11], [4987, 4988], [0, 65535]])
+    qa, qr = _ragged_q(inp, pos)
+    bqa, bqr = brute_mla.q_rows(inp["x"].tolist(), inp["W_q_a"].tolist(),
+                                inp["q_norm_w"].tolist(), inp["W_q_b"].tolist(),
+                                inp["wkv_b"].tolist(), pos.tolist(), TINY.n_heads, TINY.nope,
+                                TINY.rope)
+    assert qa.shape == (3, 2, TINY.n_heads, TINY.kv_rank) and qr.shape == (3, 2, TINY.n_heads,
+                                                                            TINY.rope)
+    torch.testing.assert_close(qa, torch.tensor(bqa, dtype=torch.float64), rtol=1e-11, atol=1e-12)
+    torch.testing.assert_close(qr, torch.tensor(bqr, dtype=torch.float64), rtol=1e-10, atol=1e-11)
+
+
+def test_prepare_q_ragged_equal_rows_equal_shared_positions():
+    """Every sequence at the same positions: exactly the shared-positions Q path."""
+    inp = R.make_inputs(4, 3, 5, TINY, seed=32, dtype=torch.float64)
+    pos = inp["positions"]
+    qa, qr = _ragged_q(inp, pos.unsqueeze(0).expand(4, -1))
+    W_uk = R.split_wkv_b(inp["wkv_b"], TINY.nope)[0]
+    sqa, sqr = R.prepare_q_mla_absorbed(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
+                                        W_uk, pos, TINY.nope, TINY.rope)
+    torch.testing.assert_close(qa, sqa, rtol=0, atol=1e-14)
+    torch.testing.assert_close(qr, sqr, rtol=0, atol=1e-14)
+
+
+def test_prepare_q_ragged_planted_shared_row_is_caught():
+    """A ragged Q path that used sequence 0's positions for every sequence is rejected."""
+    inp = R.make_inputs(3, 2, 4, TINY, seed=33, dtype=torch.float64)
+    pos = torch.tensor([[1, 2], [300, 301], [7, 4000]])
+    good_qa, good_qr = _ragged_q(inp, pos)
+    bqa, bqr = brute_mla.q_rows(inp["x"].tolist(), inp["W_q_a"].tolist(),
+                                inp["q_norm_w"].tolist(), inp["W_q_b"].tolist(),
+                                inp["wkv_b"].tolist(), pos.tolist(), TINY.n_heads, TINY.nope,
+                                TINY.rope)
+    bqr = torch.tensor(bqr, dtype=torch.float64)
+    torch.testing.assert_close(good_qr, bqr, rtol=1e-10, atol=1e-11)
+    bad_qa, bad_qr = _ragged_q(inp, pos[:1].expand(3, -1))
+    assert (bad_qr - bqr).abs().max().item() > 1e-3
