@@ -116,6 +116,21 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims,
                   const void* pe_cache, const void* W_uv, double scale, int causal,
                   void* out, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/* mla_attention without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation).  No counterpart in the reference.  The scratch memory is a fixed device array
+ * of the library, MLA_ATTENTION_NOALLOC_MAX_BYTES (64 MiB) per GPU, held from the library's
+ * load until the process ends: it covers decode (Sq = 1) at B <= 128 for any Sk.
+ * A shape whose mla_attention_workspace_bytes() exceeds it is rejected with
+ * MLA_ERR_WORKSPACE.  The call allocates nothing and runs the same kernels as mla_attention
+ * (same results, bit for bit).  All calls on one GPU share the array: calls that overlap on
+ * one GPU (several streams or host threads) race and must be serialised by the caller. */
+#define MLA_ATTENTION_NOALLOC_MAX_BYTES ((size_t)64 << 20)
+int mla_attention_noalloc(mla_dtype_t dtype, const mla_dims_t* dims,
+                          const void* q_absorbed, const void* q_rope, const void* c_kv,
+                          const void* pe_cache, const void* W_uv, double scale, int causal,
+                          void* out, hipStream_t stream);
+
 /* Attention over a long key range without materialising the [B*Sq*H, Sk] score matrix:
  * keys are processed in chunks of `key_chunk` (a multiple of mla_score_tile(); 0 = choose
  * so the per-chunk score buffer stays <= 1 GiB).  Each chunk runs 3a -> 3b -> 3c into a

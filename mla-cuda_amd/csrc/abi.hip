@@ -12,6 +12,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/mla/mla.h"
@@ -653,6 +654,47 @@ int kv_append_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, con
     return ok();
 }
 
+// ------------------------------------------------------------------ allocation-free attention
+//
+// mla_attention_noalloc takes its workspace from `scratch`, a device array of this file,
+// instead of a caller buffer.  Each GPU holds its own copy of the array (at its own
+// address) from the library's load until the process ends.  In host code `scratch` is a
+// host-side stand-in for the symbol: its device address comes from hipGetSymbolAddress,
+// looked up once per device with that device current, and only that address is handed to
+// the kernels.  Every call on one GPU shares the array, so calls that overlap on one GPU
+// (two streams, two host threads) race; the kernels write every scratch byte they read
+// before reading it, so nothing needs clearing between calls.
+constexpr size_t kScratchBytes = MLA_ATTENTION_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch address on the device that `stream` belongs to (the current device for the
+// null stream).
+int scratch_for_stream(hipStream_t stream, void** out) {
+    int cur = 0, dev = 0;
+    MLA_TRY_HIP(hipGetDevice(&cur), "hipGetDevice");
+    dev = cur;
+    if (stream) MLA_TRY_HIP(hipStreamGetDevice(stream, &dev), "hipStreamGetDevice");
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(MLA_ERR_UNSUPPORTED, "device %d is beyond the %d devices the scratch table "
+                    "covers", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        if (dev != cur) MLA_TRY_HIP(hipSetDevice(dev), "hipSetDevice");
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) MLA_TRY_HIP(hipSetDevice(cur), "hipSetDevice (restore)");
+        if (e != hipSuccess) return hip_fail(e, "scratch symbol lookup");
+        if (!p) return fail(MLA_ERR_HIP, "scratch symbol lookup returned NULL");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MLA_OK;
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -933,6 +975,31 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
     return ok();
+}
+
+int mla_attention_noalloc(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                          const void* q_rope, const void* c_kv, const void* pe_cache,
+                          const void* W_uv, double scale, int causal, void* out,
+                          hipStream_t stream) {
+    MLA_CHECK(check_dtype(dtype));
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const size_t need = attn_layout(dtype, dims).total;
+    if (need > kScratchBytes)
+        return fail(MLA_ERR_WORKSPACE,
+                    "mla_attention_noalloc: this shape needs %zu bytes of scratch, more than "
+                    "the %zu bytes the library holds per GPU; use mla_attention with a "
+                    "caller workspace", need, kScratchBytes);
+    void* ws = nullptr;
+    MLA_CHECK(scratch_for_stream(stream, &ws));
+    return mla_attention(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache, W_uv, scale, causal,
+                         out, ws, kScratchBytes, stream);
 }
 
 size_t mla_attention_streaming_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,

@@ -433,3 +433,30 @@ def test_work_list_validation_and_size(lib):
     assert lib.mla_attention_work_list_ints(F32, ctypes.byref(d)) == 0
     st = lib.mla_attention_work_list(F32, ctypes.byref(d), P16, P16, n, None)
     assert st == MLA_ERR_INVALID_ARGUMENT and "batch" in _err(lib)
+
+
+def test_noalloc_attention_validation(lib):
+    """The allocation-free attention validates like mla_attention and rejects, before any HIP
+    call, a shape whose workspace exceeds the library's fixed scratch (64 MiB per GPU)."""
+    args = [P16] * 5
+    limit = 64 << 20
+    for B, Sq, Sk in [(128, 1, 4989), (1, 1, 65536), (64, 1, 4989), (8, 1, 4989)]:
+        d = dsv3(B, Sq, Sk)
+        for dt in (F32, BF16):
+            assert lib.mla_attention_workspace_bytes(dt, ctypes.byref(d), 0) <= limit
+    d = dsv3(4, 128, 32768)           # chunked prefill: 128 MiB of workspace
+    assert lib.mla_attention_workspace_bytes(F32, ctypes.byref(d), 1) > limit
+    st = lib.mla_attention_noalloc(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 1, P16,
+                                   None)
+    assert st == MLA_ERR_WORKSPACE and "scratch" in _err(lib)
+    d = dsv3(2, 3, 2)
+    st = lib.mla_attention_noalloc(F32, ctypes.byref(d), *args, ctypes.c_double(13.85), 1, P16,
+                                   None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "sk >= sq" in _err(lib)
+    d = dsv3(2, 1, 100)
+    st = lib.mla_attention_noalloc(F32, ctypes.byref(d), P16, P16, None, P16, P16,
+                                   ctypes.c_double(13.85), 0, P16, None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "c_kv" in _err(lib)
+    st = lib.mla_attention_noalloc(F32, ctypes.byref(d), *args, ctypes.c_double(0.0), 0, P16,
+                                   None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "scale" in _err(lib)
