@@ -8,7 +8,9 @@ One "step" is one MLA layer, steps 2a1 -> 3d, through the drop-in surface
 in HBM.  The default workload is the headline decode shape: B=128, Sq=1, Sk=4989, fp32,
 DeepSeek-V3 dims.  Output: ONE JSON line on stdout.
 
-Timed region: W untimed warm-up layers, then exactly K layers bracketed by
+Timed region: --settle seconds (default 2) of untimed layers, so the GPU clock has
+reached the level it holds under sustained load, then W untimed warm-up layers, then
+exactly K layers bracketed by
 torch.cuda.synchronize() on both sides, each layer between its own pair of HIP events on
 the current stream and preceded (outside the pair) by a 512 MB device read that evicts
 the MALL and L2s (leaving clean lines); `value` is the mean per-layer time (median and a
@@ -16,6 +18,10 @@ back-to-back figure beside it).  A second, separately timed pass runs the same k
 between consecutive steps; it gives each step's average launch duration, from which the
 per-step GFLOP/s, GB/s, MFMA % and HBM % (algorithmic work, formulas below) and the
 `roofline` object of the dominant kernel are computed.
+
+With the default fp32 cfg2 workload the line also carries `bf16_cfg4`: the bf16 decode
+(B=128, Sk=4989, bf16 storage) layer time and its fused attention's roofline, measured
+the same way.
 
 cpu_baseline: the CPU oracle (oracle/mla_ref.py, the reference's PyTorch formulation
 restated) timed on this machine's host cores on the same inputs -- the only place this
@@ -138,46 +144,11 @@ def cpu_baseline(inp, gpu_out, budget_s=30.0, causal=False):
             "os_cpu_count": os.cpu_count(), "cpu_model": model}, err, b_use
 
 
-def main():
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--dtype", default=None, choices=["f32", "bf16"],
-                    help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
-                    help="only run a plain device copy of BYTES, 3 times (calibrates the "
-                         "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
-    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
-                    help="JSON of HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a 1 GiB copy calibration")
-    args = ap.parse_args()
-
-    world = int(os.environ.get("WORLD_SIZE", "1"))
-    if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
-        sys.exit(2)
-
+def measure(args, ext, dev, neighbours=True):
+    """Time one configuration (args.config, args.dtype); returns the JSON record."""
     import torch
-    import mla_custom_cuda as ext
     import mla_inputs
 
-    if not torch.cuda.is_available():
-        print("bench.py needs a ROCm GPU", file=sys.stderr)
-        sys.exit(1)
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    if args.copy_probe:
-        src = torch.empty(args.copy_probe // 4, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_probe_bytes": args.copy_probe}), flush=True)
-        return
     dims = mla_inputs.DEEPSEEK_V3
     B, Sq, Sk, desc = CONFIGS[args.config]
     dname = args.dtype or ("bf16" if args.config == "cfg4" else "f32")
@@ -210,11 +181,22 @@ def main():
     # write-back then competes with the timed layer's own reads (measured: the B=1 q
     # up-projection's 151 MB weight stream takes 53 us after a write flush, 34 us after a
     # read), a cost a decode loop, whose big traffic is weight and cache reads, does not pay.
-    # The warm-up layers follow the same flush-then-layer pattern.  The clock takes ~15
-    # layers (~25 ms) of this loop to settle: with 3 warm-up layers the first timed layer
-    # ran 13% slower than the tenth, with 10 (pattern-matched) 4%, so the default warm-up is
-    # 20 layers and the mean is not carried by the ramp.
+    # The warm-up layers follow the same flush-then-layer pattern.
+    # The GPU's clock follows the load over seconds: after an idle spell the first few
+    # milliseconds run fast, the next ~100 ms dip 20-35% below the level the clock holds
+    # after ~2 s of sustained work (measured on the fused bf16 attention, back to back:
+    # ~215 us per call, then 290-337 us, then 215-225 us from about 2 s on).  A serving
+    # loop runs at that settled level, so --settle seconds (default 2) of the same
+    # flush-then-layer loop precede the warm-up layers.
     flush = torch.zeros(512 << 18, dtype=torch.float32, device=dev)   # 512 MB
+    t_settle = time.perf_counter()
+    n_settle = 0
+    while time.perf_counter() - t_settle < args.settle:
+        for _ in range(10):
+            flush_sum = flush.sum()   # noqa: F841
+            out = layer()
+        torch.cuda.synchronize()
+        n_settle += 10
     for _ in range(args.warmup):
         flush_sum = flush.sum()   # noqa: F841
         out = layer()
@@ -360,78 +342,30 @@ def main():
         traffic = None
     roofline.update({"traffic": traffic, "algorithmic_flop": fl, "algorithmic_bytes": by})
 
-    # ---- the path's neighbours, timed separately (not part of the layer's value):
-    # the wkv_b split (weight prep), the KV-cache append of this step's Sq tokens per
-    # sequence, and the output projection wo of the layer's output.
     nb = {}
-    e_b = 2 if dname == "bf16" else 4
-    H, R_, D_, V_, hid = dims.n_heads, dims.kv_rank, dims.rope, dims.v, dims.hidden
-    bq = B * Sq
-    gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
-    W_kv_a = (torch.randn(hid, R_ + D_, device=dev, generator=gen) / math.sqrt(hid)).to(dt)
-    kv_gain = (1.0 + 0.1 * torch.randn(R_, device=dev, generator=gen)).to(dt)
-    W_o = (torch.randn(H * V_, hid, device=dev, generator=gen) / math.sqrt(H * V_)).to(dt)
-    kv_pos = torch.arange(Sk - Sq, Sk, device=dev)
-    nb_calls = {
-        "split_wkv_b": (lambda: ext.split_wkv_b(g["wkv_b"], dims.nope),
-                        0, 2 * e_b * H * (dims.nope + V_) * R_),
-        "kv_append": (lambda: ext.kv_append(g["x"], W_kv_a, kv_gain, kv_pos, g["c_kv"],
-                                            g["pe_cache"], Sk - Sq, eps),
-                      2 * bq * hid * (R_ + D_),
-                      e_b * (bq * hid + hid * (R_ + D_) + R_ + bq * (R_ + D_)) + 8 * Sq),
-        "o_proj": (lambda: ext.o_proj(out, W_o), 2 * bq * H * V_ * hid,
-                   e_b * (bq * H * V_ + H * V_ * hid + bq * hid)),
-    }
-    for name, (fn, fl, by) in nb_calls.items():
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) / args.steps * 1e-3
-        mfma_bound = fl > 0 and fl / by > peak_mfma / PEAK_HBM
-        frac = (fl / t / peak_mfma) if mfma_bound else (by / t / PEAK_HBM)
-        nb[name] = {"us": round(t * 1e6, 2), "gflop": round(fl / 1e9, 3),
-                    "mbytes": round(by / 1e6, 2), "tflops": round(fl / t / 1e12, 2),
-                    "gbps": round(by / t / 1e9, 1), "bound": "mfma" if mfma_bound else "hbm",
-                    "frac": round(frac, 4)}
-    # attention alone over the same keys: dense, then through a shuffled pool of 64-key
-    # pages (full lengths: the dense work, plus the page-table indirection), then with
-    # ragged lengths U[1, Sk] (work is still that of the longest sequence: masked tiles
-    # are computed)
-    if not causal:
-        page = 64
-        mp = -(-Sk // page)
-        gp = torch.Generator().manual_seed(args.seed + 2)
-        perm = torch.randperm(B * mp, generator=gp)
-        pad = mp * page - Sk
-        def pool(t):
-            tp = torch.nn.functional.pad(t, (0, 0, 0, pad)).reshape(B * mp, page, t.shape[-1])
-            out_pool = torch.empty_like(tp)
-            out_pool[perm.to(dev)] = tp
-            return out_pool
-        ck_pool, pe_pool = pool(g["c_kv"]), pool(g["pe_cache"])
-        table = perm.reshape(B, mp).int().to(dev)
-        full = torch.full((B,), Sk, dtype=torch.int32, device=dev)
-        ragged = torch.randint(1, Sk + 1, (B,), generator=gp, dtype=torch.int32).to(dev)
-        qa_b, qr_b = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
-                                    g["positions"], dims.nope, dims.rope, eps)
-        fl_attn = work["3a"][0] + work["3c"][0] + work["3d"][0]
-        keys_ragged = int(ragged.sum().item())
-        att_calls = {
-            "attention_dense": (lambda: ext.mla_attention(qa_b, qr_b, g["c_kv"], g["pe_cache"],
-                                                          W_uv_d, scale), fl_attn),
-            "attention_paged": (lambda: ext.mla_attention_paged(
-                qa_b, qr_b, ck_pool, pe_pool, table, full, W_uv_d, scale), fl_attn),
-            "attention_paged_ragged": (lambda: ext.mla_attention_paged(
-                qa_b, qr_b, ck_pool, pe_pool, table, ragged, W_uv_d, scale),
-                fl_attn * keys_ragged / (B * Sk)),
+    if neighbours:
+        # ---- the path's neighbours, timed separately (not part of the layer's value):
+        # the wkv_b split (weight prep), the KV-cache append of this step's Sq tokens per
+        # sequence, and the output projection wo of the layer's output.
+        e_b = 2 if dname == "bf16" else 4
+        H, R_, D_, V_, hid = dims.n_heads, dims.kv_rank, dims.rope, dims.v, dims.hidden
+        bq = B * Sq
+        gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
+        W_kv_a = (torch.randn(hid, R_ + D_, device=dev, generator=gen) / math.sqrt(hid)).to(dt)
+        kv_gain = (1.0 + 0.1 * torch.randn(R_, device=dev, generator=gen)).to(dt)
+        W_o = (torch.randn(H * V_, hid, device=dev, generator=gen) / math.sqrt(H * V_)).to(dt)
+        kv_pos = torch.arange(Sk - Sq, Sk, device=dev)
+        nb_calls = {
+            "split_wkv_b": (lambda: ext.split_wkv_b(g["wkv_b"], dims.nope),
+                            0, 2 * e_b * H * (dims.nope + V_) * R_),
+            "kv_append": (lambda: ext.kv_append(g["x"], W_kv_a, kv_gain, kv_pos, g["c_kv"],
+                                                g["pe_cache"], Sk - Sq, eps),
+                          2 * bq * hid * (R_ + D_),
+                          e_b * (bq * hid + hid * (R_ + D_) + R_ + bq * (R_ + D_)) + 8 * Sq),
+            "o_proj": (lambda: ext.o_proj(out, W_o), 2 * bq * H * V_ * hid,
+                       e_b * (bq * H * V_ + H * V_ * hid + bq * hid)),
         }
-        for name, (fn, fl) in att_calls.items():
+        for name, (fn, fl, by) in nb_calls.items():
             for _ in range(3):
                 fn()
             torch.cuda.synchronize()
@@ -442,34 +376,83 @@ def main():
             e1.record()
             torch.cuda.synchronize()
             t = e0.elapsed_time(e1) / args.steps * 1e-3
+            mfma_bound = fl > 0 and fl / by > peak_mfma / PEAK_HBM
+            frac = (fl / t / peak_mfma) if mfma_bound else (by / t / PEAK_HBM)
             nb[name] = {"us": round(t * 1e6, 2), "gflop": round(fl / 1e9, 3),
-                        "tflops": round(fl / t / 1e12, 2), "bound": "mfma" if dname == "f32" else "hbm",
-                        "mfma_pct": round(100 * fl / t / peak_mfma, 1)}
-        nb["attention_paged_ragged"]["mean_keys"] = round(keys_ragged / B, 1)
-        del ck_pool, pe_pool
-    else:
-        # causal: the key-chunked entry point (bounded score workspace) beside the layer's
-        # fused pass
-        qa_b, qr_b = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
-                                    g["positions"], dims.nope, dims.rope, eps)
-        fl_attn = work["3a"][0] + work["3c"][0] + work["3d"][0]
-        fn = lambda: ext.mla_attention_streaming(qa_b, qr_b, g["c_kv"], g["pe_cache"],  # noqa: E731
-                                                 W_uv_d, scale, True)
-        fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(args.steps):
+                        "mbytes": round(by / 1e6, 2), "tflops": round(fl / t / 1e12, 2),
+                        "gbps": round(by / t / 1e9, 1), "bound": "mfma" if mfma_bound else "hbm",
+                        "frac": round(frac, 4)}
+        # attention alone over the same keys: dense, then through a shuffled pool of 64-key
+        # pages (full lengths: the dense work, plus the page-table indirection), then with
+        # ragged lengths U[1, Sk] (work is still that of the longest sequence: masked tiles
+        # are computed)
+        if not causal:
+            page = 64
+            mp = -(-Sk // page)
+            gp = torch.Generator().manual_seed(args.seed + 2)
+            perm = torch.randperm(B * mp, generator=gp)
+            pad = mp * page - Sk
+            def pool(t):
+                tp = torch.nn.functional.pad(t, (0, 0, 0, pad)).reshape(B * mp, page, t.shape[-1])
+                out_pool = torch.empty_like(tp)
+                out_pool[perm.to(dev)] = tp
+                return out_pool
+            ck_pool, pe_pool = pool(g["c_kv"]), pool(g["pe_cache"])
+            table = perm.reshape(B, mp).int().to(dev)
+            full = torch.full((B,), Sk, dtype=torch.int32, device=dev)
+            ragged = torch.randint(1, Sk + 1, (B,), generator=gp, dtype=torch.int32).to(dev)
+            qa_b, qr_b = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
+                                        g["positions"], dims.nope, dims.rope, eps)
+            fl_attn = work["3a"][0] + work["3c"][0] + work["3d"][0]
+            keys_ragged = int(ragged.sum().item())
+            att_calls = {
+                "attention_dense": (lambda: ext.mla_attention(qa_b, qr_b, g["c_kv"], g["pe_cache"],
+                                                              W_uv_d, scale), fl_attn),
+                "attention_paged": (lambda: ext.mla_attention_paged(
+                    qa_b, qr_b, ck_pool, pe_pool, table, full, W_uv_d, scale), fl_attn),
+                "attention_paged_ragged": (lambda: ext.mla_attention_paged(
+                    qa_b, qr_b, ck_pool, pe_pool, table, ragged, W_uv_d, scale),
+                    fl_attn * keys_ragged / (B * Sk)),
+            }
+            for name, (fn, fl) in att_calls.items():
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(args.steps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                t = e0.elapsed_time(e1) / args.steps * 1e-3
+                nb[name] = {"us": round(t * 1e6, 2), "gflop": round(fl / 1e9, 3),
+                            "tflops": round(fl / t / 1e12, 2), "bound": "mfma" if dname == "f32" else "hbm",
+                            "mfma_pct": round(100 * fl / t / peak_mfma, 1)}
+            nb["attention_paged_ragged"]["mean_keys"] = round(keys_ragged / B, 1)
+            del ck_pool, pe_pool
+        else:
+            # causal: the key-chunked entry point (bounded score workspace) beside the layer's
+            # fused pass
+            qa_b, qr_b = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
+                                        g["positions"], dims.nope, dims.rope, eps)
+            fl_attn = work["3a"][0] + work["3c"][0] + work["3d"][0]
+            fn = lambda: ext.mla_attention_streaming(qa_b, qr_b, g["c_kv"], g["pe_cache"],  # noqa: E731
+                                                     W_uv_d, scale, True)
             fn()
-        e1.record()
-        torch.cuda.synchronize()
-        t = e0.elapsed_time(e1) / args.steps * 1e-3
-        nb["attention_streaming_chunks"] = {
-            "us": round(t * 1e6, 2), "gflop": round(fl_attn / 1e9, 3),
-            "tflops": round(fl_attn / t / 1e12, 2), "bound": "mfma",
-            "mfma_pct": round(100 * fl_attn / t / peak_mfma, 1)}
-    print(f"[bench] neighbours: " + ", ".join(f"{k} {v['us']} µs" for k, v in nb.items()),
-          file=sys.stderr, flush=True)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(args.steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            t = e0.elapsed_time(e1) / args.steps * 1e-3
+            nb["attention_streaming_chunks"] = {
+                "us": round(t * 1e6, 2), "gflop": round(fl_attn / 1e9, 3),
+                "tflops": round(fl_attn / t / 1e12, 2), "bound": "mfma",
+                "mfma_pct": round(100 * fl_attn / t / peak_mfma, 1)}
+        print(f"[bench] neighbours: " + ", ".join(f"{k} {v['us']} µs" for k, v in nb.items()),
+              file=sys.stderr, flush=True)
 
     value_us = ms_per_step * 1e3
     rec = {
@@ -479,6 +462,8 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": args.settle,
+        "settle_layers": n_settle,
         "ms_per_step": round(ms_per_step, 4),
         "median_us_per_step": round(ms_median * 1e3, 2),
         "min_max_us_per_step": [round(min(layer_ms) * 1e3, 2), round(max(layer_ms) * 1e3, 2)],
@@ -514,6 +499,65 @@ def main():
     else:
         rec["cpu_baseline"] = None
 
+    return rec
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--settle", type=float, default=2.0, metavar="SECONDS",
+                    help="seconds of untimed flush-then-layer loop before the warm-up "
+                         "layers, so the clock has settled (see measure())")
+    ap.add_argument("--no-bf16-line", action="store_true",
+                    help="cfg2 only: skip the bf16 cfg4 figures added to its JSON line")
+    ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
+    ap.add_argument("--dtype", default=None, choices=["f32", "bf16"],
+                    help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES, 3 times (calibrates the "
+                         "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "traffic.json"),
+                    help="JSON of HBM bytes per launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a 1 GiB copy calibration")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              f"(asked for --gpus {args.gpus}, WORLD_SIZE={world}).", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import mla_custom_cuda as ext
+    import mla_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.empty(args.copy_probe // 4, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": args.copy_probe}), flush=True)
+        return
+    rec = measure(args, ext, dev)
+    if args.config == "cfg2" and (args.dtype or "f32") == "f32" and not args.no_bf16_line:
+        # the bf16 decode (cfg4) beside the headline fp32 one: its layer time and the fused
+        # attention's roofline, measured the same way (neighbours and CPU baseline left out)
+        a4 = argparse.Namespace(**vars(args))
+        a4.config, a4.dtype, a4.no_cpu_baseline = "cfg4", "bf16", True
+        r4 = measure(a4, ext, dev, neighbours=False)
+        rec["bf16_cfg4"] = {k: r4[k] for k in ("value", "unit", "median_us_per_step",
+                                               "back_to_back_us_per_step", "dtype", "config",
+                                               "roofline", "fused_path_sum_us")}
+        rec["bf16_cfg4"]["steps_us_3abc"] = r4["steps_us"]["3abc"]
     print(json.dumps(rec), flush=True)
 
 

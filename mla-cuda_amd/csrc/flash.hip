@@ -1,5 +1,5 @@
-// 3a + 3b + 3c fused: one pass over the latent cache per key split, for bf16 storage
-// (flash_kernel) and fp32 storage (flash32_kernel, further below).
+// 3a + 3b + 3c fused: one pass over the latent cache per key split, for 16-bit storage
+// (flash16_kernel) and fp32 storage (flash32_kernel, further below).
 //
 // The per-step path materialises fp32 scores (3a), reduces per-tile softmax partials
 // (3b) and streams c_kv a second time for ctx (3c).  With bf16 storage that path is
@@ -7,40 +7,26 @@
 // only 0.74 GB is the cache; in fp32 it is MFMA-bound and the extra passes cost the
 // score epilogue, the combine and a second launch tail.  These kernels read every key row
 // once, keep the softmax state in registers and write only the unnormalised ctx, its row
-// sums and row maxima.
+// sums and (for a split) row maxima.
 // The arithmetic is the reference's (mla_kernels.cu:971-1032, 1058-1079, 1247-1254):
 // s = q_absorbed.c_kv + q_rope.pe, softmax over s/scale, ctx = sum_k p_k c_kv[k]; only the
-// order of operations differs (an online softmax instead of per-tile partials).
+// order of operations differs (a streaming softmax instead of per-tile partials).
 //
 // Workgroup: 4 waves over 64 rows (queries x heads) of one batch and one contiguous key
-// range (a split).  Wave w owns rows 16w .. 16w+15 and all 512 output columns, with the
-// gfx950 16x16x32 bf16 MFMA; per 32-key block:
-//   S^T[32 keys x 16 rows] = K_blk . Q^T   (2 key halves x 18 K steps; the wave's Q^T,
-//                                          576 deep, lives in 72 VGPRs for the whole kernel)
-//   online softmax per row: lane l holds 8 of the block's keys for row l%16; the other
-//                           24 sit in lanes l%16 + 16g (v_permlane16/32_swap reductions)
-//   O^T[512 cols x 16 rows] += V_blk^T . P^T (P^T is the S^T accumulator rounded to bf16,
-//                                          used in place as the B operand; O^T is 128
-//                                          accumulation registers)
-// No data moves between waves; one barrier per block guards the LDS ring.  Block j-1's
-// P.V is issued in block j's step, interleaved with block j's softmax.
-// V_blk^T fragments come from the same key-major LDS tile as K_blk through gfx950's
-// transposing ds_read_b64_tr_b16, so c_kv is staged once per workgroup, by direct
-// global->LDS loads (buffer_load_dwordx4 ... lds) into a 4-block ring: two blocks are in
-// flight while two are in use, with no VGPRs spent on staging.  The two 64-row tiles of a
-// batch are placed on one XCD, so the second read of every key block hits its L2.
+// range (a split).  Key blocks reach LDS through direct global->LDS loads
+// (buffer_load_dwordx4 ... lds) into a ring of four blocks -- two in flight while two are
+// in use -- with no VGPRs spent on staging; one barrier per block guards the ring.  The
+// two 64-row tiles of a batch are placed on one XCD, so the second read of every key
+// block hits its L2.  V^T fragments come from the same key-major LDS tile as K, through
+// gfx950's transposing ds_read_b64_tr_b16, so c_kv is staged once per workgroup.
 //
-// LDS tile of a block (36 KB): 32 latent rows of 1 KB, then 32 rope rows of 128 B.  The
-// 16-byte chunk c of latent key k sits at c ^ swz(k & 15) within its 256-byte group
-// (swz: rotate left by one of four bits); chunk c of rope key k at c ^ ((k >> 1) & 7).
-// The K slots of the MFMAs are assigned so that the four lane groups of a K fragment read
-// four different 256-byte quarters of the key rows.  Both measured free of bank conflicts
-// (SQ_LDS_BANK_CONFLICT = 0) for the fragment reads of this kernel.
-//
-// Softmax: log2 domain, t = s * log2(e)/scale.  The running maximum m is only raised when
-// a block's maximum exceeds it by more than kSlack (= 8, so p <= 256): the rescale of the
-// accumulators is then rare, and the result is the same softmax, since every term and the
-// row sum share one m.  Rows without a visible key keep m = -inf and l = 0.
+// Softmax (log2 domain, t = s * log2(e)/scale): each row keeps a fixed reference, the
+// maximum of its first visible block.  Every term is 2^(t - reference) and the output
+// accumulators are never rescaled; a row whose maximum passes the reference by a wide
+// margin (2^64 in bf16, 2^40 in fp32: far from any overflow) raises it, and the pass
+// over the split is repeated from its first key with the raised references.  The result is
+// the same softmax, since every term and the row sum share one reference.  Rows without a
+// visible key keep the reference -inf and the row sum 0.
 
 #include "kernels.h"
 #include "mma.h"
@@ -57,22 +43,14 @@ namespace {
 
 constexpr int kFR = 512, kFD = 64;                  // latent and rope widths
 constexpr int kFKeys = 32;                          // keys per block
-constexpr int kFRows = 64;                          // rows per workgroup (4 waves x 16)
+constexpr int kFRows = 64;                          // rows per workgroup
 constexpr int kFThreads = 256;
 constexpr int kQSteps = (kFR + kFD) / 32;           // 18 MFMA K steps of 32
 constexpr int kRSteps = kFR / 32;                   // 16 of them over the latent part
-constexpr int kColBlocks = kFR / 16;                // 32 blocks of 16 columns
 constexpr int kLatBytes = kFR * 2;                  // one key's latent row
 constexpr int kPeBytes = kFD * 2;                   // one key's rope row
-constexpr int kPeOff = kFKeys * kLatBytes;          // rope rows follow the latent rows
-constexpr int kStageBytes = kPeOff + kFKeys * kPeBytes;
-constexpr int kLoadsPerBlock = 9;                   // per wave: 8 latent rows, 8 rope rows
-constexpr float kSlack = 8.f;                       // log2 units
-constexpr int kSgValu = 0x002;                      // sched_group_barrier class: VALU
 
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_t;
-typedef __attribute__((address_space(3))) v4bf lds_v4bf;
 
 struct FlashArgs {
     const uint16_t* qa; const uint16_t* qr;     // [B*Sq*H, R], [B*Sq*H, D]
@@ -155,11 +133,9 @@ __device__ __forceinline__ int64_t flash_key_row(const FlashArgs& a, int b, int 
     return (int64_t)page * a.page_size + k % a.page_size;
 }
 
-// Chunk permutations (see the header): latent rows (1 KB) keep chunk c of key k at
-// c ^ swz(k & 15) within its 256-byte group, swz = rotate left by one bit of four; rope
-// rows (128 B) keep chunk c of key k at c ^ ((k >> 1) & 7).
+// Chunk permutation of the fp32 pass's LDS rows: 16-byte chunk c of key k sits at
+// c ^ swz(k & 15) within its 256-byte group, swz = rotate left by one bit of four.
 __device__ __forceinline__ int swz(int k) { return ((k << 1) | (k >> 3)) & 15; }
-__device__ __forceinline__ int swz_pe(int k) { return (k >> 1) & 7; }
 
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -181,13 +157,6 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor words (base, 32-bit data format, range kRsrcRange), as make_rsrc.
-__device__ __forceinline__ v4i rsrc_words(const void* base) {
-    const uint64_t p = reinterpret_cast<uint64_t>(base);
-    return v4i{(int32_t)(uint32_t)p, (int32_t)((uint32_t)(p >> 32) & 0xffff), kRsrcRange,
-               0x00020000};
-}
 
 // 16 bytes per lane from buffer offset soff + voff into LDS at lds + 16*lane (gfx950
 // buffer_load_dwordx4 ... lds).  Written as asm so that the compiler neither tracks it
@@ -220,13 +189,6 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)reinterpret_cast<uintptr_t>((const lds_t*)p);
 }
 
-// 16x16x32 bf16 MFMA: lane l supplies A[l%16][8(l/16) .. +7] and B[8(l/16) .. +7][l%16];
-// accumulator element i of lane l is D[4(l/16) + i][l%16].
-__device__ __forceinline__ v4f mfma16(v4u a, v4u b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(v8bf, a),
-                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
-}
-
 // Max / sum over the 4 lanes l%16 + 16g (g = 0..3) that hold one row: v_permlane16_swap
 // pairs the rows of 16 lanes (0,1) and (2,3), v_permlane32_swap the two halves; given the
 // same value twice each returns the pair's two values in every lane, combined in one order.
@@ -240,286 +202,423 @@ __device__ __forceinline__ float row4_reduce(float v, Op op) {
     return op(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
+// Descriptor words of `bytes` bytes at base + off (off in bytes); wave-uniform arguments
+// (readfirstlane keeps the words in scalar registers, as the load instruction needs).
+__device__ __forceinline__ v4i rsrc_span(uint64_t base, uint32_t off, uint32_t bytes) {
+    const uint64_t p = base + off;
+    return v4i{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)p),
+               __builtin_amdgcn_readfirstlane((int32_t)((uint32_t)(p >> 32) & 0xffff)),
+               __builtin_amdgcn_readfirstlane((int32_t)bytes), 0x00020000};
+}
+
+// ------------------------------------------------------------------ 16-bit: key-split waves
+// The 16-bit pass on 32-row waves that split the keys.  A workgroup's 64 rows are two
+// 32-row tiles; wave w = 2 rt + kh owns row tile rt and keys 16kh .. 16kh+15 of every
+// 32-key block, at the full 576 depths, so the waves never exchange scores and none
+// repeats another's softmax (32 rows per wave is the most the register file holds: the
+// output accumulators take all 256 AGPRs, Q^T 144 VGPRs):
+//   S^T[16 keys x 32 rows]: two 16x16x32 MFMAs per K fragment (one per 16-row half of the
+//     tile), 18 K steps; the wave's Q^T (both halves, 576 deep) lives in 144 VGPRs.  K step
+//     s < 16 is latent depth chunk 16g + s for lane group g = l/16 (the groups read four
+//     256-byte quarters of a key row), step 16 + r rope chunk 4r + g.  Accumulator element
+//     i of lane l is key 4g + i of row (16 half) + l%16.
+//   softmax per lane: 8 scores, against a fixed per-row reference (first visible block's
+//     maximum; a row that passes it by k2Headroom raises it and the pass is repeated, as in
+//     flash32_kernel), so the 256 O accumulators are never rescaled
+//   O^T[512 cols x 32 rows] += V^T[512 x 16 keys] . P^T[16 keys x 32 rows]: sixteen
+//     32x32x16 MFMAs.  P^T is the score accumulator rounded to 16 bits after one
+//     v_permlane16_swap per register pair, which moves lane l's 4 keys of one row half next
+//     to lane l^16's 4 keys of the same row: lane l then holds keys 8(l/32) .. +7 of row l%32,
+//     the MFMA's B layout.  V^T comes from two transposing 64-bit reads per MFMA.
+// The two key halves of a row tile merge once, through LDS, after the last block (the
+// standard rescale by 2^(m_half - max)).  Per wave and 32-key block: 36 + 16 MFMAs (1088
+// MFMA cycles), 18 KB of K reads and 16 KB of V reads.
+// Measured on one wave per SIMD: a 16x16x32 MFMA issues every 16-17 cycles and a 32x32x16
+// every 32, dependent or not; a simple VALU instruction takes ~5 cycles and v_exp_f32 ~14,
+// and VALU work issued between MFMAs runs under them.  So the step keeps the MFMA stream
+// fed around the barrier (the previous block's P.V goes first), keeps the softmax's rare
+// cases behind uniform branches and interleaves its common VALU work with P.V MFMAs, and
+// spreads the block's nine cache loads over the step.
+// LDS: the latent rows of the NS stages (32 x 1 KB each), then their rope rows; chunk c of
+// latent key k sits at (c & ~15) | ((c & 15) ^ sw16(k & 15)), chunk c of rope key k at
+// c ^ ((k >> 1) & 7).  gfx950 serves a 128-bit LDS read in 16-lane cycles made of the lane
+// octets (56-63, 0-7), (8-15, 16-23), (24-31, 32-39), (40-47, 48-55), and a 64-bit read
+// (also the transposing one) in 32-lane halves; a cycle is conflict-free when its lanes
+// touch distinct 16-byte (8-byte) slots of 256 bytes.  Under that rule (measured with a
+// probe and the SQ_LDS_BANK_CONFLICT counter) every K, V and staging access is conflict-free,
+// and each is one per-lane base XOR a constant plus an immediate offset.
+constexpr int k2Keys = 32;
+constexpr int k2LatStage = k2Keys * kLatBytes;            // 32 KB
+constexpr int k2PeStage = k2Keys * kPeBytes;              // 4 KB
+constexpr int k2Loads = 9;                                // cache loads per wave and block
+constexpr float k2Headroom = 64.f;                        // log2 units above a row's reference
+constexpr int k2MaxPasses = 8;
+
+__device__ __forceinline__ int sw16(int k) { return ((k & 3) << 2) | ((k >> 2) & 3); }
+
+__device__ __forceinline__ v16f mfma32bf(v4u a, v4u b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a),
+                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+}
+
+// The score MFMAs of flash16_kernel (16x16x32 bf16: lane l supplies A[l%16][8(l/16) .. +7]
+// and B[8(l/16) .. +7][l%16]; accumulator element i of lane l is D[4(l/16) + i][l%16]),
+// written as inline asm so that their accumulators stay in
+// VGPRs (the 256 AGPRs hold the output accumulators; left to itself, the register allocator
+// puts these in AGPRs and moves output blocks back and forth every block).  The hazards the
+// compiler would otherwise resolve for them: two independent chains alternate, so an MFMA
+// never reads the accumulator the previous one wrote; the K fragments come from LDS reads
+// the compiler waits for; and after the last MFMA of a block 16 wait states pass before any
+// VALU reads an accumulator (the 16x16x32 bf16 MFMA needs at most 11).
+__device__ __forceinline__ void mfma16_v_first(v4u a, v4u b, v4f& c) {
+    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma16_v(v4u a, v4u b, v4f& c) {
+    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+}
+__device__ __forceinline__ void mfma16_v_last(v4u a, v4u b, v4f& c) {
+    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
+}
+
 template <int NS>
-__global__ void __launch_bounds__(kFThreads, 1) flash_kernel(FlashArgs a) {
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStageBytes];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int l16 = lane & 15, g = lane >> 4;
+__global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
+    static_assert(NS == 4, "stage offsets: stages 2-3 are stages 0-1 XOR 64 KB");
+    constexpr int kPeBase = NS * k2LatStage;                    // 128 KB
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kPeBase + NS * k2PeStage];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // a scalar from here on
+    const int rt = wave >> 1, kh = wave & 1;
+    const int l16 = lane & 15, g = lane >> 4, l32 = lane & 31, hw = lane >> 5;
     const FlashWork work = flash_work(a);
     if (work.skip) return;   // past the end of a work list: the whole workgroup leaves
 
-    const int rt = work.rt;
     const int b = work.b;
     const int rows_b = a.Sq * a.H;
-    const int r0 = rt * kFRows;
-    const int row = r0 + 16 * wave + l16;            // this lane's row within the batch
+    const int r0 = work.rt * kFRows;
+    const int rbase = r0 + 32 * rt;                  // first row of this wave's tile
+    const int rowS0 = rbase + l16, rowS1 = rbase + 16 + l16;   // score-layout rows
+    const int rowO = rbase + l32;                    // output-layout row
 
-    // keys of this split; the causal rule (query s sees keys <= Sk_b - Sq + s) also trims
-    // the range to the tile's last query
     const int skb = flash_batch_keys(a, b);
     const int k_lo = work.k_lo;
     int k_hi = min(skb, k_lo + work.k_len);
-    int lim = k_hi - 1;                              // last visible key of this lane's row
+    int lim0 = k_hi - 1, lim1 = k_hi - 1;            // last visible key of each score row
     if (a.causal) {
-        lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
+        lim0 = min(lim0, skb - a.Sq + min(rowS0, rows_b - 1) / a.H);
+        lim1 = min(lim1, skb - a.Sq + min(rowS1, rows_b - 1) / a.H);
         k_hi = min(k_hi, skb - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
     }
-    const int nb = k_hi > k_lo ? (k_hi - k_lo + kFKeys - 1) / kFKeys : 0;
-    // the smallest row limit of the wave: its first row's (rows ascend with the lanes)
-    const int lim_wave = __builtin_amdgcn_readfirstlane(lim);
+    const int nb = k_hi > k_lo ? (k_hi - k_lo + k2Keys - 1) / k2Keys : 0;
+    // the wave's smallest row limit: its first row's (lane 0, first half)
+    const int lim_wave = __builtin_amdgcn_readfirstlane(lim0);
 
-    // ---- Q^T fragments: lane l holds row l%16's K slots of group g for every step s:
-    // latent step s < 16 is depth 8(16g + s) .. +7 (the groups read four separate 256-byte
-    // quarters of a key row, which keeps the K fragment reads free of bank conflicts),
-    // rope step 16 + q is rope depth 8(4q + g) .. +7
+    // ---- Q^T of both row halves: latent step s is depth chunk 16g + s, rope step 16 + r
+    // rope chunk 4r + g
     const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qa + (int64_t)b * rows_b * kFR);
     const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.qr + (int64_t)b * rows_b * kFD);
-    const uint32_t qmask = oob_mask(row, rows_b);
-    v4u qf[kQSteps];
+    v4u qf[2][kQSteps];
     #pragma unroll
-    for (int s = 0; s < kQSteps; ++s)
-        qf[s] = s < kRSteps
-                    ? load16(rq, ((uint32_t)row * kLatBytes + 256u * g + 16u * s) | qmask)
-                    : load16(rr, ((uint32_t)row * kPeBytes + 64u * (s - kRSteps) + 16u * g) | qmask);
+    for (int t = 0; t < 2; ++t) {
+        const int row = t ? rowS1 : rowS0;
+        const uint32_t qmask = oob_mask(row, rows_b);
+        #pragma unroll
+        for (int s = 0; s < kQSteps; ++s)
+            qf[t][s] = s < kRSteps
+                           ? load16(rq, ((uint32_t)row * kLatBytes + 256u * g + 16u * s) | qmask)
+                           : load16(rr, ((uint32_t)row * kPeBytes + 64u * (s - kRSteps) + 16u * g) | qmask);
+    }
     // Q is in registers before the first key block is requested: the cache loads are not
     // seen by the compiler's wait-count tracking, which would otherwise keep waiting on Q
     // (and so on every cache load issued since) inside the key loop
     wait_vm<0>();
 
-    // ---- direct global->LDS staging of key blocks: wave w loads keys 8w .. 8w+7
+    // ---- direct global->LDS staging: wave w loads keys 8w .. 8w+7 of a block; lane i
+    // fills physical chunk i of a latent row, i.e. loads logical chunk i ^ sw16(key & 15)
     const uint32_t lds0 = lds_addr(smem);
-    // rope rows of keys 8w .. 8w+7: lane i fills chunk i%8 of key 8w + i/8
     const uint32_t pe_lane = (uint32_t)(lane >> 3) * kPeBytes +
-                             16u * ((lane & 7) ^ swz_pe(8 * wave + (lane >> 3)));
-    // latent row of key 8w + q: lane i fills LDS chunk i, i.e. loads logical chunk
-    // i ^ swz(key & 15) of its 256-byte group (blocks start at multiples of 32 keys)
-    uint32_t lat_lane[8];
-    #pragma unroll
-    for (int q = 0; q < 8; ++q)
-        lat_lane[q] = 16u * ((lane & ~15) | ((lane ^ swz((8 * wave + q) & 15)) & 15));
-
-    auto issue = [&](int j, int stage) __attribute__((always_inline)) {
-        const int kb = k_lo + kFKeys * j + 8 * wave;     // this wave's first key
-        // the LDS base goes to M0: wave-uniform, made scalar explicitly
-        const uint32_t st = __builtin_amdgcn_readfirstlane(lds0 + stage * kStageBytes + 8 * wave * kLatBytes);
-        const uint32_t st_pe = __builtin_amdgcn_readfirstlane(lds0 + stage * kStageBytes + kPeOff + 8 * wave * kPeBytes);
-        const uint32_t kb_s = __builtin_amdgcn_readfirstlane(kb);
-        // descriptors at the cache row of the wave's first key (its 8 keys share a page)
-        const int64_t row0 = flash_key_row(a, b, (int)kb_s, __builtin_amdgcn_readfirstlane(k_hi));
-        const v4i rk = rsrc_words(a.ckv + row0 * kFR);
-        const v4i rp = rsrc_words(a.pe + row0 * kFD);
-        #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            const uint32_t voff = (int)kb_s + q < k_hi ? lat_lane[q] : kOob;
-            dma16(rk, st + q * kLatBytes, voff, q * kLatBytes);
-        }
-        const uint32_t voff = kb + (lane >> 3) < k_hi ? pe_lane : kOob;
-        dma16(rp, st_pe, voff, 0);
+                             16u * ((lane & 7) ^ ((8 * wave + (lane >> 3)) >> 1 & 7));
+    const uint32_t lane16 = 16u * lane;
+    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
+    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe);
+    const int k_hi_s = __builtin_amdgcn_readfirstlane(k_hi);
+    // The descriptors cover exactly the wave's keys in range (its 8 keys are consecutive cache
+    // rows of one page), so keys past the end read as zeros with no per-lane work; a block
+    // past the last one loads nothing but zeros, so every step issues its 9 loads and every
+    // wait counts the same 9 per block.  The 9 loads of a block go out one at a time between
+    // the MFMAs of a step: issued back to back by all four waves they queue in the CU's
+    // address unit and stall the MFMA stream behind them.
+    struct Loads { v4i rk, rp; uint32_t st, st_pe; };
+    auto loads_of = [&](int j) __attribute__((always_inline)) {
+        const int stage = j % NS;
+        const int kb = __builtin_amdgcn_readfirstlane(k_lo + k2Keys * j + 8 * wave);
+        const uint32_t left = (uint32_t)max(0, min(8, k_hi_s - kb));
+        Loads d;
+        d.st = __builtin_amdgcn_readfirstlane(lds0 + stage * k2LatStage + 8 * wave * kLatBytes);
+        d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + kPeBase + stage * k2PeStage + 8 * wave * kPeBytes);
+        const uint64_t row0 = (uint64_t)flash_key_row(a, b, kb, k_hi_s);
+        d.rk = rsrc_span(ck_base + row0 * kLatBytes, 0, left * kLatBytes);
+        d.rp = rsrc_span(pe_base + row0 * kPeBytes, 0, left * kPeBytes);
+        return d;
+    };
+    auto issue_one = [&](const Loads& d, int q) __attribute__((always_inline)) {
+        if (q < 8) dma16(d.rk, d.st + q * kLatBytes, lane16 ^ (16u * sw16((8 * wave + q) & 15)), q * kLatBytes);
+        else dma16(d.rp, d.st_pe, pe_lane, 0);
     };
 
-    // ---- per-lane LDS offsets of the fragments
-    // K fragment (A operand) of key half kh (keys 16kh + l%16), latent step s: logical chunk
-    // 16g + s of the latent row (held at 16g + (s ^ swz(key & 15))); rope step 16 + q:
-    // chunk 4q + g of the rope row
-    const int fk = swz(l16);   // (16kh + l16) & 15 == l16
-    uint32_t k_off[16];
-    #pragma unroll
-    for (int s = 0; s < 16; ++s) k_off[s] = l16 * kLatBytes + 256u * g + 16u * (s ^ fk);
-    uint32_t p_off[2];
-    #pragma unroll
-    for (int q = 0; q < 2; ++q)
-        p_off[q] = kPeOff + l16 * kPeBytes + 16u * ((4 * q + g) ^ swz_pe(l16));
-    // V^T fragment (A operand) of 16-col block mb, half r2: lane (g, j = l%16, q = j/4,
-    // c = j%4) addresses key 16r2 + 4g + q, cols 16mb + 4c .. +3, i.e. logical chunk
-    // 2mb + c/2 = 16(mb/8) + (2(mb%8) + c/2), half c%2
-    uint32_t v_off[8];   // [mb % 8]
+    // ---- per-lane LDS bases (byte offsets from smem); each read is base XOR a constant
+    // plus an immediate, re-derived per step so no offset is held across the loop
+    const int kk = 16 * kh + l16;                    // this lane's key in a block (K reads)
+    uint32_t kb0 = kk * kLatBytes + 256u * g + 16u * sw16(l16);
+    uint32_t pb0 = kPeBase + kk * kPeBytes + 16u * (g ^ ((kk >> 1) & 7));
+    uint32_t vb0;
     {
-        const int j = lane & 15, q = j >> 2, c = j & 3;
-        const int kx = 4 * g + q, fv = swz(kx);   // (16r2 + kx) & 15 == kx
-        #pragma unroll
-        for (int m8 = 0; m8 < 8; ++m8) {
-            const int chunk = 2 * m8 + (c >> 1);
-            v_off[m8] = kx * kLatBytes + 16u * (chunk ^ fv) + 8u * (c & 1);
-        }
+        const int ch = g & 1, q = l16 >> 2, r = l16 & 3;
+        vb0 = (16 * kh + 8 * hw + q) * kLatBytes + 16u * ((q << 2) | ((2 * ch + (r >> 1)) ^ (2 * hw))) +
+              8u * (r & 1);
     }
-
-    v4f O[kColBlocks];
-    #pragma unroll
-    for (int i = 0; i < kColBlocks; ++i) O[i] = v4f{};
-    float m_run = -INFINITY, l_run = 0.f;
-    uint32_t pk[4] = {0, 0, 0, 0};   // P^T of the previous block, bf16 pairs
-
-    // V^T fragments of column blocks [c0, c0 + N) of the block in stage ST (K slots: keys
-    // 4g + 0..3, then 16 + 4g + 0..3)
-    auto read_v = [&](auto st_tag, int c0, auto n_tag, v4u* va) __attribute__((always_inline)) {
-        constexpr int ST = decltype(st_tag)::value;
-        constexpr int N = decltype(n_tag)::value;
-        const uint8_t* st = smem + ST * kStageBytes;
-        #pragma unroll
-        for (int i = 0; i < N; ++i) {
-            const int mb = c0 + i;
-            const uint32_t off = v_off[mb & 7] + 256u * (mb >> 3);
-            const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_v4bf*)(st + off));
-            const v4bf hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                (lds_v4bf*)(st + off + 16 * kLatBytes));
-            va[i] = __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        }
+    // stage st's copy of a latent base is base ^ 64 KB (st >> 1) + 32 KB (st & 1), of a rope
+    // base base + 4 KB st; the bases stay below 32 KB (rope: inside their 4 KB), so no carry
+    // reaches the bits the reads XOR in
+    auto lat_base = [&](uint32_t base, int st) __attribute__((always_inline)) {
+        return (base ^ (65536u * (uint32_t)(st >> 1))) + (uint32_t)(st & 1) * k2LatStage;
     };
-    using Half = std::integral_constant<int, kColBlocks / 2>;
+    auto k_read = [&](uint32_t kbs, uint32_t pbs, int s) __attribute__((always_inline)) {
+        const uint32_t off = s < kRSteps ? (kbs ^ (16u * s)) : (pbs ^ (64u * (s - kRSteps)));
+        return *reinterpret_cast<const v4u*>(smem + off);
+    };
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
+    // V^T of column block cb (columns 32cb ..), keys 8(l/32) .. +7 of the wave's half
+    auto v_read = [&](uint32_t vbs, int cb) __attribute__((always_inline)) {
+        const uint32_t o = 256u * (cb >> 2);
+        const uint32_t c = 64u * (cb & 3);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + ((vbs ^ c) + o)));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(smem + ((vbs ^ (c | 16u)) + o + 4 * kLatBytes)));
+        return __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
 
-    // One 32-key block j held in ring stage ST: its scores, then block j-1's P.V with
-    // block j's softmax spread between the MFMAs.
-    auto step = [&](int j, auto st_tag, auto has_prev) __attribute__((always_inline)) {
-        constexpr int ST = decltype(st_tag)::value;
-        constexpr bool PREV = decltype(has_prev)::value;
-        constexpr int SP = (ST + NS - 1) % NS;
-        const int ahead = min(nb - 1, j + NS - 3) - j;   // blocks issued after block j
-        if constexpr (NS >= 4) {
-            if (ahead >= 2) wait_vm<2 * kLoadsPerBlock>();
-            else if (ahead == 1) wait_vm<kLoadsPerBlock>();
-            else wait_vm<0>();
-        } else {
-            if (ahead >= 1) wait_vm<kLoadsPerBlock>();
-            else wait_vm<0>();
-        }
-        lds_barrier();   // block j is in LDS for every wave; every wave is past block j-2's P.V
-        if (j + NS - 2 < nb) issue(j + NS - 2, (ST + NS - 2) % NS);
+    v16f O[16];
+    float m_ref[2] = {-INFINITY, -INFINITY}, m_neg[2] = {0.f, 0.f};
+    float thr[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+    int pass = 1;
+    bool overflow = false;   // this pass raised a row's reference (wave-uniform)
+    v4u pb = {};             // P^T of the previous block in the B layout of the P.V MFMA
+    v4u vq[2];               // the next two V^T fragments of the previous block
 
-        const uint8_t* st = smem + ST * kStageBytes;
-
-        // S^T of block j: two 16-key halves x 18 K steps; K fragment reads kWin ahead
-        constexpr int kWin = 6;
-        auto read_k = [&](int i) __attribute__((always_inline)) {
-            const int kh = i & 1, s = i >> 1;
-            const uint32_t off = s < kRSteps ? k_off[s] + kh * 16 * kLatBytes
-                                             : p_off[s - kRSteps] + kh * 16 * kPeBytes;
-            return *reinterpret_cast<const v4u*>(st + off);
-        };
-        v4u kf[kWin];
-        #pragma unroll
-        for (int i = 0; i < kWin; ++i) kf[i] = read_k(i);
-        // the first half of block j-1's V^T fragments are read during the score MFMAs
-        v4u va[kColBlocks / 2];
-        if constexpr (PREV) read_v(std::integral_constant<int, SP>{}, 0, Half{}, va);
-        v4f s0 = v4f{}, s1 = v4f{};
-        #pragma unroll
-        for (int i = 0; i < 2 * kQSteps; ++i) {
-            const v4u cur = kf[i % kWin];
-            if (i + kWin < 2 * kQSteps) kf[i % kWin] = read_k(i + kWin);
-            if (i & 1) s1 = mfma16(cur, qf[i >> 1], s1);
-            else s0 = mfma16(cur, qf[i >> 1], s0);
-        }
-        __builtin_amdgcn_sched_group_barrier(kSgDsRd, kWin, 0);
-        if constexpr (PREV) __builtin_amdgcn_sched_group_barrier(kSgDsRd, kColBlocks, 0);
-        #pragma unroll
-        for (int i = 0; i < 2 * kQSteps - kWin; ++i) {
-            __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(kSgDsRd, 1, 0);
-        }
-        __builtin_amdgcn_sched_group_barrier(kSgMfma, kWin, 0);
-        __builtin_amdgcn_sched_barrier(0);
-
-        // online softmax of block j: lane l holds keys 4g + i (s0) and 16 + 4g + i (s1) of
-        // row l%16.  Raw scores: c > 0, so max(s) * c is exactly max(s * c), and
-        // p = 2^(s c - m) is one fma and one v_exp_f32.  Masked keys get s = -inf.
-        const int kb = k_lo + kFKeys * j;
-        if (kb + kFKeys - 1 > lim_wave) {
+    // The softmax of block j's scores sc[0..1] against the rows' fixed references.  The
+    // rare cases come first, each behind one wave-uniform branch: a block with masked keys
+    // (the end of the range, a causal limit, or the block past the end, whose scores are
+    // then all masked), and a row maximum past its reference's threshold (or a row without
+    // a reference yet), which reduces the row maxima over the row's four lanes and moves
+    // the reference (flagging the pass for a repeat if it had one).  The common path --
+    // numerators, row sums, 16-bit P^T -- is branch-free and goes out in four parts that
+    // the step interleaves with P.V MFMAs.
+    struct Soft { v4f sc[2]; float e[2][4]; uint32_t x[2], y[2]; v4u pb; };
+    auto soft_rare = [&](Soft& t, int j) __attribute__((always_inline)) {
+        const int kq0 = k_lo + k2Keys * j + 16 * kh;
+        if (kq0 + 15 > lim_wave) {
+            const int kq = kq0 + 4 * g;
             #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                s0[i] = kb + 4 * g + i <= lim ? s0[i] : -INFINITY;
-                s1[i] = kb + 16 + 4 * g + i <= lim ? s1[i] : -INFINITY;
+                t.sc[0][i] = kq + i <= lim0 ? t.sc[0][i] : -INFINITY;
+                t.sc[1][i] = kq + i <= lim1 ? t.sc[1][i] : -INFINITY;
             }
         }
-        float bm = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                         fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-        bm = row4_reduce(bm, OpMax{}) * a.c;
-        const bool raise = bm > m_run + kSlack;
-        // 2^(m_run - bm) is 0 on a row's first raise (m_run = -inf); other rows keep 1
-        const float f = raise ? __builtin_amdgcn_exp2f(m_run - bm) : 1.f;
-        // the second half of block j-1's V^T fragments, then its P.V (old scale)
-        v4u vb[kColBlocks / 2];
-        if constexpr (PREV) {
-            read_v(std::integral_constant<int, SP>{}, kColBlocks / 2, Half{}, vb);
-            const v4u pb = {pk[0], pk[1], pk[2], pk[3]};
-            #pragma unroll
-            for (int i = 0; i < kColBlocks / 2; ++i) O[i] = mfma16(va[i], pb, O[i]);
-            #pragma unroll
-            for (int i = 0; i < kColBlocks / 2; ++i)
-                O[kColBlocks / 2 + i] = mfma16(vb[i], pb, O[kColBlocks / 2 + i]);
-        }
-        m_run = raise ? bm : m_run;
-        // a row with no visible key so far has m_run = -inf and every s = -inf: p = 0
-        const float m_neg = m_run == -INFINITY ? 0.f : -m_run;
-        float p[8];
+        float mx[2];
         #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], a.c, m_neg));
-            p[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], a.c, m_neg));
-        }
-        const float ls = ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
-        l_run = l_run * f + ls;
-        #pragma unroll
-        for (int i = 0; i < 4; ++i) pk[i] = pack_bf16x2(p[2 * i], p[2 * i + 1]);
-        if constexpr (PREV) {
-            __builtin_amdgcn_sched_group_barrier(kSgDsRd, kColBlocks, 0);
+        for (int h = 0; h < 2; ++h)
+            mx[h] = fmaxf(fmaxf(t.sc[h][0], t.sc[h][1]), fmaxf(t.sc[h][2], t.sc[h][3]));
+        // rows are uniform over their four lanes after the reduction; NaN scores come here too
+        if (__builtin_amdgcn_ballot_w64(!(mx[0] * a.c <= thr[0]) || !(mx[1] * a.c <= thr[1]))) {
             #pragma unroll
-            for (int i = 0; i < kColBlocks; ++i) {
-                __builtin_amdgcn_sched_group_barrier(kSgMfma, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgValu, 2, 0);
+            for (int h = 0; h < 2; ++h) {
+                const float bm = row4_reduce(mx[h], OpMax{}) * a.c;
+                const bool over = pass < k2MaxPasses && m_ref[h] != -INFINITY && bm > thr[h];
+                overflow |= __builtin_amdgcn_ballot_w64(over) != 0;
+                if (m_ref[h] == -INFINITY || over) {
+                    m_ref[h] = bm;
+                    m_neg[h] = bm == -INFINITY ? 0.f : -bm;
+                    thr[h] = bm + k2Headroom;
+                }
             }
         }
-        asm volatile("" ::"v"(pk[0]), "v"(pk[1]), "v"(pk[2]), "v"(pk[3]), "v"(l_run));
-        // rescale after block j-1's P.V (which is in the old scale) has been accumulated
-        if (__builtin_amdgcn_ballot_w64(raise)) {
+    };
+    auto soft_part = [&](Soft& t, auto part_tag) __attribute__((always_inline)) {
+        constexpr int P = decltype(part_tag)::value;
+        if constexpr (P == 0 || P == 1) {   // numerators of one row half
             #pragma unroll
-            for (int mb = 0; mb < kColBlocks; ++mb) O[mb] *= f;
+            for (int i = 0; i < 4; ++i)
+                t.e[P][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(t.sc[P][i], a.c, m_neg[P]));
+        } else if constexpr (P == 2) {   // row sums; 16-bit P^T
+            l_run[0] += (t.e[0][0] + t.e[0][1]) + (t.e[0][2] + t.e[0][3]);
+            l_run[1] += (t.e[1][0] + t.e[1][1]) + (t.e[1][2] + t.e[1][3]);
+            #pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                t.x[d] = pack_bf16x2(t.e[0][2 * d], t.e[0][2 * d + 1]);
+                t.y[d] = pack_bf16x2(t.e[1][2 * d], t.e[1][2 * d + 1]);
+            }
+        } else {   // lane l (row half l/16 & 1) takes the other half's keys from lane l ^ 16
+            const auto s0 = __builtin_amdgcn_permlane16_swap(t.x[0], t.y[0], false, false);
+            const auto s1 = __builtin_amdgcn_permlane16_swap(t.x[1], t.y[1], false, false);
+            t.pb = v4u{s0[0], s1[0], s0[1], s1[1]};
         }
     };
 
-    // ---- prologue: blocks 0 .. NS-3 in flight; block 0 without a predecessor; then the
-    // blocks, NS per trip so that every step's ring stage is a constant; then the last
-    // block's P.V
-    #pragma unroll
-    for (int j = 0; j < NS - 2; ++j)
-        if (j < nb) issue(j, j);
-    if (nb > 0) step(0, std::integral_constant<int, 0>{}, std::false_type{});
-    for (int j0 = 1; j0 < nb; j0 += NS) {
-        step(j0, std::integral_constant<int, 1 % NS>{}, std::true_type{});
-        if (j0 + 1 < nb) step(j0 + 1, std::integral_constant<int, 2 % NS>{}, std::true_type{});
-        if constexpr (NS > 2)
-            if (j0 + 2 < nb) step(j0 + 2, std::integral_constant<int, 3 % NS>{}, std::true_type{});
-        if constexpr (NS > 3)
-            if (j0 + 3 < nb) step(j0 + 3, std::integral_constant<int, 4 % NS>{}, std::true_type{});
-    }
-    if (nb > 0) {
-        // block nb-1 sits in stage (nb-1) % NS; no later loads overwrite it
-        auto last = [&](auto st_tag) __attribute__((always_inline)) {
-            v4u va[kColBlocks];
-            read_v(st_tag, 0, std::integral_constant<int, kColBlocks>{}, va);
-            const v4u pb = {pk[0], pk[1], pk[2], pk[3]};
-            #pragma unroll
-            for (int i = 0; i < kColBlocks; ++i) O[i] = mfma16(va[i], pb, O[i]);
+    // One 32-key block j in stage j % NS.  On entry pb and vq hold block j-1's P^T and its
+    // first two V^T fragments (read before the barrier from a stage no load overwrites
+    // before step j+1), so the MFMA stream resumes right after the barrier:
+    //   P.V column blocks 0, 1 of block j-1 while block j's first K fragments arrive;
+    //   18 K steps of block j's scores (two MFMAs each), with column blocks 2..7 of block
+    //   j-1 and the nine loads of block j+2 spread among them;
+    //   column blocks 8, 9 under block j's rare softmax cases, then its common softmax in
+    //   four parts beside column blocks 10..15;
+    //   block j's first two V^T fragments for the next step.
+    // Step 0 has no previous block, and step nb only finishes block nb-1 (its scores, of
+    // whatever stage nb % NS holds, are all masked).
+    auto step = [&](int j, auto has_prev) __attribute__((always_inline)) {
+        constexpr bool PREV = decltype(has_prev)::value;
+        const Loads next = loads_of(j + NS - 2);   // scalar work, ahead of the barrier
+        wait_vm<k2Loads>();   // block j has landed; block j+1's loads may be in flight
+        lds_barrier();   // block j is in LDS for every wave; every wave is past block j-2's P.V
+
+        constexpr int kWin = 3;
+        asm volatile("" : "+v"(kb0), "+v"(pb0), "+v"(vb0));   // offsets derived per step
+        const int st = j % NS;
+        const uint32_t kbs = lat_base(kb0, st), pbs = pb0 + (uint32_t)st * k2PeStage;
+        const uint32_t vbs = lat_base(vb0, (j + NS - 1) % NS);
+        v4u kf[kWin];
+        #pragma unroll
+        for (int i = 0; i < kWin; ++i) kf[i] = k_read(kbs, pbs, i);
+        auto pv = [&](int cb) __attribute__((always_inline)) {
+            const v4u vc = vq[cb & 1];
+            if (cb + 2 < 16) vq[cb & 1] = v_read(vbs, cb + 2);
+            O[cb] = mfma32bf(vc, pb, O[cb]);
         };
-        switch ((nb - 1) % NS) {
-            case 0: last(std::integral_constant<int, 0>{}); break;
-            case 1: last(std::integral_constant<int, 1 % NS>{}); break;
-            case 2: last(std::integral_constant<int, 2 % NS>{}); break;
-            default: last(std::integral_constant<int, 3 % NS>{}); break;
+        if constexpr (PREV) {
+            pv(0);
+            pv(1);
         }
+        Soft t;
+        #pragma unroll
+        for (int s = 0; s < kQSteps; ++s) {
+            const v4u cur = kf[s % kWin];
+            if (s + kWin < kQSteps) kf[s % kWin] = k_read(kbs, pbs, s + kWin);
+            if (s == 0) {
+                mfma16_v_first(cur, qf[0][s], t.sc[0]);
+                mfma16_v_first(cur, qf[1][s], t.sc[1]);
+            } else if (s + 1 < kQSteps) {
+                mfma16_v(cur, qf[0][s], t.sc[0]);
+                mfma16_v(cur, qf[1][s], t.sc[1]);
+            } else {
+                mfma16_v(cur, qf[0][s], t.sc[0]);
+                mfma16_v_last(cur, qf[1][s], t.sc[1]);
+            }
+            if (s % 2 == 0) issue_one(next, s / 2);
+            if constexpr (PREV) {
+                if (s % 3 == 0) pv(2 + s / 3);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (PREV) {
+            pv(8);
+            pv(9);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        soft_rare(t, j);
+        __builtin_amdgcn_sched_barrier(0);
+        auto part = [&](auto p_tag, int cb0, int ncb) __attribute__((always_inline)) {
+            if constexpr (PREV) {
+                for (int cb = cb0; cb < cb0 + ncb; ++cb) pv(cb);
+            }
+            soft_part(t, p_tag);
+            __builtin_amdgcn_sched_barrier(0);
+        };
+        part(std::integral_constant<int, 0>{}, 10, 2);
+        part(std::integral_constant<int, 1>{}, 12, 2);
+        part(std::integral_constant<int, 2>{}, 14, 1);
+        part(std::integral_constant<int, 3>{}, 15, 1);
+        pb = t.pb;
+        const uint32_t vbn = lat_base(vb0, st);
+        vq[0] = v_read(vbn, 0);
+        vq[1] = v_read(vbn, 1);
+    };
+
+    // A pass over the split's keys; repeated from the first key, by every wave, only when a
+    // row's maximum outgrew its reference (each repeat raises that row's reference by more
+    // than the headroom; after k2MaxPasses passes the last one stands).  A pass that raised
+    // a reference runs to its end (its sums are then discarded); the waves learn of it
+    // through four flags in the then idle ring.
+    int* flags = reinterpret_cast<int*>(smem);
+    for (;; ++pass) {
+        #pragma unroll
+        for (int i = 0; i < 16; ++i) O[i] = v16f{};
+        l_run[0] = l_run[1] = 0.f;
+        overflow = false;
+        if (nb == 0) break;
+        #pragma unroll
+        for (int j = 0; j < NS - 2; ++j) {
+            const Loads d = loads_of(j);
+            #pragma unroll
+            for (int q = 0; q < k2Loads; ++q) issue_one(d, q);
+        }
+        step(0, std::false_type{});
+        #pragma unroll 1
+        for (int j = 1; j <= nb; ++j) step(j, std::true_type{});
+        wait_vm<0>();    // the zero loads of the two blocks past the end have landed
+        lds_barrier();   // every wave is done with the ring
+        if (lane == 0) flags[wave] = overflow ? 1 : 0;
+        lds_barrier();
+        const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+        lds_barrier();   // the flags are read before the ring is written again
+        if (!again) break;
     }
 
-    // ---- this split's partial state: O (lane l: row l%16, columns 16mb + 4g .. +3), m, l
-    l_run = row4_reduce(l_run, OpSum{});
-    if (row < rows_b) {
-        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
-        if (g == 0) {
-            if (!work.direct) a.m[slot] = m_run;
-            (work.direct ? a.l_direct : a.l)[slot] = l_run;
-        }
-        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR;
+    // ---- merge the two key halves of each row tile: wave (rt, 1) leaves its O, row maxima
+    // and row sums in LDS, wave (rt, 0) rescales both to the larger maximum and writes
+    // (O region: 64 KB per row tile, lane-major so each lane reads back its own layout)
+    l_run[0] = row4_reduce(l_run[0], OpSum{});
+    l_run[1] = row4_reduce(l_run[1], OpSum{});
+    float* ml = reinterpret_cast<float*>(smem + 2 * 65536);   // [rt][kh][m, l][32 rows]
+    v4f* oreg = reinterpret_cast<v4f*>(smem + rt * 65536) + lane;
+    if (g == 0) {
+        float* mlw = ml + (rt * 2 + kh) * 64;
+        mlw[l16] = m_ref[0];
+        mlw[16 + l16] = m_ref[1];
+        mlw[32 + l16] = l_run[0];
+        mlw[48 + l16] = l_run[1];
+    }
+    if (kh == 1) {
         #pragma unroll
-        for (int i = 0; i < kColBlocks; ++i)
-            *reinterpret_cast<v4f*>(orow + 16 * i + 4 * g) = O[i];
+        for (int cb = 0; cb < 16; ++cb)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+                oreg[64 * (4 * cb + q)] = v4f{O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]};
+    }
+    lds_barrier();
+    if (kh == 1) return;
+    const float* mla = ml + (rt * 2) * 64;
+    const float* mlb = mla + 64;
+    const float ma = mla[l32], mb = mlb[l32];
+    const float M = fmaxf(ma, mb);
+    const float fa = ma == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ma - M);
+    const float fb = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
+    const float lsum = mla[32 + l32] * fa + mlb[32 + l32] * fb;
+    if (rowO < rows_b) {
+        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + rowO;
+        if (hw == 0) {
+            if (!work.direct) a.m[slot] = M;
+            (work.direct ? a.l_direct : a.l)[slot] = lsum;
+        }
+        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR + 4 * hw;
+        #pragma unroll
+        for (int cb = 0; cb < 16; ++cb)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const v4f ob = oreg[64 * (4 * cb + q)];
+                const v4f oa = {O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]};
+                *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) = oa * fa + ob * fb;
+            }
     }
 }
 
@@ -568,15 +667,6 @@ __device__ __forceinline__ v4f mfma16f(float a, float b, v4f c) {
 constexpr float k32Headroom = 64.f;
 constexpr int k32MaxPasses = 8;
 
-// Descriptor words of `bytes` bytes at base + off (off in bytes); wave-uniform arguments
-// (readfirstlane keeps the words in scalar registers, as the load instruction needs).
-__device__ __forceinline__ v4i rsrc_span(uint64_t base, uint32_t off, uint32_t bytes) {
-    const uint64_t p = base + off;
-    return v4i{__builtin_amdgcn_readfirstlane((int32_t)(uint32_t)p),
-               __builtin_amdgcn_readfirstlane((int32_t)((uint32_t)(p >> 32) & 0xffff)),
-               __builtin_amdgcn_readfirstlane((int32_t)bytes), 0x00020000};
-}
-
 template <int NS>
 __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     static_assert(NS == 4, "two latent bases cover stages 0-1 and 2-3");
@@ -589,7 +679,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     const float* qr = reinterpret_cast<const float*>(a.qr);
 
     const FlashWork work = flash_work(a);
-    if (work.skip) return;   // as in flash_kernel (restart[] is not read before a barrier)
+    if (work.skip) return;   // the whole workgroup leaves (restart[] is not read before a barrier)
 
     const int rt = work.rt;
     const int b = work.b;
@@ -620,7 +710,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     #pragma unroll
     for (int r = 0; r < k32PeReads; ++r)
         qf[k32LatReads + r] = load16(rr, ((uint32_t)row * k32PeBytes + 64u * g + 16u * r) | qmask);
-    wait_vm<0>();   // as in flash_kernel: no wait on Q inside the key loop
+    wait_vm<0>();   // Q is in registers before the first cache load (see flash16_kernel)
 
     // ---- direct global->LDS staging: wave w loads keys 4w .. 4w+3 of a block
     const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
@@ -1150,7 +1240,7 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         if (e != hipSuccess) return e;
     }
     if (p.bf16)
-        hipLaunchKernelGGL(flash_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
+        hipLaunchKernelGGL(flash16_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
