@@ -152,9 +152,10 @@ def measure(args, ext, dev, neighbours=True):
     dims = mla_inputs.DEEPSEEK_V3
     B, Sq, Sk, desc = CONFIGS[args.config]
     dname = args.dtype or ("bf16" if args.config == "cfg4" else "f32")
-    dt = torch.bfloat16 if dname == "bf16" else torch.float32
-    if dname == "bf16" and "bf16" not in desc:
-        desc = desc.replace("fp32", "bf16")
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16}.get(dname, torch.float32)
+    half = dname != "f32"   # 16-bit storage and MFMA (bf16 or fp16)
+    if half and dname not in desc:
+        desc = desc.replace("fp32", dname).replace("bf16", dname)
     print(f"[bench] config {args.config}: {desc}", file=sys.stderr, flush=True)
 
     inp = build_inputs(B, Sq, Sk, args.seed, dt)
@@ -307,8 +308,8 @@ def measure(args, ext, dev, neighbours=True):
         step_us["3abc"] = statistics.mean(e0.elapsed_time(e1) for e0, e1 in fev) * 1e3
         names = names + ["3abc"]
 
-    work = step_work(B, Sq, Sk, dims, e=2 if dname == "bf16" else 4)
-    peak_mfma = PEAK_BF16 if dname == "bf16" else PEAK_F32
+    work = step_work(B, Sq, Sk, dims, e=2 if half else 4)
+    peak_mfma = PEAK_BF16 if half else PEAK_F32   # the fp16 MFMA peak equals the bf16 one
     per_step = {}
     for n in names:
         fl, by = work[n]
@@ -347,7 +348,7 @@ def measure(args, ext, dev, neighbours=True):
         # ---- the path's neighbours, timed separately (not part of the layer's value):
         # the wkv_b split (weight prep), the KV-cache append of this step's Sq tokens per
         # sequence, and the output projection wo of the layer's output.
-        e_b = 2 if dname == "bf16" else 4
+        e_b = 2 if half else 4
         H, R_, D_, V_, hid = dims.n_heads, dims.kv_rank, dims.rope, dims.v, dims.hidden
         bq = B * Sq
         gen = torch.Generator(device=dev).manual_seed(args.seed + 1)
@@ -513,7 +514,7 @@ def main():
     ap.add_argument("--no-bf16-line", action="store_true",
                     help="cfg2 only: skip the bf16 cfg4 figures added to its JSON line")
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
-    ap.add_argument("--dtype", default=None, choices=["f32", "bf16"],
+    ap.add_argument("--dtype", default=None, choices=["f32", "bf16", "f16"],
                     help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--seed", type=int, default=0)

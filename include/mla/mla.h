@@ -36,6 +36,7 @@ typedef struct ihipStream_t* hipStream_t;
 typedef enum mla_dtype {
     MLA_DTYPE_F32 = 0,   /* float32 storage, float32 MFMA (v_mfma_f32_32x32x2_f32)       */
     MLA_DTYPE_BF16 = 1,  /* bfloat16 storage, float32 accumulation on bf16 MFMA          */
+    MLA_DTYPE_F16 = 2,   /* float16 storage, float32 accumulation on fp16 MFMA            */
 } mla_dtype_t;
 
 typedef enum mla_status {
@@ -202,7 +203,7 @@ int mla_ctx(mla_dtype_t dtype, const mla_dims_t* dims, const float* scores,
             int32_t ld_scores, const float* alpha, const void* c_kv, float* ctx,
             void* workspace, size_t workspace_bytes, hipStream_t stream);
 
-/* 3a + 3b + 3c as one pass over the cache (bf16 or float32 with kv_rank = 512 and
+/* 3a + 3b + 3c as one pass over the cache (16-bit or float32 with kv_rank = 512 and
  * rope = 64 only; MLA_ERR_UNSUPPORTED otherwise): ctx [B*Sq*H, kv_rank] and row_sum
  * [B*Sq*H], float32, such that ctx[f] / row_sum[f] = sum_k softmax_k(t[f, :]) c_kv[b, k]
  * -- what mla_ctx and mla_combine produce, up to one positive factor per row shared by
@@ -297,7 +298,7 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
  * chunk count [B], then the items {b, c} (chunk c of sequence b covers keys [c*chunk,
  * min((c+1)*chunk, seq_lens[b]))): the full-length chunks first, then the shorter last
  * chunks, longest first.  Uses dims->batch, sq, heads and sk (= max_pages * page_size);
- * dtype selects the key block (16 keys for float32, 32 for bf16).
+ * dtype selects the key block (16 keys for float32, 32 for bf16 and float16).
  * mla_attention_work_list_ints() gives the list's length in ints (0 if dims are invalid). */
 int32_t mla_attention_work_list_ints(mla_dtype_t dtype, const mla_dims_t* dims);
 int mla_attention_work_list(mla_dtype_t dtype, const mla_dims_t* dims, const int32_t* seq_lens,

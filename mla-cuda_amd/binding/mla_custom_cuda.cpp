@@ -36,8 +36,9 @@ void check_status(int st, const char* what) {
 mla_dtype_t to_mla_dtype(const torch::Tensor& t, const char* name) {
     if (t.scalar_type() == torch::kFloat32) return MLA_DTYPE_F32;
     if (t.scalar_type() == torch::kBFloat16) return MLA_DTYPE_BF16;
+    if (t.scalar_type() == torch::kFloat16) return MLA_DTYPE_F16;
     TORCH_CHECK(false, "MLA: ", name, " has dtype ", t.scalar_type(),
-                "; supported dtypes are float32 and bfloat16");
+                "; supported dtypes are float32, bfloat16 and float16");
     return MLA_DTYPE_F32;
 }
 

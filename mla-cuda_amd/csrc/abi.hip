@@ -68,19 +68,26 @@ int check_ptr(const void* p, const char* name) {
     } while (0)
 
 int check_dtype(mla_dtype_t dt) {
-    if (dt == MLA_DTYPE_F32 || dt == MLA_DTYPE_BF16) return MLA_OK;
+    if (dt == MLA_DTYPE_F32 || dt == MLA_DTYPE_BF16 || dt == MLA_DTYPE_F16) return MLA_OK;
     return fail(MLA_ERR_INVALID_ARGUMENT, "unknown dtype %d", (int)dt);
 }
 
-bool is_bf16(mla_dtype_t dt) { return dt == MLA_DTYPE_BF16; }
-OutType storage_out(mla_dtype_t dt) { return is_bf16(dt) ? kOutBF16 : kOutF32; }
+// 16-bit storage (bf16 or fp16); the kernels take the format as a second flag
+bool is_half(mla_dtype_t dt) { return dt == MLA_DTYPE_BF16 || dt == MLA_DTYPE_F16; }
+bool is_f16(mla_dtype_t dt) { return dt == MLA_DTYPE_F16; }
+OutType storage_out(mla_dtype_t dt) {
+    return dt == MLA_DTYPE_BF16 ? kOutBF16 : dt == MLA_DTYPE_F16 ? kOutF16 : kOutF32;
+}
+const char* dtype_name(mla_dtype_t dt) {
+    return dt == MLA_DTYPE_BF16 ? "bf16" : dt == MLA_DTYPE_F16 ? "fp16" : "fp32";
+}
 
-// Row lengths of storage-dtype tensors must be whole 16-byte chunks: 4 fp32 / 8 bf16.
+// Row lengths of storage-dtype tensors must be whole 16-byte chunks: 4 fp32 / 8 16-bit.
 int check_row(mla_dtype_t dt, int v, const char* name) {
-    const int q = is_bf16(dt) ? 8 : 4;
+    const int q = is_half(dt) ? 8 : 4;
     if (v <= 0 || v % q != 0)
         return fail(MLA_ERR_INVALID_ARGUMENT, "%s must be a positive multiple of %d for %s (got %d)",
-                    name, q, is_bf16(dt) ? "bf16" : "fp32", v);
+                    name, q, dtype_name(dt), v);
     return MLA_OK;
 }
 
@@ -206,7 +213,7 @@ int check_ws(void* ws, size_t have, size_t need) {
 GemmProblem q_down_problem(mla_dtype_t dt, const mla_dims_t* d, const void* x, const void* W,
                            float* C) {
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = !is_half(dt);
     p.A = x; p.lda = d->hidden;
     p.B = W; p.ldb = d->q_lora;
     p.C = C; p.ldc = d->q_lora;
@@ -218,7 +225,7 @@ GemmProblem q_up_problem(mla_dtype_t dt, const mla_dims_t* d, const void* q_lat,
                          float* C) {
     const int n = d->heads * (d->nope + d->rope);
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = !is_half(dt);
     p.A = q_lat; p.lda = d->q_lora;
     p.B = W; p.ldb = n;
     p.C = C; p.ldc = n;
@@ -230,7 +237,7 @@ GemmProblem absorb_problem(mla_dtype_t dt, const mla_dims_t* d, const float* q_r
                            const void* W_uk, void* q_abs) {
     const int qk = d->nope + d->rope;
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
     p.A = q_raw; p.lda = (int64_t)d->heads * qk; p.sAg = qk;
     p.B = W_uk; p.ldb = d->kv_rank; p.sBg = (int64_t)d->nope * d->kv_rank;
     p.C = q_abs; p.ldc = (int64_t)d->heads * d->kv_rank; p.sCg = d->kv_rank;
@@ -242,7 +249,7 @@ GemmProblem ctx_problem(mla_dtype_t dt, const mla_dims_t* d, const float* p_scor
                         const float* alpha, const void* c_kv, float* ctx) {
     const int rows_b = d->sq * d->heads;
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = true;
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = true;
     p.A = p_scores; p.lda = ld_p; p.sAg = (int64_t)rows_b * ld_p;
     p.B = c_kv; p.ldb = d->kv_rank; p.sBg = (int64_t)d->sk * d->kv_rank;
     p.C = ctx; p.ldc = d->kv_rank; p.sCg = (int64_t)rows_b * d->kv_rank;
@@ -255,7 +262,7 @@ GemmProblem ctx_problem(mla_dtype_t dt, const mla_dims_t* d, const float* p_scor
 GemmProblem out_problem(mla_dtype_t dt, const mla_dims_t* d, const float* ctx,
                         const float* row_sum, const void* W_uv, void* out) {
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
     p.A = ctx; p.lda = (int64_t)d->heads * d->kv_rank; p.sAg = d->kv_rank;
     p.B = W_uv; p.ldb = d->kv_rank; p.sBg = (int64_t)d->v * d->kv_rank; p.b_nt = true;
     p.C = out; p.ldc = (int64_t)d->heads * d->v; p.sCg = d->v;
@@ -293,12 +300,12 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     return L;
 }
 
-// 3a+3b+3c as one fused pass over the cache (flash.hip), for bf16 and fp32 storage at the
+// 3a+3b+3c as one fused pass over the cache (flash.hip), for 16-bit and fp32 storage at the
 // DeepSeek-V3 widths.  MLA_ATTENTION_PATH=split selects the per-step kernels instead.
 FlashProblem flash_problem(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* qr,
                            const void* ckv, const void* pe, double scale, int causal) {
     FlashProblem p;
-    p.bf16 = is_bf16(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt);
     p.qa = qa; p.qr = qr; p.ckv = ckv; p.pe = pe;
     p.B = d->batch; p.Sq = d->sq; p.Sk = d->sk; p.H = d->heads; p.R = d->kv_rank;
     p.D = d->rope; p.key_stride = d->sk;
@@ -310,7 +317,7 @@ FlashProblem flash_problem(mla_dtype_t dt, const mla_dims_t* d, const void* qa, 
 bool flash_eligible(mla_dtype_t dt, const mla_dims_t* d) {
     // per-lane 32-bit buffer offsets: a batch's query rows and key rows (R elements each)
     constexpr int64_t kRange = 0x7fffffff;
-    const int64_t row_bytes = 512 * (is_bf16(dt) ? 2 : 4);
+    const int64_t row_bytes = 512 * (is_half(dt) ? 2 : 4);
     if ((int64_t)d->sq * d->heads * row_bytes >= kRange || (int64_t)d->sk * row_bytes >= kRange)
         return false;
     return flash_supported(flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0));
@@ -436,7 +443,7 @@ int run_scores(mla_dtype_t dt, const mla_dims_t* d, const void* qa, const void* 
                int page_size = 0) {
     ScoresProblem sp;
     sp.qa = qa; sp.qr = qr; sp.ckv = ckv; sp.pe = pe;
-    sp.bf16 = is_bf16(dt);
+    sp.half = is_half(dt); sp.f16 = is_f16(dt);
     sp.p = p; sp.m_part = m_part; sp.l_part = l_part;
     sp.B = d->batch; sp.Sq = d->sq; sp.Sk = d->sk; sp.H = d->heads;
     sp.R = d->kv_rank; sp.D = d->rope; sp.ld_p = ld_p; sp.P = cdiv(d->sk, kScoreTile);
@@ -502,7 +509,7 @@ GemmProblem kv_problem(mla_dtype_t dt, const mla_dims_t* d, const void* x, const
                        float* C) {
     const int n = d->kv_rank + d->rope;
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = !is_half(dt);
     p.A = x; p.lda = d->hidden;
     p.B = W; p.ldb = n;
     p.C = C; p.ldc = n;
@@ -514,7 +521,7 @@ GemmProblem oproj_problem(mla_dtype_t dt, const mla_dims_t* d, const void* attn,
                           void* out) {
     const int k = d->heads * d->v;
     GemmProblem p;
-    p.bf16 = is_bf16(dt); p.a_f32 = !is_bf16(dt); p.out_type = storage_out(dt);
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = !is_half(dt); p.out_type = storage_out(dt);
     p.A = attn; p.lda = k;
     p.B = W; p.ldb = d->hidden;
     p.C = out; p.ldc = d->hidden;
@@ -712,7 +719,7 @@ size_t mla_gemm_workspace_bytes(mla_dtype_t dtype, int32_t M, int32_t N, int32_t
     if (M <= 0 || N <= 0 || K <= 0) return 0;
     GemmProblem p;
     p.M = M; p.N = N; p.K = K;
-    p.bf16 = is_bf16(dtype); p.a_f32 = !is_bf16(dtype);
+    p.half = is_half(dtype); p.f16 = is_f16(dtype); p.a_f32 = !is_half(dtype);
     return plan_gemm(p).workspace_bytes;
 }
 
@@ -728,7 +735,7 @@ int mla_gemm(mla_dtype_t dtype, const void* A, const void* W, float* C, int32_t 
     GemmProblem p;
     p.A = A; p.lda = K;
     p.B = W; p.ldb = N;
-    p.bf16 = is_bf16(dtype); p.a_f32 = !is_bf16(dtype);
+    p.half = is_half(dtype); p.f16 = is_f16(dtype); p.a_f32 = !is_half(dtype);
     p.C = C; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
     const GemmPlan plan = plan_gemm(p);
@@ -1030,7 +1037,7 @@ int mla_attention_streaming(mla_dtype_t dtype, const mla_dims_t* dims, const voi
     MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
 
     const int rows = dims->batch * dims->sq * dims->heads;
-    const size_t esz = is_bf16(dtype) ? 2 : 4;
+    const size_t esz = is_half(dtype) ? 2 : 4;
     float* p = at<float>(workspace, L.off_p);
     float* m = at<float>(workspace, L.off_m);
     float* l = at<float>(workspace, L.off_l);
@@ -1079,7 +1086,7 @@ int mla_split_wkv_b(mla_dtype_t dtype, const mla_dims_t* dims, const void* wkv_b
     MLA_CHECK(check_ptr(wkv_b, "wkv_b"));
     MLA_CHECK(check_ptr(W_uk, "W_uk"));
     MLA_CHECK(check_ptr(W_uv, "W_uv"));
-    const int64_t row_bytes = (int64_t)dims->kv_rank * (is_bf16(dtype) ? 2 : 4);
+    const int64_t row_bytes = (int64_t)dims->kv_rank * (is_half(dtype) ? 2 : 4);
     MLA_TRY_HIP(launch_split_rows(wkv_b, W_uk, W_uv, dims->heads, dims->nope, dims->v, row_bytes,
                                   stream),
                 "wkv_b split launch");

@@ -3,7 +3,6 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
-#include <hip/hip_bf16.h>
 #include <stdint.h>
 
 #include "gpu_shape.h"
@@ -96,15 +95,56 @@ __device__ __forceinline__ int xcd_logical_block(int bid, int nblocks) {
 }
 
 // ----------------------------------------------------------------------------------
-// Element conversion helpers
+// 16-bit storage formats.  Both are raw 16-bit words in memory and in LDS; conversions
+// from fp32 round to nearest even, as torch does (a NaN stays a NaN):
+//   bfloat16 -- gfx950's v_cvt_pk_bf16_f32, two values per instruction;
+//   fp16     -- v_cvt_f16_f32 in the default rounding mode (values past 65504 become
+//               infinities, values below 2^-24 flush to zero, as in IEEE binary16).
+// Half<TL> gives kernels templated on the format one interface: TL = bf16_t or f16_t.
+// Store16<OUT> maps an output-format code (kernels.h OutType: 1 bf16, 2 fp16) to it.
 // ----------------------------------------------------------------------------------
-__device__ __forceinline__ float to_f32(float v) { return v; }
-__device__ __forceinline__ float to_f32(__hip_bfloat16 v) { return __bfloat162float(v); }
+typedef uint16_t bf16_t;
+typedef _Float16 f16_t;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
-template <typename T> __device__ __forceinline__ T from_f32(float v);
-template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
-template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
-    return __float2bfloat16(v);
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
 }
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    const f16x2_t v = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+template <typename TL> struct Half;
+template <> struct Half<bf16_t> {
+    static constexpr bool kF16 = false;
+    __device__ static __forceinline__ uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+    __device__ static __forceinline__ uint32_t bits(float f) { return f32_to_bf16_bits(f); }
+    __device__ static __forceinline__ float to_f32(uint32_t h) { return bf16_bits_to_f32(h); }
+};
+template <> struct Half<f16_t> {
+    static constexpr bool kF16 = true;
+    __device__ static __forceinline__ uint32_t pack2(float lo, float hi) { return pack_f16x2(lo, hi); }
+    __device__ static __forceinline__ uint32_t bits(float f) { return f32_to_f16_bits(f); }
+    __device__ static __forceinline__ float to_f32(uint32_t h) { return f16_bits_to_f32(h); }
+};
+
+template <int OUT> struct Store16;
+template <> struct Store16<1> : Half<bf16_t> {};
+template <> struct Store16<2> : Half<f16_t> {};
 
 }  // namespace mla

@@ -223,7 +223,8 @@ __device__ __forceinline__ v4i rsrc_span(uint64_t base, uint32_t off, uint32_t b
 //     256-byte quarters of a key row), step 16 + r rope chunk 4r + g.  Accumulator element
 //     i of lane l is key 4g + i of row (16 half) + l%16.
 //   softmax per lane: 8 scores, against a fixed per-row reference (first visible block's
-//     maximum; a row that passes it by k2Headroom raises it and the pass is repeated, as in
+//     maximum; a row that passes it by the headroom (2^64 for bf16, 2^15 for fp16, which
+//     P^T is rounded to) raises it and the pass is repeated, as in
 //     flash32_kernel), so the 256 O accumulators are never rescaled
 //   O^T[512 cols x 32 rows] += V^T[512 x 16 keys] . P^T[16 keys x 32 rows]: sixteen
 //     32x32x16 MFMAs.  P^T is the score accumulator rounded to 16 bits after one
@@ -256,9 +257,15 @@ constexpr int k2MaxPasses = 8;
 
 __device__ __forceinline__ int sw16(int k) { return ((k & 3) << 2) | ((k >> 2) & 3); }
 
-__device__ __forceinline__ v16f mfma32bf(v4u a, v4u b, v16f c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a),
-                                                   __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+// 32x32x16 MFMA in the storage format TL (bf16_t or f16_t)
+template <typename TL>
+__device__ __forceinline__ v16f mfma32h(v4u a, v4u b, v16f c) {
+    if constexpr (Half<TL>::kF16)
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a),
+                                                      __builtin_bit_cast(v8h, b), c, 0, 0, 0);
+    else
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a),
+                                                       __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
 }
 
 // The score MFMAs of flash16_kernel (16x16x32 bf16: lane l supplies A[l%16][8(l/16) .. +7]
@@ -270,18 +277,34 @@ __device__ __forceinline__ v16f mfma32bf(v4u a, v4u b, v16f c) {
 // never reads the accumulator the previous one wrote; the K fragments come from LDS reads
 // the compiler waits for; and after the last MFMA of a block 16 wait states pass before any
 // VALU reads an accumulator (the 16x16x32 bf16 MFMA needs at most 11).
+// (TL picks the bf16 or the fp16 form; both have the same layout and timing.)
+template <typename TL>
 __device__ __forceinline__ void mfma16_v_first(v4u a, v4u b, v4f& c) {
-    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+    if constexpr (Half<TL>::kF16)
+        asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
+    else
+        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=&v"(c) : "v"(a), "v"(b));
 }
+template <typename TL>
 __device__ __forceinline__ void mfma16_v(v4u a, v4u b, v4f& c) {
-    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    if constexpr (Half<TL>::kF16)
+        asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
+    else
+        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+v"(c) : "v"(a), "v"(b));
 }
+template <typename TL>
 __device__ __forceinline__ void mfma16_v_last(v4u a, v4u b, v4f& c) {
-    asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
+    if constexpr (Half<TL>::kF16)
+        asm("v_mfma_f32_16x16x32_f16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
+    else
+        asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
 }
 
-template <int NS>
+template <int NS, typename TL>
 __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
+    // P^T is rounded to TL: with bf16's 8 exponent bits a term may reach 2^64 over its
+    // row's reference; fp16 stops at 65504, so there a term stays below 2^15
+    constexpr float kHeadroom = Half<TL>::kF16 ? 15.f : k2Headroom;
     static_assert(NS == 4, "stage offsets: stages 2-3 are stages 0-1 XOR 64 KB");
     constexpr int kPeBase = NS * k2LatStage;                    // 128 KB
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kPeBase + NS * k2PeStage];
@@ -439,7 +462,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
                 if (m_ref[h] == -INFINITY || over) {
                     m_ref[h] = bm;
                     m_neg[h] = bm == -INFINITY ? 0.f : -bm;
-                    thr[h] = bm + k2Headroom;
+                    thr[h] = bm + kHeadroom;
                 }
             }
         }
@@ -455,8 +478,8 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
             l_run[1] += (t.e[1][0] + t.e[1][1]) + (t.e[1][2] + t.e[1][3]);
             #pragma unroll
             for (int d = 0; d < 2; ++d) {
-                t.x[d] = pack_bf16x2(t.e[0][2 * d], t.e[0][2 * d + 1]);
-                t.y[d] = pack_bf16x2(t.e[1][2 * d], t.e[1][2 * d + 1]);
+                t.x[d] = Half<TL>::pack2(t.e[0][2 * d], t.e[0][2 * d + 1]);
+                t.y[d] = Half<TL>::pack2(t.e[1][2 * d], t.e[1][2 * d + 1]);
             }
         } else {   // lane l (row half l/16 & 1) takes the other half's keys from lane l ^ 16
             const auto s0 = __builtin_amdgcn_permlane16_swap(t.x[0], t.y[0], false, false);
@@ -493,7 +516,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
         auto pv = [&](int cb) __attribute__((always_inline)) {
             const v4u vc = vq[cb & 1];
             if (cb + 2 < 16) vq[cb & 1] = v_read(vbs, cb + 2);
-            O[cb] = mfma32bf(vc, pb, O[cb]);
+            O[cb] = mfma32h<TL>(vc, pb, O[cb]);
         };
         if constexpr (PREV) {
             pv(0);
@@ -505,14 +528,14 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
             const v4u cur = kf[s % kWin];
             if (s + kWin < kQSteps) kf[s % kWin] = k_read(kbs, pbs, s + kWin);
             if (s == 0) {
-                mfma16_v_first(cur, qf[0][s], t.sc[0]);
-                mfma16_v_first(cur, qf[1][s], t.sc[1]);
+                mfma16_v_first<TL>(cur, qf[0][s], t.sc[0]);
+                mfma16_v_first<TL>(cur, qf[1][s], t.sc[1]);
             } else if (s + 1 < kQSteps) {
-                mfma16_v(cur, qf[0][s], t.sc[0]);
-                mfma16_v(cur, qf[1][s], t.sc[1]);
+                mfma16_v<TL>(cur, qf[0][s], t.sc[0]);
+                mfma16_v<TL>(cur, qf[1][s], t.sc[1]);
             } else {
-                mfma16_v(cur, qf[0][s], t.sc[0]);
-                mfma16_v_last(cur, qf[1][s], t.sc[1]);
+                mfma16_v<TL>(cur, qf[0][s], t.sc[0]);
+                mfma16_v_last<TL>(cur, qf[1][s], t.sc[1]);
             }
             if (s % 2 == 0) issue_one(next, s / 2);
             if constexpr (PREV) {
@@ -1146,7 +1169,7 @@ FlashPlan plan_flash(const FlashProblem& p) {
     FlashPlan f;
     f.row_tiles = (p.Sq * p.H + kFRows - 1) / kFRows;
     const int base = p.B * f.row_tiles;
-    const int block_keys = p.bf16 ? kFKeys : k32Keys;
+    const int block_keys = p.half ? kFKeys : k32Keys;
     const int blocks = (p.Sk + block_keys - 1) / block_keys;
     const size_t rows = (size_t)p.B * p.Sq * p.H;
     const size_t rows_b = (size_t)p.Sq * p.H;
@@ -1182,7 +1205,7 @@ hipError_t launch_flash_worklist(const FlashProblem& p, const FlashPlan& f, int*
                                  hipStream_t stream) {
     if (!f.balanced || !p.seq_lens) return hipErrorInvalidValue;
     hipLaunchKernelGGL(flash_worklist_kernel, dim3(1), dim3(kWlThreads), 0, stream, p.seq_lens,
-                       p.B, p.Sk, f.row_tiles, p.bf16 ? kFKeys : k32Keys, f.max_items, wl);
+                       p.B, p.Sk, f.row_tiles, p.half ? kFKeys : k32Keys, f.max_items, wl);
     return hipGetLastError();
 }
 
@@ -1239,8 +1262,10 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipError_t e = launch_flash_worklist(p, f, wl, stream);
         if (e != hipSuccess) return e;
     }
-    if (p.bf16)
-        hipLaunchKernelGGL(flash16_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
+    if (p.half && p.f16)
+        hipLaunchKernelGGL((flash16_kernel<kFStages, f16_t>), dim3(grid), dim3(kFThreads), 0, stream, a);
+    else if (p.half)
+        hipLaunchKernelGGL((flash16_kernel<kFStages, bf16_t>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();

@@ -1,4 +1,4 @@
-// Batched MFMA GEMM for the layer's dense contractions, fp32 or bf16:
+// Batched MFMA GEMM for the layer's dense contractions, fp32, bf16 or fp16:
 //   2a1 / 2a2  x @ W_q_a, q_lat @ W_q_b          (NN, G = 1)
 //   2c         q_nope[h] @ W_uk[h]                (NN, G = heads)
 //   3c         (p * alpha) @ c_kv[b]              (NN, G = batch, A scaled by alpha)
@@ -6,14 +6,14 @@
 //
 // Workgroup = 4 wave64s.  A BM x BN output tile is split 2x2 / 4x1 / 1x4 over the waves,
 // each wave covering its sub-tile with 32x32 MFMA accumulator blocks
-// (v_mfma_f32_32x32x2_f32, or v_mfma_f32_32x32x16_bf16 in the bf16 path; see mma.h).
-// K is walked in slices of 128 bytes per row (32 fp32 / 64 bf16) staged through
+// (v_mfma_f32_32x32x2_f32, or the 32x32x16 bf16 / fp16 MFMA in the 16-bit paths; see
+// mma.h).  K is walked in slices of 128 bytes per row (32 fp32 / 64 16-bit) staged through
 // double-buffered LDS: the next slice's 128-bit global loads are in flight while the
 // current slice feeds the MFMAs.  Within a slice, K is permuted so each lane's operands
 // for one K step are 16 contiguous bytes: one ds_read_b128 per fragment for K-contiguous
-// operands, four ds_read_b32 (fp32) / eight ds_read_u16 (bf16) for N-contiguous ones.
-// In the bf16 path, fp32 A operands (q_raw, p, ctx) are scaled in fp32 and rounded to
-// bf16 (nearest even) as they are written to LDS.
+// operands, four ds_read_b32 (fp32) / eight ds_read_u16 (16-bit) for N-contiguous ones.
+// In the 16-bit paths, fp32 A operands (q_raw, p, ctx) are scaled in fp32 and rounded to
+// the storage format (nearest even) as they are written to LDS.
 //
 // LDS rows of K-contiguous tiles are 144 B (128 B + 16 B pad): the eight lanes of a
 // ds_read_b128 / ds_write_b128 phase then land on disjoint bank groups.  N-contiguous
@@ -57,8 +57,8 @@ constexpr int nn_row_words() {
     return BN * (int)sizeof(TL) / 4 + (sizeof(TL) == 4 ? 8 : 4);
 }
 
-// TL: LDS / MFMA element type (float or bf16_t).  TA: global element type of A (float,
-// or bf16_t when TL is bf16).  B is always TL in global memory.
+// TL: LDS / MFMA element type (float, bf16_t or f16_t).  TA: global element type of A
+// (float, or TL when TL is 16-bit).  B is always TL in global memory.
 // PD = depth of the register prefetch ring (slices in flight while one feeds the MFMAs):
 // 2 -- one slice of MFMA work (~4K cycles per wave in fp32, 8x less in bf16) does not
 // cover the HBM latency of a long-K stream such as 3c's scores x c_kv; with two slices in
@@ -241,8 +241,8 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             } else if constexpr (A_F32) {
                 const float s = (AMODE == kAPlain) ? 1.f : rsc[slot][i];
                 const v4f f0 = raf[slot][i][0] * s, f1 = raf[slot][i][A_F4 - 1] * s;
-                w = v4u{pack_bf16x2(f0[0], f0[1]), pack_bf16x2(f0[2], f0[3]),
-                        pack_bf16x2(f1[0], f1[1]), pack_bf16x2(f1[2], f1[3])};
+                w = v4u{Half<TL>::pack2(f0[0], f0[1]), Half<TL>::pack2(f0[2], f0[3]),
+                        Half<TL>::pack2(f1[0], f1[1]), Half<TL>::pack2(f1[2], f1[3])};
             } else {
                 w = ra[slot][i];
             }
@@ -333,7 +333,7 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             to_ws ? make_rsrc(a.ws + (int64_t)sp_ * a.ws_split + ((int64_t)g_ * a.M + m0_) * a.N + n0_)
                   : (kF32Out ? make_rsrc(static_cast<float*>(a.C) + (int64_t)g_ * a.sCg +
                                          (int64_t)m0_ * a.ldc + n0_)
-                             : make_rsrc(static_cast<bf16_t*>(a.C) + (int64_t)g_ * a.sCg +
+                             : make_rsrc(static_cast<uint16_t*>(a.C) + (int64_t)g_ * a.sCg +
                                          (int64_t)m0_ * a.ldc + n0_));
         #pragma unroll
         for (int i = 0; i < TM; ++i) {
@@ -348,12 +348,13 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
                     const int re = 8 * (e >> 2) + (e & 3);
                     const int soff = __builtin_amdgcn_readfirstlane((int)(re * ld * esz));
                     const uint32_t off = lane_off | oob_mask(m0_ + r0 + re, a.M);
-                    if (to_ws || kF32Out)
+                    if (to_ws || kF32Out) {
                         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[i][j][e]), rso,
                                                               (int)off, soff, 0);
-                    else
+                    } else if constexpr (!kF32Out) {
                         __builtin_amdgcn_raw_buffer_store_b16(
-                            (uint16_t)f32_to_bf16_bits(acc[i][j][e]), rso, (int)off, soff, 0);
+                            (uint16_t)Store16<OUT>::bits(acc[i][j][e]), rso, (int)off, soff, 0);
+                    }
                 }
             }
         }
@@ -475,8 +476,8 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
         const int m = gm % M;
         const int g = gm / M;
         const int64_t off = (int64_t)g * sCg + (int64_t)m * ldc + n;
-        if (OUT == kOutF32) static_cast<float*>(C)[off] = s;
-        else static_cast<bf16_t*>(C)[off] = (bf16_t)f32_to_bf16_bits(s);
+        if constexpr (OUT == kOutF32) static_cast<float*>(C)[off] = s;
+        else static_cast<uint16_t*>(C)[off] = (uint16_t)Store16<OUT>::bits(s);
     }
 }
 
@@ -508,58 +509,67 @@ hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipSt
 
 // The operand/epilogue combinations the layer uses (others are rejected):
 //   fp32:  NN plain  -> f32 (2a1, 2a2, 2c) | NN alpha -> f32 (3c) | NT rowrecip -> f32 (3d)
-//   bf16:  NN plain, A bf16 -> f32 (2a1, 2a2) or -> bf16 (wo) | NN plain, A f32 -> bf16 (2c)
-//          NN alpha, A f32 -> f32 (3c)         | NT rowrecip, A f32 -> bf16 (3d)
+//   16-bit (bf16 or fp16, TL): NN plain, A 16-bit -> f32 (2a1, 2a2) or -> 16-bit (wo) |
+//          NN plain, A f32 -> 16-bit (2c) | NN alpha, A f32 -> f32 (3c) |
+//          NT rowrecip, A f32 -> 16-bit (3d)
 // A split-K launch writes fp32 partials whatever the output type.
-hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
-                    bool persist, hipStream_t stream) {
+template <typename TL>
+hipError_t dispatch16(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
+                      bool persist, hipStream_t stream) {
+    constexpr int O16 = Half<TL>::kF16 ? kOutF16 : kOutBF16;
     const bool split = a.split > 1;
+    const bool f32_out = split || p.out_type == kOutF32;
+    if (!f32_out && p.out_type != O16) return hipErrorInvalidValue;
     if (persist) {   // NN plain with f32 output or partials (2c, 2a1, 2a2)
-        if (p.b_nt || p.amode != kAPlain || p.b_pages || !(p.out_type == kOutF32 || split))
+        if (p.b_nt || p.amode != kAPlain || p.b_pages || !f32_out || p.a_f32)
             return hipErrorInvalidValue;
-        if (!p.bf16)
-            return launch_tiles<float, float, false, kAPlain, kOutF32, false, true>(a, bm, bn,
-                                                                                   nblocks, stream);
-        if (!p.a_f32)
-            return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutF32, false, true>(
-                a, bm, bn, nblocks, stream);
-        return hipErrorInvalidValue;
+        return launch_tiles<TL, TL, false, kAPlain, kOutF32, false, true>(a, bm, bn, nblocks,
+                                                                           stream);
     }
     if (p.b_pages) {   // paged NN B: 3c over a paged cache only
-        if (p.b_nt || p.amode != kAAlpha || !(p.out_type == kOutF32 || split))
-            return hipErrorInvalidValue;
-        if (!p.bf16)
-            return launch_tiles<float, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
-        if (p.a_f32)
-            return launch_tiles<bf16_t, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
-        return hipErrorInvalidValue;
-    }
-    if (!p.bf16) {
-        if (!p.b_nt && p.amode == kAPlain && (p.out_type == kOutF32 || split))
-            return launch_tiles<float, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
-        if (!p.b_nt && p.amode == kAAlpha && (p.out_type == kOutF32 || split))
-            return launch_tiles<float, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
-        if (p.b_nt && p.amode == kARowRecip && (p.out_type == kOutF32 || split))
-            return launch_tiles<float, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
-        return hipErrorInvalidValue;
+        if (p.b_nt || p.amode != kAAlpha || !f32_out || !p.a_f32) return hipErrorInvalidValue;
+        return launch_tiles<TL, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
     }
     if (!p.b_nt && p.amode == kAPlain && !p.a_f32) {
-        if (split || p.out_type == kOutF32)
-            return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
-        return launch_tiles<bf16_t, bf16_t, false, kAPlain, kOutBF16>(a, bm, bn, nblocks, stream);
+        if (f32_out) return launch_tiles<TL, TL, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<TL, TL, false, kAPlain, O16>(a, bm, bn, nblocks, stream);
     }
     if (!p.b_nt && p.amode == kAPlain && p.a_f32) {
-        if (split || p.out_type == kOutF32)
-            return launch_tiles<bf16_t, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
-        return launch_tiles<bf16_t, float, false, kAPlain, kOutBF16>(a, bm, bn, nblocks, stream);
+        if (f32_out) return launch_tiles<TL, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<TL, float, false, kAPlain, O16>(a, bm, bn, nblocks, stream);
     }
-    if (!p.b_nt && p.amode == kAAlpha && p.a_f32 && (p.out_type == kOutF32 || split))
-        return launch_tiles<bf16_t, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
+    if (!p.b_nt && p.amode == kAAlpha && p.a_f32 && f32_out)
+        return launch_tiles<TL, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
     if (p.b_nt && p.amode == kARowRecip && p.a_f32) {
-        if (split || p.out_type == kOutF32)
-            return launch_tiles<bf16_t, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
-        return launch_tiles<bf16_t, float, true, kARowRecip, kOutBF16>(a, bm, bn, nblocks, stream);
+        if (f32_out)
+            return launch_tiles<TL, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<TL, float, true, kARowRecip, O16>(a, bm, bn, nblocks, stream);
     }
+    return hipErrorInvalidValue;
+}
+
+hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int nblocks,
+                    bool persist, hipStream_t stream) {
+    if (p.half)
+        return p.f16 ? dispatch16<f16_t>(p, a, bm, bn, nblocks, persist, stream)
+                     : dispatch16<bf16_t>(p, a, bm, bn, nblocks, persist, stream);
+    const bool split = a.split > 1;
+    const bool f32_out = split || p.out_type == kOutF32;
+    if (persist) {   // NN plain with f32 output or partials (2c, 2a1, 2a2)
+        if (p.b_nt || p.amode != kAPlain || p.b_pages || !f32_out) return hipErrorInvalidValue;
+        return launch_tiles<float, float, false, kAPlain, kOutF32, false, true>(a, bm, bn,
+                                                                               nblocks, stream);
+    }
+    if (p.b_pages) {   // paged NN B: 3c over a paged cache only
+        if (p.b_nt || p.amode != kAAlpha || !f32_out) return hipErrorInvalidValue;
+        return launch_tiles<float, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
+    }
+    if (!p.b_nt && p.amode == kAPlain && f32_out)
+        return launch_tiles<float, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+    if (!p.b_nt && p.amode == kAAlpha && f32_out)
+        return launch_tiles<float, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
+    if (p.b_nt && p.amode == kARowRecip && f32_out)
+        return launch_tiles<float, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);
     return hipErrorInvalidValue;
 }
 
@@ -581,11 +591,11 @@ constexpr TileShape kTiles[] = {
     {128, 128, 0.80}, {128, 96, 0.78}, {128, 64, 0.72}, {64, 128, 0.72},
     {64, 64, 0.60},   {32, 128, 0.55}, {128, 32, 0.55}};
 
-int lds_bytes(int bm, int bn, bool nt, bool bf16) {
+int lds_bytes(int bm, int bn, bool nt, bool half) {
     const int a = 2 * bm * kRowWords * 4;
-    const int nn_row = bf16 ? bn * 2 + 16 : bn * 4 + 32;
-    // bf16 N-contiguous B is staged transposed, i.e. in the NT layout
-    const int b = (nt || bf16) ? 2 * bn * kRowWords * 4 : 2 * 32 * nn_row;
+    const int nn_row = half ? bn * 2 + 16 : bn * 4 + 32;
+    // 16-bit N-contiguous B is staged transposed, i.e. in the NT layout
+    const int b = (nt || half) ? 2 * bn * kRowWords * 4 : 2 * 32 * nn_row;
     return a + b;
 }
 
@@ -596,7 +606,7 @@ int lds_bytes(int bm, int bn, bool nt, bool bf16) {
 // The last column is the tiles per workgroup of a persistent grid (1: one per tile); 2c
 // at B = 128 runs 128x64 tiles two per workgroup, 30.5 us against 32.8 us for one 128x128
 // tile per workgroup.
-struct TunedPlan { int M, N, K, G; bool nt, bf16; int bm, bn, split, tiles_per_wg = 1; };
+struct TunedPlan { int M, N, K, G; bool nt, half; int bm, bn, split, tiles_per_wg = 1; };
 constexpr TunedPlan kTuned[] = {
     // B = 128 decode, fp32: 2a1, 2a2, 2c, 3d, wo, kv
     {128, 1536, 7168, 1, false, false, 64, 64, 16},
@@ -630,7 +640,7 @@ constexpr TunedPlan kTuned[] = {
 bool tuned_plan(const GemmProblem& p, GemmPlan* out) {
     for (const auto& t : kTuned)
         if (t.M == p.M && t.N == p.N && t.K == p.K && t.G == p.G && t.nt == p.b_nt &&
-            t.bf16 == p.bf16) {
+            t.half == p.half) {
             out->bm = t.bm; out->bn = t.bn; out->split = t.split;
             out->tiles_per_wg = t.tiles_per_wg;
             return true;
@@ -671,12 +681,12 @@ bool plan_override(const GemmProblem& p, GemmPlan* out) {
 
 GemmPlan plan_gemm(const GemmProblem& p) {
     // fp32 MFMA: 256 flop/clk/CU at 2.4 GHz; dense bf16 MFMA is 16x that
-    const double kCuRate = 256.0 * 2.4e9 * (p.bf16 ? 16.0 : 1.0);
+    const double kCuRate = 256.0 * 2.4e9 * (p.half ? 16.0 : 1.0);
     constexpr double kHbm = 5.0e12;             // sustained HBM B/s
     constexpr double kReduceLaunch = 3e-6;      // s
-    const int kBK = p.bf16 ? 64 : 32;           // K per slice
-    const double eb = p.bf16 ? 2.0 : 4.0;       // bytes per B element
-    const double ea = p.a_f32 || !p.bf16 ? 4.0 : 2.0;
+    const int kBK = p.half ? 64 : 32;           // K per slice
+    const double eb = p.half ? 2.0 : 4.0;       // bytes per B element
+    const double ea = p.a_f32 || !p.half ? 4.0 : 2.0;
     const int kslices = cdiv(p.K, kBK);
     GemmPlan best;
     double best_t = 1e300;
@@ -684,7 +694,7 @@ GemmPlan plan_gemm(const GemmProblem& p) {
         for (const auto& t : kTiles) {
             const int tm = cdiv(p.M, t.bm), tn = cdiv(p.N, t.bn);
             const int64_t tiles = (int64_t)tm * tn * p.G;
-            const int occ = std::max(1, std::min(2, 163840 / lds_bytes(t.bm, t.bn, p.b_nt, p.bf16)));
+            const int occ = std::max(1, std::min(2, 163840 / lds_bytes(t.bm, t.bn, p.b_nt, p.half)));
             for (int split = 1; split <= std::max(1, kslices / 2); split *= 2) {
                 const int per = cdiv(kslices, split);
                 const int real_split = cdiv(kslices, per);
@@ -749,12 +759,12 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     a.alpha_shift = 0;
     if (p.amode == kAAlpha) {
         // one alpha per slice: the tile is a power of two and a multiple of the slice
-        const int ks = p.bf16 ? 64 : 32;
+        const int ks = p.half ? 64 : 32;
         if (p.alpha_tile < ks || (p.alpha_tile & (p.alpha_tile - 1)) != 0) return hipErrorInvalidValue;
         while ((1 << a.alpha_shift) < p.alpha_tile) ++a.alpha_shift;
     }
     // every staging offset (a row of a 128-row tile) must stay below the buffer range
-    const int64_t ea = (p.a_f32 || !p.bf16) ? 4 : 2, eb = p.bf16 ? 2 : 4;
+    const int64_t ea = (p.a_f32 || !p.half) ? 4 : 2, eb = p.half ? 2 : 4;
     if (128 * std::max({p.lda * ea, p.ldb * eb, (int64_t)p.alpha_ld * 4}) >= kRsrcRange)
         return hipErrorInvalidValue;
     const int64_t nblocks64 = (int64_t)a.tiles_m * a.tiles_n * a.G * a.split;
@@ -764,8 +774,8 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     // other problem keeps one workgroup per tile
     const bool persist = plan.tiles_per_wg > 1 && p.M % plan.bm == 0 && p.N % plan.bn == 0 &&
                          !p.b_nt && p.amode == kAPlain && !p.k_len && !p.b_pages &&
-                         (p.out_type == kOutF32 || plan.split > 1) && (!p.bf16 || !p.a_f32) &&
-                         plan.k_chunk % (p.bf16 ? 64 : 32) == 0;
+                         (p.out_type == kOutF32 || plan.split > 1) && (!p.half || !p.a_f32) &&
+                         plan.k_chunk % (p.half ? 64 : 32) == 0;
     if (persist) nblocks = cdiv(nblocks, plan.tiles_per_wg);
     hipError_t e = dispatch(p, a, plan.bm, plan.bn, nblocks, persist, stream);
     if (e != hipSuccess || plan.split == 1 || !reduce) return e;
@@ -774,8 +784,11 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     if (p.out_type == kOutF32)
         hipLaunchKernelGGL(split_reduce_kernel<kOutF32>, dim3(rblocks), dim3(256), 0, stream,
                            a.ws, a.ws_split, plan.split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
-    else
+    else if (p.out_type == kOutBF16)
         hipLaunchKernelGGL(split_reduce_kernel<kOutBF16>, dim3(rblocks), dim3(256), 0, stream,
+                           a.ws, a.ws_split, plan.split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
+    else
+        hipLaunchKernelGGL(split_reduce_kernel<kOutF16>, dim3(rblocks), dim3(256), 0, stream,
                            a.ws, a.ws_split, plan.split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
     return hipGetLastError();
 }

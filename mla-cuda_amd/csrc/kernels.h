@@ -8,15 +8,15 @@
 namespace mla {
 
 // ---------------------------------------------------------------- batched MFMA GEMM
-// C[g][m][n] = sum_k opA(A)[g][m][k] * opB(B)[g][k][n]   (fp32 accumulate; fp32 or bf16
-// MFMA as GemmProblem::bf16 says)
+// C[g][m][n] = sum_k opA(A)[g][m][k] * opB(B)[g][k][n]   (fp32 accumulate; fp32, bf16 or
+// fp16 MFMA as GemmProblem::half / f16 say)
 //   A[g][m][k]  at A + g*sAg + m*lda + k
 //   B (NN)      at B + g*sBg + k*ldb + n      B (NT) at B + g*sBg + n*ldb + k
 //   C[g][m][n]  at C + g*sCg + m*ldc + n
 // A modes: kAPlain; kARowRecip (row m of batch g scaled by 1/rs[m*rs_m + g*rs_g]);
 //          kAAlpha (A[g][m][k] scaled by alpha[(g*M + m)*alpha_ld + k/alpha_tile]).
 enum AMode { kAPlain = 0, kARowRecip = 1, kAAlpha = 2 };
-enum OutType { kOutF32 = 0, kOutBF16 = 1 };
+enum OutType { kOutF32 = 0, kOutBF16 = 1, kOutF16 = 2 };   // the codes Store16<> takes
 
 struct GemmProblem {
     const void* A = nullptr; int64_t lda = 0, sAg = 0;
@@ -24,7 +24,8 @@ struct GemmProblem {
     void* C = nullptr;        int64_t ldc = 0, sCg = 0;
     int M = 0, N = 0, K = 0, G = 1;
     bool b_nt = false;
-    bool bf16 = false;   // B (weights / cache) and the MFMA are bf16 (else fp32)
+    bool half = false;   // B (weights / cache) and the MFMA are 16-bit (else fp32)
+    bool f16 = false;    // the 16-bit format is fp16 (else bfloat16)
     bool a_f32 = true;   // A is fp32 in global memory (else the storage dtype)
     AMode amode = kAPlain;
     const float* rs = nullptr; int64_t rs_m = 0, rs_g = 0;
@@ -97,7 +98,8 @@ struct ScoresProblem {
     const void* qr = nullptr;    // [B*Sq*H, D]
     const void* ckv = nullptr;   // [B, Sk, R]
     const void* pe = nullptr;    // [B, Sk, D]
-    bool bf16 = false;           // storage / MFMA dtype bf16 (else fp32)
+    bool half = false;           // storage / MFMA dtype 16-bit (else fp32)
+    bool f16 = false;            // the 16-bit format is fp16 (else bfloat16)
     float* p = nullptr;          // [B*Sq*H, ld_p]
     float* m_part = nullptr;     // [B*Sq*H, P]
     float* l_part = nullptr;
@@ -121,7 +123,8 @@ constexpr int kScoreTile = 128;  // keys per softmax partial (one 3a workgroup's
 // One pass over the cache per key split: ctx [rows, R] (unnormalised) and row_sum [rows]
 // for 3d, as 3c and 3b produce them.  bf16 or fp32 storage, R = 512, D = 64 only.
 struct FlashProblem {
-    bool bf16 = true;            // storage dtype (else fp32)
+    bool half = true;            // storage dtype 16-bit (else fp32)
+    bool f16 = false;            // the 16-bit format is fp16 (else bfloat16)
     const void* qa = nullptr;    // [B*Sq*H, R]
     const void* qr = nullptr;    // [B*Sq*H, D]
     const void* ckv = nullptr;   // [B, key_stride, R]

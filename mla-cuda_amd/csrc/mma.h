@@ -5,6 +5,7 @@
 // byte 32*step + 16*(l/32) of its row (one ds_read_b128) and feeds
 //   fp32: four v_mfma_f32_32x32x2_f32  (4 k values per lane, K = 8 per step)
 //   bf16: one   v_mfma_f32_32x32x16_bf16 (8 k values per lane, K = 16 per step)
+//   fp16: one   v_mfma_f32_32x32x16_f16  (the same layout)
 // Both instructions take row/column l%32 from lane l and split K between the two
 // half-waves, and A and B fragments are always read from the same k offsets, so the
 // product is exact whatever order the hardware assigns to the k values inside a lane.
@@ -16,20 +17,6 @@
 namespace mla {
 
 typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-
-// bf16 storage is raw 16-bit words.  Conversion is gfx950's v_cvt_pk_bf16_f32: IEEE
-// round to nearest even, two values per instruction (as torch rounds; a NaN stays a NaN).
-typedef uint16_t bf16_t;
-typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
-    return __builtin_bit_cast(uint32_t, v);
-}
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-    return __builtin_bit_cast(uint16_t, (__bf16)f);
-}
-__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
 
 template <typename TL> struct Mma;
 
@@ -52,6 +39,16 @@ template <> struct Mma<bf16_t> {
     __device__ static __forceinline__ v16f sub(v4u a, v4u b, int, v16f c) {
         return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(v8bf, a),
                                                        __builtin_bit_cast(v8bf, b), c, 0, 0, 0);
+    }
+};
+
+template <> struct Mma<f16_t> {
+    static constexpr int kElems = 8;
+    static constexpr int kSlice = 64;
+    static constexpr int kSub = 1;
+    __device__ static __forceinline__ v16f sub(v4u a, v4u b, int, v16f c) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, a),
+                                                      __builtin_bit_cast(v8h, b), c, 0, 0, 0);
     }
 };
 

@@ -68,17 +68,18 @@ __device__ __forceinline__ void rms_row(const float* base, int nsplit, int64_t s
     const float inv = rsqrtf(total / (float)N + eps);
 
     auto emit = [&](int c4, const v4f& v) {
-        if (OUT == kOutF32) {
+        if constexpr (OUT == kOutF32) {
             const v4f g = *reinterpret_cast<const v4f*>(static_cast<const float*>(gain_v) + 4 * c4);
             v4f o;
             #pragma unroll
             for (int j = 0; j < 4; ++j) o[j] = v[j] * inv * g[j];
             *reinterpret_cast<v4f*>(static_cast<float*>(out_row) + 4 * c4) = o;
         } else {
-            const __hip_bfloat16* g = static_cast<const __hip_bfloat16*>(gain_v) + 4 * c4;
-            __hip_bfloat16* o = static_cast<__hip_bfloat16*>(out_row) + 4 * c4;
+            const uint16_t* g = static_cast<const uint16_t*>(gain_v) + 4 * c4;
+            uint16_t* o = static_cast<uint16_t*>(out_row) + 4 * c4;
             #pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = __float2bfloat16(v[j] * inv * __bfloat162float(g[j]));
+            for (int j = 0; j < 4; ++j)
+                o[j] = (uint16_t)Store16<OUT>::bits(v[j] * inv * Store16<OUT>::to_f32(g[j]));
         }
     };
     #pragma unroll
@@ -98,7 +99,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     const int row = blockIdx.x;
     void* out_row = OUT == kOutF32
                         ? static_cast<void*>(static_cast<float*>(out_v) + (int64_t)row * N)
-                        : static_cast<void*>(static_cast<__hip_bfloat16*>(out_v) + (int64_t)row * N);
+                        : static_cast<void*>(static_cast<uint16_t*>(out_v) + (int64_t)row * N);
     rms_row<OUT>(in + (int64_t)row * N, nsplit, split_stride, gain_v, out_row, N, eps, red);
 }
 
@@ -145,12 +146,10 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
         const float e = rope_even(x.x, x.y, cs[i], sn[i]);
         const float o = rope_odd(x.x, x.y, cs[i], sn[i]);
         const int64_t dst = ((int64_t)bq * H + h) * rope + 2 * i;
-        if (OUT == kOutF32) {
+        if constexpr (OUT == kOutF32) {
             *reinterpret_cast<float2*>(static_cast<float*>(out_v) + dst) = make_float2(e, o);
         } else {
-            __hip_bfloat16* op = static_cast<__hip_bfloat16*>(out_v) + dst;
-            op[0] = __float2bfloat16(e);
-            op[1] = __float2bfloat16(o);
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(out_v) + dst) = Store16<OUT>::pack2(e, o);
         }
     }
 }
@@ -256,17 +255,17 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict_
         const float ang = rope_angle(pos, inv_freq[i]);
         const float c = cosf(ang), sn = sinf(ang);
         const float e = rope_even(x0, x1, c, sn), o = rope_odd(x0, x1, c, sn);
-        if (OUT == kOutF32) {
+        if constexpr (OUT == kOutF32) {
             float* dst = static_cast<float*>(pe) + crow * D + 2 * i;
             dst[0] = e; dst[1] = o;
         } else {
-            __hip_bfloat16* dst = static_cast<__hip_bfloat16*>(pe) + crow * D + 2 * i;
-            dst[0] = __float2bfloat16(e); dst[1] = __float2bfloat16(o);
+            *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(pe) + crow * D + 2 * i) =
+                Store16<OUT>::pack2(e, o);
         }
     }
     void* out_row = OUT == kOutF32
                         ? static_cast<void*>(static_cast<float*>(c_kv) + crow * R)
-                        : static_cast<void*>(static_cast<__hip_bfloat16*>(c_kv) + crow * R);
+                        : static_cast<void*>(static_cast<uint16_t*>(c_kv) + crow * R);
     rms_row<OUT>(base, nsplit, split_stride, gain, out_row, R, eps, red);
 }
 
@@ -300,8 +299,11 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, con
     if (out_type == kOutF32)
         hipLaunchKernelGGL(rmsnorm_kernel<kOutF32>, dim3(M), dim3(256), 0, stream, in, nsplit,
                            split_stride, gain, out, N, eps);
-    else
+    else if (out_type == kOutBF16)
         hipLaunchKernelGGL(rmsnorm_kernel<kOutBF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
+                           split_stride, gain, out, N, eps);
+    else
+        hipLaunchKernelGGL(rmsnorm_kernel<kOutF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
                            split_stride, gain, out, N, eps);
     return hipGetLastError();
 }
@@ -315,8 +317,11 @@ hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float
     if (out_type == kOutF32)
         hipLaunchKernelGGL(rope_kernel<kOutF32>, grid, dim3(256), 0, stream, q_raw, positions,
                            inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
-    else
+    else if (out_type == kOutBF16)
         hipLaunchKernelGGL(rope_kernel<kOutBF16>, grid, dim3(256), 0, stream, q_raw, positions,
+                           inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
+    else
+        hipLaunchKernelGGL(rope_kernel<kOutF16>, grid, dim3(256), 0, stream, q_raw, positions,
                            inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
     return hipGetLastError();
 }
@@ -353,8 +358,13 @@ hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, c
                            in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
                            D, start_row, cache_rows, pos_per_batch ? 1 : 0, block_table,
                            page_size, max_pages, eps);
-    else
+    else if (out_type == kOutBF16)
         hipLaunchKernelGGL(kv_append_kernel<kOutBF16>, dim3((unsigned)rows), dim3(256), 0, stream,
+                           in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
+                           D, start_row, cache_rows, pos_per_batch ? 1 : 0, block_table,
+                           page_size, max_pages, eps);
+    else
+        hipLaunchKernelGGL(kv_append_kernel<kOutF16>, dim3((unsigned)rows), dim3(256), 0, stream,
                            in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
                            D, start_row, cache_rows, pos_per_batch ? 1 : 0, block_table,
                            page_size, max_pages, eps);

@@ -5,10 +5,10 @@
 // (R+D)-deep reduction whose last D columns come from the second operand pair.
 //
 // Workgroup tile: 128 rows x 128 keys (one softmax partial).  Each of the 4 waves owns
-// 32 rows x 128 keys = 4 MFMA accumulator blocks (fp32 or bf16 steps, mma.h), so a row's 128 keys
+// 32 rows x 128 keys = 4 MFMA accumulator blocks (fp32 or 16-bit steps, mma.h), so a row's 128 keys
 // live in one wave: the row max and row sum need no LDS, only a 32-lane reduction
 // (DPP + ds_swizzle) of each accumulator register.  Depth is walked in 128-byte slices
-// (32 fp32 / 64 bf16) staged through double-buffered LDS, exactly like the GEMM engine.
+// (32 fp32 / 64 16-bit) staged through double-buffered LDS, exactly like the GEMM engine.
 //
 // Epilogue per row and 128-key tile j (mla_kernels.cu:971-1032 computes the same
 // quantities): m_j = max over visible keys of t = s/scale, p = exp(t - m_j) stored into
@@ -81,7 +81,7 @@ __device__ __forceinline__ TileId tile_id(const ScoresArgs& a, int t) {
 
 // PD = depth of the register prefetch ring: while slice s feeds the MFMAs from LDS, slices
 // s+1 .. s+PD are in flight from global memory.  fp32 is MFMA-bound with ~4K MFMA cycles
-// per slice and uses PD = 1; bf16 slices hold 8x less MFMA work and keep two slices in
+// per slice and uses PD = 1; 16-bit slices hold 8x less MFMA work and keep two slices in
 // flight (PD = 2).
 // PARTIAL: R or D is not a whole number of slices, so a slice's column chunks past the row
 // width must read as zeros (a per-load mask that whole slices do without).
@@ -329,7 +329,7 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
                           (int64_t)p.max_pages * p.page_size < p.Sk))
         return hipErrorInvalidValue;
     // every staging offset (a row of the 128-row tile) must stay below the buffer range
-    const int64_t row_bytes = (int64_t)std::max(p.R, p.D) * (p.bf16 ? 2 : 4);
+    const int64_t row_bytes = (int64_t)std::max(p.R, p.D) * (p.half ? 2 : 4);
     if (kBM * row_bytes >= kRsrcRange || (int64_t)kBM * p.ld_p * 4 >= kRsrcRange)
         return hipErrorInvalidValue;
     const int64_t tiles = (int64_t)p.B * a.tiles_r * a.P;
@@ -338,9 +338,12 @@ hipError_t launch_scores(const ScoresProblem& p, hipStream_t stream) {
     // two resident workgroups per CU (launch bounds and 74 KB of LDS each)
     const int64_t nblocks = std::min<int64_t>(tiles, 2 * kNumCUs);
     const dim3 grid((unsigned)nblocks), block(kThreads);
-    const int ks = p.bf16 ? 64 : 32;   // slice width
+    const int ks = p.half ? 64 : 32;   // slice width
     const bool partial = p.R % ks != 0 || p.D % ks != 0;
-    if (p.bf16) {
+    if (p.half && p.f16) {
+        if (partial) hipLaunchKernelGGL((scores_kernel<f16_t, 2, true>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((scores_kernel<f16_t, 2, false>), grid, block, 0, stream, a);
+    } else if (p.half) {
         if (partial) hipLaunchKernelGGL((scores_kernel<bf16_t, 2, true>), grid, block, 0, stream, a);
         else hipLaunchKernelGGL((scores_kernel<bf16_t, 2, false>), grid, block, 0, stream, a);
     } else {

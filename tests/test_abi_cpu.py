@@ -120,6 +120,17 @@ def test_gemm_validation(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "unknown dtype" in _err(lib)
 
 
+def test_fp16_is_a_storage_dtype(lib):
+    """MLA_DTYPE_F16 (2) passes the dtype check and takes the 16-bit row rule (multiples
+    of 8 elements), like bf16; the next code is still unknown."""
+    st = lib.mla_gemm(2, P16, P16, P16, 0, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "M must be positive" in _err(lib)
+    st = lib.mla_gemm(2, P16, P16, P16, 4, 20, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "multiple of 8 for fp16" in _err(lib)
+    st = lib.mla_gemm(3, P16, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "unknown dtype" in _err(lib)
+
+
 def test_gemm_split_needs_workspace(lib):
     need = lib.mla_gemm_workspace_bytes(F32, 1, 1536, 7168)
     assert need > 0, "B=1 2a1 is split over K"

@@ -41,7 +41,8 @@ def _layer(ext, g, W_uk, W_uv):
     return run
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["f32", "bf16", "f16"])
 @pytest.mark.parametrize("B,Sk", [(2, 300), (3, 1000)])
 def test_layer_graph_replay(ext, dtype, B, Sk):
     inp = R.make_inputs(B, 1, Sk, seed=B + Sk)

@@ -50,7 +50,7 @@ def kv_inputs(B, Sq, rows, seed, dtype=torch.float32, hidden=D.hidden):
     return [t.to(dtype) for t in (x, W, gain, ck, pe)]
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_split_wkv_b_is_exact(ext, dtype):
     g = torch.Generator().manual_seed(1)
     wkv_b = torch.randn(D.n_heads, D.nope + D.v, D.kv_rank, generator=g).to(dtype)
@@ -76,9 +76,10 @@ def test_kv_append_matches_oracle(ext, B, Sq, rows, start):
     assert torch.equal(got_c[:, keep], ck[:, keep]) and torch.equal(got_p[:, keep], pe[:, keep])
 
 
-def test_kv_append_bf16(ext):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_kv_append_16bit(ext, dtype):
     B, Sq, rows, start = 2, 3, 50, 10
-    x, W, gain, ck, pe = kv_inputs(B, Sq, rows, seed=5, dtype=torch.bfloat16)
+    x, W, gain, ck, pe = kv_inputs(B, Sq, rows, seed=5, dtype=dtype)
     pos = torch.arange(start, start + Sq)
     ck_g, pe_g = gpu(ck), gpu(pe)
     ext.kv_append(gpu(x), gpu(W), gpu(gain), gpu(pos), ck_g, pe_g, start, 1e-6)
@@ -138,12 +139,13 @@ def test_o_proj_matches_oracle(ext, B, Sq):
     torch.testing.assert_close(out[pick], ref, **TOL)
 
 
-def test_o_proj_bf16(ext):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_o_proj_16bit(ext, dtype):
     g = torch.Generator().manual_seed(3)
-    attn = torch.randn(4, 2, D.n_heads, D.v, generator=g).to(torch.bfloat16)
+    attn = torch.randn(4, 2, D.n_heads, D.v, generator=g).to(dtype)
     W_o = (torch.randn(D.n_heads * D.v, D.hidden, generator=g) /
-           math.sqrt(D.n_heads * D.v)).to(torch.bfloat16)
+           math.sqrt(D.n_heads * D.v)).to(dtype)
     out = ext.o_proj(gpu(attn), gpu(W_o))
-    assert out.dtype == torch.bfloat16
+    assert out.dtype == dtype
     ref = R.o_proj(attn.float(), W_o.float())
     torch.testing.assert_close(out.cpu().float(), ref, **TOL_BF16)

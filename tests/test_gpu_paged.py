@@ -106,7 +106,8 @@ def test_paged_equals_dense_bitwise(ext, monkeypatch, path):
     assert torch.equal(dense.cpu(), paged.cpu())
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
+                         ids=["f32", "bf16", "f16"])
 def test_paged_balanced_work_list(ext, dtype):
     """One long sequence among short ones: the fused pass's work list cuts the long one into
     many key chunks (merged per row) while the short ones are single chunks written
@@ -170,14 +171,15 @@ def test_paged_equal_short_lengths_equal_dense(ext):
 
 
 @PATHS
-def test_paged_attention_bf16(ext, monkeypatch, path):
-    """bf16 with the layer's scaling (q and W_uv ~ 1/sqrt(kv_rank)), so the outputs are
-    O(1) like the layer's and the bf16 tolerance is meaningful."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_paged_attention_16bit(ext, monkeypatch, path, dtype):
+    """16-bit storage with the layer's scaling (q and W_uv ~ 1/sqrt(kv_rank)), so the
+    outputs are O(1) like the layer's and the 16-bit tolerance is meaningful."""
     set_path(monkeypatch, path)
     lens, page = [700, 64, 1], 64
     qa, qr, ck, pe, table, sl, wuv = paged_inputs(3, 1, lens, page, 11, seed=9)
     s = 1 / math.sqrt(D.kv_rank)
-    qa, qr, ck, pe, wuv = [t.to(torch.bfloat16) for t in (qa * s, qr * s, ck, pe, wuv * s)]
+    qa, qr, ck, pe, wuv = [t.to(dtype) for t in (qa * s, qr * s, ck, pe, wuv * s)]
     out = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(table), gpu(sl),
                                   gpu(wuv), SCALE).float().cpu()
     f = lambda t: t.float()  # noqa: E731
