@@ -167,10 +167,21 @@ def measure(args, ext, dev, neighbours=True):
     eps = 1e-6
 
     causal = args.config == "cfg5"
+    fp8kv = args.kv_cache == "fp8"
+    if fp8kv:
+        # the layer's cache as fp8 e4m3 codes with one per-tensor scale (amax / 448); the
+        # per-step pass and the neighbours below keep the bf16 cache
+        if dname != "bf16":
+            raise SystemExit("--kv-cache fp8 needs bf16 queries (--dtype bf16 or cfg4)")
+        kv_scale = float(torch.maximum(g["c_kv"].abs().max(), g["pe_cache"].abs().max()).float()) / 448.0
+        ck_l = (g["c_kv"].float() / kv_scale).to(torch.float8_e4m3fn)
+        pe_l = (g["pe_cache"].float() / kv_scale).to(torch.float8_e4m3fn)
 
     def layer():
         qa, qr = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
                                 g["positions"], dims.nope, dims.rope, eps)
+        if fp8kv:
+            return ext.mla_attention_fp8kv(qa, qr, ck_l, pe_l, kv_scale, W_uv_d, scale, causal)
         # causal (cfg5) too: the fused pass streams the keys through its online softmax
         # and keeps no score matrix
         return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale, causal)
@@ -415,6 +426,15 @@ def measure(args, ext, dev, neighbours=True):
                     qa_b, qr_b, ck_pool, pe_pool, table, ragged, W_uv_d, scale),
                     fl_attn * keys_ragged / (B * Sk)),
             }
+            if dname == "bf16":
+                # the same attention over an fp8 (e4m3) copy of the cache, one per-tensor
+                # scale (amax / 448): half the cache bytes
+                kv_scale = float(torch.maximum(g["c_kv"].abs().max(),
+                                               g["pe_cache"].abs().max()).float()) / 448.0
+                ck8 = (g["c_kv"].float() / kv_scale).to(torch.float8_e4m3fn)
+                pe8 = (g["pe_cache"].float() / kv_scale).to(torch.float8_e4m3fn)
+                att_calls["attention_fp8kv"] = (lambda: ext.mla_attention_fp8kv(
+                    qa_b, qr_b, ck8, pe8, kv_scale, W_uv_d, scale), fl_attn)
             for name, (fn, fl) in att_calls.items():
                 for _ in range(3):
                     fn()
@@ -430,6 +450,9 @@ def measure(args, ext, dev, neighbours=True):
                             "tflops": round(fl / t / 1e12, 2), "bound": "mfma" if dname == "f32" else "hbm",
                             "mfma_pct": round(100 * fl / t / peak_mfma, 1)}
             nb["attention_paged_ragged"]["mean_keys"] = round(keys_ragged / B, 1)
+            if "attention_fp8kv" in nb:
+                nb["attention_fp8kv"]["cache_mbytes"] = round(B * Sk * (dims.kv_rank + dims.rope) / 1e6, 1)
+                del ck8, pe8
             del ck_pool, pe_pool
         else:
             # causal: the key-chunked entry point (bounded score workspace) beside the layer's
@@ -476,6 +499,7 @@ def measure(args, ext, dev, neighbours=True):
                         if args.config == "cfg2" and dname == "f32" else None),
         "vs_baseline_ref": "reference kernels, RTX A6000, 16.92 ms (README.md:367)",
         "dtype": dname,
+        "kv_cache": "fp8_e4m3" if fp8kv else dname,
         "data": "synthetic",
         "config": {"workload": desc, "B": B, "Sq": Sq, "Sk": Sk, "hidden": dims.hidden,
                    "heads": dims.n_heads, "q_lora": dims.q_lora, "kv_rank": dims.kv_rank,
@@ -517,6 +541,9 @@ def main():
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16", "f16"],
                     help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kv-cache", default="same", choices=["same", "fp8"],
+                    help="cache format of the timed layer: the storage dtype, or fp8 e4m3 with "
+                         "a per-tensor scale (bf16 queries only)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES, 3 times (calibrates the "

@@ -132,6 +132,25 @@ int mla_attention_noalloc(mla_dtype_t dtype, const mla_dims_t* dims,
                           const void* pe_cache, const void* W_uv, double scale, int causal,
                           void* out, hipStream_t stream);
 
+/* Attention over an fp8 KV cache (the cache-format row of the hot path's next steps; the
+ * reference keeps the cache in the query dtype, mla_kernels.cu:1489, 847-848).
+ *   c_kv_fp8 [B, Sk, kv_rank], pe_fp8 [B, Sk, rope]   uint8: OCP float8 e4m3 codes
+ *            (torch.float8_e4m3fn) of value / kv_scale, one scale for both
+ *   q_absorbed, q_rope, W_uv, out                    bf16 (dtype must be MLA_DTYPE_BF16)
+ * Result: mla_attention on the decoded cache (code * kv_scale), at bf16 accuracy.  The fused
+ * pass decodes the rows in LDS (e4m3 -> bf16 is exact) and applies kv_scale to the scores and
+ * the output.  kv_rank 512 and rope 64 only (MLA_ERR_UNSUPPORTED otherwise); the cache moves
+ * half the bytes of a bf16 cache. */
+size_t mla_attention_fp8kv_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                           int causal);
+int mla_attention_fp8kv(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                        const void* q_rope, const void* c_kv_fp8, const void* pe_fp8,
+                        float kv_scale, const void* W_uv, double scale, int causal, void* out,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream);
+/* The fp8 cache's decoder on its own: out[i] = e4m3 code[i] * scale (float32), through the
+ * same conversion the attention uses. */
+int mla_fp8_dequantize(const void* codes, int64_t n, float scale, float* out, hipStream_t stream);
+
 /* Attention over a long key range without materialising the [B*Sq*H, Sk] score matrix:
  * keys are processed in chunks of `key_chunk` (a multiple of mla_score_tile(); 0 = choose
  * so the per-chunk score buffer stays <= 1 GiB).  Each chunk runs 3a -> 3b -> 3c into a

@@ -208,6 +208,56 @@ torch::Tensor op_mla_attention(torch::Tensor q_absorbed, torch::Tensor q_rope, t
     return out;
 }
 
+// Attention over an fp8 cache: c_kv / pe_cache hold e4m3 codes (torch.float8_e4m3fn or
+// their bytes as uint8) of value / kv_scale; the queries, W_uv and the output are bf16.
+torch::Tensor op_mla_attention_fp8kv(torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                     torch::Tensor c_kv, torch::Tensor pe_cache, double kv_scale,
+                                     torch::Tensor W_uv, double scale, bool causal) {
+    mla_dims_t d = attn_dims(q_absorbed, q_rope, c_kv, pe_cache, &W_uv);
+    TORCH_CHECK(q_absorbed.scalar_type() == torch::kBFloat16,
+                "MLA: an fp8 cache is read with bfloat16 queries (q_absorbed has dtype ",
+                q_absorbed.scalar_type(), ")");
+    check_same_dtype(q_absorbed, q_rope, "q_rope");
+    check_same_dtype(q_absorbed, W_uv, "W_uv");
+    for (const torch::Tensor* t : {&c_kv, &pe_cache})
+        TORCH_CHECK(t->scalar_type() == torch::kFloat8_e4m3fn || t->scalar_type() == torch::kByte,
+                    "MLA: the fp8 cache must be float8_e4m3fn or uint8 codes (got ",
+                    t->scalar_type(), ")");
+    TORCH_CHECK(d.sk > 0, "MLA: c_kv must hold at least one key");
+    TORCH_CHECK(!causal || d.sk >= d.sq, "MLA: causal attention needs Sk >= Sq");
+    check_device({&q_absorbed, &q_rope, &c_kv, &pe_cache, &W_uv});
+
+    c10::DeviceGuard guard(q_absorbed.device());
+    auto qa = q_absorbed.contiguous();
+    auto qr = q_rope.contiguous();
+    auto ck = c_kv.contiguous();
+    auto pe = pe_cache.contiguous();
+    auto wuv = W_uv.contiguous();
+    auto out = torch::empty({d.batch, d.sq, d.heads, d.v}, qa.options());
+    const size_t wsb = mla_attention_fp8kv_workspace_bytes(MLA_DTYPE_BF16, &d, causal ? 1 : 0);
+    auto ws = workspace(wsb, qa);
+    check_status(mla_attention_fp8kv(MLA_DTYPE_BF16, &d, qa.data_ptr(), qr.data_ptr(),
+                                     ck.data_ptr(), pe.data_ptr(), (float)kv_scale,
+                                     wuv.data_ptr(), scale, causal ? 1 : 0, out.data_ptr(),
+                                     ws.data_ptr(), wsb, current_stream()),
+                 "mla_attention_fp8kv");
+    return out;
+}
+
+// e4m3 codes -> float32 values code * scale, with the attention's own conversion
+torch::Tensor op_fp8_dequantize(torch::Tensor codes, double scale) {
+    TORCH_CHECK(codes.scalar_type() == torch::kFloat8_e4m3fn || codes.scalar_type() == torch::kByte,
+                "MLA: codes must be float8_e4m3fn or uint8 (got ", codes.scalar_type(), ")");
+    check_device({&codes});
+    c10::DeviceGuard guard(codes.device());
+    auto c = codes.contiguous();
+    auto out = torch::empty(c.sizes(), c.options().dtype(torch::kFloat32));
+    check_status(mla_fp8_dequantize(c.data_ptr(), c.numel(), (float)scale, out.data_ptr<float>(),
+                                    current_stream()),
+                 "mla_fp8_dequantize");
+    return out;
+}
+
 // Same contract as mla_attention, with keys processed in bounded chunks (the score matrix
 // is never materialised whole); key_chunk = 0 picks the chunk so one chunk's fp32 score
 // buffer stays within 1 GiB.
@@ -720,6 +770,14 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Q path 2a1 -> 2a-n -> 2a2 -> 2b -> 2c: returns [q_absorbed, q_rope]",
           py::arg("x"), py::arg("W_q_a"), py::arg("q_norm_w"), py::arg("W_q_b"), py::arg("W_uk"),
           py::arg("positions"), py::arg("nope_dim"), py::arg("rope_dim"), py::arg("eps"));
+    m.def("mla_attention_fp8kv", &op_mla_attention_fp8kv,
+          "Attention over an fp8 e4m3 cache (codes of value / kv_scale; bf16 queries and "
+          "output): returns out [B, Sq, H, v]",
+          py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),
+          py::arg("kv_scale"), py::arg("W_uv"), py::arg("scale"), py::arg("causal") = false);
+    m.def("fp8_dequantize", &op_fp8_dequantize,
+          "e4m3 codes -> float32 code * scale, with the fused attention's conversion",
+          py::arg("codes"), py::arg("scale") = 1.0);
     m.def("mla_attention", &op_mla_attention,
           "Absorbed attention 3a -> 3b -> 3c -> 3d: returns out [B, Sq, H, v]",
           py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),

@@ -702,6 +702,51 @@ int scratch_for_stream(hipStream_t stream, void** out) {
     return MLA_OK;
 }
 
+// fp8 KV cache (mla_attention_fp8kv)
+
+struct Fp8Layout {
+    FlashPlan flash;
+    GemmPlan out;
+    size_t off_rowsum, off_ctx, off_out_ws, off_part, total;
+};
+
+FlashProblem fp8_problem(const mla_dims_t* d, const void* qa, const void* qr, const void* ckv,
+                         const void* pe, float kv_scale, double scale, int causal) {
+    FlashProblem p = flash_problem(MLA_DTYPE_BF16, d, qa, qr, ckv, pe, scale, causal);
+    p.fp8_kv = true;
+    p.kv_scale = kv_scale;
+    return p;
+}
+
+Fp8Layout fp8_layout(const mla_dims_t* d) {
+    Fp8Layout L;
+    const size_t rows = (size_t)d->batch * d->sq * d->heads;
+    L.flash = plan_flash(fp8_problem(d, nullptr, nullptr, nullptr, nullptr, 1.f, 1.0, 0));
+    L.out = plan_gemm(out_problem(MLA_DTYPE_BF16, d, nullptr, nullptr, nullptr, nullptr));
+    size_t o = 0;
+    L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
+    L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
+    L.off_out_ws = o; o = align_up(o + L.out.workspace_bytes);
+    L.off_part = o;   o = align_up(o + L.flash.partial_bytes);
+    L.total = o;
+    return L;
+}
+
+int check_fp8_attn(mla_dtype_t dtype, const mla_dims_t* dims, int causal, float kv_scale) {
+    if (dtype != MLA_DTYPE_BF16)
+        return fail(MLA_ERR_UNSUPPORTED, "an fp8 cache is read with bf16 queries (dtype %d)",
+                    (int)dtype);
+    MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    if (!(kv_scale > 0.f) || !std::isfinite(kv_scale))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "kv_scale must be positive and finite");
+    // the cache rows are bytes: the fused pass reads whole 16-byte chunks
+    if (dims->kv_rank % 16 != 0 || dims->rope % 16 != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 cache rows must be multiples of 16 bytes");
+    if (!flash_supported(fp8_problem(dims, nullptr, nullptr, nullptr, nullptr, kv_scale, 1.0, causal)))
+        return fail(MLA_ERR_UNSUPPORTED, "an fp8 cache needs kv_rank 512 and rope 64");
+    return MLA_OK;
+}
+
 }  // namespace
 
 // ====================================================================== C ABI
@@ -981,6 +1026,46 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
     // 3d
     GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
+    return ok();
+}
+
+// ------------------------------------------------------------------ fp8 KV cache
+
+size_t mla_attention_fp8kv_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal) {
+    if (!dims || check_fp8_attn(dtype, dims, causal, 1.f) != MLA_OK) return 0;
+    return fp8_layout(dims).total;
+}
+
+int mla_attention_fp8kv(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                        const void* q_rope, const void* c_kv_fp8, const void* pe_fp8,
+                        float kv_scale, const void* W_uv, double scale, int causal, void* out,
+                        void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_fp8_attn(dtype, dims, causal, kv_scale));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv_fp8, "c_kv_fp8"));
+    MLA_CHECK(check_ptr(pe_fp8, "pe_fp8"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const Fp8Layout L = fp8_layout(dims);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+    float* row_sum = at<float>(workspace, L.off_rowsum);
+    float* ctx = at<float>(workspace, L.off_ctx);
+    const FlashProblem fp = fp8_problem(dims, q_absorbed, q_rope, c_kv_fp8, pe_fp8, kv_scale,
+                                        scale, causal);
+    MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part), stream),
+                "fp8-cache attention launch");
+    GemmProblem op = out_problem(MLA_DTYPE_BF16, dims, ctx, row_sum, W_uv, out);
+    MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
+    return ok();
+}
+
+int mla_fp8_dequantize(const void* codes, int64_t n, float scale, float* out, hipStream_t stream) {
+    if (n < 0) return fail(MLA_ERR_INVALID_ARGUMENT, "n must not be negative (got %lld)", (long long)n);
+    if (n == 0) return ok();
+    if (!codes || !out) return fail(MLA_ERR_INVALID_ARGUMENT, "codes and out must not be NULL");
+    MLA_TRY_HIP(launch_fp8_dequant(codes, n, scale, out, stream), "fp8 dequantize launch");
     return ok();
 }
 

@@ -60,7 +60,8 @@ struct FlashArgs {
     float* l;          // [n_split][B*Sq*H]      row sum per split
     int B, Sq, Sk, H, n_split, keys_per_split, row_tiles;
     int64_t key_stride;
-    float c;           // log2(e) / scale
+    float c;           // log2(e) / scale (times kv_scale for an fp8 cache)
+    float o_scale;     // factor of the ctx rows written (kv_scale for an fp8 cache, else 1)
     int causal;
     // ragged / paged keys (both optional): batch b has min(seq_lens[b], Sk) keys, and its
     // key rows [j*page_size, (j+1)*page_size) are rows of page block_table[b*max_pages + j]
@@ -252,6 +253,7 @@ constexpr int k2Keys = 32;
 constexpr int k2LatStage = k2Keys * kLatBytes;            // 32 KB
 constexpr int k2PeStage = k2Keys * kPeBytes;              // 4 KB
 constexpr int k2Loads = 9;                                // cache loads per wave and block
+constexpr int k8Loads = 5;                                // (fp8 cache: 4 latent, 1 rope)
 constexpr float k2Headroom = 64.f;                        // log2 units above a row's reference
 constexpr int k2MaxPasses = 8;
 
@@ -300,14 +302,19 @@ __device__ __forceinline__ void mfma16_v_last(v4u a, v4u b, v4f& c) {
         asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
 }
 
-template <int NS, typename TL>
+template <int NS, typename TL, bool FP8>
 __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     // P^T is rounded to TL: with bf16's 8 exponent bits a term may reach 2^64 over its
     // row's reference; fp16 stops at 65504, so there a term stays below 2^15
     constexpr float kHeadroom = Half<TL>::kF16 ? 15.f : k2Headroom;
-    static_assert(NS == 4, "stage offsets: stages 2-3 are stages 0-1 XOR 64 KB");
-    constexpr int kPeBase = NS * k2LatStage;                    // 128 KB
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[kPeBase + NS * k2PeStage];
+    static_assert(NS == (FP8 ? 3 : 4), "stage offsets: stage 2 (3) is stage 0 (1) XOR 64 KB");
+    static_assert(!FP8 || !Half<TL>::kF16, "an fp8 cache is read with bf16 queries");
+    constexpr int kPeBase = NS * k2LatStage;                    // 128 KB (fp8: 96 KB)
+    // fp8 cache: two stages of raw cache bytes, 5 KB per wave (4 KB latent, 512 B rope,
+    // 512 B that the rope load's idle lanes fill with zeros)
+    constexpr int kF8Base = kPeBase + NS * k2PeStage, kF8Wave = 5120, kF8Stage = 4 * kF8Wave;
+    constexpr int kLoads = FP8 ? k8Loads : k2Loads;             // cache loads per wave and block
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kF8Base + (FP8 ? 2 * kF8Stage : 0)];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // a scalar from here on
     const int rt = wave >> 1, kh = wave & 1;
@@ -371,21 +378,79 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     // the MFMAs of a step: issued back to back by all four waves they queue in the CU's
     // address unit and stall the MFMA stream behind them.
     struct Loads { v4i rk, rp; uint32_t st, st_pe; };
+    // (fp8 cache: the raw rows, R and D bytes each, go to the wave's region of fp8 stage
+    // j & 1 unpermuted; the wave converts them into the bf16 ring itself, see below)
     auto loads_of = [&](int j) __attribute__((always_inline)) {
         const int stage = j % NS;
         const int kb = __builtin_amdgcn_readfirstlane(k_lo + k2Keys * j + 8 * wave);
         const uint32_t left = (uint32_t)max(0, min(8, k_hi_s - kb));
         Loads d;
-        d.st = __builtin_amdgcn_readfirstlane(lds0 + stage * k2LatStage + 8 * wave * kLatBytes);
-        d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + kPeBase + stage * k2PeStage + 8 * wave * kPeBytes);
         const uint64_t row0 = (uint64_t)flash_key_row(a, b, kb, k_hi_s);
-        d.rk = rsrc_span(ck_base + row0 * kLatBytes, 0, left * kLatBytes);
-        d.rp = rsrc_span(pe_base + row0 * kPeBytes, 0, left * kPeBytes);
+        if constexpr (FP8) {
+            d.st = __builtin_amdgcn_readfirstlane(lds0 + kF8Base + (j & 1) * kF8Stage + wave * kF8Wave);
+            d.st_pe = d.st + 8 * kFR;
+            d.rk = rsrc_span(ck_base + row0 * kFR, 0, left * kFR);
+            d.rp = rsrc_span(pe_base + row0 * kFD, 0, left * kFD);
+        } else {
+            d.st = __builtin_amdgcn_readfirstlane(lds0 + stage * k2LatStage + 8 * wave * kLatBytes);
+            d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + kPeBase + stage * k2PeStage + 8 * wave * kPeBytes);
+            d.rk = rsrc_span(ck_base + row0 * kLatBytes, 0, left * kLatBytes);
+            d.rp = rsrc_span(pe_base + row0 * kPeBytes, 0, left * kPeBytes);
+        }
         return d;
     };
+    const uint32_t pe8_lane = lane < 32 ? lane16 : kOob;   // 8 rope rows of 64 B: 32 lanes
     auto issue_one = [&](const Loads& d, int q) __attribute__((always_inline)) {
-        if (q < 8) dma16(d.rk, d.st + q * kLatBytes, lane16 ^ (16u * sw16((8 * wave + q) & 15)), q * kLatBytes);
-        else dma16(d.rp, d.st_pe, pe_lane, 0);
+        if constexpr (FP8) {
+            if (q < 4) dma16(d.rk, d.st + q * 1024, lane16, q * 1024);
+            else dma16(d.rp, d.st_pe, pe8_lane, 0);
+        } else {
+            if (q < 8) dma16(d.rk, d.st + q * kLatBytes, lane16 ^ (16u * sw16((8 * wave + q) & 15)), q * kLatBytes);
+            else dma16(d.rp, d.st_pe, pe_lane, 0);
+        }
+    };
+
+    // ---- fp8 cache: each wave converts the rows it loaded (keys 8w .. 8w+7 of a block) into
+    // the bf16 ring, in the layout the direct loads write.  Part q < 4 is one 16-byte read
+    // per lane: lane l holds bytes 16 (l % 32) .. +15 of key 2q + l/32, i.e. bf16 chunks
+    // c0 = 2 (l % 32) and c0 + 1 of that key; part 4 is the rope rows (lanes < 32: key l/4,
+    // chunks 2 (l % 4), +1).  OCP e4m3 -> bf16 is exact (v_cvt_scalef32_pk_bf16_fp8 with
+    // scale 1); the cache scale is applied to the scores and the output instead.  Since c0
+    // is even, chunk c0 + 1 sits at chunk c0's position XOR 16 bytes.
+    uint32_t cv_lat[4], cv_pe = 0;
+    if constexpr (FP8) {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int kw = 8 * wave + 2 * q + hw;
+            cv_lat[q] = kw * kLatBytes + 256u * ((lane & 31) >> 3) + 16u * ((2 * (lane & 7)) ^ sw16(kw & 15));
+        }
+        const int kwp = 8 * wave + ((lane >> 2) & 7);
+        cv_pe = kPeBase + kwp * kPeBytes + 16u * ((2 * (lane & 3)) ^ ((kwp >> 1) & 7));
+    }
+    auto f8_read = [&](int j, int q) __attribute__((always_inline)) {
+        const uint32_t off = kF8Base + (j & 1) * kF8Stage + wave * kF8Wave + (q < 4 ? 1024 * q : 8 * kFR) + lane16;
+        return *reinterpret_cast<const v4u*>(smem + off);
+    };
+    auto f8_write = [&](int j, int q, v4u raw) __attribute__((always_inline)) {
+        // bytes 0-1 (word_sel false) and 2-3 (true) of a dword to two bf16
+        auto lo2 = [](uint32_t w) __attribute__((always_inline)) {
+            return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false));
+        };
+        auto hi2 = [](uint32_t w) __attribute__((always_inline)) {
+            return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true));
+        };
+        const v4u c0 = {lo2(raw[0]), hi2(raw[0]), lo2(raw[1]), hi2(raw[1])};
+        const v4u c1 = {lo2(raw[2]), hi2(raw[2]), lo2(raw[3]), hi2(raw[3])};
+        const int st = j % NS;
+        if (q < 4) {
+            const uint32_t o = cv_lat[q] + (uint32_t)st * k2LatStage;
+            *reinterpret_cast<v4u*>(smem + o) = c0;
+            *reinterpret_cast<v4u*>(smem + (o ^ 16u)) = c1;
+        } else if (lane < 32) {
+            const uint32_t o = cv_pe + (uint32_t)st * k2PeStage;
+            *reinterpret_cast<v4u*>(smem + o) = c0;
+            *reinterpret_cast<v4u*>(smem + (o ^ 16u)) = c1;
+        }
     };
 
     // ---- per-lane LDS bases (byte offsets from smem); each read is base XOR a constant
@@ -501,8 +566,11 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     // whatever stage nb % NS holds, are all masked).
     auto step = [&](int j, auto has_prev) __attribute__((always_inline)) {
         constexpr bool PREV = decltype(has_prev)::value;
-        const Loads next = loads_of(j + NS - 2);   // scalar work, ahead of the barrier
-        wait_vm<k2Loads>();   // block j has landed; block j+1's loads may be in flight
+        const Loads next = loads_of(j + 2);   // scalar work, ahead of the barrier
+        if constexpr (FP8)
+            wait_vm<0>();         // block j+1's raw rows (loaded in step j-1) have landed
+        else
+            wait_vm<kLoads>();    // block j has landed; block j+1's loads may be in flight
         lds_barrier();   // block j is in LDS for every wave; every wave is past block j-2's P.V
 
         constexpr int kWin = 3;
@@ -523,6 +591,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
             pv(1);
         }
         Soft t;
+        v4u f8raw;
         #pragma unroll
         for (int s = 0; s < kQSteps; ++s) {
             const v4u cur = kf[s % kWin];
@@ -537,7 +606,15 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
                 mfma16_v<TL>(cur, qf[0][s], t.sc[0]);
                 mfma16_v_last<TL>(cur, qf[1][s], t.sc[1]);
             }
-            if (s % 2 == 0) issue_one(next, s / 2);
+            if constexpr (FP8) {
+                // block j+2's raw rows into the fp8 stage block j left; block j+1's into
+                // the bf16 stage block j-2 left, each part read a K step before it is written
+                if (s < kLoads) issue_one(next, s);
+                if (s >= 5 && s < 15 && (s & 1)) f8raw = f8_read(j + 1, (s - 5) / 2);
+                if (s >= 6 && s < 16 && !(s & 1)) f8_write(j + 1, (s - 6) / 2, f8raw);
+            } else {
+                if (s % 2 == 0) issue_one(next, s / 2);
+            }
             if constexpr (PREV) {
                 if (s % 3 == 0) pv(2 + s / 3);
             }
@@ -580,15 +657,20 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
         overflow = false;
         if (nb == 0) break;
         #pragma unroll
-        for (int j = 0; j < NS - 2; ++j) {
+        for (int j = 0; j < 2; ++j) {
             const Loads d = loads_of(j);
             #pragma unroll
-            for (int q = 0; q < k2Loads; ++q) issue_one(d, q);
+            for (int q = 0; q < kLoads; ++q) issue_one(d, q);
+        }
+        if constexpr (FP8) {   // block 0 into the bf16 ring before the first step
+            wait_vm<kLoads>();
+            #pragma unroll
+            for (int q = 0; q < kLoads; ++q) f8_write(0, q, f8_read(0, q));
         }
         step(0, std::false_type{});
         #pragma unroll 1
         for (int j = 1; j <= nb; ++j) step(j, std::true_type{});
-        wait_vm<0>();    // the zero loads of the two blocks past the end have landed
+        wait_vm<0>();    // the zero loads of the blocks past the end have landed
         lds_barrier();   // every wave is done with the ring
         if (lane == 0) flags[wave] = overflow ? 1 : 0;
         lds_barrier();
@@ -627,6 +709,8 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     const float fa = ma == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ma - M);
     const float fb = mb == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mb - M);
     const float lsum = mla[32 + l32] * fa + mlb[32 + l32] * fb;
+    // an fp8 cache's values are its codes times kv_scale: ctx takes the factor once here
+    const float oa_f = FP8 ? fa * a.o_scale : fa, ob_f = FP8 ? fb * a.o_scale : fb;
     if (rowO < rows_b) {
         const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + rowO;
         if (hw == 0) {
@@ -640,7 +724,7 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
             for (int q = 0; q < 4; ++q) {
                 const v4f ob = oreg[64 * (4 * cb + q)];
                 const v4f oa = {O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]};
-                *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) = oa * fa + ob * fb;
+                *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) = oa * oa_f + ob * ob_f;
             }
     }
 }
@@ -1162,6 +1246,8 @@ __global__ void __launch_bounds__(kWlThreads) flash_worklist_kernel(const int* _
 }  // namespace
 
 bool flash_supported(const FlashProblem& p) {
+    if (p.fp8_kv && !(p.half && !p.f16 && p.kv_scale > 0.f && std::isfinite(p.kv_scale)))
+        return false;   // an fp8 cache is read with bf16 queries and a positive scale
     return p.R == kFR && p.D == kFD && p.B > 0 && p.Sq > 0 && p.H > 0 && p.Sk > 0;
 }
 
@@ -1251,6 +1337,11 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     a.row_tiles = f.row_tiles;
     a.key_stride = p.key_stride > 0 ? p.key_stride : p.Sk;
     a.c = 1.4426950408889634f / p.scale;
+    a.o_scale = 1.f;
+    if (p.fp8_kv) {   // scores and ctx take the cache scale (the codes enter the MFMAs)
+        a.c *= p.kv_scale;
+        a.o_scale = p.kv_scale;
+    }
     a.causal = p.causal ? 1 : 0;
     a.seq_lens = p.seq_lens;
     a.block_table = p.block_table;
@@ -1262,10 +1353,12 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipError_t e = launch_flash_worklist(p, f, wl, stream);
         if (e != hipSuccess) return e;
     }
-    if (p.half && p.f16)
-        hipLaunchKernelGGL((flash16_kernel<kFStages, f16_t>), dim3(grid), dim3(kFThreads), 0, stream, a);
+    if (p.fp8_kv)
+        hipLaunchKernelGGL((flash16_kernel<3, bf16_t, true>), dim3(grid), dim3(kFThreads), 0, stream, a);
+    else if (p.half && p.f16)
+        hipLaunchKernelGGL((flash16_kernel<kFStages, f16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else if (p.half)
-        hipLaunchKernelGGL((flash16_kernel<kFStages, bf16_t>), dim3(grid), dim3(kFThreads), 0, stream, a);
+        hipLaunchKernelGGL((flash16_kernel<kFStages, bf16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();

@@ -89,6 +89,9 @@ hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, c
                             bool pos_per_batch = false, const int* block_table = nullptr,
                             int page_size = 0, int max_pages = 0);
 // Split each group of rows_a + rows_b rows (row_bytes each) of src into dst_a / dst_b.
+// out[i] = e4m3 code[i] * scale (the fused attention's own fp8 -> bf16 conversion, then fp32)
+hipError_t launch_fp8_dequant(const void* codes, int64_t n, float scale, float* out,
+                              hipStream_t stream);
 hipError_t launch_split_rows(const void* src, void* dst_a, void* dst_b, int64_t groups,
                              int rows_a, int rows_b, int64_t row_bytes, hipStream_t stream);
 
@@ -121,7 +124,8 @@ constexpr int kScoreTile = 128;  // keys per softmax partial (one 3a workgroup's
 
 // ---------------------------------------------------------------- 3a+3b+3c fused
 // One pass over the cache per key split: ctx [rows, R] (unnormalised) and row_sum [rows]
-// for 3d, as 3c and 3b produce them.  bf16 or fp32 storage, R = 512, D = 64 only.
+// for 3d, as 3c and 3b produce them.  16-bit or fp32 storage (or an fp8 cache with bf16
+// queries), R = 512, D = 64 only.
 struct FlashProblem {
     bool half = true;            // storage dtype 16-bit (else fp32)
     bool f16 = false;            // the 16-bit format is fp16 (else bfloat16)
@@ -142,6 +146,10 @@ struct FlashProblem {
     int page_size = 0;
     bool ragged = false;         // plan for per-batch key counts (a size query sets this
                                  // without seq_lens; a launch with it needs seq_lens)
+    // fp8 cache (bf16 queries only): ckv / pe hold OCP e4m3 codes of value / kv_scale,
+    // one byte per element (rows of R and D bytes)
+    bool fp8_kv = false;
+    float kv_scale = 1.f;
 };
 struct FlashPlan {
     int row_tiles = 1;           // 64-row tiles per batch

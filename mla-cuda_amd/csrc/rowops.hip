@@ -269,6 +269,29 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict_
     rms_row<OUT>(base, nsplit, split_stride, gain, out_row, R, eps, red);
 }
 
+// ---- fp8 cache decoding: out[i] = code[i] * scale, OCP e4m3 codes, through the same
+// conversion the fused attention uses (v_cvt_scalef32_pk_bf16_fp8 with scale 1, exact for
+// every code, then bf16 -> fp32, then the fp32 product).  Thread t takes codes 4t .. 4t+3.
+__global__ void __launch_bounds__(256) fp8_dequant_kernel(const uint8_t* __restrict__ codes,
+                                                          int64_t n, float scale,
+                                                          float* __restrict__ out) {
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 4 * t < n;
+         t += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t i0 = 4 * t;
+        uint32_t w = 0;
+        #pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (i0 + k < n) w |= (uint32_t)codes[i0 + k] << (8 * k);
+        const uint32_t lo = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false));
+        const uint32_t hi = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true));
+        const float v[4] = {bf16_bits_to_f32(lo & 0xffffu), bf16_bits_to_f32(lo >> 16),
+                            bf16_bits_to_f32(hi & 0xffffu), bf16_bits_to_f32(hi >> 16)};
+        #pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (i0 + k < n) out[i0 + k] = v[k] * scale;
+    }
+}
+
 // ---- wkv_b split: row r of wkv_b [H, nope + v, R] goes to W_uk (j < nope) or W_uv.
 // One thread per 16-byte chunk; rows are whole chunks (R * element size % 16 == 0).
 __global__ void __launch_bounds__(256) split_rows_kernel(const v4u_t* __restrict__ src,
@@ -368,6 +391,16 @@ hipError_t launch_kv_append(const float* in, int nsplit, int64_t split_stride, c
                            in, nsplit, split_stride, gain, positions, inv_freq, c_kv, pe, Sq, R,
                            D, start_row, cache_rows, pos_per_batch ? 1 : 0, block_table,
                            page_size, max_pages, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_fp8_dequant(const void* codes, int64_t n, float scale, float* out,
+                              hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    const int64_t threads = (n + 3) / 4;
+    const int blocks = (int)std::min<int64_t>((threads + 255) / 256, 16 * kNumCUs);
+    hipLaunchKernelGGL(fp8_dequant_kernel, dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const uint8_t*>(codes), n, scale, out);
     return hipGetLastError();
 }
 

@@ -20,7 +20,9 @@ What it restates (reference = pgangwar-ucsd/mla-cuda):
 * the path's neighbours, which the reference names but does not implement: the KV-cache
   append (``kv_append``) and the output projection (``o_proj``);
 * a ragged, paged cache (``gather_pages``, ``mla_attention_paged``, ``prepare_q_ragged``,
-  ``kv_append_paged``): the same per-sequence math over keys found through a page table.
+  ``kv_append_paged``): the same per-sequence math over keys found through a page table;
+* an fp8 cache (``e4m3_values``, ``decode_e4m3``, ``mla_attention_fp8kv``): OCP float8
+  E4M3 codes of value / kv_scale, decoded and then the same attention in float32.
 
 Arithmetic runs in torch on the CPU, in float32 for float32/bfloat16/float16 inputs and in
 float64 for float64 inputs -- the reference's accumulate-dtype policy
@@ -461,3 +463,50 @@ def make_inputs(B: int, Sq: int, Sk: int, dims: MLADims = DSV3, seed: int = 0,
     inp["pe_cache"] = rn(B, Sk, d.rope)
     inp["positions"] = torch.arange(Sk - Sq, Sk, dtype=torch.int64)
     return inp
+
+
+# ---------------------------------------------------------------------------
+# fp8 (OCP E4M3) cache
+# ---------------------------------------------------------------------------
+
+
+def e4m3_values() -> torch.Tensor:
+    """The 256 values of the OCP 8-bit floating point format E4M3 (OCP "8-bit Floating Point
+    Specification (OFP8)" v1.0), indexed by code: sign bit 7, a 4-bit exponent with bias 7 in
+    bits 6-3, a 3-bit mantissa in bits 2-0.  Exponent field 0 holds the subnormals
+    m/8 * 2^-6; codes 0x7F and 0xFF are NaN; there are no infinities (the largest finite
+    magnitude is 448).  torch.float8_e4m3fn is this format."""
+    out = torch.empty(256, dtype=torch.float64)
+    for code in range(256):
+        sign = -1.0 if code & 0x80 else 1.0
+        e = (code >> 3) & 0xF
+        m = code & 0x7
+        if e == 0xF and m == 0x7:
+            out[code] = float("nan")
+        elif e == 0:
+            out[code] = sign * (m / 8.0) * 2.0 ** -6
+        else:
+            out[code] = sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+    return out.float()
+
+
+_E4M3 = None
+
+
+def decode_e4m3(codes: torch.Tensor, scale: float = 1.0) -> torch.Tensor:
+    """float32 values code * scale of a uint8 (or float8_e4m3fn) tensor of E4M3 codes."""
+    global _E4M3
+    if _E4M3 is None:
+        _E4M3 = e4m3_values()
+    if codes.dtype != torch.uint8:
+        codes = codes.view(torch.uint8)
+    return _E4M3[codes.long()] * scale
+
+
+def mla_attention_fp8kv(q_absorbed, q_rope, c_kv_codes, pe_codes, kv_scale: float, W_uv,
+                        scale: float, causal: bool = False):
+    """mla_attention_official on the decoded fp8 cache (code * kv_scale), in float32 on the
+    queries' and W_uv's values."""
+    return mla_attention_official(q_absorbed.float(), q_rope.float(),
+                                  decode_e4m3(c_kv_codes, kv_scale),
+                                  decode_e4m3(pe_codes, kv_scale), W_uv.float(), scale, causal)

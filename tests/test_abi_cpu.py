@@ -131,6 +131,21 @@ def test_fp16_is_a_storage_dtype(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "unknown dtype" in _err(lib)
 
 
+def test_fp8kv_validation(lib):
+    """The fp8-cache attention takes bf16 queries only and a positive finite kv_scale, and
+    sizes a workspace for the DeepSeek-V3 widths."""
+    dims = Dims(2, 1, 64, 7168, 1536, 128, 128, 64, 512, 128)
+    lib.mla_attention_fp8kv_workspace_bytes.restype = ctypes.c_size_t
+    assert lib.mla_attention_fp8kv_workspace_bytes(1, ctypes.byref(dims), 0) > 0
+    assert lib.mla_attention_fp8kv_workspace_bytes(0, ctypes.byref(dims), 0) == 0
+    call = lambda dt, s: lib.mla_attention_fp8kv(  # noqa: E731
+        dt, ctypes.byref(dims), P16, P16, P16, P16, ctypes.c_float(s), P16, ctypes.c_double(1.0),
+        0, P16, None, ctypes.c_size_t(0), None)
+    assert call(0, 1.0) == MLA_ERR_UNSUPPORTED and "bf16 queries" in _err(lib)
+    assert call(1, 0.0) == MLA_ERR_INVALID_ARGUMENT and "kv_scale" in _err(lib)
+    assert call(1, float("inf")) == MLA_ERR_INVALID_ARGUMENT
+
+
 def test_gemm_split_needs_workspace(lib):
     need = lib.mla_gemm_workspace_bytes(F32, 1, 1536, 7168)
     assert need > 0, "B=1 2a1 is split over K"

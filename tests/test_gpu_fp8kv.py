@@ -1,0 +1,109 @@
+"""GPU parity of attention over an fp8 KV cache (mla_attention_fp8kv).
+
+The cache holds OCP E4M3 codes (torch.float8_e4m3fn) of value / kv_scale; queries, W_uv and
+the output are bf16.  The oracle decodes the codes with its own restated E4M3 table
+(oracle/mla_ref.py e4m3_values, pinned against torch's float8_e4m3fn in test_oracle.py) and
+runs the attention in float32; the bf16 tolerance applies (rtol/atol 2e-2 on O(1) outputs).
+The decoder the kernel uses is checked on its own over all 256 codes.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import mla_ref as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+D = R.DSV3
+SCALE = math.sqrt(D.qk_head)
+BF = torch.bfloat16
+F8 = torch.float8_e4m3fn
+TOL = dict(rtol=2e-2, atol=2e-2)
+
+
+@pytest.fixture(scope="module")
+def ext():
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU")
+    import mla_custom_cuda
+    return mla_custom_cuda
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.375])
+def test_fp8_decoder_all_codes(ext, scale):
+    """The kernel's e4m3 -> bf16 -> fp32 decoding of every code equals the format's value
+    (NaN exactly at 0x7F and 0xFF), times the scale."""
+    codes = torch.arange(256, dtype=torch.uint8)
+    got = ext.fp8_dequantize(codes.to(DEV), scale).cpu()
+    want = R.e4m3_values() * scale
+    nan = torch.isnan(want)
+    assert torch.equal(torch.isnan(got), nan)
+    assert torch.equal(got[~nan], want[~nan])
+    # odd lengths take the tail path of the decoder
+    got7 = ext.fp8_dequantize(codes[:7].to(DEV), scale).cpu()
+    assert torch.equal(got7, want[:7])
+
+
+def fp8_inputs(B, Sq, Sk, seed):
+    """bf16 queries and W_uv scaled like the layer's (1/sqrt(kv_rank)), a N(0,1) cache
+    quantized with the per-tensor scale amax / 448."""
+    g = torch.Generator().manual_seed(seed)
+    s = 1 / math.sqrt(D.kv_rank)
+    qa = (torch.randn(B, Sq, D.n_heads, D.kv_rank, generator=g) * s).to(BF)
+    qr = (torch.randn(B, Sq, D.n_heads, D.rope, generator=g) * s).to(BF)
+    ck = torch.randn(B, Sk, D.kv_rank, generator=g)
+    pe = torch.randn(B, Sk, D.rope, generator=g)
+    wuv = (torch.randn(D.n_heads, D.v, D.kv_rank, generator=g) * s).to(BF)
+    kv_scale = float(max(ck.abs().max(), pe.abs().max())) / 448.0
+    return qa, qr, (ck / kv_scale).to(F8), (pe / kv_scale).to(F8), kv_scale, wuv
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", [(2, 1, 4989, False), (1, 1, 64, False),
+                                            (3, 2, 1000, False), (1, 8, 700, True),
+                                            (1, 1, 33, False), (5, 1, 2047, False)])
+def test_fp8kv_attention_matches_oracle(ext, B, Sq, Sk, causal):
+    qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(B, Sq, Sk, seed=B * 100 + Sk)
+    out = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale, wuv.to(DEV),
+                                  SCALE, causal).cpu()
+    assert out.dtype == BF and torch.isfinite(out.float()).all()
+    ref = R.mla_attention_fp8kv(qa, qr, ck, pe, kv_scale, wuv, SCALE, causal)
+    torch.testing.assert_close(out.float(), ref, **TOL)
+
+
+def test_fp8kv_uint8_codes_and_scale(ext):
+    """The cache may come as raw uint8 codes; the same codes under two scales give the
+    attention of the two decoded caches."""
+    qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(2, 1, 777, seed=5)
+    args = [t.to(DEV) for t in (qa, qr)]
+    for s in (kv_scale, 2.5 * kv_scale):
+        out = ext.mla_attention_fp8kv(*args, ck.view(torch.uint8).to(DEV),
+                                      pe.view(torch.uint8).to(DEV), s, wuv.to(DEV), SCALE).cpu()
+        ref = R.mla_attention_fp8kv(qa, qr, ck, pe, s, wuv, SCALE)
+        torch.testing.assert_close(out.float(), ref, **TOL)
+
+
+def test_fp8kv_b128_full_size(ext):
+    """B=128 decode at Sk=4989 (the bf16 configuration's shape) over an fp8 cache, every
+    sequence against the oracle."""
+    qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(128, 1, 4989, seed=0)
+    out = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale, wuv.to(DEV),
+                                  SCALE).cpu()
+    ref = R.mla_attention_fp8kv(qa, qr, ck, pe, kv_scale, wuv, SCALE)
+    torch.testing.assert_close(out.float(), ref, **TOL)
+
+
+def test_fp8kv_close_to_the_bf16_cache(ext):
+    """Against the bf16 path on the unquantized cache the fp8 cache costs only its own
+    rounding: the two outputs agree to a few percent of the output scale."""
+    qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(2, 1, 3000, seed=11)
+    out8 = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale,
+                                   wuv.to(DEV), SCALE).cpu().float()
+    ck16 = (ck.float() * kv_scale).to(BF)
+    pe16 = (pe.float() * kv_scale).to(BF)
+    out16 = ext.mla_attention(*(t.to(DEV) for t in (qa, qr, ck16, pe16, wuv)), SCALE).cpu().float()
+    assert (out8 - out16).abs().max() <= 2e-2 * out16.abs().max() + 2e-2

@@ -471,3 +471,57 @@ def test_prepare_q_ragged_planted_shared_row_is_caught():
     torch.testing.assert_close(good_qr, bqr, rtol=1e-10, atol=1e-11)
     bad_qa, bad_qr = _ragged_q(inp, pos[:1].expand(3, -1))
     assert (bad_qr - bqr).abs().max().item() > 1e-3
+
+
+# ---- fp8 (OCP E4M3) cache ---------------------------------------------------
+
+
+def test_e4m3_table_matches_torch_float8_e4m3fn():
+    """The restated E4M3 decode table equals torch's own float8_e4m3fn for every code (NaN
+    exactly at 0x7F and 0xFF), and spot values fixed by the format: 448 the largest,
+    2^-9 the smallest subnormal, 2^-6 the smallest normal."""
+    table = R.e4m3_values()
+    torch_vals = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    nan = torch.isnan(table)
+    assert torch.equal(nan, torch.isnan(torch_vals))
+    assert nan.nonzero().flatten().tolist() == [0x7F, 0xFF]
+    assert torch.equal(table[~nan], torch_vals[~nan])
+    assert table[0x7E] == 448.0 and table[0x01] == 2.0 ** -9 and table[0x08] == 2.0 ** -6
+    assert table[0x80] == 0.0 and math.copysign(1.0, table[0x80].item()) == -1.0
+
+
+def test_e4m3_rounding_is_nearest_even():
+    """torch's float8_e4m3fn conversion (how the tests build caches) rounds to the nearest
+    E4M3 value, ties to the even code, checked by brute force against the table."""
+    table = R.e4m3_values().double()
+    finite = ~torch.isnan(table)
+    grid, codes = table[finite], torch.arange(256)[finite]
+    g = torch.Generator().manual_seed(3)
+    x = torch.cat([torch.randn(4000, generator=g, dtype=torch.float64) * s for s in (0.01, 1, 50)])
+    # exact midpoints between neighbours, which must go to the even code
+    pos = torch.sort(grid[grid > 0]).values
+    x = torch.cat([x, (pos[:-1] + pos[1:]) / 2])
+    got = x.float().to(torch.float8_e4m3fn).view(torch.uint8).long()
+    dist = (x[:, None] - grid[None, :]).abs()
+    best = dist.min(dim=1).values
+    for i in range(len(x)):
+        cand = codes[dist[i] == best[i]].tolist()
+        want = cand[0] if len(cand) == 1 else [c for c in cand if c % 2 == 0][0]
+        assert got[i].item() == want or table[got[i]] == table[want], (x[i].item(), cand)
+
+
+def test_fp8kv_attention_is_attention_on_the_decoded_cache():
+    """mla_attention_fp8kv is mla_attention_official on code * kv_scale: a planted mistake
+    (decoding without the scale) is caught."""
+    g = torch.Generator().manual_seed(9)
+    B, Sq, Sk, H, Rk, Dr, V = 2, 1, 40, 4, 16, 8, 8
+    qa, qr = torch.randn(B, Sq, H, Rk, generator=g), torch.randn(B, Sq, H, Dr, generator=g)
+    ck = (torch.randn(B, Sk, Rk, generator=g) * 3).to(torch.float8_e4m3fn)
+    pe = torch.randn(B, Sk, Dr, generator=g).to(torch.float8_e4m3fn)
+    wuv = torch.randn(H, V, Rk, generator=g)
+    s = 0.25
+    got = R.mla_attention_fp8kv(qa, qr, ck, pe, s, wuv, 3.0)
+    ref = R.mla_attention_official(qa, qr, ck.float() * s, pe.float() * s, wuv, 3.0)
+    torch.testing.assert_close(got, ref, rtol=1e-6, atol=1e-6)
+    wrong = R.mla_attention_official(qa, qr, ck.float(), pe.float(), wuv, 3.0)
+    assert (got - wrong).abs().max() > 1e-2
