@@ -62,6 +62,187 @@ CONFIGS = {
 }
 
 
+# The reference's published scenario matrix (exhaustive_benchmark_suite.py:78-174; all
+# non-causal, fp32) with its RTX A6000 figures in ms (README.md:366-375: PyTorch baseline,
+# its fused CUDA path), and two prefill shapes it leaves out because their score matrix does
+# not fit a 48 GB card (:75-76), run here unpublished.
+#   name: (B, Sq, Sk, timed iterations, A6000 baseline ms, A6000 fused ms)
+SCENARIOS = {
+    "decode_single_user_long_ctx": (1, 1, 65536, 10, 1.91, 2.39),
+    "decode_serving_avg_ctx": (128, 1, 4989, 15, 14.27, 16.92),
+    "decode_serving_long_ctx": (128, 1, 8192, 15, 23.61, 26.55),
+    "decode_serving_high_batch": (256, 1, 2048, 15, 12.91, 15.06),
+    "decode_speculative_2tok": (64, 2, 512, 20, 2.59, 3.38),
+    "decode_speculative_4tok": (64, 4, 768, 20, 6.16, 7.53),
+    "decode_speculative_long_ctx": (132, 4, 4096, 10, 47.19, 54.90),
+    "prefill_chat_batch": (8, 512, 512, 20, 70.55, 87.32),
+    "prefill_chunk_2k": (1, 2048, 2048, 10, 94.15, 113.11),
+    "prefill_chunk_4k": (1, 4096, 4096, 10, 355.46, 417.61),
+    "prefill_chunk_8k": (1, 8192, 8192, 5, None, None),
+    "prefill_batch_2k": (16, 2048, 2048, 5, None, None),
+}
+
+
+def torch_layer(g, W_uk, W_uv, dims, scale, eps=1e-6, causal=False):
+    """The reference's PyTorch formulation of the layer (exhaustive_benchmark_suite.py:247-304:
+    two projections around an RMSNorm, per-head absorption, interleaved RoPE, a softmax over
+    the materialised scores) executed by torch on this GPU, its products on rocBLAS /
+    hipBLASLt: the same-GPU library baseline.  In 16-bit the batched products get contiguous
+    right operands (torch's batched 16-bit products have faulted on transposed views on this
+    stack)."""
+    import torch
+    x = g["x"]
+    B, Sq, _ = x.shape
+    H, nope, rope, R = dims.n_heads, dims.nope, dims.rope, dims.kv_rank
+    Sk = g["c_kv"].shape[1]
+    lat = torch.matmul(x, g["W_q_a"]).float()
+    lat = (lat * torch.rsqrt(lat.square().mean(-1, keepdim=True) + eps)).to(x.dtype) * g["q_norm_w"]
+    q = torch.matmul(lat, g["W_q_b"]).view(B, Sq, H, nope + rope)
+    q_nope = q[..., :nope].permute(2, 0, 1, 3).reshape(H, B * Sq, nope)
+    qa = torch.bmm(q_nope, W_uk).view(H, B, Sq, R).permute(1, 2, 0, 3).reshape(B, Sq * H, R)
+    inv = 1.0 / 10000 ** (torch.arange(0, rope, 2, device=x.device, dtype=torch.float32) / rope)
+    ang = torch.outer(g["positions"].float(), inv)
+    cos, sin = torch.cos(ang).view(1, Sq, 1, -1), torch.sin(ang).view(1, Sq, 1, -1)
+    qp = q[..., nope:].float()
+    ev, od = qp[..., 0::2], qp[..., 1::2]
+    qr = torch.stack((ev * cos - od * sin, ev * sin + od * cos), -1).flatten(-2)
+    qr = qr.to(x.dtype).reshape(B, Sq * H, rope)
+    kT, pT, wT = g["c_kv"].transpose(1, 2), g["pe_cache"].transpose(1, 2), W_uv.transpose(1, 2)
+    if x.dtype != torch.float32:
+        kT, pT, wT = kT.contiguous(), pT.contiguous(), wT.contiguous()
+    s = torch.bmm(qa, kT)
+    s.add_(torch.bmm(qr, pT)).div_(scale)
+    if causal:
+        vis = (torch.arange(Sk, device=x.device)[None, :]
+               <= torch.arange(Sk - Sq, Sk, device=x.device)[:, None])
+        s.view(B, Sq, H, Sk).masked_fill_(~vis[None, :, None, :], float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    del s
+    ctx = torch.bmm(p, g["c_kv"]).view(B, Sq, H, R).permute(2, 0, 1, 3).reshape(H, B * Sq, R)
+    out = torch.bmm(ctx, wT)
+    return out.view(H, B, Sq, -1).permute(1, 2, 0, 3)
+
+
+def time_flushed(fn, iters, warmup, flush):
+    """Mean ms of `iters` calls of fn, each preceded (outside its event pair) by a read of
+    `flush` that evicts the MALL and L2s, after `warmup` calls made the same way."""
+    import torch
+    for _ in range(warmup):
+        flush.sum()
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(iters)]
+    for e0, e1 in ev:
+        flush.sum()
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return statistics.mean(e0.elapsed_time(e1) for e0, e1 in ev)
+
+
+def graph_vs_eager(layer, out_ref, n, settle_s, marker=None):
+    """Capture `layer` in a HIP graph, replay it for `settle_s` seconds (the capture leaves the
+    GPU idle, and the clock dips for ~100 ms after an idle spell before it settles), check the
+    replay against `out_ref` bit for bit, then time two rounds of n eager layers back to back
+    followed by n replays; returns (eager µs, replay µs) per layer of the last round.
+    `marker`, a small device tensor, gets an in-place op before each timed region so a kernel
+    trace shows where each region starts."""
+    import torch
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = layer()
+    t0 = time.perf_counter()
+    while True:
+        for _ in range(10):
+            graph.replay()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= settle_s:
+            break
+    if not torch.equal(out_g, out_ref):
+        raise RuntimeError("graph replay differs from the eager layer")
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for _ in range(2):
+        if marker is not None:
+            marker.add_(1.0)
+        ev[0].record()
+        for _ in range(n):
+            layer()
+        ev[1].record()
+        if marker is not None:
+            marker.mul_(2.0)
+        ev[2].record()
+        for _ in range(n):
+            graph.replay()
+        ev[3].record()
+        torch.cuda.synchronize()
+    del graph, out_g
+    return ev[0].elapsed_time(ev[1]) / n * 1e3, ev[2].elapsed_time(ev[3]) / n * 1e3
+
+
+def in_layer_kernel_us(layer, flush, n):
+    """Each step's kernel time inside the real layer: n flush-then-layer iterations under
+    torch's profiler (kernel start and end from the GPU's own timestamps), the library's
+    kernels attributed to steps by launch order -- the layer launches its GEMMs in the order
+    2a1, 2a2, 2c, 3d, a split-K reduce right after its GEMM, RMSNorm (2a-n, which also sums
+    2a1's split partials) and RoPE (2b) between them, and the fused attention's kernels
+    (work list, pass, merge) as 3abc.  Returns {step: mean µs per layer} plus the layer's
+    span from its first kernel's start to its last kernel's end, or None if the profiler
+    records no kernels."""
+    import torch
+    from torch.profiler import ProfilerActivity, profile
+
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        for _ in range(n):
+            flush.sum()
+            layer()
+        torch.cuda.synchronize()
+    ks = []
+    for e in prof.events():
+        if e.device_type != torch.autograd.DeviceType.CUDA:
+            continue
+        ks.append((e.time_range.start, e.time_range.end, e.name))
+    ks.sort()
+    gemm_steps = ("2a1", "2a2", "2c", "3d")
+    tot = {}
+    spans = []
+    layers = 0
+    cur = None
+    for t0, t1, name in ks:
+        if not any(k in name for k in ("gemm_kernel", "split_reduce", "rmsnorm_kernel",
+                                        "rope_kernel", "flash")):
+            cur = None                # the flush between layers
+            continue
+        if cur is None:
+            cur = {"gemm": 0, "step": None, "t0": t0}
+            layers += 1
+            spans.append([t0, t1])
+        spans[-1][1] = t1
+        if "gemm_kernel" in name:
+            step = gemm_steps[min(cur["gemm"], 3)]
+            cur["gemm"] += 1
+        elif "split_reduce" in name:
+            step = cur["step"] or "2a1"
+        elif "rmsnorm" in name:
+            step = "2a-n"
+        elif "rope_kernel" in name:
+            step = "2b"
+        elif "flash" in name:
+            step = "3abc"
+        else:
+            step = "other"
+        cur["step"] = step
+        tot[step] = tot.get(step, 0.0) + (t1 - t0)
+    if not layers:
+        return None
+    out = {k: round(v / layers, 2) for k, v in tot.items()}
+    out["kernels_sum"] = round(sum(tot.values()) / layers, 2)
+    out["layer_span"] = round(sum(b - a for a, b in spans) / layers, 2)
+    out["layers"] = layers
+    return out
+
+
 def step_work(B, Sq, Sk, dims, e=4):
     """Algorithmic FLOPs and compulsory HBM bytes per step (each input read once, each
     output written once; fp32 intermediates).  FLOP formulas follow the reference's own
@@ -186,6 +367,20 @@ def measure(args, ext, dev, neighbours=True):
         # and keeps no score matrix
         return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv_d, scale, causal)
 
+    if args.graph_compare:
+        # only the graph-versus-eager comparison, 50 layers a region, with marker kernels
+        # between the regions for a kernel trace
+        out = layer()
+        torch.cuda.synchronize()
+        marker = torch.zeros(3, device=dev)
+        eager_us, graph_us = graph_vs_eager(layer, out, 50, args.settle, marker)
+        print(f"[bench] eager back to back {eager_us:.1f} µs/layer, graph replay "
+              f"{graph_us:.1f} µs/layer", file=sys.stderr, flush=True)
+        return {"graph_compare": args.config, "dtype": dname, "layers_per_region": 50,
+                "eager_b2b_us_per_step": round(eager_us, 2),
+                "graph_replay_us_per_step": round(graph_us, 2),
+                "config": {"workload": desc, "B": B, "Sq": Sq, "Sk": Sk}}
+
     # ---- timed region: the fused boundary calls.  Each timed layer is preceded by a 512 MB
     # device read outside its event pair, so no layer finds the previous one's weights or
     # cache in the 256 MB MALL or the L2s; value = mean over the layers (median beside it).
@@ -238,33 +433,49 @@ def measure(args, ext, dev, neighbours=True):
     end.record()
     torch.cuda.synchronize()
     b2b_us = round(start.elapsed_time(end) / args.steps * 1e3, 2)
+
+    # each step's kernel time inside the flushed layer (GPU timestamps, no events between
+    # the steps), for the fused path
+    in_layer = None
+    if (os.environ.get("MLA_ATTENTION_PATH") != "split" and not fp8kv):
+        try:
+            in_layer = in_layer_kernel_us(layer, flush, min(10, args.steps))
+        except Exception as e:   # the profiler is a measurement aid, not the product
+            print(f"[bench] in-layer kernel times unavailable ({e})", file=sys.stderr, flush=True)
+        if in_layer:
+            print("[bench] in-layer kernel µs: " + ", ".join(f"{k} {v}" for k, v in in_layer.items()),
+                  file=sys.stderr, flush=True)
+
+    # the same layer through torch on this GPU (the reference's PyTorch formulation,
+    # rocBLAS / hipBLASLt products), timed with the same flush-then-layer protocol
+    torch_same = None
+    if not fp8kv:
+        try:
+            def t_layer():
+                return torch_layer(g, W_uk_d, W_uv_d, dims, scale, eps, causal)
+            t_out = t_layer()
+            t_diff = (t_out.float() - out.float()).abs().max().item()
+            del t_out
+            t_ms = time_flushed(t_layer, args.steps, min(5, args.warmup), flush)
+            torch_same = {"us": round(t_ms * 1e3, 2),
+                          "torch_over_layer": round(t_ms / ms_per_step, 3),
+                          "max_abs_diff_vs_layer": t_diff}
+            print(f"[bench] torch formulation on this GPU: {t_ms * 1e3:.1f} µs "
+                  f"({t_ms / ms_per_step:.2f}x the layer)", file=sys.stderr, flush=True)
+        except torch.cuda.OutOfMemoryError:
+            torch_same = {"us": None, "note": "out of memory"}
+        torch.cuda.empty_cache()
     del flush
 
     # The same layer replayed from a HIP graph (captured once; every replay runs all of the
-    # layer's kernels), as a serving loop would launch it.  Reported beside the eager
-    # figure, which stays the headline: on this stack the replay runs a few percent slower
-    # than back-to-back eager launches once the GPU is the bottleneck.  The replay must
-    # reproduce the eager output bit for bit.
-    graph_us = None
+    # layer's kernels), as a serving loop would launch it, against eager launches back to
+    # back, both after the replays have settled the clock again.  The replay must reproduce
+    # the eager output bit for bit.
+    graph_us = b2b_settled_us = None
     try:
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            out_g = layer()
-        for _ in range(max(1, args.warmup)):
-            graph.replay()
-        torch.cuda.synchronize()
-        if not torch.equal(out_g, out):
-            raise RuntimeError("graph replay differs from the eager layer")
-        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        g0.record()
-        for _ in range(args.steps):
-            graph.replay()
-        g1.record()
-        torch.cuda.synchronize()
-        graph_us = round(g0.elapsed_time(g1) / args.steps * 1e3, 2)
-        print(f"[bench] fused layer, graph replay: {graph_us:.1f} µs/step", file=sys.stderr,
-              flush=True)
-        del graph, out_g
+        b2b_settled_us, graph_us = graph_vs_eager(layer, out, args.steps, args.settle)
+        print(f"[bench] fused layer, graph replay: {graph_us:.1f} µs/step (eager back to back "
+              f"{b2b_settled_us:.1f})", file=sys.stderr, flush=True)
     except RuntimeError as e:
         print(f"[bench] graph replay unavailable ({e})", file=sys.stderr, flush=True)
 
@@ -353,6 +564,21 @@ def measure(args, ext, dev, neighbours=True):
     except (OSError, ValueError):
         traffic = None
     roofline.update({"traffic": traffic, "algorithmic_flop": fl, "algorithmic_bytes": by})
+
+    in_layer_steps = None
+    if in_layer:
+        in_layer_steps = {}
+        for n in ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d"):
+            if n not in in_layer:
+                continue
+            fl, by = work[n]
+            t = in_layer[n] * 1e-6
+            in_layer_steps[n] = {"us": in_layer[n], "tflops": round(fl / t / 1e12, 2),
+                                 "gbps": round(by / t / 1e9, 1),
+                                 "mfma_pct": round(100 * fl / t / peak_mfma, 1),
+                                 "hbm_pct": round(100 * by / t / PEAK_HBM, 1)}
+        in_layer_steps["kernels_sum_us"] = in_layer["kernels_sum"]
+        in_layer_steps["layer_span_us"] = in_layer["layer_span"]
 
     nb = {}
     if neighbours:
@@ -492,7 +718,9 @@ def measure(args, ext, dev, neighbours=True):
         "median_us_per_step": round(ms_median * 1e3, 2),
         "min_max_us_per_step": [round(min(layer_ms) * 1e3, 2), round(max(layer_ms) * 1e3, 2)],
         "back_to_back_us_per_step": b2b_us,
-        "graph_replay_us_per_step": graph_us,
+        "graph_replay_us_per_step": None if graph_us is None else round(graph_us, 2),
+        "graph_vs_eager_b2b_us_per_step": (None if b2b_settled_us is None
+                                           else round(b2b_settled_us, 2)),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": (round(value_us / REF_A6000_US, 4)
@@ -506,12 +734,14 @@ def measure(args, ext, dev, neighbours=True):
                    "nope": dims.nope, "rope": dims.rope, "v": dims.v},
         "roofline": roofline,
         "steps_us": per_step,
+        "steps_in_layer_us": in_layer_steps,
         "per_step_sum_us": round(steps_sum, 2),
         "fused_path_sum_us": (round(sum(step_us[n] for n in ("2a1", "2a-n", "2a2", "2b", "2c",
                                                              "3abc", "3d")), 2)
                               if fused_attn else None),
         "per_step_vs_fused_max_abs": same,
         "neighbours": nb,
+        "torch_same_gpu": torch_same,
         "wall_s_timed": round(t_wall, 3),
     }
 
@@ -525,6 +755,97 @@ def measure(args, ext, dev, neighbours=True):
         rec["cpu_baseline"] = None
 
     return rec
+
+
+def suite(args, ext, dev):
+    """The reference's scenario matrix (SCENARIOS): per scenario the layer through the
+    drop-in calls (weights split once, as a serving process holds them) and the same layer
+    through torch on this GPU, both timed like the headline (flush read, then the layer
+    between events; the reference's own loop, exhaustive_benchmark_suite.py:410-427, flushes
+    with a 256 MB write and takes min(10, iters) warm-up calls, as here).  Each scenario first
+    checks the layer against the torch result with the reference's suite gate (:466-471).
+    Returns one JSON record."""
+    import torch
+    import mla_inputs
+
+    dims = mla_inputs.DEEPSEEK_V3
+    scale = math.sqrt(dims.qk_head)
+    flush = torch.zeros(512 << 18, dtype=torch.float32, device=dev)
+    names = args.suite_only.split(",") if args.suite_only else list(SCENARIOS)
+    rows = []
+    settled = False
+    for name in names:
+        B, Sq, Sk, iters, ref_base, ref_fused = SCENARIOS[name]
+        print(f"[suite] {name}: B={B} Sq={Sq} Sk={Sk}", file=sys.stderr, flush=True)
+        g = mla_inputs.make_inputs(B, Sq, Sk, seed=args.seed, device=dev)
+        W_uk = g["wkv_b"][:, :dims.nope, :].contiguous()
+        W_uv = g["wkv_b"][:, dims.nope:, :].contiguous()
+
+        def ours():
+            qa, qr = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk,
+                                    g["positions"], dims.nope, dims.rope, 1e-6)
+            return ext.mla_attention(qa, qr, g["c_kv"], g["pe_cache"], W_uv, scale)
+
+        def base():
+            return torch_layer(g, W_uk, W_uv, dims, scale)
+
+        if not settled:
+            t0 = time.perf_counter()
+            while time.perf_counter() - t0 < args.settle:
+                flush.sum()
+                ours()
+                torch.cuda.synchronize()
+            settled = True
+        o = ours()
+        try:
+            b = base()
+        except torch.cuda.OutOfMemoryError:
+            b = None
+        row = {"scenario": name, "phase": "prefill" if Sq > 4 else "decode",
+               "B": B, "Sq": Sq, "Sk": Sk, "iters": iters}
+        if b is not None:
+            tol = dict(rtol=3e-2, atol=3e-2)
+            if Sk > 2048:
+                tol = dict(rtol=5e-2, atol=max(3e-2, 3e-5 * Sk))
+            row["max_abs_diff_vs_torch"] = (o - b).abs().max().item()
+            row["max_abs_torch"] = b.abs().max().item()
+            row["gate_pass"] = bool(torch.allclose(b, o, **tol))
+            del b
+        del o
+        torch.cuda.empty_cache()
+        ours_ms = time_flushed(ours, iters, min(10, iters), flush)
+        try:
+            base_ms = time_flushed(base, iters, min(10, iters), flush)
+        except torch.cuda.OutOfMemoryError:
+            base_ms = None
+        torch.cuda.empty_cache()
+        w = step_work(B, Sq, Sk, dims)
+        fl = sum(w[k][0] for k in ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d"))
+        row.update({"layer_ms": round(ours_ms, 4),
+                    "layer_tflops": round(fl / (ours_ms * 1e-3) / 1e12, 1),
+                    "layer_mfma_pct": round(100 * fl / (ours_ms * 1e-3) / PEAK_F32, 1),
+                    "torch_ms": None if base_ms is None else round(base_ms, 4),
+                    "torch_over_layer": None if base_ms is None else round(base_ms / ours_ms, 3),
+                    "a6000_baseline_ms": ref_base, "a6000_fused_ms": ref_fused,
+                    "a6000_fused_over_layer": (None if ref_fused is None
+                                               else round(ref_fused / ours_ms, 2))})
+        print(f"[suite]   layer {ours_ms:.3f} ms ({row['layer_mfma_pct']}% fp32 MFMA), torch "
+              f"{base_ms if base_ms is None else round(base_ms, 3)} ms, A6000 fused {ref_fused} ms",
+              file=sys.stderr, flush=True)
+        rows.append(row)
+        del g, W_uk, W_uv
+        torch.cuda.empty_cache()
+
+    def gmean(xs):
+        xs = [x for x in xs if x]
+        return round(math.exp(sum(math.log(x) for x in xs) / len(xs)), 3) if xs else None
+
+    return {"suite": "reference scenario matrix (exhaustive_benchmark_suite.py:78-174)",
+            "unit": "ms per layer", "dtype": "f32", "n_gpus": 1, "data": "synthetic",
+            "rows": rows,
+            "geomean_torch_over_layer": gmean([r["torch_over_layer"] for r in rows]),
+            "geomean_a6000_fused_over_layer": gmean([r["a6000_fused_over_layer"] for r in rows]),
+            "all_gates_pass": all(r.get("gate_pass", True) for r in rows)}
 
 
 def main():
@@ -545,6 +866,14 @@ def main():
                     help="cache format of the timed layer: the storage dtype, or fp8 e4m3 with "
                          "a per-tensor scale (bf16 queries only)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--graph-compare", action="store_true",
+                    help="only time eager back-to-back layers against HIP-graph replays of the "
+                         "same layer (after a settle), marker kernels between the regions")
+    ap.add_argument("--suite", action="store_true",
+                    help="run the reference's scenario matrix instead (fp32; the layer and "
+                         "torch's formulation on this GPU per scenario); one JSON line")
+    ap.add_argument("--suite-only", default="", metavar="NAMES",
+                    help="comma-separated scenario names for --suite (default: all)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES, 3 times (calibrates the "
                          "FETCH_SIZE / WRITE_SIZE counters against a known byte count)")
@@ -575,7 +904,13 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes": args.copy_probe}), flush=True)
         return
+    if args.suite:
+        print(json.dumps(suite(args, ext, dev)), flush=True)
+        return
     rec = measure(args, ext, dev)
+    if args.graph_compare:
+        print(json.dumps(rec), flush=True)
+        return
     if args.config == "cfg2" and (args.dtype or "f32") == "f32" and not args.no_bf16_line:
         # the bf16 decode (cfg4) beside the headline fp32 one: its layer time and the fused
         # attention's roofline, measured the same way (neighbours and CPU baseline left out)

@@ -14,7 +14,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
-from typing import Dict
+from typing import Dict, Optional
 
 import torch
 
@@ -38,11 +38,15 @@ DEEPSEEK_V3 = Dims()
 
 
 def make_inputs(B: int, Sq: int, Sk: int, dims: Dims = DEEPSEEK_V3, seed: int = 0,
-                dtype: torch.dtype = torch.float32) -> Dict[str, torch.Tensor]:
-    g = torch.Generator().manual_seed(seed)
+                dtype: torch.dtype = torch.float32,
+                device: Optional[torch.device] = None) -> Dict[str, torch.Tensor]:
+    """With ``device`` the tensors are drawn there by that device's generator (same
+    distributions and order, different values): fast set-up of large shapes for timing."""
+    g = torch.Generator(device=device) if device is not None else torch.Generator()
+    g.manual_seed(seed)
 
     def normal(*shape, std=1.0):
-        t = torch.randn(*shape, generator=g, dtype=torch.float32)
+        t = torch.randn(*shape, generator=g, dtype=torch.float32, device=device)
         if std != 1.0:
             t.mul_(std)
         return t.to(dtype)
@@ -52,10 +56,10 @@ def make_inputs(B: int, Sq: int, Sk: int, dims: Dims = DEEPSEEK_V3, seed: int = 
         "x": normal(B, Sq, d.hidden),
         "W_q_a": normal(d.hidden, d.q_lora, std=1.0 / math.sqrt(d.hidden)),
     }
-    out["q_norm_w"] = (1.0 + 0.1 * torch.randn(d.q_lora, generator=g)).to(dtype)
+    out["q_norm_w"] = (1.0 + 0.1 * torch.randn(d.q_lora, generator=g, device=device)).to(dtype)
     out["W_q_b"] = normal(d.q_lora, d.n_heads * d.qk_head, std=1.0 / math.sqrt(d.q_lora))
     out["wkv_b"] = normal(d.n_heads, d.nope + d.v, d.kv_rank, std=1.0 / math.sqrt(d.kv_rank))
     out["c_kv"] = normal(B, Sk, d.kv_rank)
     out["pe_cache"] = normal(B, Sk, d.rope)
-    out["positions"] = torch.arange(Sk - Sq, Sk, dtype=torch.int64)
+    out["positions"] = torch.arange(Sk - Sq, Sk, dtype=torch.int64, device=device)
     return out
