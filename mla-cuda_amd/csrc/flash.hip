@@ -35,7 +35,9 @@
 #include <math.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
+#include <utility>
 
 namespace mla {
 
@@ -1022,6 +1024,292 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ fp32: key-split waves
+// The fp32 pass for batches too small to fill the chip with flash32_kernel's 64-row
+// workgroups.  Those need many key splits there, and their split partials outgrow the
+// cache (B=1, Sk=4989: 104 splits of 48 keys write 27 MB of partials, merged by a second
+// kernel, for an 11.5 MB cache).  Here a workgroup is 16 rows and its four waves split the
+// workgroup's keys (wave w: the w-th quarter of its 16-key blocks), so the same number of
+// workgroups needs a quarter of the splits.  Each wave runs on its own until its keys are
+// done: no LDS ring and no barrier in the loop, the cache read straight into registers.
+// At fp32 a block's MFMA work (144 + 128 16x16x4 MFMAs, ~8,700 cycles per wave) is long
+// against its 68 16-byte loads per lane (the 16 keys' K rows and V^T fragments, mostly L2
+// hits: the row tiles of one split are neighbours on one XCD), so 17 loads in flight hide
+// the latency.
+//   S^T[16 keys x 16 rows] = K . Q^T: load r < 32 of lane (l16, g) is key l16's latent
+//     floats 16r + 4g .. +3 (4 MFMAs, one per float), loads 32..35 its rope floats 16r' +
+//     4g .. +3; the Q^T fragment of step r is the same depths of row l16, read from the
+//     workgroup's copy of its 16 query rows in LDS (the four waves share the rows), so the
+//     MFMAs sum the same products as a plain dot product.  Accumulator element v of lane l
+//     is key 4g + v of row l16.
+//   softmax as in flash32_kernel (fixed reference, 2^64 headroom); a wave whose row
+//     outgrows its reference repeats its own keys, the other waves are not involved
+//   O^T[512 x 16 rows] += V^T . P^T: load 36 + 8i + c is key 4g + i's columns 64c + 4 l16
+//     .. +3, four MFMAs with B = p[i] (A row l16 <-> column 64c + 4 l16 + q for O[c][q]);
+//     accumulator element v of O[c][q] is column 64c + 16g + 4v + q of row l16.
+// Load n of a block always lands in register slot n % 34 (68 = 2 x 34), and the first 34
+// loads of block j+1 are issued under block j's P.V MFMAs; loads past the wave's keys
+// read zeros (each block's buffer resource spans only the keys it has).  After the last
+// block the four waves' (m, l, O) merge through LDS (rescaled by 2^(m_w - max_w m_w), in
+// wave order), and the workgroup writes ctx / row_sum (one split) or its split's partial
+// slot, in flash32_kernel's layout, for flash_merge_kernel.
+template <int... I, class F>
+__device__ __forceinline__ void static_for_seq(std::integer_sequence<int, I...>, F&& f) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_seq(std::make_integer_sequence<int, N>{}, f);
+}
+
+constexpr int kWRows = 16;
+constexpr int kWKeys = 16;
+constexpr int kWLoads = 68;               // 16-byte loads per lane and block: 36 K, 32 V
+constexpr int kWWin = 34;                 // loads in flight
+constexpr int kWPitch = kFR + 4;          // floats per row of the LDS merge buffer
+// Q rows in LDS: 584 floats (2,336 bytes) apart, so that the 16-byte slot of lane (l16, g)'s
+// read is 2 l16 + g (mod 16) plus a constant: distinct within each 16-lane LDS cycle
+constexpr int kWQPitch = kFR + kFD + 8;
+constexpr int kWQWin = 4;                 // Q^T fragment reads in flight
+static_assert(kWLoads % kWWin == 0, "a load's register slot is the same in every block");
+
+__global__ void __launch_bounds__(kFThreads, 1) flash32w_kernel(FlashArgs a) {
+    // the workgroup's 16 query rows during the pass, the four waves' states after it
+    __shared__ __attribute__((aligned(16))) float mo[4 * kWRows * kWPitch];
+    __shared__ float mm[4 * kWRows], ml[4 * kWRows];
+    static_assert(kWRows * kWQPitch <= 4 * kWRows * kWPitch, "Q rows fit the merge buffer");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4;
+
+    // workgroup -> (batch, split, 16-row tile); the row tiles of a split are consecutive
+    // logical workgroups, i.e. on one XCD
+    const int wg = xcd_logical_block(blockIdx.x, gridDim.x);
+    const int rt = wg % a.row_tiles;
+    const int sp = (wg / a.row_tiles) % a.n_split;
+    const int b = wg / (a.row_tiles * a.n_split);
+    const int rows_b = a.Sq * a.H;
+    const int r0 = rt * kWRows;
+    const int row = r0 + l16;
+
+    const int k_lo = sp * a.keys_per_split;
+    int k_hi = min(a.Sk, k_lo + a.keys_per_split);
+    int lim = k_hi - 1;
+    if (a.causal) {
+        lim = min(lim, a.Sk - a.Sq + min(row, rows_b - 1) / a.H);
+        k_hi = min(k_hi, a.Sk - a.Sq + min(r0 + kWRows - 1, rows_b - 1) / a.H + 1);
+    }
+    // this wave's blocks: a quarter of the workgroup's, contiguous
+    const int nblk = k_hi > k_lo ? (k_hi - k_lo + kWKeys - 1) / kWKeys : 0;
+    const int per = (nblk + 3) >> 2;
+    const int jw = min(nblk, wave * per);
+    const int nb = min(nblk, jw + per) - jw;
+    const int kw0 = k_lo + kWKeys * jw;
+    const int kw1 = min(k_hi, kw0 + kWKeys * nb);
+
+    // ---- the 16 query rows into LDS (latent then rope, kWQPitch floats apart): thread t
+    // copies 16-byte chunks t, t + 256, .. of the 16 x 144; rows past the batch are zeros
+    {
+        const __amdgpu_buffer_rsrc_t rq =
+            make_rsrc(reinterpret_cast<const float*>(a.qa) + (int64_t)b * rows_b * kFR);
+        const __amdgpu_buffer_rsrc_t rr =
+            make_rsrc(reinterpret_cast<const float*>(a.qr) + (int64_t)b * rows_b * kFD);
+        // (one descriptor per loop: a per-lane choice of descriptor would make the
+        // compiler loop over the lanes' distinct descriptors)
+        constexpr int kLatCh = kFR / 4, kPeCh = kFD / 4;   // 128 + 16 chunks per row
+        static_assert(kWRows * kLatCh % kFThreads == 0 && kWRows * kPeCh == kFThreads,
+                      "whole chunks per thread");
+        #pragma unroll
+        for (int i = 0; i < kWRows * kLatCh / kFThreads; ++i) {
+            const int e = tid + kFThreads * i;
+            const int qrow = e / kLatCh, ch = e % kLatCh;
+            const uint32_t mask = oob_mask(r0 + qrow, rows_b);
+            *reinterpret_cast<v4u*>(mo + qrow * kWQPitch + 4 * ch) =
+                load16(rq, ((uint32_t)(r0 + qrow) * (kFR * 4) + 16u * ch) | mask);
+        }
+        {
+            const int qrow = tid / kPeCh, ch = tid % kPeCh;
+            const uint32_t mask = oob_mask(r0 + qrow, rows_b);
+            *reinterpret_cast<v4u*>(mo + qrow * kWQPitch + kFR + 4 * ch) =
+                load16(rr, ((uint32_t)(r0 + qrow) * (kFD * 4) + 16u * ch) | mask);
+        }
+    }
+    __syncthreads();
+    // Q^T fragment of K step r: row l16's floats 16r + 4g .. +3 (rope at 512 + 16(r - 32))
+    const float* q_lane = mo + l16 * kWQPitch + 4 * g;
+    auto q_read = [&](int r) __attribute__((always_inline)) {
+        return *reinterpret_cast<const v4u*>(q_lane + 16 * r);
+    };
+
+    // ---- the cache: block jj's buffer resources span its keys inside [kw0, kw1)
+    const char* ck_b = reinterpret_cast<const char*>(a.ckv) + (int64_t)b * a.key_stride * (kFR * 4);
+    const char* pe_b = reinterpret_cast<const char*>(a.pe) + (int64_t)b * a.key_stride * (kFD * 4);
+    // (readfirstlane: the values are wave-uniform, and the compiler must know it, or it
+    // wraps every load in a loop over the lanes' distinct descriptors)
+    auto rsrc_u = [](const char* ptr, int bytes) __attribute__((always_inline)) {
+        const uint64_t v = reinterpret_cast<uint64_t>(ptr);
+        const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+        const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+        return __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
+            __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+    };
+    auto rs_k = [&](int jj) __attribute__((always_inline)) {
+        const int kb = kw0 + kWKeys * jj;
+        const int left = max(0, min(kWKeys, kw1 - kb));
+        return rsrc_u(ck_b + (int64_t)kb * (kFR * 4), left * (kFR * 4));
+    };
+    auto rs_p = [&](int jj) __attribute__((always_inline)) {
+        const int kb = kw0 + kWKeys * jj;
+        const int left = max(0, min(kWKeys, kw1 - kb));
+        return rsrc_u(pe_b + (int64_t)kb * (kFD * 4), left * (kFD * 4));
+    };
+    const uint32_t k_off = (uint32_t)l16 * (kFR * 4) + 16u * g;
+    const uint32_t p_off = (uint32_t)l16 * (kFD * 4) + 16u * g;
+    const uint32_t v_off = (uint32_t)(4 * g) * (kFR * 4) + 16u * l16;
+    auto load_n = [&](auto n_tag, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rp)
+        __attribute__((always_inline)) {
+        constexpr int n = decltype(n_tag)::value;
+        if constexpr (n < k32LatReads) return load16(rk, k_off + 64u * n);
+        else if constexpr (n < k32LatReads + k32PeReads)
+            return load16(rp, p_off + 64u * (n - k32LatReads));
+        else {
+            constexpr int i = (n - 36) >> 3, c = (n - 36) & 7;
+            return load16(rk, v_off + (uint32_t)(i * kFR * 4 + 256 * c));
+        }
+    };
+
+    v4f O[8][4];   // [c][q]
+    v4u buf[kWWin];
+    float m_ref = -INFINITY, m_neg = 0.f, thr = -INFINITY, l_run = 0.f;
+    for (int pass = 1;; ++pass) {
+        #pragma unroll
+        for (int c = 0; c < 8; ++c)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q) O[c][q] = v4f{};
+        l_run = 0.f;
+        {
+            const auto rk = rs_k(0);
+            const auto rp = rs_p(0);
+            static_for<kWWin>([&](auto n) { buf[n] = load_n(n, rk, rp); });
+        }
+        bool again = false;
+        for (int jj = 0; jj < nb; ++jj) {
+            const auto rk = rs_k(jj), rp = rs_p(jj), rk1 = rs_k(jj + 1), rp1 = rs_p(jj + 1);
+            v4f s2[2] = {v4f{}, v4f{}};
+            float p[4];
+            v4u qb[kWQWin];
+            #pragma unroll
+            for (int r = 0; r < kWQWin; ++r) qb[r] = q_read(r);
+            static_for<kWLoads>([&](auto n_tag) {
+                constexpr int n = decltype(n_tag)::value;
+                constexpr int slot = n % kWWin;
+                const v4u cur = buf[slot];
+                if constexpr (n < k32LatReads + k32PeReads) {
+                    const v4u qv = qb[n % kWQWin];
+                    if constexpr (n + kWQWin < k32LatReads + k32PeReads) qb[n % kWQWin] = q_read(n + kWQWin);
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        s2[q & 1] = mfma16f(__uint_as_float(cur[q]), __uint_as_float(qv[q]), s2[q & 1]);
+                } else {
+                    constexpr int i = (n - 36) >> 3, c = (n - 36) & 7;
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        O[c][q] = mfma16f(__uint_as_float(cur[q]), p[i], O[c][q]);
+                }
+                if constexpr (n + kWWin < kWLoads)
+                    buf[slot] = load_n(std::integral_constant<int, n + kWWin>{}, rk, rp);
+                else
+                    buf[slot] = load_n(std::integral_constant<int, n + kWWin - kWLoads>{}, rk1, rp1);
+                // each step in program order: its four MFMAs, then the load kWWin ahead and
+                // the Q^T read kWQWin ahead (left alone, the scheduler sinks loads and reads
+                // to their uses and exposes their latency)
+                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (n == k32LatReads + k32PeReads - 1) {
+                    // softmax numerators of the block: element v of lane l is key kb + 4g + v
+                    // of row l16 (the mask is branch-free, so the score part stays one
+                    // scheduling region)
+                    v4f sc = s2[0] + s2[1];
+                    const int kb = kw0 + kWKeys * jj;
+                    #pragma unroll
+                    for (int v = 0; v < 4; ++v) sc[v] = kb + 4 * g + v <= lim ? sc[v] : -INFINITY;
+                    const float smax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                    if (__builtin_amdgcn_ballot_w64(!(smax * a.c <= thr))) {
+                        const float bm = row4_reduce(smax, OpMax{}) * a.c;
+                        const bool over = pass < k32MaxPasses && m_ref != -INFINITY && bm > thr;
+                        if (__builtin_amdgcn_ballot_w64(over)) again = true;
+                        if (m_ref == -INFINITY || over) {
+                            m_ref = bm;
+                            m_neg = bm == -INFINITY ? 0.f : -bm;
+                            thr = bm + k32Headroom;
+                        }
+                    }
+                    #pragma unroll
+                    for (int v = 0; v < 4; ++v)
+                        p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], a.c, m_neg));
+                    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+                }
+            });
+            if (again) break;
+        }
+        if (!again) break;
+    }
+
+    // ---- the four waves' states merge through LDS (over the query rows: every wave is
+    // past its last Q^T read first)
+    l_run = row4_reduce(l_run, OpSum{});
+    __syncthreads();
+    float* mow = mo + (wave * kWRows + l16) * kWPitch;
+    #pragma unroll
+    for (int c = 0; c < 8; ++c)
+        #pragma unroll
+        for (int v = 0; v < 4; ++v)
+            *reinterpret_cast<v4f*>(mow + 64 * c + 16 * g + 4 * v) =
+                v4f{O[c][0][v], O[c][1][v], O[c][2][v], O[c][3][v]};
+    if (g == 0) {
+        mm[wave * kWRows + l16] = m_ref;
+        ml[wave * kWRows + l16] = l_run;
+    }
+    __syncthreads();
+    // wave w writes columns 128w .. 128w+127: lane l has row l/4, 32 columns from 32 (l%4)
+    const int rr_ = lane >> 2;
+    const int cb = 128 * wave + 32 * (lane & 3);
+    float M = -INFINITY;
+    #pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, mm[w * kWRows + rr_]);
+    float f[4];
+    #pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float mw = mm[w * kWRows + rr_];
+        f[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - M);
+    }
+    v4f acc[8];
+    float L = 0.f;
+    #pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const float* src = mo + (w * kWRows + rr_) * kWPitch + cb;
+        #pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const v4f x = *reinterpret_cast<const v4f*>(src + 4 * k);
+            acc[k] = w == 0 ? f[0] * x : acc[k] + f[w] * x;
+        }
+        L = w == 0 ? f[0] * ml[rr_] : L + f[w] * ml[w * kWRows + rr_];
+    }
+    const int orow = r0 + rr_;
+    if (orow < rows_b) {
+        const bool direct = a.n_split == 1;
+        const int64_t slot = (direct ? (int64_t)b : (int64_t)sp * a.B + b) * rows_b + orow;
+        float* dst = (direct ? a.o_direct : a.o) + slot * kFR + cb;
+        #pragma unroll
+        for (int k = 0; k < 8; ++k) *reinterpret_cast<v4f*>(dst + 4 * k) = acc[k];
+        if (wave == 0 && (lane & 3) == 0) {
+            if (!direct) a.m[slot] = M;
+            (direct ? a.l_direct : a.l)[slot] = L;
+        }
+    }
+}
+
 constexpr int kFStages = 4;   // LDS ring depth
 
 // ctx = sum_s w_s O_s, row_sum = sum_s w_s l_s, w_s = 2^(m_s - max_s m_s).  One workgroup
@@ -1271,6 +1559,33 @@ FlashPlan plan_flash(const FlashProblem& p) {
         f.partial_bytes = wl_bytes + (size_t)f.max_items * rows_b * (kFR + 2) * sizeof(float);
         return f;
     }
+    // fp32 batches that would need key splits to fill the chip with 64-row workgroups may
+    // run on 16-row workgroups of key-split waves (flash32w_kernel): a quarter of the
+    // splits for as many workgroups.  Splits for about one workgroup per CU; each wave gets
+    // the same whole number of 16-key blocks, and the fewest splits that keep that number.
+    // Its fixed cost per launch is lower (less Q to load, a quarter of the split partials
+    // to write and merge) but a block costs it ~5.4 us against ~4.2 in the 64-row kernel,
+    // so it is taken up to 8 blocks per wave (measured at B=1: Sk 512 / 4989 / 16384 20.0 /
+    // 35.4 / 64.6 us against 25.2 / 46.8 / 75.4; B=2..4, Sk=4989: 47.2 / 63.5 / 75.0
+    // against 58.2 / 67.7 / 77.0; B=8: 129.9 against 119.0, 20 blocks per wave).
+    // MLA_FLASH32_WAVE=0 / 1 forces the choice (both kernels give the same results to
+    // rounding).
+    const char* wave_env = std::getenv("MLA_FLASH32_WAVE");
+    const bool wave_ok = !p.half && !p.fp8_kv && !p.block_table;
+    const int base16 = p.B * ((p.Sq * p.H + kWRows - 1) / kWRows);
+    const int wblocks = (p.Sk + kWKeys - 1) / kWKeys;
+    const int target = std::max(1, (kNumCUs + base16 / 2) / base16);
+    const int bpw = std::max(1, (wblocks + 4 * target - 1) / (4 * target));
+    constexpr int kWaveMaxBlocks = 8;
+    if (wave_ok && (wave_env ? wave_env[0] == '1' : base < kNumCUs && bpw <= kWaveMaxBlocks)) {
+        f.wave = true;
+        f.row_tiles = (p.Sq * p.H + kWRows - 1) / kWRows;
+        f.n_split = (wblocks + 4 * bpw - 1) / (4 * bpw);
+        f.keys_per_split = 4 * bpw * kWKeys;
+        f.partial_bytes = f.n_split > 1 ? rows * f.n_split * (kFR + 2) * sizeof(float)
+                                        : rows * sizeof(float);
+        return f;
+    }
     // about one workgroup per CU (the LDS ring admits one per CU), at least one key block
     // per split
     f.keys_per_split = dense_keys_per_split(p.Sk, base, block_keys);
@@ -1320,6 +1635,13 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         a.m = slots + (size_t)f.max_items * rows_b * kFR;
         a.l = a.m + (size_t)f.max_items * rows_b;
         grid = f.max_items * f.row_tiles;
+    } else if (f.wave) {
+        // the wave kernel writes ctx / row_sum itself with one split
+        a.o = partials;
+        a.m = partials + (size_t)f.n_split * rows * kFR;
+        a.l = a.m + (size_t)f.n_split * rows;
+        if (f.n_split == 1) a.m = a.l = a.o = nullptr;
+        grid = p.B * f.row_tiles * f.n_split;
     } else if (f.n_split > 1) {
         a.o = partials;
         a.m = partials + (size_t)f.n_split * rows * kFR;
@@ -1359,6 +1681,8 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipLaunchKernelGGL((flash16_kernel<kFStages, f16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else if (p.half)
         hipLaunchKernelGGL((flash16_kernel<kFStages, bf16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
+    else if (f.wave)
+        hipLaunchKernelGGL(flash32w_kernel, dim3(grid), dim3(kFThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();

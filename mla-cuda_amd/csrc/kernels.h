@@ -152,7 +152,8 @@ struct FlashProblem {
     float kv_scale = 1.f;
 };
 struct FlashPlan {
-    int row_tiles = 1;           // 64-row tiles per batch
+    bool wave = false;           // fp32 pass on 16-row workgroups of key-split waves
+    int row_tiles = 1;           // row tiles per batch (64 rows; 16 with `wave`)
     int n_split = 1;             // key splits (one workgroup each)
     int keys_per_split = 0;      // multiple of the key block
     bool balanced = false;       // ragged keys: a device-built work list of key chunks

@@ -123,13 +123,45 @@ def test_fused_rising_row_max(ext):
     torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOL)
 
 
+# fp32 runs on two kernels: 64-row workgroups (flash32_kernel) when the batch fills the
+# chip, 16-row workgroups of key-split waves (flash32w_kernel) when it would need key
+# splits; MLA_FLASH32_WAVE=0 / 1 forces either, and both must match the oracle everywhere
+FP32_KERNELS = pytest.mark.parametrize("wave", ["0", "1"], ids=["wg64", "wave16"])
+
+
+@FP32_KERNELS
+@pytest.mark.parametrize("B,Sq,Sk,H,causal", [
+    (1, 1, 1, 128, False), (1, 1, 17, 128, False), (1, 1, 4989, 128, False),
+    (8, 1, 4989, 128, False), (3, 2, 300, 128, True), (2, 16, 1000, 128, True),
+    (2, 3, 257, 40, False), (1, 512, 1024, 1, True), (40, 1, 700, 128, False),
+    (1, 1, 65, 128, False)])
+def test_fp32_kernels_vs_oracle(ext, monkeypatch, wave, B, Sq, Sk, H, causal):
+    monkeypatch.setenv("MLA_FLASH32_WAVE", wave)
+    args = inputs(B, Sq, Sk, H=H, seed=3 * Sk + B, dt=F32)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[F32])
+
+
+@FP32_KERNELS
+def test_fp32_kernels_full_size(ext, monkeypatch, wave):
+    """B=128, Sk=4989 on either kernel (the key-split waves at a full grid: no key split,
+    1,024 workgroups), every sequence against the oracle."""
+    monkeypatch.setenv("MLA_FLASH32_WAVE", wave)
+    args = inputs(128, 1, 4989, seed=77, dt=F32)
+    got = run(ext, args, False)
+    qa, qr, ck, pe, wuv = args
+    ref = R.mla_attention_official(qa, qr, ck, pe, wuv, SCALE)
+    torch.testing.assert_close(got, ref, **TOLS[F32])
+
+
+@FP32_KERNELS
 @pytest.mark.parametrize("jump", [100.0, 400.0])
-def test_fused_f32_restart(ext, jump):
+def test_fused_f32_restart(ext, monkeypatch, wave, jump):
     """fp32 keeps each row's exponentials against the first visible block's maximum; a
     row whose later maximum passes it by the 2^64 headroom restarts the pass.  Here the
     scores rise by `jump` (log2 units) over the keys in steps of ~0.35 per key, so the
     kernel restarts one (100) or several (400) times; a one-key spike at key 900 of
     another sequence restarts from a late block."""
+    monkeypatch.setenv("MLA_FLASH32_WAVE", wave)
     B, Sq, Sk = 2, 1, 1200
     qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=13, dt=F32)
     u = torch.randn(D.kv_rank, generator=torch.Generator().manual_seed(14))
