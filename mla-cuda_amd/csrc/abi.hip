@@ -579,13 +579,24 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
     MLA_TRY_HIP(launch_rmsnorm(lat_acc, nsplit, (int64_t)bq * dims->q_lora, q_norm_w, lat,
                                storage_out(dtype), bq, dims->q_lora, (float)eps, stream),
                 "2a-n launch");
-    // 2a2
+    // 2a2, then 2b.  A split-K 2a2 leaves its partials in its workspace and the RoPE kernel
+    // sums them (the nope columns into raw for 2c): no reduction launch.
     GemmProblem up = q_up_problem(dtype, dims, lat, W_q_b, raw);
-    MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
-    // 2b
-    MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch, dims->sq,
-                            dims->heads, dims->nope, dims->rope, stream, pos_per_batch),
-                "2b launch");
+    if (L.up.split > 1) {
+        float* up_parts = at<float>(workspace, L.off_up_ws);
+        MLA_TRY_HIP(launch_gemm_partials(up, L.up, up_parts, stream), "2a2 launch");
+        MLA_TRY_HIP(launch_rope(up_parts, positions, inv_freq, q_rope, storage_out(dtype),
+                                dims->batch, dims->sq, dims->heads, dims->nope, dims->rope,
+                                stream, pos_per_batch, L.up.split,
+                                (int64_t)bq * dims->heads * (dims->nope + dims->rope), raw),
+                    "2b launch");
+    } else {
+        MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
+        MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch,
+                                dims->sq, dims->heads, dims->nope, dims->rope, stream,
+                                pos_per_batch),
+                    "2b launch");
+    }
     // 2c
     GemmProblem ab = absorb_problem(dtype, dims, raw, W_uk, q_absorbed);
     MLA_TRY_HIP(launch_gemm(ab, L.absorb, at<void>(workspace, L.off_abs_ws), stream),

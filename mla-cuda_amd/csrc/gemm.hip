@@ -626,11 +626,11 @@ constexpr TunedPlan kTuned[] = {
     {1, 1536, 7168, 1, false, false, 32, 128, 16},
     {1, 24576, 1536, 1, false, false, 32, 128, 4},
     {1, 512, 128, 128, false, false, 32, 128, 1},
-    {1, 128, 512, 128, true, false, 32, 128, 2},
+    {1, 128, 512, 128, true, false, 32, 128, 1},
     {8, 1536, 7168, 1, false, false, 32, 128, 16},
     {8, 24576, 1536, 1, false, false, 32, 128, 4},
     {8, 512, 128, 128, false, false, 32, 128, 1},
-    {8, 128, 512, 128, true, false, 32, 128, 2},
+    {8, 128, 512, 128, true, false, 32, 128, 1},
     {32, 1536, 7168, 1, false, false, 32, 128, 16},
     {32, 24576, 1536, 1, false, false, 32, 128, 2},
     {32, 512, 128, 128, false, false, 32, 128, 1},

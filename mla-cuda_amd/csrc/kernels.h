@@ -63,9 +63,13 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride,
                           float eps, hipStream_t stream);
 // 2b
 // positions [Sq] shared by the batch, or [B*Sq] per sequence (pos_per_batch)
+// With nope_out, q_raw is 2a2's split-K partials ([nsplit][B*Sq][H*(nope+rope)],
+// split_stride floats apart): the kernel sums them in split order, writes the nope columns
+// to nope_out (same layout as q_raw) and rotates the summed rope columns.
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope,
-                       int rope, hipStream_t stream, bool pos_per_batch = false);
+                       int rope, hipStream_t stream, bool pos_per_batch = false, int nsplit = 1,
+                       int64_t split_stride = 0, float* nope_out = nullptr);
 // 3b (row_max may be null; when given it receives M = max_j m_part[row, j])
 hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
                           float* row_sum, float* row_max, int rows, int P, hipStream_t stream);

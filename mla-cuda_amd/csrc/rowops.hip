@@ -103,13 +103,20 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     rms_row<OUT>(in + (int64_t)row * N, nsplit, split_stride, gain_v, out_row, N, eps, red);
 }
 
-// ---- 2b: one workgroup per (query row bq, chunk of 32 heads).  Every head of a row uses
+// ---- 2b: one workgroup per (query row bq, chunk of 32 heads; 4 when it also sums 2a2's
+// split partials, below).  Every head of a row uses
 // the same rope/2 angles, so the workgroup evaluates them once into LDS: angle =
 // float(pos) * inv_freq[i] in fp32 with the caller's inv_freq table, then accurate
 // cosf/sinf (not the fast intrinsics: at positions ~5e3 an angle ulp is ~5e-4 rad and
 // large arguments need full range reduction).  Threads then rotate the (head, pair)
 // elements of the chunk with 64-bit loads and stores.
+// When 2a2 ran split-K, q_raw is its partials ([nsplit][rows][H*qk], split_stride apart)
+// and this kernel also does the split sum (in split order from 0, as split_reduce_kernel
+// does, so the result is the same to the bit): the nope columns of its heads go to
+// nope_out (for 2c), the rope columns are summed before the rotation.  That saves 2a2's
+// reduction launch at small batches.
 constexpr int kRopeHeads = 32;
+constexpr int kRopeSumHeads = 4;   // heads per workgroup when it also sums 2a2's partials
 constexpr int kRopeMaxHalf = 256;
 
 // Rotation of the interleaved pair (x0, x1) = (x[2i], x[2i+1]) by angle pos * inv_freq[i].
@@ -121,6 +128,8 @@ __device__ __forceinline__ float rope_odd(float x0, float x1, float c, float s) 
 
 template <int OUT>
 __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_raw,
+                                                   int nsplit, int64_t split_stride,
+                                                   float* __restrict__ nope_out,
                                                    const int64_t* __restrict__ positions,
                                                    const float* __restrict__ inv_freq,
                                                    void* out_v, int Sq, int H, int nope,
@@ -129,20 +138,39 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
     const int half = rope >> 1;
     const int qk = nope + rope;
     const int bq = blockIdx.x;
-    const int h0 = blockIdx.y * kRopeHeads;
-    const int nh = min(kRopeHeads, H - h0);
+    const int hpw = nope_out ? kRopeSumHeads : kRopeHeads;
+    const int h0 = blockIdx.y * hpw;
+    const int nh = min(hpw, H - h0);
     const int64_t pos = positions[pos_per_batch ? bq : bq % Sq];
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const float ang = rope_angle(pos, inv_freq[i]);
         cs[i] = cosf(ang);
         sn[i] = sinf(ang);
     }
+    const int64_t row0 = (int64_t)bq * H * qk;
+    if (nope_out) {
+        const int nq = nope >> 2;
+        for (int idx = threadIdx.x; idx < nh * nq; idx += blockDim.x) {
+            const int64_t off = row0 + (int64_t)(h0 + idx / nq) * qk + 4 * (idx % nq);
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int q = 0; q < nsplit; ++q) {
+                const float4 v = *reinterpret_cast<const float4*>(q_raw + q * split_stride + off);
+                acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+            }
+            *reinterpret_cast<float4*>(nope_out + off) = acc;
+        }
+    }
     __syncthreads();
-    const float* src = q_raw + (int64_t)bq * H * qk + nope;
+    const float* src = q_raw + row0 + nope;
     for (int idx = threadIdx.x; idx < nh * half; idx += blockDim.x) {
         const int h = h0 + idx / half;
         const int i = idx % half;
-        const float2 x = *reinterpret_cast<const float2*>(src + (int64_t)h * qk + 2 * i);
+        float2 x = make_float2(0.f, 0.f);
+        for (int q = 0; q < nsplit; ++q) {
+            const float2 v = *reinterpret_cast<const float2*>(src + q * split_stride + (int64_t)h * qk + 2 * i);
+            x.x += v.x;
+            x.y += v.y;
+        }
         const float e = rope_even(x.x, x.y, cs[i], sn[i]);
         const float o = rope_odd(x.x, x.y, cs[i], sn[i]);
         const int64_t dst = ((int64_t)bq * H + h) * rope + 2 * i;
@@ -333,18 +361,22 @@ hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, con
 
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope, int rope,
-                       hipStream_t stream, bool pos_per_batch) {
+                       hipStream_t stream, bool pos_per_batch, int nsplit, int64_t split_stride,
+                       float* nope_out) {
     if ((int64_t)B * Sq <= 0 || H <= 0) return hipSuccess;
-    if (rope / 2 > kRopeMaxHalf) return hipErrorInvalidValue;
-    const dim3 grid(B * Sq, (H + kRopeHeads - 1) / kRopeHeads);
+    if (rope / 2 > kRopeMaxHalf || nsplit < 1) return hipErrorInvalidValue;
+    if (nope_out && nope % 4 != 0) return hipErrorInvalidValue;   // float4 nope columns
+    // the split sum reads nsplit times the row's bytes: more, smaller workgroups
+    const int hpw = nope_out ? kRopeSumHeads : kRopeHeads;
+    const dim3 grid(B * Sq, (H + hpw - 1) / hpw);
     if (out_type == kOutF32)
-        hipLaunchKernelGGL(rope_kernel<kOutF32>, grid, dim3(256), 0, stream, q_raw, positions,
+        hipLaunchKernelGGL(rope_kernel<kOutF32>, grid, dim3(256), 0, stream, q_raw, nsplit, split_stride, nope_out, positions,
                            inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
     else if (out_type == kOutBF16)
-        hipLaunchKernelGGL(rope_kernel<kOutBF16>, grid, dim3(256), 0, stream, q_raw, positions,
+        hipLaunchKernelGGL(rope_kernel<kOutBF16>, grid, dim3(256), 0, stream, q_raw, nsplit, split_stride, nope_out, positions,
                            inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
     else
-        hipLaunchKernelGGL(rope_kernel<kOutF16>, grid, dim3(256), 0, stream, q_raw, positions,
+        hipLaunchKernelGGL(rope_kernel<kOutF16>, grid, dim3(256), 0, stream, q_raw, nsplit, split_stride, nope_out, positions,
                            inv_freq, q_rope, Sq, H, nope, rope, pos_per_batch ? 1 : 0);
     return hipGetLastError();
 }
