@@ -1587,8 +1587,12 @@ FlashPlan plan_flash(const FlashProblem& p) {
         return f;
     }
     // about one workgroup per CU (the LDS ring admits one per CU), at least one key block
-    // per split
+    // per split; MLA_FLASH_SPLITS=n forces n splits (for measurements)
     f.keys_per_split = dense_keys_per_split(p.Sk, base, block_keys);
+    if (const char* sp_env = std::getenv("MLA_FLASH_SPLITS")) {
+        const int n = std::atoi(sp_env);
+        if (n >= 1) f.keys_per_split = (blocks + std::min(n, blocks) - 1) / std::min(n, blocks) * block_keys;
+    }
     const int per = f.keys_per_split / block_keys;
     f.n_split = (blocks + per - 1) / per;
     // split partials (O, m, l); with one split O and l go straight to ctx / row_sum and

@@ -46,15 +46,46 @@ MLA_HD int wl_max_items(int B, int row_tiles) {
     return (kWlPerCu * kNumCUs / row_tiles + B + 1 + kNumXCDs - 1) / kNumXCDs * kNumXCDs;
 }
 
-// Keys per split of a dense batch of Sk keys: about one workgroup per CU for base =
-// B * row_tiles workgroups per split, at least one key block per split.  (Measured at B=1:
-// Sk=512 takes 25.0 us in 32 one-block splits against 33.0 us in 8 four-block ones; at
-// Sk=4989 the split size leaves the time unchanged.)
+// Keys per split of a dense batch of Sk keys, base = B * row_tiles workgroups per split.
+// Below one workgroup per CU: about one workgroup per CU, at least one key block per split.
+// (Measured at B=1: Sk=512 takes 25.0 us in 32 one-block splits against 33.0 us in 8
+// four-block ones; at Sk=4989 the split size leaves the time unchanged.)
+// From one workgroup per CU up, the rounds of workgroups set the time, and a base just
+// past a multiple of the CU count leaves the last round nearly empty (B=132 decode: 264
+// workgroups run as two rounds of one).  A split s of 1..4 is taken when its rounds of
+// shorter workgroups plus the merge of s partial rows cost less:
+//   ceil(base s / CUs) (ceil(blocks / s) + F)   block times,
+//   + rows s 2,056 bytes at ~5 TB/s in block times (rows = 64 base),
+// with a block ~4.2 us per workgroup and F = 4 in fp32 (16 keys), ~0.9 us and F = 20 in
+// 16-bit (32 keys; its queries, ring fill, key-half merge and fp32 partial rows weigh more
+// against the short blocks).  Both fitted to measured sweeps of s = 1..4 at B = 128..240,
+// Sq = 1 and B = 96, 132 at Sq = 4 (fp32 B = 132: 2,701 -> 1,743 us at s = 4; bf16 B = 200
+// stays at s = 1, 325 us against 380 at s = 3).  Integers, so the host planner and the
+// device's work list decide alike; a larger split must win by 3%.
 MLA_HD int dense_keys_per_split(int Sk, int base, int block_keys) {
     const int blocks = (Sk + block_keys - 1) / block_keys;
-    int split = (kNumCUs + base / 2) / base;
-    split = wl_min(wl_max(split, 1), blocks);
-    return (blocks + split - 1) / split * block_keys;
+    if (base < kNumCUs) {
+        int split = (kNumCUs + base / 2) / base;
+        split = wl_min(wl_max(split, 1), blocks);
+        return (blocks + split - 1) / split * block_keys;
+    }
+    // bytes the merge moves in one block time: 5e12 B/s x 4.2e-6 s (fp32), x 0.9e-6 s (16-bit)
+    const long long bytes_per_block = block_keys == 16 ? 21000000LL : 4500000LL;
+    const long long fixed = block_keys == 16 ? 4 : 20;
+    const long long rows = 64LL * base;
+    int best_s = 1;
+    long long best = -1;
+    for (int s = 1; s <= wl_min(4, blocks); ++s) {
+        const long long per = (blocks + s - 1) / s;
+        const long long rounds = ((long long)base * s + kNumCUs - 1) / kNumCUs;
+        long long cost = rounds * (per + fixed) * 1000;
+        if (s > 1) cost += rows * s * 2056LL * 1000 / bytes_per_block;
+        if (best < 0 || cost * 100 < best * 97) {
+            best = cost;
+            best_s = s;
+        }
+    }
+    return (blocks + best_s - 1) / best_s * block_keys;
 }
 
 // A sequence's key count as the kernels use it: seq_lens[b] clamped to [0, Sk] (Sk = the

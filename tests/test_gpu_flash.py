@@ -153,6 +153,16 @@ def test_fp32_kernels_full_size(ext, monkeypatch, wave):
     torch.testing.assert_close(got, ref, **TOLS[F32])
 
 
+@DTYPES
+@pytest.mark.parametrize("B,Sq,Sk", [(132, 1, 4989), (200, 1, 1000), (70, 4, 700)])
+def test_fused_key_split_past_one_round(ext, dt, B, Sq, Sk):
+    """Batches just past one workgroup per CU (264, 400 and 560 workgroups per split): the
+    planner splits the keys so that the last round is not nearly empty; every sequence
+    against the oracle."""
+    args = inputs(B, Sq, Sk, seed=B + Sk, dt=dt)
+    torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOLS[dt])
+
+
 @FP32_KERNELS
 @pytest.mark.parametrize("jump", [100.0, 400.0])
 def test_fused_f32_restart(ext, monkeypatch, wave, jump):
