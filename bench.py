@@ -187,7 +187,9 @@ def in_layer_kernel_us(layer, flush, n):
     kernels attributed to steps by launch order -- the layer launches its GEMMs in the order
     2a1, 2a2, 2c, 3d, a split-K reduce right after its GEMM, RMSNorm (2a-n, which also sums
     2a1's split partials) and RoPE (2b) between them, and the fused attention's kernels
-    (work list, pass, merge) as 3abc.  Returns {step: mean µs per layer} plus the layer's
+    (work list, pass, merge) as 3abc; at decode-sized fp32 batches 3d may be
+    out_small_kernel, which also does the pass's split merge.  Returns {step: mean µs per
+    layer} plus the layer's
     span from its first kernel's start to its last kernel's end, or None if the profiler
     records no kernels."""
     import torch
@@ -211,7 +213,7 @@ def in_layer_kernel_us(layer, flush, n):
     cur = None
     for t0, t1, name in ks:
         if not any(k in name for k in ("gemm_kernel", "split_reduce", "rmsnorm_kernel",
-                                        "rope_kernel", "flash")):
+                                        "rope_kernel", "flash", "out_small")):
             cur = None                # the flush between layers
             continue
         if cur is None:
@@ -230,6 +232,8 @@ def in_layer_kernel_us(layer, flush, n):
             step = "2b"
         elif "flash" in name:
             step = "3abc"
+        elif "out_small" in name:      # 3d with the attention's split merge folded in
+            step = "3d"
         else:
             step = "other"
         cur["step"] = step

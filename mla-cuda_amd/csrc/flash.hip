@@ -1614,8 +1614,19 @@ hipError_t launch_flash_worklist(const FlashProblem& p, const FlashPlan& f, int*
     return hipGetLastError();
 }
 
+FlashPartials flash_partials(const FlashProblem& p, const FlashPlan& f, const float* partials) {
+    const size_t rows = (size_t)p.B * p.Sq * p.H;
+    FlashPartials r{nullptr, nullptr, nullptr, f.balanced ? 0 : f.n_split};
+    if (!f.balanced && f.n_split > 1) {
+        r.o = partials;
+        r.m = partials + (size_t)f.n_split * rows * kFR;
+        r.l = r.m + (size_t)f.n_split * rows;
+    }
+    return r;
+}
+
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, float* row_sum,
-                        float* partials, hipStream_t stream) {
+                        float* partials, hipStream_t stream, bool merge) {
     const int rows = p.B * p.Sq * p.H;
     const int rows_b = p.Sq * p.H;
     FlashArgs a;
@@ -1691,6 +1702,7 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || (!f.balanced && f.n_split == 1)) return e;
+    if (!merge && !f.balanced) return e;   // the caller folds the merge in
     hipLaunchKernelGGL(flash_merge_kernel, dim3((unsigned)rows), dim3(256), 0, stream, a.o,
                        a.m, a.l, ctx, row_sum, p.B, rows_b, f.n_split, a.wl);
     return hipGetLastError();

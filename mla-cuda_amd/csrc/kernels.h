@@ -166,8 +166,25 @@ struct FlashPlan {
 };
 bool flash_supported(const FlashProblem& p);
 FlashPlan plan_flash(const FlashProblem& p);
+// merge = false leaves a split pass's partials unmerged (flash_partials() locates them)
+// for a consumer that folds the merge in (launch_out_small).
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& plan, float* ctx, float* row_sum,
-                        float* partials, hipStream_t stream);
+                        float* partials, hipStream_t stream, bool merge = true);
+// Where a dense (not balanced) pass leaves its state: n_split > 1 -> partial rows o
+// [n_split][rows][R], log2-domain references m and row sums l [n_split][rows] (slot
+// s * B * rows_b + row); n_split == 1 -> ctx / row_sum themselves.
+struct FlashPartials { const float* o; const float* m; const float* l; int n_split; };
+FlashPartials flash_partials(const FlashProblem& p, const FlashPlan& plan, const float* partials);
+// 3d for decode-sized fp32 batches (B*Sq <= kOutSmallRows, R = 512), with the fused
+// attention's split merge folded in: out[B*Sq][H][V] from the pass's state (fp.n_split > 1:
+// partials, else ctx / row_sum) and W_uv [H][V][R].
+constexpr int kOutSmallRows = 4;
+// Where it pays (measured): the rows of a head's merge, B*Sq*n_split, are what its two
+// workgroups per head read before the W_uv stream, so it is taken up to 32 of them.
+constexpr int kOutSmallMergeRows = 32;
+hipError_t launch_out_small(const FlashPartials& fp, const float* ctx, const float* row_sum,
+                            const float* W_uv, float* out, int B, int Sq, int H, int R, int V,
+                            hipStream_t stream);
 // The work list alone (plan.balanced, seq_lens given): wl receives flash_worklist_ints()
 // ints, laid out as worklist.h describes.
 int flash_worklist_ints(const FlashProblem& p, const FlashPlan& plan);

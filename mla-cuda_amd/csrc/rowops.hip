@@ -341,6 +341,150 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const v4u_t* __restrict
     }
 }
 
+
+// ---- 3d for decode-sized fp32 batches (M = B*Sq <= kOutSmallRows), with the fused
+// attention's key-split merge folded in.  Two workgroups per head, 64 output columns each.
+//   1. The head's M normalised ctx rows go to LDS: from a split pass's partials, wave w
+//      summing splits w, w+4, .. of every row (weights 2^(m_s - max_s m_s), lane: 8
+//      columns) and the four waves' sums added in wave order; from ctx / row_sum when the
+//      pass ran unsplit.  Then ctx_n = ctx / row_sum.
+//   2. The W_uv rows of the workgroup's columns (2 KB each, contiguous in K) stream once:
+//      each 16-lane group of a wave takes four rows (the lanes' 16-byte loads cover 256
+//      contiguous bytes per instruction), all in flight at once, against all M ctx rows:
+//      out[m][h][n] = sum_k ctx_n[m][k] W_uv[h][n][k], reduced over the 16 lanes with four
+//      DPP steps.
+// This replaces flash_merge_kernel plus the 3d GEMM, whose 32-row MFMA tile is 1/32 full at
+// M = 1 (4.2 MFLOP of tile work per head, ~6.8 us at one CU's fp32 MFMA rate).
+constexpr int kOutR = 512;
+constexpr int kOutCols = 64;   // output columns per workgroup
+
+template <class Op>
+__device__ __forceinline__ float row16_reduce(float v, Op op) {
+    v = op(v, dpp_move<0xB1>(v));   // lane ^ 1
+    v = op(v, dpp_move<0x4E>(v));   // lane ^ 2
+    v = op(v, dpp_move<0x141>(v));  // other quad of 8
+    return op(v, dpp_move<0x140>(v));   // other half of 16
+}
+
+__global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict__ o,
+                                                        const float* __restrict__ mpart,
+                                                        const float* __restrict__ lpart,
+                                                        int n_split,
+                                                        const float* __restrict__ ctx,
+                                                        const float* __restrict__ rs,
+                                                        const float* __restrict__ W,
+                                                        float* __restrict__ out, int B, int Sq,
+                                                        int H, int V) {
+    __shared__ __attribute__((aligned(16))) float part[4][kOutSmallRows][kOutR];
+    __shared__ float lsum[4][kOutSmallRows];
+    const int col_blocks = (V + kOutCols - 1) / kOutCols;
+    const int h = blockIdx.x / col_blocks, c0 = (blockIdx.x % col_blocks) * kOutCols;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int M = B * Sq, rows_b = Sq * H;
+    const int64_t step = (int64_t)B * rows_b;   // between a row's split slots
+    int64_t slot0[kOutSmallRows];
+    #pragma unroll
+    for (int mi = 0; mi < kOutSmallRows; ++mi)
+        slot0[mi] = mi < M ? (int64_t)(mi / Sq) * rows_b + (int64_t)(mi % Sq) * H + h : 0;
+    if (n_split > 1) {
+        float mx[kOutSmallRows];
+        v4f a0[kOutSmallRows], a1[kOutSmallRows];
+        float ls[kOutSmallRows];
+        #pragma unroll
+        for (int mi = 0; mi < kOutSmallRows; ++mi) {
+            mx[mi] = -INFINITY;
+            if (mi < M)
+                for (int s = lane; s < n_split; s += 64)
+                    mx[mi] = fmaxf(mx[mi], mpart[slot0[mi] + s * step]);
+            mx[mi] = wave_reduce(mx[mi], OpMax{});
+            a0[mi] = v4f{0.f, 0.f, 0.f, 0.f};
+            a1[mi] = a0[mi];
+            ls[mi] = 0.f;
+        }
+        #pragma unroll 2
+        for (int s = wave; s < n_split; s += 4) {
+            #pragma unroll
+            for (int mi = 0; mi < kOutSmallRows; ++mi) {
+                if (mi < M) {
+                    const int64_t slot = slot0[mi] + s * step;
+                    const float ms = mpart[slot];
+                    const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx[mi]);
+                    const v4f* src = reinterpret_cast<const v4f*>(o + slot * kOutR) + 2 * lane;
+                    a0[mi] += w * src[0];
+                    a1[mi] += w * src[1];
+                    ls[mi] += w * lpart[slot];
+                }
+            }
+        }
+        #pragma unroll
+        for (int mi = 0; mi < kOutSmallRows; ++mi) {
+            if (mi < M) {
+                *reinterpret_cast<v4f*>(&part[wave][mi][8 * lane]) = a0[mi];
+                *reinterpret_cast<v4f*>(&part[wave][mi][8 * lane + 4]) = a1[mi];
+                if (lane == 0) lsum[wave][mi] = ls[mi];
+            }
+        }
+        __syncthreads();
+        // wave w normalises rows w, w+4, .. (in place in part[0])
+        for (int mi = wave; mi < M; mi += 4) {
+            const float inv = 1.f / (((lsum[0][mi] + lsum[1][mi]) + lsum[2][mi]) + lsum[3][mi]);
+            #pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+                const int k = 8 * lane + 4 * jj;
+                const v4f x = ((*reinterpret_cast<const v4f*>(&part[0][mi][k]) +
+                                *reinterpret_cast<const v4f*>(&part[1][mi][k])) +
+                               *reinterpret_cast<const v4f*>(&part[2][mi][k])) +
+                              *reinterpret_cast<const v4f*>(&part[3][mi][k]);
+                *reinterpret_cast<v4f*>(&part[0][mi][k]) = x * inv;
+            }
+        }
+    } else {
+        for (int mi = wave; mi < M; mi += 4) {
+            const int64_t r = slot0[mi];
+            const float inv = 1.f / rs[r];
+            const v4f* src = reinterpret_cast<const v4f*>(ctx + r * kOutR) + 2 * lane;
+            *reinterpret_cast<v4f*>(&part[0][mi][8 * lane]) = src[0] * inv;
+            *reinterpret_cast<v4f*>(&part[0][mi][8 * lane + 4]) = src[1] * inv;
+        }
+    }
+    __syncthreads();
+    // 16-lane group grp of wave w takes columns c0 + 16 w + grp + 4 j, j = 0..3, all four
+    // rows in flight at once (128 KB per workgroup); lane li of the group holds floats
+    // 64 q + 4 li .. +3 (q = 0..7) of each row, and each ctx chunk read from LDS serves all
+    // four rows
+    const int grp = lane >> 4, li = lane & 15;
+    const float* Wh = W + (int64_t)h * V * kOutR;
+    v4f wv[4][8];
+    int nn[4];
+    #pragma unroll
+    for (int jr = 0; jr < 4; ++jr) {
+        nn[jr] = c0 + 16 * wave + grp + 4 * jr;
+        const v4f* wr = reinterpret_cast<const v4f*>(Wh + (int64_t)min(nn[jr], V - 1) * kOutR) + li;
+        #pragma unroll
+        for (int q = 0; q < 8; ++q) wv[jr][q] = wr[16 * q];
+    }
+    #pragma unroll
+    for (int mi = 0; mi < kOutSmallRows; ++mi) {
+        if (mi < M) {
+            v4f acc[4];
+            #pragma unroll
+            for (int jr = 0; jr < 4; ++jr) acc[jr] = v4f{0.f, 0.f, 0.f, 0.f};
+            #pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const v4f c = *reinterpret_cast<const v4f*>(&part[0][mi][64 * q + 4 * li]);
+                #pragma unroll
+                for (int jr = 0; jr < 4; ++jr) acc[jr] += wv[jr][q] * c;
+            }
+            #pragma unroll
+            for (int jr = 0; jr < 4; ++jr) {
+                const float sum = row16_reduce((acc[jr][0] + acc[jr][1]) + (acc[jr][2] + acc[jr][3]),
+                                               OpSum{});
+                if (li == 0 && nn[jr] < V) out[((int64_t)mi * H + h) * V + nn[jr]] = sum;
+            }
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, const void* gain,
@@ -446,6 +590,21 @@ hipError_t launch_split_rows(const void* src, void* dst_a, void* dst_b, int64_t 
     hipLaunchKernelGGL(split_rows_kernel, dim3(blocks), dim3(256), 0, stream,
                        static_cast<const v4u_t*>(src), static_cast<v4u_t*>(dst_a),
                        static_cast<v4u_t*>(dst_b), rows, rows_a, rows_a + rows_b, chunks);
+    return hipGetLastError();
+}
+
+
+hipError_t launch_out_small(const FlashPartials& fp, const float* ctx, const float* row_sum,
+                            const float* W_uv, float* out, int B, int Sq, int H, int R, int V,
+                            hipStream_t stream) {
+    const int M = B * Sq;
+    // each workgroup's 4 waves x 4 groups x 4 rows cover its kOutCols columns
+    static_assert(kOutCols == 4 * 4 * 4, "column coverage");
+    if (M < 1 || M > kOutSmallRows || R != kOutR || H <= 0 || V <= 0) return hipErrorInvalidValue;
+    if (fp.n_split > 1 ? !(fp.o && fp.m && fp.l) : !(ctx && row_sum)) return hipErrorInvalidValue;
+    const int col_blocks = (V + kOutCols - 1) / kOutCols;
+    hipLaunchKernelGGL(out_small_kernel, dim3(H * col_blocks), dim3(256), 0, stream, fp.o, fp.m, fp.l,
+                       fp.n_split, ctx, row_sum, W_uv, out, B, Sq, H, V);
     return hipGetLastError();
 }
 

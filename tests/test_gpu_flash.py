@@ -153,6 +153,21 @@ def test_fp32_kernels_full_size(ext, monkeypatch, wave):
     torch.testing.assert_close(got, ref, **TOLS[F32])
 
 
+@pytest.mark.parametrize("small", ["1", "0"], ids=["fused-3d", "gemm-3d"])
+@pytest.mark.parametrize("B,Sq,Sk,causal", [(1, 1, 4989, False), (3, 1, 4989, False),
+                                            (3, 1, 100, False), (1, 4, 700, True),
+                                            (1, 4, 64, True), (1, 1, 33, False),
+                                            (4, 1, 512, False)])
+def test_fp32_decode_3d_with_merge(ext, monkeypatch, small, B, Sq, Sk, causal):
+    """At B*Sq <= 4 (fp32) with few split rows to merge, mla_attention runs 3d on a kernel
+    that also merges the pass's key splits (or reads ctx / row_sum when the pass ran
+    unsplit: B=1, Sq=4, Sk=64); MLA_OUT_SMALL=0 keeps the merge kernel and the 3d GEMM.
+    Both against the oracle."""
+    monkeypatch.setenv("MLA_OUT_SMALL", small)
+    args = inputs(B, Sq, Sk, seed=5 * Sk + B, dt=F32)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[F32])
+
+
 @DTYPES
 @pytest.mark.parametrize("B,Sq,Sk", [(132, 1, 4989), (200, 1, 1000), (70, 4, 700)])
 def test_fused_key_split_past_one_round(ext, dt, B, Sq, Sk):
@@ -212,11 +227,12 @@ def test_fused_full_size_vs_split_path(ext, monkeypatch, dt):
 @DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,causal", [(2, 1, 300, False), (1, 1, 4989, False),
                                             (2, 4, 500, True)])
-def test_attn_ctx_step_vs_oracle(ext, dt, B, Sq, Sk, causal):
+def test_attn_ctx_step_vs_oracle(ext, monkeypatch, dt, B, Sq, Sk, causal):
     """The per-step fused entry point: ctx / row_sum equals the oracle's softmax-weighted
     c_kv (float64 reference on the values the kernel reads; bf16 P is rounded only in the
     kernel), and feeding (ctx, row_sum) to the 3d step gives mla_attention's output bit
-    for bit."""
+    for bit when mla_attention runs the same 3d GEMM (decode-sized fp32 batches otherwise
+    take 3d with the split merge folded in, equal to rounding)."""
     qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=3 * Sk + B, dt=dt)
     ctx, rs = ext.attn_ctx(gpu(qa), gpu(qr), gpu(ck), gpu(pe), SCALE, causal)
     assert ctx.dtype == torch.float32 and ctx.shape == (B, Sq, D.n_heads, D.kv_rank)
@@ -230,5 +246,8 @@ def test_attn_ctx_step_vs_oracle(ext, dt, B, Sq, Sk, causal):
     tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
     torch.testing.assert_close(got, ref, **tol)
     out = ext.out(ctx, rs, gpu(wuv))
+    own = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
+    monkeypatch.setenv("MLA_OUT_SMALL", "0")
     full = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
     assert torch.equal(out, full)
+    torch.testing.assert_close(own.float().cpu(), full.float().cpu(), **TOLS[dt])
