@@ -1280,8 +1280,18 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
         fp.seq_lens = seq_lens;
         fp.block_table = block_table;
         fp.page_size = page_size;
-        MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part),
-                                 stream),
+        float* part = at<float>(workspace, L.off_part);
+        if (use_out_small(dtype, dims, L.flash)) {
+            MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream, false),
+                        "fused paged attention launch");
+            MLA_TRY_HIP(launch_out_small(flash_partials(fp, L.flash, part), ctx, row_sum,
+                                         static_cast<const float*>(W_uv),
+                                         static_cast<float*>(out), dims->batch, dims->sq,
+                                         dims->heads, dims->kv_rank, dims->v, stream),
+                        "3d launch");
+            return ok();
+        }
+        MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream),
                     "fused paged attention launch");
         GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
         MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
@@ -1310,6 +1320,7 @@ int32_t mla_attention_work_list_ints(mla_dtype_t dtype, const mla_dims_t* dims) 
     if (!dims || check_dtype(dtype) != MLA_OK || check_work_list_dims(dims) != MLA_OK) return 0;
     FlashProblem fp = flash_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr, 1.0, 0);
     fp.ragged = true;
+    fp.want_list = true;   // the list itself, also where the attention would not build one
     return flash_worklist_ints(fp, plan_flash(fp));
 }
 
@@ -1321,6 +1332,7 @@ int mla_attention_work_list(mla_dtype_t dtype, const mla_dims_t* dims, const int
     MLA_CHECK(check_ptr(work_list, "work_list"));
     FlashProblem fp = flash_problem(dtype, dims, nullptr, nullptr, nullptr, nullptr, 1.0, 0);
     fp.ragged = true;
+    fp.want_list = true;
     fp.seq_lens = seq_lens;
     const FlashPlan plan = plan_flash(fp);
     const int need = flash_worklist_ints(fp, plan);

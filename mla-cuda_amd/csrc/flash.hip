@@ -1093,12 +1093,14 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32w_kernel(FlashArgs a) {
     const int r0 = rt * kWRows;
     const int row = r0 + l16;
 
+    // the batch's keys (its length when ragged); a split past them has no keys
+    const int skb = flash_batch_keys(a, b);
     const int k_lo = sp * a.keys_per_split;
-    int k_hi = min(a.Sk, k_lo + a.keys_per_split);
+    int k_hi = min(skb, k_lo + a.keys_per_split);
     int lim = k_hi - 1;
     if (a.causal) {
-        lim = min(lim, a.Sk - a.Sq + min(row, rows_b - 1) / a.H);
-        k_hi = min(k_hi, a.Sk - a.Sq + min(r0 + kWRows - 1, rows_b - 1) / a.H + 1);
+        lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
+        k_hi = min(k_hi, skb - a.Sq + min(r0 + kWRows - 1, rows_b - 1) / a.H + 1);
     }
     // this wave's blocks: a quarter of the workgroup's, contiguous
     const int nblk = k_hi > k_lo ? (k_hi - k_lo + kWKeys - 1) / kWKeys : 0;
@@ -1142,9 +1144,10 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32w_kernel(FlashArgs a) {
         return *reinterpret_cast<const v4u*>(q_lane + 16 * r);
     };
 
-    // ---- the cache: block jj's buffer resources span its keys inside [kw0, kw1)
-    const char* ck_b = reinterpret_cast<const char*>(a.ckv) + (int64_t)b * a.key_stride * (kFR * 4);
-    const char* pe_b = reinterpret_cast<const char*>(a.pe) + (int64_t)b * a.key_stride * (kFD * 4);
+    // ---- the cache: block jj's buffer resources span its keys inside [kw0, kw1), from the
+    // cache row of its first key (a paged cache's 16-key blocks never straddle a page)
+    const char* ck_b = reinterpret_cast<const char*>(a.ckv);
+    const char* pe_b = reinterpret_cast<const char*>(a.pe);
     // (readfirstlane: the values are wave-uniform, and the compiler must know it, or it
     // wraps every load in a loop over the lanes' distinct descriptors)
     auto rsrc_u = [](const char* ptr, int bytes) __attribute__((always_inline)) {
@@ -1155,15 +1158,13 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32w_kernel(FlashArgs a) {
             reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), (short)0,
             __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
     };
-    auto rs_k = [&](int jj) __attribute__((always_inline)) {
+    auto rs_kp = [&](int jj, __amdgpu_buffer_rsrc_t* rk, __amdgpu_buffer_rsrc_t* rp)
+        __attribute__((always_inline)) {
         const int kb = kw0 + kWKeys * jj;
         const int left = max(0, min(kWKeys, kw1 - kb));
-        return rsrc_u(ck_b + (int64_t)kb * (kFR * 4), left * (kFR * 4));
-    };
-    auto rs_p = [&](int jj) __attribute__((always_inline)) {
-        const int kb = kw0 + kWKeys * jj;
-        const int left = max(0, min(kWKeys, kw1 - kb));
-        return rsrc_u(pe_b + (int64_t)kb * (kFD * 4), left * (kFD * 4));
+        const int64_t row0 = flash_key_row(a, b, kb, kw1);
+        *rk = rsrc_u(ck_b + row0 * (kFR * 4), left * (kFR * 4));
+        *rp = rsrc_u(pe_b + row0 * (kFD * 4), left * (kFD * 4));
     };
     const uint32_t k_off = (uint32_t)l16 * (kFR * 4) + 16u * g;
     const uint32_t p_off = (uint32_t)l16 * (kFD * 4) + 16u * g;
@@ -1190,13 +1191,15 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32w_kernel(FlashArgs a) {
             for (int q = 0; q < 4; ++q) O[c][q] = v4f{};
         l_run = 0.f;
         {
-            const auto rk = rs_k(0);
-            const auto rp = rs_p(0);
+            __amdgpu_buffer_rsrc_t rk, rp;
+            rs_kp(0, &rk, &rp);
             static_for<kWWin>([&](auto n) { buf[n] = load_n(n, rk, rp); });
         }
         bool again = false;
         for (int jj = 0; jj < nb; ++jj) {
-            const auto rk = rs_k(jj), rp = rs_p(jj), rk1 = rs_k(jj + 1), rp1 = rs_p(jj + 1);
+            __amdgpu_buffer_rsrc_t rk, rp, rk1, rp1;
+            rs_kp(jj, &rk, &rp);
+            rs_kp(jj + 1, &rk1, &rp1);
             v4f s2[2] = {v4f{}, v4f{}};
             float p[4];
             v4u qb[kWQWin];
@@ -1547,18 +1550,6 @@ FlashPlan plan_flash(const FlashProblem& p) {
     const int blocks = (p.Sk + block_keys - 1) / block_keys;
     const size_t rows = (size_t)p.B * p.Sq * p.H;
     const size_t rows_b = (size_t)p.Sq * p.H;
-    if (p.seq_lens || p.ragged) {
-        // ragged keys: a work list built on the device from the key counts balances the
-        // grid (flash_worklist_kernel); the partial slots, the list and its grid are sized
-        // for its largest case
-        f.balanced = true;
-        f.max_items = wl_max_items(p.B, f.row_tiles);
-        f.n_split = 0;
-        f.keys_per_split = 0;
-        const size_t wl_bytes = ((size_t)wl_ints(p.B, f.max_items) * sizeof(int) + 255) / 256 * 256;
-        f.partial_bytes = wl_bytes + (size_t)f.max_items * rows_b * (kFR + 2) * sizeof(float);
-        return f;
-    }
     // fp32 batches that would need key splits to fill the chip with 64-row workgroups may
     // run on 16-row workgroups of key-split waves (flash32w_kernel): a quarter of the
     // splits for as many workgroups.  Splits for about one workgroup per CU; each wave gets
@@ -1571,7 +1562,10 @@ FlashPlan plan_flash(const FlashProblem& p) {
     // MLA_FLASH32_WAVE=0 / 1 forces the choice (both kernels give the same results to
     // rounding).
     const char* wave_env = std::getenv("MLA_FLASH32_WAVE");
-    const bool wave_ok = !p.half && !p.fp8_kv && !p.block_table;
+    // (ragged and paged batches too, on uniform splits of the table's span: a short
+    // sequence's later splits are empty workgroups -- at these batch sizes that costs less
+    // than the balanced work list's 64-row pass)
+    const bool wave_ok = !p.half && !p.fp8_kv && !p.want_list;
     const int base16 = p.B * ((p.Sq * p.H + kWRows - 1) / kWRows);
     const int wblocks = (p.Sk + kWKeys - 1) / kWKeys;
     const int target = std::max(1, (kNumCUs + base16 / 2) / base16);
@@ -1584,6 +1578,18 @@ FlashPlan plan_flash(const FlashProblem& p) {
         f.keys_per_split = 4 * bpw * kWKeys;
         f.partial_bytes = f.n_split > 1 ? rows * f.n_split * (kFR + 2) * sizeof(float)
                                         : rows * sizeof(float);
+        return f;
+    }
+    if (p.seq_lens || p.ragged) {
+        // ragged keys: a work list built on the device from the key counts balances the
+        // grid (flash_worklist_kernel); the partial slots, the list and its grid are sized
+        // for its largest case
+        f.balanced = true;
+        f.max_items = wl_max_items(p.B, f.row_tiles);
+        f.n_split = 0;
+        f.keys_per_split = 0;
+        const size_t wl_bytes = ((size_t)wl_ints(p.B, f.max_items) * sizeof(int) + 255) / 256 * 256;
+        f.partial_bytes = wl_bytes + (size_t)f.max_items * rows_b * (kFR + 2) * sizeof(float);
         return f;
     }
     // about one workgroup per CU (the LDS ring admits one per CU), at least one key block

@@ -150,6 +150,8 @@ struct FlashProblem {
     int page_size = 0;
     bool ragged = false;         // plan for per-batch key counts (a size query sets this
                                  // without seq_lens; a launch with it needs seq_lens)
+    bool want_list = false;      // plan the balanced work list even where a small fp32
+                                 // batch would run the key-split waves (list inspection)
     // fp8 cache (bf16 queries only): ckv / pe hold OCP e4m3 codes of value / kv_scale,
     // one byte per element (rows of R and D bytes)
     bool fp8_kv = false;

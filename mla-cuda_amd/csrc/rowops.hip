@@ -427,7 +427,9 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
         __syncthreads();
         // wave w normalises rows w, w+4, .. (in place in part[0])
         for (int mi = wave; mi < M; mi += 4) {
-            const float inv = 1.f / (((lsum[0][mi] + lsum[1][mi]) + lsum[2][mi]) + lsum[3][mi]);
+            // a row without visible keys (row sum 0) gives zeros, as the 3d GEMM does
+            const float L = ((lsum[0][mi] + lsum[1][mi]) + lsum[2][mi]) + lsum[3][mi];
+            const float inv = L == 0.f ? 0.f : 1.f / L;
             #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 const int k = 8 * lane + 4 * jj;
@@ -441,7 +443,7 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
     } else {
         for (int mi = wave; mi < M; mi += 4) {
             const int64_t r = slot0[mi];
-            const float inv = 1.f / rs[r];
+            const float inv = rs[r] == 0.f ? 0.f : 1.f / rs[r];
             const v4f* src = reinterpret_cast<const v4f*>(ctx + r * kOutR) + 2 * lane;
             *reinterpret_cast<v4f*>(&part[0][mi][8 * lane]) = src[0] * inv;
             *reinterpret_cast<v4f*>(&part[0][mi][8 * lane + 4]) = src[1] * inv;
