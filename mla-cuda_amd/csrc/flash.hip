@@ -731,6 +731,352 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ 16-bit: specialised waves
+// The same 64-row tile, 32-key blocks, staging and LDS ring as flash16_kernel, on eight
+// waves whose work is split by kind instead of by key half (two waves per SIMD, so one
+// issues while the other waits on LDS):
+//   score waves 0-3 (row tile rt = w/2, key half kh = w%2): K reads, the 36 score MFMAs
+//     and the softmax of flash16_kernel; they write P^T (16-bit, 32 rows x 16 keys) into
+//     one of two LDS P stages instead of keeping it;
+//   P.V waves 4-7 (row tile rt, column half ch): O^T for 256 columns x 32 rows (128
+//     VGPRs), one block behind: in step j they read block j-1's P^T for both key halves
+//     and its V^T fragments (transposing reads, as before) and run 16 32x32x16 MFMAs;
+//     they also issue the staging loads (flash16_kernel's, block j+2 in step j) between
+//     their MFMAs and wait for them before each step's barrier.  With the loads in the
+//     score waves instead, the pass took about 10% longer: the score waves carry the
+//     longer MFMA chain and the softmax, and the loads' issue cost lands on it.
+// Both key halves of a row must share one reference for their P^T to sum in one O, so at
+// the first block of a pass the two score waves of a row tile exchange their proposals
+// through LDS (the row maximum over the block, or the reference a previous pass raised)
+// and both take the larger; a row's first visible key lies in that block's first half, so
+// every row with keys gets a finite reference there.  A row that later passes it raises
+// its own half's reference and flags the pass for a repeat, as before.  P.V of block j-1
+// reads stage (j-1) % 4 of the ring while block j+2 loads into stage (j+2) % 4, and P^T
+// stage (j-1) & 1 while the score waves write stage j & 1: one barrier per step orders all
+// of it.  The two kinds run separate loops with the same barriers, so neither holds the
+// other's registers: Q^T (144) and O^T (128) both fit the 256 VGPRs of a wave at two waves
+// per SIMD, with no AGPRs.  The P.V loop starts at block 1 (block 0's step only has its
+// barriers), so the accumulators never meet a branch inside the loop; with that step inside
+// the loop the register allocator copies and spills them.  No key-half merge at the end:
+// the score waves leave row sums and references in LDS and the P.V waves write the rows.
+constexpr int kXThreads = 512;
+constexpr int kXPPitch = 80;                              // bytes per P^T row: 32 keys + pad
+constexpr int kXPStage = 2 * 32 * kXPPitch;               // both row tiles
+
+template <typename TL>
+__global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
+    constexpr int NS = 4;
+    constexpr float kHeadroom = Half<TL>::kF16 ? 15.f : k2Headroom;
+    constexpr int kPeBase = NS * k2LatStage;                    // 128 KB
+    constexpr int kPBase = kPeBase + NS * k2PeStage;            // 144 KB: two P^T stages
+    constexpr int kXBase = kPBase + 2 * kXPStage;               // references, sums, flags
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kXBase + 2 * 128 * 4 + 64];
+    float* xref = reinterpret_cast<float*>(smem + kXBase);      // [rt][kh][32 rows]
+    float* xl = xref + 128;                                     // [rt][kh][32 rows]
+    int* flags = reinterpret_cast<int*>(xl + 128);              // [score wave]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4, l32 = lane & 31, hw = lane >> 5;
+    const FlashWork work = flash_work(a);
+    if (work.skip) return;   // past the end of a work list: the whole workgroup leaves
+
+    const int b = work.b;
+    const int rows_b = a.Sq * a.H;
+    const int r0 = work.rt * kFRows;
+    const int skb = flash_batch_keys(a, b);
+    const int k_lo = work.k_lo;
+    const int k_end = min(skb, k_lo + work.k_len);
+    int k_hi = k_end;
+    if (a.causal) k_hi = min(k_hi, skb - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
+    const int nb = k_hi > k_lo ? (k_hi - k_lo + k2Keys - 1) / k2Keys : 0;
+    auto lat_base = [&](uint32_t base, int st) __attribute__((always_inline)) {
+        return (base ^ (65536u * (uint32_t)(st >> 1))) + (uint32_t)(st & 1) * k2LatStage;
+    };
+
+    if (wave < 4) {
+        // ================================ score waves
+        const int rt = wave >> 1, kh = wave & 1;
+        const int rbase = r0 + 32 * rt;
+        const int rowS0 = rbase + l16, rowS1 = rbase + 16 + l16;
+        int lim0 = k_end - 1, lim1 = k_end - 1;
+        if (a.causal) {
+            lim0 = min(lim0, skb - a.Sq + min(rowS0, rows_b - 1) / a.H);
+            lim1 = min(lim1, skb - a.Sq + min(rowS1, rows_b - 1) / a.H);
+        }
+        const int lim_wave = __builtin_amdgcn_readfirstlane(lim0);
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qa + (int64_t)b * rows_b * kFR);
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.qr + (int64_t)b * rows_b * kFD);
+        v4u qf[2][kQSteps];
+        #pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int row = t ? rowS1 : rowS0;
+            const uint32_t qmask = oob_mask(row, rows_b);
+            #pragma unroll
+            for (int s = 0; s < kQSteps; ++s)
+                qf[t][s] = s < kRSteps
+                               ? load16(rq, ((uint32_t)row * kLatBytes + 256u * g + 16u * s) | qmask)
+                               : load16(rr, ((uint32_t)row * kPeBytes + 64u * (s - kRSteps) + 16u * g) | qmask);
+        }
+        wait_vm<0>();   // Q in registers
+
+        const int kk = 16 * kh + l16;
+        uint32_t kb0 = kk * kLatBytes + 256u * g + 16u * sw16(l16);
+        uint32_t pb0 = kPeBase + kk * kPeBytes + 16u * (g ^ ((kk >> 1) & 7));
+        auto k_read = [&](uint32_t kbs, uint32_t pbs, int s) __attribute__((always_inline)) {
+            const uint32_t off = s < kRSteps ? (kbs ^ (16u * s)) : (pbs ^ (64u * (s - kRSteps)));
+            return *reinterpret_cast<const v4u*>(smem + off);
+        };
+        // P^T writes: rows 16h + l16 of the tile, keys 16kh + 4g .. +3 (8 bytes)
+        const uint32_t pw0 = kPBase + rt * 32 * kXPPitch + l16 * kXPPitch + 2u * (16 * kh + 4 * g);
+
+        float m_ref[2] = {-INFINITY, -INFINITY}, m_neg[2] = {0.f, 0.f};
+        float thr[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+        for (int pass = 1;; ++pass) {
+            l_run[0] = l_run[1] = 0.f;
+            bool overflow = false;
+            if (nb == 0) break;
+            #pragma unroll 1
+            for (int j = 0; j <= nb; ++j) {
+                lds_barrier();        // A_j: block j is in LDS, P.V of block j-2 is done
+                v4f sc[2];
+                if (j < nb) {
+                    constexpr int kWin = 3;
+                    asm volatile("" : "+v"(kb0), "+v"(pb0));
+                    const int st = j % NS;
+                    const uint32_t kbs = lat_base(kb0, st), pbs = pb0 + (uint32_t)st * k2PeStage;
+                    v4u kf[kWin];
+                    #pragma unroll
+                    for (int i = 0; i < kWin; ++i) kf[i] = k_read(kbs, pbs, i);
+                    #pragma unroll
+                    for (int s = 0; s < kQSteps; ++s) {
+                        const v4u cur = kf[s % kWin];
+                        if (s + kWin < kQSteps) kf[s % kWin] = k_read(kbs, pbs, s + kWin);
+                        if (s == 0) {
+                            mfma16_v_first<TL>(cur, qf[0][s], sc[0]);
+                            mfma16_v_first<TL>(cur, qf[1][s], sc[1]);
+                        } else if (s + 1 < kQSteps) {
+                            mfma16_v<TL>(cur, qf[0][s], sc[0]);
+                            mfma16_v<TL>(cur, qf[1][s], sc[1]);
+                        } else {
+                            mfma16_v<TL>(cur, qf[0][s], sc[0]);
+                            mfma16_v_last<TL>(cur, qf[1][s], sc[1]);
+                        }
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int kq0 = k_lo + k2Keys * j + 16 * kh;
+                    if (kq0 + 15 > lim_wave) {
+                        const int kq = kq0 + 4 * g;
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            sc[0][i] = kq + i <= lim0 ? sc[0][i] : -INFINITY;
+                            sc[1][i] = kq + i <= lim1 ? sc[1][i] : -INFINITY;
+                        }
+                    }
+                    if (j == 0) {
+                        // the pass's reference proposal of each row: the raised one of a
+                        // previous pass, else this block's maximum over the half's keys
+                        #pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float mx = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+                            const float bm = row4_reduce(mx, OpMax{}) * a.c;
+                            const float prop = m_ref[h] == -INFINITY ? bm : m_ref[h];
+                            if (g == 0) xref[(rt * 2 + kh) * 32 + 16 * h + l16] = prop;
+                        }
+                    }
+                }
+                if (j == 0) {
+                    lds_barrier();    // X: both halves' proposals are in LDS
+                    #pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int r = 16 * h + l16;
+                        const float ref = fmaxf(xref[(rt * 2) * 32 + r], xref[(rt * 2 + 1) * 32 + r]);
+                        m_ref[h] = ref;
+                        m_neg[h] = ref == -INFINITY ? 0.f : -ref;
+                        thr[h] = ref + kHeadroom;
+                    }
+                }
+                if (j < nb) {
+                    float mx[2];
+                    #pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        mx[h] = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+                    // a row past its threshold raises its reference and flags a repeat (NaN
+                    // scores come here too); rows without a reference have no visible key
+                    if (__builtin_amdgcn_ballot_w64(!(mx[0] * a.c <= thr[0]) || !(mx[1] * a.c <= thr[1]))) {
+                        #pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float bm = row4_reduce(mx[h], OpMax{}) * a.c;
+                            const bool over = pass < k2MaxPasses && m_ref[h] != -INFINITY && bm > thr[h];
+                            overflow |= __builtin_amdgcn_ballot_w64(over) != 0;
+                            if (over) {
+                                m_ref[h] = bm;
+                                m_neg[h] = -bm;
+                                thr[h] = bm + kHeadroom;
+                            }
+                        }
+                    }
+                    const uint32_t pws = pw0 + (uint32_t)(j & 1) * kXPStage;
+                    #pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        float e[4];
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h][i], a.c, m_neg[h]));
+                        l_run[h] += (e[0] + e[1]) + (e[2] + e[3]);
+                        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+                        *reinterpret_cast<v2u*>(smem + pws + 16u * h * kXPPitch) =
+                            v2u{Half<TL>::pack2(e[0], e[1]), Half<TL>::pack2(e[2], e[3])};
+                    }
+                }
+            }
+            lds_barrier();   // B1: every wave is done with the ring
+            if (lane == 0) flags[wave] = overflow ? 1 : 0;
+            lds_barrier();   // B2
+            const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+            lds_barrier();   // B3: the flags are read before they are written again
+            if (!again) break;
+        }
+        // row sums of the half and the shared references for the P.V waves
+        #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float l = row4_reduce(l_run[h], OpSum{});
+            if (g == 0) {
+                xl[(rt * 2 + kh) * 32 + 16 * h + l16] = l;
+                if (kh == 0) xref[(rt * 2) * 32 + 16 * h + l16] = m_ref[h];
+            }
+        }
+        lds_barrier();   // F: sums and references are in LDS
+        return;
+    }
+
+    // ==================================== P.V waves
+    const int rt = (wave - 4) >> 1, ch = (wave - 4) & 1;
+    const int rowO = r0 + 32 * rt + l32;
+    // V^T fragments of key half ks (keys 16ks + 8(l/32) .. +7) of column block cb
+    uint32_t vb0[2];
+    #pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int cq = g & 1, q = l16 >> 2, r = l16 & 3;
+        vb0[ks] = (16 * ks + 8 * hw + q) * kLatBytes +
+                  16u * ((q << 2) | ((2 * cq + (r >> 1)) ^ (2 * hw))) + 8u * (r & 1);
+    }
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
+    auto v_read = [&](uint32_t vbs, int cb) __attribute__((always_inline)) {
+        const uint32_t o = 256u * (cb >> 2);
+        const uint32_t c = 64u * (cb & 3);
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + ((vbs ^ c) + o)));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(smem + ((vbs ^ (c | 16u)) + o + 4 * kLatBytes)));
+        return __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    // P^T of key half ks in the B layout: row l32, keys 16ks + 8(l/32) .. +7
+    const uint32_t pr0 = kPBase + rt * 32 * kXPPitch + l32 * kXPPitch + 16u * hw;
+    // staging: P.V wave 4 + w loads keys 8w .. 8w+7 of a block (flash16_kernel's layout),
+    // block j+2 during step j, and waits for block j before barrier A_j
+    const int wv = wave - 4;
+    const uint32_t lds0 = lds_addr(smem);
+    const uint32_t pe_lane = (uint32_t)(lane >> 3) * kPeBytes +
+                             16u * ((lane & 7) ^ ((8 * wv + (lane >> 3)) >> 1 & 7));
+    const uint32_t lane16 = 16u * lane;
+    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
+    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe);
+    const int k_hi_s = __builtin_amdgcn_readfirstlane(k_hi);
+    struct Loads { v4i rk, rp; uint32_t st, st_pe; };
+    auto loads_of = [&](int j) __attribute__((always_inline)) {
+        const int stage = j % NS;
+        const int kb = __builtin_amdgcn_readfirstlane(k_lo + k2Keys * j + 8 * wv);
+        const uint32_t left = (uint32_t)max(0, min(8, k_hi_s - kb));
+        Loads d;
+        const uint64_t row0 = (uint64_t)flash_key_row(a, b, kb, k_hi_s);
+        d.st = __builtin_amdgcn_readfirstlane(lds0 + stage * k2LatStage + 8 * wv * kLatBytes);
+        d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + kPeBase + stage * k2PeStage + 8 * wv * kPeBytes);
+        d.rk = rsrc_span(ck_base + row0 * kLatBytes, 0, left * kLatBytes);
+        d.rp = rsrc_span(pe_base + row0 * kPeBytes, 0, left * kPeBytes);
+        return d;
+    };
+    auto issue_one = [&](const Loads& d, int q) __attribute__((always_inline)) {
+        if (q < 8) dma16(d.rk, d.st + q * kLatBytes, lane16 ^ (16u * sw16((8 * wv + q) & 15)), q * kLatBytes);
+        else dma16(d.rp, d.st_pe, pe_lane, 0);
+    };
+    v16f O[8];
+    for (int pass = 1;; ++pass) {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) O[i] = v16f{};
+        if (nb == 0) break;
+        #pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const Loads d = loads_of(j);
+            #pragma unroll
+            for (int q = 0; q < k2Loads; ++q) issue_one(d, q);
+        }
+        wait_vm<k2Loads>();                // block 0 has landed; block 1 may be in flight
+        lds_barrier();                     // A_0
+        {
+            const Loads d = loads_of(2);   // stage 2 is free from the pass's start
+            #pragma unroll
+            for (int q = 0; q < k2Loads; ++q) issue_one(d, q);
+        }
+        lds_barrier();                     // X
+        #pragma unroll 1
+        for (int j = 1; j <= nb; ++j) {
+            const Loads next = loads_of(j + 2);
+            wait_vm<k2Loads>();            // block j has landed; block j+1 may be in flight
+            lds_barrier();                 // A_j
+            {
+                asm volatile("" : "+v"(vb0[0]), "+v"(vb0[1]));
+                const int st = (j - 1) % NS;
+                const uint32_t prs = pr0 + (uint32_t)((j - 1) & 1) * kXPStage;
+                const v4u p0 = *reinterpret_cast<const v4u*>(smem + prs);
+                const v4u p1 = *reinterpret_cast<const v4u*>(smem + prs + 32u);
+                const uint32_t vs0 = lat_base(vb0[0], st), vs1 = lat_base(vb0[1], st);
+                constexpr int kVWin = 4;
+                v4u vf[kVWin];
+                // fragment t: key half t/8, column block 8ch + t%8 (consecutive MFMAs use
+                // different accumulators; each block's second one comes 8 MFMAs later)
+                auto vfrag = [&](int t) __attribute__((always_inline)) {
+                    return v_read((t >> 3) ? vs1 : vs0, 8 * ch + (t & 7));
+                };
+                #pragma unroll
+                for (int t = 0; t < kVWin; ++t) vf[t] = vfrag(t);
+                #pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const v4u cur = vf[t % kVWin];
+                    if (t + kVWin < 16) vf[t % kVWin] = vfrag(t + kVWin);
+                    O[t & 7] = mfma32h<TL>(cur, (t >> 3) ? p1 : p0, O[t & 7]);
+                    // block j+2 into stage (j+2) % 4, which block j-2 left at barrier A_j
+                    if (t % 2 == 0) issue_one(next, t / 2);
+                    if (t == 15) issue_one(next, 8);
+                }
+            }
+        }
+        wait_vm<0>();    // the zero loads of the blocks past the end have landed
+        lds_barrier();   // B1
+        lds_barrier();   // B2
+        const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+        lds_barrier();   // B3
+        if (!again) break;
+    }
+    lds_barrier();       // F
+    if (rowO < rows_b) {
+        const float* xlr = xl + rt * 64;
+        const float lsum = xlr[l32] + xlr[32 + l32];
+        const float M = xref[rt * 64 + l32];
+        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + rowO;
+        if (ch == 0 && hw == 0) {
+            if (!work.direct) a.m[slot] = M;
+            (work.direct ? a.l_direct : a.l)[slot] = lsum;
+        }
+        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR + 256 * ch + 4 * hw;
+        #pragma unroll
+        for (int cb = 0; cb < 8; ++cb)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) =
+                    v4f{O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]};
+    }
+}
+
 // ------------------------------------------------------------------ fp32 variant
 // Same pass with fp32 storage on the 16x16x4 fp32 MFMA (lane l supplies A[l%16][l/16] and
 // B[l/16][l%16]; accumulator element i of lane l is D[4(l/16) + i][l%16]).  A 16-key block
@@ -1696,8 +2042,15 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipError_t e = launch_flash_worklist(p, f, wl, stream);
         if (e != hipSuccess) return e;
     }
+    // 16-bit: the specialised-wave pass unless MLA_FLASH16_SPEC=0 asks for the key-split one
+    const char* spec_env = std::getenv("MLA_FLASH16_SPEC");
+    const bool spec = !(spec_env && spec_env[0] == '0');
     if (p.fp8_kv)
         hipLaunchKernelGGL((flash16_kernel<3, bf16_t, true>), dim3(grid), dim3(kFThreads), 0, stream, a);
+    else if (p.half && spec && p.f16)
+        hipLaunchKernelGGL(flash16x_kernel<f16_t>, dim3(grid), dim3(kXThreads), 0, stream, a);
+    else if (p.half && spec)
+        hipLaunchKernelGGL(flash16x_kernel<bf16_t>, dim3(grid), dim3(kXThreads), 0, stream, a);
     else if (p.half && p.f16)
         hipLaunchKernelGGL((flash16_kernel<kFStages, f16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else if (p.half)
