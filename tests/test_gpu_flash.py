@@ -123,6 +123,52 @@ def test_fused_rising_row_max(ext):
     torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOL)
 
 
+# bf16 and fp16 run on two kernels: eight specialised waves (flash16x_kernel, the default:
+# score waves, and P.V waves one key block behind that share each row's reference) or four
+# key-split waves (flash16_kernel); MLA_FLASH16_SPEC=1 / 0 forces either, and both must
+# match the oracle everywhere
+H16 = torch.float16
+HALF_TOLS = {BF: TOLS[BF], H16: dict(rtol=1e-2, atol=1e-2)}
+FP16_KERNELS = pytest.mark.parametrize("spec", ["1", "0"], ids=["specialised", "key-split"])
+HALF_DTYPES = pytest.mark.parametrize("dt", [BF, H16], ids=["bf16", "f16"])
+
+
+@FP16_KERNELS
+@HALF_DTYPES
+@pytest.mark.parametrize("B,Sq,Sk,H,causal", [
+    (1, 1, 5, 128, False), (2, 1, 33, 128, False), (3, 2, 300, 128, True),
+    (4, 1, 4989, 128, False), (2, 16, 1000, 128, True), (2, 3, 257, 40, False),
+    (1, 512, 1024, 1, True)])
+def test_16bit_kernels_vs_oracle(ext, monkeypatch, spec, dt, B, Sq, Sk, H, causal):
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    args = inputs(B, Sq, Sk, H=H, seed=3 * Sk + B, dt=dt)
+    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **HALF_TOLS[dt])
+
+
+@FP16_KERNELS
+@HALF_DTYPES
+def test_16bit_kernels_repeat_passes(ext, monkeypatch, spec, dt):
+    """Every row's scores climb along the keys past the kernel's headroom over its reference
+    (2^15 for fp16, 2^64 for bf16) several times: each pass raises the references and the
+    pass repeats with them (in the specialised kernel both key halves of a row must agree on
+    the raised reference before they add into one O)."""
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    B, Sq, Sk = 2, 1, 2048
+    climb = 40.0 if dt == H16 else 200.0        # log2 units from the first key to the last
+    g = torch.Generator().manual_seed(23)
+    qa = torch.zeros(B, Sq, D.n_heads, D.kv_rank)
+    qa[..., 0] = 1.0
+    qr = torch.zeros(B, Sq, D.n_heads, D.rope)
+    ck = 0.01 * torch.randn(B, Sk, D.kv_rank, generator=g)
+    ck[..., 0] = torch.linspace(0.0, climb * SCALE / math.log2(math.e), Sk)
+    pe = torch.zeros(B, Sk, D.rope)
+    wuv = torch.randn(D.n_heads, D.v, D.kv_rank, generator=g) / math.sqrt(D.kv_rank)
+    args = tuple(x.to(dt) for x in (qa, qr, ck, pe, wuv))
+    out = run(ext, args, False)
+    assert torch.isfinite(out).all()
+    torch.testing.assert_close(out, oracle(args, False), rtol=2e-2, atol=2e-2)
+
+
 # fp32 runs on two kernels: 64-row workgroups (flash32_kernel) when the batch fills the
 # chip, 16-row workgroups of key-split waves (flash32w_kernel) when it would need key
 # splits; MLA_FLASH32_WAVE=0 / 1 forces either, and both must match the oracle everywhere
