@@ -304,6 +304,54 @@ __device__ __forceinline__ void mfma16_v_last(v4u a, v4u b, v4f& c) {
         asm("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0\n\ts_nop 7\n\ts_nop 7" : "+v"(c) : "v"(a), "v"(b));
 }
 
+// fp8 cache staging, shared by both 16-bit kernels.  The loader of keys 8w .. 8w+7 of a
+// block puts their raw rows, R and D bytes each, unpermuted into its 5 KB region of fp8
+// stage j & 1 (4 KB latent, 512 B rope, 512 B that the rope load's idle lanes fill with
+// zeros), and converts them into the bf16 ring in the layout the direct loads write.  Part
+// q < 4 is one 16-byte read per lane: lane l holds bytes 16 (l % 32) .. +15 of key 2q + l/32,
+// i.e. bf16 chunks c0 = 2 (l % 32) and c0 + 1 of that key; part 4 is the rope rows (lanes
+// < 32: key l/4, chunks 2 (l % 4), +1).  OCP e4m3 -> bf16 is exact
+// (v_cvt_scalef32_pk_bf16_fp8 with scale 1); the cache scale is applied to the scores and
+// the output instead.  Since c0 is even, chunk c0 + 1 sits at chunk c0's position XOR 16.
+constexpr int kF8Wave = 5120, kF8Stage = 4 * kF8Wave;
+struct F8Stage {
+    uint32_t lat[4], pe;   // bf16 ring offsets (stage 0) of this lane's chunks
+    __device__ F8Stage(int w, int lane, uint32_t pe_base) {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int kw = 8 * w + 2 * q + (lane >> 5);
+            lat[q] = kw * kLatBytes + 256u * ((lane & 31) >> 3) + 16u * ((2 * (lane & 7)) ^ sw16(kw & 15));
+        }
+        const int kwp = 8 * w + ((lane >> 2) & 7);
+        pe = pe_base + kwp * kPeBytes + 16u * ((2 * (lane & 3)) ^ ((kwp >> 1) & 7));
+    }
+    // part q of the raw rows in the loader's region at byte offset `region`
+    __device__ v4u read(const uint8_t* smem, uint32_t region, int q, int lane) const {
+        return *reinterpret_cast<const v4u*>(smem + region + (q < 4 ? 1024 * q : 8 * kFR) + 16u * lane);
+    }
+    // part q, converted, into bf16 ring stage st
+    __device__ void write(uint8_t* smem, int st, int q, v4u raw, int lane) const {
+        // bytes 0-1 (word_sel false) and 2-3 (true) of a dword to two bf16
+        auto lo2 = [](uint32_t w) __attribute__((always_inline)) {
+            return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false));
+        };
+        auto hi2 = [](uint32_t w) __attribute__((always_inline)) {
+            return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true));
+        };
+        const v4u c0 = {lo2(raw[0]), hi2(raw[0]), lo2(raw[1]), hi2(raw[1])};
+        const v4u c1 = {lo2(raw[2]), hi2(raw[2]), lo2(raw[3]), hi2(raw[3])};
+        if (q < 4) {
+            const uint32_t o = lat[q] + (uint32_t)st * k2LatStage;
+            *reinterpret_cast<v4u*>(smem + o) = c0;
+            *reinterpret_cast<v4u*>(smem + (o ^ 16u)) = c1;
+        } else if (lane < 32) {
+            const uint32_t o = pe + (uint32_t)st * k2PeStage;
+            *reinterpret_cast<v4u*>(smem + o) = c0;
+            *reinterpret_cast<v4u*>(smem + (o ^ 16u)) = c1;
+        }
+    }
+};
+
 template <int NS, typename TL, bool FP8>
 __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     // P^T is rounded to TL: with bf16's 8 exponent bits a term may reach 2^64 over its
@@ -312,9 +360,8 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     static_assert(NS == (FP8 ? 3 : 4), "stage offsets: stage 2 (3) is stage 0 (1) XOR 64 KB");
     static_assert(!FP8 || !Half<TL>::kF16, "an fp8 cache is read with bf16 queries");
     constexpr int kPeBase = NS * k2LatStage;                    // 128 KB (fp8: 96 KB)
-    // fp8 cache: two stages of raw cache bytes, 5 KB per wave (4 KB latent, 512 B rope,
-    // 512 B that the rope load's idle lanes fill with zeros)
-    constexpr int kF8Base = kPeBase + NS * k2PeStage, kF8Wave = 5120, kF8Stage = 4 * kF8Wave;
+    // fp8 cache: two stages of raw cache bytes, 5 KB per wave (F8Stage)
+    constexpr int kF8Base = kPeBase + NS * k2PeStage;
     constexpr int kLoads = FP8 ? k8Loads : k2Loads;             // cache loads per wave and block
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kF8Base + (FP8 ? 2 * kF8Stage : 0)];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -413,46 +460,13 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
     };
 
     // ---- fp8 cache: each wave converts the rows it loaded (keys 8w .. 8w+7 of a block) into
-    // the bf16 ring, in the layout the direct loads write.  Part q < 4 is one 16-byte read
-    // per lane: lane l holds bytes 16 (l % 32) .. +15 of key 2q + l/32, i.e. bf16 chunks
-    // c0 = 2 (l % 32) and c0 + 1 of that key; part 4 is the rope rows (lanes < 32: key l/4,
-    // chunks 2 (l % 4), +1).  OCP e4m3 -> bf16 is exact (v_cvt_scalef32_pk_bf16_fp8 with
-    // scale 1); the cache scale is applied to the scores and the output instead.  Since c0
-    // is even, chunk c0 + 1 sits at chunk c0's position XOR 16 bytes.
-    uint32_t cv_lat[4], cv_pe = 0;
-    if constexpr (FP8) {
-        #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const int kw = 8 * wave + 2 * q + hw;
-            cv_lat[q] = kw * kLatBytes + 256u * ((lane & 31) >> 3) + 16u * ((2 * (lane & 7)) ^ sw16(kw & 15));
-        }
-        const int kwp = 8 * wave + ((lane >> 2) & 7);
-        cv_pe = kPeBase + kwp * kPeBytes + 16u * ((2 * (lane & 3)) ^ ((kwp >> 1) & 7));
-    }
+    // the bf16 ring (F8Stage)
+    const F8Stage f8(wave, lane, kPeBase);
     auto f8_read = [&](int j, int q) __attribute__((always_inline)) {
-        const uint32_t off = kF8Base + (j & 1) * kF8Stage + wave * kF8Wave + (q < 4 ? 1024 * q : 8 * kFR) + lane16;
-        return *reinterpret_cast<const v4u*>(smem + off);
+        return f8.read(smem, kF8Base + (j & 1) * kF8Stage + wave * kF8Wave, q, lane);
     };
     auto f8_write = [&](int j, int q, v4u raw) __attribute__((always_inline)) {
-        // bytes 0-1 (word_sel false) and 2-3 (true) of a dword to two bf16
-        auto lo2 = [](uint32_t w) __attribute__((always_inline)) {
-            return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false));
-        };
-        auto hi2 = [](uint32_t w) __attribute__((always_inline)) {
-            return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true));
-        };
-        const v4u c0 = {lo2(raw[0]), hi2(raw[0]), lo2(raw[1]), hi2(raw[1])};
-        const v4u c1 = {lo2(raw[2]), hi2(raw[2]), lo2(raw[3]), hi2(raw[3])};
-        const int st = j % NS;
-        if (q < 4) {
-            const uint32_t o = cv_lat[q] + (uint32_t)st * k2LatStage;
-            *reinterpret_cast<v4u*>(smem + o) = c0;
-            *reinterpret_cast<v4u*>(smem + (o ^ 16u)) = c1;
-        } else if (lane < 32) {
-            const uint32_t o = cv_pe + (uint32_t)st * k2PeStage;
-            *reinterpret_cast<v4u*>(smem + o) = c0;
-            *reinterpret_cast<v4u*>(smem + (o ^ 16u)) = c1;
-        }
+        f8.write(smem, j % NS, q, raw, lane);
     };
 
     // ---- per-lane LDS bases (byte offsets from smem); each read is base XOR a constant
@@ -759,17 +773,23 @@ __global__ void __launch_bounds__(kFThreads, 1) flash16_kernel(FlashArgs a) {
 // barriers), so the accumulators never meet a branch inside the loop; with that step inside
 // the loop the register allocator copies and spills them.  No key-half merge at the end:
 // the score waves leave row sums and references in LDS and the P.V waves write the rows.
+// An fp8 cache (FP8): the P.V waves load the raw rows into two fp8 stages (F8Stage) and,
+// during step j, convert block j+1 into the bf16 ring (three stages, into the one block j-2
+// left) while block j+2's raw rows load; the score waves see the same bf16 ring as ever.
 constexpr int kXThreads = 512;
 constexpr int kXPPitch = 80;                              // bytes per P^T row: 32 keys + pad
 constexpr int kXPStage = 2 * 32 * kXPPitch;               // both row tiles
 
-template <typename TL>
+template <typename TL, bool FP8>
 __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
-    constexpr int NS = 4;
+    static_assert(!FP8 || !Half<TL>::kF16, "an fp8 cache is read with bf16 queries");
+    constexpr int NS = FP8 ? 3 : 4;                             // bf16 ring stages
     constexpr float kHeadroom = Half<TL>::kF16 ? 15.f : k2Headroom;
-    constexpr int kPeBase = NS * k2LatStage;                    // 128 KB
-    constexpr int kPBase = kPeBase + NS * k2PeStage;            // 144 KB: two P^T stages
-    constexpr int kXBase = kPBase + 2 * kXPStage;               // references, sums, flags
+    constexpr int kLoads = FP8 ? k8Loads : k2Loads;             // cache loads per wave and block
+    constexpr int kPeBase = NS * k2LatStage;                    // 128 KB (fp8: 96 KB)
+    constexpr int kPBase = kPeBase + NS * k2PeStage;            // two P^T stages
+    constexpr int kF8Base = kPBase + 2 * kXPStage;              // fp8: two raw stages
+    constexpr int kXBase = kF8Base + (FP8 ? 2 * kF8Stage : 0);  // references, sums, flags
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kXBase + 2 * 128 * 4 + 64];
     float* xref = reinterpret_cast<float*>(smem + kXBase);      // [rt][kh][32 rows]
     float* xl = xref + 128;                                     // [rt][kh][32 rows]
@@ -973,7 +993,8 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
     // P^T of key half ks in the B layout: row l32, keys 16ks + 8(l/32) .. +7
     const uint32_t pr0 = kPBase + rt * 32 * kXPPitch + l32 * kXPPitch + 16u * hw;
     // staging: P.V wave 4 + w loads keys 8w .. 8w+7 of a block (flash16_kernel's layout),
-    // block j+2 during step j, and waits for block j before barrier A_j
+    // block j+2 during step j, and waits for block j before barrier A_j (fp8: for block j+1
+    // before converting it, in the same step)
     const int wv = wave - 4;
     const uint32_t lds0 = lds_addr(smem);
     const uint32_t pe_lane = (uint32_t)(lane >> 3) * kPeBytes +
@@ -989,15 +1010,35 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
         const uint32_t left = (uint32_t)max(0, min(8, k_hi_s - kb));
         Loads d;
         const uint64_t row0 = (uint64_t)flash_key_row(a, b, kb, k_hi_s);
-        d.st = __builtin_amdgcn_readfirstlane(lds0 + stage * k2LatStage + 8 * wv * kLatBytes);
-        d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + kPeBase + stage * k2PeStage + 8 * wv * kPeBytes);
-        d.rk = rsrc_span(ck_base + row0 * kLatBytes, 0, left * kLatBytes);
-        d.rp = rsrc_span(pe_base + row0 * kPeBytes, 0, left * kPeBytes);
+        if constexpr (FP8) {
+            d.st = __builtin_amdgcn_readfirstlane(lds0 + kF8Base + (j & 1) * kF8Stage + wv * kF8Wave);
+            d.st_pe = d.st + 8 * kFR;
+            d.rk = rsrc_span(ck_base + row0 * kFR, 0, left * kFR);
+            d.rp = rsrc_span(pe_base + row0 * kFD, 0, left * kFD);
+        } else {
+            d.st = __builtin_amdgcn_readfirstlane(lds0 + stage * k2LatStage + 8 * wv * kLatBytes);
+            d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + kPeBase + stage * k2PeStage + 8 * wv * kPeBytes);
+            d.rk = rsrc_span(ck_base + row0 * kLatBytes, 0, left * kLatBytes);
+            d.rp = rsrc_span(pe_base + row0 * kPeBytes, 0, left * kPeBytes);
+        }
         return d;
     };
+    const uint32_t pe8_lane = lane < 32 ? lane16 : kOob;   // 8 rope rows of 64 B: 32 lanes
     auto issue_one = [&](const Loads& d, int q) __attribute__((always_inline)) {
-        if (q < 8) dma16(d.rk, d.st + q * kLatBytes, lane16 ^ (16u * sw16((8 * wv + q) & 15)), q * kLatBytes);
-        else dma16(d.rp, d.st_pe, pe_lane, 0);
+        if constexpr (FP8) {
+            if (q < 4) dma16(d.rk, d.st + q * 1024, lane16, q * 1024);
+            else dma16(d.rp, d.st_pe, pe8_lane, 0);
+        } else {
+            if (q < 8) dma16(d.rk, d.st + q * kLatBytes, lane16 ^ (16u * sw16((8 * wv + q) & 15)), q * kLatBytes);
+            else dma16(d.rp, d.st_pe, pe_lane, 0);
+        }
+    };
+    const F8Stage f8(wv, lane, kPeBase);
+    auto f8_read = [&](int j, int q) __attribute__((always_inline)) {
+        return f8.read(smem, kF8Base + (j & 1) * kF8Stage + wv * kF8Wave, q, lane);
+    };
+    auto f8_write = [&](int j, int q, v4u raw) __attribute__((always_inline)) {
+        f8.write(smem, j % NS, q, raw, lane);
     };
     v16f O[8];
     for (int pass = 1;; ++pass) {
@@ -1008,21 +1049,31 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
         for (int j = 0; j < 2; ++j) {
             const Loads d = loads_of(j);
             #pragma unroll
-            for (int q = 0; q < k2Loads; ++q) issue_one(d, q);
+            for (int q = 0; q < kLoads; ++q) issue_one(d, q);
         }
-        wait_vm<k2Loads>();                // block 0 has landed; block 1 may be in flight
+        wait_vm<kLoads>();                 // block 0 has landed; block 1 may be in flight
+        if constexpr (FP8) {               // block 0 into the bf16 ring
+            #pragma unroll
+            for (int q = 0; q < kLoads; ++q) f8_write(0, q, f8_read(0, q));
+        }
         lds_barrier();                     // A_0
         {
             const Loads d = loads_of(2);   // stage 2 is free from the pass's start
             #pragma unroll
-            for (int q = 0; q < k2Loads; ++q) issue_one(d, q);
+            for (int q = 0; q < kLoads; ++q) issue_one(d, q);
+        }
+        if constexpr (FP8) {               // block 1, landed, into the bf16 ring
+            wait_vm<kLoads>();
+            #pragma unroll
+            for (int q = 0; q < kLoads; ++q) f8_write(1, q, f8_read(1, q));
         }
         lds_barrier();                     // X
         #pragma unroll 1
         for (int j = 1; j <= nb; ++j) {
             const Loads next = loads_of(j + 2);
-            wait_vm<k2Loads>();            // block j has landed; block j+1 may be in flight
-            lds_barrier();                 // A_j
+            if constexpr (!FP8)
+                wait_vm<k2Loads>();        // block j has landed; block j+1 may be in flight
+            lds_barrier();                 // A_j (fp8: block j was converted in step j-1)
             {
                 asm volatile("" : "+v"(vb0[0]), "+v"(vb0[1]));
                 const int st = (j - 1) % NS;
@@ -1039,14 +1090,25 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
                 };
                 #pragma unroll
                 for (int t = 0; t < kVWin; ++t) vf[t] = vfrag(t);
+                v4u f8raw;
                 #pragma unroll
                 for (int t = 0; t < 16; ++t) {
                     const v4u cur = vf[t % kVWin];
                     if (t + kVWin < 16) vf[t % kVWin] = vfrag(t + kVWin);
                     O[t & 7] = mfma32h<TL>(cur, (t >> 3) ? p1 : p0, O[t & 7]);
-                    // block j+2 into stage (j+2) % 4, which block j-2 left at barrier A_j
-                    if (t % 2 == 0) issue_one(next, t / 2);
-                    if (t == 15) issue_one(next, 8);
+                    if constexpr (FP8) {
+                        // block j+2's raw rows into the fp8 stage block j left; then block
+                        // j+1's, landed, into bf16 stage (j+1) % 3, which block j-2 left at
+                        // barrier A_j, each part read an MFMA before it is written
+                        if (t < kLoads) issue_one(next, t);
+                        if (t == kLoads) wait_vm<kLoads>();
+                        if (t >= 5 && t < 15 && (t & 1)) f8raw = f8_read(j + 1, (t - 5) / 2);
+                        if (t >= 6 && t < 16 && !(t & 1)) f8_write(j + 1, (t - 6) / 2, f8raw);
+                    } else {
+                        // block j+2 into stage (j+2) % 4, which block j-2 left at barrier A_j
+                        if (t % 2 == 0) issue_one(next, t / 2);
+                        if (t == 15) issue_one(next, 8);
+                    }
                 }
             }
         }
@@ -1068,12 +1130,14 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
             (work.direct ? a.l_direct : a.l)[slot] = lsum;
         }
         float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR + 256 * ch + 4 * hw;
+        // an fp8 cache's values are its codes times kv_scale: ctx takes the factor here
+        const float of = FP8 ? a.o_scale : 1.f;
         #pragma unroll
         for (int cb = 0; cb < 8; ++cb)
             #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) =
-                    v4f{O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]};
+                    v4f{O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]} * of;
     }
 }
 
@@ -2045,12 +2109,14 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     // 16-bit: the specialised-wave pass unless MLA_FLASH16_SPEC=0 asks for the key-split one
     const char* spec_env = std::getenv("MLA_FLASH16_SPEC");
     const bool spec = !(spec_env && spec_env[0] == '0');
-    if (p.fp8_kv)
+    if (p.fp8_kv && spec)
+        hipLaunchKernelGGL((flash16x_kernel<bf16_t, true>), dim3(grid), dim3(kXThreads), 0, stream, a);
+    else if (p.fp8_kv)
         hipLaunchKernelGGL((flash16_kernel<3, bf16_t, true>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else if (p.half && spec && p.f16)
-        hipLaunchKernelGGL(flash16x_kernel<f16_t>, dim3(grid), dim3(kXThreads), 0, stream, a);
+        hipLaunchKernelGGL((flash16x_kernel<f16_t, false>), dim3(grid), dim3(kXThreads), 0, stream, a);
     else if (p.half && spec)
-        hipLaunchKernelGGL(flash16x_kernel<bf16_t>, dim3(grid), dim3(kXThreads), 0, stream, a);
+        hipLaunchKernelGGL((flash16x_kernel<bf16_t, false>), dim3(grid), dim3(kXThreads), 0, stream, a);
     else if (p.half && p.f16)
         hipLaunchKernelGGL((flash16_kernel<kFStages, f16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else if (p.half)

@@ -4,7 +4,9 @@ The cache holds OCP E4M3 codes (torch.float8_e4m3fn) of value / kv_scale; querie
 the output are bf16.  The oracle decodes the codes with its own restated E4M3 table
 (oracle/mla_ref.py e4m3_values, pinned against torch's float8_e4m3fn in test_oracle.py) and
 runs the attention in float32; the bf16 tolerance applies (rtol/atol 2e-2 on O(1) outputs).
-The decoder the kernel uses is checked on its own over all 256 codes.
+The decoder the kernel uses is checked on its own over all 256 codes.  The fused pass runs on
+either 16-bit kernel (MLA_FLASH16_SPEC=1, the default: specialised waves, whose P.V waves
+convert the codes; 0: key-split waves); the parity tests run both.
 """
 
 from __future__ import annotations
@@ -63,10 +65,15 @@ def fp8_inputs(B, Sq, Sk, seed):
     return qa, qr, (ck / kv_scale).to(F8), (pe / kv_scale).to(F8), kv_scale, wuv
 
 
+KERNELS = pytest.mark.parametrize("spec", ["1", "0"], ids=["specialised", "key-split"])
+
+
+@KERNELS
 @pytest.mark.parametrize("B,Sq,Sk,causal", [(2, 1, 4989, False), (1, 1, 64, False),
                                             (3, 2, 1000, False), (1, 8, 700, True),
                                             (1, 1, 33, False), (5, 1, 2047, False)])
-def test_fp8kv_attention_matches_oracle(ext, B, Sq, Sk, causal):
+def test_fp8kv_attention_matches_oracle(ext, monkeypatch, spec, B, Sq, Sk, causal):
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
     qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(B, Sq, Sk, seed=B * 100 + Sk)
     out = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale, wuv.to(DEV),
                                   SCALE, causal).cpu()
@@ -87,9 +94,11 @@ def test_fp8kv_uint8_codes_and_scale(ext):
         torch.testing.assert_close(out.float(), ref, **TOL)
 
 
-def test_fp8kv_b128_full_size(ext):
+@KERNELS
+def test_fp8kv_b128_full_size(ext, monkeypatch, spec):
     """B=128 decode at Sk=4989 (the bf16 configuration's shape) over an fp8 cache, every
     sequence against the oracle."""
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
     qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(128, 1, 4989, seed=0)
     out = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale, wuv.to(DEV),
                                   SCALE).cpu()
