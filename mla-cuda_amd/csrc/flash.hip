@@ -1434,6 +1434,270 @@ __global__ void __launch_bounds__(kFThreads, 1) flash32_kernel(FlashArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ fp32: specialised waves
+// flash32_kernel's 64-row tile, 16-key blocks, LDS ring and softmax on eight waves split by
+// kind, two per SIMD, so that one wave's MFMAs run while the other waits on LDS, on the
+// barrier or on its softmax:
+//   score wave w (rows 16w .. 16w+15): Q^T in 144 VGPRs, the K reads, the 144 score MFMAs
+//     and the softmax (reference, threshold and repeat flag as in flash32_kernel); it
+//     writes P^T in its accumulator layout (element i of lane l is key 4(l/16) + i of row
+//     l%16) to its pair's 1 KB slot of P stage j & 1;
+//   P.V wave 4 + w (the same rows): O^T in 128 VGPRs, one block behind: in step j it reads
+//     block j-1's P^T slot, whose lane layout is its B operand, and runs the 128 P.V MFMAs
+//     over block j-1's V^T; it also issues the staging loads (block j+2 in step j, spread
+//     over its MFMAs) and waits for block j before the step's barrier.
+// A wave pair owns its 16 rows whole, so no reference crosses waves.  One barrier per step
+// orders the ring (K of block j, V of block j-1, block j+2 loading into the stage block
+// j-2 left) and the P stages.  A pass runs to its end; a repeat is decided from the score
+// waves' flags after it.  The P.V loop starts at block 1 (block 0's step only has its
+// barrier), so the accumulators meet no branch inside the loop.
+constexpr int k32XPStage = 4 * 1024;      // P^T slots of the four wave pairs
+
+template <int NS>
+__global__ void __launch_bounds__(kXThreads, 1) flash32x_kernel(FlashArgs a) {
+    static_assert(NS == 4, "the ring keeps block j-1 (V), block j (K) and two in flight");
+    constexpr int kPBase = NS * k32StageBytes;
+    constexpr int kXBase = kPBase + 2 * k32XPStage;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kXBase + 2 * 64 * 4 + 16];
+    float* xm = reinterpret_cast<float*>(smem + kXBase);   // [64 rows] references
+    float* xl = xm + 64;                                   // [64 rows] row sums
+    int* flags = reinterpret_cast<int*>(xl + 64);          // [score wave]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int pw = wave & 3;                               // the wave pair
+    const int l16 = lane & 15, g = lane >> 4;
+    const FlashWork work = flash_work(a);
+    if (work.skip) return;   // past the end of a work list: the whole workgroup leaves
+
+    const int b = work.b;
+    const int rows_b = a.Sq * a.H;
+    const int r0 = work.rt * kFRows;
+    const int row = r0 + 16 * pw + l16;
+    const int skb = flash_batch_keys(a, b);
+    const int k_lo = work.k_lo;
+    int k_hi = min(skb, k_lo + work.k_len);
+    int lim = k_hi - 1;
+    if (a.causal) {
+        lim = min(lim, skb - a.Sq + min(row, rows_b - 1) / a.H);
+        k_hi = min(k_hi, skb - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
+    }
+    const int nb = k_hi > k_lo ? (k_hi - k_lo + k32Keys - 1) / k32Keys : 0;
+    const uint32_t lat0 = NS * k32PeStage;
+    const uint32_t pslot = kPBase + pw * 1024 + 16u * lane;   // + stage * k32XPStage
+
+    if (wave < 4) {
+        // ================================ score waves
+        const int lim_wave = __builtin_amdgcn_readfirstlane(lim);
+        const float* qa = reinterpret_cast<const float*>(a.qa);
+        const float* qr = reinterpret_cast<const float*>(a.qr);
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(qa + (int64_t)b * rows_b * kFR);
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(qr + (int64_t)b * rows_b * kFD);
+        const uint32_t qmask = oob_mask(row, rows_b);
+        v4u qf[k32LatReads + k32PeReads];
+        #pragma unroll
+        for (int r = 0; r < k32LatReads; ++r)
+            qf[r] = load16(rq, ((uint32_t)row * (kFR * 4) + 512u * g + 16u * r) | qmask);
+        #pragma unroll
+        for (int r = 0; r < k32PeReads; ++r)
+            qf[k32LatReads + r] = load16(rr, ((uint32_t)row * k32PeBytes + 64u * g + 16u * r) | qmask);
+        wait_vm<0>();   // Q in registers
+
+        uint32_t k_base = lat0 + l16 * k32Pitch + 512u * g;   // + stage * k32LatStage
+        uint32_t p_off[k32PeReads];
+        #pragma unroll
+        for (int r = 0; r < k32PeReads; ++r)
+            p_off[r] = l16 * k32PeBytes + 16u * ((4 * g + r) ^ swz(l16));
+        float m_ref = -INFINITY, m_neg = 0.f, thr = -INFINITY, l_run = 0.f;
+        for (int pass = 1;; ++pass) {
+            l_run = 0.f;
+            bool overflow = false;
+            if (nb == 0) break;
+            #pragma unroll 1
+            for (int j = 0; j <= nb; ++j) {
+                lds_barrier();        // A_j: block j is in LDS, P.V of block j-2 is done
+                if (j < nb) {
+                    constexpr int KW = 4;
+                    constexpr int KR = k32LatReads + k32PeReads;
+                    asm volatile("" : "+v"(k_base));
+                    const int st = j % NS;
+                    const uint32_t kbs = k_base + (uint32_t)st * k32LatStage;
+                    const uint32_t pbs = (uint32_t)st * k32PeStage;
+                    auto k_read = [&](int r) __attribute__((always_inline)) {
+                        const uint32_t off = r < k32LatReads ? kbs + 16u * r : p_off[r - k32LatReads] + pbs;
+                        return *reinterpret_cast<const v4u*>(smem + off);
+                    };
+                    v4u kq[KW];
+                    #pragma unroll
+                    for (int r = 0; r < KW; ++r) kq[r] = k_read(r);
+                    v4f s2[2] = {v4f{}, v4f{}};
+                    #pragma unroll
+                    for (int r = 0; r < KR; ++r) {
+                        const v4u cur = kq[r % KW];
+                        if (r + KW < KR) kq[r % KW] = k_read(r + KW);
+                        #pragma unroll
+                        for (int q = 0; q < 4; ++q)
+                            s2[q & 1] = mfma16f(__uint_as_float(cur[q]), __uint_as_float(qf[r][q]), s2[q & 1]);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(kSgDsRd, KW, 0);
+                    #pragma unroll
+                    for (int r = 0; r < KR - KW; ++r) {
+                        __builtin_amdgcn_sched_group_barrier(kSgMfma, 4, 0);
+                        __builtin_amdgcn_sched_group_barrier(kSgDsRd, 1, 0);
+                    }
+                    __builtin_amdgcn_sched_group_barrier(kSgMfma, 4 * KW, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                    v4f sc = s2[0] + s2[1];
+                    // element i of lane l is key kb + 4g + i of row l%16
+                    const int kb = k_lo + k32Keys * j;
+                    if (kb + k32Keys - 1 > lim_wave) {
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i) sc[i] = kb + 4 * g + i <= lim ? sc[i] : -INFINITY;
+                    }
+                    const float smax = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+                    // a row's first visible keys set its reference (O is still zero for it);
+                    // a row whose maximum passes reference + headroom flags a repeat (rows
+                    // are uniform over their 4 lanes after the reduction; NaN scores take
+                    // this path too)
+                    if (__builtin_amdgcn_ballot_w64(!(smax * a.c <= thr))) {
+                        const float bm = row4_reduce(smax, OpMax{}) * a.c;
+                        const bool over = pass < k32MaxPasses && m_ref != -INFINITY && bm > thr;
+                        overflow |= __builtin_amdgcn_ballot_w64(over) != 0;
+                        if (m_ref == -INFINITY || over) {
+                            m_ref = bm;
+                            m_neg = bm == -INFINITY ? 0.f : -bm;
+                            thr = bm + k32Headroom;
+                        }
+                    }
+                    v4f p;
+                    #pragma unroll
+                    for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[i], a.c, m_neg));
+                    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+                    *reinterpret_cast<v4f*>(smem + pslot + (uint32_t)(j & 1) * k32XPStage) = p;
+                }
+            }
+            lds_barrier();   // B1: every wave is done with the ring
+            if (lane == 0) flags[wave] = overflow ? 1 : 0;
+            lds_barrier();   // B2
+            const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+            lds_barrier();   // B3: the flags are read before they are written again
+            if (!again) break;
+        }
+        l_run = row4_reduce(l_run, OpSum{});
+        if (g == 0) {
+            xm[16 * pw + l16] = m_ref;
+            xl[16 * pw + l16] = l_run;
+        }
+        lds_barrier();   // F: references and row sums are in LDS
+        return;
+    }
+
+    // ==================================== P.V waves
+    // staging: P.V wave 4 + w loads keys 4w .. 4w+3 of a block (flash32_kernel's layout),
+    // block j+2 during step j; blocks past the end load zeros
+    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
+    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe);
+    const uint32_t lds0 = lds_addr(smem);
+    const int k_hi_s = __builtin_amdgcn_readfirstlane(k_hi);
+    uint32_t lat_lane[4];
+    #pragma unroll
+    for (int k = 0; k < 4; ++k) lat_lane[k] = 16u * lane + (uint32_t)k * (kFR * 4);
+    const uint32_t pe_lane = (uint32_t)(lane >> 4) * k32PeBytes +
+                             16u * ((lane & 15) ^ swz((4 * pw + (lane >> 4)) & 15));
+    struct Loads { v4i rk, rp; uint32_t st, st_pe; };
+    auto loads_of = [&](int j) __attribute__((always_inline)) {
+        const int stage = j % NS;
+        const int kb = __builtin_amdgcn_readfirstlane(k_lo + k32Keys * j + 4 * pw);
+        const uint32_t left = (uint32_t)max(0, min(4, k_hi_s - kb));
+        const uint64_t row0 = (uint64_t)flash_key_row(a, b, kb, k_hi_s);
+        Loads d;
+        d.rk = rsrc_span(ck_base + row0 * (kFR * 4), 0, left * (kFR * 4));
+        d.rp = rsrc_span(pe_base + row0 * k32PeBytes, 0, left * k32PeBytes);
+        d.st = __builtin_amdgcn_readfirstlane(lds0 + NS * k32PeStage + stage * k32LatStage + 4 * pw * k32Pitch);
+        d.st_pe = __builtin_amdgcn_readfirstlane(lds0 + stage * k32PeStage + 4 * pw * k32PeBytes);
+        return d;
+    };
+    // load q < 8: half q % 2 of key q / 2's latent row; load 8: the four keys' rope rows
+    auto issue_one = [&](const Loads& d, int q) __attribute__((always_inline)) {
+        if (q < 8) {
+            if (q & 1) dma16_imm<1024>(d.rk, d.st + (q >> 1) * k32Pitch, lat_lane[q >> 1]);
+            else dma16_imm<0>(d.rk, d.st + (q >> 1) * k32Pitch, lat_lane[q >> 1]);
+        } else {
+            dma16_imm<0>(d.rp, d.st_pe, pe_lane);
+        }
+    };
+    uint32_t v_base = lat0 + 4 * g * k32Pitch + 8u * l16;   // + stage * k32LatStage
+    typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+    v4f O[2 * 16];   // [mh][r]
+    for (int pass = 1;; ++pass) {
+        #pragma unroll
+        for (int i = 0; i < 32; ++i) O[i] = v4f{};
+        if (nb == 0) break;
+        #pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const Loads d = loads_of(j);
+            #pragma unroll
+            for (int q = 0; q < k32Loads; ++q) issue_one(d, q);
+        }
+        wait_vm<k32Loads>();               // block 0 has landed; block 1 may be in flight
+        lds_barrier();                     // A_0
+        {
+            const Loads d = loads_of(2);   // stage 2 is free from the pass's start
+            #pragma unroll
+            for (int q = 0; q < k32Loads; ++q) issue_one(d, q);
+        }
+        #pragma unroll 1
+        for (int j = 1; j <= nb; ++j) {
+            const Loads next = loads_of(j + 2);
+            wait_vm<k32Loads>();           // block j has landed; block j+1 may be in flight
+            lds_barrier();                 // A_j: block j-1's P^T is in its slot
+            constexpr int VW = 8;          // V reads in flight
+            asm volatile("" : "+v"(v_base));
+            const uint32_t vbs = v_base + (uint32_t)((j - 1) % NS) * k32LatStage;
+            // V read t: K step i = t / 16 (keys 4g + i), column pair 32mh + 2*l16, mh = t % 16
+            auto v_read = [&](int t) __attribute__((always_inline)) {
+                return *reinterpret_cast<const v2u*>(smem + vbs + (t >> 4) * k32Pitch + 128u * (t & 15));
+            };
+            v2u vq[VW];
+            #pragma unroll
+            for (int t = 0; t < VW; ++t) vq[t] = v_read(t);
+            const v4f p = *reinterpret_cast<const v4f*>(smem + pslot + (uint32_t)((j - 1) & 1) * k32XPStage);
+            #pragma unroll
+            for (int t = 0; t < 64; ++t) {
+                const v2u cur = vq[t % VW];
+                if (t + VW < 64) vq[t % VW] = v_read(t + VW);
+                const int mh = t & 15, i = t >> 4;
+                O[2 * mh] = mfma16f(__uint_as_float(cur[0]), p[i], O[2 * mh]);
+                O[2 * mh + 1] = mfma16f(__uint_as_float(cur[1]), p[i], O[2 * mh + 1]);
+                // block j+2 into stage (j+2) % 4, which block j-2 left at barrier A_j
+                if (t % 7 == 3 && t / 7 < k32Loads) issue_one(next, t / 7);
+            }
+        }
+        wait_vm<0>();    // the zero loads of the blocks past the end have landed
+        lds_barrier();   // B1
+        lds_barrier();   // B2
+        const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+        lds_barrier();   // B3
+        if (!again) break;
+    }
+    lds_barrier();       // F
+    // ---- partial state: lane l holds row l%16, columns 32mh + 8g + 2i + r of O[mh][r][i]
+    if (row < rows_b) {
+        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
+        if (g == 0) {
+            if (!work.direct) a.m[slot] = xm[16 * pw + l16];
+            (work.direct ? a.l_direct : a.l)[slot] = xl[16 * pw + l16];
+        }
+        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR;
+        #pragma unroll
+        for (int mh = 0; mh < 16; ++mh) {
+            const v4f lo = {O[2 * mh][0], O[2 * mh + 1][0], O[2 * mh][1], O[2 * mh + 1][1]};
+            const v4f hi = {O[2 * mh][2], O[2 * mh + 1][2], O[2 * mh][3], O[2 * mh + 1][3]};
+            *reinterpret_cast<v4f*>(orow + 32 * mh + 8 * g) = lo;
+            *reinterpret_cast<v4f*>(orow + 32 * mh + 8 * g + 4) = hi;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ fp32: key-split waves
 // The fp32 pass for batches too small to fill the chip with flash32_kernel's 64-row
 // workgroups.  Those need many key splits there, and their split partials outgrow the
@@ -2109,6 +2373,10 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     // 16-bit: the specialised-wave pass unless MLA_FLASH16_SPEC=0 asks for the key-split one
     const char* spec_env = std::getenv("MLA_FLASH16_SPEC");
     const bool spec = !(spec_env && spec_env[0] == '0');
+    // fp32, 64-row workgroups: the specialised-wave pass unless MLA_FLASH32_SPEC=0 asks for
+    // flash32_kernel
+    const char* spec32_env = std::getenv("MLA_FLASH32_SPEC");
+    const bool spec32 = !(spec32_env && spec32_env[0] == '0');
     if (p.fp8_kv && spec)
         hipLaunchKernelGGL((flash16x_kernel<bf16_t, true>), dim3(grid), dim3(kXThreads), 0, stream, a);
     else if (p.fp8_kv)
@@ -2123,6 +2391,8 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         hipLaunchKernelGGL((flash16_kernel<kFStages, bf16_t, false>), dim3(grid), dim3(kFThreads), 0, stream, a);
     else if (f.wave)
         hipLaunchKernelGGL(flash32w_kernel, dim3(grid), dim3(kFThreads), 0, stream, a);
+    else if (spec32)
+        hipLaunchKernelGGL(flash32x_kernel<kFStages>, dim3(grid), dim3(kXThreads), 0, stream, a);
     else
         hipLaunchKernelGGL(flash32_kernel<kFStages>, dim3(grid), dim3(kFThreads), 0, stream, a);
     hipError_t e = hipGetLastError();

@@ -169,10 +169,17 @@ def test_16bit_kernels_repeat_passes(ext, monkeypatch, spec, dt):
     torch.testing.assert_close(out, oracle(args, False), rtol=2e-2, atol=2e-2)
 
 
-# fp32 runs on two kernels: 64-row workgroups (flash32_kernel) when the batch fills the
-# chip, 16-row workgroups of key-split waves (flash32w_kernel) when it would need key
-# splits; MLA_FLASH32_WAVE=0 / 1 forces either, and both must match the oracle everywhere
-FP32_KERNELS = pytest.mark.parametrize("wave", ["0", "1"], ids=["wg64", "wave16"])
+# fp32 runs on three kernels: 64-row workgroups when the batch fills the chip, on eight
+# specialised waves (flash32x_kernel, the default) or four (flash32_kernel,
+# MLA_FLASH32_SPEC=0), and 16-row workgroups of key-split waves (flash32w_kernel) when it
+# would need key splits; MLA_FLASH32_WAVE=0 / 1 forces the 64-row or the 16-row kind, and
+# every kernel must match the oracle everywhere
+FP32_KERNELS = pytest.mark.parametrize("wave", ["0", "0s", "1"], ids=["wg64-spec", "wg64", "wave16"])
+
+
+def set_fp32_kernel(monkeypatch, wave):
+    monkeypatch.setenv("MLA_FLASH32_WAVE", wave[0])
+    monkeypatch.setenv("MLA_FLASH32_SPEC", "0" if wave == "0s" else "1")
 
 
 @FP32_KERNELS
@@ -182,7 +189,7 @@ FP32_KERNELS = pytest.mark.parametrize("wave", ["0", "1"], ids=["wg64", "wave16"
     (2, 3, 257, 40, False), (1, 512, 1024, 1, True), (40, 1, 700, 128, False),
     (1, 1, 65, 128, False)])
 def test_fp32_kernels_vs_oracle(ext, monkeypatch, wave, B, Sq, Sk, H, causal):
-    monkeypatch.setenv("MLA_FLASH32_WAVE", wave)
+    set_fp32_kernel(monkeypatch, wave)
     args = inputs(B, Sq, Sk, H=H, seed=3 * Sk + B, dt=F32)
     torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[F32])
 
@@ -191,7 +198,7 @@ def test_fp32_kernels_vs_oracle(ext, monkeypatch, wave, B, Sq, Sk, H, causal):
 def test_fp32_kernels_full_size(ext, monkeypatch, wave):
     """B=128, Sk=4989 on either kernel (the key-split waves at a full grid: no key split,
     1,024 workgroups), every sequence against the oracle."""
-    monkeypatch.setenv("MLA_FLASH32_WAVE", wave)
+    set_fp32_kernel(monkeypatch, wave)
     args = inputs(128, 1, 4989, seed=77, dt=F32)
     got = run(ext, args, False)
     qa, qr, ck, pe, wuv = args
@@ -232,7 +239,7 @@ def test_fused_f32_restart(ext, monkeypatch, wave, jump):
     scores rise by `jump` (log2 units) over the keys in steps of ~0.35 per key, so the
     kernel restarts one (100) or several (400) times; a one-key spike at key 900 of
     another sequence restarts from a late block."""
-    monkeypatch.setenv("MLA_FLASH32_WAVE", wave)
+    set_fp32_kernel(monkeypatch, wave)
     B, Sq, Sk = 2, 1, 1200
     qa, qr, ck, pe, wuv = inputs(B, Sq, Sk, seed=13, dt=F32)
     u = torch.randn(D.kv_rank, generator=torch.Generator().manual_seed(14))
