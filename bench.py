@@ -676,6 +676,12 @@ def measure(args, ext, dev, neighbours=True):
                 pe8 = (g["pe_cache"].float() / kv_scale).to(torch.float8_e4m3fn)
                 att_calls["attention_fp8kv"] = (lambda: ext.mla_attention_fp8kv(
                     qa_b, qr_b, ck8, pe8, kv_scale, W_uv_d, scale), fl_attn)
+                # and over the same pages as fp8 codes, at the ragged lengths
+                ck8_pool = (ck_pool.float() / kv_scale).to(torch.float8_e4m3fn)
+                pe8_pool = (pe_pool.float() / kv_scale).to(torch.float8_e4m3fn)
+                att_calls["attention_paged_ragged_fp8kv"] = (lambda: ext.mla_attention_paged_fp8kv(
+                    qa_b, qr_b, ck8_pool, pe8_pool, table, ragged, kv_scale, W_uv_d, scale),
+                    fl_attn * keys_ragged / (B * Sk))
             for name, (fn, fl) in att_calls.items():
                 for _ in range(3):
                     fn()
@@ -693,7 +699,8 @@ def measure(args, ext, dev, neighbours=True):
             nb["attention_paged_ragged"]["mean_keys"] = round(keys_ragged / B, 1)
             if "attention_fp8kv" in nb:
                 nb["attention_fp8kv"]["cache_mbytes"] = round(B * Sk * (dims.kv_rank + dims.rope) / 1e6, 1)
-                del ck8, pe8
+                nb["attention_paged_ragged_fp8kv"]["mean_keys"] = round(keys_ragged / B, 1)
+                del ck8, pe8, ck8_pool, pe8_pool
             del ck_pool, pe_pool
         else:
             # causal: the key-chunked entry point (bounded score workspace) beside the layer's

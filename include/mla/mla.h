@@ -311,6 +311,25 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
                         const void* W_uv, double scale, int causal, void* out, void* workspace,
                         size_t workspace_bytes, hipStream_t stream);
 
+/* Attention over a paged fp8 cache: mla_attention_paged's pools, block table, seq_lens and
+ * causal rule, with the pools holding mla_attention_fp8kv's e4m3 codes.  It combines two
+ * cache formats that the reference has neither of (one dense cache in the query dtype,
+ * mla_kernels.cu:1489, 847-848).
+ *   c_kv_pages_fp8 [num_pages, page_size, kv_rank], pe_pages_fp8 [.., rope]   uint8 codes
+ *                  of value / kv_scale, one scale for both pools
+ *   q_absorbed, q_rope, W_uv, out                                          bf16
+ * dtype must be MLA_DTYPE_BF16; kv_rank 512 and rope 64 only; page_size a positive multiple
+ * of 64 and dims->sk = max_pages * page_size.  The fused pass runs on the work list that
+ * mla_attention_paged builds. */
+size_t mla_attention_paged_fp8kv_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                                 int causal, int32_t page_size);
+int mla_attention_paged_fp8kv(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                              const void* q_rope, const void* c_kv_pages_fp8,
+                              const void* pe_pages_fp8, const int32_t* block_table,
+                              const int32_t* seq_lens, int32_t page_size, float kv_scale,
+                              const void* W_uv, double scale, int causal, void* out,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* The work list that mla_attention_paged's fused pass builds on the device from seq_lens,
  * written to `work_list` for inspection (a per-step view of that kernel; no reference
  * counterpart).  int32 layout: [0] item count, [1] keys per chunk, first partial slot [B],

@@ -9,9 +9,11 @@
 // plus one op per step (gemm, rmsnorm, rope, absorb, scores, combine, ctx, out) that runs
 // the very kernels the fused calls run, and the path's neighbours: split_wkv_b (weight
 // prep), kv_append (the cache write) and o_proj (wo); mla_attention_paged and
-// kv_append_paged for a ragged, paged cache (q_absorbed takes [B, Sq] positions for it).  This file only validates tensors, allocates
-// outputs and workspace from torch's caching allocator and passes raw pointers and the
-// current HIP stream to the C ABI; all device work lives in libmla_amd.so.
+// kv_append_paged for a ragged, paged cache (q_absorbed takes [B, Sq] positions for it);
+// mla_attention_fp8kv and mla_attention_paged_fp8kv for an e4m3 cache.  This file only
+// validates tensors, allocates outputs and workspace from torch's caching allocator and
+// passes raw pointers and the current HIP stream to the C ABI; all device work lives in
+// libmla_amd.so.
 //
 // Validation order: shapes and dtypes first, then device, so every shape error is
 // reported (and testable) without a GPU.
@@ -587,6 +589,49 @@ torch::Tensor op_mla_attention_paged(torch::Tensor q_absorbed, torch::Tensor q_r
     return out;
 }
 
+// Attention over a paged fp8 cache: the pools hold e4m3 codes (torch.float8_e4m3fn or
+// their bytes as uint8) of value / kv_scale; sequence b attends to its first seq_lens[b]
+// keys through its row of block_table; the queries, W_uv and the output are bf16.
+torch::Tensor op_mla_attention_paged_fp8kv(torch::Tensor q_absorbed, torch::Tensor q_rope,
+                                           torch::Tensor c_kv_pages, torch::Tensor pe_pages,
+                                           torch::Tensor block_table, torch::Tensor seq_lens,
+                                           double kv_scale, torch::Tensor W_uv, double scale,
+                                           bool causal) {
+    int64_t page = 0;
+    mla_dims_t d = paged_dims(q_absorbed, q_rope, c_kv_pages, pe_pages, block_table, &seq_lens,
+                              &W_uv, &page);
+    TORCH_CHECK(q_absorbed.scalar_type() == torch::kBFloat16,
+                "MLA: an fp8 cache is read with bfloat16 queries (q_absorbed has dtype ",
+                q_absorbed.scalar_type(), ")");
+    check_same_dtype(q_absorbed, q_rope, "q_rope");
+    check_same_dtype(q_absorbed, W_uv, "W_uv");
+    for (const torch::Tensor* t : {&c_kv_pages, &pe_pages})
+        TORCH_CHECK(t->scalar_type() == torch::kFloat8_e4m3fn || t->scalar_type() == torch::kByte,
+                    "MLA: the fp8 cache must be float8_e4m3fn or uint8 codes (got ",
+                    t->scalar_type(), ")");
+    check_device({&q_absorbed, &q_rope, &c_kv_pages, &pe_pages, &block_table, &seq_lens, &W_uv});
+
+    c10::DeviceGuard guard(q_absorbed.device());
+    auto qa = q_absorbed.contiguous();
+    auto qr = q_rope.contiguous();
+    auto ck = c_kv_pages.contiguous();
+    auto pe = pe_pages.contiguous();
+    auto tab = block_table.contiguous();
+    auto lens = seq_lens.contiguous();
+    auto wuv = W_uv.contiguous();
+    auto out = torch::empty({d.batch, d.sq, d.heads, d.v}, qa.options());
+    const size_t wsb = mla_attention_paged_fp8kv_workspace_bytes(MLA_DTYPE_BF16, &d, causal ? 1 : 0,
+                                                                 (int32_t)page);
+    auto ws = workspace(wsb, qa);
+    check_status(mla_attention_paged_fp8kv(MLA_DTYPE_BF16, &d, qa.data_ptr(), qr.data_ptr(),
+                                           ck.data_ptr(), pe.data_ptr(), tab.data_ptr<int32_t>(),
+                                           lens.data_ptr<int32_t>(), (int32_t)page, (float)kv_scale,
+                                           wuv.data_ptr(), scale, causal ? 1 : 0, out.data_ptr(),
+                                           ws.data_ptr(), wsb, current_stream()),
+                 "mla_attention_paged_fp8kv");
+    return out;
+}
+
 // The work list the fused paged pass builds from seq_lens (int32, layout in mla.h).
 torch::Tensor op_attention_work_list(torch::Tensor seq_lens, int64_t Sq, int64_t H, int64_t Sk,
                                      torch::ScalarType dtype) {
@@ -822,6 +867,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv_pages"), py::arg("pe_pages"),
           py::arg("block_table"), py::arg("seq_lens"), py::arg("W_uv"), py::arg("scale"),
           py::arg("causal") = false);
+    m.def("mla_attention_paged_fp8kv", &op_mla_attention_paged_fp8kv,
+          "Attention over a paged fp8 e4m3 cache (codes of value / kv_scale; bf16 queries and "
+          "output): returns out [B, Sq, H, v]",
+          py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv_pages"), py::arg("pe_pages"),
+          py::arg("block_table"), py::arg("seq_lens"), py::arg("kv_scale"), py::arg("W_uv"),
+          py::arg("scale"), py::arg("causal") = false);
     m.def("attention_work_list", &op_attention_work_list,
           "The fused paged pass's device-built work list for seq_lens (int32)",
           py::arg("seq_lens"), py::arg("Sq"), py::arg("H"), py::arg("Sk"), py::arg("dtype"));

@@ -729,10 +729,13 @@ FlashProblem fp8_problem(const mla_dims_t* d, const void* qa, const void* qr, co
     return p;
 }
 
-Fp8Layout fp8_layout(const mla_dims_t* d) {
+// ragged: the paged pool's plan (the balanced work list and its partial slots)
+Fp8Layout fp8_layout(const mla_dims_t* d, bool ragged = false) {
     Fp8Layout L;
     const size_t rows = (size_t)d->batch * d->sq * d->heads;
-    L.flash = plan_flash(fp8_problem(d, nullptr, nullptr, nullptr, nullptr, 1.f, 1.0, 0));
+    FlashProblem fp = fp8_problem(d, nullptr, nullptr, nullptr, nullptr, 1.f, 1.0, 0);
+    fp.ragged = ragged;
+    L.flash = plan_flash(fp);
     L.out = plan_gemm(out_problem(MLA_DTYPE_BF16, d, nullptr, nullptr, nullptr, nullptr));
     size_t o = 0;
     L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
@@ -1089,6 +1092,49 @@ int mla_attention_fp8kv(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
                                         scale, causal);
     MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part), stream),
                 "fp8-cache attention launch");
+    GemmProblem op = out_problem(MLA_DTYPE_BF16, dims, ctx, row_sum, W_uv, out);
+    MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
+    return ok();
+}
+
+size_t mla_attention_paged_fp8kv_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims,
+                                                 int causal, int32_t page_size) {
+    if (!dims || check_fp8_attn(dtype, dims, causal, 1.f) != MLA_OK ||
+        check_pages(dims, page_size) != MLA_OK)
+        return 0;
+    return fp8_layout(dims, true).total;
+}
+
+int mla_attention_paged_fp8kv(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absorbed,
+                              const void* q_rope, const void* c_kv_pages_fp8,
+                              const void* pe_pages_fp8, const int32_t* block_table,
+                              const int32_t* seq_lens, int32_t page_size, float kv_scale,
+                              const void* W_uv, double scale, int causal, void* out,
+                              void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    MLA_CHECK(check_fp8_attn(dtype, dims, causal, kv_scale));
+    MLA_CHECK(check_pages(dims, page_size));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv_pages_fp8, "c_kv_pages_fp8"));
+    MLA_CHECK(check_ptr(pe_pages_fp8, "pe_pages_fp8"));
+    MLA_CHECK(check_ptr(block_table, "block_table"));
+    MLA_CHECK(check_ptr(seq_lens, "seq_lens"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const Fp8Layout L = fp8_layout(dims, true);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+    float* row_sum = at<float>(workspace, L.off_rowsum);
+    float* ctx = at<float>(workspace, L.off_ctx);
+    // the fp8 pass over the pages (each sequence to its own length, the key chunks balanced
+    // by the device-built work list, merged into ctx / row_sum), then 3d
+    FlashProblem fp = fp8_problem(dims, q_absorbed, q_rope, c_kv_pages_fp8, pe_pages_fp8,
+                                  kv_scale, scale, causal);
+    fp.seq_lens = seq_lens;
+    fp.block_table = block_table;
+    fp.page_size = page_size;
+    MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part), stream),
+                "paged fp8-cache attention launch");
     GemmProblem op = out_problem(MLA_DTYPE_BF16, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
     return ok();

@@ -146,6 +146,32 @@ def test_fp8kv_validation(lib):
     assert call(1, float("inf")) == MLA_ERR_INVALID_ARGUMENT
 
 
+def test_paged_fp8kv_validation(lib):
+    """The paged fp8-cache attention takes the fp8 rules (bf16 queries, a positive finite
+    kv_scale) and the page rules (page_size a positive multiple of 64 dividing dims.sk), and
+    sizes its workspace like the dense fp8 call plus the work list and its partial slots."""
+    d = Dims(128, 1, 4992, 7168, 1536, 128, 128, 64, 512, 128)
+    lib.mla_attention_paged_fp8kv_workspace_bytes.restype = ctypes.c_size_t
+    lib.mla_attention_fp8kv_workspace_bytes.restype = ctypes.c_size_t
+    ws = lib.mla_attention_paged_fp8kv_workspace_bytes(1, ctypes.byref(d), 0, 64)
+    dense = lib.mla_attention_fp8kv_workspace_bytes(1, ctypes.byref(d), 0)
+    row_tiles, B = 2, 128
+    items = -(-(4 * 256 // row_tiles + B + 1) // 8) * 8
+    extra = items * 128 * (512 + 2) * 4 + (2 + 2 * B + 2 * items) * 4
+    assert dense > 0 and dense < ws <= dense + extra + 4096
+    assert lib.mla_attention_paged_fp8kv_workspace_bytes(0, ctypes.byref(d), 0, 64) == 0
+    assert lib.mla_attention_paged_fp8kv_workspace_bytes(1, ctypes.byref(d), 0, 96) == 0
+    call = lambda dt, page, s, lens=P16: lib.mla_attention_paged_fp8kv(  # noqa: E731
+        dt, ctypes.byref(d), P16, P16, P16, P16, P16, lens, page, ctypes.c_float(s), P16,
+        ctypes.c_double(13.85), 0, P16, P16, ctypes.c_size_t(ws), None)
+    assert call(0, 64, 1.0) == MLA_ERR_UNSUPPORTED and "bf16 queries" in _err(lib)
+    assert call(1, 64, 0.0) == MLA_ERR_INVALID_ARGUMENT and "kv_scale" in _err(lib)
+    assert call(1, 100, 1.0) == MLA_ERR_INVALID_ARGUMENT and "page_size" in _err(lib)
+    assert call(1, 64, 1.0, None) == MLA_ERR_INVALID_ARGUMENT and "seq_lens must not be NULL" in _err(lib)
+    d.sk = 4989
+    assert call(1, 64, 1.0) == MLA_ERR_INVALID_ARGUMENT and "max_pages * page_size" in _err(lib)
+
+
 def test_gemm_split_needs_workspace(lib):
     need = lib.mla_gemm_workspace_bytes(F32, 1, 1536, 7168)
     assert need > 0, "B=1 2a1 is split over K"
@@ -437,6 +463,16 @@ def test_binding_paged_shape_errors(ext):
         ext.q_absorbed(torch.zeros(2, 1, 64), torch.zeros(64, 32), torch.zeros(32),
                        torch.zeros(32, 4 * 24), torch.zeros(4, 16, 16),
                        torch.zeros(3, 1, dtype=torch.int64), 16, 8, 1e-6)
+    f8 = torch.zeros(5, 64, 16, dtype=torch.uint8), torch.zeros(5, 64, 8, dtype=torch.uint8)
+    bf = lambda t: t.to(torch.bfloat16)  # noqa: E731
+    with pytest.raises(RuntimeError, match="bfloat16 queries"):
+        ext.mla_attention_paged_fp8kv(qa, qr, *f8, tab, sl, 1.0, wuv, 1.0)
+    with pytest.raises(RuntimeError, match="float8_e4m3fn or uint8"):
+        ext.mla_attention_paged_fp8kv(bf(qa), bf(qr), bf(ck), bf(pe), tab, sl, 1.0, bf(wuv), 1.0)
+    with pytest.raises(RuntimeError, match="block_table must be int32"):
+        ext.mla_attention_paged_fp8kv(bf(qa), bf(qr), *f8, tab.long(), sl, 1.0, bf(wuv), 1.0)
+    with pytest.raises(RuntimeError, match="ROCm GPU device"):
+        ext.mla_attention_paged_fp8kv(bf(qa), bf(qr), *f8, tab, sl, 1.0, bf(wuv), 1.0)
 
 
 

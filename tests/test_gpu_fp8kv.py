@@ -116,3 +116,88 @@ def test_fp8kv_close_to_the_bf16_cache(ext):
     pe16 = (pe.float() * kv_scale).to(BF)
     out16 = ext.mla_attention(*(t.to(DEV) for t in (qa, qr, ck16, pe16, wuv)), SCALE).cpu().float()
     assert (out8 - out16).abs().max() <= 2e-2 * out16.abs().max() + 2e-2
+
+
+# ---- paged fp8 cache (mla_attention_paged_fp8kv)
+
+def paged_fp8_inputs(B, Sq, lens, page, max_pages, seed, spare=5):
+    """fp8_inputs' queries and W_uv with a shuffled pool of B*max_pages + spare pages (a
+    sequence's pages scattered among the others' and unused ones) of e4m3 codes, one scale
+    amax / 448 for both pools."""
+    g = torch.Generator().manual_seed(seed)
+    s = 1 / math.sqrt(D.kv_rank)
+    n_pages = B * max_pages + spare
+    table = torch.randperm(n_pages, generator=g)[:B * max_pages].reshape(B, max_pages).int()
+    qa = (torch.randn(B, Sq, D.n_heads, D.kv_rank, generator=g) * s).to(BF)
+    qr = (torch.randn(B, Sq, D.n_heads, D.rope, generator=g) * s).to(BF)
+    ck = torch.randn(n_pages, page, D.kv_rank, generator=g)
+    pe = torch.randn(n_pages, page, D.rope, generator=g)
+    wuv = (torch.randn(D.n_heads, D.v, D.kv_rank, generator=g) * s).to(BF)
+    kv_scale = float(max(ck.abs().max(), pe.abs().max())) / 448.0
+    return (qa, qr, (ck / kv_scale).to(F8), (pe / kv_scale).to(F8), table,
+            torch.tensor(lens, dtype=torch.int32), kv_scale, wuv)
+
+
+def paged_fp8_oracle(qa, qr, ck, pe, table, sl, kv_scale, wuv, causal=False):
+    """The paged oracle (each sequence over its own gathered keys) on the decoded pools."""
+    return R.mla_attention_paged(qa.float(), qr.float(), R.decode_e4m3(ck, kv_scale),
+                                 R.decode_e4m3(pe, kv_scale), table, sl, wuv.float(), SCALE,
+                                 causal)
+
+
+def run_paged_fp8(ext, qa, qr, ck, pe, table, sl, kv_scale, wuv, causal=False):
+    return ext.mla_attention_paged_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe, table, sl)),
+                                         kv_scale, wuv.to(DEV), SCALE, causal).cpu()
+
+
+@KERNELS
+@pytest.mark.parametrize("page,lens,causal,Sq", [
+    (64, [640, 1, 333, 65], False, 1),
+    (128, [1000, 129, 500], False, 1),
+    (64, [200, 77, 640], True, 4),
+    (64, [0, 300, 0, 64], False, 1),
+])
+def test_paged_fp8kv_matches_oracle(ext, monkeypatch, spec, page, lens, causal, Sq):
+    """Ragged lengths (not multiples of the page), shuffled pools and, in the last case,
+    empty sequences, whose rows are zeros as in the oracle."""
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    B = len(lens)
+    max_pages = max(1, -(-max(lens) // page))
+    inp = paged_fp8_inputs(B, Sq, lens, page, max_pages, seed=page + 7 * B)
+    out = run_paged_fp8(ext, *inp, causal=causal)
+    assert out.dtype == BF and torch.isfinite(out.float()).all()
+    torch.testing.assert_close(out.float(), paged_fp8_oracle(*inp, causal=causal), **TOL)
+    for b, n in enumerate(lens):
+        if n == 0:
+            assert not out[b].float().any()
+
+
+def test_paged_fp8kv_equals_dense_layout(ext):
+    """Full lengths with the pages in sequence order hold the dense cache: the paged call
+    agrees with mla_attention_fp8kv on it, and with the oracle."""
+    B, Sk, page = 3, 4992, 64
+    qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(B, 1, Sk, seed=31)
+    mp = Sk // page
+    table = torch.arange(B * mp, dtype=torch.int32).reshape(B, mp)
+    sl = torch.full((B,), Sk, dtype=torch.int32)
+    dense = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale,
+                                    wuv.to(DEV), SCALE).cpu()
+    paged = run_paged_fp8(ext, qa, qr, ck.reshape(-1, page, D.kv_rank),
+                          pe.reshape(-1, page, D.rope), table, sl, kv_scale, wuv)
+    torch.testing.assert_close(paged.float(), dense.float(), **TOL)
+    torch.testing.assert_close(paged.float(),
+                               R.mla_attention_fp8kv(qa, qr, ck, pe, kv_scale, wuv, SCALE), **TOL)
+
+
+@KERNELS
+def test_paged_fp8kv_b128_ragged_full_size(ext, monkeypatch, spec):
+    """B=128 decode over a ragged paged fp8 cache up to Sk=4989 keys, every sequence
+    against the oracle."""
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    g = torch.Generator().manual_seed(128)
+    lens = torch.randint(1, 4990, (128,), generator=g).tolist()
+    lens[0], lens[1] = 4989, 1
+    page = 64
+    inp = paged_fp8_inputs(128, 1, lens, page, -(-4989 // page), seed=128)
+    out = run_paged_fp8(ext, *inp)
+    torch.testing.assert_close(out.float(), paged_fp8_oracle(*inp), **TOL)
