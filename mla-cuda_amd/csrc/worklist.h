@@ -28,10 +28,17 @@
 namespace mla {
 
 constexpr int kWlHead = 2;
-// A ragged list spreads the total key count over kWlPerCu workgroups per CU: at B=128 with
-// lengths uniform in [1, 4989] (fp32), 1 per CU took 1185 us, 2: 950, 3: 901, 4: 870-905,
-// 6: 926, 8: 907 (more pieces shorten the tail; each piece costs its Q load and partials).
+// A ragged list spreads the total key count over kWlPerCu workgroups per CU (fp32) or
+// kWlPerCu16 (bf16, fp16 and the fp8 cache).  At B=128 with lengths uniform in [1, 4989],
+// fp32: 1 per CU took 1185 us, 2: 950, 3: 901, 4: 870-905, 6: 926, 8: 907 (more pieces
+// shorten the tail; each piece costs its Q load and partials).  16-bit: 1 per CU took
+// 150.5 us, 2: 165.7, 3: 185.4, 4: 202.4 (fp8 cache 186.3 / 208.1 / 229.9 / 254.2; one
+// sequence of 4989 keys per seven of 300: bf16 95.7 us at 1 against 153.9 at 4): a 16-bit
+// key block is ~5x shorter than an fp32 one, so a piece's fixed cost weighs ~5x more.
+// The list is sized for the larger kWlPerCu.
 constexpr int kWlPerCu = 4;
+constexpr int kWlPerCu16 = 1;
+static_assert(kWlPerCu16 <= kWlPerCu, "the list is sized for kWlPerCu pieces per CU");
 constexpr int kWlBuckets = 256;     // length buckets of the last-chunk counting sort
 constexpr int kWlThreads = 256;     // threads of the device builder
 
@@ -107,13 +114,14 @@ MLA_HD int wl_bucket(int L, int chunk) {
 // Chunk before the fit check, from the batch's total, minimum and maximum key counts:
 //   every sequence the same length L -> the dense plan's keys per split for L, so the list
 //     reproduces the dense launch exactly (same key ranges, same merge order);
-//   otherwise -> the total key count spread over kWlPerCu workgroups per CU (a multiple of
-//     the key block, so a wave's keys never straddle a page; at least 4 blocks; at most
-//     the key span rounded up to a block).
+//   otherwise -> the total key count spread over kWlPerCu (fp32, 16-key blocks) or
+//     kWlPerCu16 (16-bit, 32-key blocks) workgroups per CU (a multiple of the key block,
+//     so a wave's keys never straddle a page; at least 4 blocks; at most the key span
+//     rounded up to a block).
 MLA_HD int wl_initial_chunk(long long tot, int mn, int mx, int B, int Sk, int row_tiles,
                             int block_keys) {
     if (mn == mx) return dense_keys_per_split(wl_max(1, mx), B * row_tiles, block_keys);
-    const long long wgs = (long long)kWlPerCu * kNumCUs;
+    const long long wgs = (long long)(block_keys == 16 ? kWlPerCu : kWlPerCu16) * kNumCUs;
     const long long want = (tot * row_tiles + wgs - 1) / wgs;
     const long long cap = (long long)(Sk + block_keys - 1) / block_keys * block_keys;
     long long chunk = (want + block_keys - 1) / block_keys * block_keys;
