@@ -701,11 +701,21 @@ int scratch_for_stream(hipStream_t stream, void** out) {
                     "covers", dev, kMaxDevices);
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
-        if (dev != cur) MLA_TRY_HIP(hipSetDevice(dev), "hipSetDevice");
+        // The first call on a device may come while the caller captures `stream` into a
+        // graph.  The lookup enqueues nothing, but it can load the code object, which
+        // strict capture modes refuse; this thread runs it in relaxed mode and restores
+        // the caller's mode afterwards.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        MLA_TRY_HIP(hipThreadExchangeStreamCaptureMode(&mode), "capture mode (relax)");
+        hipError_t e = hipSuccess;
         void* p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (dev != cur) MLA_TRY_HIP(hipSetDevice(cur), "hipSetDevice (restore)");
+        if (dev != cur) e = hipSetDevice(dev);
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t e_back = dev != cur ? hipSetDevice(cur) : hipSuccess;
+        const hipError_t e_mode = hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess) return hip_fail(e, "scratch symbol lookup");
+        if (e_back != hipSuccess) return hip_fail(e_back, "hipSetDevice (restore)");
+        if (e_mode != hipSuccess) return hip_fail(e_mode, "capture mode (restore)");
         if (!p) return fail(MLA_ERR_HIP, "scratch symbol lookup returned NULL");
         g_scratch_ptr[dev] = p;
     }
@@ -758,6 +768,16 @@ int check_fp8_attn(mla_dtype_t dtype, const mla_dims_t* dims, int causal, float 
         return fail(MLA_ERR_INVALID_ARGUMENT, "fp8 cache rows must be multiples of 16 bytes");
     if (!flash_supported(fp8_problem(dims, nullptr, nullptr, nullptr, nullptr, kv_scale, 1.0, causal)))
         return fail(MLA_ERR_UNSUPPORTED, "an fp8 cache needs kv_rank 512 and rope 64");
+    // the fused pass forms 32-bit per-lane buffer offsets within one sequence: its query
+    // rows (bf16, 1 KiB each) and its dense cache rows (one byte per element) must span less
+    // than 2^31 bytes -- the bound flash_eligible puts on the 16-bit path, which has the
+    // per-step path to fall back on; the fp8 cache has none
+    constexpr int64_t kRange = 0x7fffffff;
+    if ((int64_t)dims->sq * dims->heads * dims->kv_rank * 2 >= kRange ||
+        (int64_t)dims->sk * dims->kv_rank >= kRange)
+        return fail(MLA_ERR_UNSUPPORTED, "an fp8-cache call needs Sq * heads * kv_rank * 2 and "
+                    "Sk * kv_rank below 2^31 bytes (Sq %d, heads %d, Sk %d)", dims->sq,
+                    dims->heads, dims->sk);
     return MLA_OK;
 }
 

@@ -146,6 +146,30 @@ def test_fp8kv_validation(lib):
     assert call(1, float("inf")) == MLA_ERR_INVALID_ARGUMENT
 
 
+def test_fp8kv_refuses_query_spans_past_32_bit_offsets(lib):
+    """The fused fp8 pass forms 32-bit buffer offsets within a sequence's query rows (bf16,
+    1 KiB each) and has no per-step path to fall back on: Sq * heads * 1 KiB >= 2^31 is
+    refused (UNSUPPORTED, zero workspace), dense and paged, where bf16 at the same shape
+    falls back to the split path.  One query row less than the limit is accepted."""
+    lib.mla_attention_fp8kv_workspace_bytes.restype = ctypes.c_size_t
+    lib.mla_attention_paged_fp8kv_workspace_bytes.restype = ctypes.c_size_t
+    big = Dims(1, 16384, 64, 7168, 1536, 128, 128, 64, 512, 128)     # 2 GiB of query rows
+    assert lib.mla_attention_fp8kv_workspace_bytes(1, ctypes.byref(big), 0) == 0
+    assert lib.mla_attention_paged_fp8kv_workspace_bytes(1, ctypes.byref(big), 0, 64) == 0
+    st = lib.mla_attention_fp8kv(1, ctypes.byref(big), P16, P16, P16, P16, ctypes.c_float(1.0),
+                                 P16, ctypes.c_double(13.85), 0, P16, P16,
+                                 ctypes.c_size_t(1 << 40), None)
+    assert st == MLA_ERR_UNSUPPORTED and "2^31" in _err(lib)
+    st = lib.mla_attention_paged_fp8kv(1, ctypes.byref(big), P16, P16, P16, P16, P16, P16, 64,
+                                       ctypes.c_float(1.0), P16, ctypes.c_double(13.85), 0, P16,
+                                       P16, ctypes.c_size_t(1 << 40), None)
+    assert st == MLA_ERR_UNSUPPORTED and "2^31" in _err(lib)
+    # the bf16 path at the same shape still plans (on the per-step kernels)
+    assert lib.mla_attention_workspace_bytes(1, ctypes.byref(big), 0) > 0
+    ok = Dims(1, 16383, 16384, 7168, 1536, 128, 128, 64, 512, 128)   # 2^31 - 128 KiB
+    assert lib.mla_attention_fp8kv_workspace_bytes(1, ctypes.byref(ok), 0) > 0
+
+
 def test_paged_fp8kv_validation(lib):
     """The paged fp8-cache attention takes the fp8 rules (bf16 queries, a positive finite
     kv_scale) and the page rules (page_size a positive multiple of 64 dividing dims.sk), and

@@ -5,7 +5,8 @@ Per step, the oracle runs in fp32 on the very bf16 values the kernel reads (and,
 kernel rounds an fp32 operand to bf16 before its MFMA -- q_raw in 2c, p*alpha in 3c, ctx in
 3d -- on the rounded operand), so each step is held to fp32-accumulation accuracy.  The
 whole layer is compared with the fp32 oracle on the bf16-rounded inputs at the bf16
-tolerance rtol 2e-2 (atol 2e-2 on O(1) outputs).
+tolerance of tests/attn_cases.py: rtol 2e-2, atol 2e-3 on the layer's outputs (standard
+deviation ~0.03 at Sk = 4989).
 """
 
 from __future__ import annotations
@@ -15,6 +16,7 @@ import math
 import pytest
 import torch
 
+import attn_cases as C
 from oracle import mla_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -124,7 +126,7 @@ def test_layer_bf16_vs_fp32_oracle(ext, B, Sq, Sk):
     f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
     ref = R.mla_layer(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], f32["wkv_b"],
                       f32["c_kv"], f32["pe_cache"], f32["positions"])
-    torch.testing.assert_close(out.float().cpu(), ref, rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(out.float().cpu(), ref, **C.tol(BF, ref))
 
 
 def test_layer_bf16_cfg4_full_size(ext):
@@ -136,4 +138,4 @@ def test_layer_bf16_cfg4_full_size(ext):
     f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
     ref = R.mla_layer(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], f32["wkv_b"],
                       f32["c_kv"], f32["pe_cache"], f32["positions"])
-    torch.testing.assert_close(out.float().cpu(), ref, rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(out.float().cpu(), ref, **C.tol(BF, ref))

@@ -2,12 +2,18 @@
 
 mla_attention takes the fused path for bf16 and fp32 at R = 512, D = 64;
 MLA_ATTENTION_PATH=split selects the per-step kernels.  Both are held to the float64
-oracle on the very values the kernels read -- bf16 at rtol/atol 2e-2 (P is rounded to bf16
-inside the kernel), fp32 at rtol/atol 1e-4 -- and to each other.  Shapes cover a partial
-last key block, a single key, key splits merged across workgroups (small B), causal masks
-with Sq > 1, splits that a tile's causal limit leaves empty, row tiles that do not fill 64
-rows (H = 40, H = 1), and a row maximum that keeps rising: past the bf16 kernel's rescale
-slack, and past the fp32 kernel's exponent headroom (which restarts its pass).
+oracle on the very values the kernels read, and to each other.  The queries have the
+layer's spread (scores of unit standard deviation, tests/attn_cases.py), so the softmax
+is far from flat; tolerances are fp32 rtol/atol 1e-4 and bf16 rtol 2e-2 with atol 2e-3
+(fp16 1e-2 / 1e-3) on the long-cache outputs of standard deviation ~0.03, an atol that
+grows with the output's largest element only where a few keys make the outputs O(1)
+(attn_cases.tol).  tests/test_parity_power_cpu.py shows on these inputs that a dropped
+rope term, an ignored causal mask, a flat softmax, a wrong score scale or a stale key
+block each fail them.  Shapes cover a partial last key block, a single key, key splits
+merged across workgroups (small B), causal masks with Sq > 1, splits that a tile's causal
+limit leaves empty, row tiles that do not fill 64 rows (H = 40, H = 1), and a row maximum
+that keeps rising: past the bf16 kernel's rescale slack, and past the fp32 kernel's
+exponent headroom (which restarts its pass).
 """
 
 from __future__ import annotations
@@ -17,6 +23,7 @@ import math
 import pytest
 import torch
 
+import attn_cases as C
 from oracle import mla_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -26,8 +33,7 @@ D = R.DSV3
 SCALE = math.sqrt(D.qk_head)
 BF = torch.bfloat16
 F32 = torch.float32
-TOLS = {BF: dict(rtol=2e-2, atol=2e-2), F32: dict(rtol=1e-4, atol=1e-4)}
-TOL = TOLS[BF]
+TOLS = {F32: C.TOL_F32}
 DTYPES = pytest.mark.parametrize("dt", [BF, F32], ids=["bf16", "f32"])
 
 
@@ -43,11 +49,12 @@ def gpu(t):
     return t.to(DEV)
 
 
-def inputs(B, Sq, Sk, H=D.n_heads, seed=0, qs=0.05, dt=BF):
-    g = torch.Generator().manual_seed(seed)
-    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(dt)  # noqa: E731
-    return (mk(B, Sq, H, D.kv_rank, sc=qs), mk(B, Sq, H, D.rope, sc=qs), mk(B, Sk, D.kv_rank),
-            mk(B, Sk, D.rope), mk(H, D.v, D.kv_rank, sc=1 / math.sqrt(D.kv_rank)))
+def inputs(B, Sq, Sk, H=D.n_heads, seed=0, dt=BF):
+    return C.attn_inputs(B, Sq, Sk, H=H, seed=seed, dt=dt)
+
+
+def close(got, ref, dt):
+    torch.testing.assert_close(got, ref, **C.tol(dt, ref))
 
 
 def oracle(args, causal):
@@ -68,25 +75,14 @@ def run(ext, args, causal, path=None, monkeypatch=None):
     return out.float().cpu()
 
 
-SHAPES = [
-    # B, Sq, Sk, causal
-    (1, 1, 1, False),
-    (1, 1, 5, False),
-    (2, 1, 32, False),
-    (2, 1, 33, False),
-    (3, 2, 300, True),
-    (1, 4, 700, True),
-    (1, 1, 4989, False),     # 39 key splits, merged
-    (4, 1, 4989, False),
-    (2, 16, 1000, True),
-]
+SHAPES = C.FUSED_CASES
 
 
 @DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,causal", SHAPES)
 def test_fused_vs_oracle(ext, dt, B, Sq, Sk, causal):
     args = inputs(B, Sq, Sk, seed=Sk + B, dt=dt)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[dt])
+    close(run(ext, args, causal), oracle(args, causal), dt)
 
 
 @DTYPES
@@ -95,8 +91,7 @@ def test_fused_vs_split_path(ext, monkeypatch, dt, B, Sq, Sk, causal):
     args = inputs(B, Sq, Sk, seed=7 * Sk + B, dt=dt)
     fused = run(ext, args, causal)
     split = run(ext, args, causal, "split", monkeypatch)
-    tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
-    torch.testing.assert_close(fused, split, **tol)
+    close(fused, split, dt)
 
 
 @DTYPES
@@ -104,7 +99,7 @@ def test_fused_vs_split_path(ext, monkeypatch, dt, B, Sq, Sk, causal):
                                               (3, 1, 100, 1, False)])
 def test_fused_partial_row_tiles(ext, dt, B, Sq, Sk, H, causal):
     args = inputs(B, Sq, Sk, H=H, seed=H + Sk, dt=dt)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[dt])
+    close(run(ext, args, causal), oracle(args, causal), dt)
 
 
 def test_fused_rising_row_max(ext):
@@ -120,7 +115,7 @@ def test_fused_rising_row_max(ext):
     ramp = torch.arange(Sk, dtype=torch.float32) * 0.0525
     ck = (ck.float() * 0.05 + ramp[None, :, None] * u).to(BF)
     args = (qa, qr, ck, pe, wuv)
-    torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOL)
+    close(run(ext, args, False), oracle(args, False), BF)
 
 
 # bf16 and fp16 run on two kernels: eight specialised waves (flash16x_kernel, the default:
@@ -128,21 +123,27 @@ def test_fused_rising_row_max(ext):
 # key-split waves (flash16_kernel); MLA_FLASH16_SPEC=1 / 0 forces either, and both must
 # match the oracle everywhere
 H16 = torch.float16
-HALF_TOLS = {BF: TOLS[BF], H16: dict(rtol=1e-2, atol=1e-2)}
 FP16_KERNELS = pytest.mark.parametrize("spec", ["1", "0"], ids=["specialised", "key-split"])
 HALF_DTYPES = pytest.mark.parametrize("dt", [BF, H16], ids=["bf16", "f16"])
 
 
 @FP16_KERNELS
 @HALF_DTYPES
-@pytest.mark.parametrize("B,Sq,Sk,H,causal", [
-    (1, 1, 5, 128, False), (2, 1, 33, 128, False), (3, 2, 300, 128, True),
-    (4, 1, 4989, 128, False), (2, 16, 1000, 128, True), (2, 3, 257, 40, False),
-    (1, 512, 1024, 1, True)])
+@pytest.mark.parametrize("B,Sq,Sk,H,causal", C.FLASH16_CASES)
 def test_16bit_kernels_vs_oracle(ext, monkeypatch, spec, dt, B, Sq, Sk, H, causal):
     monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
     args = inputs(B, Sq, Sk, H=H, seed=3 * Sk + B, dt=dt)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **HALF_TOLS[dt])
+    close(run(ext, args, causal), oracle(args, causal), dt)
+
+
+@FP16_KERNELS
+def test_16bit_kernels_full_size(ext, monkeypatch, spec):
+    """B=128, Sk=4989 in bf16 (the cfg4 attention) on either 16-bit kernel, every sequence
+    against the oracle."""
+    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    args = inputs(128, 1, 4989, seed=78, dt=BF)
+    ref = R.mla_attention_official(*(t.float() for t in args), SCALE)
+    close(run(ext, args, False), ref, BF)
 
 
 @FP16_KERNELS
@@ -191,7 +192,7 @@ def set_fp32_kernel(monkeypatch, wave):
 def test_fp32_kernels_vs_oracle(ext, monkeypatch, wave, B, Sq, Sk, H, causal):
     set_fp32_kernel(monkeypatch, wave)
     args = inputs(B, Sq, Sk, H=H, seed=3 * Sk + B, dt=F32)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[F32])
+    close(run(ext, args, causal), oracle(args, causal), F32)
 
 
 @FP32_KERNELS
@@ -218,7 +219,7 @@ def test_fp32_decode_3d_with_merge(ext, monkeypatch, small, B, Sq, Sk, causal):
     Both against the oracle."""
     monkeypatch.setenv("MLA_OUT_SMALL", small)
     args = inputs(B, Sq, Sk, seed=5 * Sk + B, dt=F32)
-    torch.testing.assert_close(run(ext, args, causal), oracle(args, causal), **TOLS[F32])
+    close(run(ext, args, causal), oracle(args, causal), F32)
 
 
 @DTYPES
@@ -228,7 +229,7 @@ def test_fused_key_split_past_one_round(ext, dt, B, Sq, Sk):
     planner splits the keys so that the last round is not nearly empty; every sequence
     against the oracle."""
     args = inputs(B, Sq, Sk, seed=B + Sk, dt=dt)
-    torch.testing.assert_close(run(ext, args, False), oracle(args, False), **TOLS[dt])
+    close(run(ext, args, False), oracle(args, False), dt)
 
 
 @FP32_KERNELS
@@ -267,14 +268,13 @@ def test_fused_deterministic(ext, dt):
 def test_fused_full_size_vs_split_path(ext, monkeypatch, dt):
     """B=128, Sq=1, Sk=4989 (the cfg2 / cfg4 attention): the fused and per-step paths agree
     on every sequence; the oracle checks three of them."""
-    args = inputs(128, 1, 4989, seed=0, qs=0.1, dt=dt)
+    args = inputs(128, 1, 4989, seed=0, dt=dt)
     fused = run(ext, args, False)
     split = run(ext, args, False, "split", monkeypatch)
-    tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
-    torch.testing.assert_close(fused, split, **tol)
+    close(fused, split, dt)
     pick = [0, 77, 127]
     ref = oracle(tuple(t[pick] for t in args[:4]) + (args[4],), False)
-    torch.testing.assert_close(fused[pick], ref, **TOLS[dt])
+    close(fused[pick], ref, dt)
 
 
 @DTYPES
@@ -296,11 +296,10 @@ def test_attn_ctx_step_vs_oracle(ext, monkeypatch, dt, B, Sq, Sk, causal):
     if causal:
         s = s.masked_fill(~R.causal_mask(Sq, Sk)[None, :, None, :], float("-inf"))
     ref = torch.einsum("bqhk,bkr->bqhr", torch.softmax(s, dim=-1), ck.double()).float()
-    tol = dict(rtol=1e-2, atol=1e-2) if dt == BF else TOLS[F32]
-    torch.testing.assert_close(got, ref, **tol)
+    close(got, ref, dt)
     out = ext.out(ctx, rs, gpu(wuv))
     own = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
     monkeypatch.setenv("MLA_OUT_SMALL", "0")
     full = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
     assert torch.equal(out, full)
-    torch.testing.assert_close(own.float().cpu(), full.float().cpu(), **TOLS[dt])
+    close(own.float().cpu(), full.float().cpu(), dt)

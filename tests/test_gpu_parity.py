@@ -9,8 +9,8 @@ copied to the GPU, so HIP path and oracle see identical values.  Tolerances:
 * per-step fp32 intermediates: rtol/atol 1e-4 on O(1) quantities, 1e-5 on softmax factors.
 
 Layer tests compare every sequence with the oracle, the headline size (B=128, Sk=4989)
-included; the long-context causal shape compares its whole Q path and 16 query rows of the
-attention, each against the oracle on exactly the keys it sees.
+included; the long-context causal shape compares its whole Q path and all 512 query rows
+of the attention, each against the oracle on exactly the keys it sees.
 """
 
 from __future__ import annotations
@@ -270,9 +270,11 @@ def test_layer_cfg2_full_size(ext):
 def test_layer_cfg5_fused_causal_full_size(ext):
     """The chunked-prefill configuration through the path bench.py times: q_absorbed at
     Sq=128 with positions Sk-128 .. Sk-1, then the fused mla_attention(causal=True), B=4,
-    Sk=32768, fp32.  The Q path is compared whole; the attention on 16 (sequence, query)
-    rows -- each sequence's first and last query and two between -- against the oracle on
-    exactly the keys each query sees (key j visible to query s iff j <= Sk - Sq + s)."""
+    Sk=32768, fp32.  The Q path is compared whole, and so is the attention: all 512
+    (sequence, query) rows against the oracle on exactly the keys each query sees (key j
+    visible to query s iff j <= Sk - Sq + s).  The oracle runs in blocks of 32 queries:
+    queries s0 .. s0+31 over keys [0, Sk - Sq + s0 + 32) are the causal problem of
+    R.causal_mask(32, Sk - Sq + s0 + 32), the same visibility rule."""
     B, Sq, Sk = 4, 128, 32768
     inp = R.make_inputs(B, Sq, Sk, seed=0)
     qa, qr, out = run_layer(ext, inp, causal=True)
@@ -282,14 +284,17 @@ def test_layer_cfg5_fused_causal_full_size(ext):
                                         W_uk, inp["positions"], D.nope, D.rope)
     torch.testing.assert_close(qa.cpu(), rqa, **TOL)
     torch.testing.assert_close(qr.cpu(), rqr, **TOL)
-    qa_c, qr_c = qa.cpu(), qr.cpu()
+    qa_c, qr_c, out_c = qa.cpu(), qr.cpu(), out.cpu()
+    step = 32
     for b in range(B):
-        for s in (0, 41 + 7 * b, 90 - 5 * b, Sq - 1):
-            lim = Sk - Sq + s + 1
-            ref = R.mla_attention_official(qa_c[b:b + 1, s:s + 1], qr_c[b:b + 1, s:s + 1],
+        for s0 in range(0, Sq, step):
+            lim = Sk - Sq + s0 + step
+            ref = R.mla_attention_official(qa_c[b:b + 1, s0:s0 + step],
+                                           qr_c[b:b + 1, s0:s0 + step],
                                            inp["c_kv"][b:b + 1, :lim],
-                                           inp["pe_cache"][b:b + 1, :lim], W_uv, SCALE)
-            torch.testing.assert_close(out[b, s].cpu(), ref[0, 0], **TOL)
+                                           inp["pe_cache"][b:b + 1, :lim], W_uv, SCALE,
+                                           causal=True)
+            torch.testing.assert_close(out_c[b, s0:s0 + step], ref[0], **TOL)
 
 
 def test_reference_input_convention(ext):

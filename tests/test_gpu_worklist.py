@@ -19,6 +19,7 @@ import pytest
 import torch
 
 import wl_check as W
+import attn_cases as C
 from oracle import mla_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -96,8 +97,8 @@ def test_zero_length_sequences_give_zero_rows(ext, monkeypatch, path, causal):
     n_pages = B * mp + 2
     table = torch.randperm(n_pages, generator=g)[:B * mp].reshape(B, mp).int()
     s = 1 / math.sqrt(D.kv_rank)
-    qa = torch.randn(B, Sq, D.n_heads, D.kv_rank, generator=g) * s
-    qr = torch.randn(B, Sq, D.n_heads, D.rope, generator=g) * s
+    qa = torch.randn(B, Sq, D.n_heads, D.kv_rank, generator=g) * C.LAYER_QA_STD
+    qr = torch.randn(B, Sq, D.n_heads, D.rope, generator=g) * C.LAYER_QR_STD
     ck = torch.randn(n_pages, page, D.kv_rank, generator=g)
     pe = torch.randn(n_pages, page, D.rope, generator=g)
     wuv = torch.randn(D.n_heads, D.v, D.kv_rank, generator=g) * s

@@ -4,7 +4,10 @@ It is called through the C ABI (ctypes on libmla_amd.so, device pointers of torc
 torch's current stream) and compared with mla_attention, the entry point whose kernels it
 shares, called through the C ABI with a caller workspace: bit for bit on two calls in a row
 (the second with a smaller input, so it runs in scratch left over from the first), in fp32
-and bf16, and against the CPU oracle.  A shape over the scratch limit is refused.
+and bf16, and against the CPU oracle.  A shape over the scratch limit is refused.  The first
+test captures mla_attention_noalloc into a graph (torch.cuda.CUDAGraph); run first in a fresh
+process, that capture holds the call's first use on the device, where the library looks up
+the scratch array's address.
 """
 
 from __future__ import annotations
@@ -16,6 +19,7 @@ import os
 import pytest
 import torch
 
+import attn_cases as C
 from oracle import mla_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -48,7 +52,8 @@ def _inputs(B, Sq, Sk, seed, dtype):
     g = torch.Generator().manual_seed(seed)
     s = 1 / math.sqrt(D.kv_rank)
     mk = lambda *shape, sc=1.0: (torch.randn(*shape, generator=g) * sc).to(dtype)  # noqa: E731
-    return (mk(B, Sq, D.n_heads, D.kv_rank, sc=s), mk(B, Sq, D.n_heads, D.rope, sc=s),
+    return (mk(B, Sq, D.n_heads, D.kv_rank, sc=C.LAYER_QA_STD),
+            mk(B, Sq, D.n_heads, D.rope, sc=C.LAYER_QR_STD),
             mk(B, Sk, D.kv_rank), mk(B, Sk, D.rope), mk(D.n_heads, D.v, D.kv_rank, sc=s))
 
 
@@ -73,6 +78,39 @@ def _call(lib, noalloc, dt, host, causal):
     return out.cpu()
 
 
+def test_noalloc_under_graph_capture(lib):
+    """mla_attention_noalloc captured into a graph (in a fresh process, its first call on the
+    device, made inside the capture) and replayed four times with new inputs copied into
+    the captured buffers; eager mla_attention and eager mla_attention_noalloc calls run
+    between the replays, and every replay equals mla_attention bit for bit."""
+    dtype, dt, B, Sq, Sk = torch.bfloat16, 1, 4, 1, 1000
+    host = _inputs(B, Sq, Sk, seed=60, dtype=dtype)
+    bufs = [t.to(DEV) for t in host]
+    out = torch.empty(B, Sq, D.n_heads, D.v, dtype=dtype, device=DEV)
+    d = Dims(B, Sq, Sk, 7168, 1536, D.n_heads, 128, D.rope, D.kv_rank, D.v)
+    ptrs = [ctypes.c_void_p(t.data_ptr()) for t in bufs]
+    torch.cuda.synchronize()
+    print("noalloc graph capture: bf16 B=4 Sq=1 Sk=1000", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        st = lib.mla_attention_noalloc(dt, ctypes.byref(d), *ptrs, ctypes.c_double(SCALE), 0,
+                                       ctypes.c_void_p(out.data_ptr()), stream)
+    assert st == MLA_OK, lib.mla_last_error().decode()
+    torch.cuda.synchronize()
+    for i in range(4):
+        h = host if i == 0 else _inputs(B, Sq, Sk, seed=60 + i, dtype=dtype)
+        for buf, src in zip(bufs, h):
+            buf.copy_(src.to(DEV))
+        print(f"noalloc graph replay {i}", flush=True)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.cpu()
+        want = _call(lib, False, dt, h, False)
+        assert torch.equal(got, want), f"replay {i} differs from mla_attention"
+        assert torch.equal(_call(lib, True, dt, h, False), want)
+
+
 @pytest.mark.parametrize("dtype,dt", [(torch.float32, 0), (torch.bfloat16, 1)],
                          ids=["f32", "bf16"])
 def test_noalloc_matches_mla_attention(lib, dtype, dt):
@@ -86,8 +124,7 @@ def test_noalloc_matches_mla_attention(lib, dtype, dt):
         if i == 1:
             f = [t.float() for t in host]
             oracle = R.mla_attention_official(*f, SCALE, causal=causal)
-            tol = 1e-4 if dtype == torch.float32 else 2e-2
-            torch.testing.assert_close(got.float(), oracle, rtol=tol, atol=tol)
+            torch.testing.assert_close(got.float(), oracle, **C.tol(dtype, oracle))
 
 
 def test_noalloc_refuses_a_shape_over_its_scratch(lib):
