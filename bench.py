@@ -21,7 +21,10 @@ per-step GFLOP/s, GB/s, MFMA % and HBM % (algorithmic work, formulas below) and 
 
 With the default fp32 cfg2 workload the line also carries `bf16_cfg4`: the bf16 decode
 (B=128, Sk=4989, bf16 storage) layer time and its fused attention's roofline, measured
-the same way.
+the same way; and `other_configs`: every other BASELINE configuration in fp32 (cfg1 B=1
+Sk=512; B=1, 8, 32 at Sk=4989; cfg5 B=4 Sq=128 Sk=32768 causal), each with its layer time,
+in-layer kernel times, fused-attention roofline and the layer's roofline fraction (the sum
+of the steps' bounds over the layer time).
 
 cpu_baseline: the CPU oracle (oracle/mla_ref.py, the reference's PyTorch formulation
 restated) timed on this machine's host cores on the same inputs -- the only place this
@@ -251,29 +254,31 @@ def in_layer_kernel_us(layer, flush, n):
     return out
 
 
-def step_work(B, Sq, Sk, dims, e=4):
+def step_work(B, Sq, Sk, dims, e=4, causal=False):
     """Algorithmic FLOPs and compulsory HBM bytes per step (each input read once, each
     output written once; fp32 intermediates).  FLOP formulas follow the reference's own
-    roofline (stage_profile.py:85-93)."""
+    roofline (stage_profile.py:85-93); with a causal mask the score and ctx FLOPs count the
+    keys a query sees, Sk - Sq + 1 + i for query i, i.e. Sk - (Sq - 1) / 2 on average."""
     H, R, D, V = dims.n_heads, dims.kv_rank, dims.rope, dims.v
     hid, ql, qk, nope = dims.hidden, dims.q_lora, dims.qk_head, dims.nope
     bq = B * Sq
     flat = bq * H
     P = -(-Sk // 128)
+    Sv = Sk - (Sq - 1) / 2 if causal else Sk     # mean visible keys per query
     w = {
         "2a1": (2 * bq * hid * ql, e * (bq * hid + hid * ql) + 4 * bq * ql),
         "2a-n": (3 * bq * ql, 4 * bq * ql + e * ql + e * bq * ql),
         "2a2": (2 * bq * ql * H * qk, e * (bq * ql + ql * H * qk) + 4 * bq * H * qk),
         "2b": (6 * bq * H * D // 2, 4 * bq * H * D + e * bq * H * D),
         "2c": (2 * bq * H * nope * R, 4 * bq * H * nope + e * H * nope * R + e * bq * H * R),
-        "3a": (2 * flat * Sk * (R + D), e * (flat * (R + D) + B * Sk * (R + D))
+        "3a": (2 * flat * Sv * (R + D), e * (flat * (R + D) + B * Sk * (R + D))
                + 4 * (flat * Sk + 2 * flat * P)),
         "3b": (3 * flat * P, 4 * (3 * flat * P + flat)),
-        "3c": (2 * flat * Sk * R, 4 * (flat * Sk + flat * P) + e * (B * Sk * R) + 4 * flat * R),
+        "3c": (2 * flat * Sv * R, 4 * (flat * Sk + flat * P) + e * (B * Sk * R) + 4 * flat * R),
         "3d": (2 * flat * R * V, 4 * flat * R + e * H * V * R + 4 * flat + e * flat * V),
         # 3a+3b+3c fused (the layer's attention kernel at kv_rank 512 / rope 64): queries
         # and cache read once, the unnormalised ctx and row sums written once
-        "3abc": (2 * flat * Sk * (R + D) + 2 * flat * Sk * R,
+        "3abc": (2 * flat * Sv * (R + D) + 2 * flat * Sv * R,
                  e * (flat * (R + D) + B * Sk * (R + D)) + 4 * flat * R + 4 * flat),
     }
     return w
@@ -333,8 +338,10 @@ def cpu_baseline(inp, gpu_out, budget_s=30.0, causal=False):
             "os_cpu_count": os.cpu_count(), "cpu_model": model}, err, b_use
 
 
-def measure(args, ext, dev, neighbours=True):
-    """Time one configuration (args.config, args.dtype); returns the JSON record."""
+def measure(args, ext, dev, neighbours=True, light=False):
+    """Time one configuration (args.config, args.dtype); returns the JSON record.
+    light: only the layer (flushed and back to back), its in-layer kernel times and the
+    fused attention's own timing -- no torch formulation, graph replay or per-step pass."""
     import torch
     import mla_inputs
 
@@ -457,7 +464,7 @@ def measure(args, ext, dev, neighbours=True):
     # the same layer through torch on this GPU (the reference's PyTorch formulation,
     # rocBLAS / hipBLASLt products), timed with the same flush-then-layer protocol
     torch_same = None
-    if not fp8kv:
+    if not fp8kv and not light:
         try:
             def t_layer():
                 return torch_layer(g, W_uk_d, W_uv_d, dims, scale, eps, causal)
@@ -481,9 +488,10 @@ def measure(args, ext, dev, neighbours=True):
     # the eager output bit for bit.
     graph_us = b2b_settled_us = None
     try:
-        b2b_settled_us, graph_us = graph_vs_eager(layer, out, args.steps, args.settle)
-        print(f"[bench] fused layer, graph replay: {graph_us:.1f} µs/step (eager back to back "
-              f"{b2b_settled_us:.1f})", file=sys.stderr, flush=True)
+        if not light:
+            b2b_settled_us, graph_us = graph_vs_eager(layer, out, args.steps, args.settle)
+            print(f"[bench] fused layer, graph replay: {graph_us:.1f} µs/step (eager back to "
+                  f"back {b2b_settled_us:.1f})", file=sys.stderr, flush=True)
     except RuntimeError as e:
         print(f"[bench] graph replay unavailable ({e})", file=sys.stderr, flush=True)
 
@@ -505,17 +513,21 @@ def measure(args, ext, dev, neighbours=True):
         o = ext.out(ctx, rs, W_uv_d); ev[9].record()
         return o
 
-    for _ in range(2):
-        steps([torch.cuda.Event(enable_timing=True) for _ in range(10)])
-    torch.cuda.synchronize()
-    all_ev = [[torch.cuda.Event(enable_timing=True) for _ in range(10)] for _ in range(args.steps)]
-    for ev in all_ev:
-        o_steps = steps(ev)
-    torch.cuda.synchronize()
-    step_us = {n: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in all_ev) * 1e3
-               for i, n in enumerate(names)}
-    steps_sum = sum(step_us.values())
-    same = (o_steps - out).abs().max().item()
+    if light:
+        names, step_us, steps_sum, same = [], {}, None, None
+    else:
+        for _ in range(2):
+            steps([torch.cuda.Event(enable_timing=True) for _ in range(10)])
+        torch.cuda.synchronize()
+        all_ev = [[torch.cuda.Event(enable_timing=True) for _ in range(10)]
+                  for _ in range(args.steps)]
+        for ev in all_ev:
+            o_steps = steps(ev)
+        torch.cuda.synchronize()
+        step_us = {n: statistics.mean(ev[i].elapsed_time(ev[i + 1]) for ev in all_ev) * 1e3
+                   for i, n in enumerate(names)}
+        steps_sum = sum(step_us.values())
+        same = (o_steps - out).abs().max().item()
 
     # the layer's attention runs 3a+3b+3c as one fused kernel (attn_ctx) at the
     # DeepSeek-V3 widths, timed here the same way; the per-step 3a/3b/3c above are the
@@ -538,7 +550,7 @@ def measure(args, ext, dev, neighbours=True):
         step_us["3abc"] = statistics.mean(e0.elapsed_time(e1) for e0, e1 in fev) * 1e3
         names = names + ["3abc"]
 
-    work = step_work(B, Sq, Sk, dims, e=2 if half else 4)
+    work = step_work(B, Sq, Sk, dims, e=2 if half else 4, causal=causal)
     peak_mfma = PEAK_BF16 if half else PEAK_F32   # the fp16 MFMA peak equals the bf16 one
     per_step = {}
     for n in names:
@@ -574,26 +586,48 @@ def measure(args, ext, dev, neighbours=True):
     roofline.update({"traffic": traffic, "algorithmic_flop": fl, "algorithmic_bytes": by})
 
     in_layer_steps = None
+    fused_steps = ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d")
     if in_layer:
-        # the profiler's session runs the kernels a few to ~15% longer than the event-timed
-        # layers (measured at cfg2: every kernel ~10-15%, against a rocprofv3 trace of the
-        # same build); the durations are rescaled so that they sum to the event-timed layer
+        # each kernel's duration inside the flushed layer as the profiler measured it; the
+        # figures are reported as measured.  The profiler's session runs the kernels a few
+        # to ~15% longer than the event-timed layers, so `layer_over_span` (event-timed
+        # layer / profiled span, <= 1) is given beside them for reference only.
         span_il = in_layer["layer_span"]
-        scale_il = min(1.0, ms_per_step * 1e3 / span_il) if span_il > 0 else 1.0
-        in_layer_steps = {"profiler_scale": round(scale_il, 4)}
-        for n in ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d"):
+        in_layer_steps = {"layer_over_span": (round(min(1.0, ms_per_step * 1e3 / span_il), 4)
+                                              if span_il > 0 else None)}
+        for n in fused_steps:
             if n not in in_layer:
                 continue
             fl, by = work[n]
-            us_n = round(in_layer[n] * scale_il, 2)
-            t = us_n * 1e-6
-            in_layer_steps[n] = {"us": us_n, "us_profiled": in_layer[n],
+            t = in_layer[n] * 1e-6
+            in_layer_steps[n] = {"us": in_layer[n],
                                  "tflops": round(fl / t / 1e12, 2),
                                  "gbps": round(by / t / 1e9, 1),
                                  "mfma_pct": round(100 * fl / t / peak_mfma, 1),
                                  "hbm_pct": round(100 * by / t / PEAK_HBM, 1)}
         in_layer_steps["kernels_sum_us"] = in_layer["kernels_sum"]
         in_layer_steps["layer_span_us"] = in_layer["layer_span"]
+
+    # the layer against its roofline: the sum over the fused path's steps of each step's
+    # bound max(FLOPs / MFMA peak, bytes / HBM peak), and the in-layer kernel that takes
+    # the most time with its own roofline fraction
+    def bound_us(n):
+        fl_n, by_n = work[n]
+        return max(fl_n / peak_mfma, by_n / PEAK_HBM) * 1e6
+    layer_bound_us = sum(bound_us(n) for n in fused_steps)
+    dominant_in_layer = None
+    if in_layer_steps:
+        cand = [n for n in fused_steps if n in in_layer_steps]
+        top = max(cand, key=lambda n: in_layer_steps[n]["us"])
+        fl_t, by_t = work[top]
+        t = in_layer_steps[top]["us"] * 1e-6
+        mf = fl_t / by_t > peak_mfma / PEAK_HBM
+        ach = fl_t / t / 1e12 if mf else by_t / t / 1e9
+        pk = peak_mfma / 1e12 if mf else PEAK_HBM / 1e9
+        dominant_in_layer = {"kernel": top, "us": in_layer_steps[top]["us"],
+                             "bound": "mfma" if mf else "hbm", "achieved": round(ach, 2),
+                             "peak": pk, "unit": "TFLOP/s" if mf else "GB/s",
+                             "frac": round(ach / pk, 4)}
 
     nb = {}
     if neighbours:
@@ -757,10 +791,13 @@ def measure(args, ext, dev, neighbours=True):
         "roofline": roofline,
         "steps_us": per_step,
         "steps_in_layer_us": in_layer_steps,
-        "per_step_sum_us": round(steps_sum, 2),
+        "dominant_in_layer": dominant_in_layer,
+        "layer_bound_us": round(layer_bound_us, 1),
+        "layer_roofline_frac": round(layer_bound_us / value_us, 4),
+        "per_step_sum_us": None if steps_sum is None else round(steps_sum, 2),
         "fused_path_sum_us": (round(sum(step_us[n] for n in ("2a1", "2a-n", "2a2", "2b", "2c",
                                                              "3abc", "3d")), 2)
-                              if fused_attn else None),
+                              if fused_attn and not light else None),
         "per_step_vs_fused_max_abs": same,
         "neighbours": nb,
         "torch_same_gpu": torch_same,
@@ -880,6 +917,9 @@ def main():
                          "layers, so the clock has settled (see measure())")
     ap.add_argument("--no-bf16-line", action="store_true",
                     help="cfg2 only: skip the bf16 cfg4 figures added to its JSON line")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="cfg2 only: skip the other BASELINE configurations (cfg1, B=1/8/32, "
+                         "cfg5) added to its JSON line")
     ap.add_argument("--config", default="cfg2", choices=sorted(CONFIGS))
     ap.add_argument("--dtype", default=None, choices=["f32", "bf16", "f16"],
                     help="storage/MFMA dtype (default: f32, bf16 for cfg4)")
@@ -943,6 +983,26 @@ def main():
                                                "back_to_back_us_per_step", "dtype", "config",
                                                "roofline", "fused_path_sum_us")}
         rec["bf16_cfg4"]["steps_us_3abc"] = r4["steps_us"]["3abc"]
+        for k in ("steps_in_layer_us", "dominant_in_layer", "layer_bound_us",
+                  "layer_roofline_frac"):
+            rec["bf16_cfg4"][k] = r4[k]
+    if args.config == "cfg2" and (args.dtype or "f32") == "f32" and not args.no_other_configs:
+        # every other BASELINE configuration, fp32, timed the same way (flushed layers after
+        # a settle), with its in-layer kernel times, its fused attention's roofline and the
+        # layer's own roofline fraction: cfg1 (B=1, Sk=512), the small-batch sweep B = 1, 8,
+        # 32 at Sk=4989, and the causal chunked prefill cfg5 (B=4, Sq=128, Sk=32768)
+        rec["other_configs"] = {}
+        for name in ("cfg1", "b1", "b8", "b32", "cfg5"):
+            a = argparse.Namespace(**vars(args))
+            a.config, a.dtype, a.no_cpu_baseline = name, "f32", True
+            a.settle = min(args.settle, 1.0)
+            if name == "cfg5":     # ~34 ms layers
+                a.steps, a.warmup = min(args.steps, 5), min(args.warmup, 2)
+            r = measure(a, ext, dev, neighbours=False, light=True)
+            rec["other_configs"][name] = {k: r[k] for k in (
+                "value", "unit", "median_us_per_step", "back_to_back_us_per_step", "steps",
+                "dtype", "config", "roofline", "steps_in_layer_us", "dominant_in_layer",
+                "layer_bound_us", "layer_roofline_frac")}
     print(json.dumps(rec), flush=True)
 
 
