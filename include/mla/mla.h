@@ -11,7 +11,10 @@
  *     given in the comments; every pointer must be 16-byte aligned.
  *   - `dtype` names the storage type of the layer's inputs and outputs.  Intermediates that
  *     the reference keeps in its accumulate dtype (mla_kernels.cu:115-120) are float32
- *     here ("acc" below): q_lat_acc, q_raw, scores, m/l/alpha, row_sum, ctx.
+ *     here ("acc" below): q_lat_acc, q_raw, scores, m/l/alpha, row_sum, ctx -- float64
+ *     under MLA_DTYPE_F64, which the two fused entry points (and their ragged and
+ *     no-workspace variants) take; every other entry point refuses it with
+ *     MLA_ERR_UNSUPPORTED.
  *   - Work is enqueued on `stream` (NULL = the null stream); no entry point synchronises
  *     the host, none allocates device memory.  Scratch memory comes from the caller through
  *     `workspace` / `workspace_bytes`, sized by the matching *_workspace_bytes() query.
@@ -37,6 +40,10 @@ typedef enum mla_dtype {
     MLA_DTYPE_F32 = 0,   /* float32 storage, float32 MFMA (v_mfma_f32_32x32x2_f32)       */
     MLA_DTYPE_BF16 = 1,  /* bfloat16 storage, float32 accumulation on bf16 MFMA          */
     MLA_DTYPE_F16 = 2,   /* float16 storage, float32 accumulation on fp16 MFMA            */
+    MLA_DTYPE_F64 = 3,   /* float64 storage and intermediates, double MFMA
+                            (v_mfma_f64_16x16x4_f64): the reference's double dispatch,
+                            mla_kernels.cu:674, 1561.  mla_q_absorbed(_ragged) and
+                            mla_attention(_noalloc) only                                 */
 } mla_dtype_t;
 
 typedef enum mla_status {
@@ -84,8 +91,10 @@ int32_t mla_score_ld(int32_t sk);
  *   W_q_b      [q_lora, H*(nope+rope)]         dtype
  *   W_uk       [H, nope, kv_rank]              dtype
  *   positions  [Sq]                            int64  absolute position of each query
- *   inv_freq   [rope/2]                        float32 RoPE inverse frequencies, computed by
- *                                              the caller as 1/10000^(2i/rope) in float32
+ *   inv_freq   [rope/2]                        RoPE inverse frequencies 1/10000^(2i/rope),
+ *                                              computed by the caller in float32 (float64
+ *                                              under MLA_DTYPE_F64), the accumulate dtype
+ *                                              the reference evaluates them in
  *   q_absorbed [B, Sq, H, kv_rank]             dtype  (out)
  *   q_rope     [B, Sq, H, rope]                dtype  (out)
  */
@@ -93,7 +102,7 @@ size_t mla_q_absorbed_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims)
 int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims,
                    const void* x, const void* W_q_a, const void* q_norm_w,
                    const void* W_q_b, const void* W_uk, const int64_t* positions,
-                   const float* inv_freq, double eps,
+                   const void* inv_freq, double eps,
                    void* q_absorbed, void* q_rope,
                    void* workspace, size_t workspace_bytes, hipStream_t stream);
 
@@ -108,6 +117,8 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims,
  *              (not in the reference; used for chunked prefill)
  * At kv_rank 512 / rope 64 this runs 3a+3b+3c as one fused pass (mla_attn_ctx), whose
  * workspace holds no score matrix; MLA_ATTENTION_PATH=split selects the per-step kernels.
+ * Under MLA_DTYPE_F64 it runs the reference's decomposition in double (scores
+ * [B*Sq*H, Sk] in the workspace, a row softmax, ctx, then 3d).
  * The variable is read by the size query and by the call: a caller that changes it in
  * between gets MLA_ERR_WORKSPACE when the workspace is too small.
  */
@@ -291,7 +302,7 @@ int mla_kv_append(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, cons
  * mla_q_absorbed. */
 int mla_q_absorbed_ragged(mla_dtype_t dtype, const mla_dims_t* dims, const void* x,
                           const void* W_q_a, const void* q_norm_w, const void* W_q_b,
-                          const void* W_uk, const int64_t* positions, const float* inv_freq,
+                          const void* W_uk, const int64_t* positions, const void* inv_freq,
                           double eps, void* q_absorbed, void* q_rope, void* workspace,
                           size_t workspace_bytes, hipStream_t stream);
 

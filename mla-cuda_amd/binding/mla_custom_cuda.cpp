@@ -39,8 +39,10 @@ mla_dtype_t to_mla_dtype(const torch::Tensor& t, const char* name) {
     if (t.scalar_type() == torch::kFloat32) return MLA_DTYPE_F32;
     if (t.scalar_type() == torch::kBFloat16) return MLA_DTYPE_BF16;
     if (t.scalar_type() == torch::kFloat16) return MLA_DTYPE_F16;
+    if (t.scalar_type() == torch::kFloat64) return MLA_DTYPE_F64;
     TORCH_CHECK(false, "MLA: ", name, " has dtype ", t.scalar_type(),
-                "; supported dtypes are float32, bfloat16 and float16");
+                "; supported dtypes are float32, bfloat16, float16 and float64 (float64 in "
+                "q_absorbed and mla_attention)");
     return MLA_DTYPE_F32;
 }
 
@@ -70,26 +72,30 @@ torch::Tensor workspace(size_t bytes, const torch::Tensor& like) {
                         like.options().dtype(torch::kUInt8));
 }
 
-// RoPE inverse frequencies with the reference oracle's own float32 expression,
-// 1 / 10000 ** (arange(0, rope, 2) / rope)  (exhaustive_benchmark_suite.py:216-219),
-// evaluated by the same ATen CPU ops so kernel and oracle angles are bit-identical.
-torch::Tensor rope_inv_freq(int64_t rope) {
+// RoPE inverse frequencies with the reference oracle's own expression,
+// 1 / 10000 ** (arange(0, rope, 2) / rope)  (exhaustive_benchmark_suite.py:216-219), in the
+// accumulate dtype (float32, float64 for float64 inputs), evaluated by the same ATen CPU ops
+// so kernel and oracle angles are bit-identical.
+torch::Tensor rope_inv_freq(int64_t rope, torch::ScalarType acc = torch::kFloat32) {
     TORCH_CHECK(rope > 0 && rope % 2 == 0, "MLA: rope_dim must be positive and even");
-    auto e = torch::arange(0, rope, 2, torch::TensorOptions().dtype(torch::kFloat32)) / rope;
+    auto e = torch::arange(0, rope, 2, torch::TensorOptions().dtype(acc)) / rope;
     return torch::pow(10000, e).reciprocal();
 }
 
 // The table lives on the device once per (device, rope width): a per-call host->device
 // copy would be a synchronous pageable copy that stalls the caller's stream every layer.
 // The cache is intentionally leaked so no tensor is freed after the HIP runtime shuts down.
-torch::Tensor device_inv_freq(int64_t rope, const torch::Device& dev) {
+torch::Tensor device_inv_freq(int64_t rope, const torch::Device& dev,
+                              torch::ScalarType acc = torch::kFloat32) {
     static std::mutex mu;
     static auto* cache = new std::map<std::pair<int, int64_t>, torch::Tensor>();
     std::lock_guard<std::mutex> lock(mu);
-    const auto key = std::make_pair(static_cast<int>(dev.index()), rope);
+    // one table per (device, rope width, accumulate dtype)
+    const auto key = std::make_pair(static_cast<int>(dev.index()),
+                                    rope * 2 + (acc == torch::kFloat64 ? 1 : 0));
     auto it = cache->find(key);
     if (it != cache->end()) return it->second;
-    auto t = rope_inv_freq(rope).to(dev);
+    auto t = rope_inv_freq(rope, acc).to(dev);
     cache->emplace(key, t);
     return t;
 }
@@ -134,7 +140,8 @@ std::vector<torch::Tensor> op_q_absorbed(torch::Tensor x, torch::Tensor W_q_a, t
     auto wb = W_q_b.contiguous();
     auto wuk = W_uk.contiguous();
     auto pos = positions.to(torch::kLong).contiguous();
-    auto inv_freq = device_inv_freq(rope_dim, x.device());
+    auto inv_freq = device_inv_freq(rope_dim, x.device(),
+                                    dt == MLA_DTYPE_F64 ? torch::kFloat64 : torch::kFloat32);
 
     mla_dims_t d{};
     d.batch = (int32_t)B; d.sq = (int32_t)Sq; d.hidden = (int32_t)hidden;
@@ -147,7 +154,7 @@ std::vector<torch::Tensor> op_q_absorbed(torch::Tensor x, torch::Tensor W_q_a, t
     auto ws = workspace(wsb, x);
     auto q_fn = per_seq ? mla_q_absorbed_ragged : mla_q_absorbed;
     check_status(q_fn(dt, &d, xc.data_ptr(), wa.data_ptr(), g.data_ptr(), wb.data_ptr(),
-                      wuk.data_ptr(), pos.data_ptr<int64_t>(), inv_freq.data_ptr<float>(), eps,
+                      wuk.data_ptr(), pos.data_ptr<int64_t>(), inv_freq.data_ptr(), eps,
                       qa.data_ptr(), qr.data_ptr(), ws.data_ptr(), wsb, current_stream()),
                  "q_absorbed");
     return {qa, qr};
@@ -831,7 +838,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
           "Attention with keys in bounded chunks (online-softmax merge): returns out [B, Sq, H, v]",
           py::arg("q_absorbed"), py::arg("q_rope"), py::arg("c_kv"), py::arg("pe_cache"),
           py::arg("W_uv"), py::arg("scale"), py::arg("causal") = false, py::arg("key_chunk") = 0);
-    m.def("rope_inv_freq", &rope_inv_freq, "float32 RoPE inverse-frequency table", py::arg("rope"));
+    m.def("rope_inv_freq",
+          [](int64_t rope, bool float64) {
+              return rope_inv_freq(rope, float64 ? torch::kFloat64 : torch::kFloat32);
+          },
+          "RoPE inverse-frequency table q_absorbed passes to the library (float32, or float64 "
+          "for float64 inputs)", py::arg("rope"), py::arg("float64") = false);
     m.def("gemm", &step_gemm, "2a1/2a2: float32 C = A @ W", py::arg("A"), py::arg("W"));
     m.def("rmsnorm", &step_rmsnorm, "2a-n", py::arg("input"), py::arg("gain"), py::arg("eps"));
     m.def("rope", &step_rope, "2b", py::arg("q_raw"), py::arg("positions"), py::arg("B"),

@@ -69,6 +69,9 @@ int check_ptr(const void* p, const char* name) {
 
 int check_dtype(mla_dtype_t dt) {
     if (dt == MLA_DTYPE_F32 || dt == MLA_DTYPE_BF16 || dt == MLA_DTYPE_F16) return MLA_OK;
+    if (dt == MLA_DTYPE_F64)
+        return fail(MLA_ERR_UNSUPPORTED, "float64 is taken by mla_q_absorbed, "
+                    "mla_q_absorbed_ragged, mla_attention and mla_attention_noalloc only");
     return fail(MLA_ERR_INVALID_ARGUMENT, "unknown dtype %d", (int)dt);
 }
 
@@ -84,6 +87,9 @@ const char* dtype_name(mla_dtype_t dt) {
 
 // Row lengths of storage-dtype tensors must be whole 16-byte chunks: 4 fp32 / 8 16-bit.
 int check_row(mla_dtype_t dt, int v, const char* name) {
+    // float64 has its own shape rules (check_f64_*); every path that reaches here is one
+    // that does not take it
+    if (dt == MLA_DTYPE_F64) return check_dtype(dt);
     const int q = is_half(dt) ? 8 : 4;
     if (v <= 0 || v % q != 0)
         return fail(MLA_ERR_INVALID_ARGUMENT, "%s must be a positive multiple of %d for %s (got %d)",
@@ -538,11 +544,22 @@ size_t kv_ws_bytes(mla_dtype_t dt, const mla_dims_t* d, GemmPlan* plan_out) {
                     (size_t)(d->kv_rank + d->rope) * sizeof(float));
 }
 
+int q_absorbed_f64(const mla_dims_t* d, const void* x, const void* W_q_a, const void* q_norm_w,
+                   const void* W_q_b, const void* W_uk, const int64_t* positions,
+                   const void* inv_freq, double eps, void* q_absorbed, void* q_rope,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream,
+                   bool pos_per_batch);
+
 int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_q_a,
                    const void* q_norm_w, const void* W_q_b, const void* W_uk,
-                   const int64_t* positions, const float* inv_freq, double eps,
+                   const int64_t* positions, const void* inv_freq_tab, double eps,
                    void* q_absorbed, void* q_rope, void* workspace, size_t workspace_bytes,
                    hipStream_t stream, bool pos_per_batch) {
+    if (dtype == MLA_DTYPE_F64)
+        return q_absorbed_f64(dims, x, W_q_a, q_norm_w, W_q_b, W_uk, positions, inv_freq_tab,
+                              eps, q_absorbed, q_rope, workspace, workspace_bytes, stream,
+                              pos_per_batch);
+    const float* inv_freq = static_cast<const float*>(inv_freq_tab);
     MLA_CHECK(check_dtype(dtype));
     MLA_CHECK(check_q_dims(dtype, dims));
     MLA_CHECK(check_ptr(x, "x"));
@@ -723,6 +740,188 @@ int scratch_for_stream(hipStream_t stream, void** out) {
     return MLA_OK;
 }
 
+// ------------------------------------------------------------------ float64 (f64.hip)
+//
+// The reference's double dispatch (mla_kernels.cu:674, 1561) with double intermediates
+// (:118-120): the per-step decomposition in double on the double-MFMA GEMM.  Shapes only
+// need to be positive (rope even); the grids put M / 64 in y and the batch in z, which
+// bounds those at 65535.
+
+int check_f64_grid(int64_t m, int64_t g, const char* what) {
+    if ((m + 63) / 64 > 65535 || g > 65535)
+        return fail(MLA_ERR_UNSUPPORTED, "float64 %s: %lld rows in %lld groups is past the "
+                    "grid's limits (65535 row tiles of 64, 65535 groups)", what, (long long)m,
+                    (long long)g);
+    return MLA_OK;
+}
+
+int check_f64_q_dims(const mla_dims_t* d) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_pos(d->hidden, "dims.hidden"));
+    MLA_CHECK(check_pos(d->q_lora, "dims.q_lora"));
+    MLA_CHECK(check_pos(d->nope, "dims.nope"));
+    MLA_CHECK(check_pos(d->kv_rank, "dims.kv_rank"));
+    if (d->rope <= 0 || d->rope % 2 != 0)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "dims.rope must be positive and even (got %d)",
+                    d->rope);
+    const int64_t bq = (int64_t)d->batch * d->sq;
+    if (bq * d->heads * (int64_t)(d->nope + d->rope) > kMaxI32)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    return check_f64_grid(bq, d->heads, "Q path");
+}
+
+int check_f64_attn_dims(const mla_dims_t* d, int causal) {
+    if (!d) return fail(MLA_ERR_INVALID_ARGUMENT, "dims must not be NULL");
+    MLA_CHECK(check_pos(d->batch, "dims.batch"));
+    MLA_CHECK(check_pos(d->sq, "dims.sq"));
+    MLA_CHECK(check_pos(d->sk, "dims.sk"));
+    MLA_CHECK(check_pos(d->heads, "dims.heads"));
+    MLA_CHECK(check_pos(d->rope, "dims.rope"));
+    MLA_CHECK(check_pos(d->kv_rank, "dims.kv_rank"));
+    MLA_CHECK(check_pos(d->v, "dims.v"));
+    if (causal && d->sk < d->sq)
+        return fail(MLA_ERR_INVALID_ARGUMENT,
+                    "causal attention needs sk >= sq (got sk=%d, sq=%d)", d->sk, d->sq);
+    const int64_t rows_b = (int64_t)d->sq * d->heads;
+    if (rows_b * d->batch > kMaxI32 / 2)
+        return fail(MLA_ERR_INVALID_ARGUMENT, "batch*sq*heads too large");
+    MLA_CHECK(check_f64_grid(rows_b, d->batch, "scores"));
+    return check_f64_grid((int64_t)d->batch * d->sq, d->heads, "output");
+}
+
+struct QLayout64 { size_t off_lat, off_raw, total; };
+QLayout64 q_layout64(const mla_dims_t* d) {
+    QLayout64 L;
+    const size_t bq = (size_t)d->batch * d->sq;
+    size_t o = 0;
+    L.off_lat = o; o = align_up(o + bq * d->q_lora * sizeof(double));
+    L.off_raw = o; o = align_up(o + bq * d->heads * (size_t)(d->nope + d->rope) * sizeof(double));
+    L.total = o;
+    return L;
+}
+
+struct AttnLayout64 { size_t off_s, off_ctx, total; };
+AttnLayout64 attn_layout64(const mla_dims_t* d) {
+    AttnLayout64 L;
+    const size_t rows = (size_t)d->batch * d->sq * d->heads;
+    size_t o = 0;
+    L.off_s = o;   o = align_up(o + rows * (size_t)d->sk * sizeof(double));
+    L.off_ctx = o; o = align_up(o + rows * (size_t)d->kv_rank * sizeof(double));
+    L.total = o;
+    return L;
+}
+
+// 2a1 -> 2a-n -> 2a2 -> 2b -> 2c in double; inv_freq is a double table
+int q_absorbed_f64(const mla_dims_t* d, const void* x, const void* W_q_a, const void* q_norm_w,
+                   const void* W_q_b, const void* W_uk, const int64_t* positions,
+                   const void* inv_freq, double eps, void* q_absorbed, void* q_rope,
+                   void* workspace, size_t workspace_bytes, hipStream_t stream,
+                   bool pos_per_batch) {
+    MLA_CHECK(check_f64_q_dims(d));
+    MLA_CHECK(check_ptr(x, "x"));
+    MLA_CHECK(check_ptr(W_q_a, "W_q_a"));
+    MLA_CHECK(check_ptr(q_norm_w, "q_norm_w"));
+    MLA_CHECK(check_ptr(W_q_b, "W_q_b"));
+    MLA_CHECK(check_ptr(W_uk, "W_uk"));
+    MLA_CHECK(check_ptr(positions, "positions"));
+    MLA_CHECK(check_ptr(inv_freq, "inv_freq"));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    if (!(eps >= 0.0) || !std::isfinite(eps))
+        return fail(MLA_ERR_INVALID_ARGUMENT, "eps must be finite and >= 0");
+    const QLayout64 L = q_layout64(d);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+    double* lat = at<double>(workspace, L.off_lat);
+    double* raw = at<double>(workspace, L.off_raw);
+    const int bq = d->batch * d->sq;
+    const int qk = d->nope + d->rope;
+    const int64_t n_raw = (int64_t)d->heads * qk;
+    // 2a1: lat [bq, q_lora] = x [bq, hidden] . W_q_a [hidden, q_lora]
+    Gemm64Problem p;
+    p.A = static_cast<const double*>(x); p.lda = d->hidden;
+    p.B = static_cast<const double*>(W_q_a); p.ldb = d->q_lora;
+    p.C = lat; p.ldc = d->q_lora;
+    p.M = bq; p.N = d->q_lora; p.K = d->hidden;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "2a1 launch (f64)");
+    // 2a-n, in place
+    MLA_TRY_HIP(launch_rmsnorm64(lat, static_cast<const double*>(q_norm_w), bq, d->q_lora, eps,
+                                 stream), "2a-n launch (f64)");
+    // 2a2: raw [bq, H*(nope+rope)] = lat . W_q_b
+    p = Gemm64Problem();
+    p.A = lat; p.lda = d->q_lora;
+    p.B = static_cast<const double*>(W_q_b); p.ldb = n_raw;
+    p.C = raw; p.ldc = n_raw;
+    p.M = bq; p.N = (int)n_raw; p.K = d->q_lora;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "2a2 launch (f64)");
+    // 2b
+    MLA_TRY_HIP(launch_rope64(raw, positions, static_cast<const double*>(inv_freq),
+                              static_cast<double*>(q_rope), d->batch, d->sq, d->heads, d->nope,
+                              d->rope, pos_per_batch, stream), "2b launch (f64)");
+    // 2c, one group per head: q_absorbed[m, h, :] = raw[m, h*qk : h*qk+nope] . W_uk[h]
+    p = Gemm64Problem();
+    p.A = raw; p.lda = n_raw; p.sA = qk;
+    p.B = static_cast<const double*>(W_uk); p.ldb = d->kv_rank; p.sB = (int64_t)d->nope * d->kv_rank;
+    p.C = static_cast<double*>(q_absorbed); p.ldc = (int64_t)d->heads * d->kv_rank;
+    p.sC = d->kv_rank;
+    p.M = bq; p.N = d->kv_rank; p.K = d->nope; p.G = d->heads;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "2c launch (f64)");
+    return ok();
+}
+
+// 3a -> softmax -> 3c -> 3d in double
+int attention_f64(const mla_dims_t* d, const void* q_absorbed, const void* q_rope,
+                  const void* c_kv, const void* pe_cache, const void* W_uv, double scale,
+                  int causal, void* out, void* workspace, size_t workspace_bytes,
+                  hipStream_t stream) {
+    MLA_CHECK(check_f64_attn_dims(d, causal));
+    MLA_CHECK(check_scale(scale));
+    MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
+    MLA_CHECK(check_ptr(q_rope, "q_rope"));
+    MLA_CHECK(check_ptr(c_kv, "c_kv"));
+    MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
+    MLA_CHECK(check_ptr(W_uv, "W_uv"));
+    MLA_CHECK(check_ptr(out, "out"));
+    const AttnLayout64 L = attn_layout64(d);
+    MLA_CHECK(check_ws(workspace, workspace_bytes, L.total));
+    double* S = at<double>(workspace, L.off_s);
+    double* ctx = at<double>(workspace, L.off_ctx);
+    const int rows_b = d->sq * d->heads;
+    const int64_t R = d->kv_rank, Dr = d->rope, Sk = d->sk;
+    const double* ckv = static_cast<const double*>(c_kv);
+    // 3a: S[b] = q_absorbed[b] . c_kv[b]^T, then += q_rope[b] . pe[b]^T  ([rows_b, Sk])
+    Gemm64Problem p;
+    p.A = static_cast<const double*>(q_absorbed); p.lda = R; p.sA = rows_b * R;
+    p.B = ckv; p.ldb = R; p.sB = Sk * R; p.b_nt = true;
+    p.C = S; p.ldc = Sk; p.sC = rows_b * Sk;
+    p.M = rows_b; p.N = d->sk; p.K = d->kv_rank; p.G = d->batch;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "3a launch (f64)");
+    p.A = static_cast<const double*>(q_rope); p.lda = Dr; p.sA = rows_b * Dr;
+    p.B = static_cast<const double*>(pe_cache); p.ldb = Dr; p.sB = Sk * Dr;
+    p.K = d->rope; p.beta = 1.0;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "3a rope launch (f64)");
+    // 3b: softmax of S / scale over each row's visible keys
+    MLA_TRY_HIP(launch_softmax64(S, d->batch * rows_b, d->sk, d->sq, d->heads, scale,
+                                 causal != 0, stream), "softmax launch (f64)");
+    // 3c: ctx[b] = P[b] . c_kv[b]  ([rows_b, R])
+    p = Gemm64Problem();
+    p.A = S; p.lda = Sk; p.sA = rows_b * Sk;
+    p.B = ckv; p.ldb = R; p.sB = Sk * R;
+    p.C = ctx; p.ldc = R; p.sC = rows_b * R;
+    p.M = rows_b; p.N = d->kv_rank; p.K = d->sk; p.G = d->batch;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "3c launch (f64)");
+    // 3d, one group per head: out[m, h, :] = ctx[m, h, :] . W_uv[h]^T
+    p = Gemm64Problem();
+    p.A = ctx; p.lda = (int64_t)d->heads * R; p.sA = R;
+    p.B = static_cast<const double*>(W_uv); p.ldb = R; p.sB = (int64_t)d->v * R; p.b_nt = true;
+    p.C = static_cast<double*>(out); p.ldc = (int64_t)d->heads * d->v; p.sC = d->v;
+    p.M = d->batch * d->sq; p.N = d->v; p.K = d->kv_rank; p.G = d->heads;
+    MLA_TRY_HIP(launch_gemm64(p, stream), "3d launch (f64)");
+    return ok();
+}
+
 // fp8 KV cache (mla_attention_fp8kv)
 
 struct Fp8Layout {
@@ -807,7 +1006,7 @@ int32_t mla_score_tile(void) { return kScoreTile; }
 int32_t mla_score_ld(int32_t sk) { return sk <= 0 ? 0 : ((sk + 31) / 32) * 32; }
 
 size_t mla_gemm_workspace_bytes(mla_dtype_t dtype, int32_t M, int32_t N, int32_t K) {
-    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    if (M <= 0 || N <= 0 || K <= 0 || check_dtype(dtype) != MLA_OK) return 0;
     GemmProblem p;
     p.M = M; p.N = N; p.K = K;
     p.half = is_half(dtype); p.f16 = is_f16(dtype); p.a_f32 = !is_half(dtype);
@@ -997,13 +1196,15 @@ int mla_out(mla_dtype_t dtype, const mla_dims_t* dims, const float* ctx, const f
 }
 
 size_t mla_q_absorbed_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims) {
+    if (dtype == MLA_DTYPE_F64)
+        return dims && check_f64_q_dims(dims) == MLA_OK ? q_layout64(dims).total : 0;
     if (!dims || check_q_dims(dtype, dims) != MLA_OK) return 0;
     return q_layout(dtype, dims).total;
 }
 
 int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, const void* W_q_a,
                    const void* q_norm_w, const void* W_q_b, const void* W_uk,
-                   const int64_t* positions, const float* inv_freq, double eps,
+                   const int64_t* positions, const void* inv_freq, double eps,
                    void* q_absorbed, void* q_rope, void* workspace, size_t workspace_bytes,
                    hipStream_t stream) {
     return q_absorbed_impl(dtype, dims, x, W_q_a, q_norm_w, W_q_b, W_uk, positions, inv_freq, eps,
@@ -1012,7 +1213,7 @@ int mla_q_absorbed(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, con
 
 int mla_q_absorbed_ragged(mla_dtype_t dtype, const mla_dims_t* dims, const void* x,
                           const void* W_q_a, const void* q_norm_w, const void* W_q_b,
-                          const void* W_uk, const int64_t* positions, const float* inv_freq,
+                          const void* W_uk, const int64_t* positions, const void* inv_freq,
                           double eps, void* q_absorbed, void* q_rope, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
     return q_absorbed_impl(dtype, dims, x, W_q_a, q_norm_w, W_q_b, W_uk, positions, inv_freq, eps,
@@ -1020,6 +1221,8 @@ int mla_q_absorbed_ragged(mla_dtype_t dtype, const mla_dims_t* dims, const void*
 }
 
 size_t mla_attention_workspace_bytes(mla_dtype_t dtype, const mla_dims_t* dims, int causal) {
+    if (dtype == MLA_DTYPE_F64)
+        return dims && check_f64_attn_dims(dims, causal) == MLA_OK ? attn_layout64(dims).total : 0;
     if (!dims || check_attn_dims(dtype, dims, causal) != MLA_OK) return 0;
     return attn_layout(dtype, dims).total;
 }
@@ -1028,6 +1231,9 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
                   const void* q_rope, const void* c_kv, const void* pe_cache, const void* W_uv,
                   double scale, int causal, void* out, void* workspace, size_t workspace_bytes,
                   hipStream_t stream) {
+    if (dtype == MLA_DTYPE_F64)
+        return attention_f64(dims, q_absorbed, q_rope, c_kv, pe_cache, W_uv, scale, causal, out,
+                             workspace, workspace_bytes, stream);
     MLA_CHECK(check_dtype(dtype));
     MLA_CHECK(check_attn_dims(dtype, dims, causal));
     MLA_CHECK(check_scale(scale));
@@ -1172,8 +1378,12 @@ int mla_attention_noalloc(mla_dtype_t dtype, const mla_dims_t* dims, const void*
                           const void* q_rope, const void* c_kv, const void* pe_cache,
                           const void* W_uv, double scale, int causal, void* out,
                           hipStream_t stream) {
-    MLA_CHECK(check_dtype(dtype));
-    MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    if (dtype == MLA_DTYPE_F64) {
+        MLA_CHECK(check_f64_attn_dims(dims, causal));
+    } else {
+        MLA_CHECK(check_dtype(dtype));
+        MLA_CHECK(check_attn_dims(dtype, dims, causal));
+    }
     MLA_CHECK(check_scale(scale));
     MLA_CHECK(check_ptr(q_absorbed, "q_absorbed"));
     MLA_CHECK(check_ptr(q_rope, "q_rope"));
@@ -1181,7 +1391,8 @@ int mla_attention_noalloc(mla_dtype_t dtype, const mla_dims_t* dims, const void*
     MLA_CHECK(check_ptr(pe_cache, "pe_cache"));
     MLA_CHECK(check_ptr(W_uv, "W_uv"));
     MLA_CHECK(check_ptr(out, "out"));
-    const size_t need = attn_layout(dtype, dims).total;
+    const size_t need = dtype == MLA_DTYPE_F64 ? attn_layout64(dims).total
+                                               : attn_layout(dtype, dims).total;
     if (need > kScratchBytes)
         return fail(MLA_ERR_WORKSPACE,
                     "mla_attention_noalloc: this shape needs %zu bytes of scratch, more than "

@@ -193,4 +193,30 @@ int flash_worklist_ints(const FlashProblem& p, const FlashPlan& plan);
 hipError_t launch_flash_worklist(const FlashProblem& p, const FlashPlan& plan, int* wl,
                                  hipStream_t stream);
 
+// ---------------------------------------------------------------- float64 path (f64.hip)
+// C[g] = alpha * A[g] . op(B[g]) + beta * C[g] in double on the double MFMA (beta 0: C is
+// not read):  A[g][m][k] at A + g*sA + m*lda + k;  B (NN) at B + g*sB + k*ldb + n,
+// B (NT, b_nt) at B + g*sB + n*ldb + k;  C[g][m][n] at C + g*sC + m*ldc + n.
+struct Gemm64Problem {
+    const double* A = nullptr; int64_t lda = 0, sA = 0;
+    const double* B = nullptr; int64_t ldb = 0, sB = 0;
+    double* C = nullptr;       int64_t ldc = 0, sC = 0;
+    int M = 0, N = 0, K = 0, G = 1;
+    bool b_nt = false;
+    double alpha = 1.0, beta = 0.0;
+};
+hipError_t launch_gemm64(const Gemm64Problem& p, hipStream_t stream);
+// 2a-n in place on x [M][N]: x = (x / sqrt(mean(x^2) + eps)) * gain
+hipError_t launch_rmsnorm64(double* x, const double* gain, int M, int N, double eps,
+                            hipStream_t stream);
+// 2b: q_rope [B*Sq][H][rope] from q_raw [B*Sq][H*(nope+rope)], positions [Sq] (or [B*Sq]
+// with per_batch), inv_freq [rope/2]
+hipError_t launch_rope64(const double* q_raw, const int64_t* pos, const double* inv_freq,
+                         double* q_rope, int B, int Sq, int H, int nope, int rope,
+                         bool per_batch, hipStream_t stream);
+// in place on S [rows][Sk] (row = (b*Sq + s)*H + h): softmax over the visible keys of
+// S / scale, zeros where masked
+hipError_t launch_softmax64(double* S, int rows, int Sk, int Sq, int H, double scale,
+                            bool causal, hipStream_t stream);
+
 }  // namespace mla

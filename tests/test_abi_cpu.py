@@ -127,8 +127,51 @@ def test_fp16_is_a_storage_dtype(lib):
     assert st == MLA_ERR_INVALID_ARGUMENT and "M must be positive" in _err(lib)
     st = lib.mla_gemm(2, P16, P16, P16, 4, 20, 16, None, ctypes.c_size_t(0), None)
     assert st == MLA_ERR_INVALID_ARGUMENT and "multiple of 8 for fp16" in _err(lib)
-    st = lib.mla_gemm(3, P16, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
+    st = lib.mla_gemm(4, P16, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
     assert st == MLA_ERR_INVALID_ARGUMENT and "unknown dtype" in _err(lib)
+
+
+F64 = 3
+
+
+def test_fp64_is_taken_by_the_fused_entry_points_only(lib):
+    """MLA_DTYPE_F64 (3): the two fused entry points (and the no-workspace attention) size a
+    double workspace -- the [B*Sq*H, Sk] score matrix plus ctx, or the Q path's q_lat and
+    q_raw -- and every other entry point refuses it (MLA_ERR_UNSUPPORTED) before touching
+    the device."""
+    d = dsv3(B=1, Sq=1, Sk=64)
+    ws = lib.mla_attention_workspace_bytes(F64, ctypes.byref(d), 0)
+    rows = 128
+    assert ws >= rows * 64 * 8 + rows * 512 * 8
+    assert ws < rows * 64 * 8 + rows * 512 * 8 + 4096
+    wq = lib.mla_q_absorbed_workspace_bytes(F64, ctypes.byref(d))
+    assert wq >= 1536 * 8 + 128 * 192 * 8
+    st = lib.mla_gemm(F64, P16, P16, P16, 4, 16, 16, None, ctypes.c_size_t(0), None)
+    assert st == MLA_ERR_UNSUPPORTED and "float64" in _err(lib)
+    lib.mla_attention_fp8kv_workspace_bytes.restype = ctypes.c_size_t
+    assert lib.mla_attention_fp8kv_workspace_bytes(F64, ctypes.byref(d), 0) == 0
+    assert lib.mla_attention_streaming_workspace_bytes(F64, ctypes.byref(d), 0, 0) == 0
+    st = lib.mla_attention_streaming(F64, ctypes.byref(d), P16, P16, P16, P16, P16,
+                                     ctypes.c_double(13.85), 0, 0, P16, P16,
+                                     ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_UNSUPPORTED and "float64" in _err(lib)
+    st = lib.mla_rope(F64, ctypes.byref(d), P16, P16, P16, P16, None)
+    assert st == MLA_ERR_UNSUPPORTED
+    # the f64 shape rules: positive dims, an even rope width; rejected before any HIP call
+    bad = dsv3(B=1, Sq=1, Sk=64)
+    bad.rope = 7
+    assert lib.mla_q_absorbed_workspace_bytes(F64, ctypes.byref(bad)) == 0
+    st = lib.mla_q_absorbed(F64, ctypes.byref(bad), P16, P16, P16, P16, P16, P16, P16,
+                            ctypes.c_double(1e-6), P16, P16, P16, ctypes.c_size_t(1 << 30), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "rope" in _err(lib)
+    st = lib.mla_attention(F64, ctypes.byref(d), P16, P16, P16, P16, P16, ctypes.c_double(13.85),
+                           0, P16, P16, ctypes.c_size_t(ws - 1), None)
+    assert st == MLA_ERR_WORKSPACE
+    st = lib.mla_attention(F64, ctypes.byref(d), P16, P_ODD, P16, P16, P16,
+                           ctypes.c_double(13.85), 0, P16, P16, ctypes.c_size_t(ws), None)
+    assert st == MLA_ERR_INVALID_ARGUMENT and "aligned" in _err(lib)
+    causal = dsv3(B=1, Sq=8, Sk=4)
+    assert lib.mla_attention_workspace_bytes(F64, ctypes.byref(causal), 1) == 0
 
 
 def test_fp8kv_validation(lib):
@@ -402,6 +445,9 @@ def test_binding_inv_freq_matches_oracle_bitwise(ext):
     from oracle import mla_ref as R
     for rope in (64, 16, 128):
         assert torch.equal(ext.rope_inv_freq(rope), R.rope_inv_freq(rope, torch.float32))
+        f64 = ext.rope_inv_freq(rope, float64=True)
+        assert f64.dtype == torch.float64
+        assert torch.equal(f64, R.rope_inv_freq(rope, torch.float64))
 
 
 def _attn(B=1, Sq=1, Sk=8, H=4, Rk=16, D=8, V=8, dtype=torch.float32):
@@ -421,7 +467,9 @@ def test_binding_attention_shape_errors(ext):
     with pytest.raises(RuntimeError, match="q_absorbed must be"):
         ext.mla_attention(qa[0], qr, ck, pe, wuv, 1.0)
     with pytest.raises(RuntimeError, match="dtype"):
-        ext.mla_attention(qa.double(), qr.double(), ck.double(), pe.double(), wuv.double(), 1.0)
+        ext.mla_attention(qa.int(), qr.int(), ck.int(), pe.int(), wuv.int(), 1.0)
+    with pytest.raises(RuntimeError, match="c_kv has dtype"):
+        ext.mla_attention(qa.double(), qr.double(), ck, pe.double(), wuv.double(), 1.0)
     with pytest.raises(RuntimeError, match="c_kv has dtype"):
         ext.mla_attention(qa, qr, ck.bfloat16(), pe, wuv, 1.0)
     with pytest.raises(RuntimeError, match="causal attention needs Sk >= Sq"):

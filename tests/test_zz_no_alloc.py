@@ -127,6 +127,17 @@ def test_noalloc_matches_mla_attention(lib, dtype, dt):
             torch.testing.assert_close(got.float(), oracle, **C.tol(dtype, oracle))
 
 
+def test_noalloc_float64(lib):
+    """float64 (MLA_DTYPE_F64) through the no-workspace entry point: two calls in a row, the
+    second smaller, each bit for bit equal to mla_attention with a caller workspace."""
+    for i, (B, Sq, Sk, causal) in enumerate([(2, 2, 1000, True), (1, 1, 300, False)]):
+        print(f"noalloc float64 call {i}: B={B} Sq={Sq} Sk={Sk} causal={causal}", flush=True)
+        host = _inputs(B, Sq, Sk, seed=70 + i, dtype=torch.float64)
+        got = _call(lib, True, 3, host, causal)
+        ref = _call(lib, False, 3, host, causal)
+        assert got.dtype == torch.float64 and torch.equal(got, ref)
+
+
 def test_noalloc_refuses_a_shape_over_its_scratch(lib):
     B, Sq, Sk = 4, 128, 1024          # 4*128*128 rows of ctx: 128 MiB of workspace
     d = Dims(B, Sq, Sk, 7168, 1536, D.n_heads, 128, D.rope, D.kv_rank, D.v)
