@@ -36,6 +36,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -780,7 +781,11 @@ constexpr int kXThreads = 512;
 constexpr int kXPPitch = 80;                              // bytes per P^T row: 32 keys + pad
 constexpr int kXPStage = 2 * 32 * kXPPitch;               // both row tiles
 
-template <typename TL, bool FP8>
+// PV64: each P.V wave covers all 64 rows of the tile and a quarter of the columns (128),
+// instead of one row tile and half the columns: the same 128 accumulator registers and 16
+// MFMAs per block, half the V^T fragment reads (each V^T fragment feeds both row tiles) for
+// twice the P^T reads.
+template <typename TL, bool FP8, bool PV64 = false>
 __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
     static_assert(!FP8 || !Half<TL>::kF16, "an fp8 cache is read with bf16 queries");
     constexpr int NS = FP8 ? 3 : 4;                             // bf16 ring stages
@@ -971,6 +976,7 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
 
     // ==================================== P.V waves
     const int rt = (wave - 4) >> 1, ch = (wave - 4) & 1;
+    const int cq = wave - 4;             // PV64: column quarter
     const int rowO = r0 + 32 * rt + l32;
     // V^T fragments of key half ks (keys 16ks + 8(l/32) .. +7) of column block cb
     uint32_t vb0[2];
@@ -990,8 +996,9 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
             (lds_v4s*)(smem + ((vbs ^ (c | 16u)) + o + 4 * kLatBytes)));
         return __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
     };
-    // P^T of key half ks in the B layout: row l32, keys 16ks + 8(l/32) .. +7
-    const uint32_t pr0 = kPBase + rt * 32 * kXPPitch + l32 * kXPPitch + 16u * hw;
+    // P^T of key half ks in the B layout: row l32, keys 16ks + 8(l/32) .. +7 (PV64: of row
+    // tile 0; row tile 1's is 32 rows further)
+    const uint32_t pr0 = kPBase + (PV64 ? 0 : rt * 32 * kXPPitch) + l32 * kXPPitch + 16u * hw;
     // staging: P.V wave 4 + w loads keys 8w .. 8w+7 of a block (flash16_kernel's layout),
     // block j+2 during step j, and waits for block j before barrier A_j (fp8: for block j+1
     // before converting it, in the same step)
@@ -1078,24 +1085,41 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
                 asm volatile("" : "+v"(vb0[0]), "+v"(vb0[1]));
                 const int st = (j - 1) % NS;
                 const uint32_t prs = pr0 + (uint32_t)((j - 1) & 1) * kXPStage;
-                const v4u p0 = *reinterpret_cast<const v4u*>(smem + prs);
-                const v4u p1 = *reinterpret_cast<const v4u*>(smem + prs + 32u);
+                // P^T fragments [row tile][key half] (without PV64 only row tile 0's slot
+                // is used: this wave's own tile)
+                v4u pf[2][2];
+                #pragma unroll
+                for (int t = 0; t < (PV64 ? 2 : 1); ++t)
+                    #pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        pf[t][ks] = *reinterpret_cast<const v4u*>(smem + prs + t * 32 * kXPPitch + 32u * ks);
                 const uint32_t vs0 = lat_base(vb0[0], st), vs1 = lat_base(vb0[1], st);
                 constexpr int kVWin = 4;
                 v4u vf[kVWin];
-                // fragment t: key half t/8, column block 8ch + t%8 (consecutive MFMAs use
-                // different accumulators; each block's second one comes 8 MFMAs later)
-                auto vfrag = [&](int t) __attribute__((always_inline)) {
-                    return v_read((t >> 3) ? vs1 : vs0, 8 * ch + (t & 7));
+                // without PV64, fragment f (one per MFMA t): key half f/8, column block
+                // 8ch + f%8; with PV64 (one per two MFMAs, t = 2f and 2f + 1 for the two row
+                // tiles): key half f/4, column block 4cq + f%4.  Consecutive MFMAs use
+                // different accumulators; each one's next use comes 8 MFMAs later.
+                constexpr int kVFrags = PV64 ? 8 : 16;
+                auto vfrag = [&](int f) __attribute__((always_inline)) {
+                    if constexpr (PV64) return v_read((f >> 2) ? vs1 : vs0, 4 * cq + (f & 3));
+                    else return v_read((f >> 3) ? vs1 : vs0, 8 * ch + (f & 7));
                 };
                 #pragma unroll
-                for (int t = 0; t < kVWin; ++t) vf[t] = vfrag(t);
+                for (int f = 0; f < kVWin; ++f) vf[f] = vfrag(f);
                 v4u f8raw;
+                v4u cur;
                 #pragma unroll
                 for (int t = 0; t < 16; ++t) {
-                    const v4u cur = vf[t % kVWin];
-                    if (t + kVWin < 16) vf[t % kVWin] = vfrag(t + kVWin);
-                    O[t & 7] = mfma32h<TL>(cur, (t >> 3) ? p1 : p0, O[t & 7]);
+                    const int f = PV64 ? t >> 1 : t;
+                    if (!PV64 || (t & 1) == 0) {
+                        cur = vf[f % kVWin];
+                        if (f + kVWin < kVFrags) vf[f % kVWin] = vfrag(f + kVWin);
+                    }
+                    if constexpr (PV64)
+                        O[t & 7] = mfma32h<TL>(cur, pf[t & 1][f >> 2], O[t & 7]);
+                    else
+                        O[t & 7] = mfma32h<TL>(cur, pf[0][t >> 3], O[t & 7]);
                     if constexpr (FP8) {
                         // block j+2's raw rows into the fp8 stage block j left; then block
                         // j+1's, landed, into bf16 stage (j+1) % 3, which block j-2 left at
@@ -1120,7 +1144,32 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
         if (!again) break;
     }
     lds_barrier();       // F
-    if (rowO < rows_b) {
+    // an fp8 cache's values are its codes times kv_scale: ctx takes the factor here
+    const float of = FP8 ? a.o_scale : 1.f;
+    if constexpr (PV64) {
+        // both row tiles, columns 128cq .. +127: O[2 cb + t] is column block cb of row tile t
+        #pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int row = r0 + 32 * t + l32;
+            if (row >= rows_b) continue;
+            const float* xlr = xl + t * 64;
+            const float lsum = xlr[l32] + xlr[32 + l32];
+            const float M = xref[t * 64 + l32];
+            const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
+            if (cq == 0 && hw == 0) {
+                if (!work.direct) a.m[slot] = M;
+                (work.direct ? a.l_direct : a.l)[slot] = lsum;
+            }
+            float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR + 128 * cq + 4 * hw;
+            #pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                #pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) =
+                        v4f{O[2 * cb + t][4 * q], O[2 * cb + t][4 * q + 1],
+                            O[2 * cb + t][4 * q + 2], O[2 * cb + t][4 * q + 3]} * of;
+        }
+    } else if (rowO < rows_b) {
         const float* xlr = xl + rt * 64;
         const float lsum = xlr[l32] + xlr[32 + l32];
         const float M = xref[rt * 64 + l32];
@@ -1130,14 +1179,388 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
             (work.direct ? a.l_direct : a.l)[slot] = lsum;
         }
         float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR + 256 * ch + 4 * hw;
-        // an fp8 cache's values are its codes times kv_scale: ctx takes the factor here
-        const float of = FP8 ? a.o_scale : 1.f;
         #pragma unroll
         for (int cb = 0; cb < 8; ++cb)
             #pragma unroll
             for (int q = 0; q < 4; ++q)
                 *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) =
                     v4f{O[cb][4 * q], O[cb][4 * q + 1], O[cb][4 * q + 2], O[cb][4 * q + 3]} * of;
+    }
+}
+
+// ------------------------------------------------------------------ fp8 cache: a ring of codes
+// The fp8-cache pass on flash16x_kernel's eight specialised waves (PV64 layout: each P.V
+// wave covers the tile's 64 rows and 128 columns), with only the e4m3 codes in LDS: every
+// fragment is read as codes and converted to bf16 in registers, straight into the MFMA
+// operand (v_cvt_scalef32_pk_bf16_fp8, exact, scale 1; kv_scale goes to the score
+// coefficient and the output as before).  A block is 18 KB (32 keys x 512 latent bytes,
+// then 32 x 64 rope bytes) instead of the bf16 ring's 36 KB, so the ring holds eight
+// blocks: the P.V waves issue block j+6 during step j, 108 KB in flight per workgroup.
+//   Score waves: K step s of lane group g = l/16 is depth 32s + 8g .. +7 of key 16kh + l%16
+//     (Q^T is loaded in the same order): an 8-byte read (ds_read_b64) and four conversions.
+//   P.V waves: the V^T fragment of key half ks and column block cb (32 columns) comes from
+//     ds_read_b64_tr_b8: within each 16-lane group, lanes 2r and 2r+1 address bytes
+//     0-7 and 8-15 of one 16-byte row (key r of the group's eight) and lane j receives byte
+//     column j of those eight rows -- eight keys of one column, the operand lane's K values.
+//   Layout: 16-byte chunk c of latent row k sits at c ^ swz(k & 15) (bits 0-3 of the chunk
+//     index: within its 256-byte window), chunk c of rope row k at c ^ ((k >> 2) & 3).
+//     Each 32-lane half of a K read then touches 16 keys x 2 halves of chunks and each
+//     half of a V^T read 8 keys x 4 eight-byte slots, all distinct 8-byte slots of 256
+//     bytes: no bank conflicts.  The direct-to-LDS loads write chunk positions in order and
+//     take the permutation in their global offsets.
+//   Loads: P.V wave w loads latent keys 8w .. 8w+7 (four 1 KB loads, two rows each); waves
+//     0 and 1 also load the rope rows of keys 16w .. 16w+15 (one 1 KB load).
+constexpr int k8LatBytes = kFR;                        // 512 B of codes per latent row
+constexpr int k8PeBytes = kFD;                         // 64 B per rope row
+constexpr int k8LatStage = 32 * k8LatBytes;            // 16 KB
+constexpr int k8Stage = k8LatStage + 32 * k8PeBytes;   // 18 KB per block
+constexpr int k8NS = 8;                                // ring stages
+constexpr int k8Ahead = k8NS - 2;                      // blocks in flight past the next one
+
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+typedef int32_t v2i __attribute__((ext_vector_type(2)));
+
+// eight e4m3 codes (bytes 0..7) -> eight bf16 in operand order
+__device__ __forceinline__ v4u fp8x8_bf16(v2u r) {
+    auto lo2 = [](uint32_t w) __attribute__((always_inline)) {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, false));
+    };
+    auto hi2 = [](uint32_t w) __attribute__((always_inline)) {
+        return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.f, true));
+    };
+    return v4u{lo2(r[0]), hi2(r[0]), lo2(r[1]), hi2(r[1])};
+}
+
+__global__ void __launch_bounds__(kXThreads, 1) flash16x8_kernel(FlashArgs a) {
+    typedef bf16_t TL;
+    constexpr float kHeadroom = k2Headroom;
+    constexpr int kPBase = k8NS * k8Stage;                      // 144 KB: two P^T stages
+    constexpr int kXBase = kPBase + 2 * kXPStage;               // references, sums, flags
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kXBase + 2 * 128 * 4 + 64];
+    float* xref = reinterpret_cast<float*>(smem + kXBase);      // [rt][kh][32 rows]
+    float* xl = xref + 128;                                     // [rt][kh][32 rows]
+    int* flags = reinterpret_cast<int*>(xl + 128);              // [score wave]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, g = lane >> 4, l32 = lane & 31, hw = lane >> 5;
+    const FlashWork work = flash_work(a);
+    if (work.skip) return;   // past the end of a work list: the whole workgroup leaves
+
+    const int b = work.b;
+    const int rows_b = a.Sq * a.H;
+    const int r0 = work.rt * kFRows;
+    const int skb = flash_batch_keys(a, b);
+    const int k_lo = work.k_lo;
+    const int k_end = min(skb, k_lo + work.k_len);
+    int k_hi = k_end;
+    if (a.causal) k_hi = min(k_hi, skb - a.Sq + min(r0 + kFRows - 1, rows_b - 1) / a.H + 1);
+    const int nb = k_hi > k_lo ? (k_hi - k_lo + k2Keys - 1) / k2Keys : 0;
+
+    if (wave < 4) {
+        // ================================ score waves
+        const int rt = wave >> 1, kh = wave & 1;
+        const int rbase = r0 + 32 * rt;
+        const int rowS0 = rbase + l16, rowS1 = rbase + 16 + l16;
+        int lim0 = k_end - 1, lim1 = k_end - 1;
+        if (a.causal) {
+            lim0 = min(lim0, skb - a.Sq + min(rowS0, rows_b - 1) / a.H);
+            lim1 = min(lim1, skb - a.Sq + min(rowS1, rows_b - 1) / a.H);
+        }
+        const int lim_wave = __builtin_amdgcn_readfirstlane(lim0);
+        const __amdgpu_buffer_rsrc_t rq = make_rsrc(a.qa + (int64_t)b * rows_b * kFR);
+        const __amdgpu_buffer_rsrc_t rr = make_rsrc(a.qr + (int64_t)b * rows_b * kFD);
+        // Q^T fragments: step s of lane group g is depth 32s + 8g .. +7 (bf16: 16 bytes)
+        v4u qf[2][kQSteps];
+        #pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const int row = t ? rowS1 : rowS0;
+            const uint32_t qmask = oob_mask(row, rows_b);
+            #pragma unroll
+            for (int s = 0; s < kQSteps; ++s)
+                qf[t][s] = s < kRSteps
+                               ? load16(rq, ((uint32_t)row * kLatBytes + 64u * s + 16u * g) | qmask)
+                               : load16(rr, ((uint32_t)row * kPeBytes + 64u * (s - kRSteps) + 16u * g) | qmask);
+        }
+        wait_vm<0>();   // Q in registers
+
+        // K step s: bytes 32s + 8g of key kk's latent row, i.e. chunk 2s + g/2 at position
+        // (2s + g/2) ^ x, x = swz(kk & 15): 32 (s ^ x/2) + 16 (g/2 ^ x%2) + 8 (g%2); the rope
+        // steps likewise with y = (kk >> 2) & 3 over 64-byte rows
+        const int kk = 16 * kh + l16;
+        const int x = swz(kk & 15), y = (kk >> 2) & 3;
+        uint32_t kb0 = kk * k8LatBytes + 8u * (g & 1) + 16u * ((g >> 1) ^ (x & 1)) + 32u * (x >> 1);
+        uint32_t pb0 = k8LatStage + kk * k8PeBytes + 8u * (g & 1) + 16u * ((g >> 1) ^ (y & 1)) +
+                             32u * (y >> 1);
+        auto k_read = [&](uint32_t sbase, int s) __attribute__((always_inline)) {
+            const uint32_t off = s < kRSteps ? (kb0 ^ (32u * s)) : (pb0 ^ (32u * (s - kRSteps)));
+            return *reinterpret_cast<const v2u*>(smem + sbase + off);
+        };
+        // P^T writes: rows 16h + l16 of the tile, keys 16kh + 4g .. +3 (8 bytes)
+        const uint32_t pw0 = kPBase + rt * 32 * kXPPitch + l16 * kXPPitch + 2u * (16 * kh + 4 * g);
+
+        float m_ref[2] = {-INFINITY, -INFINITY}, m_neg[2] = {0.f, 0.f};
+        float thr[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+        for (int pass = 1;; ++pass) {
+            l_run[0] = l_run[1] = 0.f;
+            bool overflow = false;
+            if (nb == 0) break;
+            #pragma unroll 1
+            for (int j = 0; j <= nb; ++j) {
+                lds_barrier();        // A_j: block j is in LDS, P.V of block j-2 is done
+                v4f sc[2];
+                if (j < nb) {
+                    constexpr int kWin = 4;
+                    asm volatile("" : "+v"(kb0), "+v"(pb0));
+                    const uint32_t sbase = (uint32_t)(j % k8NS) * k8Stage;
+                    v2u kf[kWin];
+                    #pragma unroll
+                    for (int i = 0; i < kWin; ++i) kf[i] = k_read(sbase, i);
+                    // the compiler's own MFMA (not the asm form of the bf16 kernel): the K
+                    // operand is written by the conversions just before, a VALU-write ->
+                    // MFMA-read dependency whose wait states only the compiler inserts
+                    sc[0] = sc[1] = v4f{};
+                    #pragma unroll
+                    for (int s = 0; s < kQSteps; ++s) {
+                        const v4u cur = fp8x8_bf16(kf[s % kWin]);
+                        if (s + kWin < kQSteps) kf[s % kWin] = k_read(sbase, s + kWin);
+                        #pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                                __builtin_bit_cast(v8bf, cur), __builtin_bit_cast(v8bf, qf[h][s]), sc[h],
+                                0, 0, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int kq0 = k_lo + k2Keys * j + 16 * kh;
+                    if (kq0 + 15 > lim_wave) {
+                        const int kq = kq0 + 4 * g;
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            sc[0][i] = kq + i <= lim0 ? sc[0][i] : -INFINITY;
+                            sc[1][i] = kq + i <= lim1 ? sc[1][i] : -INFINITY;
+                        }
+                    }
+                    if (j == 0) {
+                        // the pass's reference proposal of each row: the raised one of a
+                        // previous pass, else this block's maximum over the half's keys
+                        #pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float mx = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+                            const float bm = row4_reduce(mx, OpMax{}) * a.c;
+                            const float prop = m_ref[h] == -INFINITY ? bm : m_ref[h];
+                            if (g == 0) xref[(rt * 2 + kh) * 32 + 16 * h + l16] = prop;
+                        }
+                    }
+                }
+                if (j == 0) {
+                    lds_barrier();    // X: both halves' proposals are in LDS
+                    #pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const int r = 16 * h + l16;
+                        const float ref = fmaxf(xref[(rt * 2) * 32 + r], xref[(rt * 2 + 1) * 32 + r]);
+                        m_ref[h] = ref;
+                        m_neg[h] = ref == -INFINITY ? 0.f : -ref;
+                        thr[h] = ref + kHeadroom;
+                    }
+                }
+                if (j < nb) {
+                    float mx[2];
+                    #pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        mx[h] = fmaxf(fmaxf(sc[h][0], sc[h][1]), fmaxf(sc[h][2], sc[h][3]));
+                    // a row past its threshold raises its reference and flags a repeat (NaN
+                    // scores come here too); rows without a reference have no visible key
+                    if (__builtin_amdgcn_ballot_w64(!(mx[0] * a.c <= thr[0]) || !(mx[1] * a.c <= thr[1]))) {
+                        #pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            const float bm = row4_reduce(mx[h], OpMax{}) * a.c;
+                            const bool over = pass < k2MaxPasses && m_ref[h] != -INFINITY && bm > thr[h];
+                            overflow |= __builtin_amdgcn_ballot_w64(over) != 0;
+                            if (over) {
+                                m_ref[h] = bm;
+                                m_neg[h] = -bm;
+                                thr[h] = bm + kHeadroom;
+                            }
+                        }
+                    }
+                    const uint32_t pws = pw0 + (uint32_t)(j & 1) * kXPStage;
+                    #pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        float e[4];
+                        #pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            e[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[h][i], a.c, m_neg[h]));
+                        l_run[h] += (e[0] + e[1]) + (e[2] + e[3]);
+                        *reinterpret_cast<v2u*>(smem + pws + 16u * h * kXPPitch) =
+                            v2u{Half<TL>::pack2(e[0], e[1]), Half<TL>::pack2(e[2], e[3])};
+                    }
+                }
+            }
+            lds_barrier();   // B1: every wave is done with the ring
+            if (lane == 0) flags[wave] = overflow ? 1 : 0;
+            lds_barrier();   // B2
+            const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+            lds_barrier();   // B3: the flags are read before they are written again
+            if (!again) break;
+        }
+        // row sums of the half and the shared references for the P.V waves
+        #pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const float l = row4_reduce(l_run[h], OpSum{});
+            if (g == 0) {
+                xl[(rt * 2 + kh) * 32 + 16 * h + l16] = l;
+                if (kh == 0) xref[(rt * 2) * 32 + 16 * h + l16] = m_ref[h];
+            }
+        }
+        lds_barrier();   // F: sums and references are in LDS
+        return;
+    }
+
+    // ==================================== P.V waves: columns 128cq .. +127, both row tiles
+    const int cq = wave - 4;
+    // V^T fragment of key half ks: lane 16G + 2r + h addresses key 16ks + 8(G/2) + r, byte
+    // column 16 (G%2) + 8h of the column block, i.e. chunk (2cb + G%2) ^ x at 8h, with
+    // x = swz(key & 15): 32 (cb ^ x/2) + 16 (G%2 ^ x%2) + 8h
+    uint32_t vb0[2];
+    #pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int G = lane >> 4, r = (lane & 15) >> 1, h = lane & 1;
+        const int key = 16 * ks + 8 * (G >> 1) + r;
+        const int x = swz(key & 15);
+        vb0[ks] = key * k8LatBytes + 8u * h + 16u * ((G & 1) ^ (x & 1)) + 32u * (x >> 1);
+    }
+    typedef __attribute__((address_space(3))) v2i lds_v2i_t;
+    auto v_read = [&](uint32_t sbase, int ks, int cb) __attribute__((always_inline)) {
+        const v2i r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            (lds_v2i_t*)(smem + sbase + (vb0[ks] ^ (32u * cb))));
+        return __builtin_bit_cast(v2u, r);
+    };
+    // P^T of row tile t, key half ks in the B layout: row l32, keys 16ks + 8(l/32) .. +7
+    const uint32_t pr0 = kPBase + l32 * kXPPitch + 16u * hw;
+    // staging (see above): latent keys 8cq .. 8cq+7; waves 0 and 1 also the rope rows of keys
+    // 16cq .. 16cq+15
+    const int wv = cq;
+    const bool pe_loader = wv < 2;
+    const uint32_t lds0 = lds_addr(smem);
+    uint32_t lat_voff[4];
+    #pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int key = 8 * wv + 2 * q + hw;
+        lat_voff[q] = (uint32_t)(2 * q + hw) * k8LatBytes + 16u * ((lane & 31) ^ swz(key & 15));
+    }
+    const int pkey = 16 * wv + (lane >> 2);
+    const uint32_t pe_voff = (uint32_t)(lane >> 2) * k8PeBytes + 16u * ((lane & 3) ^ ((pkey >> 2) & 3));
+    const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
+    const uint64_t pe_base = reinterpret_cast<uint64_t>(a.pe);
+    const int k_hi_s = __builtin_amdgcn_readfirstlane(k_hi);
+    struct Loads { v4i rk, rp; uint32_t st, st_pe; };
+    auto loads_of = [&](int j) __attribute__((always_inline)) {
+        const uint32_t sb = lds0 + (uint32_t)(j % k8NS) * k8Stage;
+        const int kb = __builtin_amdgcn_readfirstlane(k_lo + k2Keys * j + 8 * wv);
+        const uint32_t left = (uint32_t)max(0, min(8, k_hi_s - kb));
+        Loads d;
+        d.st = __builtin_amdgcn_readfirstlane(sb + 8 * wv * k8LatBytes);
+        d.rk = rsrc_span(ck_base + (uint64_t)flash_key_row(a, b, kb, k_hi_s) * kFR, 0, left * kFR);
+        // (waves 2 and 3 keep a descriptor they never use)
+        const int kp = __builtin_amdgcn_readfirstlane(k_lo + k2Keys * j + 16 * (wv & 1));
+        const uint32_t left_p = (uint32_t)max(0, min(16, k_hi_s - kp));
+        d.st_pe = __builtin_amdgcn_readfirstlane(sb + k8LatStage + 16 * (wv & 1) * k8PeBytes);
+        d.rp = rsrc_span(pe_base + (uint64_t)flash_key_row(a, b, kp, k_hi_s) * kFD, 0, left_p * kFD);
+        return d;
+    };
+    auto issue_one = [&](const Loads& d, int q) __attribute__((always_inline)) {
+        if (q < 4) dma16(d.rk, d.st + q * 1024, lat_voff[q], 0);
+        else dma16(d.rp, d.st_pe, pe_voff, 0);
+    };
+    // loads per block: 5 for the rope loaders, 4 for the others; wait until at most n
+    // blocks' loads are outstanding
+    auto issue_block = [&](const Loads& d) __attribute__((always_inline)) {
+        #pragma unroll
+        for (int q = 0; q < 4; ++q) issue_one(d, q);
+        if (pe_loader) issue_one(d, 4);
+    };
+    auto wait_blocks = [&](auto n_blocks) __attribute__((always_inline)) {
+        constexpr int n = decltype(n_blocks)::value;
+        if (pe_loader) wait_vm<5 * n>();
+        else wait_vm<4 * n>();
+    };
+    v16f O[8];
+    for (int pass = 1;; ++pass) {
+        #pragma unroll
+        for (int i = 0; i < 8; ++i) O[i] = v16f{};
+        if (nb == 0) break;
+        #pragma unroll
+        for (int j = 0; j < k8Ahead; ++j) issue_block(loads_of(j));
+        wait_blocks(std::integral_constant<int, k8Ahead - 1>{});   // block 0 has landed
+        lds_barrier();                     // A_0
+        issue_block(loads_of(k8Ahead));    // its stage is free from the pass's start
+        lds_barrier();                     // X
+        #pragma unroll 1
+        for (int j = 1; j <= nb; ++j) {
+            const Loads next = loads_of(j + k8Ahead);
+            // blocks 0 .. j+5 are issued: block j has landed when at most five are in flight
+            wait_blocks(std::integral_constant<int, k8Ahead - 1>{});
+            lds_barrier();                 // A_j
+            {
+                asm volatile("" : "+v"(vb0[0]), "+v"(vb0[1]));
+                const uint32_t sbase = (uint32_t)((j - 1) % k8NS) * k8Stage;
+                const uint32_t prs = pr0 + (uint32_t)((j - 1) & 1) * kXPStage;
+                v4u pf[2][2];
+                #pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    #pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        pf[t][ks] = *reinterpret_cast<const v4u*>(smem + prs + t * 32 * kXPPitch + 32u * ks);
+                // fragment f (one per two MFMAs, t = 2f and 2f + 1 for the two row tiles):
+                // key half f/4, column block 4cq + f%4
+                constexpr int kVWin = 3;
+                v2u vf[kVWin];
+                #pragma unroll
+                for (int f = 0; f < kVWin; ++f) vf[f] = v_read(sbase, f >> 2, 4 * cq + (f & 3));
+                v4u cur;
+                #pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    const int f = t >> 1;
+                    if ((t & 1) == 0) {
+                        cur = fp8x8_bf16(vf[f % kVWin]);
+                        if (f + kVWin < 8) vf[f % kVWin] = v_read(sbase, (f + kVWin) >> 2, 4 * cq + ((f + kVWin) & 3));
+                    }
+                    O[t & 7] = mfma32h<TL>(cur, pf[t & 1][f >> 2], O[t & 7]);
+                    // block j+6 into stage (j+6) % 8, which block j-2 left at barrier A_j
+                    if (t % 3 == 0 && t / 3 < 4) issue_one(next, t / 3);
+                    if (t == 13 && pe_loader) issue_one(next, 4);
+                }
+            }
+        }
+        wait_vm<0>();    // the zero loads of the blocks past the end have landed
+        lds_barrier();   // B1
+        lds_barrier();   // B2
+        const bool again = (flags[0] | flags[1] | flags[2] | flags[3]) != 0;
+        lds_barrier();   // B3
+        if (!again) break;
+    }
+    lds_barrier();       // F
+    // both row tiles, columns 128cq .. +127: O[2 cb + t] is column block cb of row tile t; an
+    // fp8 cache's values are its codes times kv_scale, so ctx takes the factor here
+    #pragma unroll
+    for (int t = 0; t < 2; ++t) {
+        const int row = r0 + 32 * t + l32;
+        if (row >= rows_b) continue;
+        const float* xlr = xl + t * 64;
+        const float lsum = xlr[l32] + xlr[32 + l32];
+        const float M = xref[t * 64 + l32];
+        const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
+        if (cq == 0 && hw == 0) {
+            if (!work.direct) a.m[slot] = M;
+            (work.direct ? a.l_direct : a.l)[slot] = lsum;
+        }
+        float* orow = (work.direct ? a.o_direct : a.o) + slot * kFR + 128 * cq + 4 * hw;
+        #pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+            #pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<v4f*>(orow + 32 * cb + 8 * q) =
+                    v4f{O[2 * cb + t][4 * q], O[2 * cb + t][4 * q + 1], O[2 * cb + t][4 * q + 2],
+                        O[2 * cb + t][4 * q + 3]} * a.o_scale;
     }
 }
 
@@ -2377,7 +2800,25 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     // flash32_kernel
     const char* spec32_env = std::getenv("MLA_FLASH32_SPEC");
     const bool spec32 = !(spec32_env && spec32_env[0] == '0');
-    if (p.fp8_kv && spec)
+    // 16-bit specialised waves: the P.V waves over 64 rows x 128 columns (measured at cfg4,
+    // bf16: 177-179 us against 178-186 us, and the same results bit for bit), or over 32 rows
+    // x 256 columns with MLA_FLASH16_PV=32
+    const char* pv_env = std::getenv("MLA_FLASH16_PV");
+    const bool pv64 = !(pv_env && std::strcmp(pv_env, "32") == 0);
+    // an fp8 cache: the code-ring pass (flash16x8_kernel; cfg4 shape, attention with 3d:
+    // 171 us against 220-240 us) unless MLA_FLASH16_FP8=convert asks for the pass that
+    // converts each block into a bf16 ring
+    const char* f8_env = std::getenv("MLA_FLASH16_FP8");
+    const bool f8_convert = f8_env && std::strcmp(f8_env, "convert") == 0;
+    if (p.fp8_kv && spec && !f8_convert)
+        hipLaunchKernelGGL(flash16x8_kernel, dim3(grid), dim3(kXThreads), 0, stream, a);
+    else if (p.fp8_kv && spec && pv64)
+        hipLaunchKernelGGL((flash16x_kernel<bf16_t, true, true>), dim3(grid), dim3(kXThreads), 0, stream, a);
+    else if (p.half && spec && pv64 && p.f16)
+        hipLaunchKernelGGL((flash16x_kernel<f16_t, false, true>), dim3(grid), dim3(kXThreads), 0, stream, a);
+    else if (p.half && spec && pv64)
+        hipLaunchKernelGGL((flash16x_kernel<bf16_t, false, true>), dim3(grid), dim3(kXThreads), 0, stream, a);
+    else if (p.fp8_kv && spec)
         hipLaunchKernelGGL((flash16x_kernel<bf16_t, true>), dim3(grid), dim3(kXThreads), 0, stream, a);
     else if (p.fp8_kv)
         hipLaunchKernelGGL((flash16_kernel<3, bf16_t, true>), dim3(grid), dim3(kFThreads), 0, stream, a);

@@ -119,11 +119,22 @@ def test_fused_rising_row_max(ext):
 
 
 # bf16 and fp16 run on two kernels: eight specialised waves (flash16x_kernel, the default:
-# score waves, and P.V waves one key block behind that share each row's reference) or four
-# key-split waves (flash16_kernel); MLA_FLASH16_SPEC=1 / 0 forces either, and both must
-# match the oracle everywhere
+# score waves, and P.V waves one key block behind that share each row's reference; the P.V
+# waves over 64 rows x 128 columns, or 32 x 256 with MLA_FLASH16_PV=32) or four key-split
+# waves (flash16_kernel, MLA_FLASH16_SPEC=0); every variant must match the oracle everywhere
 H16 = torch.float16
-FP16_KERNELS = pytest.mark.parametrize("spec", ["1", "0"], ids=["specialised", "key-split"])
+FP16_KERNELS = pytest.mark.parametrize("spec", ["1", "pv32", "0"],
+                                       ids=["specialised", "specialised-pv32", "key-split"])
+
+
+def set_16bit_kernel(monkeypatch, spec):
+    """specialised waves with the P.V waves over 64 rows x 128 columns (the default) or 32
+    rows x 256 columns (MLA_FLASH16_PV=32), or the key-split waves (MLA_FLASH16_SPEC=0)"""
+    monkeypatch.setenv("MLA_FLASH16_SPEC", "0" if spec == "0" else "1")
+    if spec == "pv32":
+        monkeypatch.setenv("MLA_FLASH16_PV", "32")
+    else:
+        monkeypatch.delenv("MLA_FLASH16_PV", raising=False)
 HALF_DTYPES = pytest.mark.parametrize("dt", [BF, H16], ids=["bf16", "f16"])
 
 
@@ -131,7 +142,7 @@ HALF_DTYPES = pytest.mark.parametrize("dt", [BF, H16], ids=["bf16", "f16"])
 @HALF_DTYPES
 @pytest.mark.parametrize("B,Sq,Sk,H,causal", C.FLASH16_CASES)
 def test_16bit_kernels_vs_oracle(ext, monkeypatch, spec, dt, B, Sq, Sk, H, causal):
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_16bit_kernel(monkeypatch, spec)
     args = inputs(B, Sq, Sk, H=H, seed=3 * Sk + B, dt=dt)
     close(run(ext, args, causal), oracle(args, causal), dt)
 
@@ -140,7 +151,7 @@ def test_16bit_kernels_vs_oracle(ext, monkeypatch, spec, dt, B, Sq, Sk, H, causa
 def test_16bit_kernels_full_size(ext, monkeypatch, spec):
     """B=128, Sk=4989 in bf16 (the cfg4 attention) on either 16-bit kernel, every sequence
     against the oracle."""
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_16bit_kernel(monkeypatch, spec)
     args = inputs(128, 1, 4989, seed=78, dt=BF)
     ref = R.mla_attention_official(*(t.float() for t in args), SCALE)
     close(run(ext, args, False), ref, BF)
@@ -153,7 +164,7 @@ def test_16bit_kernels_repeat_passes(ext, monkeypatch, spec, dt):
     (2^15 for fp16, 2^64 for bf16) several times: each pass raises the references and the
     pass repeats with them (in the specialised kernel both key halves of a row must agree on
     the raised reference before they add into one O)."""
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_16bit_kernel(monkeypatch, spec)
     B, Sq, Sk = 2, 1, 2048
     climb = 40.0 if dt == H16 else 200.0        # log2 units from the first key to the last
     g = torch.Generator().manual_seed(23)

@@ -10,9 +10,10 @@ outputs of standard deviation ~0.03 (larger only where a few keys make the outpu
 tests/test_parity_power_cpu.py shows, on these very inputs, that a dropped rope term, an
 ignored causal mask, a flat softmax, a wrong score scale, a stale key block or a doubled
 kv_scale each fail it.  The decoder the kernel uses is checked on its own over all 256
-codes.  The fused pass runs on either 16-bit kernel (MLA_FLASH16_SPEC=1, the default:
-specialised waves, whose P.V waves convert the codes; 0: key-split waves); the parity
-tests run both.
+codes.  The fused pass runs on the specialised waves with only the e4m3 codes in LDS, converted to
+bf16 in registers as each fragment is read (the default), on the same waves converting each
+block into a bf16 ring (MLA_FLASH16_FP8=convert), or on the key-split waves
+(MLA_FLASH16_SPEC=0); the parity tests run all three.
 """
 
 from __future__ import annotations
@@ -62,13 +63,25 @@ def test_fp8_decoder_all_codes(ext, scale):
 fp8_inputs = C.fp8_inputs
 
 
-KERNELS = pytest.mark.parametrize("spec", ["1", "0"], ids=["specialised", "key-split"])
+# the fp8 pass on the specialised waves with only the codes in LDS (the default), the same
+# waves converting each block into a bf16 ring (MLA_FLASH16_FP8=convert), or the key-split
+# waves (MLA_FLASH16_SPEC=0)
+KERNELS = pytest.mark.parametrize("spec", ["1", "convert", "0"],
+                                  ids=["code-ring", "convert-ring", "key-split"])
+
+
+def set_fp8_kernel(monkeypatch, spec):
+    monkeypatch.setenv("MLA_FLASH16_SPEC", "0" if spec == "0" else "1")
+    if spec == "convert":
+        monkeypatch.setenv("MLA_FLASH16_FP8", "convert")
+    else:
+        monkeypatch.delenv("MLA_FLASH16_FP8", raising=False)
 
 
 @KERNELS
 @pytest.mark.parametrize("B,Sq,Sk,causal", C.FP8_DENSE_CASES)
 def test_fp8kv_attention_matches_oracle(ext, monkeypatch, spec, B, Sq, Sk, causal):
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_fp8_kernel(monkeypatch, spec)
     qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(B, Sq, Sk, seed=B * 100 + Sk)
     out = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale, wuv.to(DEV),
                                   SCALE, causal).cpu()
@@ -90,7 +103,7 @@ def test_fp8kv_uint8_codes_and_scale(ext):
 def test_fp8kv_b128_full_size(ext, monkeypatch, spec):
     """B=128 decode at Sk=4989 (the bf16 configuration's shape) over an fp8 cache, every
     sequence against the oracle."""
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_fp8_kernel(monkeypatch, spec)
     qa, qr, ck, pe, kv_scale, wuv = fp8_inputs(128, 1, 4989, seed=C.FP8_FULL_SEED)
     out = ext.mla_attention_fp8kv(*(t.to(DEV) for t in (qa, qr, ck, pe)), kv_scale, wuv.to(DEV),
                                   SCALE).cpu()
@@ -131,7 +144,7 @@ def run_paged_fp8(ext, qa, qr, ck, pe, table, sl, kv_scale, wuv, causal=False):
 def test_paged_fp8kv_matches_oracle(ext, monkeypatch, spec, page, lens, causal, Sq):
     """Ragged lengths (not multiples of the page), shuffled pools and, in the last case,
     empty sequences, whose rows are zeros as in the oracle."""
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_fp8_kernel(monkeypatch, spec)
     B = len(lens)
     max_pages = max(1, -(-max(lens) // page))
     inp = paged_fp8_inputs(B, Sq, lens, page, max_pages, seed=page + 7 * B)
@@ -162,7 +175,7 @@ def test_paged_fp8kv_equals_dense_layout(ext):
 def test_paged_fp8kv_b128_ragged_full_size(ext, monkeypatch, spec):
     """B=128 decode over a ragged paged fp8 cache up to Sk=4989 keys, every sequence
     against the oracle."""
-    monkeypatch.setenv("MLA_FLASH16_SPEC", spec)
+    set_fp8_kernel(monkeypatch, spec)
     lens = C.fp8_full_paged_lens()
     page = 64
     inp = paged_fp8_inputs(128, 1, lens, page, -(-4989 // page), seed=128)
