@@ -1007,7 +1007,8 @@ int32_t mla_score_ld(int32_t sk) { return sk <= 0 ? 0 : ((sk + 31) / 32) * 32; }
 
 size_t mla_gemm_workspace_bytes(mla_dtype_t dtype, int32_t M, int32_t N, int32_t K) {
     if (M <= 0 || N <= 0 || K <= 0 || check_dtype(dtype) != MLA_OK) return 0;
-    GemmProblem p;
+    GemmProblem p;   // mla_gemm's problem, without the pointers
+    p.lda = K; p.ldb = N; p.ldc = N;
     p.M = M; p.N = N; p.K = K;
     p.half = is_half(dtype); p.f16 = is_f16(dtype); p.a_f32 = !is_half(dtype);
     return plan_gemm(p).workspace_bytes;

@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 namespace mla {
@@ -677,6 +678,48 @@ bool plan_override(const GemmProblem& p, GemmPlan* out) {
     return false;
 }
 
+// Weight-streaming plans (wgemm.hip), exact shapes: 16-bit products whose weight operand
+// dominates the traffic.  MLA_WGEMM=0 turns the engine off (every shape goes to the tiled
+// engine); MLA_WGEMM_PLAN="M,N,K,G=bn,split[,stages];..." forces a weight-streaming plan for a
+// matching problem (tuning aid, same validity checks).
+struct WTunedPlan { int M, N, K, G, bn, split, stages; };
+constexpr WTunedPlan kWTuned[] = {
+    // B = 128 decode, bf16 / fp16: 2a1, 2a2
+    {128, 1536, 7168, 1, 64, 8, 4},
+    {128, 24576, 1536, 1, 128, 1, 4},
+};
+
+bool wgemm_plan(const GemmProblem& p, GemmPlan* out) {
+    const char* off = getenv("MLA_WGEMM");
+    if (off && strcmp(off, "0") == 0) return false;
+    int bn = 0, split = 0, stages = 4;
+    if (const char* env = getenv("MLA_WGEMM_PLAN")) {
+        const char* s = env;
+        while (*s && !bn) {
+            long M, N, K, G;
+            int b, sp, used = 0, used2 = 0, ns = 4;
+            if (sscanf(s, "%ld,%ld,%ld,%ld=%d,%d%n", &M, &N, &K, &G, &b, &sp, &used) != 6) break;
+            if (sscanf(s + used, ",%d%n", &ns, &used2) == 1) used += used2;
+            if (M == p.M && N == p.N && K == p.K && G == p.G) { bn = b; split = sp; stages = ns; }
+            s += used;
+            while (*s == ';' || *s == ' ') ++s;
+        }
+    }
+    for (const auto& t : kWTuned)
+        if (!bn && t.M == p.M && t.N == p.N && t.K == p.K && t.G == p.G) {
+            bn = t.bn; split = t.split; stages = t.stages;
+        }
+    const bool ring_ok = (bn == 128 && (stages == 3 || stages == 4)) ||
+                         (bn == 64 && (stages == 3 || stages == 4 || stages == 6));
+    if (!bn || split < 1 || !ring_ok || !wgemm_supported(p, bn, split)) return false;
+    const int kslices = cdiv(p.K, 64);
+    const int per = cdiv(kslices, std::min(split, kslices));
+    if (!wgemm_supported(p, bn, cdiv(kslices, per))) return false;
+    out->bm = 128; out->bn = bn; out->split = split; out->tiles_per_wg = 1; out->wgemm = true;
+    out->stages = stages;
+    return true;
+}
+
 }  // namespace
 
 GemmPlan plan_gemm(const GemmProblem& p) {
@@ -690,7 +733,7 @@ GemmPlan plan_gemm(const GemmProblem& p) {
     const int kslices = cdiv(p.K, kBK);
     GemmPlan best;
     double best_t = 1e300;
-    if (!plan_override(p, &best) && !tuned_plan(p, &best)) {
+    if (!wgemm_plan(p, &best) && !plan_override(p, &best) && !tuned_plan(p, &best)) {
         for (const auto& t : kTiles) {
             const int tm = cdiv(p.M, t.bm), tn = cdiv(p.N, t.bn);
             const int64_t tiles = (int64_t)tm * tn * p.G;
@@ -735,6 +778,22 @@ GemmPlan plan_gemm(const GemmProblem& p) {
 
 namespace {
 
+// Sum split-K partials into C, converting to the output type.
+hipError_t split_reduce(const GemmProblem& p, const GemmArgs& a, int split, hipStream_t stream) {
+    const int64_t total = (int64_t)p.G * p.M * p.N;
+    const int rblocks = (int)std::min<int64_t>((total + 255) / 256, 8 * kNumCUs);
+    if (p.out_type == kOutF32)
+        hipLaunchKernelGGL(split_reduce_kernel<kOutF32>, dim3(rblocks), dim3(256), 0, stream,
+                           a.ws, a.ws_split, split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
+    else if (p.out_type == kOutBF16)
+        hipLaunchKernelGGL(split_reduce_kernel<kOutBF16>, dim3(rblocks), dim3(256), 0, stream,
+                           a.ws, a.ws_split, split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
+    else
+        hipLaunchKernelGGL(split_reduce_kernel<kOutF16>, dim3(rblocks), dim3(256), 0, stream,
+                           a.ws, a.ws_split, split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* workspace,
                             bool reduce, hipStream_t stream) {
     // the epilogue addresses a tile's rows with 32-bit offsets from the tile's first row
@@ -769,6 +828,11 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
         return hipErrorInvalidValue;
     const int64_t nblocks64 = (int64_t)a.tiles_m * a.tiles_n * a.G * a.split;
     if (nblocks64 <= 0 || nblocks64 > 0x7fffffff) return hipErrorInvalidValue;
+    if (plan.wgemm && wgemm_aligned(p)) {
+        const hipError_t e = launch_wgemm(p, plan, a.ws, stream);
+        if (e != hipSuccess || plan.split == 1 || !reduce) return e;
+        return split_reduce(p, a, plan.split, stream);
+    }
     int nblocks = (int)nblocks64;
     // persistent grid: full tiles of a plain NN product with no per-group K limit; any
     // other problem keeps one workgroup per tile
@@ -779,18 +843,7 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     if (persist) nblocks = cdiv(nblocks, plan.tiles_per_wg);
     hipError_t e = dispatch(p, a, plan.bm, plan.bn, nblocks, persist, stream);
     if (e != hipSuccess || plan.split == 1 || !reduce) return e;
-    const int64_t total = (int64_t)p.G * p.M * p.N;
-    const int rblocks = (int)std::min<int64_t>((total + 255) / 256, 8 * kNumCUs);
-    if (p.out_type == kOutF32)
-        hipLaunchKernelGGL(split_reduce_kernel<kOutF32>, dim3(rblocks), dim3(256), 0, stream,
-                           a.ws, a.ws_split, plan.split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
-    else if (p.out_type == kOutBF16)
-        hipLaunchKernelGGL(split_reduce_kernel<kOutBF16>, dim3(rblocks), dim3(256), 0, stream,
-                           a.ws, a.ws_split, plan.split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
-    else
-        hipLaunchKernelGGL(split_reduce_kernel<kOutF16>, dim3(rblocks), dim3(256), 0, stream,
-                           a.ws, a.ws_split, plan.split, p.C, p.ldc, p.sCg, p.G, p.M, p.N);
-    return hipGetLastError();
+    return split_reduce(p, a, plan.split, stream);
 }
 
 }  // namespace

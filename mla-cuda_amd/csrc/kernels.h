@@ -46,9 +46,20 @@ struct GemmPlan {
     int k_chunk = 0;          // K elements per slice (multiple of 32)
     int tiles_per_wg = 1;     // > 1: persistent grid of ceil(tiles / tiles_per_wg) workgroups
     size_t workspace_bytes = 0;  // fp32 partials when split > 1
+    bool wgemm = false;       // the weight-streaming engine (wgemm.hip): bm 128, bn 64 / 128
+    int stages = 4;           // its LDS ring depth
 };
 
 GemmPlan plan_gemm(const GemmProblem& p);
+// Weight-streaming engine: 16-bit A and B, NN, plain A, N % bn == 0, K % 64 == 0; fp32
+// output, or split-K partials (any output type: the reduction converts).
+// (shape conditions only, so that plans and workspace sizes depend on the shape alone; the
+// operand pointers must also be 16-byte aligned -- wgemm_aligned -- or the launch takes the
+// tiled engine with the same plan)
+bool wgemm_supported(const GemmProblem& p, int bn, int split);
+bool wgemm_aligned(const GemmProblem& p);
+hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* partials,
+                        hipStream_t stream);
 hipError_t launch_gemm(const GemmProblem& p, const GemmPlan& plan, void* workspace,
                        hipStream_t stream);
 // Split-K slices only (plan.split > 1): fp32 partials [split][G][M][N] into `partials`,

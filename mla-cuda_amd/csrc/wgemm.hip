@@ -1,0 +1,250 @@
+// Weight-streaming GEMM for the 16-bit (bf16 / fp16) products whose A operand is a small
+// batch of activation rows (M <= 128 per tile) and whose B operand is a weight matrix
+// streamed once from HBM: 2a1 (x @ W_q_a) and 2a2 (q_lat @ W_q_b) of the Q path, NN, fp32
+// output or split-K partials.  It replaces gemm_kernel for those shapes
+// (gemm.hip: plan_gemm picks it), whose staging round-trips every operand byte through
+// registers and transposes the N-contiguous weights on the way into LDS.
+//
+// Workgroup = 4 wave64s over a 128-row x BN-column tile (BN = 128 or 64), 2 x 2 waves of
+// 64 x BN/2, on the 32x32x16 16-bit MFMA.  K is walked in 64-deep slices through a 4-stage
+// LDS ring, and both operands go global -> LDS with direct-to-LDS loads (no registers):
+//   A: 128 rows x 128 bytes per slice, read back as K-contiguous fragments (ds_read_b128);
+//   W: 64 rows x 2*BN bytes per slice, N-contiguous as in memory, read back as the MFMA's
+//      K-contiguous B fragments with the transposing ds_read_b64_tr_b16 (two per fragment:
+//      within each 16-lane group lanes 4q .. 4q+3 address row q and lane j receives
+//      column j of the four rows).
+// Three slices are in flight while one feeds the MFMAs, and one barrier per slice orders
+// the ring.  Chunk permutations keep every LDS read free of bank conflicts: 16-byte chunk c
+// of A row r sits at c ^ ((r >> 1) & 7), and chunk c of W row r at c ^ (4 (r & 3)) for
+// BN = 128 (16 chunks a row), c ^ (4 ((r >> 1) & 1)) for BN = 64 (8 chunks); the loads
+// write chunk positions in order and take the permutation in their global offsets.
+// Rows past M and slices past the workgroup's K range load zeros (out-of-range buffer
+// offsets), so every slice issues the same loads and one wait count serves them all.
+#include "kernels.h"
+#include "mma.h"
+#include "stage.h"
+
+namespace mla {
+
+namespace {
+
+constexpr int kWBM = 128;                     // rows per workgroup
+constexpr int kWKS = 64;                      // K per slice
+constexpr int kWThreads = 256;
+constexpr int kWAStage = kWBM * kWKS * 2;     // 16 KB of A per slice
+constexpr int kWLoadsA = kWAStage / 1024 / 4; // 1 KB loads per wave and slice: 4
+
+struct WArgs {
+    const uint16_t* A; int64_t lda, sAg;      // elements
+    const uint16_t* B; int64_t ldb, sBg;
+    float* C; int64_t ldc, sCg;               // split == 1
+    float* ws; int64_t ws_split;              // split > 1: partials [split][G][M][N]
+    int M, N, K, G, split, k_chunk, tiles_m, tiles_n;
+};
+
+template <typename TL, int BN, int NS, int MINB>
+__global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
+    constexpr int kBRow = 2 * BN;                        // bytes per W row of a slice
+    constexpr int kBStage = kWKS * kBRow;                // 16 KB / 8 KB
+    constexpr int kStage = kWAStage + kBStage;
+    constexpr int kLoadsB = kBStage / 1024 / 4;          // 4 / 2 per wave and slice
+    constexpr int kLoads = kWLoadsA + kLoadsB;
+    constexpr int kRowsPerLoadB = 1024 / kBRow;          // 4 / 8 W rows per 1 KB load
+    constexpr int CB = BN / 64;                          // 32-column blocks per wave
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int t = xcd_logical_block(blockIdx.x, gridDim.x);
+    const int tn = t % a.tiles_n; t /= a.tiles_n;
+    const int tm = t % a.tiles_m; t /= a.tiles_m;
+    const int sp = t % a.split;
+    const int g = t / a.split;
+    const int m0 = tm * kWBM, n0 = tn * BN;
+    const int k_begin = sp * a.k_chunk;
+    const int nsl = (min(a.K, k_begin + a.k_chunk) - k_begin) / kWKS;   // whole slices
+    const int rows_a = min(kWBM, a.M - m0);
+
+    // ---- staging: wave w loads A rows 32w .. 32w+31 (four loads of 8 rows x 128 B) and W
+    // rows w*kLoadsB*kRowsPerLoadB .. of each slice (loads of kRowsPerLoadB rows)
+    const uint32_t lds0 = lds_addr(smem);
+    const uint64_t a_base = reinterpret_cast<uint64_t>(a.A + g * a.sAg + (int64_t)m0 * a.lda);
+    const uint64_t b_base = reinterpret_cast<uint64_t>(a.B + g * a.sBg + n0);
+    uint32_t a_voff[kWLoadsA], b_voff[kLoadsB];
+    #pragma unroll
+    for (int q = 0; q < kWLoadsA; ++q) {
+        const int row = 32 * wave + 8 * q + (lane >> 3);
+        a_voff[q] = (uint32_t)row * (uint32_t)a.lda * 2u + 16u * ((lane & 7) ^ ((row >> 1) & 7));
+    }
+    #pragma unroll
+    for (int q = 0; q < kLoadsB; ++q) {
+        const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
+        const int pos = lane % (kBRow / 16);
+        const int sw = BN == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+        b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 16u * (pos ^ sw);
+    }
+    // valid bytes of a slice: A rows below rows_a, all 64 W rows (whole slices)
+    const uint32_t a_bytes = (uint32_t)(rows_a - 1) * (uint32_t)a.lda * 2u + 128u;
+    const uint32_t b_bytes = (uint32_t)(kWKS - 1) * (uint32_t)a.ldb * 2u + (uint32_t)kBRow;
+    auto issue_slice = [&](int s) __attribute__((always_inline)) {
+        const uint32_t st = lds0 + (uint32_t)(s % NS) * kStage;
+        const int k = k_begin + s * kWKS;
+        const bool live = s < nsl;
+        const v4i ra = rsrc_span(a_base + 2ull * (uint64_t)k, 0, live ? a_bytes : 0u);
+        const v4i rb = rsrc_span(b_base + 2ull * (uint64_t)k * (uint64_t)a.ldb, 0, live ? b_bytes : 0u);
+        #pragma unroll
+        for (int q = 0; q < kWLoadsA; ++q)
+            dma16(ra, __builtin_amdgcn_readfirstlane(st + (uint32_t)(32 * wave + 8 * q) * 128u),
+                  a_voff[q], 0);
+        #pragma unroll
+        for (int q = 0; q < kLoadsB; ++q)
+            dma16(rb, __builtin_amdgcn_readfirstlane(
+                          st + kWAStage + (uint32_t)((wave * kLoadsB + q) * kRowsPerLoadB) * kBRow),
+                  b_voff[q], 0);
+    };
+
+    // ---- fragments: wave (wm, wn) covers rows 64wm .. +63 and columns (BN/2)wn .. +BN/2-1
+    const int wm = wave >> 1, wn = wave & 1;
+    // A fragment of row block rb, K step kt: row 64wm + 32rb + l%32, bytes 32kt + 16(l/32)
+    uint32_t a_rd[2];
+    #pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+        const int row = 64 * wm + 32 * rb + (lane & 31);
+        a_rd[rb] = (uint32_t)row * 128u + 16u * ((lane >> 5) ^ ((row >> 1) & 7));
+    }
+    // W fragment half p of column block cb, K step kt: lane 16G + 4q + i reads row
+    // 16kt + 8(G/2) + 4p + q, columns (BN/2)wn + 32cb + 16(G%2) + 4i .. +3
+    const int G = lane >> 4, q4 = (lane >> 2) & 3, i4 = lane & 3;
+    uint32_t b_rd[CB];
+    #pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+        const int chunk = ((BN / 2) * wn + 32 * cb + 16 * (G & 1) + 4 * i4) / 8;
+        const int sw = BN == 128 ? 4 * q4 : 4 * (q4 >> 1);
+        b_rd[cb] = kWAStage + (uint32_t)(8 * (G >> 1) + q4) * kBRow + 16u * (chunk ^ sw) + 8u * (i4 & 1);
+    }
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
+    auto b_frag = [&](uint32_t st, int kt, int cb) __attribute__((always_inline)) {
+        const uint32_t o = st + b_rd[cb] + (uint32_t)(16 * kt) * kBRow;
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + o));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + o + 4 * kBRow));
+        return __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    auto a_frag = [&](uint32_t st, int kt, int rb) __attribute__((always_inline)) {
+        // chunk 2kt + l/32 at (2kt + l/32) ^ s: a_rd holds (l/32) ^ s, and 2kt ^ s = 2kt ^
+        // (s & 6) ^ (s & 1) -- the XOR with 32kt only touches bits 5-6 of the offset
+        return *reinterpret_cast<const v4u*>(smem + st + (a_rd[rb] ^ (32u * kt)));
+    };
+
+    v16f acc[2][CB];
+    #pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+        #pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
+
+    #pragma unroll
+    for (int s = 0; s < NS - 1; ++s) issue_slice(s);
+    #pragma unroll 1
+    for (int s = 0; s < nsl; ++s) {
+        wait_vm<(NS - 2) * kLoads>();   // slice s has landed (the NS - 2 after it may not)
+        lds_barrier();                    // every wave's part of it; slice s-1 is consumed
+        issue_slice(s + NS - 1);          // into stage (s - 1) % NS
+        const uint32_t st = (uint32_t)(s % NS) * kStage;
+        #pragma unroll
+        for (int kt = 0; kt < kWKS / 16; ++kt) {
+            v4u af[2], bf[CB];
+            #pragma unroll
+            for (int rb = 0; rb < 2; ++rb) af[rb] = a_frag(st, kt, rb);
+            #pragma unroll
+            for (int cb = 0; cb < CB; ++cb) bf[cb] = b_frag(st, kt, cb);
+            #pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                #pragma unroll
+                for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = Mma<TL>::sub(af[rb], bf[cb], 0, acc[rb][cb]);
+        }
+    }
+    wait_vm<0>();   // the zero loads past the range have landed
+
+    // ---- epilogue: fp32 C, or this split's partials
+    float* out;
+    int64_t ld;
+    if (a.split > 1) {
+        out = a.ws + (int64_t)sp * a.ws_split + (int64_t)g * a.M * a.N;
+        ld = a.N;
+    } else {
+        out = a.C + (int64_t)g * a.sCg;
+        ld = a.ldc;
+    }
+    #pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+        #pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+            #pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = 64 * wm + 32 * rb + acc_row(e, lane);
+                if (row < rows_a)
+                    out[(int64_t)(m0 + row) * ld + n0 + (BN / 2) * wn + 32 * cb + (lane & 31)] =
+                        acc[rb][cb][e];
+            }
+}
+
+// Stage counts per column tile: 128 columns x 4 stages (128 KB of LDS, one workgroup per
+// CU) or 3 (96 KB); 64 columns x 3 (72 KB, two per CU), 4 or 6 stages (96 / 144 KB).
+template <typename TL>
+hipError_t launch_wgemm_t(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 block,
+                          hipStream_t stream) {
+    if (plan.bn == 128 && plan.stages == 4)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1>), grid, block, 0, stream, a);
+    else if (plan.bn == 128 && plan.stages == 3)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 3, 1>), grid, block, 0, stream, a);
+    else if (plan.bn == 64 && plan.stages == 3)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 3, 2>), grid, block, 0, stream, a);
+    else if (plan.bn == 64 && plan.stages == 4)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 4, 1>), grid, block, 0, stream, a);
+    else if (plan.bn == 64 && plan.stages == 6)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 6, 1>), grid, block, 0, stream, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool wgemm_supported(const GemmProblem& p, int bn, int split) {
+    return p.half && !p.a_f32 && !p.b_nt && p.amode == kAPlain &&
+           (p.out_type == kOutF32 || split > 1) && split >= 1 &&
+           !p.k_len && !p.b_pages && (bn == 64 || bn == 128) && p.N % bn == 0 &&
+           p.K % kWKS == 0 && p.lda >= kWKS && p.ldb >= bn && p.M > 0 && p.G >= 1 &&
+           // 16-byte aligned rows and groups for the 16-byte loads
+           p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sAg % 8 == 0 && p.sBg % 8 == 0 &&
+           // 32-bit buffer offsets within a tile: 128 A rows, 64 W rows
+           (int64_t)kWBM * p.lda * 2 < kRsrcRange && (int64_t)kWKS * p.ldb * 2 < kRsrcRange;
+}
+
+bool wgemm_aligned(const GemmProblem& p) {
+    return (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0;
+}
+
+hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* partials,
+                        hipStream_t stream) {
+    if (!wgemm_supported(p, plan.bn, plan.split) || !wgemm_aligned(p) || plan.k_chunk <= 0 ||
+        plan.k_chunk % kWKS != 0 || (int64_t)plan.k_chunk * plan.split < p.K)
+        return hipErrorInvalidValue;
+    WArgs a;
+    a.A = static_cast<const uint16_t*>(p.A); a.lda = p.lda; a.sAg = p.sAg;
+    a.B = static_cast<const uint16_t*>(p.B); a.ldb = p.ldb; a.sBg = p.sBg;
+    a.C = static_cast<float*>(p.C); a.ldc = p.ldc; a.sCg = p.sCg;
+    a.ws = partials; a.ws_split = (int64_t)p.G * p.M * p.N;
+    a.M = p.M; a.N = p.N; a.K = p.K; a.G = p.G;
+    a.split = plan.split; a.k_chunk = plan.k_chunk;
+    a.tiles_m = (p.M + kWBM - 1) / kWBM;
+    a.tiles_n = p.N / plan.bn;
+    if (plan.split > 1 && !partials) return hipErrorInvalidValue;
+    const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * a.split * a.G;
+    if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)blocks), block(kWThreads);
+    if (p.f16) return launch_wgemm_t<f16_t>(a, plan, grid, block, stream);
+    return launch_wgemm_t<bf16_t>(a, plan, grid, block, stream);
+}
+
+}  // namespace mla

@@ -55,6 +55,31 @@ def test_gemm_bf16(ext, M, N, K):
     torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("dt", [BF, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("M,N,K,plan", [
+    (128, 1536, 7168, "64,8"),      # 2a1 at B = 128
+    (128, 24576, 1536, "128,1"),    # 2a2 at B = 128
+    (40, 256, 192, "128,1"),        # rows off the 128-row tile
+    (130, 128, 128, "64,2"),        # two row tiles, the second of 2 rows
+    (7, 128, 320, "128,3"),         # slices 2, 2, 1 over the splits
+    (1, 576, 7168, "64,16"),        # the KV projection's shape at B = 1
+    (128, 64, 4096, "64,64"),       # one slice per split
+])
+def test_weight_streaming_gemm(ext, monkeypatch, dt, M, N, K, plan):
+    """The weight-streaming engine (forced by MLA_WGEMM_PLAN) against the float64 product
+    of the same 16-bit values, and against the tiled engine (MLA_WGEMM=0)."""
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn(M, K, generator=g).to(dt)
+    W = (torch.randn(K, N, generator=g) / math.sqrt(K)).to(dt)
+    monkeypatch.setenv("MLA_WGEMM_PLAN", f"{M},{N},{K},1={plan}")
+    got = ext.gemm(gpu(A), gpu(W)).cpu()
+    ref = (A.double() @ W.double()).float()
+    torch.testing.assert_close(got, ref, rtol=1e-4, atol=1e-4)
+    monkeypatch.setenv("MLA_WGEMM", "0")
+    tiled = ext.gemm(gpu(A), gpu(W)).cpu()
+    torch.testing.assert_close(got, tiled, rtol=1e-4, atol=1e-4)
+
+
 def test_rmsnorm_rope_bf16(ext):
     g = torch.Generator().manual_seed(3)
     x = torch.randn(16, 1536, generator=g)
