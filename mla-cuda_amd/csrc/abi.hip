@@ -239,12 +239,14 @@ GemmProblem q_up_problem(mla_dtype_t dt, const mla_dims_t* d, const void* q_lat,
     return p;
 }
 
-GemmProblem absorb_problem(mla_dtype_t dt, const mla_dims_t* d, const float* q_raw,
-                           const void* W_uk, void* q_abs) {
+// A is q_raw's nope columns (fp32, [B*Sq, H*(nope+rope)]), or with nope16 the 16-bit
+// q_nope [B*Sq, H, nope] that 2a2's fused epilogue writes.
+GemmProblem absorb_problem(mla_dtype_t dt, const mla_dims_t* d, const void* q_raw,
+                           const void* W_uk, void* q_abs, bool nope16 = false) {
     const int qk = d->nope + d->rope;
     GemmProblem p;
-    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = true; p.out_type = storage_out(dt);
-    p.A = q_raw; p.lda = (int64_t)d->heads * qk; p.sAg = qk;
+    p.half = is_half(dt); p.f16 = is_f16(dt); p.a_f32 = !nope16; p.out_type = storage_out(dt);
+    p.A = q_raw; p.lda = (int64_t)d->heads * (nope16 ? d->nope : qk); p.sAg = nope16 ? d->nope : qk;
     p.B = W_uk; p.ldb = d->kv_rank; p.sBg = (int64_t)d->nope * d->kv_rank;
     p.C = q_abs; p.ldc = (int64_t)d->heads * d->kv_rank; p.sCg = d->kv_rank;
     p.M = d->batch * d->sq; p.N = d->kv_rank; p.K = d->nope; p.G = d->heads;
@@ -281,8 +283,18 @@ GemmProblem out_problem(mla_dtype_t dt, const mla_dims_t* d, const float* ctx,
 
 struct QLayout {
     GemmPlan down, up, absorb;
-    size_t off_lat_acc, off_lat, off_raw, off_up_ws, off_abs_ws, total;
+    bool fused;   // 2a2 writes q_nope and the rotated q_rope itself (no 2b launch)
+    size_t off_lat_acc, off_lat, off_raw, off_up_ws, off_abs_ws, off_rope_tab, total;
 };
+
+// 2a2's fused epilogue (wgemm.hip) for a 16-bit weight-streaming 2a2 plan without split-K;
+// MLA_QUP_FUSE=0 keeps the separate 2b launch (a comparison aid: both give the same bits).
+bool qup_fused(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up) {
+    const char* env = getenv("MLA_QUP_FUSE");
+    if (env && strcmp(env, "0") == 0) return false;
+    return is_half(dt) && up.wgemm && up.split == 1 && d->nope % 32 == 0 && d->rope % 32 == 0 &&
+           d->rope > 0 && d->rope <= 64;
+}
 
 QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     QLayout L;
@@ -290,7 +302,8 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     const size_t n_raw = (size_t)d->heads * (d->nope + d->rope);
     L.down = plan_gemm(q_down_problem(dt, d, nullptr, nullptr, nullptr));
     L.up = plan_gemm(q_up_problem(dt, d, nullptr, nullptr, nullptr));
-    L.absorb = plan_gemm(absorb_problem(dt, d, nullptr, nullptr, nullptr));
+    L.fused = qup_fused(dt, d, L.up);
+    L.absorb = plan_gemm(absorb_problem(dt, d, nullptr, nullptr, nullptr, L.fused));
     size_t o = 0;
     L.off_lat_acc = o;  // 2a1 output or its split partials (summed by the norm kernel)
     o = align_up(o + (size_t)L.down.split * bq * d->q_lora * sizeof(float));
@@ -302,6 +315,8 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     o = align_up(o + L.up.workspace_bytes);
     L.off_abs_ws = o;
     o = align_up(o + L.absorb.workspace_bytes);
+    L.off_rope_tab = o;   // 2a-n's RoPE angle table for the fused epilogue
+    if (L.fused) o = align_up(o + bq * (size_t)d->rope * sizeof(float));
     L.total = o;
     return L;
 }
@@ -592,13 +607,33 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
     } else {
         MLA_TRY_HIP(launch_gemm(down, down_plan, nullptr, stream), "2a1 launch");
     }
-    // 2a-n
+    // 2a-n (with the fused epilogue, also the rows' RoPE cos / sin table)
+    RopeTable rt;
+    if (L.fused) {
+        rt.cos_sin = at<float>(workspace, L.off_rope_tab);
+        rt.positions = positions; rt.inv_freq = inv_freq; rt.half = dims->rope / 2;
+        rt.Sq = dims->sq; rt.per_batch = pos_per_batch;
+    }
     MLA_TRY_HIP(launch_rmsnorm(lat_acc, nsplit, (int64_t)bq * dims->q_lora, q_norm_w, lat,
-                               storage_out(dtype), bq, dims->q_lora, (float)eps, stream),
+                               storage_out(dtype), bq, dims->q_lora, (float)eps, stream, rt),
                 "2a-n launch");
     // 2a2, then 2b.  A split-K 2a2 leaves its partials in its workspace and the RoPE kernel
-    // sums them (the nope columns into raw for 2c): no reduction launch.
+    // sums them (the nope columns into raw for 2c): no reduction launch.  With the fused
+    // epilogue 2a2 writes the 16-bit q_nope (into raw's space) and q_rope itself.
     GemmProblem up = q_up_problem(dtype, dims, lat, W_q_b, raw);
+    if (L.fused) {
+        QUpEpilogue qe;
+        qe.q_nope = raw; qe.q_rope = q_rope; qe.cos_sin = rt.cos_sin;
+        qe.H = dims->heads; qe.nope = dims->nope; qe.rope = dims->rope;
+        up.qup = &qe;
+        up.C = nullptr;
+        MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream),
+                    "2a2 + 2b launch");
+        GemmProblem ab = absorb_problem(dtype, dims, raw, W_uk, q_absorbed, true);
+        MLA_TRY_HIP(launch_gemm(ab, L.absorb, at<void>(workspace, L.off_abs_ws), stream),
+                    "2c launch");
+        return ok();
+    }
     if (L.up.split > 1) {
         float* up_parts = at<float>(workspace, L.off_up_ws);
         MLA_TRY_HIP(launch_gemm_partials(up, L.up, up_parts, stream), "2a2 launch");

@@ -82,6 +82,34 @@ __device__ __forceinline__ int load_uniform(const int* p) {
 }
 
 // ----------------------------------------------------------------------------------
+// RoPE rotation of the interleaved pair (x0, x1) = (x[2i], x[2i+1]) by the angle
+// pos * inv_freq[i] (exhaustive_benchmark_suite.py:210-232); the angle is formed in fp32
+// from the caller's inv_freq table, and cos / sin are the accurate cosf / sinf.  2b
+// (rowops.hip), the KV append and 2a2's fused epilogue (wgemm.hip) share these.
+// ----------------------------------------------------------------------------------
+__device__ __forceinline__ float rope_angle(int64_t pos, float inv_freq) {
+    return (float)pos * inv_freq;
+}
+// cos and sin of the angle, both from one sincosf: every kernel that rotates calls this, so
+// the values agree to the bit across kernels (separate cosf / sinf calls may or may not be
+// merged into a sincos by the compiler, depending on the context).
+__device__ __forceinline__ void rope_cos_sin(float ang, float* c, float* s) { sincosf(ang, s, c); }
+// Written with one explicit fma each, and the result pinned to an fp32 register value (the
+// empty asm), so that every kernel that inlines them rounds the same way: the compiler can
+// neither pick another contraction nor fuse the fma with a following fp16 conversion into
+// v_fma_mix, which rounds once to 16 bits instead of to fp32 and then to 16 bits.
+__device__ __forceinline__ float fp32_pinned(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+__device__ __forceinline__ float rope_even(float x0, float x1, float c, float s) {
+    return fp32_pinned(__builtin_fmaf(x0, c, -(x1 * s)));
+}
+__device__ __forceinline__ float rope_odd(float x0, float x1, float c, float s) {
+    return fp32_pinned(__builtin_fmaf(x0, s, x1 * c));
+}
+
+// ----------------------------------------------------------------------------------
 // XCD-aware block order.  The dispatcher hands workgroup b to XCD b % 8; this maps the
 // hardware id to a logical tile id so that each XCD walks a CONTIGUOUS run of logical
 // tiles (and therefore keeps the operands those tiles share in its own L2).

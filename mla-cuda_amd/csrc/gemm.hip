@@ -828,6 +828,7 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
         return hipErrorInvalidValue;
     const int64_t nblocks64 = (int64_t)a.tiles_m * a.tiles_n * a.G * a.split;
     if (nblocks64 <= 0 || nblocks64 > 0x7fffffff) return hipErrorInvalidValue;
+    if (p.qup && !(plan.wgemm && wgemm_aligned(p))) return hipErrorInvalidValue;
     if (plan.wgemm && wgemm_aligned(p)) {
         const hipError_t e = launch_wgemm(p, plan, a.ws, stream);
         if (e != hipSuccess || plan.split == 1 || !reduce) return e;

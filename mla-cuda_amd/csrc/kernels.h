@@ -18,6 +18,30 @@ namespace mla {
 enum AMode { kAPlain = 0, kARowRecip = 1, kAAlpha = 2 };
 enum OutType { kOutF32 = 0, kOutBF16 = 1, kOutF16 = 2 };   // the codes Store16<> takes
 
+// 2a2's fused epilogue (16-bit weight-streaming plans with split 1 only): instead of the
+// fp32 product C [M, H*(nope+rope)], the nope columns of every head go to q_nope
+// [M, H, nope] and the rope columns, rotated, to q_rope [M, H, rope], both rounded once to
+// the storage format -- the rounding 2c and 2b apply to the same fp32 values.  The rotation
+// of row m, pair i takes cos_sin[2 (m * rope/2 + i)] and the sin after it, the table the
+// 2a-n launch writes (RopeTable).  nope and rope are multiples of 32, rope <= 64.
+struct QUpEpilogue {
+    void* q_nope = nullptr;
+    void* q_rope = nullptr;
+    const float* cos_sin = nullptr;
+    int H = 0, nope = 0, rope = 0;
+};
+
+// Optional output of the 2a-n launch for that epilogue: row m's cos and sin of the angles
+// pos(m) * inv_freq[i], i < half, with pos(m) = positions[m] (per_batch) or
+// positions[m % Sq] -- the angles and the sincosf of 2b.
+struct RopeTable {
+    float* cos_sin = nullptr;
+    const int64_t* positions = nullptr;
+    const float* inv_freq = nullptr;
+    int half = 0, Sq = 1;
+    bool per_batch = false;
+};
+
 struct GemmProblem {
     const void* A = nullptr; int64_t lda = 0, sAg = 0;
     const void* B = nullptr; int64_t ldb = 0, sBg = 0;
@@ -37,6 +61,7 @@ struct GemmProblem {
     const int* k_len = nullptr;
     const int* b_pages = nullptr;
     int page_size = 0, max_pages = 0;
+    const QUpEpilogue* qup = nullptr;   // weight-streaming plans only (launch_wgemm)
 };
 
 // Tile/split plan chosen for a problem (pure function of the shape; see plan_gemm).
@@ -57,6 +82,8 @@ GemmPlan plan_gemm(const GemmProblem& p);
 // operand pointers must also be 16-byte aligned -- wgemm_aligned -- or the launch takes the
 // tiled engine with the same plan)
 bool wgemm_supported(const GemmProblem& p, int bn, int split);
+// The fused 2a2 epilogue applies to a problem that wgemm_supported takes with split 1.
+bool qup_supported(const GemmProblem& p, const QUpEpilogue& q);
 bool wgemm_aligned(const GemmProblem& p);
 hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* partials,
                         hipStream_t stream);
@@ -71,7 +98,7 @@ hipError_t launch_gemm_partials(const GemmProblem& p, const GemmPlan& plan, floa
 // 2a-n: out[m][:] = sum_s in[s][m][:] * rsqrt(mean((sum_s in)^2) + eps) * gain
 hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride,
                           const void* gain, void* out, OutType out_type, int M, int N,
-                          float eps, hipStream_t stream);
+                          float eps, hipStream_t stream, const RopeTable& rope_table = {});
 // 2b
 // positions [Sq] shared by the batch, or [B*Sq] per sequence (pos_per_batch)
 // With nope_out, q_raw is 2a2's split-K partials ([nsplit][B*Sq][H*(nope+rope)],

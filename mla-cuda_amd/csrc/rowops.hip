@@ -94,9 +94,20 @@ __device__ __forceinline__ void rms_row(const float* base, int nsplit, int64_t s
 template <int OUT>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ in, int nsplit,
                                                       int64_t split_stride, const void* gain_v,
-                                                      void* out_v, int N, float eps) {
+                                                      void* out_v, int N, float eps,
+                                                      RopeTable rt) {
     __shared__ float red[4];
     const int row = blockIdx.x;
+    // the row's RoPE angle table for 2a2's fused epilogue, when asked for
+    if (rt.cos_sin && (int)threadIdx.x < rt.half) {
+        const int i = threadIdx.x;
+        const int64_t pos = rt.positions[rt.per_batch ? row : row % rt.Sq];
+        float c, s;
+        rope_cos_sin(rope_angle(pos, rt.inv_freq[i]), &c, &s);
+        float* t = rt.cos_sin + 2 * ((int64_t)row * rt.half + i);
+        t[0] = c;
+        t[1] = s;
+    }
     void* out_row = OUT == kOutF32
                         ? static_cast<void*>(static_cast<float*>(out_v) + (int64_t)row * N)
                         : static_cast<void*>(static_cast<uint16_t*>(out_v) + (int64_t)row * N);
@@ -106,8 +117,8 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
 // ---- 2b: one workgroup per (query row bq, chunk of 32 heads; 4 when it also sums 2a2's
 // split partials, below).  Every head of a row uses
 // the same rope/2 angles, so the workgroup evaluates them once into LDS: angle =
-// float(pos) * inv_freq[i] in fp32 with the caller's inv_freq table, then accurate
-// cosf/sinf (not the fast intrinsics: at positions ~5e3 an angle ulp is ~5e-4 rad and
+// float(pos) * inv_freq[i] in fp32 with the caller's inv_freq table, then the accurate
+// sincosf (not the fast intrinsics: at positions ~5e3 an angle ulp is ~5e-4 rad and
 // large arguments need full range reduction).  Threads then rotate the (head, pair)
 // elements of the chunk with 64-bit loads and stores.
 // When 2a2 ran split-K, q_raw is its partials ([nsplit][rows][H*qk], split_stride apart)
@@ -119,12 +130,6 @@ constexpr int kRopeHeads = 32;
 constexpr int kRopeSumHeads = 4;   // heads per workgroup when it also sums 2a2's partials
 constexpr int kRopeMaxHalf = 256;
 
-// Rotation of the interleaved pair (x0, x1) = (x[2i], x[2i+1]) by angle pos * inv_freq[i].
-__device__ __forceinline__ float rope_angle(int64_t pos, float inv_freq) {
-    return (float)pos * inv_freq;
-}
-__device__ __forceinline__ float rope_even(float x0, float x1, float c, float s) { return x0 * c - x1 * s; }
-__device__ __forceinline__ float rope_odd(float x0, float x1, float c, float s) { return x0 * s + x1 * c; }
 
 template <int OUT>
 __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_raw,
@@ -144,8 +149,7 @@ __global__ void __launch_bounds__(256) rope_kernel(const float* __restrict__ q_r
     const int64_t pos = positions[pos_per_batch ? bq : bq % Sq];
     for (int i = threadIdx.x; i < half; i += blockDim.x) {
         const float ang = rope_angle(pos, inv_freq[i]);
-        cs[i] = cosf(ang);
-        sn[i] = sinf(ang);
+        rope_cos_sin(ang, &cs[i], &sn[i]);
     }
     const int64_t row0 = (int64_t)bq * H * qk;
     if (nope_out) {
@@ -281,7 +285,8 @@ __global__ void __launch_bounds__(256) kv_append_kernel(const float* __restrict_
             x1 += base[q * split_stride + R + 2 * i + 1];
         }
         const float ang = rope_angle(pos, inv_freq[i]);
-        const float c = cosf(ang), sn = sinf(ang);
+        float c, sn;
+        rope_cos_sin(ang, &c, &sn);
         const float e = rope_even(x0, x1, c, sn), o = rope_odd(x0, x1, c, sn);
         if constexpr (OUT == kOutF32) {
             float* dst = static_cast<float*>(pe) + crow * D + 2 * i;
@@ -491,17 +496,19 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
 
 hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, const void* gain,
                           void* out, OutType out_type, int M, int N, float eps,
-                          hipStream_t stream) {
+                          hipStream_t stream, const RopeTable& rt) {
     if (M <= 0) return hipSuccess;
+    if (rt.cos_sin && (rt.half <= 0 || rt.half > 256 || !rt.positions || !rt.inv_freq || rt.Sq < 1))
+        return hipErrorInvalidValue;
     if (out_type == kOutF32)
         hipLaunchKernelGGL(rmsnorm_kernel<kOutF32>, dim3(M), dim3(256), 0, stream, in, nsplit,
-                           split_stride, gain, out, N, eps);
+                           split_stride, gain, out, N, eps, rt);
     else if (out_type == kOutBF16)
         hipLaunchKernelGGL(rmsnorm_kernel<kOutBF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
-                           split_stride, gain, out, N, eps);
+                           split_stride, gain, out, N, eps, rt);
     else
         hipLaunchKernelGGL(rmsnorm_kernel<kOutF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
-                           split_stride, gain, out, N, eps);
+                           split_stride, gain, out, N, eps, rt);
     return hipGetLastError();
 }
 

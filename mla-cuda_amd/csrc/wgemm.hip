@@ -28,6 +28,8 @@ namespace mla {
 
 namespace {
 
+typedef float v2f __attribute__((ext_vector_type(2)));
+
 constexpr int kWBM = 128;                     // rows per workgroup
 constexpr int kWKS = 64;                      // K per slice
 constexpr int kWThreads = 256;
@@ -40,9 +42,10 @@ struct WArgs {
     float* C; int64_t ldc, sCg;               // split == 1
     float* ws; int64_t ws_split;              // split > 1: partials [split][G][M][N]
     int M, N, K, G, split, k_chunk, tiles_m, tiles_n;
+    QUpEpilogue q;                            // the fused 2a2 epilogue (QUP kernels)
 };
 
-template <typename TL, int BN, int NS, int MINB>
+template <typename TL, int BN, int NS, int MINB, bool QUP>
 __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     constexpr int kBRow = 2 * BN;                        // bytes per W row of a slice
     constexpr int kBStage = kWKS * kBRow;                // 16 KB / 8 KB
@@ -51,7 +54,9 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     constexpr int kLoads = kWLoadsA + kLoadsB;
     constexpr int kRowsPerLoadB = 1024 / kBRow;          // 4 / 8 W rows per 1 KB load
     constexpr int CB = BN / 64;                          // 32-column blocks per wave
-    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage];
+    // QUP: the tile rows' RoPE table (rows x 32 pairs x (cos, sin)) after the ring
+    constexpr int kTab = QUP ? kWBM * 32 * 8 : 0;
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage + kTab];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -142,8 +147,25 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         #pragma unroll
         for (int cb = 0; cb < CB; ++cb) acc[rb][cb] = v16f{};
 
+    // QUP: a tile with rope columns loads its rows' cos / sin table (2a-n wrote it) into LDS
+    // ahead of the ring, 1 KB = 1024 / (8 half) rows per load; rows past M read zeros.  The
+    // first slice's wait covers these loads too (vmcnt retires in order).
+    bool has_rope = false;
+    if constexpr (QUP) {
+        const int qk = a.q.nope + a.q.rope, half = a.q.rope >> 1;
+        #pragma unroll
+        for (int c = 0; c < BN; c += 32) has_rope |= (n0 + c) % qk >= a.q.nope;
+        if (has_rope) {
+            const v4i rt = rsrc_span(reinterpret_cast<uint64_t>(a.q.cos_sin + 2 * (int64_t)m0 * half),
+                                     0, (uint32_t)(rows_a * half * 8));
+            for (int b = wave; b < half; b += 4)   // kWBM * half * 8 bytes = half KB
+                dma16(rt, __builtin_amdgcn_readfirstlane(lds0 + NS * kStage + 1024u * b),
+                      1024u * b + 16u * lane, 0);
+        }
+    }
     #pragma unroll
     for (int s = 0; s < NS - 1; ++s) issue_slice(s);
+
     #pragma unroll 1
     for (int s = 0; s < nsl; ++s) {
         wait_vm<(NS - 2) * kLoads>();   // slice s has landed (the NS - 2 after it may not)
@@ -164,6 +186,52 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         }
     }
     wait_vm<0>();   // the zero loads past the range have landed
+
+    if constexpr (QUP) {
+        // ---- fused 2a2 epilogue: nope blocks to q_nope, rope blocks rotated to q_rope.
+        // Every 32-column block lies inside one head's nope or rope part (nope, rope and
+        // the block start are multiples of 32); the pair partner of column c is column c ^ 1,
+        // the neighbouring lane.  cos / sin come from the table 2a-n wrote for these rows,
+        // staged in LDS at the start.
+        const int half = a.q.rope >> 1;
+        const int qk = a.q.nope + a.q.rope;
+        if (has_rope) __syncthreads();   // every wave's table loads (uniform per workgroup)
+        const int64_t ld_nope = (int64_t)a.q.H * a.q.nope, ld_rope = (int64_t)a.q.H * a.q.rope;
+        #pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            #pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                const int c0 = n0 + (BN / 2) * wn + 32 * cb;
+                const int h = c0 / qk, j0 = c0 - h * qk;
+                if (j0 < a.q.nope) {
+                    uint16_t* dst = static_cast<uint16_t*>(a.q.q_nope) + (int64_t)h * a.q.nope + j0 + (lane & 31);
+                    #pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const int row = 64 * wm + 32 * rb + acc_row(e, lane);
+                        if (row < rows_a)
+                            dst[(int64_t)(m0 + row) * ld_nope] = (uint16_t)Half<TL>::bits(acc[rb][cb][e]);
+                    }
+                } else {
+                    const int r = j0 - a.q.nope + (lane & 31);   // rope column of the head
+                    const int i = r >> 1;
+                    uint16_t* dst = static_cast<uint16_t*>(a.q.q_rope) + (int64_t)h * a.q.rope + r;
+                    #pragma unroll
+                    for (int e = 0; e < 16; ++e) {
+                        const float own = acc[rb][cb][e];
+                        const float other = dpp_move<0xB1>(own);   // lane ^ 1
+                        const int row = 64 * wm + 32 * rb + acc_row(e, lane);
+                        if (row < rows_a) {
+                            const v2f t = *reinterpret_cast<const v2f*>(
+                                smem + NS * kStage + 8 * (row * half + i));
+                            const float c = t[0], sn = t[1];
+                            const float v = (lane & 1) ? rope_odd(other, own, c, sn) : rope_even(own, other, c, sn);
+                            dst[(int64_t)(m0 + row) * ld_rope] = (uint16_t)Half<TL>::bits(v);
+                        }
+                    }
+                }
+            }
+        return;
+    }
 
     // ---- epilogue: fp32 C, or this split's partials
     float* out;
@@ -189,20 +257,21 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
 }
 
 // Stage counts per column tile: 128 columns x 4 stages (128 KB of LDS, one workgroup per
-// CU) or 3 (96 KB); 64 columns x 3 (72 KB, two per CU), 4 or 6 stages (96 / 144 KB).
-template <typename TL>
+// CU) or 3 (96 KB); 64 columns x 3 (72 KB, two per CU), 4 or 6 stages (96 / 144 KB).  The
+// fused 2a2 epilogue adds 32 KB for its RoPE table (160 KB at 128 x 4; not with 64 x 6).
+template <typename TL, bool QUP>
 hipError_t launch_wgemm_t(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 block,
                           hipStream_t stream) {
     if (plan.bn == 128 && plan.stages == 4)
-        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1, QUP>), grid, block, 0, stream, a);
     else if (plan.bn == 128 && plan.stages == 3)
-        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 3, 1>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 3, 1, QUP>), grid, block, 0, stream, a);
     else if (plan.bn == 64 && plan.stages == 3)
-        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 3, 2>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 3, 2, QUP>), grid, block, 0, stream, a);
     else if (plan.bn == 64 && plan.stages == 4)
-        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 4, 1>), grid, block, 0, stream, a);
-    else if (plan.bn == 64 && plan.stages == 6)
-        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 6, 1>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 4, 1, QUP>), grid, block, 0, stream, a);
+    else if (plan.bn == 64 && plan.stages == 6 && !QUP)   // no room for the QUP table
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 6, 1, false>), grid, block, 0, stream, a);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
@@ -219,6 +288,13 @@ bool wgemm_supported(const GemmProblem& p, int bn, int split) {
            p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sAg % 8 == 0 && p.sBg % 8 == 0 &&
            // 32-bit buffer offsets within a tile: 128 A rows, 64 W rows
            (int64_t)kWBM * p.lda * 2 < kRsrcRange && (int64_t)kWKS * p.ldb * 2 < kRsrcRange;
+}
+
+bool qup_supported(const GemmProblem& p, const QUpEpilogue& q) {
+    return p.half && p.G == 1 && q.H > 0 && q.nope > 0 && q.nope % 32 == 0 && q.rope > 0 &&
+           q.rope % 32 == 0 && q.rope <= 64 &&
+           (int64_t)p.N == (int64_t)q.H * (q.nope + q.rope) && q.q_nope && q.q_rope &&
+           q.cos_sin;
 }
 
 bool wgemm_aligned(const GemmProblem& p) {
@@ -243,8 +319,14 @@ hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* parti
     const int64_t blocks = (int64_t)a.tiles_m * a.tiles_n * a.split * a.G;
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 grid((unsigned)blocks), block(kWThreads);
-    if (p.f16) return launch_wgemm_t<f16_t>(a, plan, grid, block, stream);
-    return launch_wgemm_t<bf16_t>(a, plan, grid, block, stream);
+    if (p.qup) {
+        if (plan.split != 1 || !qup_supported(p, *p.qup)) return hipErrorInvalidValue;
+        a.q = *p.qup;
+        if (p.f16) return launch_wgemm_t<f16_t, true>(a, plan, grid, block, stream);
+        return launch_wgemm_t<bf16_t, true>(a, plan, grid, block, stream);
+    }
+    if (p.f16) return launch_wgemm_t<f16_t, false>(a, plan, grid, block, stream);
+    return launch_wgemm_t<bf16_t, false>(a, plan, grid, block, stream);
 }
 
 }  // namespace mla

@@ -80,6 +80,35 @@ def test_weight_streaming_gemm(ext, monkeypatch, dt, M, N, K, plan):
     torch.testing.assert_close(got, tiled, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("dt", [BF, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("B,Sq,per_seq", [(2, 3, False), (5, 1, True), (128, 1, False)])
+def test_q_absorbed_fused_epilogue(ext, monkeypatch, dt, B, Sq, per_seq):
+    """2a2 on the weight-streaming engine with its fused epilogue (q_nope for 2c and the
+    rotated q_rope written by 2a2 itself) gives the same bits as 2a2 + the 2b launch
+    (MLA_QUP_FUSE=0) on the same plan, and matches the fp32 oracle; positions shared by
+    the batch (up to 4988) or per sequence."""
+    inp = R.make_inputs(B, Sq, 4989, seed=B + Sq, dtype=dt)
+    W_uk, _ = R.split_wkv_b(inp["wkv_b"], D.nope)
+    pos = inp["positions"]
+    if per_seq:
+        pos = torch.tensor([[4988 - 97 * b] for b in range(B)]) if Sq == 1 else pos
+    args = [gpu(inp[k]) for k in ("x", "W_q_a", "q_norm_w", "W_q_b")] + [gpu(W_uk.contiguous()),
+                                                                        gpu(pos)]
+    M, N = B * Sq, D.n_heads * D.qk_head
+    monkeypatch.setenv("MLA_WGEMM_PLAN", f"{M},{N},{D.q_lora},1=128,1")
+    qa, qr = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    monkeypatch.setenv("MLA_QUP_FUSE", "0")
+    qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    assert qa.dtype == dt and qr.dtype == dt
+    assert torch.equal(qa, qa0) and torch.equal(qr, qr0)
+    f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
+    prep = R.prepare_q_ragged if per_seq else R.prepare_q_mla_absorbed
+    rqa, rqr = prep(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], W_uk.float(), pos,
+                    D.nope, D.rope)
+    torch.testing.assert_close(qa.float(), rqa, **C.tol(dt, rqa))
+    torch.testing.assert_close(qr.float(), rqr, **C.tol(dt, rqr))
+
+
 def test_rmsnorm_rope_bf16(ext):
     g = torch.Generator().manual_seed(3)
     x = torch.randn(16, 1536, generator=g)
