@@ -23,9 +23,21 @@ typedef uint32_t v4u_t __attribute__((ext_vector_type(4)));   // 16 raw bytes
 // so both normalise with the same arithmetic and summation order.
 constexpr int kNormCache = 4;  // float4 per thread kept in registers (256*4*4 = 4096 wide)
 
-// Sum of nsplit partial rows (slice order) at float4 column c4.
+// Sum of nsplit partial rows (slice order) at float4 column c4.  NS > 0: nsplit == NS,
+// known at compile time, and all NS loads are issued before the first add (one memory
+// latency instead of one per batch); the additions run in the same order either way.
+template <int NS = 0>
 __device__ __forceinline__ v4f sum_partials4(const float* base, int nsplit, int64_t split_stride,
                                              int c4) {
+    if constexpr (NS > 0) {
+        v4f p[NS];
+        #pragma unroll
+        for (int s = 0; s < NS; ++s) p[s] = *reinterpret_cast<const v4f*>(base + s * split_stride + 4 * c4);
+        v4f v = p[0];
+        #pragma unroll
+        for (int s = 1; s < NS; ++s) v += p[s];
+        return v;
+    }
     v4f v = *reinterpret_cast<const v4f*>(base + 4 * c4);
     int s = 1;
     for (; s + 4 <= nsplit; s += 4) {
@@ -42,7 +54,7 @@ __device__ __forceinline__ v4f sum_partials4(const float* base, int nsplit, int6
 
 // out_row[0:N] = row * rsqrt(mean(row^2) + eps) * gain, row = summed partials at `base`.
 // Called by all 256 threads of the workgroup (it synchronises through `red`).
-template <int OUT>
+template <int OUT, int NS = 0>
 __device__ __forceinline__ void rms_row(const float* base, int nsplit, int64_t split_stride,
                                         const void* gain_v, void* out_row, int N, float eps,
                                         float* red) {
@@ -53,12 +65,12 @@ __device__ __forceinline__ void rms_row(const float* base, int nsplit, int64_t s
     #pragma unroll
     for (int j = 0; j < kNormCache; ++j) {
         const int c4 = tid + 256 * j;
-        cache[j] = (c4 < n4) ? sum_partials4(base, nsplit, split_stride, c4) : v4f{0.f, 0.f, 0.f, 0.f};
+        cache[j] = (c4 < n4) ? sum_partials4<NS>(base, nsplit, split_stride, c4) : v4f{0.f, 0.f, 0.f, 0.f};
         ss += cache[j][0] * cache[j][0] + cache[j][1] * cache[j][1] +
               cache[j][2] * cache[j][2] + cache[j][3] * cache[j][3];
     }
     for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256) {
-        const v4f v = sum_partials4(base, nsplit, split_stride, c4);
+        const v4f v = sum_partials4<NS>(base, nsplit, split_stride, c4);
         ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
     }
     ss = wave_reduce(ss, OpSum());
@@ -88,10 +100,10 @@ __device__ __forceinline__ void rms_row(const float* base, int nsplit, int64_t s
         if (c4 < n4) emit(c4, cache[j]);
     }
     for (int c4 = tid + 256 * kNormCache; c4 < n4; c4 += 256)
-        emit(c4, sum_partials4(base, nsplit, split_stride, c4));
+        emit(c4, sum_partials4<NS>(base, nsplit, split_stride, c4));
 }
 
-template <int OUT>
+template <int OUT, int NS>
 __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ in, int nsplit,
                                                       int64_t split_stride, const void* gain_v,
                                                       void* out_v, int N, float eps,
@@ -111,7 +123,7 @@ __global__ void __launch_bounds__(256) rmsnorm_kernel(const float* __restrict__ 
     void* out_row = OUT == kOutF32
                         ? static_cast<void*>(static_cast<float*>(out_v) + (int64_t)row * N)
                         : static_cast<void*>(static_cast<uint16_t*>(out_v) + (int64_t)row * N);
-    rms_row<OUT>(in + (int64_t)row * N, nsplit, split_stride, gain_v, out_row, N, eps, red);
+    rms_row<OUT, NS>(in + (int64_t)row * N, nsplit, split_stride, gain_v, out_row, N, eps, red);
 }
 
 // ---- 2b: one workgroup per (query row bq, chunk of 32 heads; 4 when it also sums 2a2's
@@ -494,22 +506,34 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
 
 }  // namespace
 
+namespace {
+// the split counts 2a1's plans use get the all-loads-first sum
+template <int OUT>
+hipError_t launch_rmsnorm_t(const float* in, int nsplit, int64_t split_stride, const void* gain,
+                            void* out, int M, int N, float eps, hipStream_t stream,
+                            const RopeTable& rt) {
+    if (nsplit == 8)
+        hipLaunchKernelGGL((rmsnorm_kernel<OUT, 8>), dim3(M), dim3(256), 0, stream, in, nsplit,
+                           split_stride, gain, out, N, eps, rt);
+    else if (nsplit == 16)
+        hipLaunchKernelGGL((rmsnorm_kernel<OUT, 16>), dim3(M), dim3(256), 0, stream, in, nsplit,
+                           split_stride, gain, out, N, eps, rt);
+    else
+        hipLaunchKernelGGL((rmsnorm_kernel<OUT, 0>), dim3(M), dim3(256), 0, stream, in, nsplit,
+                           split_stride, gain, out, N, eps, rt);
+    return hipGetLastError();
+}
+}  // namespace
+
 hipError_t launch_rmsnorm(const float* in, int nsplit, int64_t split_stride, const void* gain,
                           void* out, OutType out_type, int M, int N, float eps,
                           hipStream_t stream, const RopeTable& rt) {
     if (M <= 0) return hipSuccess;
     if (rt.cos_sin && (rt.half <= 0 || rt.half > 256 || !rt.positions || !rt.inv_freq || rt.Sq < 1))
         return hipErrorInvalidValue;
-    if (out_type == kOutF32)
-        hipLaunchKernelGGL(rmsnorm_kernel<kOutF32>, dim3(M), dim3(256), 0, stream, in, nsplit,
-                           split_stride, gain, out, N, eps, rt);
-    else if (out_type == kOutBF16)
-        hipLaunchKernelGGL(rmsnorm_kernel<kOutBF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
-                           split_stride, gain, out, N, eps, rt);
-    else
-        hipLaunchKernelGGL(rmsnorm_kernel<kOutF16>, dim3(M), dim3(256), 0, stream, in, nsplit,
-                           split_stride, gain, out, N, eps, rt);
-    return hipGetLastError();
+    if (out_type == kOutF32) return launch_rmsnorm_t<kOutF32>(in, nsplit, split_stride, gain, out, M, N, eps, stream, rt);
+    if (out_type == kOutBF16) return launch_rmsnorm_t<kOutBF16>(in, nsplit, split_stride, gain, out, M, N, eps, stream, rt);
+    return launch_rmsnorm_t<kOutF16>(in, nsplit, split_stride, gain, out, M, N, eps, stream, rt);
 }
 
 hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float* inv_freq,
