@@ -140,6 +140,23 @@ def test_o_proj_matches_oracle(ext, B, Sq):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_o_proj_16bit_b128(ext, monkeypatch, dtype):
+    """B=128 decode: the weight-streaming plan (4 K splits, summed by the reduction that
+    also rounds to the storage format), every row against the oracle and against the
+    tiled engine (MLA_WGEMM=0)."""
+    g = torch.Generator().manual_seed(5)
+    attn = torch.randn(128, 1, D.n_heads, D.v, generator=g).to(dtype)
+    W_o = (torch.randn(D.n_heads * D.v, D.hidden, generator=g) /
+           math.sqrt(D.n_heads * D.v)).to(dtype)
+    out = ext.o_proj(gpu(attn), gpu(W_o)).cpu().float()
+    ref = R.o_proj(attn.float(), W_o.float())
+    torch.testing.assert_close(out, ref, **TOL_BF16)
+    monkeypatch.setenv("MLA_WGEMM", "0")
+    tiled = ext.o_proj(gpu(attn), gpu(W_o)).cpu().float()
+    torch.testing.assert_close(out, tiled, **TOL_BF16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
 def test_o_proj_16bit(ext, dtype):
     g = torch.Generator().manual_seed(3)
     attn = torch.randn(4, 2, D.n_heads, D.v, generator=g).to(dtype)
