@@ -1,19 +1,21 @@
 // Weight-streaming GEMM for the 16-bit (bf16 / fp16) products whose A operand is a small
 // batch of activation rows (M <= 128 per tile) and whose B operand is a weight matrix
-// streamed once from HBM: 2a1 (x @ W_q_a) and 2a2 (q_lat @ W_q_b) of the Q path, NN, fp32
-// output or split-K partials.  It replaces gemm_kernel for those shapes
+// streamed once from HBM: 2a1 (x @ W_q_a) and 2a2 (q_lat @ W_q_b) of the Q path and the
+// output projection beside the layer; NN, one group, fp32 output or split-K partials, and
+// for 2a2 the fused epilogue that also does 2b.  It replaces gemm_kernel for those shapes
 // (gemm.hip: plan_gemm picks it), whose staging round-trips every operand byte through
 // registers and transposes the N-contiguous weights on the way into LDS.
 //
 // Workgroup = 4 wave64s over a 128-row x BN-column tile (BN = 128 or 64), 2 x 2 waves of
-// 64 x BN/2, on the 32x32x16 16-bit MFMA.  K is walked in 64-deep slices through a 4-stage
-// LDS ring, and both operands go global -> LDS with direct-to-LDS loads (no registers):
+// 64 x BN/2, on the 32x32x16 16-bit MFMA.  K is walked in 64-deep slices through an LDS
+// ring of NS stages (3, 4 or 6), and both operands go global -> LDS with direct-to-LDS
+// loads (no registers):
 //   A: 128 rows x 128 bytes per slice, read back as K-contiguous fragments (ds_read_b128);
 //   W: 64 rows x 2*BN bytes per slice, N-contiguous as in memory, read back as the MFMA's
 //      K-contiguous B fragments with the transposing ds_read_b64_tr_b16 (two per fragment:
 //      within each 16-lane group lanes 4q .. 4q+3 address row q and lane j receives
 //      column j of the four rows).
-// Three slices are in flight while one feeds the MFMAs, and one barrier per slice orders
+// NS - 1 slices are in flight while one feeds the MFMAs, and one barrier per slice orders
 // the ring.  Chunk permutations keep every LDS read free of bank conflicts: 16-byte chunk c
 // of A row r sits at c ^ ((r >> 1) & 7), and chunk c of W row r at c ^ (4 (r & 3)) for
 // BN = 128 (16 chunks a row), c ^ (4 ((r >> 1) & 1)) for BN = 64 (8 chunks); the loads
@@ -283,7 +285,7 @@ bool wgemm_supported(const GemmProblem& p, int bn, int split) {
     return p.half && !p.a_f32 && !p.b_nt && p.amode == kAPlain &&
            (p.out_type == kOutF32 || split > 1) && split >= 1 &&
            !p.k_len && !p.b_pages && (bn == 64 || bn == 128) && p.N % bn == 0 &&
-           p.K % kWKS == 0 && p.lda >= kWKS && p.ldb >= bn && p.M > 0 && p.G >= 1 &&
+           p.K % kWKS == 0 && p.lda >= kWKS && p.ldb >= bn && p.M > 0 && p.G == 1 &&
            // 16-byte aligned rows and groups for the 16-byte loads
            p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sAg % 8 == 0 && p.sBg % 8 == 0 &&
            // 32-bit buffer offsets within a tile: 128 A rows, 64 W rows
