@@ -248,6 +248,22 @@ def test_gemm_split_needs_workspace(lib):
     assert st == MLA_ERR_WORKSPACE and "too small" in _err(lib)
 
 
+def test_weight_streaming_plans_size_the_workspace(lib, monkeypatch):
+    """The 16-bit B=128 projections take the weight-streaming plans: 2a1 in 8 K splits
+    (fp32 partials [8][128][1536]), 2a2 unsplit (no workspace).  MLA_WGEMM=0 returns the
+    tiled engine's plans, whose workspace the query reports as well; MLA_WGEMM_PLAN
+    forces a plan, and a plan the engine cannot run (N % bn != 0) falls back to the
+    tiled one."""
+    assert lib.mla_gemm_workspace_bytes(BF16, 128, 1536, 7168) == 8 * 128 * 1536 * 4
+    assert lib.mla_gemm_workspace_bytes(BF16, 128, 24576, 1536) == 0
+    monkeypatch.setenv("MLA_WGEMM_PLAN", "128,24576,1536,1=128,3")
+    assert lib.mla_gemm_workspace_bytes(BF16, 128, 24576, 1536) == 3 * 128 * 24576 * 4
+    monkeypatch.setenv("MLA_WGEMM_PLAN", "40,200,128,1=128,1")
+    tiled = lib.mla_gemm_workspace_bytes(BF16, 40, 200, 128)
+    monkeypatch.setenv("MLA_WGEMM", "0")
+    assert lib.mla_gemm_workspace_bytes(BF16, 40, 200, 128) == tiled
+
+
 def test_attention_validation(lib):
     d = dsv3(2, 3, 2)
     args = [P16] * 5

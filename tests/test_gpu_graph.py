@@ -43,8 +43,10 @@ def _layer(ext, g, W_uk, W_uv):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16],
                          ids=["f32", "bf16", "f16"])
-@pytest.mark.parametrize("B,Sk", [(2, 300), (3, 1000)])
+@pytest.mark.parametrize("B,Sk", [(2, 300), (3, 1000), (128, 300)])
 def test_layer_graph_replay(ext, dtype, B, Sk):
+    """Replays equal the eager layer bit for bit.  At B = 128 the 16-bit Q path runs the
+    weight-streaming GEMMs with 2a2's fused epilogue and 2a-n's RoPE table."""
     inp = R.make_inputs(B, 1, Sk, seed=B + Sk)
     W_uk, W_uv = R.split_wkv_b(inp["wkv_b"], D.nope)
     g = {k: v.to(dtype).to(DEV) if v.is_floating_point() else v.to(DEV)
