@@ -279,6 +279,15 @@ GemmProblem out_problem(mla_dtype_t dt, const mla_dims_t* d, const float* ctx,
     return p;
 }
 
+// 3d from the fused pass's normalised 16-bit ctx (flash_ctx16_ok): A is that ctx
+// [B*Sq, H*kv_rank] in the storage format, no row scale.
+GemmProblem out_problem16(mla_dtype_t dt, const mla_dims_t* d, const void* ctx16,
+                          const void* W_uv, void* out) {
+    GemmProblem p = out_problem(dt, d, nullptr, nullptr, W_uv, out);
+    p.A = ctx16; p.a_f32 = false; p.amode = kAPlain; p.rs = nullptr;
+    return p;
+}
+
 // ------------------------------------------------------------------ workspace layouts
 
 struct QLayout {
@@ -352,6 +361,7 @@ bool use_flash(mla_dtype_t dt, const mla_dims_t* d) {
 
 struct AttnLayout {
     bool fused = false;   // the path this layout is for
+    bool ctx16 = false;   // fused: the pass writes the normalised 16-bit ctx for 3d
     int ld_p, P;
     GemmPlan ctx, out;
     FlashPlan flash;
@@ -377,6 +387,8 @@ AttnLayout attn_layout(mla_dtype_t dt, const mla_dims_t* d, bool ragged = false)
         FlashProblem fp = flash_problem(dt, d, nullptr, nullptr, nullptr, nullptr, 1.0, 0);
         fp.ragged = ragged;
         L.flash = plan_flash(fp);
+        L.ctx16 = flash_ctx16_ok(fp, L.flash);
+        if (L.ctx16) L.out = plan_gemm(out_problem16(dt, d, nullptr, nullptr, nullptr));
         L.off_p = L.off_m = L.off_l = L.off_alpha = L.off_ctx_ws = 0;
         L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
         L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
@@ -962,6 +974,7 @@ int attention_f64(const mla_dims_t* d, const void* q_absorbed, const void* q_rop
 struct Fp8Layout {
     FlashPlan flash;
     GemmPlan out;
+    bool ctx16 = false;   // the pass writes the normalised bf16 ctx for 3d
     size_t off_rowsum, off_ctx, off_out_ws, off_part, total;
 };
 
@@ -980,7 +993,9 @@ Fp8Layout fp8_layout(const mla_dims_t* d, bool ragged = false) {
     FlashProblem fp = fp8_problem(d, nullptr, nullptr, nullptr, nullptr, 1.f, 1.0, 0);
     fp.ragged = ragged;
     L.flash = plan_flash(fp);
-    L.out = plan_gemm(out_problem(MLA_DTYPE_BF16, d, nullptr, nullptr, nullptr, nullptr));
+    L.ctx16 = flash_ctx16_ok(fp, L.flash);
+    L.out = L.ctx16 ? plan_gemm(out_problem16(MLA_DTYPE_BF16, d, nullptr, nullptr, nullptr))
+                    : plan_gemm(out_problem(MLA_DTYPE_BF16, d, nullptr, nullptr, nullptr, nullptr));
     size_t o = 0;
     L.off_rowsum = o; o = align_up(o + rows * sizeof(float));
     L.off_ctx = o;    o = align_up(o + rows * d->kv_rank * sizeof(float));
@@ -1306,6 +1321,14 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
                         "3d launch");
             return ok();
         }
+        if (L.ctx16) {   // the pass writes ctx / row_sum already divided, in 16 bits
+            MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream, true, ctx),
+                        "fused attention launch");
+            GemmProblem op = out_problem16(dtype, dims, ctx, W_uv, out);
+            MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
+                        "3d launch");
+            return ok();
+        }
         MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream), "fused attention launch");
         GemmProblem op = out_problem(dtype, dims, ctx, row_sum, W_uv, out);
         MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream),
@@ -1352,9 +1375,11 @@ int mla_attention_fp8kv(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
     float* ctx = at<float>(workspace, L.off_ctx);
     const FlashProblem fp = fp8_problem(dims, q_absorbed, q_rope, c_kv_fp8, pe_fp8, kv_scale,
                                         scale, causal);
-    MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part), stream),
+    MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, at<float>(workspace, L.off_part), stream,
+                             true, L.ctx16 ? ctx : nullptr),
                 "fp8-cache attention launch");
-    GemmProblem op = out_problem(MLA_DTYPE_BF16, dims, ctx, row_sum, W_uv, out);
+    GemmProblem op = L.ctx16 ? out_problem16(MLA_DTYPE_BF16, dims, ctx, W_uv, out)
+                             : out_problem(MLA_DTYPE_BF16, dims, ctx, row_sum, W_uv, out);
     MLA_TRY_HIP(launch_gemm(op, L.out, at<void>(workspace, L.off_out_ws), stream), "3d launch");
     return ok();
 }

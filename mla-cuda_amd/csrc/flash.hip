@@ -45,6 +45,8 @@ namespace mla {
 
 namespace {
 
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
 constexpr int kFR = 512, kFD = 64;                  // latent and rope widths
 constexpr int kFKeys = 32;                          // keys per block
 constexpr int kFRows = 64;                          // rows per workgroup
@@ -77,6 +79,10 @@ struct FlashArgs {
     const int* wl;
     float* o_direct;
     float* l_direct;
+    // dense unsplit 16-bit pass only (flash_ctx16_ok): instead of o / l, write each row
+    // already normalised and rounded to the storage format, (o_scale O) (1 / l) -- what
+    // 3d's A staging forms from ctx and row_sum -- at ctx16[row][R]
+    void* ctx16;
 };
 
 // What one workgroup of the attention pass computes: batch b, row tile rt, keys
@@ -1094,6 +1100,21 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
             const float lsum = xlr[l32] + xlr[32 + l32];
             const float M = xref[t * 64 + l32];
             const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
+            if (a.ctx16) {
+                const float r = lsum == 0.f ? 0.f : 1.f / lsum;
+                uint16_t* crow = static_cast<uint16_t*>(a.ctx16) + slot * kFR + 128 * cq + 4 * hw;
+                #pragma unroll
+                for (int cb = 0; cb < 4; ++cb)
+                    #pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const v4f v = v4f{O[2 * cb + t][4 * q], O[2 * cb + t][4 * q + 1],
+                                          O[2 * cb + t][4 * q + 2], O[2 * cb + t][4 * q + 3]} * of;
+                        const v4f w = v * r;
+                        *reinterpret_cast<v2u*>(crow + 32 * cb + 8 * q) =
+                            v2u{Half<TL>::pack2(w[0], w[1]), Half<TL>::pack2(w[2], w[3])};
+                    }
+                continue;
+            }
             if (cq == 0 && hw == 0) {
                 if (!work.direct) a.m[slot] = M;
                 (work.direct ? a.l_direct : a.l)[slot] = lsum;
@@ -1155,7 +1176,6 @@ constexpr int k8Stage = k8LatStage + 32 * k8PeBytes;   // 18 KB per block
 constexpr int k8NS = 8;                                // ring stages
 constexpr int k8Ahead = k8NS - 2;                      // blocks in flight past the next one
 
-typedef uint32_t v2u __attribute__((ext_vector_type(2)));
 typedef int32_t v2i __attribute__((ext_vector_type(2)));
 
 // eight e4m3 codes (bytes 0..7) -> eight bf16 in operand order
@@ -1487,6 +1507,21 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x8_kernel(FlashArgs a) {
         const float lsum = xlr[l32] + xlr[32 + l32];
         const float M = xref[t * 64 + l32];
         const int64_t slot = (work.direct ? (int64_t)b : work.slot) * rows_b + row;
+        if (a.ctx16) {
+            const float r = lsum == 0.f ? 0.f : 1.f / lsum;
+            uint16_t* crow = static_cast<uint16_t*>(a.ctx16) + slot * kFR + 128 * cq + 4 * hw;
+            #pragma unroll
+            for (int cb = 0; cb < 4; ++cb)
+                #pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const v4f v = v4f{O[2 * cb + t][4 * q], O[2 * cb + t][4 * q + 1],
+                                      O[2 * cb + t][4 * q + 2], O[2 * cb + t][4 * q + 3]} * a.o_scale;
+                    const v4f w = v * r;
+                    *reinterpret_cast<v2u*>(crow + 32 * cb + 8 * q) =
+                        v2u{Half<bf16_t>::pack2(w[0], w[1]), Half<bf16_t>::pack2(w[2], w[3])};
+                }
+            continue;
+        }
         if (cq == 0 && hw == 0) {
             if (!work.direct) a.m[slot] = M;
             (work.direct ? a.l_direct : a.l)[slot] = lsum;
@@ -2666,8 +2701,33 @@ FlashPartials flash_partials(const FlashProblem& p, const FlashPlan& f, const fl
     return r;
 }
 
+namespace {
+// The 16-bit and fp8-cache kernel the launcher takes for p (the switches below).
+enum class Flash16 { kCodeRing, kSpecPv64, kSpecPv32, kKeySplit };
+Flash16 flash16_choice(const FlashProblem& p) {
+    const char* spec_env = std::getenv("MLA_FLASH16_SPEC");
+    const bool spec = !(spec_env && spec_env[0] == '0');
+    const char* pv_env = std::getenv("MLA_FLASH16_PV");
+    const bool pv64 = !(pv_env && std::strcmp(pv_env, "32") == 0);
+    const char* f8_env = std::getenv("MLA_FLASH16_FP8");
+    const bool f8_convert = f8_env && std::strcmp(f8_env, "convert") == 0;
+    if (!spec) return Flash16::kKeySplit;
+    if (p.fp8_kv && !f8_convert) return Flash16::kCodeRing;
+    return pv64 ? Flash16::kSpecPv64 : Flash16::kSpecPv32;
+}
+}  // namespace
+
+bool flash_ctx16_ok(const FlashProblem& p, const FlashPlan& f) {
+    const char* env = std::getenv("MLA_CTX16");
+    if (env && env[0] == '0') return false;
+    const Flash16 k = flash16_choice(p);
+    return (p.half || p.fp8_kv) && !f.balanced && !f.wave && f.n_split == 1 &&
+           (k == Flash16::kCodeRing || k == Flash16::kSpecPv64);
+}
+
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, float* row_sum,
-                        float* partials, hipStream_t stream, bool merge) {
+                        float* partials, hipStream_t stream, bool merge, void* ctx16) {
+    if (ctx16 && !flash_ctx16_ok(p, f)) return hipErrorInvalidValue;
     const int rows = p.B * p.Sq * p.H;
     const int rows_b = p.Sq * p.H;
     FlashArgs a;
@@ -2678,6 +2738,7 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     a.wl = nullptr;
     a.o_direct = ctx;
     a.l_direct = row_sum;
+    a.ctx16 = ctx16;
     int grid;
     int* wl = nullptr;
     if (f.balanced) {
@@ -2732,8 +2793,8 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
         if (e != hipSuccess) return e;
     }
     // 16-bit: the specialised-wave pass unless MLA_FLASH16_SPEC=0 asks for the key-split one
-    const char* spec_env = std::getenv("MLA_FLASH16_SPEC");
-    const bool spec = !(spec_env && spec_env[0] == '0');
+    const Flash16 k16 = flash16_choice(p);
+    const bool spec = k16 != Flash16::kKeySplit;
     // fp32, 64-row workgroups: the specialised-wave pass unless MLA_FLASH32_SPEC=0 asks for
     // flash32_kernel
     const char* spec32_env = std::getenv("MLA_FLASH32_SPEC");
@@ -2741,14 +2802,11 @@ hipError_t launch_flash(const FlashProblem& p, const FlashPlan& f, float* ctx, f
     // 16-bit specialised waves: the P.V waves over 64 rows x 128 columns (measured at cfg4,
     // bf16: 177-179 us against 178-186 us, and the same results bit for bit), or over 32 rows
     // x 256 columns with MLA_FLASH16_PV=32
-    const char* pv_env = std::getenv("MLA_FLASH16_PV");
-    const bool pv64 = !(pv_env && std::strcmp(pv_env, "32") == 0);
+    const bool pv64 = k16 != Flash16::kSpecPv32;
     // an fp8 cache: the code-ring pass (flash16x8_kernel; cfg4 shape, attention with 3d:
     // 171 us against 220-240 us) unless MLA_FLASH16_FP8=convert asks for the pass that
     // converts each block into a bf16 ring
-    const char* f8_env = std::getenv("MLA_FLASH16_FP8");
-    const bool f8_convert = f8_env && std::strcmp(f8_env, "convert") == 0;
-    if (p.fp8_kv && spec && !f8_convert)
+    if (p.fp8_kv && k16 == Flash16::kCodeRing)
         hipLaunchKernelGGL(flash16x8_kernel, dim3(grid), dim3(kXThreads), 0, stream, a);
     else if (p.fp8_kv && spec && pv64)
         hipLaunchKernelGGL((flash16x_kernel<bf16_t, true, true>), dim3(grid), dim3(kXThreads), 0, stream, a);

@@ -541,6 +541,10 @@ hipError_t dispatch16(const GemmProblem& p, const GemmArgs& a, int bm, int bn, i
     }
     if (!p.b_nt && p.amode == kAAlpha && p.a_f32 && f32_out)
         return launch_tiles<TL, float, false, kAAlpha, kOutF32>(a, bm, bn, nblocks, stream);
+    if (p.b_nt && p.amode == kAPlain && !p.a_f32) {   // 3d from a normalised 16-bit ctx
+        if (f32_out) return launch_tiles<TL, TL, true, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
+        return launch_tiles<TL, TL, true, kAPlain, O16>(a, bm, bn, nblocks, stream);
+    }
     if (p.b_nt && p.amode == kARowRecip && p.a_f32) {
         if (f32_out)
             return launch_tiles<TL, float, true, kARowRecip, kOutF32>(a, bm, bn, nblocks, stream);

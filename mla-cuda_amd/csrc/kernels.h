@@ -209,7 +209,13 @@ FlashPlan plan_flash(const FlashProblem& p);
 // merge = false leaves a split pass's partials unmerged (flash_partials() locates them)
 // for a consumer that folds the merge in (launch_out_small).
 hipError_t launch_flash(const FlashProblem& p, const FlashPlan& plan, float* ctx, float* row_sum,
-                        float* partials, hipStream_t stream, bool merge = true);
+                        float* partials, hipStream_t stream, bool merge = true,
+                        void* ctx16 = nullptr);
+// ctx16 (launch_flash): a dense unsplit 16-bit or fp8-cache pass on the default kernels can
+// write ctx already normalised by its row sum and rounded to the storage format
+// ([rows][R], the values 3d's A staging would form), instead of ctx and row_sum.
+// MLA_CTX16=0 turns this off.
+bool flash_ctx16_ok(const FlashProblem& p, const FlashPlan& plan);
 // Where a dense (not balanced) pass leaves its state: n_split > 1 -> partial rows o
 // [n_split][rows][R], log2-domain references m and row sums l [n_split][rows] (slot
 // s * B * rows_b + row); n_split == 1 -> ctx / row_sum themselves.

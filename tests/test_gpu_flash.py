@@ -157,6 +157,35 @@ def test_16bit_kernels_full_size(ext, monkeypatch, spec):
     close(run(ext, args, False), ref, BF)
 
 
+@pytest.mark.parametrize("kind", ["bf16", "f16", "fp8-code-ring", "fp8-convert"])
+def test_normalised_16bit_ctx_same_bits(ext, monkeypatch, kind):
+    """With one key split (B = 128) the default 16-bit passes write ctx already divided by
+    its row sum and rounded to the storage format -- the values 3d's staging forms from the
+    fp32 ctx and row sum -- so the output equals the MLA_CTX16=0 path bit for bit; and it
+    matches the oracle."""
+    def call():
+        if kind.startswith("fp8"):
+            return ext.mla_attention_fp8kv(*(gpu(t) for t in f8[:4]), f8[4], gpu(f8[5]),
+                                           SCALE).cpu()
+        return ext.mla_attention(*(gpu(t) for t in args), SCALE).cpu()
+
+    if kind.startswith("fp8"):
+        if kind == "fp8-convert":
+            monkeypatch.setenv("MLA_FLASH16_FP8", "convert")
+        f8 = C.fp8_inputs(128, 1, 1000, seed=9)
+        ref = R.mla_attention_fp8kv(*f8, SCALE)
+        dt = BF
+    else:
+        dt = BF if kind == "bf16" else H16
+        args = inputs(128, 1, 1000, seed=9, dt=dt)
+        ref = oracle(args, False)
+    out16 = call()
+    monkeypatch.setenv("MLA_CTX16", "0")
+    out32 = call()
+    assert torch.equal(out16, out32)
+    close(out16.float(), ref.float(), dt)
+
+
 @FP16_KERNELS
 @HALF_DTYPES
 def test_16bit_kernels_repeat_passes(ext, monkeypatch, spec, dt):
