@@ -301,7 +301,8 @@ struct QLayout {
 bool qup_fused(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up) {
     const char* env = getenv("MLA_QUP_FUSE");
     if (env && strcmp(env, "0") == 0) return false;
-    return is_half(dt) && up.wgemm && up.split == 1 && d->nope % 32 == 0 && d->rope % 32 == 0 &&
+    return is_half(dt) && up.wgemm && up.split == 1 && up.bn <= 128 && d->nope % 32 == 0 &&
+           d->rope % 32 == 0 &&
            d->rope > 0 && d->rope <= 64;
 }
 

@@ -715,7 +715,8 @@ bool wgemm_plan(const GemmProblem& p, GemmPlan* out) {
         if (!bn && t.M == p.M && t.N == p.N && t.K == p.K && t.G == p.G) {
             bn = t.bn; split = t.split; stages = t.stages;
         }
-    const bool ring_ok = (bn == 128 && (stages == 3 || stages == 4)) ||
+    const bool ring_ok = (bn == 256 && stages == 3) ||
+                         (bn == 128 && (stages == 3 || stages == 4)) ||
                          (bn == 64 && (stages == 3 || stages == 4 || stages == 6));
     if (!bn || split < 1 || !ring_ok || !wgemm_supported(p, bn, split)) return false;
     const int kslices = cdiv(p.K, 64);

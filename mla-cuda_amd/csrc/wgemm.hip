@@ -6,7 +6,7 @@
 // (gemm.hip: plan_gemm picks it), whose staging round-trips every operand byte through
 // registers and transposes the N-contiguous weights on the way into LDS.
 //
-// Workgroup = 4 wave64s over a 128-row x BN-column tile (BN = 128 or 64), 2 x 2 waves of
+// Workgroup = 4 wave64s over a 128-row x BN-column tile (BN = 256, 128 or 64), 2 x 2 waves of
 // 64 x BN/2, on the 32x32x16 16-bit MFMA.  K is walked in 64-deep slices through an LDS
 // ring of NS stages (3, 4 or 6), and both operands go global -> LDS with direct-to-LDS
 // loads (no registers):
@@ -18,7 +18,8 @@
 // NS - 1 slices are in flight while one feeds the MFMAs, and one barrier per slice orders
 // the ring.  Chunk permutations keep every LDS read free of bank conflicts: 16-byte chunk c
 // of A row r sits at c ^ ((r >> 1) & 7), and chunk c of W row r at c ^ (4 (r & 3)) for
-// BN = 128 (16 chunks a row), c ^ (4 ((r >> 1) & 1)) for BN = 64 (8 chunks); the loads
+// BN = 128 and 256 (16 or 32 chunks a row; the XOR stays inside each 256-byte window),
+// c ^ (4 ((r >> 1) & 1)) for BN = 64 (8 chunks); the loads
 // write chunk positions in order and take the permutation in their global offsets.
 // Rows past M and slices past the workgroup's K range load zeros (out-of-range buffer
 // offsets), so every slice issues the same loads and one wait count serves them all.
@@ -52,9 +53,9 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     constexpr int kBRow = 2 * BN;                        // bytes per W row of a slice
     constexpr int kBStage = kWKS * kBRow;                // 16 KB / 8 KB
     constexpr int kStage = kWAStage + kBStage;
-    constexpr int kLoadsB = kBStage / 1024 / 4;          // 4 / 2 per wave and slice
+    constexpr int kLoadsB = kBStage / 1024 / 4;          // 8 / 4 / 2 per wave and slice
     constexpr int kLoads = kWLoadsA + kLoadsB;
-    constexpr int kRowsPerLoadB = 1024 / kBRow;          // 4 / 8 W rows per 1 KB load
+    constexpr int kRowsPerLoadB = 1024 / kBRow;          // 2 / 4 / 8 W rows per 1 KB load
     constexpr int CB = BN / 64;                          // 32-column blocks per wave
     // QUP: the tile rows' RoPE table (rows x 32 pairs x (cos, sin)) after the ring
     constexpr int kTab = QUP ? kWBM * 32 * 8 : 0;
@@ -87,7 +88,7 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     for (int q = 0; q < kLoadsB; ++q) {
         const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
         const int pos = lane % (kBRow / 16);
-        const int sw = BN == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
+        const int sw = BN >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
         b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 16u * (pos ^ sw);
     }
     // valid bytes of a slice: A rows below rows_a, all 64 W rows (whole slices)
@@ -126,7 +127,7 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
         const int chunk = ((BN / 2) * wn + 32 * cb + 16 * (G & 1) + 4 * i4) / 8;
-        const int sw = BN == 128 ? 4 * q4 : 4 * (q4 >> 1);
+        const int sw = BN >= 128 ? 4 * q4 : 4 * (q4 >> 1);
         b_rd[cb] = kWAStage + (uint32_t)(8 * (G >> 1) + q4) * kBRow + 16u * (chunk ^ sw) + 8u * (i4 & 1);
     }
     typedef short v4s __attribute__((ext_vector_type(4)));
@@ -258,13 +259,16 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
             }
 }
 
-// Stage counts per column tile: 128 columns x 4 stages (128 KB of LDS, one workgroup per
-// CU) or 3 (96 KB); 64 columns x 3 (72 KB, two per CU), 4 or 6 stages (96 / 144 KB).  The
-// fused 2a2 epilogue adds 32 KB for its RoPE table (160 KB at 128 x 4; not with 64 x 6).
+// Stage counts per column tile: 256 columns x 3 stages (144 KB of LDS); 128 columns x 4
+// stages (128 KB, one workgroup per CU) or 3 (96 KB); 64 columns x 3 (72 KB, two per CU), 4
+// or 6 stages (96 / 144 KB).  The fused 2a2 epilogue adds 32 KB for its RoPE table (160 KB
+// at 128 x 4; not with 64 x 6 or 256 x 3).
 template <typename TL, bool QUP>
 hipError_t launch_wgemm_t(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 block,
                           hipStream_t stream) {
-    if (plan.bn == 128 && plan.stages == 4)
+    if (plan.bn == 256 && plan.stages == 3 && !QUP)   // 144 KB: no room for the QUP table
+        hipLaunchKernelGGL((wgemm_kernel<TL, 256, 3, 1, false>), grid, block, 0, stream, a);
+    else if (plan.bn == 128 && plan.stages == 4)
         hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1, QUP>), grid, block, 0, stream, a);
     else if (plan.bn == 128 && plan.stages == 3)
         hipLaunchKernelGGL((wgemm_kernel<TL, 128, 3, 1, QUP>), grid, block, 0, stream, a);
@@ -284,7 +288,7 @@ hipError_t launch_wgemm_t(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 
 bool wgemm_supported(const GemmProblem& p, int bn, int split) {
     return p.half && !p.a_f32 && !p.b_nt && p.amode == kAPlain &&
            (p.out_type == kOutF32 || split > 1) && split >= 1 &&
-           !p.k_len && !p.b_pages && (bn == 64 || bn == 128) && p.N % bn == 0 &&
+           !p.k_len && !p.b_pages && (bn == 64 || bn == 128 || bn == 256) && p.N % bn == 0 &&
            p.K % kWKS == 0 && p.lda >= kWKS && p.ldb >= bn && p.M > 0 && p.G == 1 &&
            // 16-byte aligned rows and groups for the 16-byte loads
            p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sAg % 8 == 0 && p.sBg % 8 == 0 &&

@@ -64,6 +64,8 @@ def test_gemm_bf16(ext, M, N, K):
     (7, 128, 320, "128,3"),         # slices 2, 2, 1 over the splits
     (1, 576, 7168, "64,16"),        # the KV projection's shape at B = 1
     (128, 64, 4096, "64,64"),       # one slice per split
+    (128, 512, 128, "256,1,3"),     # 256-column tiles (2c's plan), two slices
+    (40, 768, 192, "256,2,3"),      # 256-column tiles, rows off the tile, split
 ])
 def test_weight_streaming_gemm(ext, monkeypatch, dt, M, N, K, plan):
     """The weight-streaming engine (forced by MLA_WGEMM_PLAN) against the float64 product
