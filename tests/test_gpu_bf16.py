@@ -83,7 +83,8 @@ def test_weight_streaming_gemm(ext, monkeypatch, dt, M, N, K, plan):
 
 
 @pytest.mark.parametrize("dt", [BF, torch.float16], ids=["bf16", "f16"])
-@pytest.mark.parametrize("B,Sq,per_seq", [(2, 3, False), (5, 1, True), (128, 1, False)])
+@pytest.mark.parametrize("B,Sq,per_seq", [(2, 3, False), (5, 1, True), (128, 1, False),
+                                           (65, 2, False)])
 def test_q_absorbed_fused_epilogue(ext, monkeypatch, dt, B, Sq, per_seq):
     """2a2 on the weight-streaming engine with its fused epilogue (q_nope for 2c and the
     rotated q_rope written by 2a2 itself) gives the same bits as 2a2 + the 2b launch
