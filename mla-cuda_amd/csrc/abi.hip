@@ -293,6 +293,7 @@ GemmProblem out_problem16(mla_dtype_t dt, const mla_dims_t* d, const void* ctx16
 struct QLayout {
     GemmPlan down, up, absorb;
     bool fused;   // 2a2 writes q_nope and the rotated q_rope itself (no 2b launch)
+    bool fused_2c;  // ... and 2c too (no 2c launch, no q_nope), when the pointers allow
     size_t off_lat_acc, off_lat, off_raw, off_up_ws, off_abs_ws, off_rope_tab, total;
 };
 
@@ -306,6 +307,16 @@ bool qup_fused(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up) {
            d->rope > 0 && d->rope <= 64;
 }
 
+// 2a2's fused epilogue with 2c as well (wgemm.hip, qup_supported): one head's nope columns
+// per 128-column tile of the 128 x 4 plan; MLA_QUP_ABSORB=0 keeps the 2c launch (a
+// comparison aid: both give the same bits).
+bool qup_fused_2c(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up) {
+    const char* env = getenv("MLA_QUP_ABSORB");
+    if (env && strcmp(env, "0") == 0) return false;
+    return qup_fused(dt, d, up) && up.bn == 128 && up.stages == 4 && d->nope == 128 &&
+           d->rope == 64 && d->heads % 2 == 0 && d->kv_rank % 128 == 0 && d->kv_rank <= 512;
+}
+
 QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     QLayout L;
     const size_t bq = (size_t)d->batch * d->sq;
@@ -313,6 +324,7 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     L.down = plan_gemm(q_down_problem(dt, d, nullptr, nullptr, nullptr));
     L.up = plan_gemm(q_up_problem(dt, d, nullptr, nullptr, nullptr));
     L.fused = qup_fused(dt, d, L.up);
+    L.fused_2c = L.fused && qup_fused_2c(dt, d, L.up);
     L.absorb = plan_gemm(absorb_problem(dt, d, nullptr, nullptr, nullptr, L.fused));
     size_t o = 0;
     L.off_lat_acc = o;  // 2a1 output or its split partials (summed by the norm kernel)
@@ -640,6 +652,13 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
         qe.H = dims->heads; qe.nope = dims->nope; qe.rope = dims->rope;
         up.qup = &qe;
         up.C = nullptr;
+        if (L.fused_2c && (reinterpret_cast<uintptr_t>(W_uk) & 15) == 0 &&
+            (reinterpret_cast<uintptr_t>(q_absorbed) & 3) == 0) {
+            qe.w_uk = W_uk; qe.q_abs = q_absorbed; qe.kv = dims->kv_rank;
+            MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream),
+                        "2a2 + 2b + 2c launch");
+            return ok();
+        }
         MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream),
                     "2a2 + 2b launch");
         GemmProblem ab = absorb_problem(dtype, dims, raw, W_uk, q_absorbed, true);

@@ -24,11 +24,18 @@ enum OutType { kOutF32 = 0, kOutBF16 = 1, kOutF16 = 2 };   // the codes Store16<
 // the storage format -- the rounding 2c and 2b apply to the same fp32 values.  The rotation
 // of row m, pair i takes cos_sin[2 (m * rope/2 + i)] and the sin after it, the table the
 // 2a-n launch writes (RopeTable).  nope and rope are multiples of 32, rope <= 64.
+// With w_uk set the epilogue also does 2c: each head's 16-bit q_nope tile stays in LDS and
+// is multiplied by W_uk[h] ([H, nope, kv] contiguous) into q_abs [M, H, kv] (storage
+// format), and q_nope is not written.  That needs the 128 x 4 plan, nope = 128, rope = 64,
+// an even H and kv a multiple of 128 up to 512 (qup_supported).
 struct QUpEpilogue {
     void* q_nope = nullptr;
     void* q_rope = nullptr;
     const float* cos_sin = nullptr;
     int H = 0, nope = 0, rope = 0;
+    const void* w_uk = nullptr;
+    void* q_abs = nullptr;
+    int kv = 0;
 };
 
 // Optional output of the 2a-n launch for that epilogue: row m's cos and sin of the angles
@@ -82,8 +89,9 @@ GemmPlan plan_gemm(const GemmProblem& p);
 // operand pointers must also be 16-byte aligned -- wgemm_aligned -- or the launch takes the
 // tiled engine with the same plan)
 bool wgemm_supported(const GemmProblem& p, int bn, int split);
-// The fused 2a2 epilogue applies to a problem that wgemm_supported takes with split 1.
-bool qup_supported(const GemmProblem& p, const QUpEpilogue& q);
+// The fused 2a2 epilogue applies to a problem that wgemm_supported takes with split 1 (and
+// with w_uk set, on the plan's 128 x 4 tile only).
+bool qup_supported(const GemmProblem& p, const QUpEpilogue& q, const GemmPlan& plan);
 bool wgemm_aligned(const GemmProblem& p);
 hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* partials,
                         hipStream_t stream);

@@ -23,6 +23,16 @@
 // write chunk positions in order and take the permutation in their global offsets.
 // Rows past M and slices past the workgroup's K range load zeros (out-of-range buffer
 // offsets), so every slice issues the same loads and one wait count serves them all.
+//
+// 2a2's fused epilogues (QUP modes): kQupRope writes the nope columns as the 16-bit q_nope
+// that 2c reads and rotates the rope columns into q_rope (2b).  kQupAbsorb also does 2c: its
+// 128-column tiles are, in threes, head 2j's nope columns, head 2j+1's, and both heads' rope
+// columns (64 each; the W loads take that column map in their offsets), so a nope tile holds
+// the head's whole q_nope block.  It rounds the block to the storage format into LDS in the
+// A layout of the ring, streams W_uk[h] through the freed LDS as 64 x 128 slices in the W
+// layout (the first two during the main loop, into the RoPE table's space that a nope tile
+// does not use), and runs 2c's MFMAs on the same fragment reads, in the K order of the
+// tiled engine's 2c, so q_abs gets the same bits as 2a2 + 2c as separate launches.
 #include "kernels.h"
 #include "mma.h"
 #include "stage.h"
@@ -48,7 +58,9 @@ struct WArgs {
     QUpEpilogue q;                            // the fused 2a2 epilogue (QUP kernels)
 };
 
-template <typename TL, int BN, int NS, int MINB, bool QUP>
+constexpr int kQupNone = 0, kQupRope = 1, kQupAbsorb = 2;
+
+template <typename TL, int BN, int NS, int MINB, int QUP>
 __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     constexpr int kBRow = 2 * BN;                        // bytes per W row of a slice
     constexpr int kBStage = kWKS * kBRow;                // 16 KB / 8 KB
@@ -59,6 +71,8 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     constexpr int CB = BN / 64;                          // 32-column blocks per wave
     // QUP: the tile rows' RoPE table (rows x 32 pairs x (cos, sin)) after the ring
     constexpr int kTab = QUP ? kWBM * 32 * 8 : 0;
+    static_assert(QUP != kQupAbsorb || (BN == 128 && NS == 4),
+                  "the absorb tail's LDS plan: A2 32 KB + W_uk 96 KB in the ring, 32 KB in the table");
     __shared__ __attribute__((aligned(1024))) uint8_t smem[NS * kStage + kTab];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -69,6 +83,24 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     const int sp = t % a.split;
     const int g = t / a.split;
     const int m0 = tm * kWBM, n0 = tn * BN;
+    // kQupAbsorb: tile tn = 3j + r is head 2j + r's nope columns (r < 2) or the rope columns
+    // of heads 2j and 2j + 1 (r = 2)
+    bool rope_tile = false;
+    int head0 = 0;
+    if constexpr (QUP == kQupAbsorb) {
+        const int trip = tn / 3, r3 = tn - 3 * trip;
+        rope_tile = r3 == 2;
+        head0 = 2 * trip + (rope_tile ? 0 : r3);
+    }
+    // global column of the tile's column L
+    auto tile_col = [&](int L) __attribute__((always_inline)) -> int {
+        if constexpr (QUP == kQupAbsorb) {
+            const int qk = a.q.nope + a.q.rope;
+            return rope_tile ? (head0 + (L >> 6)) * qk + a.q.nope + (L & 63) : head0 * qk + L;
+        } else {
+            return n0 + L;
+        }
+    };
     const int k_begin = sp * a.k_chunk;
     const int nsl = (min(a.K, k_begin + a.k_chunk) - k_begin) / kWKS;   // whole slices
     const int rows_a = min(kWBM, a.M - m0);
@@ -77,7 +109,8 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     // rows w*kLoadsB*kRowsPerLoadB .. of each slice (loads of kRowsPerLoadB rows)
     const uint32_t lds0 = lds_addr(smem);
     const uint64_t a_base = reinterpret_cast<uint64_t>(a.A + g * a.sAg + (int64_t)m0 * a.lda);
-    const uint64_t b_base = reinterpret_cast<uint64_t>(a.B + g * a.sBg + n0);
+    const uint64_t b_base =
+        reinterpret_cast<uint64_t>(a.B + g * a.sBg + (QUP == kQupAbsorb ? 0 : n0));
     uint32_t a_voff[kWLoadsA], b_voff[kLoadsB];
     #pragma unroll
     for (int q = 0; q < kWLoadsA; ++q) {
@@ -89,11 +122,15 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
         const int pos = lane % (kBRow / 16);
         const int sw = BN >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
-        b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 16u * (pos ^ sw);
+        if constexpr (QUP == kQupAbsorb)
+            b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 2u * (uint32_t)tile_col(8 * (pos ^ sw));
+        else
+            b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 16u * (pos ^ sw);
     }
     // valid bytes of a slice: A rows below rows_a, all 64 W rows (whole slices)
     const uint32_t a_bytes = (uint32_t)(rows_a - 1) * (uint32_t)a.lda * 2u + 128u;
-    const uint32_t b_bytes = (uint32_t)(kWKS - 1) * (uint32_t)a.ldb * 2u + (uint32_t)kBRow;
+    const uint32_t b_bytes = (uint32_t)(kWKS - 1) * (uint32_t)a.ldb * 2u +
+                             (QUP == kQupAbsorb ? 2u * (uint32_t)a.N : (uint32_t)kBRow);
     auto issue_slice = [&](int s) __attribute__((always_inline)) {
         const uint32_t st = lds0 + (uint32_t)(s % NS) * kStage;
         const int k = k_begin + s * kWKS;
@@ -156,14 +193,49 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     bool has_rope = false;
     if constexpr (QUP) {
         const int qk = a.q.nope + a.q.rope, half = a.q.rope >> 1;
-        #pragma unroll
-        for (int c = 0; c < BN; c += 32) has_rope |= (n0 + c) % qk >= a.q.nope;
+        if constexpr (QUP == kQupAbsorb) {
+            has_rope = rope_tile;
+        } else {
+            #pragma unroll
+            for (int c = 0; c < BN; c += 32) has_rope |= (n0 + c) % qk >= a.q.nope;
+        }
         if (has_rope) {
             const v4i rt = rsrc_span(reinterpret_cast<uint64_t>(a.q.cos_sin + 2 * (int64_t)m0 * half),
                                      0, (uint32_t)(rows_a * half * 8));
             for (int b = wave; b < half; b += 4)   // kWBM * half * 8 bytes = half KB
                 dma16(rt, __builtin_amdgcn_readfirstlane(lds0 + NS * kStage + 1024u * b),
                       1024u * b + 16u * lane, 0);
+        }
+    }
+    // kQupAbsorb, nope tiles: W_uk[head0] (nope = 128 rows x kv, rows kv apart) in slices of
+    // 64 rows x 128 columns, pass p's two K halves kh, each in the W layout of a ring stage;
+    // pass 0 goes into the table's space now, passes 1 .. 3 into the ring after the main
+    // loop (slot(p, kh): the table's space for p = 0, else 32 KB p + 16 KB kh, past A2)
+    auto wuk_slot = [&](int p, int kh) __attribute__((always_inline)) -> uint32_t {
+        return (p == 0 ? (uint32_t)(NS * kStage) : 32768u * (uint32_t)p) + (uint32_t)kBStage * kh;
+    };
+    auto issue_wuk = [&](int p, int kh) __attribute__((always_inline)) {
+        if constexpr (QUP == kQupAbsorb) {
+            const int kv = a.q.kv;
+            const v4i rw = rsrc_span(reinterpret_cast<uint64_t>(
+                                         static_cast<const uint16_t*>(a.q.w_uk) +
+                                         (int64_t)head0 * a.q.nope * kv),
+                                     0, (uint32_t)(a.q.nope * kv * 2));
+            #pragma unroll
+            for (int q = 0; q < kLoadsB; ++q) {
+                const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
+                const int pos = lane % (kBRow / 16);
+                const uint32_t voff = (uint32_t)r * (uint32_t)kv * 2u + 16u * (pos ^ (4 * (r & 3)));
+                dma16(rw, __builtin_amdgcn_readfirstlane(
+                              lds0 + wuk_slot(p, kh) + (uint32_t)((wave * kLoadsB + q) * kRowsPerLoadB) * kBRow),
+                      voff, (uint32_t)(kh * kWKS * kv * 2 + 256 * p));
+            }
+        }
+    };
+    if constexpr (QUP == kQupAbsorb) {
+        if (!rope_tile) {
+            issue_wuk(0, 0);
+            issue_wuk(0, 1);
         }
     }
     #pragma unroll
@@ -190,6 +262,84 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     }
     wait_vm<0>();   // the zero loads past the range have landed
 
+    if constexpr (QUP == kQupAbsorb) {
+        if (!rope_tile) {
+            // ---- 2c for head0 on this tile's rows: q_abs = q_nope16 @ W_uk[head0]
+            const int kv = a.q.kv, passes = kv >> 7;
+            __syncthreads();   // every wave is done with the ring
+            for (int p = 1; p < passes; ++p) {
+                issue_wuk(p, 0);
+                issue_wuk(p, 1);
+            }
+            // A2: the 16-bit q_nope block, K slice kh = columns 64 kh .. at 16 KB kh, in the
+            // A layout of the ring.  Lane pairs (c, c ^ 1) swap values (DPP) so that each lane
+            // writes one dword: the even lane row R(e), the odd lane row R(e + 1).
+            const bool odd = lane & 1;
+            #pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+                #pragma unroll
+                for (int cb = 0; cb < CB; ++cb) {
+                    const int k = (32 * cb + (lane & 31)) & ~1;
+                    #pragma unroll
+                    for (int e = 0; e < 16; e += 2) {
+                        const float x0 = acc[rb][cb][e], x1 = acc[rb][cb][e + 1];
+                        const float p0 = dpp_move<0xB1>(x0), p1 = dpp_move<0xB1>(x1);
+                        const int row = 64 * wm + 32 * rb + acc_row(odd ? e + 1 : e, lane);
+                        const uint32_t w = odd ? Half<TL>::pack2(p1, x1) : Half<TL>::pack2(x0, p0);
+                        const uint32_t off = (uint32_t)kWAStage * wn + (uint32_t)row * 128u +
+                                             16u * ((k >> 3) ^ ((row >> 1) & 7)) + 2u * (k & 7);
+                        *reinterpret_cast<uint32_t*>(smem + off) = w;
+                    }
+                }
+            __syncthreads();
+            uint16_t* const qabs = static_cast<uint16_t*>(a.q.q_abs) + (int64_t)head0 * kv;
+            const int64_t ld_abs = (int64_t)a.q.H * kv;
+            #pragma unroll 1
+            for (int p = 0; p < passes; ++p) {
+                v16f acc2[2][CB];
+                #pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+                    #pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) acc2[rb][cb] = v16f{};
+                #pragma unroll
+                for (int kh = 0; kh < 2; ++kh)
+                    #pragma unroll
+                    for (int kt = 0; kt < kWKS / 16; ++kt) {
+                        v4u af[2], bf[CB];
+                        #pragma unroll
+                        for (int rb = 0; rb < 2; ++rb) af[rb] = a_frag((uint32_t)kWAStage * kh, kt, rb);
+                        #pragma unroll
+                        for (int cb = 0; cb < CB; ++cb) bf[cb] = b_frag(wuk_slot(p, kh) - kWAStage, kt, cb);
+                        #pragma unroll
+                        for (int rb = 0; rb < 2; ++rb)
+                            #pragma unroll
+                            for (int cb = 0; cb < CB; ++cb)
+                                acc2[rb][cb] = Mma<TL>::sub(af[rb], bf[cb], 0, acc2[rb][cb]);
+                    }
+                if (p == 0 && passes > 1) {   // passes 1 .. have landed (no stores issued yet)
+                    wait_vm<0>();
+                    __syncthreads();
+                }
+                #pragma unroll
+                for (int rb = 0; rb < 2; ++rb)
+                    #pragma unroll
+                    for (int cb = 0; cb < CB; ++cb) {
+                        uint16_t* const dst = qabs + 128 * p + (BN / 2) * wn + 32 * cb + ((lane & 31) & ~1);
+                        #pragma unroll
+                        for (int e = 0; e < 16; e += 2) {
+                            const float x0 = acc2[rb][cb][e], x1 = acc2[rb][cb][e + 1];
+                            const float p0 = dpp_move<0xB1>(x0), p1 = dpp_move<0xB1>(x1);
+                            const int row = 64 * wm + 32 * rb + acc_row(odd ? e + 1 : e, lane);
+                            const uint32_t w = odd ? Half<TL>::pack2(p1, x1) : Half<TL>::pack2(x0, p0);
+                            if (row < rows_a)
+                                *reinterpret_cast<uint32_t*>(dst + (int64_t)(m0 + row) * ld_abs) = w;
+                        }
+                    }
+            }
+            return;
+        }
+    }
+
     if constexpr (QUP) {
         // ---- fused 2a2 epilogue: nope blocks to q_nope, rope blocks rotated to q_rope.
         // Every 32-column block lies inside one head's nope or rope part (nope, rope and
@@ -204,7 +354,7 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         for (int rb = 0; rb < 2; ++rb)
             #pragma unroll
             for (int cb = 0; cb < CB; ++cb) {
-                const int c0 = n0 + (BN / 2) * wn + 32 * cb;
+                const int c0 = tile_col((BN / 2) * wn + 32 * cb);
                 const int h = c0 / qk, j0 = c0 - h * qk;
                 if (j0 < a.q.nope) {
                     uint16_t* dst = static_cast<uint16_t*>(a.q.q_nope) + (int64_t)h * a.q.nope + j0 + (lane & 31);
@@ -261,25 +411,31 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
 
 // Stage counts per column tile: 256 columns x 3 stages (144 KB of LDS); 128 columns x 4
 // stages (128 KB, one workgroup per CU) or 3 (96 KB); 64 columns x 3 (72 KB, two per CU), 4
-// or 6 stages (96 / 144 KB).  The fused 2a2 epilogue adds 32 KB for its RoPE table (160 KB
-// at 128 x 4; not with 64 x 6 or 256 x 3).
-template <typename TL, bool QUP>
+// or 6 stages (96 / 144 KB).  The fused 2a2 epilogues add 32 KB for the RoPE table (160 KB
+// at 128 x 4; not with 64 x 6 or 256 x 3); the one that also does 2c runs at 128 x 4 only.
+template <typename TL, int QUP>
 hipError_t launch_wgemm_t(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 block,
                           hipStream_t stream) {
-    if (plan.bn == 256 && plan.stages == 3 && !QUP)   // 144 KB: no room for the QUP table
-        hipLaunchKernelGGL((wgemm_kernel<TL, 256, 3, 1, false>), grid, block, 0, stream, a);
-    else if (plan.bn == 128 && plan.stages == 4)
+    if constexpr (QUP == kQupAbsorb) {
+        if (plan.bn == 128 && plan.stages == 4)
+            hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1, kQupAbsorb>), grid, block, 0, stream, a);
+        else
+            return hipErrorInvalidValue;
+    } else if (plan.bn == 256 && plan.stages == 3 && !QUP) {   // 144 KB: no room for the table
+        hipLaunchKernelGGL((wgemm_kernel<TL, 256, 3, 1, kQupNone>), grid, block, 0, stream, a);
+    } else if (plan.bn == 128 && plan.stages == 4) {
         hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1, QUP>), grid, block, 0, stream, a);
-    else if (plan.bn == 128 && plan.stages == 3)
+    } else if (plan.bn == 128 && plan.stages == 3) {
         hipLaunchKernelGGL((wgemm_kernel<TL, 128, 3, 1, QUP>), grid, block, 0, stream, a);
-    else if (plan.bn == 64 && plan.stages == 3)
+    } else if (plan.bn == 64 && plan.stages == 3) {
         hipLaunchKernelGGL((wgemm_kernel<TL, 64, 3, 2, QUP>), grid, block, 0, stream, a);
-    else if (plan.bn == 64 && plan.stages == 4)
+    } else if (plan.bn == 64 && plan.stages == 4) {
         hipLaunchKernelGGL((wgemm_kernel<TL, 64, 4, 1, QUP>), grid, block, 0, stream, a);
-    else if (plan.bn == 64 && plan.stages == 6 && !QUP)   // no room for the QUP table
-        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 6, 1, false>), grid, block, 0, stream, a);
-    else
+    } else if (plan.bn == 64 && plan.stages == 6 && !QUP) {   // no room for the table
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 6, 1, kQupNone>), grid, block, 0, stream, a);
+    } else {
         return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
@@ -296,11 +452,17 @@ bool wgemm_supported(const GemmProblem& p, int bn, int split) {
            (int64_t)kWBM * p.lda * 2 < kRsrcRange && (int64_t)kWKS * p.ldb * 2 < kRsrcRange;
 }
 
-bool qup_supported(const GemmProblem& p, const QUpEpilogue& q) {
-    return p.half && p.G == 1 && q.H > 0 && q.nope > 0 && q.nope % 32 == 0 && q.rope > 0 &&
-           q.rope % 32 == 0 && q.rope <= 64 &&
-           (int64_t)p.N == (int64_t)q.H * (q.nope + q.rope) && q.q_nope && q.q_rope &&
-           q.cos_sin;
+bool qup_supported(const GemmProblem& p, const QUpEpilogue& q, const GemmPlan& plan) {
+    const bool rope_ok = p.half && p.G == 1 && q.H > 0 && q.nope > 0 && q.nope % 32 == 0 &&
+                         q.rope > 0 && q.rope % 32 == 0 && q.rope <= 64 &&
+                         (int64_t)p.N == (int64_t)q.H * (q.nope + q.rope) && q.q_rope && q.cos_sin;
+    if (!q.w_uk) return rope_ok && q.q_nope;
+    // with 2c: one head's nope columns per 128-column tile, two heads' rope columns per
+    // tile, W_uk rows and q_abs rows 16-byte / 4-byte aligned, kv / 128 passes of 32 KB
+    return rope_ok && q.q_abs && plan.bn == 128 && plan.stages == 4 && q.nope == 128 &&
+           q.rope == 64 && q.H % 2 == 0 && q.kv > 0 && q.kv % 128 == 0 && q.kv <= 512 &&
+           (reinterpret_cast<uintptr_t>(q.w_uk) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(q.q_abs) & 3) == 0;
 }
 
 bool wgemm_aligned(const GemmProblem& p) {
@@ -326,13 +488,17 @@ hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* parti
     if (blocks <= 0 || blocks > 0x7fffffff) return hipErrorInvalidValue;
     const dim3 grid((unsigned)blocks), block(kWThreads);
     if (p.qup) {
-        if (plan.split != 1 || !qup_supported(p, *p.qup)) return hipErrorInvalidValue;
+        if (plan.split != 1 || !qup_supported(p, *p.qup, plan)) return hipErrorInvalidValue;
         a.q = *p.qup;
-        if (p.f16) return launch_wgemm_t<f16_t, true>(a, plan, grid, block, stream);
-        return launch_wgemm_t<bf16_t, true>(a, plan, grid, block, stream);
+        if (a.q.w_uk) {
+            if (p.f16) return launch_wgemm_t<f16_t, kQupAbsorb>(a, plan, grid, block, stream);
+            return launch_wgemm_t<bf16_t, kQupAbsorb>(a, plan, grid, block, stream);
+        }
+        if (p.f16) return launch_wgemm_t<f16_t, kQupRope>(a, plan, grid, block, stream);
+        return launch_wgemm_t<bf16_t, kQupRope>(a, plan, grid, block, stream);
     }
-    if (p.f16) return launch_wgemm_t<f16_t, false>(a, plan, grid, block, stream);
-    return launch_wgemm_t<bf16_t, false>(a, plan, grid, block, stream);
+    if (p.f16) return launch_wgemm_t<f16_t, kQupNone>(a, plan, grid, block, stream);
+    return launch_wgemm_t<bf16_t, kQupNone>(a, plan, grid, block, stream);
 }
 
 }  // namespace mla

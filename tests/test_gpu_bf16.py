@@ -86,10 +86,11 @@ def test_weight_streaming_gemm(ext, monkeypatch, dt, M, N, K, plan):
 @pytest.mark.parametrize("B,Sq,per_seq", [(2, 3, False), (5, 1, True), (128, 1, False),
                                            (65, 2, False)])
 def test_q_absorbed_fused_epilogue(ext, monkeypatch, dt, B, Sq, per_seq):
-    """2a2 on the weight-streaming engine with its fused epilogue (q_nope for 2c and the
-    rotated q_rope written by 2a2 itself) gives the same bits as 2a2 + the 2b launch
-    (MLA_QUP_FUSE=0) on the same plan, and matches the fp32 oracle; positions shared by
-    the batch (up to 4988) or per sequence."""
+    """2a2 on the weight-streaming engine with its fused epilogues gives the same bits as
+    the separate launches on the same plan, and matches the fp32 oracle; positions shared
+    by the batch (up to 4988) or per sequence.  Three forms: the default, where 2a2 also
+    rotates q_rope (2b) and runs 2c on each head's q_nope tile; MLA_QUP_ABSORB=0, where it
+    writes q_nope for the 2c launch; MLA_QUP_FUSE=0, 2a2 + the 2b launch + 2c."""
     inp = R.make_inputs(B, Sq, 4989, seed=B + Sq, dtype=dt)
     W_uk, _ = R.split_wkv_b(inp["wkv_b"], D.nope)
     pos = inp["positions"]
@@ -100,9 +101,12 @@ def test_q_absorbed_fused_epilogue(ext, monkeypatch, dt, B, Sq, per_seq):
     M, N = B * Sq, D.n_heads * D.qk_head
     monkeypatch.setenv("MLA_WGEMM_PLAN", f"{M},{N},{D.q_lora},1=128,1")
     qa, qr = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    monkeypatch.setenv("MLA_QUP_ABSORB", "0")
+    qa1, qr1 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
     monkeypatch.setenv("MLA_QUP_FUSE", "0")
     qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
     assert qa.dtype == dt and qr.dtype == dt
+    assert torch.equal(qa1, qa0) and torch.equal(qr1, qr0)
     assert torch.equal(qa, qa0) and torch.equal(qr, qr0)
     f32 = {k: (v.float() if v.is_floating_point() else v) for k, v in inp.items()}
     prep = R.prepare_q_ragged if per_seq else R.prepare_q_mla_absorbed
