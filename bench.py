@@ -37,6 +37,7 @@ import argparse
 import json
 import math
 import os
+import re
 import statistics
 import sys
 import time
@@ -189,7 +190,8 @@ def in_layer_kernel_us(layer, flush, n):
     torch's profiler (kernel start and end from the GPU's own timestamps), the library's
     kernels attributed to steps by launch order -- the layer launches its GEMMs in the order
     2a1, 2a2, 2c, 3d, a split-K reduce right after its GEMM, RMSNorm (2a-n, which also sums
-    2a1's split partials) and RoPE (2b) between them, and the fused attention's kernels
+    2a1's split partials) and RoPE (2b) between them (the 16-bit 2a2 may do 2b and 2c in its
+    epilogue: `wgemm_kernel<.., 2>`, counted as 2a2), and the fused attention's kernels
     (work list, pass, merge) as 3abc; at decode-sized fp32 batches 3d may be
     out_small_kernel, which also does the pass's split merge.  Returns {step: mean µs per
     layer} plus the layer's
@@ -227,6 +229,8 @@ def in_layer_kernel_us(layer, flush, n):
         if "gemm_kernel" in name:
             step = gemm_steps[min(cur["gemm"], 3)]
             cur["gemm"] += 1
+            if "wgemm_kernel" in name and re.search(r",\s*2>", name):
+                cur["gemm"] += 1      # 2a2 with 2b and 2c in its epilogue: no 2c launch
         elif "split_reduce" in name:
             step = cur["step"] or "2a1"
         elif "rmsnorm" in name:
@@ -599,6 +603,10 @@ def measure(args, ext, dev, neighbours=True, light=False):
             if n not in in_layer:
                 continue
             fl, by = work[n]
+            if n == "2a2":   # the steps its fused epilogue took over (no launch of their own)
+                for f in ("2b", "2c"):
+                    if f not in in_layer:
+                        fl, by = fl + work[f][0], by + work[f][1]
             t = in_layer[n] * 1e-6
             in_layer_steps[n] = {"us": in_layer[n],
                                  "tflops": round(fl / t / 1e12, 2),

@@ -28,11 +28,12 @@
 // that 2c reads and rotates the rope columns into q_rope (2b).  kQupAbsorb also does 2c: its
 // 128-column tiles are, in threes, head 2j's nope columns, head 2j+1's, and both heads' rope
 // columns (64 each; the W loads take that column map in their offsets), so a nope tile holds
-// the head's whole q_nope block.  It rounds the block to the storage format into LDS in the
-// A layout of the ring, streams W_uk[h] through the freed LDS as 64 x 128 slices in the W
-// layout (the first two during the main loop, into the RoPE table's space that a nope tile
-// does not use), and runs 2c's MFMAs on the same fragment reads, in the K order of the
-// tiled engine's 2c, so q_abs gets the same bits as 2a2 + 2c as separate launches.
+// the head's whole q_nope block.  W_uk[h] comes in as 64 x 128 slices in the W layout while
+// the main loop runs: the first two into the RoPE table's space (a nope tile has no rope
+// columns), the others in place of the ring's slices past the K range.  After the loop the
+// block is rounded to the storage format into LDS in the A layout, and 2c's MFMAs run on the
+// same fragment reads, in the K order of the tiled engine's 2c, so q_abs gets the same bits
+// as 2a2 + 2c as separate launches.
 #include "kernels.h"
 #include "mma.h"
 #include "stage.h"
@@ -131,7 +132,44 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     const uint32_t a_bytes = (uint32_t)(rows_a - 1) * (uint32_t)a.lda * 2u + 128u;
     const uint32_t b_bytes = (uint32_t)(kWKS - 1) * (uint32_t)a.ldb * 2u +
                              (QUP == kQupAbsorb ? 2u * (uint32_t)a.N : (uint32_t)kBRow);
+    // kQupAbsorb, nope tiles: W_uk[head0] (nope = 128 rows x kv, rows kv apart) in slices of
+    // 64 rows x 128 columns in the W layout of a ring stage, pass p's two K halves kh.  Pass 0
+    // goes into the table's space before the ring starts; pass p >= 1 takes the place of the
+    // ring's slice nsl + p - 1, past the K range (a stage the ring has just freed: its A
+    // part holds kh 0, its W part kh 1), which keeps the per-slice load count.  Passes past
+    // kv / 128 load zeros.  The tile's q_nope block goes into the stage of the last slice.
+    auto wuk_slot = [&](int p, int kh) __attribute__((always_inline)) -> uint32_t {
+        return (p == 0 ? (uint32_t)(NS * kStage) : (uint32_t)((nsl + p - 1) % NS) * kStage) +
+               (uint32_t)kBStage * kh;
+    };
+    auto issue_wuk = [&](int p, int kh) __attribute__((always_inline)) {
+        if constexpr (QUP == kQupAbsorb) {
+            const int kv = a.q.kv;
+            const bool live = p < (kv >> 7);
+            const v4i rw = rsrc_span(reinterpret_cast<uint64_t>(
+                                         static_cast<const uint16_t*>(a.q.w_uk) +
+                                         (int64_t)head0 * a.q.nope * kv),
+                                     0, live ? (uint32_t)(a.q.nope * kv * 2) : 0u);
+            #pragma unroll
+            for (int q = 0; q < kLoadsB; ++q) {
+                const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
+                const int pos = lane % (kBRow / 16);
+                const uint32_t voff = (uint32_t)r * (uint32_t)kv * 2u + 16u * (pos ^ (4 * (r & 3)));
+                dma16(rw, __builtin_amdgcn_readfirstlane(
+                              lds0 + wuk_slot(p, kh) + (uint32_t)((wave * kLoadsB + q) * kRowsPerLoadB) * kBRow),
+                      voff, live ? (uint32_t)(kh * kWKS * kv * 2 + 256 * p) : 0u);
+            }
+        }
+    };
     auto issue_slice = [&](int s) __attribute__((always_inline)) {
+        if constexpr (QUP == kQupAbsorb) {
+            static_assert(2 * kLoadsB == kLoads, "a W_uk pass issues a slice's load count");
+            if (!rope_tile && s >= nsl) {
+                issue_wuk(s - nsl + 1, 0);
+                issue_wuk(s - nsl + 1, 1);
+                return;
+            }
+        }
         const uint32_t st = lds0 + (uint32_t)(s % NS) * kStage;
         const int k = k_begin + s * kWKS;
         const bool live = s < nsl;
@@ -207,31 +245,6 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
                       1024u * b + 16u * lane, 0);
         }
     }
-    // kQupAbsorb, nope tiles: W_uk[head0] (nope = 128 rows x kv, rows kv apart) in slices of
-    // 64 rows x 128 columns, pass p's two K halves kh, each in the W layout of a ring stage;
-    // pass 0 goes into the table's space now, passes 1 .. 3 into the ring after the main
-    // loop (slot(p, kh): the table's space for p = 0, else 32 KB p + 16 KB kh, past A2)
-    auto wuk_slot = [&](int p, int kh) __attribute__((always_inline)) -> uint32_t {
-        return (p == 0 ? (uint32_t)(NS * kStage) : 32768u * (uint32_t)p) + (uint32_t)kBStage * kh;
-    };
-    auto issue_wuk = [&](int p, int kh) __attribute__((always_inline)) {
-        if constexpr (QUP == kQupAbsorb) {
-            const int kv = a.q.kv;
-            const v4i rw = rsrc_span(reinterpret_cast<uint64_t>(
-                                         static_cast<const uint16_t*>(a.q.w_uk) +
-                                         (int64_t)head0 * a.q.nope * kv),
-                                     0, (uint32_t)(a.q.nope * kv * 2));
-            #pragma unroll
-            for (int q = 0; q < kLoadsB; ++q) {
-                const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
-                const int pos = lane % (kBRow / 16);
-                const uint32_t voff = (uint32_t)r * (uint32_t)kv * 2u + 16u * (pos ^ (4 * (r & 3)));
-                dma16(rw, __builtin_amdgcn_readfirstlane(
-                              lds0 + wuk_slot(p, kh) + (uint32_t)((wave * kLoadsB + q) * kRowsPerLoadB) * kBRow),
-                      voff, (uint32_t)(kh * kWKS * kv * 2 + 256 * p));
-            }
-        }
-    };
     if constexpr (QUP == kQupAbsorb) {
         if (!rope_tile) {
             issue_wuk(0, 0);
@@ -266,14 +279,12 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         if (!rope_tile) {
             // ---- 2c for head0 on this tile's rows: q_abs = q_nope16 @ W_uk[head0]
             const int kv = a.q.kv, passes = kv >> 7;
-            __syncthreads();   // every wave is done with the ring
-            for (int p = 1; p < passes; ++p) {
-                issue_wuk(p, 0);
-                issue_wuk(p, 1);
-            }
-            // A2: the 16-bit q_nope block, K slice kh = columns 64 kh .. at 16 KB kh, in the
-            // A layout of the ring.  Lane pairs (c, c ^ 1) swap values (DPP) so that each lane
-            // writes one dword: the even lane row R(e), the odd lane row R(e + 1).
+            __syncthreads();   // every wave is done with the ring; W_uk has landed
+            // A2: the 16-bit q_nope block, K slice kh = columns 64 kh .. at 16 KB kh of the
+            // last slice's stage, in the A layout of the ring.  Lane pairs (c, c ^ 1) swap
+            // values (DPP) so that each lane writes one dword: the even lane row R(e), the
+            // odd lane row R(e + 1).
+            const uint32_t a2 = (uint32_t)((nsl + NS - 1) % NS) * kStage;
             const bool odd = lane & 1;
             #pragma unroll
             for (int rb = 0; rb < 2; ++rb)
@@ -286,7 +297,7 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
                         const float p0 = dpp_move<0xB1>(x0), p1 = dpp_move<0xB1>(x1);
                         const int row = 64 * wm + 32 * rb + acc_row(odd ? e + 1 : e, lane);
                         const uint32_t w = odd ? Half<TL>::pack2(p1, x1) : Half<TL>::pack2(x0, p0);
-                        const uint32_t off = (uint32_t)kWAStage * wn + (uint32_t)row * 128u +
+                        const uint32_t off = a2 + (uint32_t)kWAStage * wn + (uint32_t)row * 128u +
                                              16u * ((k >> 3) ^ ((row >> 1) & 7)) + 2u * (k & 7);
                         *reinterpret_cast<uint32_t*>(smem + off) = w;
                     }
@@ -307,7 +318,7 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
                     for (int kt = 0; kt < kWKS / 16; ++kt) {
                         v4u af[2], bf[CB];
                         #pragma unroll
-                        for (int rb = 0; rb < 2; ++rb) af[rb] = a_frag((uint32_t)kWAStage * kh, kt, rb);
+                        for (int rb = 0; rb < 2; ++rb) af[rb] = a_frag(a2 + (uint32_t)kWAStage * kh, kt, rb);
                         #pragma unroll
                         for (int cb = 0; cb < CB; ++cb) bf[cb] = b_frag(wuk_slot(p, kh) - kWAStage, kt, cb);
                         #pragma unroll
@@ -316,10 +327,6 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
                             for (int cb = 0; cb < CB; ++cb)
                                 acc2[rb][cb] = Mma<TL>::sub(af[rb], bf[cb], 0, acc2[rb][cb]);
                     }
-                if (p == 0 && passes > 1) {   // passes 1 .. have landed (no stores issued yet)
-                    wait_vm<0>();
-                    __syncthreads();
-                }
                 #pragma unroll
                 for (int rb = 0; rb < 2; ++rb)
                     #pragma unroll
