@@ -191,7 +191,8 @@ def in_layer_kernel_us(layer, flush, n):
     kernels attributed to steps by launch order -- the layer launches its GEMMs in the order
     2a1, 2a2, 2c, 3d, a split-K reduce right after its GEMM, RMSNorm (2a-n, which also sums
     2a1's split partials) and RoPE (2b) between them (the 16-bit 2a2 may do 2b and 2c in its
-    epilogue: `wgemm_kernel<.., 2>`, counted as 2a2), and the fused attention's kernels
+    epilogue: `wgemm_kernel<.., 2>`, counted as 2a2; at decode-sized fp32 batches
+    `q_small_kernel` does 2b and 2c, counted as 2c), and the fused attention's kernels
     (work list, pass, merge) as 3abc; at decode-sized fp32 batches 3d may be
     out_small_kernel, which also does the pass's split merge.  Returns {step: mean µs per
     layer} plus the layer's
@@ -212,13 +213,14 @@ def in_layer_kernel_us(layer, flush, n):
         ks.append((e.time_range.start, e.time_range.end, e.name))
     ks.sort()
     gemm_steps = ("2a1", "2a2", "2c", "3d")
+    folded = {}                       # step -> the steps its kernel also does
     tot = {}
     spans = []
     layers = 0
     cur = None
     for t0, t1, name in ks:
         if not any(k in name for k in ("gemm_kernel", "split_reduce", "rmsnorm_kernel",
-                                        "rope_kernel", "flash", "out_small")):
+                                        "rope_kernel", "q_small", "flash", "out_small")):
             cur = None                # the flush between layers
             continue
         if cur is None:
@@ -231,12 +233,17 @@ def in_layer_kernel_us(layer, flush, n):
             cur["gemm"] += 1
             if "wgemm_kernel" in name and re.search(r",\s*2>", name):
                 cur["gemm"] += 1      # 2a2 with 2b and 2c in its epilogue: no 2c launch
+                folded["2a2"] = ("2b", "2c")
         elif "split_reduce" in name:
             step = cur["step"] or "2a1"
         elif "rmsnorm" in name:
             step = "2a-n"
         elif "rope_kernel" in name:
             step = "2b"
+        elif "q_small" in name:       # 2b and 2c in one kernel at decode-sized fp32 batches
+            step = "2c"
+            cur["gemm"] += 1
+            folded["2c"] = ("2b",)
         elif "flash" in name:
             step = "3abc"
         elif "out_small" in name:      # 3d with the attention's split merge folded in
@@ -255,6 +262,7 @@ def in_layer_kernel_us(layer, flush, n):
     out["kernels_sum"] = round(sum(tot.values()) / layers, 2)
     out["layer_span"] = round(sum(b - a for a, b in spans) / layers, 2)
     out["layers"] = layers
+    out["folded"] = folded
     return out
 
 
@@ -603,10 +611,8 @@ def measure(args, ext, dev, neighbours=True, light=False):
             if n not in in_layer:
                 continue
             fl, by = work[n]
-            if n == "2a2":   # the steps its fused epilogue took over (no launch of their own)
-                for f in ("2b", "2c"):
-                    if f not in in_layer:
-                        fl, by = fl + work[f][0], by + work[f][1]
+            for f in in_layer.get("folded", {}).get(n, ()):   # steps its kernel also does
+                fl, by = fl + work[f][0], by + work[f][1]
             t = in_layer[n] * 1e-6
             in_layer_steps[n] = {"us": in_layer[n],
                                  "tflops": round(fl / t / 1e12, 2),

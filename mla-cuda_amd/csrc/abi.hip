@@ -317,6 +317,20 @@ bool qup_fused_2c(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up) {
            d->rope == 64 && d->heads % 2 == 0 && d->kv_rank % 128 == 0 && d->kv_rank <= 512;
 }
 
+// 2b + 2c as one VALU kernel at decode-sized fp32 batches (rowops.hip, launch_q_small);
+// MLA_Q_SMALL=0 keeps the 2b launch and the MFMA 2c.
+bool q_small_ok(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up, const void* W_uk,
+                const void* q_abs, const void* q_rope) {
+    const char* env = getenv("MLA_Q_SMALL");
+    if (env && strcmp(env, "0") == 0) return false;
+    return dt == MLA_DTYPE_F32 && (int64_t)d->batch * d->sq <= kQSmallRows &&
+           std::max(1, up.split) <= kQSmallMaxSplit && d->nope == 128 &&
+           d->kv_rank == 512 && d->rope % 2 == 0 && d->rope <= 64 &&
+           (reinterpret_cast<uintptr_t>(W_uk) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(q_abs) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(q_rope) & 7) == 0;
+}
+
 QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     QLayout L;
     const size_t bq = (size_t)d->batch * d->sq;
@@ -666,9 +680,21 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
                     "2c launch");
         return ok();
     }
+    const bool small = q_small_ok(dtype, dims, L.up, W_uk, q_absorbed, q_rope);
     if (L.up.split > 1) {
         float* up_parts = at<float>(workspace, L.off_up_ws);
         MLA_TRY_HIP(launch_gemm_partials(up, L.up, up_parts, stream), "2a2 launch");
+        if (small) {
+            MLA_TRY_HIP(launch_q_small(up_parts, L.up.split,
+                                       (int64_t)bq * dims->heads * (dims->nope + dims->rope),
+                                       positions, inv_freq, static_cast<const float*>(W_uk),
+                                       static_cast<float*>(q_rope),
+                                       static_cast<float*>(q_absorbed), dims->batch, dims->sq,
+                                       dims->heads, dims->nope, dims->rope, dims->kv_rank,
+                                       pos_per_batch, stream),
+                        "2b + 2c launch");
+            return ok();
+        }
         MLA_TRY_HIP(launch_rope(up_parts, positions, inv_freq, q_rope, storage_out(dtype),
                                 dims->batch, dims->sq, dims->heads, dims->nope, dims->rope,
                                 stream, pos_per_batch, L.up.split,
@@ -676,6 +702,16 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
                     "2b launch");
     } else {
         MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
+        if (small) {
+            MLA_TRY_HIP(launch_q_small(raw, 1, 0, positions, inv_freq,
+                                       static_cast<const float*>(W_uk),
+                                       static_cast<float*>(q_rope),
+                                       static_cast<float*>(q_absorbed), dims->batch, dims->sq,
+                                       dims->heads, dims->nope, dims->rope, dims->kv_rank,
+                                       pos_per_batch, stream),
+                        "2b + 2c launch");
+            return ok();
+        }
         MLA_TRY_HIP(launch_rope(raw, positions, inv_freq, q_rope, storage_out(dtype), dims->batch,
                                 dims->sq, dims->heads, dims->nope, dims->rope, stream,
                                 pos_per_batch),

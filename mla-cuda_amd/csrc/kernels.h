@@ -116,6 +116,18 @@ hipError_t launch_rope(const float* q_raw, const int64_t* positions, const float
                        void* q_rope, OutType out_type, int B, int Sq, int H, int nope,
                        int rope, hipStream_t stream, bool pos_per_batch = false, int nsplit = 1,
                        int64_t split_stride = 0, float* nope_out = nullptr);
+// 2b + 2c for decode-sized fp32 batches (B*Sq <= kQSmallRows, nope 128, kv 512, even
+// rope <= 64): from 2a2's output or its split-K partials (q_parts, nsplit of them,
+// split_stride floats apart, [B*Sq][H*(nope+rope)] each), the rotated q_rope [B*Sq][H][rope]
+// (rope_kernel's arithmetic, the same bits) and q_abs [B*Sq][H][kv] = q_nope @ W_uk[h]
+// (W_uk [H][nope][kv]) on the VALU, W_uk streamed once.  Pointers 16-byte aligned; at most
+// kQSmallMaxSplit partials.
+constexpr int kQSmallRows = 8;
+constexpr int kQSmallMaxSplit = 8;
+hipError_t launch_q_small(const float* q_parts, int nsplit, int64_t split_stride,
+                          const int64_t* positions, const float* inv_freq, const float* W_uk,
+                          float* q_rope, float* q_abs, int B, int Sq, int H, int nope, int rope,
+                          int kv, bool pos_per_batch, hipStream_t stream);
 // 3b (row_max may be null; when given it receives M = max_j m_part[row, j])
 hipError_t launch_combine(const float* m_part, const float* l_part, float* alpha,
                           float* row_sum, float* row_max, int rows, int P, hipStream_t stream);

@@ -359,6 +359,108 @@ __global__ void __launch_bounds__(256) split_rows_kernel(const v4u_t* __restrict
 }
 
 
+// ---- 2b + 2c for decode-sized fp32 batches (M = B*Sq <= kQSmallRows), from 2a2's split
+// partials: one workgroup per (head, 256-column half of q_abs).  At M <= 8 the 2c tile of
+// the MFMA engine is 1/4 .. 1/32 full and 2b is a launch of its own; here:
+//   1. The head's M q_nope rows, 2a2's partials summed in split order from 0 (rope_kernel's
+//      sum, the same bits; one 4-column quad per thread), go to LDS (rows past M as zeros).
+//      The half-0 workgroup also rotates the head's rope pairs into q_rope, one (row, pair)
+//      per thread, with rope_kernel's angle, sincosf and rotation.
+//   2. W_uk[h]'s 128 rows of the workgroup's 256 columns stream once: wave w takes rows
+//      32 w .. 32 w + 31 (1 KB per row and instruction), lane l columns 4 l .. 4 l + 3.  The
+//      partials' loads go out first (at most kQSmallMaxSplit per thread, in registers),
+//      then the 32 W_uk loads, so that step 1 waits for its own loads only and the stream
+//      runs under it; then each lane accumulates all eight q_nope rows against its rows
+//      (fp32 FMAs, row k ascending).
+//   3. The four waves' sums add in wave order through LDS and go to q_abs.
+constexpr int kQSmallNope = 128;
+constexpr int kQSmallKv = 512;
+static_assert(kQSmallRows * kQSmallNope == 4 * 256, "one q_nope quad per thread");
+
+__global__ void __launch_bounds__(256) q_small_kernel(const float* __restrict__ q_parts,
+                                                      int nsplit, int64_t split_stride,
+                                                      const int64_t* __restrict__ positions,
+                                                      const float* __restrict__ inv_freq,
+                                                      const float* __restrict__ W_uk,
+                                                      float* __restrict__ q_rope,
+                                                      float* __restrict__ q_abs, int Sq, int M,
+                                                      int H, int rope, int pos_per_batch) {
+    __shared__ __attribute__((aligned(16))) float qn[kQSmallRows][kQSmallNope];
+    __shared__ __attribute__((aligned(16))) float red[4][kQSmallRows][256];
+    const int h = blockIdx.x >> 1, c0 = 256 * (blockIdx.x & 1);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int qk = kQSmallNope + rope, half = rope >> 1;
+    // loads in the order they are needed: the partials of this thread's q_nope quad (row
+    // tid / 32, columns 4 (tid % 32) ..) and, in half 0, of its rope pair, then the W_uk rows
+    const int m = tid >> 5, k4 = 4 * (tid & 31);
+    const int64_t off_n = ((int64_t)m * H + h) * qk + k4;
+    const bool has_rope = c0 == 0 && tid < M * half;
+    const int mr = has_rope ? tid / half : 0, ir = has_rope ? tid % half : 0;
+    const int64_t off_r = ((int64_t)mr * H + h) * qk + kQSmallNope + 2 * ir;
+    v4f pn[kQSmallMaxSplit];
+    float2 pr[kQSmallMaxSplit];
+    #pragma unroll
+    for (int s = 0; s < kQSmallMaxSplit; ++s) {
+        pn[s] = v4f{0.f, 0.f, 0.f, 0.f};
+        pr[s] = make_float2(0.f, 0.f);
+        if (s < nsplit && m < M) pn[s] = *reinterpret_cast<const v4f*>(q_parts + s * split_stride + off_n);
+        if (s < nsplit && has_rope) pr[s] = *reinterpret_cast<const float2*>(q_parts + s * split_stride + off_r);
+    }
+    const float* w = W_uk + ((int64_t)h * kQSmallNope + 32 * wave) * kQSmallKv + c0 + 4 * lane;
+    v4f wr[32];
+    #pragma unroll
+    for (int r = 0; r < 32; ++r)
+        wr[r] = __builtin_nontemporal_load(reinterpret_cast<const v4f*>(w + (int64_t)r * kQSmallKv));
+    // 1. q_nope quad: the split sum in split order from 0 (rope_kernel's, the same bits)
+    v4f qs = v4f{0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+    for (int s = 0; s < kQSmallMaxSplit; ++s)
+        if (s < nsplit) qs += pn[s];
+    *reinterpret_cast<v4f*>(&qn[m][k4]) = qs;   // rows past M: zeros
+    if (has_rope) {
+        const int64_t pos = positions[pos_per_batch ? mr : mr % Sq];
+        float c, sn;
+        rope_cos_sin(rope_angle(pos, inv_freq[ir]), &c, &sn);
+        float x0 = 0.f, x1 = 0.f;
+        #pragma unroll
+        for (int s = 0; s < kQSmallMaxSplit; ++s)
+            if (s < nsplit) {
+                x0 += pr[s].x;
+                x1 += pr[s].y;
+            }
+        *reinterpret_cast<float2*>(q_rope + ((int64_t)mr * H + h) * rope + 2 * ir) =
+            make_float2(rope_even(x0, x1, c, sn), rope_odd(x0, x1, c, sn));
+    }
+    __syncthreads();
+    // 2. this wave's 32 W_uk rows against the eight q_nope rows
+    v4f acc[kQSmallRows];
+    #pragma unroll
+    for (int mm = 0; mm < kQSmallRows; ++mm) acc[mm] = v4f{0.f, 0.f, 0.f, 0.f};
+    #pragma unroll
+    for (int r4 = 0; r4 < 32; r4 += 4) {
+        #pragma unroll
+        for (int mm = 0; mm < kQSmallRows; ++mm) {
+            const v4f q = *reinterpret_cast<const v4f*>(&qn[mm][32 * wave + r4]);
+            #pragma unroll
+            for (int t = 0; t < 4; ++t)
+                #pragma unroll
+                for (int j = 0; j < 4; ++j) acc[mm][j] = __builtin_fmaf(q[t], wr[r4 + t][j], acc[mm][j]);
+        }
+    }
+    // 3. the four waves' sums in wave order
+    #pragma unroll
+    for (int mm = 0; mm < kQSmallRows; ++mm) *reinterpret_cast<v4f*>(&red[wave][mm][4 * lane]) = acc[mm];
+    __syncthreads();
+    for (int idx = tid; idx < M * 64; idx += 256) {
+        const int mm = idx >> 6, c4 = 4 * (idx & 63);
+        const v4f sum = ((*reinterpret_cast<const v4f*>(&red[0][mm][c4]) +
+                          *reinterpret_cast<const v4f*>(&red[1][mm][c4])) +
+                         *reinterpret_cast<const v4f*>(&red[2][mm][c4])) +
+                        *reinterpret_cast<const v4f*>(&red[3][mm][c4]);
+        *reinterpret_cast<v4f*>(q_abs + ((int64_t)mm * H + h) * kQSmallKv + c0 + c4) = sum;
+    }
+}
+
 // ---- 3d for decode-sized fp32 batches (M = B*Sq <= kOutSmallRows), with the fused
 // attention's key-split merge folded in.  Two workgroups per head, 64 output columns each.
 //   1. The head's M normalised ctx rows go to LDS: from a split pass's partials, wave w
@@ -626,6 +728,21 @@ hipError_t launch_split_rows(const void* src, void* dst_a, void* dst_b, int64_t 
     return hipGetLastError();
 }
 
+
+hipError_t launch_q_small(const float* q_parts, int nsplit, int64_t split_stride,
+                          const int64_t* positions, const float* inv_freq, const float* W_uk,
+                          float* q_rope, float* q_abs, int B, int Sq, int H, int nope, int rope,
+                          int kv, bool pos_per_batch, hipStream_t stream) {
+    const int M = B * Sq;
+    if (M < 1 || M > kQSmallRows || H <= 0 || nope != kQSmallNope || kv != kQSmallKv ||
+        rope <= 0 || rope % 2 != 0 || (int64_t)M * (rope / 2) > 256 || nsplit < 1 ||
+        nsplit > kQSmallMaxSplit)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(q_small_kernel, dim3(2 * H), dim3(256), 0, stream, q_parts, nsplit,
+                       split_stride, positions, inv_freq, W_uk, q_rope, q_abs, Sq, M, H, rope,
+                       pos_per_batch ? 1 : 0);
+    return hipGetLastError();
+}
 
 hipError_t launch_out_small(const FlashPartials& fp, const float* ctx, const float* row_sum,
                             const float* W_uv, float* out, int B, int Sq, int H, int R, int V,

@@ -255,6 +255,35 @@ def test_layer_cfg3_small_batch(ext, B):
     torch.testing.assert_close(out.cpu(), rout, **TOL)
 
 
+@pytest.mark.parametrize("B,Sq,per_seq", [(1, 1, False), (2, 3, False), (8, 1, True),
+                                           (3, 3, False)])
+def test_q_absorbed_small_batch_kernel(ext, monkeypatch, B, Sq, per_seq):
+    """fp32 decode batches of B*Sq <= 8 rows run 2b and 2c as one VALU kernel
+    (q_small_kernel); MLA_Q_SMALL=0 keeps the 2b launch and the MFMA 2c.  q_rope is the
+    same to the bit (same sums, angles and rotation); q_absorbed differs only in the order
+    of its fp32 sums.  Both match the oracle.  (3, 3) has 9 rows, past the kernel's 8: both
+    runs take the launches."""
+    inp = R.make_inputs(B, Sq, 4989, seed=B * 10 + Sq)
+    W_uk, _ = R.split_wkv_b(inp["wkv_b"], D.nope)
+    pos = inp["positions"]
+    if per_seq:
+        pos = torch.tensor([[4988 - 131 * b] for b in range(B)])
+    args = [gpu(inp[k]) for k in ("x", "W_q_a", "q_norm_w", "W_q_b")] + [gpu(W_uk.contiguous()),
+                                                                        gpu(pos)]
+    qa, qr = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    monkeypatch.setenv("MLA_Q_SMALL", "0")
+    qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    assert torch.equal(qr, qr0)
+    if B * Sq > 8:
+        assert torch.equal(qa, qa0)
+    torch.testing.assert_close(qa, qa0, rtol=1e-5, atol=1e-5)
+    prep = R.prepare_q_ragged if per_seq else R.prepare_q_mla_absorbed
+    rqa, rqr = prep(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"], W_uk, pos, D.nope,
+                    D.rope)
+    torch.testing.assert_close(qa, rqa, **TOL)
+    torch.testing.assert_close(qr, rqr, **TOL)
+
+
 def test_layer_cfg2_full_size(ext):
     """Headline decode shape: B=128, Sq=1, Sk=4989, fp32, full DeepSeek-V3 dims; every
     sequence against the oracle at the north-star tolerance."""
