@@ -1095,7 +1095,8 @@ bool use_out_small(mla_dtype_t dtype, const mla_dims_t* d, const FlashPlan& plan
     if (env && env[0] == '0') return false;
     const int64_t M = (int64_t)d->batch * d->sq;
     return !is_half(dtype) && !plan.balanced && M <= kOutSmallRows && d->kv_rank == 512 &&
-           M * std::max(1, plan.n_split) <= kOutSmallMergeRows;
+           plan.n_split <= kOutSmallMaxSplit && M * std::max(1, plan.n_split) <= kOutSmallMergeRows &&
+           (M <= kOutSmallMergeM || plan.n_split <= 1);
 }
 
 }  // namespace

@@ -244,10 +244,15 @@ FlashPartials flash_partials(const FlashProblem& p, const FlashPlan& plan, const
 // 3d for decode-sized fp32 batches (B*Sq <= kOutSmallRows, R = 512), with the fused
 // attention's split merge folded in: out[B*Sq][H][V] from the pass's state (fp.n_split > 1:
 // partials, else ctx / row_sum) and W_uv [H][V][R].
-constexpr int kOutSmallRows = 4;
-// Where it pays (measured): the rows of a head's merge, B*Sq*n_split, are what its two
-// workgroups per head read before the W_uv stream, so it is taken up to 32 of them.
-constexpr int kOutSmallMergeRows = 32;
+constexpr int kOutSmallRows = 8;
+constexpr int kOutSmallMaxSplit = 64;
+// Where it pays (measured, attention with 3d at Sk = 4989): both workgroups of a head read
+// the head's B*Sq*n_split partial rows beside the W_uv stream.  With a merge it is taken up
+// to B*Sq = 4 and 128 such rows (B=1: 43.1 against 49.1 us, B=2 54.1 / 60.2, B=4 87.6 /
+// 88.3); at B=8 (16 splits) the merge kernel and the 3d GEMM are faster (128.9 against
+// 132.1 us), so B*Sq = 5 .. 8 take it only for an unsplit pass.
+constexpr int kOutSmallMergeRows = 128;
+constexpr int kOutSmallMergeM = 4;
 hipError_t launch_out_small(const FlashPartials& fp, const float* ctx, const float* row_sum,
                             const float* W_uv, float* out, int B, int Sq, int H, int R, int V,
                             hipStream_t stream);

@@ -463,17 +463,21 @@ __global__ void __launch_bounds__(256) q_small_kernel(const float* __restrict__ 
 
 // ---- 3d for decode-sized fp32 batches (M = B*Sq <= kOutSmallRows), with the fused
 // attention's key-split merge folded in.  Two workgroups per head, 64 output columns each.
-//   1. The head's M normalised ctx rows go to LDS: from a split pass's partials, wave w
-//      summing splits w, w+4, .. of every row (weights 2^(m_s - max_s m_s), lane: 8
-//      columns) and the four waves' sums added in wave order; from ctx / row_sum when the
-//      pass ran unsplit.  Then ctx_n = ctx / row_sum.
-//   2. The W_uv rows of the workgroup's columns (2 KB each, contiguous in K) stream once:
-//      each 16-lane group of a wave takes four rows (the lanes' 16-byte loads cover 256
-//      contiguous bytes per instruction), all in flight at once, against all M ctx rows:
-//      out[m][h][n] = sum_k ctx_n[m][k] W_uv[h][n][k], reduced over the 16 lanes with four
+//   0. The loads go out in the order they are consumed: the rows' split maxima and sums
+//      (lane s of a wave: split s), then the W_uv rows of the workgroup's columns (2 KB
+//      each, contiguous in K: each 16-lane group of a wave takes four rows, its lanes'
+//      16-byte loads covering 256 contiguous bytes per instruction), then the first
+//      kOutBatch splits of the partials.  The W_uv stream runs under the merge.
+//   1. Weights: wave w takes rows w and w + 4: m = max_s m_s, w_s = 2^(m_s - m),
+//      L = sum_s w_s l_s (wave reductions); w_s and 1 / L go to LDS.
+//   2. Merge: a thread takes 8 columns of one or two rows (M x 64 items) and sums the
+//      weighted partials over the splits in split order, kOutBatch splits of loads in flight
+//      for both items; ctx_n = sum / L into LDS (a row without visible keys gives zeros, as
+//      the 3d GEMM does).  An unsplit pass gives ctx_n = ctx / row_sum.
+//   3. out[m][h][n] = sum_k ctx_n[m][k] W_uv[h][n][k], reduced over the 16 lanes with four
 //      DPP steps.
-// This replaces flash_merge_kernel plus the 3d GEMM, whose 32-row MFMA tile is 1/32 full at
-// M = 1 (4.2 MFLOP of tile work per head, ~6.8 us at one CU's fp32 MFMA rate).
+// This replaces flash_merge_kernel plus the 3d GEMM, whose 32-row MFMA tile is 1/32 .. 1/4
+// full at M = 1 .. 8 (4.2 MFLOP of tile work per head, ~6.8 us at one CU's fp32 MFMA rate).
 constexpr int kOutR = 512;
 constexpr int kOutCols = 64;   // output columns per workgroup
 
@@ -485,6 +489,8 @@ __device__ __forceinline__ float row16_reduce(float v, Op op) {
     return op(v, dpp_move<0x140>(v));   // other half of 16
 }
 
+constexpr int kOutBatch = 8;   // splits of partial loads in flight per item
+
 __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict__ o,
                                                         const float* __restrict__ mpart,
                                                         const float* __restrict__ lpart,
@@ -494,85 +500,35 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
                                                         const float* __restrict__ W,
                                                         float* __restrict__ out, int B, int Sq,
                                                         int H, int V) {
-    __shared__ __attribute__((aligned(16))) float part[4][kOutSmallRows][kOutR];
-    __shared__ float lsum[4][kOutSmallRows];
+    __shared__ __attribute__((aligned(16))) float part[kOutSmallRows][kOutR];
+    __shared__ float wts[kOutSmallRows][kOutSmallMaxSplit];
+    __shared__ float invl[kOutSmallRows];
     const int col_blocks = (V + kOutCols - 1) / kOutCols;
     const int h = blockIdx.x / col_blocks, c0 = (blockIdx.x % col_blocks) * kOutCols;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int M = B * Sq, rows_b = Sq * H;
     const int64_t step = (int64_t)B * rows_b;   // between a row's split slots
-    int64_t slot0[kOutSmallRows];
+    auto slot0 = [&](int mi) -> int64_t {
+        return (int64_t)(mi / Sq) * rows_b + (int64_t)(mi % Sq) * H + h;
+    };
+    const bool split = n_split > 1;
+    static_assert(kOutSmallRows <= 8, "two rows per wave for the weights, two items per thread");
+
+    // 0a. split maxima and sums of rows wave and wave + 4
+    float ms[2], lv[2];
     #pragma unroll
-    for (int mi = 0; mi < kOutSmallRows; ++mi)
-        slot0[mi] = mi < M ? (int64_t)(mi / Sq) * rows_b + (int64_t)(mi % Sq) * H + h : 0;
-    if (n_split > 1) {
-        float mx[kOutSmallRows];
-        v4f a0[kOutSmallRows], a1[kOutSmallRows];
-        float ls[kOutSmallRows];
-        #pragma unroll
-        for (int mi = 0; mi < kOutSmallRows; ++mi) {
-            mx[mi] = -INFINITY;
-            if (mi < M)
-                for (int s = lane; s < n_split; s += 64)
-                    mx[mi] = fmaxf(mx[mi], mpart[slot0[mi] + s * step]);
-            mx[mi] = wave_reduce(mx[mi], OpMax{});
-            a0[mi] = v4f{0.f, 0.f, 0.f, 0.f};
-            a1[mi] = a0[mi];
-            ls[mi] = 0.f;
-        }
-        #pragma unroll 2
-        for (int s = wave; s < n_split; s += 4) {
-            #pragma unroll
-            for (int mi = 0; mi < kOutSmallRows; ++mi) {
-                if (mi < M) {
-                    const int64_t slot = slot0[mi] + s * step;
-                    const float ms = mpart[slot];
-                    const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx[mi]);
-                    const v4f* src = reinterpret_cast<const v4f*>(o + slot * kOutR) + 2 * lane;
-                    a0[mi] += w * src[0];
-                    a1[mi] += w * src[1];
-                    ls[mi] += w * lpart[slot];
-                }
-            }
-        }
-        #pragma unroll
-        for (int mi = 0; mi < kOutSmallRows; ++mi) {
-            if (mi < M) {
-                *reinterpret_cast<v4f*>(&part[wave][mi][8 * lane]) = a0[mi];
-                *reinterpret_cast<v4f*>(&part[wave][mi][8 * lane + 4]) = a1[mi];
-                if (lane == 0) lsum[wave][mi] = ls[mi];
-            }
-        }
-        __syncthreads();
-        // wave w normalises rows w, w+4, .. (in place in part[0])
-        for (int mi = wave; mi < M; mi += 4) {
-            // a row without visible keys (row sum 0) gives zeros, as the 3d GEMM does
-            const float L = ((lsum[0][mi] + lsum[1][mi]) + lsum[2][mi]) + lsum[3][mi];
-            const float inv = L == 0.f ? 0.f : 1.f / L;
-            #pragma unroll
-            for (int jj = 0; jj < 2; ++jj) {
-                const int k = 8 * lane + 4 * jj;
-                const v4f x = ((*reinterpret_cast<const v4f*>(&part[0][mi][k]) +
-                                *reinterpret_cast<const v4f*>(&part[1][mi][k])) +
-                               *reinterpret_cast<const v4f*>(&part[2][mi][k])) +
-                              *reinterpret_cast<const v4f*>(&part[3][mi][k]);
-                *reinterpret_cast<v4f*>(&part[0][mi][k]) = x * inv;
-            }
-        }
-    } else {
-        for (int mi = wave; mi < M; mi += 4) {
-            const int64_t r = slot0[mi];
-            const float inv = rs[r] == 0.f ? 0.f : 1.f / rs[r];
-            const v4f* src = reinterpret_cast<const v4f*>(ctx + r * kOutR) + 2 * lane;
-            *reinterpret_cast<v4f*>(&part[0][mi][8 * lane]) = src[0] * inv;
-            *reinterpret_cast<v4f*>(&part[0][mi][8 * lane + 4]) = src[1] * inv;
+    for (int r = 0; r < 2; ++r) {
+        const int mi = wave + 4 * r;
+        ms[r] = -INFINITY;
+        lv[r] = 0.f;
+        if (split && mi < M && lane < n_split) {
+            const int64_t sl = slot0(mi) + lane * step;
+            ms[r] = mpart[sl];
+            lv[r] = lpart[sl];
         }
     }
-    __syncthreads();
-    // 16-lane group grp of wave w takes columns c0 + 16 w + grp + 4 j, j = 0..3, all four
-    // rows in flight at once (128 KB per workgroup); lane li of the group holds floats
-    // 64 q + 4 li .. +3 (q = 0..7) of each row, and each ctx chunk read from LDS serves all
-    // four rows
+    // 0b. the W_uv rows: 16-lane group grp of wave w takes columns c0 + 16 w + grp + 4 j,
+    // j = 0..3; lane li of the group holds floats 64 q + 4 li .. +3 (q = 0..7) of each row
     const int grp = lane >> 4, li = lane & 15;
     const float* Wh = W + (int64_t)h * V * kOutR;
     v4f wv[4][8];
@@ -584,6 +540,83 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
         #pragma unroll
         for (int q = 0; q < 8; ++q) wv[jr][q] = wr[16 * q];
     }
+    // 0c. the first splits of the partials of this thread's items (row idx / 64, columns
+    // 8 (idx % 64) .. +7, idx = tid, tid + 256)
+    bool live[2];
+    int imi[2];
+    const float* ibase[2];
+    v4f pa[2][kOutBatch][2];
+    #pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int idx = tid + 256 * j;
+        live[j] = split && idx < M * 64;
+        imi[j] = live[j] ? idx >> 6 : 0;
+        ibase[j] = o + (slot0(imi[j]) * kOutR + 8 * (idx & 63));
+    }
+    auto load_batch = [&](int s0) __attribute__((always_inline)) {
+        #pragma unroll
+        for (int j = 0; j < 2; ++j)
+            #pragma unroll
+            for (int sb = 0; sb < kOutBatch; ++sb)
+                if (live[j] && s0 + sb < n_split) {
+                    const v4f* src = reinterpret_cast<const v4f*>(ibase[j] + (s0 + sb) * step * kOutR);
+                    pa[j][sb][0] = src[0];
+                    pa[j][sb][1] = src[1];
+                }
+    };
+    load_batch(0);
+
+    // 1. the split weights
+    #pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int mi = wave + 4 * r;
+        if (split && mi < M) {
+            const float mx = wave_reduce(ms[r], OpMax{});
+            const float w = (lane < n_split && ms[r] != -INFINITY) ? __builtin_amdgcn_exp2f(ms[r] - mx) : 0.f;
+            const float L = wave_reduce(w * lv[r], OpSum{});
+            if (lane < n_split) wts[mi][lane] = w;
+            if (lane == 0) invl[mi] = L == 0.f ? 0.f : 1.f / L;
+        }
+    }
+    __syncthreads();
+
+    // 2. the merge, or the unsplit pass's ctx / row_sum
+    if (split) {
+        v4f a[2][2];
+        #pragma unroll
+        for (int j = 0; j < 2; ++j) a[j][0] = a[j][1] = v4f{0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < n_split; s0 += kOutBatch) {
+            if (s0 > 0) load_batch(s0);
+            #pragma unroll
+            for (int j = 0; j < 2; ++j)
+                #pragma unroll
+                for (int sb = 0; sb < kOutBatch; ++sb)
+                    if (live[j] && s0 + sb < n_split) {
+                        const float w = wts[imi[j]][s0 + sb];
+                        a[j][0] += w * pa[j][sb][0];
+                        a[j][1] += w * pa[j][sb][1];
+                    }
+        }
+        #pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (live[j]) {
+                const int c = 8 * ((tid + 256 * j) & 63);
+                const float inv = invl[imi[j]];
+                *reinterpret_cast<v4f*>(&part[imi[j]][c]) = a[j][0] * inv;
+                *reinterpret_cast<v4f*>(&part[imi[j]][c + 4]) = a[j][1] * inv;
+            }
+    } else {
+        for (int mi = wave; mi < M; mi += 4) {
+            const int64_t r = slot0(mi);
+            const float inv = rs[r] == 0.f ? 0.f : 1.f / rs[r];
+            const v4f* src = reinterpret_cast<const v4f*>(ctx + r * kOutR) + 2 * lane;
+            *reinterpret_cast<v4f*>(&part[mi][8 * lane]) = src[0] * inv;
+            *reinterpret_cast<v4f*>(&part[mi][8 * lane + 4]) = src[1] * inv;
+        }
+    }
+    __syncthreads();
+
+    // 3. every ctx chunk read from LDS serves the group's four W_uv rows
     #pragma unroll
     for (int mi = 0; mi < kOutSmallRows; ++mi) {
         if (mi < M) {
@@ -592,7 +625,7 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
             for (int jr = 0; jr < 4; ++jr) acc[jr] = v4f{0.f, 0.f, 0.f, 0.f};
             #pragma unroll
             for (int q = 0; q < 8; ++q) {
-                const v4f c = *reinterpret_cast<const v4f*>(&part[0][mi][64 * q + 4 * li]);
+                const v4f c = *reinterpret_cast<const v4f*>(&part[mi][64 * q + 4 * li]);
                 #pragma unroll
                 for (int jr = 0; jr < 4; ++jr) acc[jr] += wv[jr][q] * c;
             }
@@ -750,7 +783,9 @@ hipError_t launch_out_small(const FlashPartials& fp, const float* ctx, const flo
     const int M = B * Sq;
     // each workgroup's 4 waves x 4 groups x 4 rows cover its kOutCols columns
     static_assert(kOutCols == 4 * 4 * 4, "column coverage");
-    if (M < 1 || M > kOutSmallRows || R != kOutR || H <= 0 || V <= 0) return hipErrorInvalidValue;
+    if (M < 1 || M > kOutSmallRows || R != kOutR || H <= 0 || V <= 0 ||
+        fp.n_split > kOutSmallMaxSplit)
+        return hipErrorInvalidValue;
     if (fp.n_split > 1 ? !(fp.o && fp.m && fp.l) : !(ctx && row_sum)) return hipErrorInvalidValue;
     const int col_blocks = (V + kOutCols - 1) / kOutCols;
     hipLaunchKernelGGL(out_small_kernel, dim3(H * col_blocks), dim3(256), 0, stream, fp.o, fp.m, fp.l,

@@ -251,12 +251,15 @@ def test_fp32_kernels_full_size(ext, monkeypatch, wave):
 @pytest.mark.parametrize("B,Sq,Sk,causal", [(1, 1, 4989, False), (3, 1, 4989, False),
                                             (3, 1, 100, False), (1, 4, 700, True),
                                             (1, 4, 64, True), (1, 1, 33, False),
-                                            (4, 1, 512, False)])
+                                            (4, 1, 512, False), (4, 1, 4989, False),
+                                            (8, 1, 4989, False), (5, 1, 1000, False),
+                                            (2, 4, 700, True), (1, 8, 64, True),
+                                            (8, 1, 64, False)])
 def test_fp32_decode_3d_with_merge(ext, monkeypatch, small, B, Sq, Sk, causal):
-    """At B*Sq <= 4 (fp32) with few split rows to merge, mla_attention runs 3d on a kernel
-    that also merges the pass's key splits (or reads ctx / row_sum when the pass ran
-    unsplit: B=1, Sq=4, Sk=64); MLA_OUT_SMALL=0 keeps the merge kernel and the 3d GEMM.
-    Both against the oracle."""
+    """At B*Sq <= 4 (fp32) with at most 128 split rows per head to merge, mla_attention runs
+    3d on a kernel that also merges the pass's key splits, and at B*Sq <= 8 on the same
+    kernel reading ctx / row_sum when the pass ran unsplit (Sk = 64); MLA_OUT_SMALL=0 keeps
+    the merge kernel and the 3d GEMM.  Both against the oracle."""
     monkeypatch.setenv("MLA_OUT_SMALL", small)
     args = inputs(B, Sq, Sk, seed=5 * Sk + B, dt=F32)
     close(run(ext, args, causal), oracle(args, causal), F32)

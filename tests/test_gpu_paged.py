@@ -89,9 +89,9 @@ def test_paged_attention_matches_oracle(ext, monkeypatch, path, page, lens, caus
 def test_paged_equals_dense_bitwise(ext, monkeypatch, path):
     """Full lengths and pages laid out in sequence order: the dense cache gives the same
     answer bit for bit on either path.  The paged fused pass always runs the 64-row kernel
-    (its work list is built on the device), so the dense call is pinned to that kernel for
-    the bitwise check; the dense call's own choice at this batch (the fp32 key-split waves)
-    agrees to rounding."""
+    (its work list is built on the device) and then the merge kernel and the 3d GEMM, so
+    the dense call is pinned to those for the bitwise check; the dense call's own choice at
+    this batch (the fp32 key-split waves, 3d with the merge folded in) agrees to rounding."""
     set_path(monkeypatch, path)
     B, Sk, page = 3, 4992, 64
     g = torch.Generator().manual_seed(31)
@@ -105,6 +105,7 @@ def test_paged_equals_dense_bitwise(ext, monkeypatch, path):
     sl = torch.full((B,), Sk, dtype=torch.int32)
     own = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
     monkeypatch.setenv("MLA_FLASH32_WAVE", "0")
+    monkeypatch.setenv("MLA_OUT_SMALL", "0")
     dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE)
     paged = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck.reshape(-1, page, D.kv_rank)),
                                     gpu(pe.reshape(-1, page, D.rope)), gpu(table), gpu(sl),
@@ -159,8 +160,8 @@ def test_paged_work_list_many_sequences(ext, uniform):
 def test_paged_equal_short_lengths_equal_dense(ext, monkeypatch):
     """Every sequence the same length L below the pool's capacity: the work list takes the
     dense plan for L, so the result equals the dense call on [B, L] bit for bit (the dense
-    call pinned to the paged pass's 64-row kernel; its own choice here, the fp32 key-split
-    waves, agrees to rounding)."""
+    call pinned to the paged pass's 64-row kernel, merge kernel and 3d GEMM; its own choice
+    here, the fp32 key-split waves and 3d with the merge folded in, agrees to rounding)."""
     B, L, page, max_pages = 3, 3000, 64, 78
     g = torch.Generator().manual_seed(8)
     qa = torch.randn(B, 1, D.n_heads, D.kv_rank, generator=g)
@@ -174,6 +175,7 @@ def test_paged_equal_short_lengths_equal_dense(ext, monkeypatch):
     dense_pe = pe.reshape(B, max_pages * page, D.rope)[:, :L].contiguous()
     own = ext.mla_attention(gpu(qa), gpu(qr), gpu(dense_ck), gpu(dense_pe), gpu(wuv), SCALE)
     monkeypatch.setenv("MLA_FLASH32_WAVE", "0")
+    monkeypatch.setenv("MLA_OUT_SMALL", "0")
     dense = ext.mla_attention(gpu(qa), gpu(qr), gpu(dense_ck), gpu(dense_pe), gpu(wuv), SCALE)
     paged = ext.mla_attention_paged(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(table), gpu(sl),
                                     gpu(wuv), SCALE)
