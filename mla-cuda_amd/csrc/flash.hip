@@ -2626,9 +2626,11 @@ FlashPlan plan_flash(const FlashProblem& p) {
     // the same whole number of 16-key blocks, and the fewest splits that keep that number.
     // Its fixed cost per launch is lower (less Q to load, a quarter of the split partials
     // to write and merge) but a block costs it ~5.4 us against ~4.2 in the 64-row kernel,
-    // so it is taken up to 8 blocks per wave (measured at B=1: Sk 512 / 4989 / 16384 20.0 /
+    // so it is taken up to 12 blocks per wave (measured at B=1: Sk 512 / 4989 / 16384 20.0 /
     // 35.4 / 64.6 us against 25.2 / 46.8 / 75.4; B=2..4, Sk=4989: 47.2 / 63.5 / 75.0
-    // against 58.2 / 67.7 / 77.0; B=8: 129.9 against 119.0, 20 blocks per wave).
+    // against 58.2 / 67.7 / 77.0; B=8: 129.9 against 119.0, 20 blocks per wave; with 3d:
+    // B=4, 10 blocks: 83.0 against 88.3, and at 16 blocks B=6 121.5 against 108.2, B=4 with
+    // Sk=8192 116.5 against 113.0, B=2 with Sk=16384 116.6 against 115.9).
     // MLA_FLASH32_WAVE=0 / 1 forces the choice (both kernels give the same results to
     // rounding).
     const char* wave_env = std::getenv("MLA_FLASH32_WAVE");
@@ -2638,9 +2640,9 @@ FlashPlan plan_flash(const FlashProblem& p) {
     const bool wave_ok = !p.half && !p.fp8_kv && !p.want_list;
     const int base16 = p.B * ((p.Sq * p.H + kWRows - 1) / kWRows);
     const int wblocks = (p.Sk + kWKeys - 1) / kWKeys;
-    const int target = std::max(1, (kNumCUs + base16 / 2) / base16);
+    const int target = std::max(1, kNumCUs / base16);   // splits that fit one round
     const int bpw = std::max(1, (wblocks + 4 * target - 1) / (4 * target));
-    constexpr int kWaveMaxBlocks = 8;
+    constexpr int kWaveMaxBlocks = 12;
     if (wave_ok && (wave_env ? wave_env[0] == '1' : base < kNumCUs && bpw <= kWaveMaxBlocks)) {
         f.wave = true;
         f.row_tiles = (p.Sq * p.H + kWRows - 1) / kWRows;

@@ -54,9 +54,12 @@ MLA_HD int wl_max_items(int B, int row_tiles) {
 }
 
 // Keys per split of a dense batch of Sk keys, base = B * row_tiles workgroups per split.
-// Below one workgroup per CU: about one workgroup per CU, at least one key block per split.
-// (Measured at B=1: Sk=512 takes 25.0 us in 32 one-block splits against 33.0 us in 8
-// four-block ones; at Sk=4989 the split size leaves the time unchanged.)
+// Below one workgroup per CU: as many splits as fit in one round of CUs (floor(CUs / base)),
+// at least one key block per split.  (Measured at B=1: Sk=512 takes 25.0 us in 32 one-block
+// splits against 33.0 us in 8 four-block ones; at Sk=4989 the split size leaves the time
+// unchanged.  Rounding the split count to nearest instead put B=5, Sk=4989 at 26 splits of
+// 12 blocks, 260 workgroups, and the 4 of the second round took the attention from ~100
+// to 154 us.)
 // From one workgroup per CU up, the rounds of workgroups set the time, and a base just
 // past a multiple of the CU count leaves the last round nearly empty (B=132 decode: 264
 // workgroups run as two rounds of one).  A split s of 1..4 is taken when its rounds of
@@ -72,7 +75,7 @@ MLA_HD int wl_max_items(int B, int row_tiles) {
 MLA_HD int dense_keys_per_split(int Sk, int base, int block_keys) {
     const int blocks = (Sk + block_keys - 1) / block_keys;
     if (base < kNumCUs) {
-        int split = (kNumCUs + base / 2) / base;
+        int split = kNumCUs / base;
         split = wl_min(wl_max(split, 1), blocks);
         return (blocks + split - 1) / split * block_keys;
     }
