@@ -470,10 +470,12 @@ __global__ void __launch_bounds__(256) q_small_kernel(const float* __restrict__ 
 //      kOutBatch splits of the partials.  The W_uv stream runs under the merge.
 //   1. Weights: wave w takes rows w and w + 4: m = max_s m_s, w_s = 2^(m_s - m),
 //      L = sum_s w_s l_s (wave reductions); w_s and 1 / L go to LDS.
-//   2. Merge: a thread takes 8 columns of one or two rows (M x 64 items) and sums the
-//      weighted partials over the splits in split order, kOutBatch splits of loads in flight
-//      for both items; ctx_n = sum / L into LDS (a row without visible keys gives zeros, as
-//      the 3d GEMM does).  An unsplit pass gives ctx_n = ctx / row_sum.
+//   2. Merge: items are (row, 8 columns), M x 64 of them.  At M = 1 and 2 each item's
+//      splits are dealt to 4 or 2 threads (split phases q, q + 4, ..), so that every thread
+//      loads; at M > 4 a thread takes two items.  A unit sums its weighted partials in split
+//      order, kOutBatch splits of loads in flight; the phases add in phase order through
+//      LDS, and ctx_n = sum / L goes to LDS (a row without visible keys gives zeros, as the
+//      3d GEMM does).  An unsplit pass gives ctx_n = ctx / row_sum.
 //   3. out[m][h][n] = sum_k ctx_n[m][k] W_uv[h][n][k], reduced over the 16 lanes with four
 //      DPP steps.
 // This replaces flash_merge_kernel plus the 3d GEMM, whose 32-row MFMA tile is 1/32 .. 1/4
@@ -503,6 +505,7 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
     __shared__ __attribute__((aligned(16))) float part[kOutSmallRows][kOutR];
     __shared__ float wts[kOutSmallRows][kOutSmallMaxSplit];
     __shared__ float invl[kOutSmallRows];
+    __shared__ __attribute__((aligned(16))) float red[4][kOutR];   // split-phase sums
     const int col_blocks = (V + kOutCols - 1) / kOutCols;
     const int h = blockIdx.x / col_blocks, c0 = (blockIdx.x % col_blocks) * kOutCols;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -540,29 +543,38 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
         #pragma unroll
         for (int q = 0; q < 8; ++q) wv[jr][q] = wr[16 * q];
     }
-    // 0c. the first splits of the partials of this thread's items (row idx / 64, columns
-    // 8 (idx % 64) .. +7, idx = tid, tid + 256)
+    // 0c. the first splits of the partials of this thread's merge unit: item (row, 8
+    // columns) it % items, splits q, q + qn, .. with q = it / items; qn = 4, 2, 1 split
+    // phases per item at M = 1, 2, >= 3 so that all 256 threads load, and at M > 4 a second
+    // item it + 256
+    const int items = M * 64;
+    const int qn = split ? max(1, min(4, 256 / items)) : 1;
+    const int q = tid / items;   // split phase of the thread's first unit (>= qn: no unit)
     bool live[2];
-    int imi[2];
+    int imi[2], ich[2];
     const float* ibase[2];
     v4f pa[2][kOutBatch][2];
     #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int idx = tid + 256 * j;
-        live[j] = split && idx < M * 64;
-        imi[j] = live[j] ? idx >> 6 : 0;
-        ibase[j] = o + (slot0(imi[j]) * kOutR + 8 * (idx & 63));
+        const int it = j == 0 ? tid % items : tid + 256;
+        live[j] = split && (j == 0 ? q < qn : it < items);
+        imi[j] = live[j] ? it >> 6 : 0;
+        ich[j] = 8 * (it & 63);
+        ibase[j] = o + (slot0(imi[j]) * kOutR + ich[j]);
     }
-    auto load_batch = [&](int s0) __attribute__((always_inline)) {
+    const int q0 = live[0] ? q : 0;   // the second item (M > 4) has qn = 1, phase 0
+    auto load_batch = [&](int k0) __attribute__((always_inline)) {
         #pragma unroll
         for (int j = 0; j < 2; ++j)
             #pragma unroll
-            for (int sb = 0; sb < kOutBatch; ++sb)
-                if (live[j] && s0 + sb < n_split) {
-                    const v4f* src = reinterpret_cast<const v4f*>(ibase[j] + (s0 + sb) * step * kOutR);
+            for (int sb = 0; sb < kOutBatch; ++sb) {
+                const int sp = (j == 0 ? q0 : 0) + qn * (k0 + sb);
+                if (live[j] && sp < n_split) {
+                    const v4f* src = reinterpret_cast<const v4f*>(ibase[j] + sp * step * kOutR);
                     pa[j][sb][0] = src[0];
                     pa[j][sb][1] = src[1];
                 }
+            }
     };
     load_batch(0);
 
@@ -580,31 +592,54 @@ __global__ void __launch_bounds__(256) out_small_kernel(const float* __restrict_
     }
     __syncthreads();
 
-    // 2. the merge, or the unsplit pass's ctx / row_sum
+    // 2. the merge (each unit's splits in order, the phases added in phase order), or the
+    // unsplit pass's ctx / row_sum
     if (split) {
         v4f a[2][2];
         #pragma unroll
         for (int j = 0; j < 2; ++j) a[j][0] = a[j][1] = v4f{0.f, 0.f, 0.f, 0.f};
-        for (int s0 = 0; s0 < n_split; s0 += kOutBatch) {
-            if (s0 > 0) load_batch(s0);
+        const int per = (n_split + qn - 1) / qn;   // splits of a unit, at most
+        for (int k0 = 0; k0 < per; k0 += kOutBatch) {
+            if (k0 > 0) load_batch(k0);
             #pragma unroll
             for (int j = 0; j < 2; ++j)
                 #pragma unroll
-                for (int sb = 0; sb < kOutBatch; ++sb)
-                    if (live[j] && s0 + sb < n_split) {
-                        const float w = wts[imi[j]][s0 + sb];
+                for (int sb = 0; sb < kOutBatch; ++sb) {
+                    const int sp = (j == 0 ? q0 : 0) + qn * (k0 + sb);
+                    if (live[j] && sp < n_split) {
+                        const float w = wts[imi[j]][sp];
                         a[j][0] += w * pa[j][sb][0];
                         a[j][1] += w * pa[j][sb][1];
                     }
+                }
         }
-        #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            if (live[j]) {
-                const int c = 8 * ((tid + 256 * j) & 63);
-                const float inv = invl[imi[j]];
-                *reinterpret_cast<v4f*>(&part[imi[j]][c]) = a[j][0] * inv;
-                *reinterpret_cast<v4f*>(&part[imi[j]][c + 4]) = a[j][1] * inv;
+        if (qn == 1) {
+            #pragma unroll
+            for (int j = 0; j < 2; ++j)
+                if (live[j]) {
+                    const float inv = invl[imi[j]];
+                    *reinterpret_cast<v4f*>(&part[imi[j]][ich[j]]) = a[j][0] * inv;
+                    *reinterpret_cast<v4f*>(&part[imi[j]][ich[j] + 4]) = a[j][1] * inv;
+                }
+        } else {
+            // phase sums through LDS (qn * M <= 4 rows of red), then added in phase order
+            if (live[0]) {
+                *reinterpret_cast<v4f*>(&red[q * M + imi[0]][ich[0]]) = a[0][0];
+                *reinterpret_cast<v4f*>(&red[q * M + imi[0]][ich[0] + 4]) = a[0][1];
             }
+            __syncthreads();
+            if (tid < items) {
+                const int mi = tid >> 6, c = 8 * (tid & 63);
+                v4f x0 = *reinterpret_cast<const v4f*>(&red[mi][c]);
+                v4f x1 = *reinterpret_cast<const v4f*>(&red[mi][c + 4]);
+                for (int qq = 1; qq < qn; ++qq) {
+                    x0 += *reinterpret_cast<const v4f*>(&red[qq * M + mi][c]);
+                    x1 += *reinterpret_cast<const v4f*>(&red[qq * M + mi][c + 4]);
+                }
+                *reinterpret_cast<v4f*>(&part[mi][c]) = x0 * invl[mi];
+                *reinterpret_cast<v4f*>(&part[mi][c + 4]) = x1 * invl[mi];
+            }
+        }
     } else {
         for (int mi = wave; mi < M; mi += 4) {
             const int64_t r = slot0(mi);
