@@ -284,6 +284,29 @@ def test_q_absorbed_small_batch_kernel(ext, monkeypatch, B, Sq, per_seq):
     torch.testing.assert_close(qr, rqr, **TOL)
 
 
+@pytest.mark.parametrize("split", [1, 8])
+def test_q_absorbed_small_batch_kernel_split_range(ext, monkeypatch, split):
+    """The small-batch 2b + 2c kernel after an unsplit 2a2 (it reads 2a2's output) and
+    after the most split partials it holds (8), 2a2's plan forced; against the two-launch
+    form and the oracle."""
+    B, Sq = 2, 1
+    inp = R.make_inputs(B, Sq, 4989, seed=70 + split)
+    W_uk, _ = R.split_wkv_b(inp["wkv_b"], D.nope)
+    args = [gpu(inp[k]) for k in ("x", "W_q_a", "q_norm_w", "W_q_b")] + [gpu(W_uk.contiguous()),
+                                                                        gpu(inp["positions"])]
+    shape = f"{B * Sq},{D.n_heads * D.qk_head},{D.q_lora},1"
+    monkeypatch.setenv("MLA_GEMM_PLAN", f"{shape}=32,128,{split}")
+    qa, qr = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    monkeypatch.setenv("MLA_Q_SMALL", "0")
+    qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    assert torch.equal(qr, qr0)
+    torch.testing.assert_close(qa, qa0, rtol=1e-5, atol=1e-5)
+    rqa, rqr = R.prepare_q_mla_absorbed(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
+                                        W_uk, inp["positions"], D.nope, D.rope)
+    torch.testing.assert_close(qa, rqa, **TOL)
+    torch.testing.assert_close(qr, rqr, **TOL)
+
+
 def test_layer_cfg2_full_size(ext):
     """Headline decode shape: B=128, Sq=1, Sk=4989, fp32, full DeepSeek-V3 dims; every
     sequence against the oracle at the north-star tolerance."""
