@@ -53,7 +53,8 @@ constexpr int kWLoadsA = kWAStage / 1024 / 4; // 1 KB loads per wave and slice: 
 struct WArgs {
     const uint16_t* A; int64_t lda, sAg;      // elements
     const uint16_t* B; int64_t ldb, sBg;
-    float* C; int64_t ldc, sCg;               // split == 1
+    float* C; int64_t ldc, sCg;               // split == 1: fp32 C, or with C16 set
+    uint16_t* C16;                            // C in the storage format (split == 1)
     float* ws; int64_t ws_split;              // split > 1: partials [split][G][M][N]
     int M, N, K, G, split, k_chunk, tiles_m, tiles_n;
     QUpEpilogue q;                            // the fused 2a2 epilogue (QUP kernels)
@@ -61,8 +62,9 @@ struct WArgs {
 
 constexpr int kQupNone = 0, kQupRope = 1, kQupAbsorb = 2;
 
-template <typename TL, int BN, int NS, int MINB, int QUP>
+template <typename TL, int BN, int NS, int MINB, int QUP, bool NT = false>
 __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
+    static_assert(!NT || QUP == kQupNone, "the fused epilogues read N-contiguous W");
     constexpr int kBRow = 2 * BN;                        // bytes per W row of a slice
     constexpr int kBStage = kWKS * kBRow;                // 16 KB / 8 KB
     constexpr int kStage = kWAStage + kBStage;
@@ -110,8 +112,8 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     // rows w*kLoadsB*kRowsPerLoadB .. of each slice (loads of kRowsPerLoadB rows)
     const uint32_t lds0 = lds_addr(smem);
     const uint64_t a_base = reinterpret_cast<uint64_t>(a.A + g * a.sAg + (int64_t)m0 * a.lda);
-    const uint64_t b_base =
-        reinterpret_cast<uint64_t>(a.B + g * a.sBg + (QUP == kQupAbsorb ? 0 : n0));
+    const uint64_t b_base = reinterpret_cast<uint64_t>(
+        a.B + g * a.sBg + (QUP == kQupAbsorb ? 0 : NT ? (int64_t)n0 * a.ldb : n0));
     uint32_t a_voff[kWLoadsA], b_voff[kLoadsB];
     #pragma unroll
     for (int q = 0; q < kWLoadsA; ++q) {
@@ -123,15 +125,21 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         const int r = (wave * kLoadsB + q) * kRowsPerLoadB + lane / (kBRow / 16);
         const int pos = lane % (kBRow / 16);
         const int sw = BN >= 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1);
-        if constexpr (QUP == kQupAbsorb)
+        if constexpr (NT) {
+            // NT: W row n (K-contiguous) staged like an A row: 8 rows x 128 bytes per load,
+            // chunk c of row n at c ^ ((n >> 1) & 7)
+            const int n = (BN / 4) * wave + 8 * q + (lane >> 3);
+            b_voff[q] = (uint32_t)n * (uint32_t)a.ldb * 2u + 16u * ((lane & 7) ^ ((n >> 1) & 7));
+        } else if constexpr (QUP == kQupAbsorb)
             b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 2u * (uint32_t)tile_col(8 * (pos ^ sw));
         else
             b_voff[q] = (uint32_t)r * (uint32_t)a.ldb * 2u + 16u * (pos ^ sw);
     }
     // valid bytes of a slice: A rows below rows_a, all 64 W rows (whole slices)
     const uint32_t a_bytes = (uint32_t)(rows_a - 1) * (uint32_t)a.lda * 2u + 128u;
-    const uint32_t b_bytes = (uint32_t)(kWKS - 1) * (uint32_t)a.ldb * 2u +
-                             (QUP == kQupAbsorb ? 2u * (uint32_t)a.N : (uint32_t)kBRow);
+    const uint32_t b_bytes = NT ? (uint32_t)(BN - 1) * (uint32_t)a.ldb * 2u + 128u
+                                : (uint32_t)(kWKS - 1) * (uint32_t)a.ldb * 2u +
+                                      (QUP == kQupAbsorb ? 2u * (uint32_t)a.N : (uint32_t)kBRow);
     // kQupAbsorb, nope tiles: W_uk[head0] (nope = 128 rows x kv, rows kv apart) in slices of
     // 64 rows x 128 columns in the W layout of a ring stage, pass p's two K halves kh.  Pass 0
     // goes into the table's space before the ring starts; pass p >= 1 takes the place of the
@@ -174,7 +182,8 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         const int k = k_begin + s * kWKS;
         const bool live = s < nsl;
         const v4i ra = rsrc_span(a_base + 2ull * (uint64_t)k, 0, live ? a_bytes : 0u);
-        const v4i rb = rsrc_span(b_base + 2ull * (uint64_t)k * (uint64_t)a.ldb, 0, live ? b_bytes : 0u);
+        const v4i rb = rsrc_span(b_base + 2ull * (uint64_t)k * (NT ? 1ull : (uint64_t)a.ldb), 0,
+                                 live ? b_bytes : 0u);
         #pragma unroll
         for (int q = 0; q < kWLoadsA; ++q)
             dma16(ra, __builtin_amdgcn_readfirstlane(st + (uint32_t)(32 * wave + 8 * q) * 128u),
@@ -182,7 +191,8 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         #pragma unroll
         for (int q = 0; q < kLoadsB; ++q)
             dma16(rb, __builtin_amdgcn_readfirstlane(
-                          st + kWAStage + (uint32_t)((wave * kLoadsB + q) * kRowsPerLoadB) * kBRow),
+                          NT ? st + kWAStage + (uint32_t)((BN / 4) * wave + 8 * q) * 128u
+                             : st + kWAStage + (uint32_t)((wave * kLoadsB + q) * kRowsPerLoadB) * kBRow),
                   b_voff[q], 0);
     };
 
@@ -198,20 +208,30 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
     // W fragment half p of column block cb, K step kt: lane 16G + 4q + i reads row
     // 16kt + 8(G/2) + 4p + q, columns (BN/2)wn + 32cb + 16(G%2) + 4i .. +3
     const int G = lane >> 4, q4 = (lane >> 2) & 3, i4 = lane & 3;
+    // (NT: W row n = (BN/2)wn + 32cb + l%32 is read like an A row, bytes 32kt + 16(l/32))
     uint32_t b_rd[CB];
     #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-        const int chunk = ((BN / 2) * wn + 32 * cb + 16 * (G & 1) + 4 * i4) / 8;
-        const int sw = BN >= 128 ? 4 * q4 : 4 * (q4 >> 1);
-        b_rd[cb] = kWAStage + (uint32_t)(8 * (G >> 1) + q4) * kBRow + 16u * (chunk ^ sw) + 8u * (i4 & 1);
+        if constexpr (NT) {
+            const int n = (BN / 2) * wn + 32 * cb + (lane & 31);
+            b_rd[cb] = kWAStage + (uint32_t)n * 128u + 16u * ((lane >> 5) ^ ((n >> 1) & 7));
+        } else {
+            const int chunk = ((BN / 2) * wn + 32 * cb + 16 * (G & 1) + 4 * i4) / 8;
+            const int sw = BN >= 128 ? 4 * q4 : 4 * (q4 >> 1);
+            b_rd[cb] = kWAStage + (uint32_t)(8 * (G >> 1) + q4) * kBRow + 16u * (chunk ^ sw) + 8u * (i4 & 1);
+        }
     }
     typedef short v4s __attribute__((ext_vector_type(4)));
     typedef __attribute__((address_space(3))) v4s lds_v4s;
     auto b_frag = [&](uint32_t st, int kt, int cb) __attribute__((always_inline)) {
-        const uint32_t o = st + b_rd[cb] + (uint32_t)(16 * kt) * kBRow;
-        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + o));
-        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + o + 4 * kBRow));
-        return __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        if constexpr (NT) {
+            return *reinterpret_cast<const v4u*>(smem + st + (b_rd[cb] ^ (32u * kt)));
+        } else {
+            const uint32_t o = st + b_rd[cb] + (uint32_t)(16 * kt) * kBRow;
+            const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + o));
+            const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4s*)(smem + o + 4 * kBRow));
+            return __builtin_bit_cast(v4u, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        }
     };
     auto a_frag = [&](uint32_t st, int kt, int rb) __attribute__((always_inline)) {
         // chunk 2kt + l/32 at (2kt + l/32) ^ s: a_rd holds (l/32) ^ s, and 2kt ^ s = 2kt ^
@@ -393,7 +413,26 @@ __global__ void __launch_bounds__(kWThreads, MINB) wgemm_kernel(WArgs a) {
         return;
     }
 
-    // ---- epilogue: fp32 C, or this split's partials
+    // ---- epilogue: fp32 C, C in the storage format, or this split's partials
+    if (a.C16) {   // split == 1; lane pairs (c, c ^ 1) swap values so each lane stores a dword
+        uint16_t* const c16 = a.C16 + (int64_t)g * a.sCg;
+        const bool odd = lane & 1;
+        #pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+            #pragma unroll
+            for (int cb = 0; cb < CB; ++cb) {
+                uint16_t* const dst = c16 + n0 + (BN / 2) * wn + 32 * cb + ((lane & 31) & ~1);
+                #pragma unroll
+                for (int e = 0; e < 16; e += 2) {
+                    const float x0 = acc[rb][cb][e], x1 = acc[rb][cb][e + 1];
+                    const float p0 = dpp_move<0xB1>(x0), p1 = dpp_move<0xB1>(x1);
+                    const int row = 64 * wm + 32 * rb + acc_row(odd ? e + 1 : e, lane);
+                    const uint32_t w = odd ? Half<TL>::pack2(p1, x1) : Half<TL>::pack2(x0, p0);
+                    if (row < rows_a) *reinterpret_cast<uint32_t*>(dst + (int64_t)(m0 + row) * a.ldc) = w;
+                }
+            }
+        return;
+    }
     float* out;
     int64_t ld;
     if (a.split > 1) {
@@ -446,21 +485,42 @@ hipError_t launch_wgemm_t(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 
     return hipGetLastError();
 }
 
+// NT (W rows K-contiguous): 128 or 64 columns, 3 or 4 stages, no fused epilogue.
+template <typename TL>
+hipError_t launch_wgemm_nt(const WArgs& a, const GemmPlan& plan, dim3 grid, dim3 block,
+                           hipStream_t stream) {
+    if (plan.bn == 128 && plan.stages == 4)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 4, 1, kQupNone, true>), grid, block, 0, stream, a);
+    else if (plan.bn == 128 && plan.stages == 3)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 128, 3, 1, kQupNone, true>), grid, block, 0, stream, a);
+    else if (plan.bn == 64 && plan.stages == 4)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 4, 1, kQupNone, true>), grid, block, 0, stream, a);
+    else if (plan.bn == 64 && plan.stages == 3)
+        hipLaunchKernelGGL((wgemm_kernel<TL, 64, 3, 2, kQupNone, true>), grid, block, 0, stream, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
 }  // namespace
 
 bool wgemm_supported(const GemmProblem& p, int bn, int split) {
-    return p.half && !p.a_f32 && !p.b_nt && p.amode == kAPlain &&
-           (p.out_type == kOutF32 || split > 1) && split >= 1 &&
-           !p.k_len && !p.b_pages && (bn == 64 || bn == 128 || bn == 256) && p.N % bn == 0 &&
-           p.K % kWKS == 0 && p.lda >= kWKS && p.ldb >= bn && p.M > 0 && p.G == 1 &&
-           // 16-byte aligned rows and groups for the 16-byte loads
+    const OutType own16 = p.f16 ? kOutF16 : kOutBF16;
+    return p.half && !p.a_f32 && p.amode == kAPlain &&
+           (p.out_type == kOutF32 || split > 1 || p.out_type == own16) && split >= 1 &&
+           !p.k_len && !p.b_pages && (bn == 64 || bn == 128 || (bn == 256 && !p.b_nt)) &&
+           p.N % bn == 0 && p.K % kWKS == 0 && p.lda >= kWKS &&
+           (p.b_nt ? p.ldb >= p.K : p.ldb >= bn) && p.M > 0 && p.G >= 1 &&
+           // 16-byte aligned rows and groups for the 16-byte loads; 4-byte 16-bit C rows
            p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sAg % 8 == 0 && p.sBg % 8 == 0 &&
-           // 32-bit buffer offsets within a tile: 128 A rows, 64 W rows
-           (int64_t)kWBM * p.lda * 2 < kRsrcRange && (int64_t)kWKS * p.ldb * 2 < kRsrcRange;
+           (p.out_type == kOutF32 || split > 1 || (p.ldc % 2 == 0 && p.sCg % 2 == 0)) &&
+           // 32-bit buffer offsets within a tile: 128 A rows, 64 W rows (NT: bn W rows)
+           (int64_t)kWBM * p.lda * 2 < kRsrcRange &&
+           (int64_t)(p.b_nt ? bn : kWKS) * p.ldb * 2 < kRsrcRange;
 }
 
 bool qup_supported(const GemmProblem& p, const QUpEpilogue& q, const GemmPlan& plan) {
-    const bool rope_ok = p.half && p.G == 1 && q.H > 0 && q.nope > 0 && q.nope % 32 == 0 &&
+    const bool rope_ok = p.half && p.G == 1 && !p.b_nt && p.out_type == kOutF32 && q.H > 0 && q.nope > 0 && q.nope % 32 == 0 &&
                          q.rope > 0 && q.rope % 32 == 0 && q.rope <= 64 &&
                          (int64_t)p.N == (int64_t)q.H * (q.nope + q.rope) && q.q_rope && q.cos_sin;
     if (!q.w_uk) return rope_ok && q.q_nope;
@@ -473,7 +533,8 @@ bool qup_supported(const GemmProblem& p, const QUpEpilogue& q, const GemmPlan& p
 }
 
 bool wgemm_aligned(const GemmProblem& p) {
-    return (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0;
+    return (reinterpret_cast<uintptr_t>(p.A) & 15) == 0 && (reinterpret_cast<uintptr_t>(p.B) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(p.C) & 3) == 0;
 }
 
 hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* partials,
@@ -484,7 +545,9 @@ hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* parti
     WArgs a;
     a.A = static_cast<const uint16_t*>(p.A); a.lda = p.lda; a.sAg = p.sAg;
     a.B = static_cast<const uint16_t*>(p.B); a.ldb = p.ldb; a.sBg = p.sBg;
-    a.C = static_cast<float*>(p.C); a.ldc = p.ldc; a.sCg = p.sCg;
+    const bool c16 = p.out_type != kOutF32 && plan.split == 1;
+    a.C = c16 ? nullptr : static_cast<float*>(p.C); a.ldc = p.ldc; a.sCg = p.sCg;
+    a.C16 = c16 ? static_cast<uint16_t*>(p.C) : nullptr;
     a.ws = partials; a.ws_split = (int64_t)p.G * p.M * p.N;
     a.M = p.M; a.N = p.N; a.K = p.K; a.G = p.G;
     a.split = plan.split; a.k_chunk = plan.k_chunk;
@@ -503,6 +566,10 @@ hipError_t launch_wgemm(const GemmProblem& p, const GemmPlan& plan, float* parti
         }
         if (p.f16) return launch_wgemm_t<f16_t, kQupRope>(a, plan, grid, block, stream);
         return launch_wgemm_t<bf16_t, kQupRope>(a, plan, grid, block, stream);
+    }
+    if (p.b_nt) {
+        if (p.f16) return launch_wgemm_nt<f16_t>(a, plan, grid, block, stream);
+        return launch_wgemm_nt<bf16_t>(a, plan, grid, block, stream);
     }
     if (p.f16) return launch_wgemm_t<f16_t, kQupNone>(a, plan, grid, block, stream);
     return launch_wgemm_t<bf16_t, kQupNone>(a, plan, grid, block, stream);

@@ -200,3 +200,28 @@ def test_layer_bf16_cfg4_full_size(ext):
     ref = R.mla_layer(f32["x"], f32["W_q_a"], f32["q_norm_w"], f32["W_q_b"], f32["wkv_b"],
                       f32["c_kv"], f32["pe_cache"], f32["positions"])
     torch.testing.assert_close(out.float().cpu(), ref, **C.tol(BF, ref))
+
+
+@pytest.mark.parametrize("dt", [BF, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("B,Sk,plan", [(128, 1000, None), (130, 300, "128,1,4"),
+                                       (128, 700, "64,1,3"), (40, 64, "64,1,4")])
+def test_out_projection_3d_weight_streaming(ext, monkeypatch, dt, B, Sk, plan):
+    """3d from the pass's normalised 16-bit ctx on the weight-streaming engine's NT tiles
+    (W_uv rows K-contiguous, G = heads, the output rounded in its epilogue): the same bits
+    as the tiled engine (MLA_WGEMM=0), over one and two row tiles and a partial one, and
+    the oracle's result at the 16-bit tolerance."""
+    g = torch.Generator().manual_seed(B + Sk)
+    mk = lambda *s, sc=1.0: (torch.randn(*s, generator=g) * sc).to(dt)  # noqa: E731
+    qa, qr = mk(B, 1, D.n_heads, D.kv_rank, sc=0.05), mk(B, 1, D.n_heads, D.rope, sc=0.05)
+    ck, pe = mk(B, Sk, D.kv_rank), mk(B, Sk, D.rope)
+    wuv = mk(D.n_heads, D.v, D.kv_rank, sc=1 / math.sqrt(D.kv_rank))
+    if plan:
+        monkeypatch.setenv("MLA_WGEMM_PLAN", f"{B},{D.v},{D.kv_rank},{D.n_heads}={plan}")
+    args = [gpu(t) for t in (qa, qr, ck, pe, wuv)]
+    got = ext.mla_attention(*args, SCALE).cpu()
+    monkeypatch.setenv("MLA_WGEMM", "0")
+    tiled = ext.mla_attention(*args, SCALE).cpu()
+    assert got.dtype == dt and torch.equal(got, tiled)
+    f = lambda t: t.float()  # noqa: E731
+    ref = R.mla_attention_official(f(qa), f(qr), f(ck), f(pe), f(wuv), SCALE)
+    torch.testing.assert_close(got.float(), ref, **C.tol(dt, ref))
