@@ -1,8 +1,9 @@
 // Weight-streaming GEMM for the 16-bit (bf16 / fp16) products whose A operand is a small
 // batch of activation rows (M <= 128 per tile) and whose B operand is a weight matrix
-// streamed once from HBM: 2a1 (x @ W_q_a) and 2a2 (q_lat @ W_q_b) of the Q path and the
-// output projection beside the layer; NN, one group, fp32 output or split-K partials, and
-// for 2a2 the fused epilogue that also does 2b.  It replaces gemm_kernel for those shapes
+// streamed once from HBM: 2a1 (x @ W_q_a) and 2a2 (q_lat @ W_q_b) of the Q path, 3d from
+// the fused pass's 16-bit ctx (NT, G = heads) and the output projection beside the layer;
+// fp32 output, output in the storage format or split-K partials, and for 2a2 the fused
+// epilogues that also do 2b and 2c.  It replaces gemm_kernel for those shapes
 // (gemm.hip: plan_gemm picks it), whose staging round-trips every operand byte through
 // registers and transposes the N-contiguous weights on the way into LDS.
 //
@@ -14,7 +15,8 @@
 //   W: 64 rows x 2*BN bytes per slice, N-contiguous as in memory, read back as the MFMA's
 //      K-contiguous B fragments with the transposing ds_read_b64_tr_b16 (two per fragment:
 //      within each 16-lane group lanes 4q .. 4q+3 address row q and lane j receives
-//      column j of the four rows).
+//      column j of the four rows); NT (W rows K-contiguous): BN rows x 128 bytes per slice,
+//      staged and read exactly like A.
 // NS - 1 slices are in flight while one feeds the MFMAs, and one barrier per slice orders
 // the ring.  Chunk permutations keep every LDS read free of bank conflicts: 16-byte chunk c
 // of A row r sits at c ^ ((r >> 1) & 7), and chunk c of W row r at c ^ (4 (r & 3)) for
