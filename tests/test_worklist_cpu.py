@@ -113,3 +113,20 @@ def test_checker_rejects_broken_lists():
         W.check_list(doubled, lens, SK_FULL, 16, mi)
     with pytest.raises(AssertionError):
         W.check_list(wl, lens, SK_FULL, 16, int(wl[0]) // 8 * 8 - 8 if wl[0] > 8 else 0)
+
+
+def test_dense_splits_fit_one_round_of_cus():
+    """Below one workgroup per CU the dense plan takes as many key splits as fit one round:
+    base x splits never passes the 256 CUs (a split count rounded to nearest once gave
+    B=5, Sk=4989 260 workgroups of one per CU, and the second round's four nearly doubled
+    the pass)."""
+    lib = W.harness()
+    for bk in (16, 32):
+        for base in range(1, 256):
+            for Sk in (1, 16, 64, 300, 512, 1000, 4989, 8192, 32768):
+                kps = lib.wl_harness_dense_keys(Sk, base, bk)
+                blocks = -(-Sk // bk)
+                n_split = -(-blocks // (kps // bk))
+                assert kps % bk == 0 and kps >= bk
+                assert base * n_split <= 256, (bk, base, Sk, n_split)
+                assert n_split <= max(1, 256 // base), (bk, base, Sk, n_split)
