@@ -191,7 +191,7 @@ def in_layer_kernel_us(layer, flush, n):
     kernels attributed to steps by launch order -- the layer launches its GEMMs in the order
     2a1, 2a2, 2c, 3d, a split-K reduce right after its GEMM, RMSNorm (2a-n, which also sums
     2a1's split partials) and RoPE (2b) between them (the 16-bit 2a2 may do 2b and 2c in its
-    epilogue: `wgemm_kernel<.., 2>`, counted as 2a2; at decode-sized fp32 batches
+    epilogue: `wgemm_kernel<.., 2, false>`, counted as 2a2; at decode-sized fp32 batches
     `q_small_kernel` does 2b and 2c, counted as 2c), and the fused attention's kernels
     (work list, pass, merge) as 3abc; at decode-sized fp32 batches 3d may be
     out_small_kernel, which also does the pass's split merge.  Returns {step: mean µs per
@@ -231,7 +231,7 @@ def in_layer_kernel_us(layer, flush, n):
         if "gemm_kernel" in name:
             step = gemm_steps[min(cur["gemm"], 3)]
             cur["gemm"] += 1
-            if "wgemm_kernel" in name and re.search(r",\s*2>", name):
+            if "wgemm_kernel" in name and re.search(r",\s*2(,\s*(false|true))?>", name):
                 cur["gemm"] += 1      # 2a2 with 2b and 2c in its epilogue: no 2c launch
                 folded["2a2"] = ("2b", "2c")
         elif "split_reduce" in name:
