@@ -464,7 +464,7 @@ def measure(args, ext, dev, neighbours=True, light=False):
     # each step's kernel time inside the flushed layer (GPU timestamps, no events between
     # the steps), for the fused path
     in_layer = None
-    if (os.environ.get("MLA_ATTENTION_PATH") != "split" and not fp8kv):
+    if os.environ.get("MLA_ATTENTION_PATH") != "split":
         try:
             in_layer = in_layer_kernel_us(layer, flush, min(10, args.steps))
         except Exception as e:   # the profiler is a measurement aid, not the product
@@ -546,7 +546,13 @@ def measure(args, ext, dev, neighbours=True, light=False):
     # decomposed kernels
     fused_attn = (dims.kv_rank == 512 and dims.rope == 64
                   and os.environ.get("MLA_ATTENTION_PATH") != "split")
-    if fused_attn:
+    if fused_attn and fp8kv:
+        # the fp8-cache pass has no entry point of its own: its time is the in-layer kernel
+        # time of the layer's pass (GPU timestamps), when the profiler gave one
+        if in_layer and "3abc" in in_layer:
+            step_us["3abc"] = in_layer["3abc"]
+            names = names + ["3abc"]
+    elif fused_attn:
         qa_f, qr_f = ext.q_absorbed(g["x"], g["W_q_a"], g["q_norm_w"], g["W_q_b"], W_uk_d,
                                     g["positions"], dims.nope, dims.rope, eps)
         for _ in range(2):
@@ -563,6 +569,13 @@ def measure(args, ext, dev, neighbours=True, light=False):
         names = names + ["3abc"]
 
     work = step_work(B, Sq, Sk, dims, e=2 if half else 4, causal=causal)
+    if fp8kv:
+        # the fp8-cache pass: bf16 queries, one byte per cache element, the normalised bf16
+        # ctx written once (3d reads it)
+        flat = B * Sq * dims.n_heads
+        width = dims.kv_rank + dims.rope
+        work["3abc"] = (work["3abc"][0],
+                        2 * flat * width + B * Sk * width + 2 * flat * dims.kv_rank)
     peak_mfma = PEAK_BF16 if half else PEAK_F32   # the fp16 MFMA peak equals the bf16 one
     per_step = {}
     for n in names:
@@ -575,8 +588,11 @@ def measure(args, ext, dev, neighbours=True, light=False):
                        "hbm_pct": round(100 * by / t / PEAK_HBM, 1)}
     dom = "3abc" if fused_attn else max(("3a", "3c"), key=lambda n: step_us[n])
     fl, by = work[dom]
-    t_dom = step_us[dom] * 1e-6
-    if fl / by > peak_mfma / PEAK_HBM:   # above the ridge: compute-bound
+    t_dom = step_us[dom] * 1e-6 if dom in step_us else None
+    if t_dom is None:
+        roofline = {"kernel": dom, "bound": None, "achieved": None, "peak": None,
+                    "unit": None, "frac": None}
+    elif fl / by > peak_mfma / PEAK_HBM:   # above the ridge: compute-bound
         achieved = fl / t_dom / 1e12
         roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                     "peak": peak_mfma / 1e12, "unit": "TFLOP/s",
@@ -590,12 +606,14 @@ def measure(args, ext, dev, neighbours=True, light=False):
     try:
         with open(args.traffic) as f:
             tr = json.load(f)
-        key = f"{args.config}/{dname}/{dom}"
+        key = f"{args.config}/{dname}{'-fp8kv' if fp8kv else ''}/{dom}"
         if key in tr.get("kernels", {}):
             traffic = tr["kernels"][key]["hbm_bytes_per_launch"]
     except (OSError, ValueError):
         traffic = None
     roofline.update({"traffic": traffic, "algorithmic_flop": fl, "algorithmic_bytes": by})
+    if fp8kv:
+        roofline["timing"] = "the pass's kernel time inside the layer (GPU timestamps)"
 
     in_layer_steps = None
     fused_steps = ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d")
@@ -1000,6 +1018,16 @@ def main():
         for k in ("steps_in_layer_us", "dominant_in_layer", "layer_bound_us",
                   "layer_roofline_frac"):
             rec["bf16_cfg4"][k] = r4[k]
+        # the same layer with the cache held as fp8 E4M3 codes (one per-tensor scale): the
+        # cache-format neighbour of the path, its layer time and fused-pass roofline
+        a8 = argparse.Namespace(**vars(a4))
+        a8.kv_cache = "fp8"
+        a8.settle = min(args.settle, 1.0)
+        r8 = measure(a8, ext, dev, neighbours=False, light=True)
+        rec["fp8kv_cfg4"] = {k: r8[k] for k in ("value", "unit", "median_us_per_step",
+                                                "back_to_back_us_per_step", "dtype", "kv_cache",
+                                                "config", "roofline", "steps_in_layer_us",
+                                                "dominant_in_layer")}
     if args.config == "cfg2" and (args.dtype or "f32") == "f32" and not args.no_other_configs:
         # every other BASELINE configuration, fp32, timed the same way (flushed layers after
         # a settle), with its in-layer kernel times, its fused attention's roofline and the
