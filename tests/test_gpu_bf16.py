@@ -225,3 +225,23 @@ def test_out_projection_3d_weight_streaming(ext, monkeypatch, dt, B, Sk, plan):
     f = lambda t: t.float()  # noqa: E731
     ref = R.mla_attention_official(f(qa), f(qr), f(ck), f(pe), f(wuv), SCALE)
     torch.testing.assert_close(got.float(), ref, **C.tol(dt, ref))
+
+
+@pytest.mark.parametrize("dt", [BF, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("B,plan", [(128, "128,1,4"), (130, "64,1,3"), (40, "128,1,3")])
+def test_absorb_on_weight_streaming_groups(ext, monkeypatch, dt, B, plan):
+    """2c as its own launch from 2a2's 16-bit q_nope (2a2's plan forced to the fused
+    epilogue, MLA_QUP_ABSORB=0) forced onto the weight-streaming engine: NN tiles over
+    G = heads groups with the output in the storage format give the same bits as the tiled
+    engine's 2c, over one, two and a partial row tile."""
+    inp = R.make_inputs(B, 1, 64, seed=B, dtype=dt)
+    W_uk, _ = R.split_wkv_b(inp["wkv_b"], D.nope)
+    args = [gpu(inp[k]) for k in ("x", "W_q_a", "q_norm_w", "W_q_b")] + [gpu(W_uk.contiguous()),
+                                                                        gpu(inp["positions"])]
+    monkeypatch.setenv("MLA_QUP_ABSORB", "0")
+    up = f"{B},{D.n_heads * D.qk_head},{D.q_lora},1=128,1"   # 2a2 fused: 16-bit q_nope
+    monkeypatch.setenv("MLA_WGEMM_PLAN", f"{up};{B},{D.kv_rank},{D.nope},{D.n_heads}={plan}")
+    qa, qr = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    monkeypatch.setenv("MLA_WGEMM_PLAN", up)
+    qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    assert torch.equal(qa, qa0) and torch.equal(qr, qr0)
