@@ -294,6 +294,7 @@ struct QLayout {
     GemmPlan down, up, absorb;
     bool fused;   // 2a2 writes q_nope and the rotated q_rope itself (no 2b launch)
     bool fused_2c;  // ... and 2c too (no 2c launch, no q_nope), when the pointers allow
+    bool rope_epi;  // fp32: 2a2 on the tiled engine rotates q_rope in its epilogue (no 2b)
     size_t off_lat_acc, off_lat, off_raw, off_up_ws, off_abs_ws, off_rope_tab, total;
 };
 
@@ -331,6 +332,21 @@ bool q_small_ok(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up, const v
            (reinterpret_cast<uintptr_t>(q_rope) & 7) == 0;
 }
 
+// fp32 2a2 in one K split on the tiled engine does 2b in its epilogue (gemm.hip, ROPE
+// kernels), on tiles whose waves hold one 32x32 block each (64x64, 32x128, 128x32).  With
+// more blocks per wave, a later block's cos / sin loads queue behind the earlier block's
+// stores on the one memory counter: M = 512 on 128x128 tiles measured 563 us against
+// 487 us with the RoPE launch, while B = 128 on 64x64 tiles gains ~3 us.
+// MLA_ROPE_EPI=0 keeps the RoPE launch (a comparison aid: both give the same bits).
+bool rope_epi_ok(mla_dtype_t dt, const mla_dims_t* d, const GemmPlan& up) {
+    const char* env = getenv("MLA_ROPE_EPI");
+    if (env && strcmp(env, "0") == 0) return false;
+    const bool one_block = (up.bm == 64 && up.bn == 64) || (up.bm == 32 && up.bn == 128) ||
+                           (up.bm == 128 && up.bn == 32);
+    return dt == MLA_DTYPE_F32 && !up.wgemm && up.split == 1 && up.tiles_per_wg == 1 &&
+           one_block && d->nope % 32 == 0 && d->rope % 32 == 0 && d->rope / 2 <= 256;
+}
+
 QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     QLayout L;
     const size_t bq = (size_t)d->batch * d->sq;
@@ -339,6 +355,7 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     L.up = plan_gemm(q_up_problem(dt, d, nullptr, nullptr, nullptr));
     L.fused = qup_fused(dt, d, L.up);
     L.fused_2c = L.fused && qup_fused_2c(dt, d, L.up);
+    L.rope_epi = rope_epi_ok(dt, d, L.up);
     L.absorb = plan_gemm(absorb_problem(dt, d, nullptr, nullptr, nullptr, L.fused));
     size_t o = 0;
     L.off_lat_acc = o;  // 2a1 output or its split partials (summed by the norm kernel)
@@ -352,7 +369,7 @@ QLayout q_layout(mla_dtype_t dt, const mla_dims_t* d) {
     L.off_abs_ws = o;
     o = align_up(o + L.absorb.workspace_bytes);
     L.off_rope_tab = o;   // 2a-n's RoPE angle table for the fused epilogue
-    if (L.fused) o = align_up(o + bq * (size_t)d->rope * sizeof(float));
+    if (L.fused || L.rope_epi) o = align_up(o + bq * (size_t)d->rope * sizeof(float));
     L.total = o;
     return L;
 }
@@ -646,9 +663,11 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
     } else {
         MLA_TRY_HIP(launch_gemm(down, down_plan, nullptr, stream), "2a1 launch");
     }
-    // 2a-n (with the fused epilogue, also the rows' RoPE cos / sin table)
+    // 2a-n (with a fused 2b, also the rows' RoPE cos / sin table)
+    const bool small = q_small_ok(dtype, dims, L.up, W_uk, q_absorbed, q_rope);
+    const bool rope_epi = L.rope_epi && !small;
     RopeTable rt;
-    if (L.fused) {
+    if (L.fused || rope_epi) {
         rt.cos_sin = at<float>(workspace, L.off_rope_tab);
         rt.positions = positions; rt.inv_freq = inv_freq; rt.half = dims->rope / 2;
         rt.Sq = dims->sq; rt.per_batch = pos_per_batch;
@@ -680,7 +699,6 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
                     "2c launch");
         return ok();
     }
-    const bool small = q_small_ok(dtype, dims, L.up, W_uk, q_absorbed, q_rope);
     if (L.up.split > 1) {
         float* up_parts = at<float>(workspace, L.off_up_ws);
         MLA_TRY_HIP(launch_gemm_partials(up, L.up, up_parts, stream), "2a2 launch");
@@ -700,6 +718,13 @@ int q_absorbed_impl(mla_dtype_t dtype, const mla_dims_t* dims, const void* x, co
                                 stream, pos_per_batch, L.up.split,
                                 (int64_t)bq * dims->heads * (dims->nope + dims->rope), raw),
                     "2b launch");
+    } else if (rope_epi) {
+        QUpEpilogue re;
+        re.q_rope = q_rope; re.cos_sin = rt.cos_sin;
+        re.H = dims->heads; re.nope = dims->nope; re.rope = dims->rope;
+        up.rope_epi = &re;
+        MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream),
+                    "2a2 + 2b launch");
     } else {
         MLA_TRY_HIP(launch_gemm(up, L.up, at<void>(workspace, L.off_up_ws), stream), "2a2 launch");
         if (small) {

@@ -50,6 +50,10 @@ struct GemmArgs {
     const float* alpha; int alpha_ld, alpha_shift;   // alpha column of k: k >> alpha_shift
     const int* k_len;                                  // per-group K limit (optional)
     const int* b_pages; int page_size, max_pages;      // paged NN B (PAGED kernels)
+    // ROPE kernels (fp32 2a2 with 2b in its epilogue): the rope columns of every head go
+    // rotated to rope_out [M][H][rope] instead of C, with row m's pair i at
+    // rope_cs[2 (m * rope/2 + i)] (cos) and the sin after it
+    float* rope_out; const float* rope_cs; int rope_H, rope_nope, rope_rope;
 };
 
 template <typename TL, int BN>
@@ -74,8 +78,11 @@ constexpr int nn_row_words() {
 // products (2c: K = 128, four slices) otherwise spend about a third of a tile in the
 // unoverlapped fill and epilogue.  Full tiles only, plain A, no per-group K limit or
 // paging (the launcher checks).
+// ROPE: fp32 C of 2a2 whose 32-column blocks in a head's rope part are rotated (2b) and
+// written to rope_out instead (the pair partner of column c is column c ^ 1, the
+// neighbouring lane), with the arithmetic of rope_kernel, so the bits are the same.
 template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT,
-          bool PAGED = false, bool PERSIST = false>
+          bool PAGED = false, bool PERSIST = false, bool ROPE = false>
 __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
     constexpr int PD = 2;
     using MM = Mma<TL>;
@@ -342,6 +349,40 @@ __global__ void __launch_bounds__(kThreads, 2) gemm_kernel(GemmArgs a) {
             for (int j = 0; j < TN; ++j) {
                 const int c = wn * WTN + j * 32 + l32;              // tile column
                 const int r0 = wm * WTM + i * 32 + 4 * half;          // tile row of e = 0
+                if constexpr (ROPE) {
+                    // a block of a head's rope part (uniform over the wave): rotate
+                    const int qk = a.rope_nope + a.rope_rope;
+                    const int c0 = n0_ + wn * WTN + j * 32;
+                    const int hh = c0 / qk, j0 = c0 - hh * qk;
+                    if (c0 < a.N && j0 >= a.rope_nope) {
+                        const int half_r = a.rope_rope >> 1;
+                        const int rc = j0 - a.rope_nope + l32;     // rope column of the head
+                        const int pi = rc >> 1;
+                        float* dst = a.rope_out + (int64_t)hh * a.rope_rope + rc;
+                        const int64_t ld_r = (int64_t)a.rope_H * a.rope_rope;
+                        // all 16 rows' (cos, sin) loads first, then the rotations and stores
+                        // (a load after a store to rope_out would wait for it)
+                        typedef float v2f_t __attribute__((ext_vector_type(2)));
+                        v2f_t cs[16];
+                        #pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const int row = min(m0_ + r0 + 8 * (e >> 2) + (e & 3), a.M - 1);
+                            cs[e] = *reinterpret_cast<const v2f_t*>(
+                                a.rope_cs + 2 * ((int64_t)row * half_r + pi));
+                        }
+                        #pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const float own = acc[i][j][e];
+                            const float other = dpp_move<0xB1>(own);   // lane ^ 1
+                            const int row = m0_ + r0 + 8 * (e >> 2) + (e & 3);
+                            if (row < a.M)
+                                dst[(int64_t)row * ld_r] =
+                                    (l32 & 1) ? rope_odd(other, own, cs[e][0], cs[e][1])
+                                              : rope_even(own, other, cs[e][0], cs[e][1]);
+                        }
+                        continue;
+                    }
+                }
                 const uint32_t lane_off =
                     (uint32_t)((r0 * ld + c) * esz) | oob_mask(n0_ + c, a.N);
                 #pragma unroll
@@ -483,19 +524,19 @@ __global__ void __launch_bounds__(256) split_reduce_kernel(const float* __restri
 }
 
 template <typename TL, typename TA, int BM, int BN, int WM, int WN, bool NT, int AMODE, int OUT,
-          bool PAGED, bool PERSIST>
+          bool PAGED, bool PERSIST, bool ROPE>
 hipError_t launch_cfg(const GemmArgs& args, int nblocks, hipStream_t stream) {
-    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT, PAGED, PERSIST>),
+    hipLaunchKernelGGL((gemm_kernel<TL, TA, BM, BN, WM, WN, NT, AMODE, OUT, PAGED, PERSIST, ROPE>),
                        dim3(nblocks), dim3(kThreads), 0, stream, args);
     return hipGetLastError();
 }
 
 template <typename TL, typename TA, bool NT, int AMODE, int OUT, bool PAGED = false,
-          bool PERSIST = false>
+          bool PERSIST = false, bool ROPE = false>
 hipError_t launch_tiles(const GemmArgs& args, int bm, int bn, int nblocks, hipStream_t stream) {
 #define MLA_TILE(BM_, BN_, WM_, WN_)                                                       \
     if (bm == BM_ && bn == BN_)                                                             \
-        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT, PAGED, PERSIST>(       \
+        return launch_cfg<TL, TA, BM_, BN_, WM_, WN_, NT, AMODE, OUT, PAGED, PERSIST, ROPE>( \
             args, nblocks, stream);
     MLA_TILE(128, 128, 2, 2)
     MLA_TILE(128, 96, 4, 1)
@@ -568,6 +609,11 @@ hipError_t dispatch(const GemmProblem& p, const GemmArgs& a, int bm, int bn, int
     if (p.b_pages) {   // paged NN B: 3c over a paged cache only
         if (p.b_nt || p.amode != kAAlpha || !f32_out) return hipErrorInvalidValue;
         return launch_tiles<float, float, false, kAAlpha, kOutF32, true>(a, bm, bn, nblocks, stream);
+    }
+    if (!p.b_nt && p.amode == kAPlain && f32_out && a.rope_out) {
+        if (split) return hipErrorInvalidValue;
+        return launch_tiles<float, float, false, kAPlain, kOutF32, false, false, true>(
+            a, bm, bn, nblocks, stream);
     }
     if (!p.b_nt && p.amode == kAPlain && f32_out)
         return launch_tiles<float, float, false, kAPlain, kOutF32>(a, bm, bn, nblocks, stream);
@@ -822,6 +868,19 @@ hipError_t launch_gemm_impl(const GemmProblem& p, const GemmPlan& plan, void* wo
     a.rs = p.rs; a.rs_m = p.rs_m; a.rs_g = p.rs_g;
     a.alpha = p.alpha; a.alpha_ld = p.alpha_ld;
     a.k_len = p.k_len; a.b_pages = p.b_pages; a.page_size = p.page_size; a.max_pages = p.max_pages;
+    a.rope_out = nullptr; a.rope_cs = nullptr; a.rope_H = a.rope_nope = a.rope_rope = 0;
+    if (p.rope_epi) {
+        // fp32 2a2 with 2b in its epilogue: one K split, plain NN, fp32 C, every 32-column
+        // block inside one head's nope or rope part
+        const QUpEpilogue& q = *p.rope_epi;
+        if (p.half || plan.wgemm || plan.split != 1 || plan.tiles_per_wg > 1 || p.b_nt ||
+            p.amode != kAPlain || p.out_type != kOutF32 || p.G != 1 || !q.q_rope ||
+            !q.cos_sin || q.H <= 0 || q.nope <= 0 || q.nope % 32 != 0 || q.rope <= 0 ||
+            q.rope % 32 != 0 || (int64_t)p.N != (int64_t)q.H * (q.nope + q.rope))
+            return hipErrorInvalidValue;
+        a.rope_out = static_cast<float*>(q.q_rope); a.rope_cs = q.cos_sin;
+        a.rope_H = q.H; a.rope_nope = q.nope; a.rope_rope = q.rope;
+    }
     if (p.b_pages && (p.page_size <= 0 || p.page_size % 64 != 0 ||
                       (int64_t)p.max_pages * p.page_size < p.K))
         return hipErrorInvalidValue;

@@ -69,6 +69,9 @@ struct GemmProblem {
     const int* b_pages = nullptr;
     int page_size = 0, max_pages = 0;
     const QUpEpilogue* qup = nullptr;   // weight-streaming plans only (launch_wgemm)
+    // fp32 tiled plans with one K split: 2b in 2a2's epilogue (q_rope, cos_sin, H, nope,
+    // rope of the struct; the nope columns still go to C)
+    const QUpEpilogue* rope_epi = nullptr;
 };
 
 // Tile/split plan chosen for a problem (pure function of the shape; see plan_gemm).

@@ -362,3 +362,32 @@ def test_reference_input_convention(ext):
     _, _, rout = oracle_layer_rows(inp, list(range(64)))
     torch.testing.assert_close(out.cpu(), rout, rtol=3e-2, atol=3e-2)
     torch.testing.assert_close(out.cpu(), rout, **TOL)
+
+
+@pytest.mark.parametrize("B,Sq,per_seq,plan", [
+    (128, 1, False, None), (130, 1, True, "64,64"), (4, 33, False, "32,128"),
+    (4, 128, False, "64,64"), (3, 40, True, "128,32")])
+def test_q_absorbed_rope_in_2a2_epilogue(ext, monkeypatch, B, Sq, per_seq, plan):
+    """fp32 batches whose 2a2 runs in one K split on tiles of one 32x32 block per wave rotate
+    q_rope in 2a2's epilogue (no 2b launch): q_rope and q_absorbed are the same bits as with
+    the RoPE launch (MLA_ROPE_EPI=0), and match the oracle; each such tile (forced where the
+    planner picks another), full and partial row tiles, positions shared or per sequence."""
+    if plan:
+        monkeypatch.setenv("MLA_GEMM_PLAN", f"{B * Sq},{D.n_heads * D.qk_head},{D.q_lora},1="
+                                            f"{plan},1")
+    inp = R.make_inputs(B, Sq, 4989, seed=B + 7 * Sq)
+    W_uk, _ = R.split_wkv_b(inp["wkv_b"], D.nope)
+    pos = inp["positions"]
+    if per_seq:
+        pos = torch.tensor([[4988 - 31 * b - Sq + 1 + s for s in range(Sq)] for b in range(B)])
+    args = [gpu(inp[k]) for k in ("x", "W_q_a", "q_norm_w", "W_q_b")] + [gpu(W_uk.contiguous()),
+                                                                        gpu(pos)]
+    qa, qr = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    monkeypatch.setenv("MLA_ROPE_EPI", "0")
+    qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, D.nope, D.rope, 1e-6))
+    assert torch.equal(qr, qr0) and torch.equal(qa, qa0)
+    prep = R.prepare_q_ragged if per_seq else R.prepare_q_mla_absorbed
+    rqa, rqr = prep(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"], W_uk, pos, D.nope,
+                    D.rope)
+    torch.testing.assert_close(qa, rqa, **TOL)
+    torch.testing.assert_close(qr, rqr, **TOL)
