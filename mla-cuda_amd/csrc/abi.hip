@@ -1115,13 +1115,20 @@ int check_fp8_attn(mla_dtype_t dtype, const mla_dims_t* dims, int causal, float 
 // measured faster (B=1, Sk=4989: attention with 3d 43.1 against 49.1 us; B=2, 3: 56.8 / 74.8
 // against 60.4 / 77.4 us; B=4, Sk=512: 36.0 against 37.7 us; B=4, Sk=4989 with 32 splits:
 // 99.0 against 91.3 us, so not there)
-bool use_out_small(mla_dtype_t dtype, const mla_dims_t* d, const FlashPlan& plan) {
+// Returns 1 for out_small_kernel with the merge folded in (or an unsplit pass), 2 for the
+// merge kernel followed by out_small_kernel on the merged ctx / row_sum (the other split
+// passes up to B*Sq = 8: 0.5-2.7 us ahead of the merge kernel and the 3d GEMM at B = 5..8,
+// Sk = 512..16384), 0 for the 3d GEMM.
+int out_small_mode(mla_dtype_t dtype, const mla_dims_t* d, const FlashPlan& plan) {
     const char* env = std::getenv("MLA_OUT_SMALL");
-    if (env && env[0] == '0') return false;
+    if (env && env[0] == '0') return 0;
     const int64_t M = (int64_t)d->batch * d->sq;
-    return !is_half(dtype) && !plan.balanced && M <= kOutSmallRows && d->kv_rank == 512 &&
-           plan.n_split <= kOutSmallMaxSplit && M * std::max(1, plan.n_split) <= kOutSmallMergeRows &&
-           (M <= kOutSmallMergeM || plan.n_split <= 1);
+    if (is_half(dtype) || plan.balanced || M > kOutSmallRows || d->kv_rank != 512) return 0;
+    if (plan.n_split <= 1) return 1;
+    if (plan.n_split <= kOutSmallMaxSplit && M * plan.n_split <= kOutSmallMergeRows &&
+        M <= kOutSmallMergeM)
+        return 1;
+    return 2;
 }
 
 }  // namespace
@@ -1393,10 +1400,12 @@ int mla_attention(mla_dtype_t dtype, const mla_dims_t* dims, const void* q_absor
         const FlashProblem fp = flash_problem(dtype, dims, q_absorbed, q_rope, c_kv, pe_cache,
                                               scale, causal);
         float* part = at<float>(workspace, L.off_part);
-        if (use_out_small(dtype, dims, L.flash)) {
-            MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream, false),
+        if (const int osm = out_small_mode(dtype, dims, L.flash)) {
+            MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream, osm == 2),
                         "fused attention launch");
-            MLA_TRY_HIP(launch_out_small(flash_partials(fp, L.flash, part), ctx, row_sum,
+            const FlashPartials merged = {nullptr, nullptr, nullptr, 1};
+            MLA_TRY_HIP(launch_out_small(osm == 2 ? merged : flash_partials(fp, L.flash, part),
+                                         ctx, row_sum,
                                          static_cast<const float*>(W_uv),
                                          static_cast<float*>(out), dims->batch, dims->sq,
                                          dims->heads, dims->kv_rank, dims->v, stream),
@@ -1701,10 +1710,12 @@ int mla_attention_paged(mla_dtype_t dtype, const mla_dims_t* dims, const void* q
         fp.block_table = block_table;
         fp.page_size = page_size;
         float* part = at<float>(workspace, L.off_part);
-        if (use_out_small(dtype, dims, L.flash)) {
-            MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream, false),
+        if (const int osm = out_small_mode(dtype, dims, L.flash)) {
+            MLA_TRY_HIP(launch_flash(fp, L.flash, ctx, row_sum, part, stream, osm == 2),
                         "fused paged attention launch");
-            MLA_TRY_HIP(launch_out_small(flash_partials(fp, L.flash, part), ctx, row_sum,
+            const FlashPartials merged = {nullptr, nullptr, nullptr, 1};
+            MLA_TRY_HIP(launch_out_small(osm == 2 ? merged : flash_partials(fp, L.flash, part),
+                                         ctx, row_sum,
                                          static_cast<const float*>(W_uv),
                                          static_cast<float*>(out), dims->batch, dims->sq,
                                          dims->heads, dims->kv_rank, dims->v, stream),

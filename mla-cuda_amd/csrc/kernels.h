@@ -253,7 +253,8 @@ constexpr int kOutSmallMaxSplit = 64;
 // the head's B*Sq*n_split partial rows beside the W_uv stream.  With a merge it is taken up
 // to B*Sq = 4 and 128 such rows (B=1: 43.1 against 49.1 us, B=2 54.1 / 60.2, B=4 87.6 /
 // 88.3); at B=8 (16 splits) the merge kernel and the 3d GEMM are faster (128.9 against
-// 132.1 us), so B*Sq = 5 .. 8 take it only for an unsplit pass.
+// 132.1 us), so B*Sq = 5 .. 8 take it after the merge kernel, on the merged ctx / row_sum
+// (B=8: 128.7 against 129.4 us for the merge kernel and the GEMM; B=5: 97.8 / 100.4).
 constexpr int kOutSmallMergeRows = 128;
 constexpr int kOutSmallMergeM = 4;
 hipError_t launch_out_small(const FlashPartials& fp, const float* ctx, const float* row_sum,

@@ -258,8 +258,9 @@ def test_fp32_kernels_full_size(ext, monkeypatch, wave):
 def test_fp32_decode_3d_with_merge(ext, monkeypatch, small, B, Sq, Sk, causal):
     """At B*Sq <= 4 (fp32) with at most 128 split rows per head to merge, mla_attention runs
     3d on a kernel that also merges the pass's key splits, and at B*Sq <= 8 on the same
-    kernel reading ctx / row_sum when the pass ran unsplit (Sk = 64); MLA_OUT_SMALL=0 keeps
-    the merge kernel and the 3d GEMM.  Both against the oracle."""
+    kernel reading ctx / row_sum, written by the pass when it ran unsplit (Sk = 64) or else
+    by the merge kernel (B*Sq = 5..8 split); MLA_OUT_SMALL=0 keeps the merge kernel and the
+    3d GEMM.  Both against the oracle."""
     monkeypatch.setenv("MLA_OUT_SMALL", small)
     args = inputs(B, Sq, Sk, seed=5 * Sk + B, dt=F32)
     close(run(ext, args, causal), oracle(args, causal), F32)
