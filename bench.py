@@ -191,7 +191,8 @@ def in_layer_kernel_us(layer, flush, n):
     kernels attributed to steps by launch order -- the layer launches its GEMMs in the order
     2a1, 2a2, 2c, 3d, a split-K reduce right after its GEMM, RMSNorm (2a-n, which also sums
     2a1's split partials) and RoPE (2b) between them (the 16-bit 2a2 may do 2b and 2c in its
-    epilogue: `wgemm_kernel<.., 2, false>`, counted as 2a2; at decode-sized fp32 batches
+    epilogue: `wgemm_kernel<.., 2, false>`, counted as 2a2; an unsplit fp32 2a2 may do 2b:
+    `gemm_kernel<.., true>`, its last template argument; at decode-sized fp32 batches
     `q_small_kernel` does 2b and 2c, counted as 2c), and the fused attention's kernels
     (work list, pass, merge) as 3abc; at decode-sized fp32 batches 3d may be
     out_small_kernel, which also does the pass's split merge.  Returns {step: mean µs per
@@ -211,7 +212,13 @@ def in_layer_kernel_us(layer, flush, n):
         if e.device_type != torch.autograd.DeviceType.CUDA:
             continue
         ks.append((e.time_range.start, e.time_range.end, e.name))
-    ks.sort()
+    return attribute_steps(ks)
+
+
+def attribute_steps(ks):
+    """`in_layer_kernel_us`'s attribution of kernel records (start, end, demangled name) to
+    steps, as described there; records of other kernels (the flush) separate the layers."""
+    ks = sorted(ks)
     gemm_steps = ("2a1", "2a2", "2c", "3d")
     folded = {}                       # step -> the steps its kernel also does
     tot = {}
@@ -234,6 +241,8 @@ def in_layer_kernel_us(layer, flush, n):
             if "wgemm_kernel" in name and re.search(r",\s*2(,\s*(false|true))?>", name):
                 cur["gemm"] += 1      # 2a2 with 2b and 2c in its epilogue: no 2c launch
                 folded["2a2"] = ("2b", "2c")
+            elif step == "2a2" and "wgemm_kernel" not in name and re.search(r",\s*true>", name):
+                folded["2a2"] = ("2b",)   # the fp32 2a2 that rotates q_rope in its epilogue
         elif "split_reduce" in name:
             step = cur["step"] or "2a1"
         elif "rmsnorm" in name:

@@ -65,3 +65,57 @@ def test_bench_scenarios_are_the_reference_matrix():
         "decode_speculative_long_ctx": (132, 4, 4096), "prefill_chat_batch": (8, 512, 512),
         "prefill_chunk_2k": (1, 2048, 2048), "prefill_chunk_4k": (1, 4096, 4096)}
     assert len(bench.SCENARIOS) == 12
+
+
+def _layer_records(names, t=0.0, dur=10.0):
+    """Kernel records (start, end, name) of one flushed layer: the flush, then `names` back
+    to back."""
+    recs = [(t, t + 100.0, "void at::native::reduce_kernel<512, 1>(...)")]
+    t += 100.0
+    for n in names:
+        recs.append((t, t + dur, n))
+        t += dur + 1.0
+    return recs, t
+
+
+def test_bench_attributes_layer_kernels_to_steps():
+    """bench.py's in-layer attribution of the library's kernels to steps, on the kernel names
+    of each layer form: the fp32 B=128 layer (2a2 rotating q_rope in its epilogue), the
+    16-bit layer (2a2 doing 2b and 2c; 3d on NT weight-streaming tiles) and the B=1 layer
+    (q_small_kernel for 2b + 2c, out_small_kernel for 3d)."""
+    import bench
+    ns = "void mla::(anonymous namespace)::"
+    args = "(mla::(anonymous namespace)::GemmArgs)"
+    g = lambda t: f"{ns}gemm_kernel<{t}>{args}"
+    w = lambda t: f"{ns}wgemm_kernel<{t}>(mla::(anonymous namespace)::WArgs)"
+    fp32 = [g("float, float, 64, 64, 2, 2, false, 0, 0, false, false, false"),
+            f"{ns}rmsnorm_kernel<0, 16>(...)",
+            g("float, float, 64, 64, 2, 2, false, 0, 0, false, false, true"),
+            g("float, float, 128, 64, 2, 2, false, 0, 0, false, true, false"),
+            f"{ns}flash32x_kernel<4>(...)",
+            g("float, float, 64, 64, 2, 2, true, 1, 0, false, false, false")]
+    recs, t = _layer_records(fp32)
+    more, _ = _layer_records(fp32, t)
+    r = bench.attribute_steps(recs + more)
+    assert r["layers"] == 2 and r["folded"] == {"2a2": ("2b",)}
+    assert all(r[s] == 10.0 for s in ("2a1", "2a-n", "2a2", "2c", "3abc", "3d"))
+    assert "2b" not in r
+
+    bf16 = [w("unsigned short, 64, 4, 1, 0, false"), f"{ns}rmsnorm_kernel<1, 8>(...)",
+            w("unsigned short, 128, 4, 1, 2, false"),
+            f"{ns}flash16x_kernel<unsigned short, false, true>(...)",
+            w("unsigned short, 64, 4, 1, 0, true")]
+    r = bench.attribute_steps(_layer_records(bf16)[0])
+    assert r["folded"] == {"2a2": ("2b", "2c")}
+    assert [s for s in ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d") if s in r] == \
+        ["2a1", "2a-n", "2a2", "3abc", "3d"]
+
+    b1 = [g("float, float, 32, 128, 1, 4, false, 0, 0, false, false, false"),
+          f"{ns}rmsnorm_kernel<0, 16>(...)",
+          g("float, float, 32, 128, 1, 4, false, 0, 0, false, false, false"),
+          f"{ns}q_small_kernel(...)", f"{ns}flash32w_kernel(...)",
+          f"{ns}flash_merge_kernel(...)", f"{ns}out_small_kernel(...)"]
+    r = bench.attribute_steps(_layer_records(b1)[0])
+    assert r["folded"] == {"2c": ("2b",)}
+    assert r["3abc"] == 20.0 and r["2c"] == 10.0 and r["3d"] == 10.0 and "2b" not in r
+    assert r["kernels_sum"] == 70.0
