@@ -1988,10 +1988,6 @@ __global__ void __launch_bounds__(kXThreads, 1) flash32x_kernel(FlashArgs a) {
     }
 
     // ==================================== P.V waves
-    // Their MFMAs go first on a SIMD whenever both waves have one ready: at equal wave
-    // priorities cfg2 took 1,338-1,342 us, with these waves at priority 1-3 1,286-1,293 us,
-    // the same bits.  (The 16-bit pass measured 5-8% slower this way, so it keeps equal ones.)
-    __builtin_amdgcn_s_setprio(1);
     // staging: P.V wave 4 + w loads keys 4w .. 4w+3 of a block (flash32_kernel's layout),
     // block j+2 during step j; blocks past the end load zeros
     const uint64_t ck_base = reinterpret_cast<uint64_t>(a.ckv);
@@ -2050,6 +2046,13 @@ __global__ void __launch_bounds__(kXThreads, 1) flash32x_kernel(FlashArgs a) {
             const Loads next = loads_of(j + 2);
             wait_vm<k32Loads>();           // block j has landed; block j+1 may be in flight
             lds_barrier();                 // A_j: block j-1's P^T is in its slot
+            // Wave priority: the first 96 of the step's 128 MFMAs go ahead of the score
+            // wave's on the SIMD, the last 32 behind them, so they run under the score
+            // wave's softmax and P^T write.  cfg2, the same bits: equal priorities 1,331-1,342
+            // us, priority 1 for the whole step 1,280-1,293 us, this 1,259-1,269 us.  (The
+            // 16-bit passes measured 5-8% slower with their P.V waves first, so they keep
+            // equal priorities.)
+            __builtin_amdgcn_s_setprio(1);
             constexpr int VW = 8;          // V reads in flight
             asm volatile("" : "+v"(v_base));
             const uint32_t vbs = v_base + (uint32_t)((j - 1) % NS) * k32LatStage;
@@ -2070,6 +2073,7 @@ __global__ void __launch_bounds__(kXThreads, 1) flash32x_kernel(FlashArgs a) {
                 O[2 * mh + 1] = mfma16f(__uint_as_float(cur[1]), p[i], O[2 * mh + 1]);
                 // block j+2 into stage (j+2) % 4, which block j-2 left at barrier A_j
                 if (t % 7 == 3 && t / 7 < k32Loads) issue_one(next, t / 7);
+                if (t == 47) __builtin_amdgcn_s_setprio(0);
             }
         }
         wait_vm<0>();    // the zero loads of the blocks past the end have landed
