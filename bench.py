@@ -215,6 +215,10 @@ def in_layer_kernel_us(layer, flush, n):
     return attribute_steps(ks)
 
 
+# the fused path's steps, in launch order
+FUSED_PATH = ("2a1", "2a-n", "2a2", "2b", "2c", "3abc", "3d")
+
+
 def attribute_steps(ks):
     """`in_layer_kernel_us`'s attribution of kernel records (start, end, demangled name) to
     steps, as described there; records of other kernels (the flush) separate the layers."""
@@ -836,9 +840,11 @@ def measure(args, ext, dev, neighbours=True, light=False):
         "layer_bound_us": round(layer_bound_us, 1),
         "layer_roofline_frac": round(layer_bound_us / value_us, 4),
         "per_step_sum_us": None if steps_sum is None else round(steps_sum, 2),
-        "fused_path_sum_us": (round(sum(step_us[n] for n in ("2a1", "2a-n", "2a2", "2b", "2c",
-                                                             "3abc", "3d")), 2)
-                              if fused_attn and not light else None),
+        # (null where a step has no time: the fp8-cache pass under another profiler)
+        "fused_path_sum_us": (round(sum(step_us[n] for n in FUSED_PATH), 2)
+                              if fused_attn and not light and all(n in step_us
+                                                                  for n in FUSED_PATH)
+                              else None),
         "per_step_vs_fused_max_abs": same,
         "neighbours": nb,
         "torch_same_gpu": torch_same,
