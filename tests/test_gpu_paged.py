@@ -73,6 +73,8 @@ def paged_inputs(B, Sq, lens, page, max_pages, seed, dtype=torch.float32, spare=
     (128, [1000, 129, 500], False, 1),
     (64, [200, 77, 640], True, 4),
     (192, [576, 300], True, 2),
+    (64, [700, 1, 333, 65, 1200, 128], False, 1),
+    (128, [300, 513, 900, 64], True, 2),
 ])
 def test_paged_attention_matches_oracle(ext, monkeypatch, path, page, lens, causal, Sq):
     set_path(monkeypatch, path)
