@@ -347,3 +347,31 @@ def test_attn_ctx_step_vs_oracle(ext, monkeypatch, dt, B, Sq, Sk, causal):
     full = ext.mla_attention(gpu(qa), gpu(qr), gpu(ck), gpu(pe), gpu(wuv), SCALE, causal)
     assert torch.equal(out, full)
     close(own.float().cpu(), full.float().cpu(), dt)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", [(40, 1, 700, False), (2, 16, 1000, True),
+                                            (130, 1, 333, False)])
+def test_fp32_specialised_waves_same_bits(ext, monkeypatch, B, Sq, Sk, causal):
+    """The eight specialised waves (flash32x_kernel, whose P.V waves change their wave
+    priority within each step) run the four-wave kernel's MFMAs in the same order on the same
+    P values: the output is the same bit for bit."""
+    monkeypatch.setenv("MLA_FLASH32_WAVE", "0")
+    args = inputs(B, Sq, Sk, seed=7 * Sk + B, dt=F32)
+    monkeypatch.setenv("MLA_FLASH32_SPEC", "1")
+    spec = run(ext, args, causal)
+    monkeypatch.setenv("MLA_FLASH32_SPEC", "0")
+    four = run(ext, args, causal)
+    assert torch.equal(spec, four)
+
+
+@pytest.mark.parametrize("B,Sq,Sk,causal", [(8, 1, 4989, False), (3, 4, 700, True)])
+def test_bf16_pv_layouts_same_bits(ext, monkeypatch, B, Sq, Sk, causal):
+    """The default 16-bit pass (P.V waves over 64 rows x 128 columns, with their wave
+    priority raised for the first MFMAs of each step) and the 32 x 256 layout
+    (MLA_FLASH16_PV=32) add the same products in the same order: the same bits."""
+    args = inputs(B, Sq, Sk, seed=11 * Sk + B, dt=BF)
+    monkeypatch.delenv("MLA_FLASH16_PV", raising=False)
+    a = run(ext, args, causal)
+    monkeypatch.setenv("MLA_FLASH16_PV", "32")
+    b = run(ext, args, causal)
+    assert torch.equal(a, b)
