@@ -1027,7 +1027,7 @@ __global__ void __launch_bounds__(kXThreads, 1) flash16x_kernel(FlashArgs a) {
             lds_barrier();                 // A_j (fp8: block j was converted in step j-1)
             // Wave priority (the default layout): the step's first 4 of 16 MFMAs go ahead of
             // the score wave's on the SIMD, the rest behind.  cfg4 bf16, the same bits: equal
-            // priorities 172.2-176.9 us, this 169.5-170.7 us; the first 2, 6, 8 or 12 MFMAs
+            // priorities 172.2-176.9 us, this 169.5-171.9 us; the first 2, 6, 8 or 12 MFMAs
             // 171.7, 172.5, 177.5 and 179.5 us (medians), the whole step 5-8% slower.
             if constexpr (PV64 && !FP8) __builtin_amdgcn_s_setprio(1);
             {
@@ -2056,7 +2056,7 @@ __global__ void __launch_bounds__(kXThreads, 1) flash32x_kernel(FlashArgs a) {
             // Wave priority: the first 96 of the step's 128 MFMAs go ahead of the score
             // wave's on the SIMD, the last 32 behind them, so they run under the score
             // wave's softmax and P^T write.  cfg2, the same bits: equal priorities 1,331-1,342
-            // us, priority 1 for the whole step 1,280-1,293 us, this 1,259-1,269 us.  (The
+            // us, priority 1 for the whole step 1,280-1,293 us, this 1,259-1,270 us.  (The
             // 16-bit passes measured 5-8% slower with their P.V waves first, so they keep
             // equal priorities.)
             __builtin_amdgcn_s_setprio(1);
