@@ -391,3 +391,26 @@ def test_q_absorbed_rope_in_2a2_epilogue(ext, monkeypatch, B, Sq, per_seq, plan)
                     D.rope)
     torch.testing.assert_close(qa, rqa, **TOL)
     torch.testing.assert_close(qr, rqr, **TOL)
+
+
+@pytest.mark.parametrize("plan", ["64,64", "32,128", "128,32"])
+def test_q_absorbed_rope_epilogue_other_dims(ext, monkeypatch, plan):
+    """The fp32 2a2 RoPE epilogue at other widths (6 heads of 64 nope + 32 rope columns, so a
+    head's rope part is one 32-column block and tiles cross heads), on each tile it runs on:
+    the same bits as the RoPE launch, and the oracle's values."""
+    dims = R.MLADims(hidden=256, n_heads=6, q_lora=128, kv_rank=128, nope=64, rope=32, v=64)
+    B, Sq = 70, 2
+    monkeypatch.setenv("MLA_GEMM_PLAN", f"{B * Sq},{dims.n_heads * dims.qk_head},{dims.q_lora},1="
+                                        f"{plan},1")
+    inp = R.make_inputs(B, Sq, 300, dims, seed=5)
+    W_uk, _ = R.split_wkv_b(inp["wkv_b"], dims.nope)
+    args = [gpu(inp[k]) for k in ("x", "W_q_a", "q_norm_w", "W_q_b")] + [gpu(W_uk.contiguous()),
+                                                                        gpu(inp["positions"])]
+    qa, qr = (t.cpu() for t in ext.q_absorbed(*args, dims.nope, dims.rope, 1e-6))
+    monkeypatch.setenv("MLA_ROPE_EPI", "0")
+    qa0, qr0 = (t.cpu() for t in ext.q_absorbed(*args, dims.nope, dims.rope, 1e-6))
+    assert torch.equal(qr, qr0) and torch.equal(qa, qa0)
+    rqa, rqr = R.prepare_q_mla_absorbed(inp["x"], inp["W_q_a"], inp["q_norm_w"], inp["W_q_b"],
+                                        W_uk, inp["positions"], dims.nope, dims.rope)
+    torch.testing.assert_close(qa, rqa, **TOL)
+    torch.testing.assert_close(qr, rqr, **TOL)
